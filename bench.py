@@ -1,0 +1,352 @@
+#!/usr/bin/env python
+"""Benchmark of the MoE MLP hot path on one MI355X.
+
+Workload: BASELINE.json config 3 -- TritonMoEMLP with n_embd=1024,
+expert_sizes=[(64, 256)], top_k=8, 16384 tokens, block_size 64, bf16, router
+logits biased by a Zipf(s=1.2) rank profile (alpha = smallest integer giving an
+empty expert and a hottest expert above 4x the mean). Synthetic data: one CPU
+torch.Generator(0) draws x ~ N(0,1), then router, w1, w2 ~ N(0, 0.02).
+
+A step is one forward + out.sum().backward() of the layer (routing, gather,
+grouped GEMM up + relu^2, grouped GEMM down, weighted combine and the full
+backward including both dW GEMMs).
+
+Prints one JSON line: value = grouped-GEMM TFLOP/s of the whole step
+(12 * d * sum_e n_e * w_e over the step's wall time), plus ms_per_step, the
+per-kernel breakdown (HIP events on the launch stream), the roofline of the
+dominant kernel and the CPU baseline (the fp32 eager per-expert-loop oracle on
+the host cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "triton-variable-moe_amd"))
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    # name: (n_embd, expert_sizes, top_k, tokens, zipf)
+    "cfg1": (768, [(8, 512)], 2, 8 * 1024, False),
+    "cfg2": (768, [(4, 512), (8, 256), (4, 128)], 2, 8 * 2048, False),
+    "cfg3": (1024, [(64, 256)], 8, 16384, True),
+    "cfg4": (2048, [(32, 1024), (64, 512), (32, 256)], 8, 32768, False),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--profile-steps", type=int, default=0,
+                    help="only run this many steps (for rocprofv3), print nothing else")
+    return ap.parse_args()
+
+
+def build_workload(name, device):
+    import numpy as np
+    import torch
+
+    from triton_moe import TritonMoEConfig, TritonMoEMLP
+
+    d, sizes, k, T, zipf = CONFIGS[name]
+    E = sum(c for c, _ in sizes)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, T, d, generator=g)
+    wr = torch.randn(E, d, generator=g) * 0.02
+    cfg = TritonMoEConfig(n_embd=d, expert_sizes=sizes, num_active_experts=k, block_size=64)
+    m = TritonMoEMLP(cfg)
+    W = m.total_expert_width
+    w1 = torch.randn(d, W, generator=g) * 0.02
+    w2 = torch.randn(W, d, generator=g) * 0.02
+    with torch.no_grad():
+        m.router.weight.copy_(wr)
+        m.w1.copy_(w1)
+        m.w2.copy_(w2)
+    m = m.to(device).to(torch.bfloat16)
+    xb = x.to(torch.bfloat16).to(device)
+    info = {"alpha": None}
+    if zipf:
+        ranks = np.random.default_rng(0).permutation(E) + 1
+        base = torch.tensor(-1.2 * np.log(ranks), dtype=torch.float32, device=device)
+        state = {"bias": None}
+        m.router.register_forward_hook(
+            lambda mod, inp, out: out if state["bias"] is None else out + state["bias"].to(out.dtype))
+        with torch.no_grad():
+            for alpha in range(1, 20):
+                state["bias"] = alpha * base
+                _, _, f_i = m(xb)
+                logits = m.router(xb.reshape(-1, d))
+                sel = torch.topk(torch.sigmoid(logits.float()), k, dim=-1).indices
+                hist = torch.bincount(sel.reshape(-1), minlength=E)
+                if hist.min().item() == 0 and hist.max().item() > 4 * hist.float().mean().item():
+                    info["alpha"] = alpha
+                    break
+        info["histogram"] = hist.tolist()
+    xb.requires_grad_(True)
+    return m, xb, info
+
+
+def gemm_flops(m, xb):
+    import torch
+
+    with torch.no_grad():
+        d = xb.shape[-1]
+        logits = m.router(xb.reshape(-1, d))
+        sel = torch.topk(torch.sigmoid(logits.float()), m.num_active_experts, dim=-1).indices
+        counts = torch.bincount(sel.reshape(-1), minlength=m.num_experts).cpu().tolist()
+    snw = sum(n * w for n, w in zip(counts, m.expert_widths))
+    return 12.0 * d * snw, counts, sel
+
+
+def time_steps(m, xb, steps, warmup):
+    import torch
+
+    def step():
+        m.zero_grad(set_to_none=True)
+        xb.grad = None
+        out, _, _ = m(xb)
+        out.sum().backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
+def kernel_breakdown(m, xb, sel, reps):
+    """Average duration of every kernel launch of a step, each timed alone in a
+    loop of `reps` launches between two HIP events on the launch stream."""
+    import torch
+
+    from triton_moe.kernels import grouped_gemm as gg
+    from triton_moe.kernels.fused_cumsum import route_device
+    from triton_moe.kernels.gather import combine_rows, gather_rows
+
+    k, E, b = m.num_active_experts, m.num_experts, m.block_size
+    d = xb.shape[-1]
+    x = xb.detach().reshape(-1, d)
+    T = x.shape[0]
+    wts = torch.rand(T * k, device=x.device).to(torch.bfloat16)
+    selv = sel.reshape(-1)
+    r = route_device(selv, E, k, b)
+    pb = r.padded_bins
+    eto = torch.cat([torch.zeros(1, dtype=torch.int32, device=x.device), pb])
+    tpe = torch.cat([pb[:1], pb[1:] - pb[:-1]])
+    meta = gg.GemmMeta(eto, m.expert_weight_offsets_t, m.expert_widths_t, tpe, E,
+                       m.max_expert_width, r.rows_bound)
+    nrd = r.info[0:1]
+    xg = gather_rows(x, r.row_src, k, r.rows_bound, num_rows_dev=nrd)
+    h, pre = gg.up_fwd(xg, m.w1.detach(), meta, 1, True, False)
+    y = gg.down_fwd(h, m.w2.detach(), meta, d)
+    G = torch.ones(T, d, dtype=torch.bfloat16, device=x.device)
+    gy = gather_rows(G, r.row_src, k, r.rows_bound, weights=wts, num_rows_dev=nrd)
+    gh, _ = gg.down_bwd(gy, h, m.w2.detach(), meta, d, False)
+    gxg, _ = gg.up_bwd(gh, x, m.w1.detach(), pre, meta, d, 1, r.gather_map)
+    w1, w2 = m.w1.detach(), m.w2.detach()
+
+    def dx_only():
+        from triton_moe import _lib
+        gx = torch.empty(meta.rows, d, dtype=torch.bfloat16, device=x.device)
+        _lib.call("vmoe_gemm_up_bwd_dx", gh.data_ptr(), pre.data_ptr(), gh.stride(0), 1,
+                  w1.data_ptr(), w1.stride(0), gx.data_ptr(), gx.stride(0), *gg._meta_args(meta),
+                  d, meta.max_width, meta.rows, _lib.stream(x.device))
+
+    def dw1_only():
+        from triton_moe import _lib
+        gw = torch.empty_like(w1)
+        _lib.call("vmoe_gemm_up_bwd_dw", x.data_ptr(), x.stride(0), T, r.gather_map.data_ptr(),
+                  gh.data_ptr(), pre.data_ptr(), gh.stride(0), 1, gw.data_ptr(), gw.stride(0),
+                  *gg._meta_args(meta), d, meta.max_width, meta.rows, _lib.stream(x.device))
+
+    def dh_only():
+        from triton_moe import _lib
+        o = torch.empty(meta.rows, meta.max_width, dtype=torch.bfloat16, device=x.device)
+        _lib.call("vmoe_gemm_down_bwd_dh", gy.data_ptr(), gy.stride(0), w2.data_ptr(),
+                  w2.stride(0), o.data_ptr(), o.stride(0), *gg._meta_args(meta), d,
+                  meta.max_width, meta.rows, _lib.stream(x.device))
+
+    def dw2_only():
+        from triton_moe import _lib
+        gw = torch.empty_like(w2)
+        _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), gy.data_ptr(),
+                  gy.stride(0), gw.data_ptr(), gw.stride(0), *gg._meta_args(meta), d,
+                  meta.max_width, meta.rows, _lib.stream(x.device))
+
+    ops = {
+        "route": lambda: route_device(selv, E, k, b),
+        "gather": lambda: gather_rows(x, r.row_src, k, r.rows_bound, num_rows_dev=nrd),
+        "gemm_up_fwd": lambda: gg.up_fwd(xg, w1, meta, 1, True, False),
+        "gemm_down_fwd": lambda: gg.down_fwd(h, w2, meta, d),
+        "combine": lambda: combine_rows(y, r.assignment_row, k, T, weights=wts),
+        "scatter_bwd_gather": lambda: gather_rows(G, r.row_src, k, r.rows_bound, weights=wts,
+                                                  num_rows_dev=nrd),
+        "gemm_down_bwd_dh": dh_only,
+        "gemm_down_bwd_dw": dw2_only,
+        "gemm_up_bwd_dx": dx_only,
+        "gemm_up_bwd_dw": dw1_only,
+        "gather_bwd_combine": lambda: combine_rows(gxg, r.assignment_row, k, T),
+    }
+    out = {}
+    stream = torch.cuda.current_stream()
+    for name, fn in ops.items():
+        fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        out[name] = e0.elapsed_time(e1) / reps * 1e3  # microseconds
+    return out
+
+
+def cpu_baseline(m, xb, sel, iters):
+    """fp32 eager per-expert-loop oracle (forward + backward) on the host."""
+    import torch
+
+    from oracle import eager
+
+    d = xb.shape[-1]
+    x = xb.detach().reshape(-1, d).float().cpu()
+    k = m.num_active_experts
+    with torch.no_grad():
+        logits = m.router(xb.detach().reshape(-1, d))
+        wts, sel2 = torch.topk(torch.sigmoid(logits.float()), k, dim=-1)
+        wts = (wts / (wts.sum(-1, keepdim=True) + 1e-20)).to(torch.bfloat16)
+    prob = eager.Problem(x, m.w1.detach().float().cpu(), m.w2.detach().float().cpu(),
+                         m.expert_widths, m.expert_offsets, sel2.cpu(), wts.cpu().float(),
+                         m.block_size)
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    G = torch.ones(x.shape[0], d)
+
+    def run():
+        f = eager.forward(prob, "fp32")
+        eager.backward(prob, f, G, "fp32")
+
+    run()
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], torch.get_num_threads()
+
+
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU (expert/data "
+                          "parallel) scaling is a design in DESIGN.md, not a measured path",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm GPU visible"}))
+        sys.exit(1)
+    device = torch.device("cuda:0")
+    torch.manual_seed(0)
+    m, xb, info = build_workload(args.config, device)
+    flops, counts, sel = gemm_flops(m, xb)
+
+    if args.profile_steps:
+        time_steps(m, xb, args.profile_steps, 1)
+        print(json.dumps({"profile_steps": args.profile_steps, "config": args.config}))
+        return
+
+    ms = time_steps(m, xb, args.steps, args.warmup)
+    value = flops / (ms * 1e-3) / 1e12
+    kern = kernel_breakdown(m, xb, sel, args.kernel_reps)
+    gemm_names = [n for n in kern if n.startswith("gemm_")]
+    gemm_us = sum(kern[n] for n in gemm_names)
+    per_gemm_flops = flops / 6.0
+    gemm_tflops = flops / (gemm_us * 1e-6) / 1e12
+    dom = max(gemm_names, key=lambda n: kern[n])
+    achieved = per_gemm_flops / (kern[dom] * 1e-6) / 1e12
+
+    d, sizes, k, T, _ = CONFIGS[args.config]
+    A = T * k
+    E = m.num_experts
+    perm_bytes = {
+        "gather": 2 * T * d + 2 * A * d + 8 * A,
+        "combine": 2 * A * d + 2 * A + 2 * T * d + 8 * A,
+        "scatter_bwd_gather": 2 * T * d + 2 * A + 2 * A * d + 8 * A,
+        "gather_bwd_combine": 2 * A * d + 2 * T * d + 8 * A,
+    }
+    perm_us = sum(kern[n] for n in perm_bytes)
+    perm_gbs = sum(perm_bytes.values()) / (perm_us * 1e-6) / 1e9
+
+    result = {
+        "metric": "MoE fwd+bwd ms + grouped-GEMM TFLOP/s (% MFMA peak), 64 experts k=8 bf16",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) tokens, N(0,0.02) weights, Zipf-biased router)",
+        "config": {"workload": f"{args.config}: TritonMoEMLP fwd+bwd, n_embd={d}, "
+                               f"expert_sizes={sizes}, top_k={k}, tokens={T}, block_size=64",
+                   "global_batch": T, "seq_len": T, "parallelism": "none (1 GPU)",
+                   "zipf_alpha": info.get("alpha"),
+                   "tokens_per_expert_min_max": [min(counts), max(counts)]},
+        "gemm_flops_per_step": flops,
+        "gemm_tflops_kernel_time": round(gemm_tflops, 2),
+        "gemm_pct_mfma_peak": round(100 * gemm_tflops / PEAK_BF16_TFLOPS, 2),
+        "permutation_gbs": round(perm_gbs, 1),
+        "permutation_pct_hbm_peak": round(100 * perm_gbs / PEAK_HBM_GBS, 2),
+        "kernel_us": {n: round(v, 2) for n, v in kern.items()},
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        sec, threads = cpu_baseline(m, xb, sel, args.cpu_iters)
+        result["cpu_baseline"] = {
+            "value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "ms_per_step": round(sec * 1e3, 1),
+            "sample": f"full {args.config} step (fp32 eager per-expert-loop oracle, fwd+bwd), "
+                      f"median of {args.cpu_iters} after 1 warmup, {cpu_model()}"}
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,200 @@
+/*
+ * vmoe.h -- C ABI of the MI355X (gfx950) variable-width MoE MLP hot path.
+ *
+ * Every entry point is asynchronous on the given HIP stream: nothing here
+ * synchronises, allocates device memory or reads device memory from the host.
+ * Buffers are raw device pointers; bf16 tensors are passed as uint16_t*
+ * (bit patterns), metadata as int32_t*. Leading dimensions are in elements.
+ * Return value: VMOE_OK (0) or a vmoe_status code; vmoe_status_string()
+ * turns it into text. A launch failure is reported as VMOE_ERR_LAUNCH.
+ *
+ * Reference interface each entry point replaces is cited as
+ * <reference file>:<line>, relative to hbfreed/triton-variable-moe.
+ */
+#ifndef VMOE_H
+#define VMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* vmoe_stream_t; /* == hipStream_t */
+
+enum vmoe_status {
+  VMOE_OK = 0,
+  VMOE_ERR_INVALID_ARG = 1, /* null pointer, negative size, bad enum */
+  VMOE_ERR_UNSUPPORTED = 2, /* size/alignment outside what the kernels take */
+  VMOE_ERR_LAUNCH = 3,      /* hipLaunchKernel / hipGetLastError failure */
+  VMOE_ERR_WORKSPACE = 4    /* workspace smaller than *_workspace_bytes() */
+};
+
+/* Rounding modes of fused_route (triton_moe/kernels/fused_cumsum.py:126-128). */
+enum vmoe_rounding { VMOE_ROUND_UP = 0, VMOE_ROUND_DOWN = 1, VMOE_ROUND_NEAREST = 2 };
+
+/* Activations of grouped_gemm_up (triton_moe/kernels/grouped_gemm.py:435). */
+enum vmoe_activation { VMOE_ACT_NONE = 0, VMOE_ACT_RELU_SQUARED = 1 };
+
+/* Bits of info[VMOE_INFO_ERRORS] written by vmoe_route. */
+enum vmoe_route_error { VMOE_ROUTE_BAD_EXPERT_ID = 1, VMOE_ROUTE_ROW_OVERFLOW = 2 };
+enum vmoe_info_slot { VMOE_INFO_ROWS = 0, VMOE_INFO_KEPT = 1, VMOE_INFO_ERRORS = 2, VMOE_INFO_LEN = 4 };
+
+const char* vmoe_status_string(int status);
+int vmoe_version(void);
+/* Largest num_experts vmoe_route accepts. */
+int vmoe_route_max_experts(void);
+
+/* ------------------------------------------------------------------------
+ * Routing.
+ * Replaces fused_route (triton_moe/kernels/fused_cumsum.py:85-171: torch.sort
+ * stable + torch.bincount + _cumsum_kernel + the rounding keep-mask) and, in
+ * the same pass, precompute_gather_map (triton_moe/kernels/grouped_gemm.py:104-149).
+ *
+ *   selected_experts  [A] int32 or int64 (selected_is_int64), flat t*k+j order
+ *   bin_ids, indices  [A] int32: expert-sorted (stable) ids and positions;
+ *                     the first info[VMOE_INFO_KEPT] entries are valid
+ *   tokens_per_expert, bins, padded_bins  [E] int32
+ *   row_src     [row_capacity] int32: padded row -> assignment index, -1 = pad
+ *   gather_map  [row_capacity] int32: padded row -> token (assignment / top_k), 0 = pad
+ *   assignment_row [A] int32: assignment -> padded row, -1 = dropped
+ *   info        [VMOE_INFO_LEN] int32: rows P, kept count, error bits
+ * Only the first P = padded_bins[E-1] rows of row_src/gather_map are written;
+ * row_capacity >= A + E*(block_size-1) always suffices.
+ * ---------------------------------------------------------------------- */
+size_t vmoe_route_workspace_bytes(int64_t num_assignments, int32_t num_experts);
+int vmoe_route(const void* selected_experts, int32_t selected_is_int64,
+               int64_t num_assignments, int32_t num_experts, int32_t top_k,
+               int32_t block_size, int32_t rounding, int32_t* bin_ids, int32_t* indices,
+               int32_t* tokens_per_expert, int32_t* bins, int32_t* padded_bins,
+               int32_t* row_src, int32_t* gather_map, int64_t row_capacity,
+               int32_t* assignment_row, int32_t* info, void* workspace,
+               size_t workspace_bytes, vmoe_stream_t stream);
+
+/* Row maps from caller-supplied routing arrays, for the stand-alone
+ * gather/scatter/gather-map entry points. Follows the per-sorted-position
+ * placement of _padded_gather_kernel (triton_moe/kernels/gather.py:34-60) and
+ * precompute_gather_map (triton_moe/kernels/grouped_gemm.py:124-149): sorted
+ * position i of expert e = bin_ids[i] lands on row
+ * padded_bins[e-1] + i - bins[e-1]. Rows nobody lands on get row_src = -1,
+ * gather_map = 0; assignments nobody places get assignment_row = -1.
+ * Any output pointer may be NULL. */
+int vmoe_row_maps(const int32_t* indices, const int32_t* bin_ids, const int32_t* bins,
+                  const int32_t* padded_bins, int64_t num_sorted, int32_t num_experts,
+                  int32_t top_k, int64_t num_rows, int64_t num_assignments,
+                  int32_t* row_src, int32_t* gather_map, int32_t* assignment_row,
+                  vmoe_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Token permutation (bf16).
+ * vmoe_gather: out[r] = x[row_src[r] / top_k] (times weights[row_src[r]] when
+ * weights != NULL, product rounded to bf16), zero where row_src[r] < 0.
+ *   - unweighted: padded_gather (triton_moe/kernels/gather.py:63-115)
+ *   - weighted:   _weighted_padded_gather, the scatter backward
+ *                 (triton_moe/kernels/gather.py:177-218, scatter.py:161-176)
+ * num_rows_dev (nullable) caps num_rows with a device-side row count.
+ * ---------------------------------------------------------------------- */
+int vmoe_gather(const uint16_t* x, int64_t x_rows, int64_t ldx, const int32_t* row_src,
+                int32_t top_k, const uint16_t* weights, int64_t num_weights, uint16_t* out,
+                int64_t ldo, int64_t num_rows, const int32_t* num_rows_dev, int64_t hidden,
+                vmoe_stream_t stream);
+
+/* vmoe_combine: out[t] = bf16( sum_j f32( bf16( y[assignment_row[t*k+j]] * w[t*k+j] ) ) ),
+ * j = 0..top_k-1 in order, slots with assignment_row < 0 contribute 0.
+ *   - weighted:   padded_scatter + intermediate.sum(1)
+ *                 (triton_moe/kernels/scatter.py:72-133)
+ *   - weights == NULL: the gather backward, padded_scatter with all-ones
+ *                 weights (triton_moe/kernels/gather.py:245-265) */
+int vmoe_combine(const uint16_t* y, int64_t y_rows, int64_t ldy, const int32_t* assignment_row,
+                 const uint16_t* weights, int32_t top_k, uint16_t* out, int64_t ldo,
+                 int64_t num_tokens, int64_t hidden, vmoe_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Variable-width grouped GEMMs (bf16 in, fp32 MFMA accumulate, bf16 out).
+ * Per-expert metadata as in the reference kernels:
+ *   eto    [E+1] expert_token_offsets (row ranges in the padded layout)
+ *   ewo    [E+1] expert_weight_offsets (column/row offset of expert e in W1/W2)
+ *   widths [E]   expert_widths
+ *   tpe    [E]   tokens_per_expert (rows tiled per expert; the module passes
+ *                the padded counts)
+ * rows_bound: upper bound of sum(tpe) and of eto[E]; sizes the grid and
+ * bounds every row index (outputs have at least rows_bound rows).
+ * Tiles are found on the device from the metadata, so no host sync is needed.
+ * hidden, every width and ewo entry, and all leading dimensions must be
+ * multiples of 8 and buffers 16-byte aligned (VMOE_ERR_UNSUPPORTED otherwise).
+ * ---------------------------------------------------------------------- */
+
+/* out = act(x_e @ W1[:, ewo[e]:ewo[e]+w_e]); pre_act = relu(z) (nullable).
+ * Rows of x_e are x[gather_map[row]] when gather_map != NULL (the reference's
+ * USE_GATHER_MAP path; x then has x_rows rows), else x[row].
+ * Replaces grouped_gemm_up / _grouped_gemm_up_kernel
+ * (triton_moe/kernels/grouped_gemm.py:212-368, 379-477). */
+int vmoe_gemm_up_fwd(const uint16_t* x, int64_t ldx, int64_t x_rows, const int32_t* gather_map,
+                     const uint16_t* w1, int64_t ldw1,
+                     uint16_t* out, uint16_t* pre_act, int64_t ldo, int32_t activation,
+                     const int32_t* eto, const int32_t* ewo, const int32_t* widths,
+                     const int32_t* tpe, int32_t num_experts, int64_t hidden,
+                     int64_t max_width, int64_t rows_bound, vmoe_stream_t stream);
+
+/* y = h_e[:, :w_e] @ W2[ewo[e]:ewo[e+1], :].
+ * Replaces grouped_gemm_down / _grouped_gemm_down_kernel
+ * (triton_moe/kernels/grouped_gemm.py:480-651). */
+int vmoe_gemm_down_fwd(const uint16_t* h, int64_t ldh, const uint16_t* w2, int64_t ldw2,
+                       uint16_t* y, int64_t ldy, const int32_t* eto, const int32_t* ewo,
+                       const int32_t* widths, const int32_t* tpe, int32_t num_experts,
+                       int64_t hidden, int64_t max_width, int64_t rows_bound,
+                       vmoe_stream_t stream);
+
+/* grad_x = GA @ W1_e^T with GA = bf16(pre>0 ? 2*grad_h*pre : 0) (relu^2) or grad_h.
+ * Replaces _grouped_gemm_up_backward_dx_kernel
+ * (triton_moe/kernels/grouped_gemm.py:654-802, launched at 1214-1250). */
+int vmoe_gemm_up_bwd_dx(const uint16_t* grad_h, const uint16_t* pre_act, int64_t ldg,
+                        int32_t activation, const uint16_t* w1, int64_t ldw1,
+                        uint16_t* grad_x, int64_t ldgx, const int32_t* eto, const int32_t* ewo,
+                        const int32_t* widths, const int32_t* tpe, int32_t num_experts,
+                        int64_t hidden, int64_t max_width, int64_t rows_bound,
+                        vmoe_stream_t stream);
+
+/* grad_w1[:, ewo[e]:+w_e] = X_e^T @ GA_e, X_e rows read as x[gather_map[row]]
+ * when gather_map != NULL (fused gather), else x[row].
+ * Replaces _grouped_gemm_up_backward_dw_kernel
+ * (triton_moe/kernels/grouped_gemm.py:805-967, launched at 1252-1290). */
+int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
+                        const int32_t* gather_map, const uint16_t* grad_h,
+                        const uint16_t* pre_act, int64_t ldg, int32_t activation,
+                        uint16_t* grad_w1, int64_t ldgw, const int32_t* eto,
+                        const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
+                        int32_t num_experts, int64_t hidden, int64_t max_width,
+                        int64_t rows_bound, vmoe_stream_t stream);
+
+/* grad_h = grad_y @ W2_e^T (columns >= w_e untouched).
+ * Replaces _grouped_gemm_down_backward_dintermediate_kernel
+ * (triton_moe/kernels/grouped_gemm.py:970-1063, launched at 1336-1362). */
+int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, const uint16_t* w2,
+                          int64_t ldw2, uint16_t* grad_h, int64_t ldgh, const int32_t* eto,
+                          const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
+                          int32_t num_experts, int64_t hidden, int64_t max_width,
+                          int64_t rows_bound, vmoe_stream_t stream);
+
+/* grad_w2[ewo[e]:+w_e, :] = H_e^T @ grad_y_e.
+ * Replaces _grouped_gemm_down_backward_dw_kernel
+ * (triton_moe/kernels/grouped_gemm.py:1066-1162, launched at 1364-1390). */
+int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint16_t* grad_y,
+                          int64_t ldgy, uint16_t* grad_w2, int64_t ldgw, const int32_t* eto,
+                          const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
+                          int32_t num_experts, int64_t hidden, int64_t max_width,
+                          int64_t rows_bound, vmoe_stream_t stream);
+
+/* Zero columns [widths[e], max_width) of every row of expert e in a padded
+ * [rows, max_width] buffer: the zero-initialised tails the reference's
+ * torch.zeros outputs carry (triton_moe/kernels/grouped_gemm.py:422,426,1328). */
+int vmoe_zero_tail_cols(uint16_t* buf, int64_t ld, const int32_t* eto, const int32_t* widths,
+                        int32_t num_experts, int64_t max_width, int64_t rows_bound,
+                        vmoe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VMOE_H */

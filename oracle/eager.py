@@ -1,0 +1,207 @@
+"""Eager per-expert-loop restatement of TritonMoEMLP (test infrastructure only).
+
+Runs on the CPU in float32 (or float64 for pinning tests). Two numerics modes:
+
+* mode="fp32": no intermediate rounding. This is the tolerance oracle the
+  HIP path is held to with a normwise bf16 tolerance.
+* mode="bf16": rounds to bf16 exactly at the points where the reference's
+  kernels store bf16 (Appendix-A semantics of the reference):
+    PRE = bf16(relu(z)), H = bf16(relu(z)^2) from the fp32 accumulator
+        (triton_moe/kernels/grouped_gemm.py:336-346)
+    Y = bf16(H @ W2)                       (grouped_gemm.py:575-583)
+    combine slot = bf16(Y * w), fp32 sum over j, bf16 result
+        (triton_moe/kernels/scatter.py:61-69, 133)
+    GY = bf16(G * w)                       (triton_moe/kernels/gather.py:170-174)
+    GH = bf16(GY @ W2^T), GW2 = bf16(H^T @ GY)   (grouped_gemm.py:1054-1063, 1153-1162)
+    GA = bf16(PRE > 0 ? 2 * GH * PRE : 0)  (grouped_gemm.py:751-766, 914-928)
+    GXg = bf16(GA @ W1^T), GW1 = bf16(Xg^T @ GA) (grouped_gemm.py:793-802, 947-967)
+    Gx = bf16(sum_j GXg[row(t, j)])        (gather.py:256-263 via padded_scatter)
+  The only remaining difference to a GPU run is fp32 summation order.
+
+Routing weights get no gradient, as in the reference (scatter.py:176).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import route as _route
+
+
+def bf(t: torch.Tensor) -> torch.Tensor:
+    """Round to bf16 (torch's round-to-nearest-even) and back to t's dtype."""
+    return t.to(torch.bfloat16).to(t.dtype)
+
+
+def expert_layout(expert_sizes) -> tuple[list[int], list[int]]:
+    """Per-expert widths and column offsets (triton_moe/moe.py:64-75)."""
+    widths, offsets = [], [0]
+    for count, size in expert_sizes:
+        for _ in range(count):
+            widths.append(int(size))
+            offsets.append(offsets[-1] + int(size))
+    return widths, offsets
+
+
+@dataclass
+class Problem:
+    """One MoE-MLP invocation: flat tokens, weights, and the routing decision."""
+
+    x: torch.Tensor          # [T, d]
+    w1: torch.Tensor         # [d, W]
+    w2: torch.Tensor         # [W, d]
+    widths: list
+    offsets: list
+    selected: torch.Tensor   # [T, k] int64
+    weights: torch.Tensor    # [T, k] (bf16 values, any float dtype)
+    block_size: int = 64
+    rounding: str = "up"
+
+    @property
+    def top_k(self) -> int:
+        return self.selected.shape[1]
+
+    @property
+    def num_experts(self) -> int:
+        return len(self.widths)
+
+
+def route(prob: Problem) -> dict:
+    """fused_route + row maps of a problem (numpy int32 arrays)."""
+    r = _route.route(prob.selected.reshape(-1).numpy(), prob.num_experts, prob.block_size,
+                     prob.rounding)
+    maps = _route.row_maps(r["indices"], r["bin_ids"], r["bins"], r["padded_bins"], prob.top_k,
+                           num_assignments=prob.selected.numel())
+    r.update(maps)
+    r["P"] = int(r["padded_bins"][-1]) if prob.num_experts else 0
+    return r
+
+
+def _rows(r: dict, e: int) -> tuple[int, int]:
+    pb = r["padded_bins"]
+    r0 = int(pb[e - 1]) if e > 0 else 0
+    return r0, int(pb[e])
+
+
+def forward(prob: Problem, mode: str = "fp32", r: dict | None = None) -> dict:
+    """Forward of the MoE MLP. Returns out [T, d] and the padded intermediates."""
+    assert mode in ("fp32", "bf16")
+    rb = bf if mode == "bf16" else (lambda t: t)
+    dt = prob.x.dtype
+    r = route(prob) if r is None else r
+    T, d = prob.x.shape
+    k = prob.top_k
+    P = r["P"]
+    max_w = max(prob.widths)
+    row_src = torch.from_numpy(r["row_src"].astype(np.int64))
+    valid = row_src >= 0
+    xg = torch.zeros(P, d, dtype=dt)
+    xg[valid] = prob.x[row_src[valid] // k]
+    z = torch.zeros(P, max_w, dtype=dt)
+    pre = torch.zeros(P, max_w, dtype=dt)
+    h = torch.zeros(P, max_w, dtype=dt)
+    y = torch.zeros(P, d, dtype=dt)
+    for e, (w, o) in enumerate(zip(prob.widths, prob.offsets)):
+        r0, r1 = _rows(r, e)
+        if r1 == r0:
+            continue
+        ze = xg[r0:r1] @ prob.w1[:, o:o + w]
+        z[r0:r1, :w] = ze
+        relu = torch.clamp_min(ze, 0)
+        pre[r0:r1, :w] = rb(relu)
+        h[r0:r1, :w] = rb(relu * relu)
+        y[r0:r1] = rb(h[r0:r1, :w] @ prob.w2[o:o + w])
+    out = combine(y, r["assignment_row"], prob.weights.to(dt).reshape(-1), k, T, mode)
+    return {"out": out, "x_gathered": xg, "z": z, "pre_act": pre, "h": h, "y": y, "route": r}
+
+
+def combine(y: torch.Tensor, assignment_row, weights_flat, k: int, T: int,
+            mode: str) -> torch.Tensor:
+    """out[t] = sum_j slot(t, j), slot = y[row] * w (rounded to bf16 in bf16 mode),
+    summed in fp32 in ascending j (scatter.py:61-69, 133)."""
+    rb = bf if mode == "bf16" else (lambda t: t)
+    ar = torch.as_tensor(np.asarray(assignment_row, np.int64)).view(T, k)
+    out = torch.zeros(T, y.shape[1], dtype=y.dtype)
+    for j in range(k):
+        rows = ar[:, j]
+        ok = rows >= 0
+        slot = torch.zeros_like(out)
+        if weights_flat is None:
+            slot[ok] = y[rows[ok]]
+        else:
+            wj = weights_flat.view(T, k)[:, j]
+            slot[ok] = rb(y[rows[ok]] * wj[ok, None])
+        out = out + slot
+    return rb(out)
+
+
+def backward(prob: Problem, fwd: dict, grad_out: torch.Tensor, mode: str = "fp32") -> dict:
+    """Gradients of the forward above for upstream grad_out [T, d]."""
+    assert mode in ("fp32", "bf16")
+    rb = bf if mode == "bf16" else (lambda t: t)
+    r = fwd["route"]
+    dt = prob.x.dtype
+    T, d = prob.x.shape
+    k = prob.top_k
+    P = r["P"]
+    max_w = max(prob.widths)
+    g = grad_out.to(dt)
+    w_flat = prob.weights.to(dt).reshape(-1)
+    row_src = torch.from_numpy(r["row_src"].astype(np.int64))
+    valid = row_src >= 0
+    gy = torch.zeros(P, d, dtype=dt)
+    gy[valid] = rb(g[row_src[valid] // k] * w_flat[row_src[valid], None])
+    gh = torch.zeros(P, max_w, dtype=dt)
+    ga = torch.zeros(P, max_w, dtype=dt)
+    gxg = torch.zeros(P, d, dtype=dt)
+    gw1 = torch.zeros_like(prob.w1, dtype=dt)
+    gw2 = torch.zeros_like(prob.w2, dtype=dt)
+    for e, (w, o) in enumerate(zip(prob.widths, prob.offsets)):
+        r0, r1 = _rows(r, e)
+        if r1 == r0:
+            continue
+        ghe = rb(gy[r0:r1] @ prob.w2[o:o + w].T)
+        gh[r0:r1, :w] = ghe
+        gw2[o:o + w] = rb(fwd["h"][r0:r1, :w].T @ gy[r0:r1])
+        pre = fwd["pre_act"][r0:r1, :w]
+        gae = rb(torch.where(pre > 0, ghe * 2.0 * pre, torch.zeros_like(pre)))
+        ga[r0:r1, :w] = gae
+        gxg[r0:r1] = rb(gae @ prob.w1[:, o:o + w].T)
+        gw1[:, o:o + w] = rb(fwd["x_gathered"][r0:r1].T @ gae)
+    gx = combine(gxg, r["assignment_row"], None, k, T, mode)
+    return {"grad_x": gx, "grad_w1": gw1, "grad_w2": gw2, "grad_y": gy, "grad_h": gh,
+            "grad_a": ga, "grad_xg": gxg}
+
+
+def aux_losses(router_logits: torch.Tensor, tokens_per_expert, widths, expert_sizes,
+               dtype=torch.bfloat16) -> dict:
+    """Auxiliary losses of TritonMoEMLP.forward (triton_moe/moe.py:253-303), in float64."""
+    L = router_logits.to(torch.float64)
+    probs = torch.sigmoid(L)
+    E = len(widths)
+    z_loss = torch.logsumexp(L, dim=-1).pow(2).mean()
+    tpe = torch.as_tensor(np.asarray(tokens_per_expert), dtype=torch.float64)
+    f_i = (tpe / tpe.sum()).to(dtype)
+    p_i = probs.mean(dim=0)
+    fi = f_i.to(torch.float64)
+    if len(set(widths)) == 1:
+        lb = E * (fi @ p_i)
+    else:
+        groups = []
+        e = 0
+        for count, _ in expert_sizes:
+            if count > 1:
+                groups.append(list(range(e, e + count)))
+            e += count
+        if not groups:
+            lb = fi @ p_i
+        else:
+            fp = fi * p_i
+            lb = torch.stack([len(gr) * fp[gr].sum() for gr in groups]).mean()
+    mean_w = sum(widths) / E
+    wn = torch.tensor([w / mean_w for w in widths], dtype=torch.float32).to(dtype)
+    compute = (probs @ wn.to(torch.float64)).mean()
+    return {"router_z_loss": z_loss, "load_balance_loss": lb, "compute_loss": compute, "f_i": f_i}

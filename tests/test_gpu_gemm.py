@@ -1,0 +1,266 @@
+"""Grouped GEMMs on the GPU against per-expert fp32 references of the same op
+(reference kernels: triton_moe/kernels/grouped_gemm.py:212-1162).
+
+References round to bf16 exactly where the reference kernels store bf16, so
+the only difference left is fp32 summation order (tolerance TIGHT, normwise).
+Tail columns and uncovered rows must be exactly zero, as the reference's
+torch.zeros outputs are.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import route as oroute
+from oracle.eager import bf, expert_layout
+from triton_moe.kernels import (
+    grouped_gemm_down,
+    grouped_gemm_down_autograd,
+    grouped_gemm_down_backward,
+    grouped_gemm_up,
+    grouped_gemm_up_autograd,
+    grouped_gemm_up_backward,
+)
+
+from _util import TIGHT, assert_close_norm, expert_rows
+
+pytestmark = pytest.mark.gpu
+
+# (tokens, hidden, expert sizes, top_k, block, skew)
+CASES = [
+    (128, 128, [(4, 256)], 2, 128, False),            # reference "small" fixture
+    (1024, 256, [(8, 512)], 2, 128, False),           # reference "uniform"
+    (1024, 256, [(4, 512), (4, 256)], 2, 128, False),  # reference "variable"
+    (256, 64, [(2, 64), (2, 128)], 2, 64, False),      # tiles wider than the problem
+    (2048, 768, [(4, 512), (8, 256), (4, 128)], 2, 64, False),  # config-2 widths
+    (2048, 1024, [(64, 256)], 8, 64, True),            # config-3 shape, skewed, empties
+]
+IDS = ["small", "uniform", "variable", "tiny_tiles", "var3", "skew64"]
+
+
+def _case(T, d, sizes, k, b, skew, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    widths, offsets = expert_layout(sizes)
+    E, W, max_w = len(widths), offsets[-1], max(widths)
+    logits = torch.randn(T, E, generator=g)
+    if skew:
+        logits[:, : E // 8] += 4.0   # hot experts
+        logits[:, E - 4:] -= 50.0    # experts that receive nothing
+    sel = torch.topk(logits, k, dim=-1).indices
+    r = oroute.route(sel.reshape(-1).numpy(), E, b, "up")
+    pb = torch.from_numpy(r["padded_bins"]).int()
+    eto = torch.cat([torch.zeros(1, dtype=torch.int32), pb])
+    tpe = torch.diff(eto)
+    P = int(eto[-1])
+    xg = torch.randn(P, d, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(d, W, generator=g) * 0.05).to(torch.bfloat16)
+    w2 = (torch.randn(W, d, generator=g) * 0.05).to(torch.bfloat16)
+    return dict(widths=widths, offsets=offsets, E=E, W=W, max_w=max_w, d=d, P=P, eto=eto,
+                tpe=tpe, ewo=torch.tensor(offsets, dtype=torch.int32),
+                wid=torch.tensor(widths, dtype=torch.int32), xg=xg, w1=w1, w2=w2,
+                rows=expert_rows(r["padded_bins"]), route=r, k=k, T=T)
+
+
+def _meta_dev(c, device):
+    return [c[n].to(device) for n in ("eto", "ewo", "wid", "tpe")]
+
+
+def _ref_up(c, xg):
+    P, max_w = c["P"], c["max_w"]
+    pre = torch.zeros(P, max_w)
+    h = torch.zeros(P, max_w)
+    for e, (r0, r1) in enumerate(c["rows"]):
+        w, o = c["widths"][e], c["offsets"][e]
+        z = xg[r0:r1].float() @ c["w1"][:, o:o + w].float()
+        pre[r0:r1, :w] = bf(torch.relu(z))
+        h[r0:r1, :w] = bf(torch.relu(z) ** 2)
+    return h, pre
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_up_down_forward(case, device):
+    c = _case(*case)
+    eto, ewo, wid, tpe = _meta_dev(c, device)
+    out, pre = grouped_gemm_up(c["xg"].to(device), c["w1"].to(device), eto, ewo, wid, tpe,
+                               c["max_w"], activation="relu_squared", save_pre_act=True)
+    h_ref, pre_ref = _ref_up(c, c["xg"])
+    assert out.shape == (c["P"], c["max_w"]) and out.dtype == torch.bfloat16
+    assert_close_norm(out, h_ref, TIGHT, "H")
+    assert_close_norm(pre, pre_ref, TIGHT, "PRE")
+    for e, (r0, r1) in enumerate(c["rows"]):
+        w = c["widths"][e]
+        assert (out[r0:r1, w:] == 0).all() and (pre[r0:r1, w:] == 0).all()
+    # down: feed the reference H with NaN in the tails (must never be read)
+    h_in = h_ref.clone()
+    for e, (r0, r1) in enumerate(c["rows"]):
+        h_in[r0:r1, c["widths"][e]:] = float("nan")
+    y = grouped_gemm_down(h_in.to(torch.bfloat16).to(device), c["w2"].to(device), eto, ewo,
+                          wid, tpe, c["d"])
+    y_ref = torch.zeros(c["P"], c["d"])
+    for e, (r0, r1) in enumerate(c["rows"]):
+        w, o = c["widths"][e], c["offsets"][e]
+        y_ref[r0:r1] = bf(h_ref[r0:r1, :w] @ c["w2"][o:o + w].float())
+    assert_close_norm(y, y_ref, TIGHT, "Y")
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+@pytest.mark.parametrize("fused_gather", [False, True])
+def test_backward_kernels(case, fused_gather, device):
+    c = _case(*case, seed=1)
+    eto, ewo, wid, tpe = _meta_dev(c, device)
+    P, d, max_w = c["P"], c["d"], c["max_w"]
+    g = torch.Generator().manual_seed(2)
+    h_ref, pre_ref = _ref_up(c, c["xg"])
+    gy = torch.randn(P, d, generator=g).to(torch.bfloat16)
+    # down backward
+    gh, gw2 = grouped_gemm_down_backward(gy.to(device), h_ref.to(torch.bfloat16).to(device),
+                                         c["w2"].to(device), eto, ewo, wid, tpe, d, max_w)
+    gh_ref = torch.zeros(P, max_w)
+    gw2_ref = torch.zeros(c["W"], d)
+    for e, (r0, r1) in enumerate(c["rows"]):
+        w, o = c["widths"][e], c["offsets"][e]
+        gh_ref[r0:r1, :w] = bf(gy[r0:r1].float() @ c["w2"][o:o + w].float().T)
+        gw2_ref[o:o + w] = bf(h_ref[r0:r1, :w].T @ gy[r0:r1].float())
+    assert_close_norm(gh, gh_ref, TIGHT, "GH")
+    assert_close_norm(gw2, gw2_ref, TIGHT, "GW2")
+    for e, (r0, r1) in enumerate(c["rows"]):
+        assert (gh[r0:r1, c["widths"][e]:] == 0).all()
+    # up backward, from the reference GH and PRE
+    ghb = gh_ref.to(torch.bfloat16)
+    if fused_gather:
+        # x_flat with a gather map: rows of xg come from x_flat[gm]
+        T = c["P"] // 2 + 1
+        x_flat = torch.randn(T, d, generator=g).to(torch.bfloat16)
+        gm = torch.randint(0, T, (P,), generator=g, dtype=torch.int32)
+        xs = x_flat[gm.long()]
+        x_arg, gm_arg = x_flat.to(device), gm.to(device)
+    else:
+        xs = c["xg"]
+        x_arg, gm_arg = c["xg"].to(device), None
+    gx, gw1 = grouped_gemm_up_backward(ghb.to(device), x_arg, c["w1"].to(device),
+                                       pre_ref.to(torch.bfloat16).to(device), eto, ewo, wid,
+                                       tpe, d, "relu_squared", gather_map=gm_arg)
+    ga = bf(torch.where(pre_ref > 0, gh_ref * 2.0 * pre_ref, torch.zeros_like(pre_ref)))
+    gx_ref = torch.zeros(P, d)
+    gw1_ref = torch.zeros(d, c["W"])
+    for e, (r0, r1) in enumerate(c["rows"]):
+        w, o = c["widths"][e], c["offsets"][e]
+        gx_ref[r0:r1] = bf(ga[r0:r1, :w] @ c["w1"][:, o:o + w].float().T)
+        gw1_ref[:, o:o + w] = bf(xs[r0:r1].float().T @ ga[r0:r1, :w])
+    assert_close_norm(gx, gx_ref, TIGHT, "GX")
+    assert_close_norm(gw1, gw1_ref, TIGHT, "GW1")
+
+
+def test_empty_experts_get_zero_weight_grads(device):
+    c = _case(512, 128, [(8, 128)], 1, 64, False)
+    # all tokens to expert 3 -> others empty
+    E = c["E"]
+    eto = torch.tensor([0, 0, 0, 0, 512, 512, 512, 512, 512], dtype=torch.int32)
+    tpe = torch.diff(eto)
+    xg = torch.randn(512, 128).to(torch.bfloat16).to(device)
+    gy = torch.randn(512, 128).to(torch.bfloat16).to(device)
+    h = torch.rand(512, 128).to(torch.bfloat16).to(device)
+    d_ = dict(eto=eto.to(device), ewo=c["ewo"].to(device), wid=c["wid"].to(device),
+              tpe=tpe.to(device))
+    _, gw2 = grouped_gemm_down_backward(gy, h, c["w2"].to(device), d_["eto"], d_["ewo"],
+                                        d_["wid"], d_["tpe"], 128, 128)
+    _, gw1 = grouped_gemm_up_backward(h, xg, c["w1"].to(device), h, d_["eto"], d_["ewo"],
+                                      d_["wid"], d_["tpe"], 128, "relu_squared")
+    for e in range(E):
+        if e != 3:
+            assert (gw2[e * 128:(e + 1) * 128] == 0).all()
+            assert (gw1[:, e * 128:(e + 1) * 128] == 0).all()
+    assert gw2[384:512].abs().sum() > 0 and gw1[:, 384:512].abs().sum() > 0
+
+
+def test_uncovered_rows_are_zero(device):
+    """tokens_per_expert below the offsets' range leaves rows zero (torch.zeros)."""
+    c = _case(256, 128, [(2, 128)], 1, 64, False)
+    eto = torch.tensor([0, 128, 256], dtype=torch.int32, device=device)
+    tpe = torch.tensor([64, 128], dtype=torch.int32, device=device)
+    xg = torch.randn(256, 128).to(torch.bfloat16).to(device)
+    out = grouped_gemm_up(xg, c["w1"].to(device), eto, c["ewo"].to(device),
+                          c["wid"].to(device), tpe, 128)
+    assert (out[64:128] == 0).all() and out[:64].abs().sum() > 0 and out[128:].abs().sum() > 0
+
+
+def test_activation_none_and_unknown(device):
+    c = _case(256, 128, [(2, 128)], 1, 64, False)
+    eto, ewo, wid, tpe = _meta_dev(c, device)
+    xg = c["xg"].to(device)
+    out, pre = grouped_gemm_up(xg, c["w1"].to(device), eto, ewo, wid, tpe, c["max_w"],
+                               activation="none", save_pre_act=True)
+    ref = torch.zeros(c["P"], c["max_w"])
+    for e, (r0, r1) in enumerate(c["rows"]):
+        w, o = c["widths"][e], c["offsets"][e]
+        ref[r0:r1, :w] = bf(c["xg"][r0:r1].float() @ c["w1"][:, o:o + w].float())
+    assert_close_norm(out, ref, TIGHT, "none")
+    assert (pre == 0).all()
+    out2 = grouped_gemm_up(xg, c["w1"].to(device), eto, ewo, wid, tpe, c["max_w"],
+                           activation="gelu")  # unknown -> none, as the reference
+    assert torch.equal(out, out2)
+    with pytest.raises(NotImplementedError):
+        grouped_gemm_up(xg, c["w1"].to(device), eto, ewo, wid, tpe, c["max_w"],
+                        activation="swiglu")
+
+
+def test_up_fwd_gather_map_path(device):
+    """grouped_gemm_up(x_flat, gather_map=gm) reads x_flat[gm[row]] (pad rows read row 0)."""
+    c = _case(512, 256, [(4, 128)], 2, 64, False)
+    eto, ewo, wid, tpe = _meta_dev(c, device)
+    T = 300
+    x_flat = torch.randn(T, 256).to(torch.bfloat16)
+    gm = torch.randint(0, T, (c["P"],), dtype=torch.int32)
+    out = grouped_gemm_up(x_flat.to(device), c["w1"].to(device), eto, ewo, wid, tpe,
+                          c["max_w"], gather_map=gm.to(device))
+    h_ref, _ = _ref_up(c, x_flat[gm.long()])
+    assert_close_norm(out, h_ref, TIGHT, "H gm")
+
+
+def test_autograd_entry_points(device):
+    """grouped_gemm_up_autograd -> grouped_gemm_down_autograd -> sum().backward()
+    (the reference's test_grouped_gemm_backward flow, in bf16)."""
+    c = _case(1024, 256, [(4, 256), (4, 128)], 2, 64, False, seed=3)
+    eto, ewo, wid, tpe = _meta_dev(c, device)
+    x = c["xg"].to(device).requires_grad_(True)
+    w1 = c["w1"].to(device).requires_grad_(True)
+    w2 = c["w2"].to(device).requires_grad_(True)
+    h = grouped_gemm_up_autograd(x, w1, eto, ewo, wid, tpe, c["max_w"], c["d"], "relu_squared")
+    y = grouped_gemm_down_autograd(h, w2, eto, ewo, wid, tpe, c["d"], c["max_w"])
+    # forward equals the raw kernels
+    raw = grouped_gemm_down(grouped_gemm_up(x.detach(), w1.detach(), eto, ewo, wid, tpe,
+                                            c["max_w"]), w2.detach(), eto, ewo, wid, tpe,
+                            c["d"])
+    assert torch.equal(y.detach(), raw)
+    y.sum().backward()
+    for t in (x, w1, w2):
+        assert t.grad is not None and torch.isfinite(t.grad.float()).all()
+        assert t.grad.abs().sum() > 0
+    # against the per-expert fp32 reference with the same bf16 rounding points
+    h_ref, pre_ref = _ref_up(c, c["xg"])
+    gy = torch.ones(c["P"], c["d"])
+    gx_ref = torch.zeros(c["P"], c["d"])
+    gw1_ref = torch.zeros_like(c["w1"], dtype=torch.float32)
+    gw2_ref = torch.zeros_like(c["w2"], dtype=torch.float32)
+    for e, (r0, r1) in enumerate(c["rows"]):
+        w, o = c["widths"][e], c["offsets"][e]
+        ghe = bf(gy[r0:r1] @ c["w2"][o:o + w].float().T)
+        gw2_ref[o:o + w] = bf(h_ref[r0:r1, :w].T @ gy[r0:r1])
+        pre = pre_ref[r0:r1, :w]
+        ga = bf(torch.where(pre > 0, ghe * 2.0 * pre, torch.zeros_like(pre)))
+        gx_ref[r0:r1] = bf(ga @ c["w1"][:, o:o + w].float().T)
+        gw1_ref[:, o:o + w] = bf(c["xg"][r0:r1].float().T @ ga)
+    assert_close_norm(x.grad, gx_ref, TIGHT, "x.grad")
+    assert_close_norm(w1.grad, gw1_ref, TIGHT, "w1.grad")
+    assert_close_norm(w2.grad, gw2_ref, TIGHT, "w2.grad")
+
+
+def test_fp32_inputs_not_supported(device):
+    """The reference also accepts fp32 (tf32 tl.dot); here bf16 only, loudly."""
+    eto = torch.tensor([0, 128, 256], dtype=torch.int32, device=device)
+    wid = torch.tensor([128, 128], dtype=torch.int32, device=device)
+    x = torch.randn(256, 64, device=device)
+    w1 = torch.randn(64, 256, device=device)
+    with pytest.raises(NotImplementedError, match="bfloat16"):
+        grouped_gemm_up(x, w1, eto, eto, wid, wid, 128)

@@ -1,0 +1,197 @@
+"""TritonMoEMLP on the GPU against the eager per-expert-loop oracle.
+
+Protocol: the oracle consumes the device module's own routing decision
+(selected experts and bf16 weights, recomputed with the module's router on
+the same inputs), upcasts the bf16 parameters exactly to fp32, and detaches
+the routing weights (the reference gives them no gradient, scatter.py:176).
+Tolerances are normwise (max|d|/max|ref|, mean|d|/mean|ref|): TIGHT against
+the bf16-faithful oracle, LOOSE against the unrounded fp32 oracle.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import eager
+from triton_moe import TritonMoEConfig, TritonMoEMLP
+
+from _util import LOOSE, TIGHT, assert_close_norm, bits_equal, make_problem, zipf_bias
+
+pytestmark = pytest.mark.gpu
+
+# name: (batch, seq, n_embd, expert_sizes, top_k, block_size, zipf)
+CONFIGS = {
+    "ref_small": (2, 64, 128, [(4, 256)], 2, 128, False),
+    "ref_uniform": (4, 256, 256, [(8, 512)], 2, 128, False),
+    "ref_variable": (4, 256, 256, [(4, 512), (4, 256)], 2, 128, False),
+    "cfg0_shape": (8, 512, 256, [(8, 512)], 2, 64, False),
+    "cfg1": (8, 1024, 768, [(8, 512)], 2, 64, False),
+    "cfg2": (8, 2048, 768, [(4, 512), (8, 256), (4, 128)], 2, 64, False),
+    "cfg3": (1, 16384, 1024, [(64, 256)], 8, 64, True),
+}
+
+
+def _module(p, d, sizes, k, b, device):
+    cfg = TritonMoEConfig(n_embd=d, expert_sizes=sizes, num_active_experts=k, block_size=b)
+    m = TritonMoEMLP(cfg).to(device).to(torch.bfloat16)
+    with torch.no_grad():
+        m.router.weight.copy_(p["wr"])
+        m.w1.copy_(p["w1"])
+        m.w2.copy_(p["w2"])
+    return m
+
+
+def _run(name, device, seed=0):
+    B, S, d, sizes, k, b, zipf = CONFIGS[name]
+    E = sum(c for c, _ in sizes)
+    bias = zipf_bias(E, alpha=3.0) if zipf else None
+    p = make_problem(B * S, d, sizes, k, b, seed=seed, skew=bias, device=device)
+    m = _module(p, d, sizes, k, b, device)
+    if bias is not None:
+        m.router.register_forward_hook(lambda mod, inp, out: out + bias.to(out.device, out.dtype))
+    x = p["x"].view(B, S, d).to(device).requires_grad_(True)
+    out, aux, f_i = m(x)
+    with torch.no_grad():
+        _, _, wts, sel = m._router(x.detach().reshape(-1, d))
+    prob = eager.Problem(p["x"].float(), p["w1"].float(), p["w2"].float(), p["widths"],
+                         p["offsets"], sel.cpu(), wts.cpu().float(), b)
+    return m, x, out, aux, f_i, prob
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_forward_backward_vs_oracle(name, device):
+    m, x, out, aux, f_i, prob = _run(name, device)
+    T, d = prob.x.shape
+    assert out.shape == x.shape and out.dtype == torch.bfloat16
+    fb = eager.forward(prob, "bf16")
+    ff = eager.forward(prob, "fp32")
+    o = out.detach().reshape(T, d)
+    assert_close_norm(o, fb["out"], TIGHT, f"{name} out vs bf16 oracle")
+    assert_close_norm(o, ff["out"], LOOSE, f"{name} out vs fp32 oracle")
+    # upstream gradient: random (exercises the weighted gather) for small
+    # configs, ones (out.sum()) for the large ones
+    if T <= 4096:
+        G = torch.randn(T, d, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+        out.backward(G.to(device).view_as(out))
+    else:
+        G = torch.ones(T, d, dtype=torch.bfloat16)
+        out.sum().backward()
+    bb = eager.backward(prob, fb, G.float(), "bf16")
+    bf_ = eager.backward(prob, ff, G.float(), "fp32")
+    for got, key in ((x.grad.reshape(T, d), "grad_x"), (m.w1.grad, "grad_w1"),
+                     (m.w2.grad, "grad_w2")):
+        assert_close_norm(got, bb[key], TIGHT, f"{name} {key} vs bf16 oracle")
+        assert_close_norm(got, bf_[key], LOOSE, f"{name} {key} vs fp32 oracle")
+    assert m.router.weight.grad is None
+
+
+def test_aux_losses_and_f_i(device):
+    m, x, out, aux, f_i, prob = _run("cfg2", device)
+    with torch.no_grad():
+        logits = m.router(x.detach().reshape(-1, x.shape[-1]))
+    r = eager.route(prob)
+    ref = eager.aux_losses(logits.float().cpu(), r["tokens_per_expert"], prob.widths,
+                           CONFIGS["cfg2"][3])
+    assert torch.equal(f_i.cpu(), ref["f_i"])
+    for key in ("router_z_loss", "load_balance_loss", "compute_loss"):
+        assert abs(aux[key].item() - ref[key].item()) <= 1e-3 * abs(ref[key].item()) + 1e-6, key
+
+
+def test_forward_with_intermediates(device):
+    m, x, out, aux, f_i, prob = _run("ref_variable", device)
+    with torch.no_grad():
+        inter = m.forward_with_intermediates(x.detach())
+    r = eager.route(prob)
+    for key in ("bin_ids", "indices", "tokens_per_expert", "bins", "padded_bins"):
+        assert torch.equal(inter[key].cpu(), torch.from_numpy(r[key])), key
+    fb = eager.forward(prob, "bf16", r)
+    assert bits_equal(inter["x_gathered"], fb["x_gathered"].to(torch.bfloat16))
+    assert_close_norm(inter["x_after_up"], fb["h"], TIGHT, "x_after_up")
+    assert_close_norm(inter["x_after_down"], fb["y"], TIGHT, "x_after_down")
+    assert_close_norm(inter["output"].reshape(fb["out"].shape), fb["out"], TIGHT, "output")
+    # the sync-free module path and the public-API path agree bit for bit
+    assert bits_equal(inter["output"], out.detach())
+    assert set(inter) >= {"x_flat", "router_logits", "router_probs", "top_k_weights",
+                          "top_k_weights_flat", "selected_experts", "selected_experts_flat",
+                          "x_scattered"}
+
+
+def test_forward_deterministic(device):
+    m, x, out1, _, _, _ = _run("cfg1", device)
+    out1.sum().backward()
+    g1 = (x.grad.clone(), m.w1.grad.clone(), m.w2.grad.clone())
+    x.grad = None
+    m.zero_grad(set_to_none=True)
+    out2, _, _ = m(x)
+    out2.sum().backward()
+    assert bits_equal(out1, out2)
+    for a, b in zip(g1, (x.grad, m.w1.grad, m.w2.grad)):
+        assert bits_equal(a, b)
+
+
+def test_forward_profiled(device):
+    m, x, out, aux, f_i, _ = _run("ref_small", device)
+
+    class StepRecorder:
+        def __init__(self):
+            self.names = []
+
+        def step(self, name):
+            import contextlib
+
+            self.names.append(name)
+            return contextlib.nullcontext()
+
+    rec = StepRecorder()
+    out2, aux2, f2 = m.forward_profiled(x.detach(), rec)
+    assert rec.names == ["flatten", "routing", "fused_route", "gather", "gemm_up", "gemm_down",
+                         "scatter", "reshape", "aux_loss"]
+    assert bits_equal(out2, out.detach()) and torch.equal(f2, f_i)
+
+
+def test_config4_full_size_sampled(device):
+    """BASELINE config 4 at full size (d=2048, 128 variable experts, k=8,
+    T=32768): outputs and x.grad are row-local, so a random sample of tokens
+    is checked exactly against the bf16 oracle restricted to those tokens;
+    weight gradients are checked on sampled columns with all their rows."""
+    B, S, d, sizes, k, b = 1, 32768, 2048, [(32, 1024), (64, 512), (32, 256)], 8, 64
+    p = make_problem(B * S, d, sizes, k, b, seed=4, device=device)
+    m = _module(p, d, sizes, k, b, device)
+    x = p["x"].view(B, S, d).to(device).requires_grad_(True)
+    out, _, _ = m(x)
+    out.sum().backward()
+    with torch.no_grad():
+        _, _, wts, sel = m._router(x.detach().reshape(-1, d))
+    g = torch.Generator().manual_seed(0)
+    tok = torch.randperm(S, generator=g)[:192].sort().values
+    sub = eager.Problem(p["x"][tok].float(), p["w1"].float(), p["w2"].float(), p["widths"],
+                        p["offsets"], sel.cpu()[tok], wts.cpu()[tok].float(), b)
+    fb = eager.forward(sub, "bf16")
+    assert_close_norm(out.detach().reshape(S, d)[tok.to(device)], fb["out"], TIGHT, "cfg4 out")
+    bb = eager.backward(sub, fb, torch.ones(len(tok), d), "bf16")
+    assert_close_norm(x.grad.reshape(S, d)[tok.to(device)], bb["grad_x"], TIGHT, "cfg4 x.grad")
+    # weight gradients: full oracle on a few experts' columns (all their tokens)
+    full = eager.Problem(p["x"].float(), p["w1"].float(), p["w2"].float(), p["widths"],
+                         p["offsets"], sel.cpu(), wts.cpu().float(), b)
+    r = eager.route(full)
+    for e in (0, 40, 127):
+        w, o = p["widths"][e], p["offsets"][e]
+        r0 = int(r["padded_bins"][e - 1]) if e else 0
+        r1 = int(r["padded_bins"][e])
+        rs = torch.from_numpy(r["row_src"][r0:r1]).long()
+        ok = rs >= 0
+        xe = torch.zeros(r1 - r0, d)
+        xe[ok] = p["x"][rs[ok] // k].float()
+        we = torch.zeros(r1 - r0)
+        we[ok] = wts.cpu().float().reshape(-1)[rs[ok]]
+        z = xe @ p["w1"][:, o:o + w].float()
+        pre = eager.bf(torch.relu(z))
+        h = eager.bf(torch.relu(z) ** 2)
+        gy = eager.bf(torch.ones(r1 - r0, d) * we[:, None])
+        gh = eager.bf(gy @ p["w2"][o:o + w].float().T)
+        ga = eager.bf(torch.where(pre > 0, gh * 2.0 * pre, torch.zeros_like(pre)))
+        gw2 = eager.bf(h.T @ gy)
+        gw1 = eager.bf(xe.T @ ga)
+        assert_close_norm(m.w2.grad[o:o + w], gw2, TIGHT, f"cfg4 gw2 e{e}")
+        assert_close_norm(m.w1.grad[:, o:o + w], gw1, TIGHT, f"cfg4 gw1 e{e}")

@@ -1,0 +1,138 @@
+"""Gather / weighted gather / combine on the GPU are bit-exact with the
+oracle (reference gather.py:34-60, 145-174 and scatter.py:35-69, 133)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import eager
+from oracle import route as oroute
+from triton_moe.kernels import (
+    fused_route,
+    padded_gather,
+    padded_gather_autograd,
+    padded_scatter,
+    padded_scatter_autograd,
+)
+from triton_moe.kernels.gather import combine_rows, gather_rows
+from triton_moe.kernels.fused_cumsum import check_route, route_device
+
+from _util import bits_equal
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(T, d, E, k, b, device, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, d, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, generator=g)
+    wts, sel = torch.topk(torch.sigmoid(logits), k, dim=-1)
+    wts = (wts / wts.sum(-1, keepdim=True)).to(torch.bfloat16)
+    r = oroute.route(sel.reshape(-1).numpy(), E, b, "up")
+    maps = oroute.row_maps(r["indices"], r["bin_ids"], r["bins"], r["padded_bins"], k,
+                           num_assignments=T * k)
+    return x, sel, wts, r, maps
+
+
+def _ref_gather(x, maps, k, w=None):
+    rs = torch.from_numpy(maps["row_src"]).long()
+    out = torch.zeros(rs.numel(), x.shape[1], dtype=torch.bfloat16)
+    ok = rs >= 0
+    v = x[rs[ok] // k].float()
+    if w is not None:
+        v = v * w.reshape(-1)[rs[ok]].float()[:, None]
+    out[ok] = v.to(torch.bfloat16)
+    return out
+
+
+@pytest.mark.parametrize("T,d,E,k,b", [(128, 128, 4, 2, 128), (1024, 256, 8, 2, 128),
+                                       (2048, 768, 16, 2, 64), (1024, 1024, 64, 8, 64),
+                                       (300, 100, 5, 2, 8), (257, 2056, 7, 3, 64)])
+def test_gather_and_weighted_gather_exact(T, d, E, k, b, device):
+    x, sel, wts, r, maps = _setup(T, d, E, k, b, device)
+    dev = lambda a: torch.as_tensor(a).to(device)  # noqa: E731
+    P = int(r["padded_bins"][-1])
+    got = padded_gather(x.to(device), dev(r["indices"]), dev(r["bin_ids"]), dev(r["bins"]),
+                        dev(r["padded_bins"]), k)
+    assert got.shape == (P, d)
+    assert bits_equal(got, _ref_gather(x, maps, k))
+    rs = dev(maps["row_src"])
+    gw = gather_rows(x.to(device), rs, k, P, weights=wts.reshape(-1).to(device))
+    assert bits_equal(gw, _ref_gather(x, maps, k, wts))
+
+
+@pytest.mark.parametrize("T,d,E,k,b", [(128, 128, 4, 2, 128), (1024, 256, 8, 2, 128),
+                                       (1024, 1024, 64, 8, 64), (300, 100, 5, 2, 8),
+                                       (100, 2056, 6, 4, 16)])
+def test_combine_exact(T, d, E, k, b, device):
+    x, sel, wts, r, maps = _setup(T, d, E, k, b, device, seed=1)
+    P = int(r["padded_bins"][-1])
+    y = torch.randn(P, d, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    ar = torch.from_numpy(maps["assignment_row"])
+    ref_w = eager.combine(y.float(), ar.numpy(), wts.reshape(-1).float(), k, T, "bf16")
+    ref_u = eager.combine(y.float(), ar.numpy(), None, k, T, "bf16")
+    got_w = combine_rows(y.to(device), ar.to(device), k, T, weights=wts.reshape(-1).to(device))
+    got_u = combine_rows(y.to(device), ar.to(device), k, T)
+    assert bits_equal(got_w, ref_w.to(torch.bfloat16))
+    assert bits_equal(got_u, ref_u.to(torch.bfloat16))
+    dev = lambda a: torch.as_tensor(a).to(device)  # noqa: E731
+    pub = padded_scatter(y.to(device), dev(r["indices"]), dev(r["bin_ids"]),
+                         wts.reshape(-1).to(device), dev(r["bins"]), dev(r["padded_bins"]), k)
+    assert bits_equal(pub, ref_w.to(torch.bfloat16))
+
+
+def test_autograd_gather_scatter(device):
+    T, d, E, k, b = 512, 256, 8, 2, 64
+    x, sel, wts, r, maps = _setup(T, d, E, k, b, device, seed=3)
+    dev = lambda a: torch.as_tensor(a).to(device)  # noqa: E731
+    idx, bid, bins, pb = (dev(r["indices"]), dev(r["bin_ids"]), dev(r["bins"]),
+                          dev(r["padded_bins"]))
+    xg = x.to(device).requires_grad_(True)
+    g = padded_gather_autograd(xg, idx, bid, bins, pb, k)
+    G = torch.randn(g.shape, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    g.backward(G.to(device))
+    ar = maps["assignment_row"]
+    ref_gx = eager.combine(G.float(), ar, None, k, T, "bf16").to(torch.bfloat16)
+    assert bits_equal(xg.grad, ref_gx)
+    # scatter backward = weighted gather (pad rows zero); weights get no grad
+    P = int(r["padded_bins"][-1])
+    y = torch.randn(P, d, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    yd = y.to(device).requires_grad_(True)
+    wd = wts.reshape(-1).to(device).requires_grad_(True)
+    out = padded_scatter_autograd(yd, idx, bid, wd, bins, pb, k)
+    GO = torch.randn(out.shape, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    out.backward(GO.to(device))
+    assert bits_equal(yd.grad, _ref_gather(GO, maps, k, wts))
+    assert wd.grad is None
+
+
+def test_strided_and_broadcast_inputs(device):
+    """Row strides other than hidden (views) and stride-0 grads (out.sum())."""
+    T, d, E, k, b = 256, 128, 4, 2, 64
+    x, sel, wts, r, maps = _setup(T, d, E, k, b, device, seed=7)
+    wide = torch.zeros(T, d + 64, dtype=torch.bfloat16)
+    wide[:, :d] = x
+    dev = lambda a: torch.as_tensor(a).to(device)  # noqa: E731
+    got = padded_gather(wide.to(device)[:, :d], dev(r["indices"]), dev(r["bin_ids"]),
+                        dev(r["bins"]), dev(r["padded_bins"]), k)
+    assert bits_equal(got, _ref_gather(x, maps, k))
+    yd = got.clone().requires_grad_(True)
+    out = padded_scatter_autograd(yd, dev(r["indices"]), dev(r["bin_ids"]),
+                                  wts.reshape(-1).to(device), dev(r["bins"]),
+                                  dev(r["padded_bins"]), k)
+    out.sum().backward()
+    ones = torch.ones(T, d, dtype=torch.bfloat16)
+    assert bits_equal(yd.grad, _ref_gather(ones, maps, k, wts))
+
+
+def test_route_maps_feed_permutation(device):
+    """route_device's own maps give the same gather as the public API."""
+    T, d, E, k = 1000, 256, 16, 4
+    x, sel, wts, r, maps = _setup(T, d, E, k, 64, device, seed=8)
+    rd = route_device(sel.reshape(-1).to(device), E, k, 64)
+    P, _ = check_route(rd)
+    got = gather_rows(x.to(device), rd.row_src, k, P)
+    assert bits_equal(got, _ref_gather(x, maps, k))
+    pub = fused_route(sel.reshape(-1).to(device), E, block_size=64)
+    assert torch.equal(pub[1].cpu(), torch.from_numpy(r["indices"]))

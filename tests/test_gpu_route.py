@@ -1,0 +1,108 @@
+"""Routing on the GPU is bit-exact with the oracle (fused_route semantics,
+triton_moe/kernels/fused_cumsum.py:85-171 and grouped_gemm.py:104-149)."""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import route as oroute
+from triton_moe.kernels import fused_route, precompute_gather_map
+from triton_moe.kernels.fused_cumsum import check_route, route_device
+
+from _util import zipf_bias
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "route_cases.json").read_text())
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("case", GOLDEN, ids=[c["name"] for c in GOLDEN])
+@pytest.mark.parametrize("dtype", [torch.int64, torch.int32])
+def test_route_golden(case, dtype, device):
+    sel = torch.tensor(case["selected"], dtype=dtype, device=device)
+    E, k, b, mode = case["num_experts"], case["top_k"], case["block_size"], case["rounding"]
+    exp = case["expected"]
+    r = route_device(sel, E, k, b, mode)
+    P, n = check_route(r)
+    assert P == (exp["padded_bins"][-1] if E else 0)
+    assert n == len(exp["bin_ids"])
+    np.testing.assert_array_equal(_np(r.bin_ids[:n]), exp["bin_ids"])
+    np.testing.assert_array_equal(_np(r.indices[:n]), exp["indices"])
+    np.testing.assert_array_equal(_np(r.tokens_per_expert), exp["tokens_per_expert"])
+    np.testing.assert_array_equal(_np(r.bins), exp["bins"])
+    np.testing.assert_array_equal(_np(r.padded_bins), exp["padded_bins"])
+    np.testing.assert_array_equal(_np(r.row_src[:P]), exp["row_src"])
+    np.testing.assert_array_equal(_np(r.gather_map[:P]), exp["gather_map"])
+    np.testing.assert_array_equal(_np(r.assignment_row), exp["assignment_row"])
+    # public entry point
+    out = fused_route(sel, E, block_size=b, rounding=mode)
+    for t, key in zip(out, ("bin_ids", "indices", "tokens_per_expert", "bins", "padded_bins")):
+        assert t.dtype == torch.int32
+        np.testing.assert_array_equal(_np(t), exp[key], err_msg=key)
+    if mode == "up" and len(case["selected"]):
+        gm = precompute_gather_map(out[1], out[0], out[3], out[4], k)
+        np.testing.assert_array_equal(_np(gm), exp["gather_map"])
+
+
+# (tokens, top_k, experts, block): the BASELINE.json shapes and the reference's
+# test fixtures (b=128), random top-k routing on the device.
+SHAPES = [(2 * 64, 2, 4, 128), (4 * 256, 2, 8, 128), (8 * 512, 2, 8, 64),
+          (8 * 1024, 2, 8, 64), (8 * 2048, 2, 16, 64), (16384, 8, 64, 64),
+          (32768, 8, 128, 64), (4096, 8, 1000, 16)]
+
+
+@pytest.mark.parametrize("T,k,E,b", SHAPES)
+@pytest.mark.parametrize("mode", ["up", "nearest", "down"])
+def test_route_random_topk(T, k, E, b, mode, device):
+    g = torch.Generator(device=device).manual_seed(T + E)
+    logits = torch.randn(T, E, device=device, generator=g)
+    if E == 64:
+        logits = logits + zipf_bias(E, alpha=3.0).to(device)
+    sel = torch.topk(logits, k, dim=-1).indices.reshape(-1)
+    r = route_device(sel, E, k, b, mode)
+    P, n = check_route(r)
+    ref = oroute.route(_np(sel), E, b, mode)
+    maps = oroute.row_maps(ref["indices"], ref["bin_ids"], ref["bins"], ref["padded_bins"], k,
+                           num_assignments=sel.numel())
+    assert P == int(ref["padded_bins"][-1]) and n == ref["bin_ids"].size
+    np.testing.assert_array_equal(_np(r.bin_ids[:n]), ref["bin_ids"])
+    np.testing.assert_array_equal(_np(r.indices[:n]), ref["indices"])
+    for key in ("tokens_per_expert", "bins", "padded_bins"):
+        np.testing.assert_array_equal(_np(getattr(r, key)), ref[key], err_msg=key)
+    np.testing.assert_array_equal(_np(r.row_src[:P]), maps["row_src"])
+    np.testing.assert_array_equal(_np(r.gather_map[:P]), maps["gather_map"])
+    np.testing.assert_array_equal(_np(r.assignment_row), maps["assignment_row"])
+
+
+def test_route_deterministic_and_large(device):
+    T, k, E = 65536, 8, 256
+    sel = torch.randint(0, E, (T * k,), device=device)
+    a = route_device(sel, E, k, 64)
+    b = route_device(sel, E, k, 64)
+    torch.cuda.synchronize()
+    for x, y in ((a.indices, b.indices), (a.row_src, b.row_src), (a.padded_bins, b.padded_bins)):
+        assert torch.equal(x, y)
+    ref = oroute.route(_np(sel), E, 64, "up")
+    np.testing.assert_array_equal(_np(a.indices), ref["indices"])
+
+
+def test_route_bad_ids_raise(device):
+    with pytest.raises(RuntimeError, match="outside"):
+        fused_route(torch.tensor([0, 7, 1], device=device), 4)
+    with pytest.raises(RuntimeError, match="outside"):
+        fused_route(torch.tensor([0, -1, 1], device=device), 4)
+
+
+def test_route_empty(device):
+    out = fused_route(torch.empty(0, dtype=torch.int64, device=device), 5, block_size=64)
+    assert out[0].numel() == 0 and out[1].numel() == 0
+    assert out[2].tolist() == [0] * 5 and out[4].tolist() == [0] * 5

@@ -1,0 +1,121 @@
+"""Pins the eager per-expert-loop oracle (oracle/eager.py) on the CPU.
+
+* fp32 mode (run in float64) against a dense all-experts formulation with a
+  routing-weight matrix (no sorting, padding or gather), forward and torch
+  autograd gradients.
+* bf16 mode against hand-computed values where each rounding point changes
+  the result, and against the fp32 mode within bf16 precision.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import eager
+
+
+def _problem(seed, T, d, sizes, k, b, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    widths, offsets = eager.expert_layout(sizes)
+    E, W = len(widths), offsets[-1]
+    x = torch.randn(T, d, generator=g, dtype=dtype)
+    w1 = torch.randn(d, W, generator=g, dtype=dtype) * 0.3
+    w2 = torch.randn(W, d, generator=g, dtype=dtype) * 0.3
+    logits = torch.randn(T, E, generator=g)
+    wts, sel = torch.topk(torch.sigmoid(logits), k, dim=-1)
+    wts = (wts / wts.sum(-1, keepdim=True)).to(torch.bfloat16).to(dtype)
+    return eager.Problem(x, w1, w2, widths, offsets, sel, wts, b)
+
+
+def _dense(prob, x, w1, w2):
+    E = prob.num_experts
+    R = torch.zeros(x.shape[0], E, dtype=x.dtype)
+    R.scatter_add_(1, prob.selected, prob.weights.to(x.dtype))
+    out = torch.zeros_like(x)
+    for e, (w, o) in enumerate(zip(prob.widths, prob.offsets)):
+        h = torch.relu(x @ w1[:, o:o + w]) ** 2
+        out = out + R[:, e:e + 1] * (h @ w2[o:o + w])
+    return out
+
+
+@pytest.mark.parametrize("sizes,k,b", [([(4, 16)], 2, 4), ([(2, 24), (3, 8), (1, 16)], 3, 8),
+                                       ([(8, 8)], 8, 16)])
+def test_fp32_forward_backward_vs_dense(sizes, k, b):
+    prob = _problem(0, 37, 12, sizes, k, b)
+    fwd = eager.forward(prob, "fp32")
+    x = prob.x.clone().requires_grad_(True)
+    w1 = prob.w1.clone().requires_grad_(True)
+    w2 = prob.w2.clone().requires_grad_(True)
+    ref = _dense(prob, x, w1, w2)
+    torch.testing.assert_close(fwd["out"], ref.detach(), rtol=1e-10, atol=1e-12)
+    G = torch.randn(ref.shape, generator=torch.Generator().manual_seed(1), dtype=ref.dtype)
+    ref.backward(G)
+    bwd = eager.backward(prob, fwd, G, "fp32")
+    torch.testing.assert_close(bwd["grad_x"], x.grad, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(bwd["grad_w1"], w1.grad, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(bwd["grad_w2"], w2.grad, rtol=1e-10, atol=1e-12)
+
+
+def test_fp32_gradcheck_dense():
+    """The dense formulation's autograd against finite differences (float64)."""
+    prob = _problem(3, 5, 4, [(3, 4)], 2, 2)
+
+    def f(x, w1, w2):
+        return _dense(prob, x, w1, w2)
+
+    args = [prob.x.clone().requires_grad_(True), prob.w1.clone().requires_grad_(True),
+            prob.w2.clone().requires_grad_(True)]
+    assert torch.autograd.gradcheck(f, args)
+
+
+def test_bf16_rounding_points_by_hand():
+    # One token, one expert of width 1: pre = 1 + 2^-7 (exact in bf16),
+    # pre^2 = 1 + 2^-6 + 2^-14 rounds to 1 + 2^-6 when H is stored as bf16.
+    f = torch.float32
+    pre = 1.0 + 2.0 ** -7
+    x = torch.tensor([[1.0]], dtype=f)
+    w1 = torch.tensor([[pre]], dtype=f)
+    w2 = torch.tensor([[1.0]], dtype=f)
+    prob = eager.Problem(x, w1, w2, [1], [0, 1], torch.tensor([[0]]),
+                         torch.tensor([[1.0]], dtype=f), 1)
+    out_bf = eager.forward(prob, "bf16")["out"].item()
+    out_fp = eager.forward(prob, "fp32")["out"].item()
+    assert out_bf == 1.0 + 2.0 ** -6
+    assert out_fp == pytest.approx(pre * pre, rel=1e-7) and out_fp != out_bf
+    # GA = bf16(2 * GH * PRE): GH = 1 + 2^-7 (w2 = that, G = 1) -> 2 * (1+2^-7)^2
+    # = 2 + 2^-5 + 2^-13 -> bf16 2 + 2^-5
+    w2b = torch.tensor([[pre]], dtype=f)
+    prob2 = eager.Problem(x, w1, w2b, [1], [0, 1], torch.tensor([[0]]),
+                          torch.tensor([[1.0]], dtype=f), 1)
+    fw = eager.forward(prob2, "bf16")
+    bw = eager.backward(prob2, fw, torch.ones(1, 1), "bf16")
+    assert bw["grad_a"][0, 0].item() == 2.0 + 2.0 ** -5
+    # combine: slot = bf16(y * w); y = 1 + 2^-7, w = 1 + 2^-7 -> 1 + 2^-6 + 2^-14 -> 1 + 2^-6
+    y = torch.tensor([[pre]], dtype=f)
+    out = eager.combine(y, [0], torch.tensor([pre], dtype=f), 1, 1, "bf16")
+    assert out.item() == 1.0 + 2.0 ** -6
+
+
+def test_bf16_mode_close_to_fp32_mode():
+    prob = _problem(5, 64, 32, [(2, 32), (4, 16)], 2, 8, dtype=torch.float32)
+    prob.x = prob.x.to(torch.bfloat16).float()
+    prob.w1 = prob.w1.to(torch.bfloat16).float()
+    prob.w2 = prob.w2.to(torch.bfloat16).float()
+    a = eager.forward(prob, "fp32")["out"]
+    b = eager.forward(prob, "bf16")["out"]
+    assert (a - b).abs().max() / a.abs().max() < 2e-2
+    assert (a - b).abs().mean() / a.abs().mean() < 1e-2
+
+
+def test_aux_losses_uniform_and_grouped():
+    g = torch.Generator().manual_seed(0)
+    L = torch.randn(50, 8, generator=g)
+    tpe = [5, 7, 0, 10, 12, 6, 4, 6]
+    a = eager.aux_losses(L, tpe, [64] * 8, [(8, 64)])
+    p = torch.sigmoid(L.double())
+    f = (torch.tensor(tpe, dtype=torch.float64) / sum(tpe)).to(torch.bfloat16).double()
+    assert torch.allclose(a["load_balance_loss"], 8 * (f * p.mean(0)).sum())
+    b = eager.aux_losses(L, tpe, [64] * 4 + [32] * 4, [(4, 64), (4, 32)])
+    fp = f * p.mean(0)
+    assert torch.allclose(b["load_balance_loss"], (4 * fp[:4].sum() + 4 * fp[4:].sum()) / 2)

@@ -1,0 +1,253 @@
+// Token permutation on gfx950: padded gather (plain and weighted) and the
+// fused weighted combine. All three are HBM-bound row copies: each wave owns
+// one row at a time and moves it with 16-byte vectors, every output row is
+// written exactly once (pad rows get zeros in the same pass, so no memset of
+// the output), and the combine sums the top_k rows of a token in fp32
+// registers, so the [T, k, d] intermediate of the reference never exists.
+//
+// Numerics (bit-exact with the reference for the same inputs):
+//   gather:    copy (triton_moe/kernels/gather.py:56-60)
+//   weighted:  bf16(v * w), the product of two bf16 is exact in fp32 and is
+//              rounded once (gather.py:170-174)
+//   combine:   out = bf16(sum_j f32(bf16(y_j * w_j))), j ascending, as
+//              padded_scatter's per-slot bf16 product followed by
+//              intermediate.sum(dim=1) with fp32 accumulation
+//              (triton_moe/kernels/scatter.py:61-69, 133)
+
+#include <algorithm>
+
+#include "vmoe_common.h"
+
+namespace vmoe {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerBlock = kThreads / kWave;
+
+// VEC = 8: rows move as uint4 (8 bf16); VEC = 1: scalar fallback for
+// unaligned shapes.
+template <int VEC>
+struct Vec;
+template <>
+struct Vec<8> {
+  using T = uint4;
+  __device__ static T load(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+  __device__ static void store(uint16_t* p, T v) { *reinterpret_cast<uint4*>(p) = v; }
+  __device__ static T zero() { return make_uint4(0, 0, 0, 0); }
+  __device__ static void to_f32(T v, float* f) {
+    f[0] = lo_f32(v.x); f[1] = hi_f32(v.x); f[2] = lo_f32(v.y); f[3] = hi_f32(v.y);
+    f[4] = lo_f32(v.z); f[5] = hi_f32(v.z); f[6] = lo_f32(v.w); f[7] = hi_f32(v.w);
+  }
+  __device__ static T from_f32(const float* f) {
+    return make_uint4(pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]),
+                      pack_bf16(f[6], f[7]));
+  }
+};
+template <>
+struct Vec<1> {
+  using T = uint16_t;
+  __device__ static T load(const uint16_t* p) { return *p; }
+  __device__ static void store(uint16_t* p, T v) { *p = v; }
+  __device__ static T zero() { return 0; }
+  __device__ static void to_f32(T v, float* f) { f[0] = bf16_to_f32(v); }
+  __device__ static T from_f32(const float* f) { return (uint16_t)f32_to_bf16(f[0]); }
+};
+
+// out[r] = x[row_src[r] / top_k] (* w[row_src[r]]), zeros for row_src < 0.
+template <int VEC, bool WEIGHTED>
+__global__ __launch_bounds__(kThreads) void gather_kernel(
+    const uint16_t* __restrict__ x, int64_t x_rows, int64_t ldx,
+    const int32_t* __restrict__ row_src, int top_k, const uint16_t* __restrict__ w,
+    int64_t nw, uint16_t* __restrict__ out, int64_t ldo, int64_t num_rows,
+    const int32_t* __restrict__ num_rows_dev, int64_t hidden) {
+  using V = Vec<VEC>;
+  const int lane = threadIdx.x & (kWave - 1);
+  int64_t rows = num_rows;
+  if (num_rows_dev) rows = min(rows, (int64_t)*num_rows_dev);
+  const int64_t nvec = hidden / VEC;
+  for (int64_t r = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; r < rows;
+       r += (int64_t)gridDim.x * kRowsPerBlock) {
+    const int32_t s = row_src[r];
+    const int64_t t = s >= 0 ? s / top_k : -1;
+    const bool live = s >= 0 && t < x_rows && (!WEIGHTED || s < nw);
+    uint16_t* orow = out + r * ldo;
+    if (!live) {
+      for (int64_t c = lane; c < nvec; c += kWave) V::store(orow + c * VEC, V::zero());
+      continue;
+    }
+    const uint16_t* xrow = x + t * ldx;
+    float scale = 1.0f;
+    if (WEIGHTED) scale = bf16_to_f32(w[s]);
+    for (int64_t c = lane; c < nvec; c += kWave) {
+      typename V::T v = V::load(xrow + c * VEC);
+      if (WEIGHTED) {
+        float f[VEC];
+        V::to_f32(v, f);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) f[i] *= scale;
+        v = V::from_f32(f);
+      }
+      V::store(orow + c * VEC, v);
+    }
+  }
+}
+
+// out[t] = bf16(sum_j f32(bf16(y[row(t,j)] * w[t*k+j]))). Each lane keeps up
+// to CHUNKS vectors of the row in fp32 registers.
+template <int VEC, bool WEIGHTED, int CHUNKS>
+__global__ __launch_bounds__(kThreads) void combine_kernel(
+    const uint16_t* __restrict__ y, int64_t y_rows, int64_t ldy,
+    const int32_t* __restrict__ assignment_row, const uint16_t* __restrict__ w, int top_k,
+    uint16_t* __restrict__ out, int64_t ldo, int64_t num_tokens, int64_t hidden) {
+  using V = Vec<VEC>;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t nvec = hidden / VEC;
+  for (int64_t t = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; t < num_tokens;
+       t += (int64_t)gridDim.x * kRowsPerBlock) {
+    for (int64_t c0 = 0; c0 < nvec; c0 += (int64_t)CHUNKS * kWave) {
+      float acc[CHUNKS][VEC];
+#pragma unroll
+      for (int ch = 0; ch < CHUNKS; ++ch)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[ch][i] = 0.0f;
+      for (int j = 0; j < top_k; ++j) {
+        const int64_t a = t * top_k + j;
+        const int32_t row = assignment_row[a];
+        if (row < 0 || row >= y_rows) continue;
+        const float scale = WEIGHTED ? bf16_to_f32(w[a]) : 1.0f;
+        const uint16_t* yrow = y + (int64_t)row * ldy;
+        typename V::T v[CHUNKS];
+#pragma unroll
+        for (int ch = 0; ch < CHUNKS; ++ch) {
+          const int64_t c = c0 + ch * kWave + lane;
+          v[ch] = c < nvec ? V::load(yrow + c * VEC) : V::zero();
+        }
+#pragma unroll
+        for (int ch = 0; ch < CHUNKS; ++ch) {
+          float f[VEC];
+          V::to_f32(v[ch], f);
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            // Round the weighted slot value to bf16 before the sum, as the
+            // reference's bf16 [T, k, d] intermediate does.
+            const float p = WEIGHTED ? bf16_to_f32(f32_to_bf16(f[i] * scale)) : f[i];
+            acc[ch][i] += p;
+          }
+        }
+      }
+#pragma unroll
+      for (int ch = 0; ch < CHUNKS; ++ch) {
+        const int64_t c = c0 + ch * kWave + lane;
+        if (c < nvec) V::store(out + t * ldo + c * VEC, V::from_f32(acc[ch]));
+      }
+    }
+  }
+}
+
+// Zero columns [widths[e], max_width) of expert e's rows [eto[e], eto[e+1]).
+__global__ __launch_bounds__(kThreads) void zero_tail_kernel(
+    uint16_t* __restrict__ buf, int64_t ld, const int32_t* __restrict__ eto,
+    const int32_t* __restrict__ widths, int E, int64_t max_width, int64_t rows_bound) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int64_t r = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; r < rows_bound;
+       r += (int64_t)gridDim.x * kRowsPerBlock) {
+    // Last expert whose range starts at or before r (binary search on eto).
+    int lo = 0, hi = E;  // answer in [0, E)
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if ((int64_t)eto[mid] <= r) lo = mid; else hi = mid;
+    }
+    if (r < eto[lo] || r >= eto[lo + 1]) continue;
+    const int64_t w0 = max<int64_t>(0, widths[lo]);
+    for (int64_t c = w0 + lane; c < max_width; c += kWave) buf[r * ld + c] = 0;
+  }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+inline int row_grid(int64_t rows) {
+  const int64_t g = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(g, 65536));
+}
+
+}  // namespace
+}  // namespace vmoe
+
+using namespace vmoe;
+
+extern "C" int vmoe_gather(const uint16_t* x, int64_t x_rows, int64_t ldx,
+                           const int32_t* row_src, int32_t top_k, const uint16_t* weights,
+                           int64_t num_weights, uint16_t* out, int64_t ldo, int64_t num_rows,
+                           const int32_t* num_rows_dev, int64_t hidden, vmoe_stream_t stream) {
+  if (num_rows < 0 || hidden < 0 || x_rows < 0 || top_k <= 0 || ldx < 0 || ldo < hidden)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_rows == 0 || hidden == 0) return VMOE_OK;
+  if (!out || !row_src || (x_rows > 0 && !x) || (weights && num_weights < 0))
+    return VMOE_ERR_INVALID_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = hidden % 8 == 0 && ldx % 8 == 0 && ldo % 8 == 0 && aligned16(x) &&
+                   aligned16(out);
+  const dim3 grid(row_grid(num_rows)), block(kThreads);
+  if (vec) {
+    if (weights)
+      hipLaunchKernelGGL((gather_kernel<8, true>), grid, block, 0, s, x, x_rows, ldx, row_src,
+                         top_k, weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
+    else
+      hipLaunchKernelGGL((gather_kernel<8, false>), grid, block, 0, s, x, x_rows, ldx, row_src,
+                         top_k, weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
+  } else {
+    if (weights)
+      hipLaunchKernelGGL((gather_kernel<1, true>), grid, block, 0, s, x, x_rows, ldx, row_src,
+                         top_k, weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
+    else
+      hipLaunchKernelGGL((gather_kernel<1, false>), grid, block, 0, s, x, x_rows, ldx, row_src,
+                         top_k, weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
+  }
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_combine(const uint16_t* y, int64_t y_rows, int64_t ldy,
+                            const int32_t* assignment_row, const uint16_t* weights,
+                            int32_t top_k, uint16_t* out, int64_t ldo, int64_t num_tokens,
+                            int64_t hidden, vmoe_stream_t stream) {
+  if (num_tokens < 0 || hidden < 0 || y_rows < 0 || top_k <= 0 || ldy < 0 || ldo < hidden)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_tokens == 0 || hidden == 0) return VMOE_OK;
+  if (!out || !assignment_row || (y_rows > 0 && !y)) return VMOE_ERR_INVALID_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = hidden % 8 == 0 && ldy % 8 == 0 && ldo % 8 == 0 && aligned16(y) &&
+                   aligned16(out);
+  const dim3 grid(row_grid(num_tokens)), block(kThreads);
+  if (vec) {
+    // Two 16-byte chunks per lane cover d <= 1024 in one pass.
+    if (weights)
+      hipLaunchKernelGGL((combine_kernel<8, true, 2>), grid, block, 0, s, y, y_rows, ldy,
+                         assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
+    else
+      hipLaunchKernelGGL((combine_kernel<8, false, 2>), grid, block, 0, s, y, y_rows, ldy,
+                         assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
+  } else {
+    if (weights)
+      hipLaunchKernelGGL((combine_kernel<1, true, 4>), grid, block, 0, s, y, y_rows, ldy,
+                         assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
+    else
+      hipLaunchKernelGGL((combine_kernel<1, false, 4>), grid, block, 0, s, y, y_rows, ldy,
+                         assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
+  }
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_zero_tail_cols(uint16_t* buf, int64_t ld, const int32_t* eto,
+                                   const int32_t* widths, int32_t E, int64_t max_width,
+                                   int64_t rows_bound, vmoe_stream_t stream) {
+  if (E <= 0 || max_width < 0 || rows_bound < 0 || ld < max_width) return VMOE_ERR_INVALID_ARG;
+  if (rows_bound == 0 || max_width == 0) return VMOE_OK;
+  if (!buf || !eto || !widths) return VMOE_ERR_INVALID_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(zero_tail_kernel, dim3(row_grid(rows_bound)), dim3(kThreads), 0, s, buf,
+                     ld, eto, widths, E, max_width, rows_bound);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}

@@ -1,0 +1,398 @@
+// Routing on gfx950: stable counting sort of expert ids, histogram, rounded
+// inclusive scans and the padded-row maps, in three launches.
+//
+// Semantics follow fused_route (triton_moe/kernels/fused_cumsum.py:85-171):
+//   sorted order = torch.sort(selected, stable=True), i.e. by expert id, ties
+//   by ascending assignment index; tokens_per_expert = bincount; rounded =
+//   round_{up,down,nearest}(count, block) (fused_cumsum.py:61-66); kept =
+//   min(count, rounded) (:71); bins / padded_bins = inclusive cumsums of kept /
+//   rounded (:76-77); with dropping, the sorted arrays keep the first `kept`
+//   entries of each expert (:154-169).
+// and precompute_gather_map (triton_moe/kernels/grouped_gemm.py:104-149):
+//   the q-th kept assignment of expert e lands on padded row
+//   padded_bins[e-1] + q, and gather_map[row] = assignment / top_k.
+//
+// Stable counting sort, MI355X style: the assignments are cut into tiles of
+// kTile; launch 1 counts experts per tile in LDS; launch 2 (one workgroup)
+// runs a single flat exclusive scan over counts laid out expert-major
+// [E][tiles], which yields for every (expert, tile) the first sorted position
+// -- expert-major order of the scan is exactly the sort key order; launch 3
+// re-reads each tile and ranks equal ids within a wave with ballots, so the
+// order inside an expert is the original order (stable), without any
+// comparison sort.
+
+#include <algorithm>
+
+#include "vmoe_common.h"
+
+namespace vmoe {
+namespace {
+
+constexpr int kRouteThreads = 256;
+constexpr int kRouteWaves = kRouteThreads / kWave;
+constexpr int kTile = 1024;                     // assignments per tile
+constexpr int kWaveSpan = kTile / kRouteWaves;  // contiguous assignments per wave
+constexpr int kMaxExperts = 2048;  // keeps every LDS array under 64 KiB
+constexpr int kScanThreads = 1024;
+
+__device__ __forceinline__ int64_t load_sel(const void* sel, int is64, int64_t p) {
+  return is64 ? reinterpret_cast<const int64_t*>(sel)[p]
+              : (int64_t)reinterpret_cast<const int32_t*>(sel)[p];
+}
+
+// Workspace layout (int32): counts [E * ntiles], bad-id flag per tile
+// [ntiles], then per expert: start (first unkept sorted position), kept,
+// bs (bins[e-1]), ps (padded_bins[e-1]).
+struct RouteWs {
+  int32_t* counts;
+  int32_t* bad;
+  int32_t* start;
+  int32_t* kept;
+  int32_t* bs;
+  int32_t* ps;
+};
+
+__host__ __device__ inline int64_t route_ntiles(int64_t A) { return (A + kTile - 1) / kTile; }
+
+__host__ __device__ inline RouteWs route_ws(void* base, int64_t A, int E) {
+  RouteWs w;
+  int32_t* p = reinterpret_cast<int32_t*>(base);
+  w.counts = p;
+  p += (int64_t)E * route_ntiles(A);
+  w.bad = p;
+  p += route_ntiles(A);
+  w.start = p; p += E;
+  w.kept = p; p += E;
+  w.bs = p; p += E;
+  w.ps = p;
+  return w;
+}
+
+// Launch 1: per-tile expert histogram.
+__global__ __launch_bounds__(kRouteThreads) void route_hist_kernel(
+    const void* __restrict__ sel, int is64, int64_t A, int E, int ntiles,
+    int32_t* __restrict__ counts, int32_t* __restrict__ bad_flags) {
+  extern __shared__ int32_t hist[];
+  __shared__ int32_t any_bad;
+  if (threadIdx.x == 0) any_bad = 0;
+  for (int e = threadIdx.x; e < E; e += kRouteThreads) hist[e] = 0;
+  __syncthreads();
+  const int64_t t0 = (int64_t)blockIdx.x * kTile;
+  const int64_t t1 = min(A, t0 + kTile);
+  bool bad = false;
+  for (int64_t p = t0 + threadIdx.x; p < t1; p += kRouteThreads) {
+    int64_t e = load_sel(sel, is64, p);
+    if (e >= 0 && e < E)
+      atomicAdd(&hist[(int)e], 1);
+    else
+      bad = true;
+  }
+  if (bad) any_bad = 1;
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kRouteThreads)
+    counts[(int64_t)e * ntiles + blockIdx.x] = hist[e];
+  if (threadIdx.x == 0) bad_flags[blockIdx.x] = any_bad;
+}
+
+__device__ __forceinline__ int32_t round_count(int32_t c, int32_t b, int mode) {
+  if (mode == VMOE_ROUND_UP) return ((c + b - 1) / b) * b;
+  if (mode == VMOE_ROUND_DOWN) return (c / b) * b;
+  return ((c + b / 2) / b) * b;
+}
+
+// Launch 2: one workgroup. Flat exclusive scan of counts[E][ntiles] in place,
+// then per-expert rounding and the bins / padded_bins scans, then the pad
+// rows of row_src / gather_map, then info[].
+__global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
+    RouteWs ws, int E, int ntiles, int block, int mode, int32_t* __restrict__ tpe,
+    int32_t* __restrict__ bins, int32_t* __restrict__ padded_bins,
+    int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int64_t row_capacity,
+    int32_t* __restrict__ info) {
+  __shared__ int32_t scan_smem[kScanThreads / kWave + 1];
+  __shared__ int32_t carry_kept, carry_rounded, any_bad;
+  extern __shared__ int32_t lds[];
+  int32_t* expert_start = lds;        // [E + 1]
+  int32_t* ps_lds = lds + E + 1;      // [E]
+  int32_t* kept_lds = ps_lds + E;     // [E]
+  int32_t* rounded_lds = kept_lds + E;  // [E]
+
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    carry_kept = 0;
+    carry_rounded = 0;
+    any_bad = 0;
+  }
+  const int64_t n = (int64_t)E * ntiles;
+  const int64_t per = (n + kScanThreads - 1) / kScanThreads;
+  const int64_t i0 = min(n, per * tid), i1 = min(n, i0 + per);
+  int32_t s = 0;
+  for (int64_t i = i0; i < i1; ++i) s += ws.counts[i];
+  int32_t total;
+  int32_t run = block_exclusive_scan<int32_t, kScanThreads>(s, scan_smem, &total);
+  // any_bad was zeroed before the scan's barriers.
+  bool bad = false;
+  for (int t = tid; t < ntiles; t += kScanThreads) bad |= ws.bad[t] != 0;
+  if (bad) any_bad = 1;
+  for (int64_t i = i0; i < i1; ++i) {
+    int32_t c = ws.counts[i];
+    ws.counts[i] = run;
+    if (i % ntiles == 0) expert_start[i / ntiles] = run;
+    run += c;
+  }
+  // With no tiles every expert starts at 0.
+  if (ntiles == 0)
+    for (int e = tid; e < E; e += kScanThreads) expert_start[e] = 0;
+  if (tid == 0) expert_start[E] = total;
+  __syncthreads();
+
+  // Per-expert counts, rounding and the two inclusive scans, 1024 experts per pass.
+  for (int e0 = 0; e0 < E; e0 += kScanThreads) {
+    const int e = e0 + tid;
+    int32_t c = 0, r = 0, k = 0;
+    if (e < E) {
+      c = expert_start[e + 1] - expert_start[e];
+      r = round_count(c, block, mode);
+      k = min(c, r);
+    }
+    int32_t tot_k, tot_r;
+    const int32_t ek = block_exclusive_scan<int32_t, kScanThreads>(k, scan_smem, &tot_k);
+    __syncthreads();
+    const int32_t er = block_exclusive_scan<int32_t, kScanThreads>(r, scan_smem, &tot_r);
+    const int32_t bk = carry_kept, br = carry_rounded;
+    if (e < E) {
+      tpe[e] = c;
+      bins[e] = bk + ek + k;
+      padded_bins[e] = br + er + r;
+      ws.start[e] = expert_start[e];
+      ws.kept[e] = k;
+      ws.bs[e] = bk + ek;
+      ws.ps[e] = br + er;
+      ps_lds[e] = br + er;
+      kept_lds[e] = k;
+      rounded_lds[e] = r;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      carry_kept = bk + tot_k;
+      carry_rounded = br + tot_r;
+    }
+    __syncthreads();
+  }
+
+  // Pad rows [ps + kept, ps + rounded) of every expert: one wave per expert.
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  for (int e = wave; e < E; e += kScanThreads / kWave) {
+    const int64_t ps = ps_lds[e];
+    for (int32_t q = kept_lds[e] + lane; q < rounded_lds[e]; q += kWave) {
+      const int64_t row = ps + q;
+      if (row < row_capacity) {
+        row_src[row] = -1;
+        gather_map[row] = 0;
+      }
+    }
+  }
+  if (tid == 0) {
+    int32_t err = any_bad ? (int32_t)VMOE_ROUTE_BAD_EXPERT_ID : 0;
+    if ((int64_t)carry_rounded > row_capacity) err |= (int32_t)VMOE_ROUTE_ROW_OVERFLOW;
+    info[VMOE_INFO_ROWS] = carry_rounded;
+    info[VMOE_INFO_KEPT] = carry_kept;
+    info[VMOE_INFO_ERRORS] = err;
+    info[3] = 0;
+  }
+}
+
+// Launch 3: stable placement. Each wave walks its kWaveSpan assignments in
+// order, 64 at a time; lanes holding the same expert id find each other with
+// ballots over the id bits, and rank = number of equal lanes below.
+__global__ __launch_bounds__(kRouteThreads) void route_place_kernel(
+    const void* __restrict__ sel, int is64, int64_t A, int E, int nbits, int ntiles,
+    int top_k, RouteWs ws, int32_t* __restrict__ bin_ids, int32_t* __restrict__ indices,
+    int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int64_t row_capacity,
+    int32_t* __restrict__ assignment_row) {
+  extern __shared__ int32_t wbase[];  // [kRouteWaves][E]
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) wbase[i] = 0;
+  __syncthreads();
+
+  const int64_t w0 = (int64_t)blockIdx.x * kTile + (int64_t)wave * kWaveSpan;
+  // Per-wave histogram of this wave's span.
+  for (int s = 0; s < kWaveSpan; s += kWave) {
+    const int64_t p = w0 + s + lane;
+    if (p < A) {
+      int64_t e = load_sel(sel, is64, p);
+      if (e >= 0 && e < E) atomicAdd(&wbase[wave * E + (int)e], 1);
+    }
+  }
+  __syncthreads();
+  // Turn the per-wave counts into per-wave first sorted positions.
+  for (int e = tid; e < E; e += kRouteThreads) {
+    int32_t run = ws.counts[(int64_t)e * ntiles + blockIdx.x];
+#pragma unroll
+    for (int w = 0; w < kRouteWaves; ++w) {
+      int32_t c = wbase[w * E + e];
+      wbase[w * E + e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+
+  int32_t* base = wbase + wave * E;
+  for (int s = 0; s < kWaveSpan; s += kWave) {
+    const int64_t p = w0 + s + lane;
+    int e = 0;
+    bool valid = false;
+    if (p < A) {
+      int64_t ev = load_sel(sel, is64, p);
+      valid = ev >= 0 && ev < E;
+      e = valid ? (int)ev : 0;
+    }
+    uint64_t same = ballot64(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t ones = ballot64(valid && bit);
+      same &= bit ? ones : ~ones;
+    }
+    const int rank = lanes_below(same);
+    int32_t first = 0;
+    if (valid) first = base[e];
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      const int32_t q = first + rank - ws.start[e];  // rank inside expert e
+      if (q < ws.kept[e]) {
+        const int32_t i = ws.bs[e] + q;
+        const int64_t row = (int64_t)ws.ps[e] + q;
+        bin_ids[i] = e;
+        indices[i] = (int32_t)p;
+        assignment_row[p] = (int32_t)row;
+        if (row < row_capacity) {
+          row_src[row] = (int32_t)p;
+          gather_map[row] = (int32_t)(p / top_k);
+        }
+      } else {
+        assignment_row[p] = -1;
+      }
+      if (rank == 0) base[e] = first + __popcll(same);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// Row maps from caller arrays (vmoe_row_maps): init, then place.
+__global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+__global__ void row_maps_place_kernel(const int32_t* __restrict__ indices,
+                                      const int32_t* __restrict__ bin_ids,
+                                      const int32_t* __restrict__ bins,
+                                      const int32_t* __restrict__ padded_bins,
+                                      int64_t num_sorted, int E, int top_k, int64_t num_rows,
+                                      int64_t num_assignments, int32_t* __restrict__ row_src,
+                                      int32_t* __restrict__ gather_map,
+                                      int32_t* __restrict__ assignment_row) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < num_sorted;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int e = bin_ids[i];
+    if (e < 0 || e >= E) continue;
+    const int64_t bs = e > 0 ? bins[e - 1] : 0;
+    const int64_t ps = e > 0 ? padded_bins[e - 1] : 0;
+    const int64_t row = ps + i - bs;
+    const int32_t a = indices[i];
+    if (row < 0 || row >= num_rows) continue;
+    if (row_src) row_src[row] = a;
+    if (gather_map) gather_map[row] = a / top_k;
+    if (assignment_row && a >= 0 && a < num_assignments) assignment_row[a] = (int32_t)row;
+  }
+}
+
+inline int grid_for(int64_t n, int threads, int cap = 65536) {
+  int64_t g = (n + threads - 1) / threads;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(g, cap));
+}
+
+}  // namespace
+}  // namespace vmoe
+
+using namespace vmoe;
+
+extern "C" int vmoe_route_max_experts(void) { return kMaxExperts; }
+
+extern "C" size_t vmoe_route_workspace_bytes(int64_t A, int32_t E) {
+  if (A < 0 || E <= 0) return 0;
+  const size_t nt = (size_t)route_ntiles(A);
+  return sizeof(int32_t) * ((size_t)E * nt + nt + 4 * (size_t)E) + 256;
+}
+
+extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_k,
+                          int32_t block, int32_t rounding, int32_t* bin_ids, int32_t* indices,
+                          int32_t* tpe, int32_t* bins, int32_t* padded_bins, int32_t* row_src,
+                          int32_t* gather_map, int64_t row_capacity, int32_t* assignment_row,
+                          int32_t* info, void* workspace, size_t ws_bytes, vmoe_stream_t stream) {
+  if (A < 0 || E <= 0 || top_k <= 0 || block <= 0 || row_capacity < 0)
+    return VMOE_ERR_INVALID_ARG;
+  if (rounding < VMOE_ROUND_UP || rounding > VMOE_ROUND_NEAREST) return VMOE_ERR_INVALID_ARG;
+  if (E > kMaxExperts || A > INT32_MAX) return VMOE_ERR_UNSUPPORTED;
+  if (!tpe || !bins || !padded_bins || !info || !workspace) return VMOE_ERR_INVALID_ARG;
+  if (A > 0 && (!sel || !bin_ids || !indices || !assignment_row)) return VMOE_ERR_INVALID_ARG;
+  if (row_capacity > 0 && (!row_src || !gather_map)) return VMOE_ERR_INVALID_ARG;
+  if (ws_bytes < vmoe_route_workspace_bytes(A, E)) return VMOE_ERR_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  const int ntiles = (int)route_ntiles(A);
+  RouteWs ws = route_ws(workspace, A, E);
+  if (ntiles > 0) {
+    hipLaunchKernelGGL(route_hist_kernel, dim3(ntiles), dim3(kRouteThreads),
+                       sizeof(int32_t) * E, s, sel, is64, A, E, ntiles, ws.counts, ws.bad);
+    VMOE_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), sizeof(int32_t) * (4 * E + 1),
+                     s, ws, E, ntiles, block, rounding, tpe, bins, padded_bins, row_src,
+                     gather_map, row_capacity, info);
+  VMOE_CHECK_LAUNCH();
+  if (ntiles > 0) {
+    int nbits = 1;
+    while ((1 << nbits) < E) ++nbits;
+    hipLaunchKernelGGL(route_place_kernel, dim3(ntiles), dim3(kRouteThreads),
+                       sizeof(int32_t) * kRouteWaves * E, s, sel, is64, A, E, nbits, ntiles,
+                       top_k, ws, bin_ids, indices, row_src, gather_map, row_capacity,
+                       assignment_row);
+    VMOE_CHECK_LAUNCH();
+  }
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_row_maps(const int32_t* indices, const int32_t* bin_ids,
+                             const int32_t* bins, const int32_t* padded_bins, int64_t num_sorted,
+                             int32_t E, int32_t top_k, int64_t num_rows, int64_t num_assignments,
+                             int32_t* row_src, int32_t* gather_map, int32_t* assignment_row,
+                             vmoe_stream_t stream) {
+  if (num_sorted < 0 || E <= 0 || top_k <= 0 || num_rows < 0 || num_assignments < 0)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_sorted > 0 && (!indices || !bin_ids || !bins || !padded_bins))
+    return VMOE_ERR_INVALID_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (row_src && num_rows > 0) {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for(num_rows, 256)), dim3(256), 0, s, row_src,
+                       num_rows, -1);
+    VMOE_CHECK_LAUNCH();
+  }
+  if (gather_map && num_rows > 0) {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for(num_rows, 256)), dim3(256), 0, s,
+                       gather_map, num_rows, 0);
+    VMOE_CHECK_LAUNCH();
+  }
+  if (assignment_row && num_assignments > 0) {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for(num_assignments, 256)), dim3(256), 0, s,
+                       assignment_row, num_assignments, -1);
+    VMOE_CHECK_LAUNCH();
+  }
+  if (num_sorted > 0) {
+    hipLaunchKernelGGL(row_maps_place_kernel, dim3(grid_for(num_sorted, 256)), dim3(256), 0, s,
+                       indices, bin_ids, bins, padded_bins, num_sorted, E, top_k, num_rows,
+                       num_assignments, row_src, gather_map, assignment_row);
+    VMOE_CHECK_LAUNCH();
+  }
+  return VMOE_OK;
+}

@@ -1,0 +1,111 @@
+"""ctypes binding of libvmoe.so (the C ABI in include/vmoe.h).
+
+The library is loaded on first use. If it is missing or fails to load, every
+kernel entry point raises RuntimeError: there is no CPU or eager fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("VMOE_LIB", _HERE / "libvmoe.so"))
+
+_c_i32p = ctypes.c_void_p
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+# name -> argtypes (all return int status unless listed in _RESTYPES)
+_SIGNATURES = {
+    "vmoe_status_string": [ctypes.c_int],
+    "vmoe_version": [],
+    "vmoe_route_max_experts": [],
+    "vmoe_route_workspace_bytes": [_i64, _i32],
+    "vmoe_route": [_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                   _i64, _vp, _vp, _vp, ctypes.c_size_t, _vp],
+    "vmoe_row_maps": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _i64, _vp, _vp, _vp, _vp],
+    "vmoe_gather": [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp],
+    "vmoe_combine": [_vp, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp],
+    "vmoe_gemm_up_fwd": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp,
+                         _vp, _i32, _i64, _i64, _i64, _vp],
+    "vmoe_gemm_down_fwd": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
+                           _i64, _i64, _vp],
+    "vmoe_gemm_up_bwd_dx": [_vp, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp,
+                            _i32, _i64, _i64, _i64, _vp],
+    "vmoe_gemm_up_bwd_dw": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _vp, _i64, _vp, _vp,
+                            _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "vmoe_gemm_down_bwd_dh": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
+                              _i64, _i64, _vp],
+    "vmoe_gemm_down_bwd_dw": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
+                              _i64, _i64, _vp],
+    "vmoe_zero_tail_cols": [_vp, _i64, _vp, _vp, _i32, _i64, _i64, _vp],
+}
+_RESTYPES = {
+    "vmoe_status_string": ctypes.c_char_p,
+    "vmoe_route_workspace_bytes": ctypes.c_size_t,
+}
+
+# Status codes (include/vmoe.h).
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_WORKSPACE = 0, 1, 2, 3, 4
+ROUNDING = {"up": 0, "down": 1, "nearest": 2}
+ACT_NONE, ACT_RELU_SQUARED = 0, 1
+INFO_ROWS, INFO_KEPT, INFO_ERRORS, INFO_LEN = 0, 1, 2, 4
+ROUTE_BAD_EXPERT_ID, ROUTE_ROW_OVERFLOW = 1, 2
+
+_lib = None
+_load_error: Exception | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises RuntimeError if it cannot be loaded."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    if _load_error is not None:
+        raise RuntimeError(f"libvmoe.so unavailable: {_load_error}") from _load_error
+    try:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(
+                f"{LIB_PATH} not found; build it with `python triton-variable-moe_amd/build.py`")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        _lib = handle
+        return _lib
+    except Exception as exc:  # noqa: BLE001 - re-raised with context
+        _load_error = exc
+        raise RuntimeError(f"libvmoe.so unavailable: {exc}") from exc
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        msg = lib().vmoe_status_string(status).decode()
+        if status == ERR_UNSUPPORTED:
+            raise NotImplementedError(f"{what}: {msg}")
+        if status == ERR_INVALID_ARG:
+            raise ValueError(f"{what}: {msg}")
+        raise RuntimeError(f"{what}: {msg} (status {status})")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu(t: torch.Tensor, what: str = "Input") -> None:
+    if not t.is_cuda:
+        raise AssertionError(f"{what} must be on CUDA")

@@ -1,0 +1,458 @@
+"""Variable-width grouped GEMMs on gfx950 bf16 MFMA (csrc/gemm.hip).
+
+Mirrors triton_moe/kernels/grouped_gemm.py of the reference:
+precompute_gather_map (:104-149), grouped_gemm_up (:379-477),
+grouped_gemm_down (:587-651), grouped_gemm_up_backward (:1166-1290),
+grouped_gemm_down_backward (:1294-1390), GroupedGemmUp (:1393-1525),
+GroupedGemmDown (:1528-1601), grouped_gemm_up_autograd (:1604-1639) and
+grouped_gemm_down_autograd (:1642-1665): same signatures, output shapes,
+zero-filled padding, saved tensors and gradient tuples.
+
+Layouts are the reference's: W1 [hidden, total_width] with experts side by
+side in columns, W2 [total_width, hidden] stacked in rows, intermediates
+[total_tokens, max_expert_width] with expert e in columns [0, width_e).
+
+The public functions read the small metadata arrays back once (the
+reference does several .item() syncs) to size outputs and validate; the
+Routed*Op functions used by the module take a prebuilt GemmMeta and never
+sync: the kernels find their tiles on the device.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch.amp import custom_bwd, custom_fwd
+from torch.autograd.function import once_differentiable
+
+from .. import _lib
+from .gather import row_maps
+
+_ACTIVATIONS = {"none": _lib.ACT_NONE, "relu_squared": _lib.ACT_RELU_SQUARED}
+
+
+def _activation_code(activation: str) -> int:
+    if activation == "swiglu":
+        raise NotImplementedError(
+            "swiglu is an incomplete placeholder in the reference and is not provided")
+    # The reference maps unknown names to "none" (grouped_gemm.py:435).
+    return _ACTIVATIONS.get(activation, _lib.ACT_NONE)
+
+
+@dataclass
+class GemmMeta:
+    """Expert metadata for one grouped GEMM call.
+
+    eto/ewo [E+1], widths/tpe [E]: device int32. rows: row count of the
+    padded buffers (sizes outputs and bounds row indices). full_rows: every
+    row < rows is written by the row tiles. full_cols: the expert column
+    ranges tile the weight matrix. uniform: every width equals max_width.
+    """
+
+    eto: torch.Tensor
+    ewo: torch.Tensor
+    widths: torch.Tensor
+    tpe: torch.Tensor
+    num_experts: int
+    max_width: int
+    rows: int
+    full_rows: bool = True
+    full_cols: bool = True
+    uniform: bool = True
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.int32).contiguous()
+
+
+def host_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, rows: int | None,
+              total_width: int | None) -> GemmMeta:
+    """Validates caller metadata on the host (one device->host copy)."""
+    eto_d, ewo_d, w_d, tpe_d = _i32(eto), _i32(ewo), _i32(widths), _i32(tpe)
+    E = w_d.numel()
+    if E == 0:
+        raise ValueError("expert_widths is empty")
+    if eto_d.numel() < E + 1 or ewo_d.numel() < E + 1 or tpe_d.numel() < E:
+        raise ValueError("expert metadata shorter than num_experts (+1)")
+    host = torch.cat([eto_d[:E + 1], ewo_d[:E + 1], w_d, tpe_d[:E]]).cpu().tolist()
+    h_eto, h_ewo = host[:E + 1], host[E + 1:2 * E + 2]
+    h_w, h_tpe = host[2 * E + 2:3 * E + 2], host[3 * E + 2:]
+    if rows is None:
+        rows = h_eto[E]
+    if any(v % 8 for v in h_w) or any(v % 8 for v in h_ewo) or hidden % 8 or max_width % 8:
+        raise NotImplementedError(
+            "hidden size, expert widths and weight offsets must be multiples of 8")
+    if any(w < 0 or w > max_width for w in h_w):
+        raise ValueError("expert width outside [0, max_expert_width]")
+    if any(b < a for a, b in zip(h_eto, h_eto[1:])) or h_eto[0] < 0 or h_eto[E] > rows:
+        raise ValueError("expert_token_offsets must be non-decreasing within [0, total_tokens]")
+    if any(t < 0 for t in h_tpe):
+        raise ValueError("tokens_per_expert must be non-negative")
+    if any(o < 0 for o in h_ewo) or (total_width is not None and any(
+            h_ewo[e] + h_w[e] > total_width or h_ewo[e + 1] > total_width for e in range(E))):
+        raise ValueError("expert weight ranges exceed the weight matrix")
+    if any(h_ewo[e + 1] - h_ewo[e] > max_width for e in range(E)):
+        raise ValueError("expert weight range wider than max_expert_width")
+    full_rows = h_eto[0] == 0 and h_eto[E] == rows and all(
+        h_tpe[e] >= h_eto[e + 1] - h_eto[e] for e in range(E))
+    full_cols = total_width is not None and h_ewo[0] == 0 and h_ewo[E] == total_width and all(
+        h_ewo[e + 1] == h_ewo[e] + h_w[e] for e in range(E))
+    uniform = all(w == max_width for w in h_w)
+    return GemmMeta(eto_d, ewo_d, w_d, tpe_d, E, int(max_width), int(rows), full_rows,
+                    full_cols, uniform)
+
+
+def _bf16(t: torch.Tensor, what: str) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise NotImplementedError(f"{what}: only bfloat16 is supported (got {t.dtype})")
+    return t if t.stride(-1) == 1 and t.stride(0) % 8 == 0 else t.contiguous()
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _alloc(rows, cols, like, zero):
+    f = torch.zeros if zero else torch.empty
+    return f(rows, cols, dtype=like.dtype, device=like.device)
+
+
+def _meta_args(m: GemmMeta):
+    return (m.eto.data_ptr(), m.ewo.data_ptr(), m.widths.data_ptr(), m.tpe.data_ptr(),
+            m.num_experts)
+
+
+def _zero_tails(buf: torch.Tensor, m: GemmMeta):
+    if m.uniform or buf.shape[0] == 0:
+        return
+    _lib.call("vmoe_zero_tail_cols", buf.data_ptr(), buf.stride(0), m.eto.data_ptr(),
+              m.widths.data_ptr(), m.num_experts, m.max_width, buf.shape[0],
+              _lib.stream(buf.device))
+
+
+# ---------------------------------------------------------------------------
+# Launchers (no host sync; shapes come from GemmMeta)
+# ---------------------------------------------------------------------------
+
+
+def up_fwd(x, w1, m: GemmMeta, act: int, save_pre: bool, zero_tails: bool,
+           gather_map: torch.Tensor | None = None):
+    """out = act(x_e @ W1_e) and pre_act = relu(z) (or zeros for act none)."""
+    x = _bf16(x, "grouped_gemm_up x")
+    w1 = _bf16(w1, "grouped_gemm_up w1")
+    hidden = x.shape[1]
+    _need(w1.shape[0] == hidden, "w1 rows must equal the hidden size of x")
+    if gather_map is None:
+        _need(x.shape[0] >= m.rows, "x has fewer rows than expert_token_offsets[-1]")
+    else:
+        _need(gather_map.numel() >= m.rows, "gather_map shorter than the padded row count")
+    out = _alloc(m.rows, m.max_width, x, not m.full_rows)
+    pre = None
+    if save_pre:
+        pre = _alloc(m.rows, m.max_width, x, not m.full_rows or act == _lib.ACT_NONE)
+    gm = None if gather_map is None else _i32(gather_map)
+    if m.rows > 0:
+        _lib.call("vmoe_gemm_up_fwd", x.data_ptr(), x.stride(0), x.shape[0], _lib.ptr(gm),
+                  w1.data_ptr(), w1.stride(0),
+                  out.data_ptr(), _lib.ptr(pre) if act == _lib.ACT_RELU_SQUARED else None,
+                  out.stride(0), act, *_meta_args(m), hidden, m.max_width, m.rows,
+                  _lib.stream(x.device))
+        if zero_tails:
+            _zero_tails(out, m)
+            if pre is not None and act == _lib.ACT_RELU_SQUARED:
+                _zero_tails(pre, m)
+    return out, pre
+
+
+def down_fwd(h, w2, m: GemmMeta, hidden: int):
+    h = _bf16(h, "grouped_gemm_down intermediate")
+    w2 = _bf16(w2, "grouped_gemm_down w2")
+    _need(w2.shape[1] == hidden, "w2 columns must equal hidden_size")
+    _need(h.shape[0] >= m.rows and h.shape[1] >= m.max_width,
+          "intermediate smaller than [rows, max_expert_width]")
+    y = _alloc(m.rows, hidden, h, not m.full_rows)
+    if m.rows > 0:
+        _lib.call("vmoe_gemm_down_fwd", h.data_ptr(), h.stride(0), w2.data_ptr(), w2.stride(0),
+                  y.data_ptr(), y.stride(0), *_meta_args(m), hidden, m.max_width, m.rows,
+                  _lib.stream(h.device))
+    return y
+
+
+def _same_ld(a, b):
+    if b is None or a.stride(0) == b.stride(0):
+        return a, b
+    return a.contiguous(), b.contiguous()
+
+
+def up_bwd(grad_h, x, w1, pre, m: GemmMeta, hidden: int, act: int,
+           gather_map: torch.Tensor | None):
+    """(grad_x in gathered rows, grad_w1)."""
+    grad_h = _bf16(grad_h, "grouped_gemm_up_backward grad_output")
+    x = _bf16(x, "grouped_gemm_up_backward x")
+    w1 = _bf16(w1, "grouped_gemm_up_backward w1")
+    if act == _lib.ACT_RELU_SQUARED:
+        pre = _bf16(pre, "grouped_gemm_up_backward pre_act")
+        grad_h, pre = _same_ld(grad_h, pre)
+    else:
+        pre = None
+    _need(w1.shape[0] == hidden and x.shape[1] == hidden, "x / w1 do not match hidden_size")
+    _need(grad_h.shape[0] >= m.rows and grad_h.shape[1] >= m.max_width,
+          "grad_output smaller than [rows, max_expert_width]")
+    if pre is not None:
+        _need(pre.shape == grad_h.shape, "pre_act and grad_output shapes differ")
+    if gather_map is None:
+        _need(x.shape[0] >= m.rows, "x has fewer rows than expert_token_offsets[-1]")
+    else:
+        _need(gather_map.numel() >= m.rows, "gather_map shorter than the padded row count")
+    grad_x = _alloc(m.rows, hidden, grad_h, not m.full_rows)
+    grad_w1 = torch.zeros_like(w1) if not m.full_cols else torch.empty_like(w1)
+    dev = grad_h.device
+    if m.rows > 0:
+        _lib.call("vmoe_gemm_up_bwd_dx", grad_h.data_ptr(), _lib.ptr(pre), grad_h.stride(0),
+                  act, w1.data_ptr(), w1.stride(0), grad_x.data_ptr(), grad_x.stride(0),
+                  *_meta_args(m), hidden, m.max_width, m.rows, _lib.stream(dev))
+    gm = None if gather_map is None else _i32(gather_map)
+    _lib.call("vmoe_gemm_up_bwd_dw", x.data_ptr(), x.stride(0), x.shape[0], _lib.ptr(gm),
+              grad_h.data_ptr(), _lib.ptr(pre), grad_h.stride(0), act, grad_w1.data_ptr(),
+              grad_w1.stride(0), *_meta_args(m), hidden, m.max_width, m.rows,
+              _lib.stream(dev))
+    return grad_x, grad_w1
+
+
+def down_bwd(grad_y, h, w2, m: GemmMeta, hidden: int, zero_tails: bool):
+    """(grad_intermediate [rows, max_width], grad_w2)."""
+    grad_y = _bf16(grad_y, "grouped_gemm_down_backward grad_output")
+    h = _bf16(h, "grouped_gemm_down_backward intermediate")
+    w2 = _bf16(w2, "grouped_gemm_down_backward w2")
+    _need(w2.shape[1] == hidden and grad_y.shape[1] == hidden,
+          "grad_output / w2 do not match hidden_size")
+    _need(grad_y.shape[0] >= m.rows, "grad_output has fewer rows than the padded row count")
+    _need(h.shape[0] >= m.rows and h.shape[1] >= m.max_width,
+          "intermediate smaller than [rows, max_expert_width]")
+    grad_h = _alloc(m.rows, m.max_width, grad_y, not m.full_rows)
+    grad_w2 = torch.zeros_like(w2) if not m.full_cols else torch.empty_like(w2)
+    dev = grad_y.device
+    if m.rows > 0:
+        _lib.call("vmoe_gemm_down_bwd_dh", grad_y.data_ptr(), grad_y.stride(0), w2.data_ptr(),
+                  w2.stride(0), grad_h.data_ptr(), grad_h.stride(0), *_meta_args(m), hidden,
+                  m.max_width, m.rows, _lib.stream(dev))
+        if zero_tails:
+            _zero_tails(grad_h, m)
+    _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), grad_y.data_ptr(),
+              grad_y.stride(0), grad_w2.data_ptr(), grad_w2.stride(0), *_meta_args(m), hidden,
+              m.max_width, m.rows, _lib.stream(dev))
+    return grad_h, grad_w2
+
+
+# ---------------------------------------------------------------------------
+# Public API (reference signatures)
+# ---------------------------------------------------------------------------
+
+
+@torch.compiler.disable
+def precompute_gather_map(indices, bin_ids, bins, padded_bins, top_k):
+    """[padded_bins[-1]] int32 map from gathered row to original token row (0 on pad rows)."""
+    _lib.require_gpu(indices)
+    total_padded = int(padded_bins[-1].item())
+    _, gm, _ = row_maps(indices, bin_ids, bins, padded_bins, top_k, total_padded, 0,
+                        want_row_src=False, want_gather_map=True)
+    return gm
+
+
+@torch.compiler.disable
+def grouped_gemm_up(x, w1, expert_token_offsets, expert_weight_offsets, expert_widths,
+                    tokens_per_expert, max_expert_width, activation="relu_squared",
+                    save_pre_act=False, gather_map=None):
+    """Grouped up-projection with fused activation.
+
+    Returns [total_tokens, max_expert_width] (and pre_act if save_pre_act),
+    total_tokens = expert_token_offsets[-1]; columns >= width_e are zero.
+    """
+    _lib.require_gpu(x)
+    act = _activation_code(activation)
+    m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                  tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1])
+    # With gather_map, rows are read as x[gather_map[row]] inside the kernel
+    # (the reference's USE_GATHER_MAP path, grouped_gemm.py:289-292).
+    out, pre = up_fwd(x, w1, m, act, save_pre_act, zero_tails=True, gather_map=gather_map)
+    if save_pre_act:
+        return out, pre
+    return out
+
+
+@torch.compiler.disable
+def grouped_gemm_down(intermediate, w2, expert_token_offsets, expert_weight_offsets,
+                      expert_widths, tokens_per_expert, hidden_size):
+    """Grouped down-projection: [total_tokens, hidden_size], total_tokens = intermediate rows."""
+    _lib.require_gpu(intermediate)
+    m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                  tokens_per_expert, intermediate.shape[1], int(hidden_size),
+                  intermediate.shape[0], w2.shape[0])
+    return down_fwd(intermediate, w2, m, int(hidden_size))
+
+
+@torch.compiler.disable
+def grouped_gemm_up_backward(grad_output, x, w1, pre_act, expert_token_offsets,
+                             expert_weight_offsets, expert_widths, tokens_per_expert,
+                             hidden_size, activation="relu_squared", gather_map=None):
+    """(grad_x [total_tokens, hidden] in gathered space, grad_w1 like w1)."""
+    _lib.require_gpu(grad_output)
+    act = _activation_code(activation)
+    m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                  tokens_per_expert, grad_output.shape[1], int(hidden_size), None,
+                  w1.shape[1])
+    return up_bwd(grad_output, x, w1, pre_act, m, int(hidden_size), act, gather_map)
+
+
+@torch.compiler.disable
+def grouped_gemm_down_backward(grad_output, intermediate, w2, expert_token_offsets,
+                               expert_weight_offsets, expert_widths, tokens_per_expert,
+                               hidden_size, max_expert_width):
+    """(grad_intermediate [total_tokens, max_expert_width], grad_w2 like w2)."""
+    _lib.require_gpu(grad_output)
+    m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                  tokens_per_expert, int(max_expert_width), int(hidden_size),
+                  intermediate.shape[0], w2.shape[0])
+    return down_bwd(grad_output, intermediate, w2, m, int(hidden_size), zero_tails=True)
+
+
+class GroupedGemmUp(torch.autograd.Function):
+    """Autograd function for the grouped up-projection with fused activation.
+
+    With x_flat and gather_map, backward reads x_flat through gather_map
+    instead of keeping x_gathered alive (grouped_gemm.py:1442-1475).
+    """
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, x, w1, expert_token_offsets, expert_weight_offsets, expert_widths,
+                tokens_per_expert, max_expert_width, hidden_size, activation, x_flat,
+                gather_map):
+        _lib.require_gpu(x)
+        x = x.to(w1.dtype)
+        act = _activation_code(activation)
+        m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                      tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1])
+        out, pre = up_fwd(x, w1, m, act, True, zero_tails=True)
+        use_gm = x_flat is not None and gather_map is not None
+        ctx.use_gather_map = use_gm
+        if use_gm:
+            ctx.save_for_backward(x_flat.to(w1.dtype), w1, pre, gather_map)
+        else:
+            ctx.save_for_backward(x, w1, pre)
+        ctx.meta = m
+        ctx.hidden_size = hidden_size
+        ctx.act = act
+        return out
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, grad_output):
+        if ctx.use_gather_map:
+            x_for_dw, w1, pre, gm = ctx.saved_tensors
+        else:
+            (x_for_dw, w1, pre), gm = ctx.saved_tensors, None
+        grad_x, grad_w1 = up_bwd(grad_output, x_for_dw, w1, pre, ctx.meta,
+                                 int(ctx.hidden_size), ctx.act, gm)
+        return grad_x, grad_w1, None, None, None, None, None, None, None, None, None
+
+
+class GroupedGemmDown(torch.autograd.Function):
+    """Autograd function for the grouped down-projection."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, intermediate, w2, expert_token_offsets, expert_weight_offsets,
+                expert_widths, tokens_per_expert, hidden_size, max_expert_width):
+        _lib.require_gpu(intermediate)
+        intermediate = intermediate.to(w2.dtype)
+        m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                      tokens_per_expert, int(max_expert_width), int(hidden_size),
+                      intermediate.shape[0], w2.shape[0])
+        out = down_fwd(intermediate, w2, m, int(hidden_size))
+        ctx.save_for_backward(intermediate, w2)
+        ctx.meta = m
+        ctx.hidden_size = hidden_size
+        return out
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, grad_output):
+        intermediate, w2 = ctx.saved_tensors
+        grad_int, grad_w2 = down_bwd(grad_output, intermediate, w2, ctx.meta,
+                                     int(ctx.hidden_size), zero_tails=True)
+        return grad_int, grad_w2, None, None, None, None, None, None
+
+
+def grouped_gemm_up_autograd(x, w1, expert_token_offsets, expert_weight_offsets, expert_widths,
+                             tokens_per_expert, max_expert_width, hidden_size,
+                             activation="relu_squared", x_flat=None, gather_map=None):
+    """Grouped GEMM up-projection with autograd support."""
+    return GroupedGemmUp.apply(x, w1, expert_token_offsets, expert_weight_offsets,
+                               expert_widths, tokens_per_expert, max_expert_width, hidden_size,
+                               activation, x_flat, gather_map)
+
+
+def grouped_gemm_down_autograd(intermediate, w2, expert_token_offsets, expert_weight_offsets,
+                               expert_widths, tokens_per_expert, hidden_size, max_expert_width):
+    """Grouped GEMM down-projection with autograd support."""
+    return GroupedGemmDown.apply(intermediate, w2, expert_token_offsets, expert_weight_offsets,
+                                 expert_widths, tokens_per_expert, hidden_size,
+                                 max_expert_width)
+
+
+# ---------------------------------------------------------------------------
+# Sync-free module path
+# ---------------------------------------------------------------------------
+
+
+class RoutedUpOp(torch.autograd.Function):
+    """Up-projection for the module: metadata from the route, no host sync.
+
+    Saves x_flat + gather_map for the dW backward, like the module's call of
+    grouped_gemm_up_autograd (triton_moe/moe.py:214-226).
+    """
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, x_gathered, w1, meta, x_flat, gather_map, hidden_size):
+        out, pre = up_fwd(x_gathered, w1, meta, _lib.ACT_RELU_SQUARED, True, zero_tails=False)
+        ctx.save_for_backward(x_flat, w1, pre, gather_map)
+        ctx.meta = meta
+        ctx.hidden_size = hidden_size
+        return out
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, grad_output):
+        x_flat, w1, pre, gm = ctx.saved_tensors
+        grad_x, grad_w1 = up_bwd(grad_output, x_flat, w1, pre, ctx.meta, ctx.hidden_size,
+                                 _lib.ACT_RELU_SQUARED, gm)
+        return grad_x, grad_w1, None, None, None, None
+
+
+class RoutedDownOp(torch.autograd.Function):
+    """Down-projection for the module: metadata from the route, no host sync."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, h, w2, meta, hidden_size):
+        y = down_fwd(h, w2, meta, hidden_size)
+        ctx.save_for_backward(h, w2)
+        ctx.meta = meta
+        ctx.hidden_size = hidden_size
+        return y
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, grad_output):
+        h, w2 = ctx.saved_tensors
+        grad_h, grad_w2 = down_bwd(grad_output, h, w2, ctx.meta, ctx.hidden_size,
+                                   zero_tails=False)
+        return grad_h, grad_w2, None, None

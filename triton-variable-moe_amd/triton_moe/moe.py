@@ -1,0 +1,303 @@
+"""MoE MLP layer on hand-written gfx950 HIP kernels.
+
+Drop-in for triton_moe/moe.py of the reference: TritonMoEConfig (:30-39) and
+TritonMoEMLP (:42-518) with the same constructor (parameter names, shapes,
+init order router -> w1 -> w2, buffers), forward returning
+(output, aux_loss, f_i), forward_with_intermediates and forward_profiled.
+
+The router Linear, sigmoid, top-k, weight normalisation and auxiliary losses
+stay in PyTorch as in the reference (moe.py:166-182, 253-274). Everything
+between them runs on libvmoe.so: routing (counting sort + scans + maps),
+gather, grouped up GEMM with fused relu^2, grouped down GEMM and weighted
+combine, and their backward. The forward and backward issue no host sync:
+buffers are sized from an upper bound of the padded row count and the kernels
+read the true counts on the device.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from einops import rearrange
+
+from .kernels import (
+    fused_route,
+    grouped_gemm_down,
+    grouped_gemm_up,
+    padded_gather,
+    padded_scatter,
+)
+from .kernels.fused_cumsum import route_device
+from .kernels.gather import RoutedGatherOp
+from .kernels.grouped_gemm import GemmMeta, RoutedDownOp, RoutedUpOp
+from .kernels.scatter import RoutedScatterOp
+
+
+@dataclass
+class TritonMoEConfig:
+    """Configuration for the MoE layer (field names and defaults of the reference)."""
+
+    n_embd: int = 768
+    expert_sizes: list = field(default_factory=lambda: [(64, 256)])
+    num_active_experts: int = 8
+    norm_topk_prob: bool = True
+    block_size: int = 64
+    use_megablocks_gather_scatter: bool = False
+
+
+class TritonMoEMLP(nn.Module):
+    """Mixture-of-experts MLP with variable-width experts.
+
+    w1 [n_embd, total_width] holds the experts side by side in columns,
+    w2 [total_width, n_embd] stacked in rows (reference moe.py:80-85).
+    """
+
+    def __init__(self, config: TritonMoEConfig):
+        super().__init__()
+        self.config = config
+        self.num_experts = sum(count for count, _ in config.expert_sizes)
+        self.num_active_experts = config.num_active_experts
+        self.norm_topk_prob = config.norm_topk_prob
+        self.block_size = config.block_size
+
+        self.expert_widths = []
+        self.expert_offsets = [0]
+        for count, size in config.expert_sizes:
+            assert size % self.block_size == 0, (
+                f"expert sizes must be divisible by {self.block_size}"
+            )
+            for _ in range(count):
+                self.expert_widths.append(size)
+                self.expert_offsets.append(self.expert_offsets[-1] + size)
+        self.total_expert_width = self.expert_offsets[-1]
+        self.max_expert_width = max(self.expert_widths)
+
+        self.router = nn.Linear(config.n_embd, self.num_experts, bias=False)
+        self.w1 = nn.Parameter(torch.empty(config.n_embd, self.total_expert_width))
+        self.w2 = nn.Parameter(torch.empty(self.total_expert_width, config.n_embd))
+        nn.init.trunc_normal_(self.w1, mean=0.0, std=0.02, a=-0.06, b=0.06)
+        nn.init.trunc_normal_(self.w2, mean=0.0, std=0.02, a=-0.06, b=0.06)
+
+        self.register_buffer(
+            "expert_widths_t", torch.tensor(self.expert_widths, dtype=torch.int32),
+            persistent=False)
+        self.register_buffer(
+            "expert_weight_offsets_t", torch.tensor(self.expert_offsets, dtype=torch.int32),
+            persistent=False)
+
+        mean_expert_width = sum(self.expert_widths) / self.num_experts
+        self.register_buffer(
+            "expert_widths_normalized",
+            torch.tensor([w / mean_expert_width for w in self.expert_widths],
+                         dtype=torch.float32),
+            persistent=False)
+
+        expert_to_group = []
+        group_sizes = []
+        valid_group_idx = 0
+        for count, _size in config.expert_sizes:
+            for _ in range(count):
+                expert_to_group.append(valid_group_idx if count > 1 else -1)
+            if count > 1:
+                group_sizes.append(count)
+                valid_group_idx += 1
+        self._num_valid_groups = len(group_sizes)
+        self._all_experts_valid = all(g >= 0 for g in expert_to_group)
+        if self._num_valid_groups > 0:
+            membership = torch.zeros(self.num_experts, self._num_valid_groups)
+            for i, g in enumerate(expert_to_group):
+                if g >= 0:
+                    membership[i, g] = 1.0
+            self.register_buffer("group_membership", membership, persistent=False)
+            self.register_buffer("group_sizes", torch.tensor(group_sizes, dtype=torch.float32),
+                                 persistent=False)
+            valid = [i for i, g in enumerate(expert_to_group) if g >= 0]
+            self.register_buffer("valid_expert_indices", torch.tensor(valid, dtype=torch.long),
+                                 persistent=False)
+        else:
+            self.register_buffer("group_membership", torch.empty(0), persistent=False)
+            self.register_buffer("group_sizes", torch.tensor([1.0]), persistent=False)
+            self.register_buffer("valid_expert_indices", torch.empty(0, dtype=torch.long),
+                                 persistent=False)
+
+    # ------------------------------------------------------------------
+    # routing front end (PyTorch, as in the reference moe.py:166-182)
+    # ------------------------------------------------------------------
+
+    def _router(self, x_flat: torch.Tensor):
+        router_logits = self.router(x_flat)
+        router_probs = F.sigmoid(router_logits.float())
+        top_k_weights, selected_experts = torch.topk(
+            router_probs, self.num_active_experts, dim=-1)
+        if self.norm_topk_prob:
+            top_k_weights = top_k_weights / (top_k_weights.sum(dim=-1, keepdim=True) + 1e-20)
+        top_k_weights = top_k_weights.to(x_flat.dtype)
+        return router_logits, router_probs, top_k_weights, selected_experts
+
+    def _aux(self, router_logits, router_probs, tokens_per_expert, dtype):
+        router_z_loss = torch.logsumexp(router_logits, dim=-1).pow(2).mean()
+        f_i = (tokens_per_expert.float() / tokens_per_expert.sum()).to(dtype)
+        load_balance_loss = self._compute_load_balance_loss(router_probs, f_i)
+        compute_loss = (
+            router_probs @ self.expert_widths_normalized.to(router_probs.dtype)).mean()
+        aux_loss = {
+            "router_z_loss": router_z_loss,
+            "load_balance_loss": load_balance_loss,
+            "compute_loss": compute_loss,
+        }
+        return aux_loss, f_i
+
+    def _experts(self, x_flat, top_k_weights_flat, selected_experts_flat):
+        """Routing + expert MLP + combine on the HIP kernels, no host sync."""
+        k = self.num_active_experts
+        r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up")
+        device = x_flat.device
+        padded_bins = r.padded_bins
+        expert_token_offsets = torch.cat(
+            [torch.zeros(1, device=device, dtype=torch.int32), padded_bins])
+        padded_tokens_per_expert = torch.cat(
+            [padded_bins[:1], padded_bins[1:] - padded_bins[:-1]])
+        meta = GemmMeta(expert_token_offsets, self.expert_weight_offsets_t,
+                        self.expert_widths_t, padded_tokens_per_expert, self.num_experts,
+                        self.max_expert_width, r.rows_bound)
+        num_rows_dev = r.info[0:1]
+        x_gathered = RoutedGatherOp.apply(x_flat, r.row_src, r.assignment_row, k, r.rows_bound,
+                                          num_rows_dev)
+        x_up = RoutedUpOp.apply(x_gathered, self.w1, meta, x_flat, r.gather_map,
+                                self.config.n_embd)
+        x_down = RoutedDownOp.apply(x_up, self.w2, meta, self.config.n_embd)
+        output_flat = RoutedScatterOp.apply(x_down, r.row_src, r.assignment_row,
+                                            top_k_weights_flat, k, x_flat.shape[0],
+                                            num_rows_dev)
+        return output_flat, r.tokens_per_expert
+
+    @torch.compiler.disable
+    def forward(
+        self, x: torch.Tensor
+    ) -> tuple[torch.Tensor, dict[str, torch.Tensor] | None, torch.Tensor | None]:
+        """x [batch, seq, n_embd] -> (output [batch, seq, n_embd], aux_loss dict, f_i)."""
+        batch_size, _seq_len, _n_embd = x.shape
+        x_flat = rearrange(x, "b s d -> (b s) d")
+        router_logits, router_probs, top_k_weights, selected_experts = self._router(x_flat)
+        top_k_weights_flat = rearrange(top_k_weights, "... -> (...)")
+        selected_experts_flat = rearrange(selected_experts, "... -> (...)")
+        output_flat, tokens_per_expert = self._experts(
+            x_flat, top_k_weights_flat, selected_experts_flat)
+        output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
+        aux_loss, f_i = self._aux(router_logits, router_probs, tokens_per_expert, x.dtype)
+        return output, aux_loss, f_i
+
+    def _compute_load_balance_loss(self, router_probs: torch.Tensor,
+                                   f_i: torch.Tensor) -> torch.Tensor:
+        """Load balance loss within expert groups (reference moe.py:276-303)."""
+        p_i = router_probs.mean(dim=0)
+        if len(set(self.expert_widths)) == 1:
+            return self.num_experts * (f_i.float() @ p_i.float())
+        if self._num_valid_groups == 0:
+            return f_i.float() @ p_i.float()
+        fi_pi = f_i.float() * p_i.float()
+        membership = self.group_membership.to(fi_pi.dtype)
+        if self._all_experts_valid:
+            group_sums = fi_pi @ membership
+        else:
+            fi_pi_valid = fi_pi.index_select(0, self.valid_expert_indices)
+            membership_valid = membership.index_select(0, self.valid_expert_indices)
+            group_sums = fi_pi_valid @ membership_valid
+        group_losses = self.group_sizes.to(fi_pi.dtype) * group_sums
+        return group_losses.mean()
+
+    def _expert_tensors(self, device):
+        return self.expert_weight_offsets_t, self.expert_widths_t
+
+    def forward_with_intermediates(self, x: torch.Tensor) -> dict[str, Any]:
+        """Forward returning every intermediate (reference moe.py:305-409), exact shapes."""
+        batch_size = x.shape[0]
+        device = x.device
+        x_flat = rearrange(x, "b s d -> (b s) d")
+        router_logits, router_probs, top_k_weights, selected_experts = self._router(x_flat)
+        top_k_weights_flat = rearrange(top_k_weights, "... -> (...)")
+        selected_experts_flat = rearrange(selected_experts, "... -> (...)")
+        bin_ids, indices, tokens_per_expert, bins, padded_bins = fused_route(
+            selected_experts_flat, self.num_experts, block_size=self.block_size,
+            rounding="up")
+        expert_token_offsets = torch.cat(
+            [torch.zeros(1, device=device, dtype=torch.int32), padded_bins])
+        padded_tokens_per_expert = torch.cat(
+            [padded_bins[:1], padded_bins[1:] - padded_bins[:-1]])
+        x_gathered = padded_gather(x_flat, indices, bin_ids, bins, padded_bins,
+                                   self.num_active_experts)
+        x_up = grouped_gemm_up(x_gathered, self.w1, expert_token_offsets,
+                               self.expert_weight_offsets_t, self.expert_widths_t,
+                               padded_tokens_per_expert, self.max_expert_width,
+                               activation="relu_squared")
+        x_down = grouped_gemm_down(x_up, self.w2, expert_token_offsets,
+                                   self.expert_weight_offsets_t, self.expert_widths_t,
+                                   padded_tokens_per_expert, self.config.n_embd)
+        output_flat = padded_scatter(x_down, indices, bin_ids, top_k_weights_flat, bins,
+                                     padded_bins, self.num_active_experts)
+        output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
+        return {
+            "output": output,
+            "x_flat": x_flat,
+            "router_logits": router_logits,
+            "router_probs": router_probs,
+            "top_k_weights": top_k_weights,
+            "top_k_weights_flat": top_k_weights_flat,
+            "selected_experts": selected_experts,
+            "selected_experts_flat": selected_experts_flat,
+            "bin_ids": bin_ids,
+            "indices": indices,
+            "tokens_per_expert": tokens_per_expert,
+            "bins": bins,
+            "padded_bins": padded_bins,
+            "x_gathered": x_gathered,
+            "x_after_up": x_up,
+            "x_after_down": x_down,
+            "x_scattered": output_flat,
+        }
+
+    def forward_profiled(
+        self, x: torch.Tensor, profiler
+    ) -> tuple[torch.Tensor, dict[str, torch.Tensor] | None, torch.Tensor | None]:
+        """Forward with per-step timing through profiler.step(name) contexts
+        (reference moe.py:411-518; step names kept)."""
+        batch_size = x.shape[0]
+        with profiler.step("flatten"):
+            x_flat = rearrange(x, "b s d -> (b s) d")
+        with profiler.step("routing"):
+            router_logits, router_probs, top_k_weights, selected_experts = self._router(x_flat)
+            top_k_weights_flat = rearrange(top_k_weights, "... -> (...)")
+            selected_experts_flat = rearrange(selected_experts, "... -> (...)")
+        k = self.num_active_experts
+        with profiler.step("fused_route"):
+            r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up")
+            padded_bins = r.padded_bins
+            expert_token_offsets = torch.cat(
+                [torch.zeros(1, device=x.device, dtype=torch.int32), padded_bins])
+            padded_tokens_per_expert = torch.cat(
+                [padded_bins[:1], padded_bins[1:] - padded_bins[:-1]])
+            meta = GemmMeta(expert_token_offsets, self.expert_weight_offsets_t,
+                            self.expert_widths_t, padded_tokens_per_expert, self.num_experts,
+                            self.max_expert_width, r.rows_bound)
+            nrd = r.info[0:1]
+        with profiler.step("gather"):
+            x_gathered = RoutedGatherOp.apply(x_flat, r.row_src, r.assignment_row, k,
+                                              r.rows_bound, nrd)
+        with profiler.step("gemm_up"):
+            x_up = RoutedUpOp.apply(x_gathered, self.w1, meta, x_flat, r.gather_map,
+                                    self.config.n_embd)
+        with profiler.step("gemm_down"):
+            x_down = RoutedDownOp.apply(x_up, self.w2, meta, self.config.n_embd)
+        with profiler.step("scatter"):
+            output_flat = RoutedScatterOp.apply(x_down, r.row_src, r.assignment_row,
+                                                top_k_weights_flat, k, x_flat.shape[0], nrd)
+        with profiler.step("reshape"):
+            output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
+        with profiler.step("aux_loss"):
+            aux_loss, f_i = self._aux(router_logits, router_probs, r.tokens_per_expert,
+                                      x.dtype)
+        return output, aux_loss, f_i
