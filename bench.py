@@ -162,6 +162,7 @@ def kernel_breakdown(m, xb, sel, reps):
     gh, _ = gg.down_bwd(gy, h, m.w2.detach(), meta, d, False)
     gxg, _ = gg.up_bwd(gh, x, m.w1.detach(), pre, meta, d, 1, r.gather_map)
     w1, w2 = m.w1.detach(), m.w2.detach()
+    ws = gg._dw_workspace(meta, d, x.device)
 
     def dx_only():
         from triton_moe import _lib
@@ -175,7 +176,8 @@ def kernel_breakdown(m, xb, sel, reps):
         gw = torch.empty_like(w1)
         _lib.call("vmoe_gemm_up_bwd_dw", x.data_ptr(), x.stride(0), T, r.gather_map.data_ptr(),
                   gh.data_ptr(), pre.data_ptr(), gh.stride(0), 1, gw.data_ptr(), gw.stride(0),
-                  *gg._meta_args(meta), d, meta.max_width, meta.rows, _lib.stream(x.device))
+                  *gg._meta_args(meta), d, meta.max_width, meta.rows, ws.data_ptr(), ws.numel(),
+                  _lib.stream(x.device))
 
     def dh_only():
         from triton_moe import _lib
@@ -189,7 +191,7 @@ def kernel_breakdown(m, xb, sel, reps):
         gw = torch.empty_like(w2)
         _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), gy.data_ptr(),
                   gy.stride(0), gw.data_ptr(), gw.stride(0), *gg._meta_args(meta), d,
-                  meta.max_width, meta.rows, _lib.stream(x.device))
+                  meta.max_width, meta.rows, ws.data_ptr(), ws.numel(), _lib.stream(x.device))
 
     ops = {
         "route": lambda: route_device(selv, E, k, b),

@@ -156,8 +156,15 @@ int vmoe_gemm_up_bwd_dx(const uint16_t* grad_h, const uint16_t* pre_act, int64_t
                         int64_t hidden, int64_t max_width, int64_t rows_bound,
                         vmoe_stream_t stream);
 
+/* Workspace of the two dW GEMMs' split-K (fp32 partial tiles) on the current
+ * device. A dW call with workspace == NULL runs without split-K (same result,
+ * one work item per output tile, slow when one expert holds most tokens). */
+size_t vmoe_gemm_dw_workspace_bytes(int32_t num_experts, int64_t hidden, int64_t max_width,
+                                    int64_t rows_bound);
+
 /* grad_w1[:, ewo[e]:+w_e] = X_e^T @ GA_e, X_e rows read as x[gather_map[row]]
- * when gather_map != NULL (fused gather), else x[row].
+ * when gather_map != NULL (fused gather), else x[row]. K (the expert's rows) is
+ * split into chunks summed in a fixed order, so results are deterministic.
  * Replaces _grouped_gemm_up_backward_dw_kernel
  * (triton_moe/kernels/grouped_gemm.py:805-967, launched at 1252-1290). */
 int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
@@ -166,7 +173,8 @@ int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
                         uint16_t* grad_w1, int64_t ldgw, const int32_t* eto,
                         const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
                         int32_t num_experts, int64_t hidden, int64_t max_width,
-                        int64_t rows_bound, vmoe_stream_t stream);
+                        int64_t rows_bound, void* workspace, size_t workspace_bytes,
+                        vmoe_stream_t stream);
 
 /* grad_h = grad_y @ W2_e^T (columns >= w_e untouched).
  * Replaces _grouped_gemm_down_backward_dintermediate_kernel
@@ -184,7 +192,8 @@ int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint16_t* grad_y
                           int64_t ldgy, uint16_t* grad_w2, int64_t ldgw, const int32_t* eto,
                           const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
                           int32_t num_experts, int64_t hidden, int64_t max_width,
-                          int64_t rows_bound, vmoe_stream_t stream);
+                          int64_t rows_bound, void* workspace, size_t workspace_bytes,
+                          vmoe_stream_t stream);
 
 /* Zero columns [widths[e], max_width) of every row of expert e in a padded
  * [rows, max_width] buffer: the zero-initialised tails the reference's

@@ -64,6 +64,8 @@ struct Args {
   int hidden;
   int act;
   int64_t rows_bound;
+  int kc;          // K rows per work item for the dW GEMMs (0 = whole K)
+  float* partial;  // fp32 partial tiles of split work items
 };
 
 // Per-expert problem: valid extents and operand origins.
@@ -389,33 +391,57 @@ struct Gemm {
       store_t(Bs, r.b, TLoad<BN>::N, TLoad<BN>::KB, TLoad<BN>::TOTAL);
   }
 
-  // Finds this workgroup's (expert, local tile) with a block scan of the
-  // per-expert tile counts. Returns false when the id is past the last tile.
-  __device__ static bool find_tile(const Args& p, int bid, int& e_out, int& local_out) {
-    __shared__ int32_t scan[kThreads / kWave + 1];
-    __shared__ int32_t s_e, s_local;
+  // Work items of expert e: its output tiles times its K chunks (chunks > 1
+  // only for the split-K dW GEMMs, p.kc > 0).
+  __device__ static void expert_work(const Args& p, int e, int& tiles, int& chunks) {
+    int mt, nt;
+    T::tile_dims(p, e, mt, nt);
+    tiles = (mt > 0 && nt > 0) ? cdiv(mt, BM) * cdiv(nt, BN) : 0;
+    chunks = 1;
+    if (p.kc > 0 && tiles > 0) {
+      const int K = T::prob(p, e).K;
+      chunks = K > p.kc ? cdiv(K, p.kc) : 1;
+    }
+  }
+
+  // Finds the expert owning index `id` in the concatenation of per-expert
+  // ranges of size a_e (a block scan over experts), the offset inside that
+  // range, and the exclusive prefix of a second per-expert count b_e.
+  // MODE 0: a = items, b = split items (GEMM); MODE 1: a = tiles, b = split
+  // items (reduce). Returns false when id is past the end.
+  template <int MODE>
+  __device__ static bool locate(const Args& p, int id, int& e_out, int& local_out,
+                                int& bpre_out, int& chunks_out) {
+    __shared__ long long scan[kThreads / kWave + 1];
+    __shared__ int32_t s_e, s_local, s_bpre, s_chunks;
     if (threadIdx.x == 0) s_e = -1;
-    int base = 0;
+    long long base = 0;
     for (int e0 = 0; e0 < p.E; e0 += kThreads) {
       const int e = e0 + threadIdx.x;
-      int tiles = 0;
-      if (e < p.E) {
-        int mt, nt;
-        T::tile_dims(p, e, mt, nt);
-        tiles = (mt > 0 && nt > 0) ? cdiv(mt, BM) * cdiv(nt, BN) : 0;
-      }
-      int total;
-      const int excl = block_exclusive_scan<int32_t, kThreads>(tiles, scan, &total);
-      if (tiles > 0 && bid >= base + excl && bid < base + excl + tiles) {
+      int tiles = 0, chunks = 1;
+      if (e < p.E) expert_work(p, e, tiles, chunks);
+      const int items = tiles * chunks;
+      const int a = MODE == 0 ? items : tiles;
+      const int b = chunks > 1 ? items : 0;
+      const long long packed = ((long long)a << 32) | (long long)b;
+      long long total;
+      const long long ex = block_exclusive_scan<long long, kThreads>(packed, scan, &total);
+      const long long pre = base + ex;
+      const int a_pre = (int)(pre >> 32), b_pre = (int)(pre & 0xFFFFFFFFll);
+      if (a > 0 && id >= a_pre && id < a_pre + a) {
         s_e = e;
-        s_local = bid - base - excl;
+        s_local = id - a_pre;
+        s_bpre = b_pre;
+        s_chunks = chunks;
       }
       base += total;
       __syncthreads();
-      if (s_e >= 0 || base > bid) break;
+      if (s_e >= 0 || (int)(base >> 32) > id) break;
     }
     e_out = s_e;
     local_out = s_local;
+    bpre_out = s_bpre;
+    chunks_out = s_chunks;
     return s_e >= 0;
   }
 
@@ -429,14 +455,21 @@ struct Gemm {
     const int g = gridDim.x, b = blockIdx.x;
     const int bid = (b % 8) * (g / 8) + b / 8;
 
-    int e, local;
-    if (!find_tile(p, bid, e, local)) return;
+    int e, local, split_pre, chunks;
+    if (!locate<0>(p, bid, e, local, split_pre, chunks)) return;
     int mt_dim, nt_dim;
     T::tile_dims(p, e, mt_dim, nt_dim);
     const int n_tiles = cdiv(nt_dim, BN);
-    const int m0 = (local / n_tiles) * BM;
-    const int n0 = (local % n_tiles) * BN;
-    const Prob q = T::prob(p, e);
+    const int tile = local / chunks, chunk = local % chunks;
+    const int m0 = (tile / n_tiles) * BM;
+    const int n0 = (tile % n_tiles) * BN;
+    Prob q = T::prob(p, e);
+    // K range of this work item: [kbeg, q.K) after clamping q.K to the chunk.
+    int kbeg = 0;
+    if (chunks > 1) {
+      kbeg = chunk * p.kc;
+      q.K = min(q.K, kbeg + p.kc);
+    }
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -450,10 +483,10 @@ struct Gemm {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int nk = q.K > 0 ? cdiv(q.K, BK) : 0;
+    const int nk = q.K > kbeg ? cdiv(q.K - kbeg, BK) : 0;
     Regs regs;
     if (nk > 0) {
-      load_tiles(p, q, m0, n0, 0, regs);
+      load_tiles(p, q, m0, n0, kbeg, regs);
       store_tiles(p, As, Bs, regs);
     }
     __syncthreads();
@@ -462,7 +495,7 @@ struct Gemm {
     const int frag_k = (lane >> 5) * 8;
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;
-      if (kt + 1 < nk) load_tiles(p, q, m0, n0, (kt + 1) * BK, regs);
+      if (kt + 1 < nk) load_tiles(p, q, m0, n0, kbeg + (kt + 1) * BK, regs);
       const uint16_t* Ac = As + cur * A_ELEMS;
       const uint16_t* Bc = Bs + cur * B_ELEMS;
 #pragma unroll
@@ -491,6 +524,25 @@ struct Gemm {
 
     // Epilogue. acc[i][j][4*g + r] sits at m = wm*WM + i*32 + (lane & 31),
     // n = wn*WN + j*32 + 8*g + 4*(lane >> 5) + r.
+    if (chunks > 1) {
+      // Split-K item: the whole fp32 tile goes to its partial slot; the
+      // reduce kernel sums the chunks in chunk order and rounds once.
+      float* slot = p.partial + (int64_t)(split_pre + local) * (BM * BN);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int ml = wm * WM + i * 32 + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            const int nl = wn * WN + j * 32 + 8 * gq + 4 * (lane >> 5);
+            *reinterpret_cast<float4*>(slot + ml * BN + nl) =
+                make_float4(acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
+                            acc[i][j][4 * gq + 3]);
+          }
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int m = m0 + wm * WM + i * 32 + (lane & 31);
@@ -525,10 +577,77 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
   Gemm<V, BM, BN, BK>::run(p);
 }
 
+// Sums the K-chunk partials of every split (expert, tile) in chunk order and
+// stores the bf16 result. One workgroup per output tile; tiles of experts that
+// were not split exit at once (their GEMM item stored bf16 directly).
+template <int V, int BM, int BN, int BK>
+__global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(Args p) {
+  using G = Gemm<V, BM, BN, BK>;
+  const int g = gridDim.x, b = blockIdx.x;
+  const int id = (b % 8) * (g / 8) + b / 8;
+  int e, tile, split_pre, chunks;
+  if (!G::template locate<1>(p, id, e, tile, split_pre, chunks)) return;
+  if (chunks <= 1) return;
+  int mt_dim, nt_dim;
+  Traits<V>::tile_dims(p, e, mt_dim, nt_dim);
+  const int n_tiles = cdiv(nt_dim, BN);
+  const int m0 = (tile / n_tiles) * BM, n0 = (tile % n_tiles) * BN;
+  const Prob q = Traits<V>::prob(p, e);
+  const float* base = p.partial + (int64_t)(split_pre + tile * chunks) * (BM * BN);
+  for (int idx = threadIdx.x * 4; idx < BM * BN; idx += kThreads * 4) {
+    const int ml = idx / BN, nl = idx % BN;
+    const int m = m0 + ml, n = n0 + nl;
+    if (m >= q.M || n >= q.N) continue;
+    float4 acc = *reinterpret_cast<const float4*>(base + idx);
+    for (int c = 1; c < chunks; ++c) {
+      const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)c * (BM * BN) + idx);
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    *reinterpret_cast<uint2*>(p.c + (q.cr + m) * p.ldc + q.cc + n) =
+        make_uint2(pack_bf16(acc.x, acc.y), pack_bf16(acc.z, acc.w));
+  }
+}
+
 // Tile configuration (one for all variants for now).
 constexpr int kBM = 128, kBN = 128, kBK = 32;
 
 inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Compute units of the current device (cached per device id).
+int cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Split-K plan of a dW GEMM: K rows per work item, and the partial-tile
+// capacity it can need. The chunk keeps a work item near a quarter of one
+// CU's share of the whole dW (tiles_max * rows_bound row-tiles), so one
+// heavily loaded expert is spread over many CUs; it never drops below 1024
+// rows, so lightly loaded layers do not pay for partials.
+struct SplitPlan {
+  int kc;
+  int64_t slots;  // partial tiles
+};
+
+SplitPlan split_plan(int64_t tiles_max, int64_t rows_bound) {
+  const int64_t cus = cu_count();
+  int64_t kc = (tiles_max * rows_bound) / (4 * cus);
+  kc = std::max<int64_t>(1024, (kc + kBK - 1) / kBK * kBK);
+  kc = std::min<int64_t>(kc, 1 << 30);
+  SplitPlan sp;
+  sp.kc = (int)kc;
+  sp.slots = tiles_max * (2 * ((rows_bound + kc - 1) / kc) + 1);
+  return sp;
+}
 
 template <int V>
 int launch(const Args& p, int64_t grid_tiles, hipStream_t s) {
@@ -550,6 +669,30 @@ int launch(const Args& p, int64_t grid_tiles, hipStream_t s) {
   hipLaunchKernelGGL(kern, dim3((unsigned)g), dim3(kThreads), G::LDS_BYTES, s, p);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
+}
+
+// dW GEMM with split-K: GEMM items, then the chunk reduction.
+template <int V>
+int launch_dw(Args p, int64_t tiles_max, void* ws, size_t ws_bytes, hipStream_t s) {
+  const int64_t E = p.E;
+  if (ws) {
+    const SplitPlan sp = split_plan(tiles_max, p.rows_bound);
+    if (ws_bytes < (size_t)sp.slots * kBM * kBN * sizeof(float)) return VMOE_ERR_WORKSPACE;
+    p.kc = sp.kc;
+    p.partial = reinterpret_cast<float*>(ws);
+    const int64_t items = tiles_max * (E + p.rows_bound / sp.kc + 1);
+    int st = launch<V>(p, items, s);
+    if (st) return st;
+    int64_t g = (E * tiles_max + 7) / 8 * 8;
+    if (g > INT32_MAX) return VMOE_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((splitk_reduce_kernel<V, kBM, kBN, kBK>), dim3((unsigned)g),
+                       dim3(kThreads), 0, s, p);
+    VMOE_CHECK_LAUNCH();
+    return VMOE_OK;
+  }
+  p.kc = 0;
+  p.partial = nullptr;
+  return launch<V>(p, E * tiles_max, s);
 }
 
 // Shared argument checks. Every dimension the kernels vectorise over must be a
@@ -648,13 +791,23 @@ extern "C" int vmoe_gemm_up_bwd_dx(const uint16_t* grad_h, const uint16_t* pre_a
   return launch<UP_DX>(p, tiles, reinterpret_cast<hipStream_t>(stream));
 }
 
+extern "C" size_t vmoe_gemm_dw_workspace_bytes(int32_t E, int64_t hidden, int64_t max_width,
+                                               int64_t rows_bound) {
+  if (E <= 0 || hidden <= 0 || max_width <= 0 || rows_bound <= 0) return 0;
+  const int64_t up_tiles = ((hidden + kBM - 1) / kBM) * ((max_width + kBN - 1) / kBN);
+  const int64_t down_tiles = ((max_width + kBM - 1) / kBM) * ((hidden + kBN - 1) / kBN);
+  const SplitPlan a = split_plan(up_tiles, rows_bound), b = split_plan(down_tiles, rows_bound);
+  return (size_t)std::max(a.slots, b.slots) * kBM * kBN * sizeof(float);
+}
+
 extern "C" int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
                                    const int32_t* gather_map, const uint16_t* grad_h,
                                    const uint16_t* pre_act, int64_t ldg, int32_t activation,
                                    uint16_t* grad_w1, int64_t ldgw, const int32_t* eto,
                                    const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
                                    int32_t E, int64_t hidden, int64_t max_width,
-                                   int64_t rows_bound, vmoe_stream_t stream) {
+                                   int64_t rows_bound, void* workspace, size_t workspace_bytes,
+                                   vmoe_stream_t stream) {
   int st = check_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
   if (st) return st;
   if (activation != VMOE_ACT_NONE && activation != VMOE_ACT_RELU_SQUARED)
@@ -671,9 +824,9 @@ extern "C" int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_row
   p.c = grad_w1; p.ldc = ldgw;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = activation; p.rows_bound = rows_bound;
-  const int64_t tiles =
-      (int64_t)E * ((hidden + kBM - 1) / kBM) * ((max_width + kBN - 1) / kBN);
-  return launch<UP_DW>(p, tiles, reinterpret_cast<hipStream_t>(stream));
+  const int64_t tiles_max = ((hidden + kBM - 1) / kBM) * ((max_width + kBN - 1) / kBN);
+  return launch_dw<UP_DW>(p, tiles_max, workspace, workspace_bytes,
+                          reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, const uint16_t* w2,
@@ -704,6 +857,7 @@ extern "C" int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint1
                                      const int32_t* eto, const int32_t* ewo,
                                      const int32_t* widths, const int32_t* tpe, int32_t E,
                                      int64_t hidden, int64_t max_width, int64_t rows_bound,
+                                     void* workspace, size_t workspace_bytes,
                                      vmoe_stream_t stream) {
   int st = check_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
   if (st) return st;
@@ -717,7 +871,7 @@ extern "C" int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint1
   p.c = grad_w2; p.ldc = ldgw;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
-  const int64_t tiles =
-      (int64_t)E * ((max_width + kBM - 1) / kBM) * ((hidden + kBN - 1) / kBN);
-  return launch<DOWN_DW>(p, tiles, reinterpret_cast<hipStream_t>(stream));
+  const int64_t tiles_max = ((max_width + kBM - 1) / kBM) * ((hidden + kBN - 1) / kBN);
+  return launch_dw<DOWN_DW>(p, tiles_max, workspace, workspace_bytes,
+                            reinterpret_cast<hipStream_t>(stream));
 }

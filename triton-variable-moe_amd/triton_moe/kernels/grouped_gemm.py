@@ -124,6 +124,12 @@ def _meta_args(m: GemmMeta):
             m.num_experts)
 
 
+def _dw_workspace(m: GemmMeta, hidden: int, device) -> torch.Tensor:
+    n = int(_lib.lib().vmoe_gemm_dw_workspace_bytes(m.num_experts, hidden, m.max_width,
+                                                    max(m.rows, 1)))
+    return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
+
+
 def _zero_tails(buf: torch.Tensor, m: GemmMeta):
     if m.uniform or buf.shape[0] == 0:
         return
@@ -214,10 +220,11 @@ def up_bwd(grad_h, x, w1, pre, m: GemmMeta, hidden: int, act: int,
                   act, w1.data_ptr(), w1.stride(0), grad_x.data_ptr(), grad_x.stride(0),
                   *_meta_args(m), hidden, m.max_width, m.rows, _lib.stream(dev))
     gm = None if gather_map is None else _i32(gather_map)
+    ws = _dw_workspace(m, hidden, dev)
     _lib.call("vmoe_gemm_up_bwd_dw", x.data_ptr(), x.stride(0), x.shape[0], _lib.ptr(gm),
               grad_h.data_ptr(), _lib.ptr(pre), grad_h.stride(0), act, grad_w1.data_ptr(),
               grad_w1.stride(0), *_meta_args(m), hidden, m.max_width, m.rows,
-              _lib.stream(dev))
+              ws.data_ptr(), ws.numel(), _lib.stream(dev))
     return grad_x, grad_w1
 
 
@@ -240,9 +247,10 @@ def down_bwd(grad_y, h, w2, m: GemmMeta, hidden: int, zero_tails: bool):
                   m.max_width, m.rows, _lib.stream(dev))
         if zero_tails:
             _zero_tails(grad_h, m)
+    ws = _dw_workspace(m, hidden, dev)
     _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), grad_y.data_ptr(),
               grad_y.stride(0), grad_w2.data_ptr(), grad_w2.stride(0), *_meta_args(m), hidden,
-              m.max_width, m.rows, _lib.stream(dev))
+              m.max_width, m.rows, ws.data_ptr(), ws.numel(), _lib.stream(dev))
     return grad_h, grad_w2
 
 
