@@ -159,35 +159,32 @@ def kernel_breakdown(m, xb, sel, reps):
     y = gg.down_fwd(h, m.w2.detach(), meta, d)
     G = torch.ones(T, d, dtype=torch.bfloat16, device=x.device)
     gy = gather_rows(G, r.row_src, k, r.rows_bound, weights=wts, num_rows_dev=nrd)
-    gh, _ = gg.down_bwd(gy, h, m.w2.detach(), meta, d, False)
-    gxg, _ = gg.up_bwd(gh, x, m.w1.detach(), pre, meta, d, 1, r.gather_map)
     w1, w2 = m.w1.detach(), m.w2.detach()
+    ga, _ = gg.down_bwd(gy, h, w2, meta, d, False, pre=pre)
+    gxg, _ = gg.up_bwd_from_ga(ga, x, w1, meta, d, r.gather_map)
     ws = gg._dw_workspace(meta, d, x.device)
+    from triton_moe import _lib
 
     def dx_only():
-        from triton_moe import _lib
         gx = torch.empty(meta.rows, d, dtype=torch.bfloat16, device=x.device)
-        _lib.call("vmoe_gemm_up_bwd_dx", gh.data_ptr(), pre.data_ptr(), gh.stride(0), 1,
-                  w1.data_ptr(), w1.stride(0), gx.data_ptr(), gx.stride(0), *gg._meta_args(meta),
-                  d, meta.max_width, meta.rows, _lib.stream(x.device))
+        _lib.call("vmoe_gemm_up_bwd_dx", ga.data_ptr(), ga.stride(0), w1.data_ptr(),
+                  w1.stride(0), gx.data_ptr(), gx.stride(0), *gg._meta_args(meta), d,
+                  meta.max_width, meta.rows, _lib.stream(x.device))
 
     def dw1_only():
-        from triton_moe import _lib
         gw = torch.empty_like(w1)
         _lib.call("vmoe_gemm_up_bwd_dw", x.data_ptr(), x.stride(0), T, r.gather_map.data_ptr(),
-                  gh.data_ptr(), pre.data_ptr(), gh.stride(0), 1, gw.data_ptr(), gw.stride(0),
+                  ga.data_ptr(), ga.stride(0), gw.data_ptr(), gw.stride(0),
                   *gg._meta_args(meta), d, meta.max_width, meta.rows, ws.data_ptr(), ws.numel(),
                   _lib.stream(x.device))
 
     def dh_only():
-        from triton_moe import _lib
         o = torch.empty(meta.rows, meta.max_width, dtype=torch.bfloat16, device=x.device)
         _lib.call("vmoe_gemm_down_bwd_dh", gy.data_ptr(), gy.stride(0), w2.data_ptr(),
-                  w2.stride(0), o.data_ptr(), o.stride(0), *gg._meta_args(meta), d,
-                  meta.max_width, meta.rows, _lib.stream(x.device))
+                  w2.stride(0), pre.data_ptr(), o.data_ptr(), o.stride(0), *gg._meta_args(meta),
+                  d, meta.max_width, meta.rows, _lib.stream(x.device))
 
     def dw2_only():
-        from triton_moe import _lib
         gw = torch.empty_like(w2)
         _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), gy.data_ptr(),
                   gy.stride(0), gw.data_ptr(), gw.stride(0), *gg._meta_args(meta), d,
@@ -201,7 +198,7 @@ def kernel_breakdown(m, xb, sel, reps):
         "combine": lambda: combine_rows(y, r.assignment_row, k, T, weights=wts),
         "scatter_bwd_gather": lambda: gather_rows(G, r.row_src, k, r.rows_bound, weights=wts,
                                                   num_rows_dev=nrd),
-        "gemm_down_bwd_dh": dh_only,
+        "gemm_down_bwd_dh_ga": dh_only,
         "gemm_down_bwd_dw": dw2_only,
         "gemm_up_bwd_dx": dx_only,
         "gemm_up_bwd_dw": dw1_only,

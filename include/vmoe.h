@@ -146,15 +146,23 @@ int vmoe_gemm_down_fwd(const uint16_t* h, int64_t ldh, const uint16_t* w2, int64
                        int64_t hidden, int64_t max_width, int64_t rows_bound,
                        vmoe_stream_t stream);
 
-/* grad_x = GA @ W1_e^T with GA = bf16(pre>0 ? 2*grad_h*pre : 0) (relu^2) or grad_h.
+/* GA = bf16(pre_act > 0 ? 2 * grad_h * pre_act : 0) elementwise over
+ * [rows, cols]: the relu^2 derivative of the reference's backward kernels
+ * (triton_moe/kernels/grouped_gemm.py:751-766, 914-928), for callers holding
+ * grad_h and pre_act separately. cols, ld, ldo multiples of 8. */
+int vmoe_relu2_grad(const uint16_t* grad_h, const uint16_t* pre_act, int64_t ld,
+                    uint16_t* grad_act, int64_t ldo, int64_t rows, int64_t cols,
+                    vmoe_stream_t stream);
+
+/* grad_x = GA_e @ W1_e^T, GA = gradient w.r.t. the pre-activation (the output
+ * of vmoe_relu2_grad, or grad_h itself for activation "none").
  * Replaces _grouped_gemm_up_backward_dx_kernel
  * (triton_moe/kernels/grouped_gemm.py:654-802, launched at 1214-1250). */
-int vmoe_gemm_up_bwd_dx(const uint16_t* grad_h, const uint16_t* pre_act, int64_t ldg,
-                        int32_t activation, const uint16_t* w1, int64_t ldw1,
-                        uint16_t* grad_x, int64_t ldgx, const int32_t* eto, const int32_t* ewo,
-                        const int32_t* widths, const int32_t* tpe, int32_t num_experts,
-                        int64_t hidden, int64_t max_width, int64_t rows_bound,
-                        vmoe_stream_t stream);
+int vmoe_gemm_up_bwd_dx(const uint16_t* grad_act, int64_t ldg, const uint16_t* w1,
+                        int64_t ldw1, uint16_t* grad_x, int64_t ldgx, const int32_t* eto,
+                        const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
+                        int32_t num_experts, int64_t hidden, int64_t max_width,
+                        int64_t rows_bound, vmoe_stream_t stream);
 
 /* Workspace of the two dW GEMMs' split-K (fp32 partial tiles) on the current
  * device. A dW call with workspace == NULL runs without split-K (same result,
@@ -168,22 +176,25 @@ size_t vmoe_gemm_dw_workspace_bytes(int32_t num_experts, int64_t hidden, int64_t
  * Replaces _grouped_gemm_up_backward_dw_kernel
  * (triton_moe/kernels/grouped_gemm.py:805-967, launched at 1252-1290). */
 int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
-                        const int32_t* gather_map, const uint16_t* grad_h,
-                        const uint16_t* pre_act, int64_t ldg, int32_t activation,
+                        const int32_t* gather_map, const uint16_t* grad_act, int64_t ldg,
                         uint16_t* grad_w1, int64_t ldgw, const int32_t* eto,
                         const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
                         int32_t num_experts, int64_t hidden, int64_t max_width,
                         int64_t rows_bound, void* workspace, size_t workspace_bytes,
                         vmoe_stream_t stream);
 
-/* grad_h = grad_y @ W2_e^T (columns >= w_e untouched).
+/* grad_h = grad_y @ W2_e^T (columns >= w_e untouched). With pre_act != NULL
+ * (same leading dimension as grad_h) the output is instead the relu^2
+ * gradient GA = bf16(pre_act > 0 ? 2 * bf16(grad_h) * pre_act : 0), computed in
+ * the epilogue, which is what the up-projection backward consumes.
  * Replaces _grouped_gemm_down_backward_dintermediate_kernel
  * (triton_moe/kernels/grouped_gemm.py:970-1063, launched at 1336-1362). */
 int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, const uint16_t* w2,
-                          int64_t ldw2, uint16_t* grad_h, int64_t ldgh, const int32_t* eto,
-                          const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
-                          int32_t num_experts, int64_t hidden, int64_t max_width,
-                          int64_t rows_bound, vmoe_stream_t stream);
+                          int64_t ldw2, const uint16_t* pre_act, uint16_t* grad_h,
+                          int64_t ldgh, const int32_t* eto, const int32_t* ewo,
+                          const int32_t* widths, const int32_t* tpe, int32_t num_experts,
+                          int64_t hidden, int64_t max_width, int64_t rows_bound,
+                          vmoe_stream_t stream);
 
 /* grad_w2[ewo[e]:+w_e, :] = H_e^T @ grad_y_e.
  * Replaces _grouped_gemm_down_backward_dw_kernel

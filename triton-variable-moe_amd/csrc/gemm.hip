@@ -12,25 +12,32 @@
 //   DOWN_DW  _grouped_gemm_down_backward_dw_kernel   (grouped_gemm.py:1066-1162)
 //
 // Design:
-//  * Tile scheduler on the device: the grid is an upper bound of the tile
-//    count; each workgroup scans the per-expert tile counts (from the same
-//    metadata the reference reads) in LDS and finds its (expert, tile), so no
-//    host sync is needed and empty experts cost nothing. Workgroup ids are
-//    remapped so that consecutive tiles (same expert, same weight slice) run on
-//    the same XCD and share its L2.
-//  * 256 threads = 4 waves in a 2x2 grid, each wave owns a (BM/2)x(BN/2) block
-//    of 32x32 MFMA accumulators (fp32).
-//  * Operands are staged through double-buffered LDS in K-contiguous form,
-//    which is what the MFMA fragments want (8 consecutive k per lane, one
-//    ds_read_b128). K-contiguous sources are copied with 16-byte vectors;
-//    M/N-contiguous sources (W1/W2 in the forward, both dW operands) are
-//    transposed in registers (4x8 blocks) on their way into LDS.
-//  * relu^2 gradient GA = bf16(pre > 0 ? 2 * grad * pre : 0) is formed on the
-//    fly in the operand load (grouped_gemm.py:751-766, 914-928); relu / relu^2
-//    are applied to the fp32 accumulator in the epilogue (grouped_gemm.py:336-346).
+//  * Tile scheduler on the device: the grid is an upper bound of the work
+//    count; each workgroup scans the per-expert work counts (from the same
+//    metadata the reference reads) and finds its (expert, tile, K chunk), so
+//    no host sync is needed and empty experts cost nothing. Workgroup ids are
+//    remapped so that consecutive tiles (same expert, same weight slice) run
+//    on the same XCD and share its L2.
+//  * 256 threads = 4 waves in a 2x2 grid; each wave owns (BM/2)x(BN/2) of
+//    32x32 MFMA accumulators (fp32; 128x128 per wave for 256x256 tiles).
+//  * Every operand tile goes global -> LDS by DMA (global_load_lds, 16 bytes
+//    per lane), never through VGPRs, in a multi-stage ring: the loads of
+//    tile k+STAGES-1 fly while tile k is multiplied.
+//      - K-contiguous sources (activations in the forward, W in dX/dH) land
+//        in "K-form": one 64-byte row per m (n), 16-byte chunk c of row r at
+//        c ^ ((r >> 1) & 3); MFMA fragments are one ds_read_b128.
+//      - M/N-contiguous sources (W1/W2 in the forward, both dW operands)
+//        land as they are in memory ("T-form": one row per k), chunk c of
+//        k-row k at c ^ 2(k & 3); fragments are two ds_read_b64_tr_b16,
+//        the gfx950 LDS transpose read, so no operand is transposed in
+//        registers. Both swizzles make the fragment reads bank-conflict free.
+//  * Epilogues: relu and relu^2 of the fp32 accumulator (PRE, H) for the up
+//    projection (grouped_gemm.py:336-346); for the down dH GEMM an optional
+//    fused relu^2 gradient GA = bf16(pre > 0 ? 2 * bf16(acc) * pre : 0)
+//    (grouped_gemm.py:751-766), so dX and dW read GA directly; split-K fp32
+//    partial tiles for the dW GEMMs, summed in chunk order by a second pass.
 
 #include <algorithm>
-#include <mutex>
 
 #include "vmoe_common.h"
 
@@ -38,24 +45,28 @@ namespace vmoe {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) char lds_char;
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4;
+typedef __attribute__((address_space(3))) bf16x8_t lds_bf16x8;
 
 constexpr int kThreads = 256;
+constexpr int kBK = 32;  // k per LDS stage: two 16-deep MFMA steps
 
 enum Variant { UP_FWD = 0, DOWN_FWD, UP_DX, UP_DW, DOWN_DH, DOWN_DW };
 
 struct Args {
-  const uint16_t* a;    // A source
-  const uint16_t* a2;   // pre_act, for the gradient prologue on A
+  const uint16_t* a;     // A source
   int64_t lda;
-  const int32_t* a_map;  // row gather for A (UP_DW fused gather), nullable
+  const int32_t* a_map;  // row gather for A (fused gather), nullable
   int64_t a_rows;        // rows of the gathered source
   const uint16_t* b;
-  const uint16_t* b2;    // pre_act, for the gradient prologue on B
   int64_t ldb;
   uint16_t* c;
-  uint16_t* c2;  // pre_act output (UP_FWD)
   int64_t ldc;
+  uint16_t* c2;          // UP_FWD: pre_act output (nullable)
+  const uint16_t* pre;   // DOWN_DH: pre_act input -> fused relu^2 gradient (nullable)
   const int32_t* eto;
   const int32_t* ewo;
   const int32_t* widths;
@@ -79,14 +90,14 @@ struct Prob {
   int64_t ar, ac, br, bc, cr, cc;
 };
 
+__device__ __forceinline__ int clamp0(int64_t v) { return (int)max<int64_t>(0, v); }
+
 template <int V>
 struct Traits;
 
-__device__ __forceinline__ int clamp0(int64_t v) { return (int)max<int64_t>(0, v); }
-
 template <>
 struct Traits<UP_FWD> {
-  static constexpr bool a_k = true, b_k = false, a_grad = false, b_grad = false;
+  static constexpr bool a_k = true, b_k = false;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.tpe[e];
     nt = p.widths[e];
@@ -98,7 +109,7 @@ struct Traits<UP_FWD> {
     q.N = clamp0(p.widths[e]);
     q.K = p.hidden;
     q.ar = t0; q.ac = 0;
-    q.br = 0; q.bc = p.ewo[e];
+    q.br = 0; q.bc = p.ewo[e];  // B(k,n) = W1[k][ewo + n]
     q.cr = t0; q.cc = 0;
     return q;
   }
@@ -106,7 +117,7 @@ struct Traits<UP_FWD> {
 
 template <>
 struct Traits<DOWN_FWD> {
-  static constexpr bool a_k = true, b_k = false, a_grad = false, b_grad = false;
+  static constexpr bool a_k = true, b_k = false;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.tpe[e];
     nt = p.hidden;
@@ -118,7 +129,7 @@ struct Traits<DOWN_FWD> {
     q.N = p.hidden;
     q.K = clamp0((int64_t)p.ewo[e + 1] - p.ewo[e]);
     q.ar = t0; q.ac = 0;
-    q.br = p.ewo[e]; q.bc = 0;
+    q.br = p.ewo[e]; q.bc = 0;  // B(k,n) = W2[ewo + k][n]
     q.cr = t0; q.cc = 0;
     return q;
   }
@@ -126,7 +137,7 @@ struct Traits<DOWN_FWD> {
 
 template <>
 struct Traits<UP_DX> {
-  static constexpr bool a_k = true, b_k = true, a_grad = true, b_grad = false;
+  static constexpr bool a_k = true, b_k = true;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.tpe[e];
     nt = p.hidden;
@@ -137,7 +148,7 @@ struct Traits<UP_DX> {
     q.M = clamp0(min<int64_t>(p.tpe[e], t1 - t0));
     q.N = p.hidden;
     q.K = clamp0((int64_t)p.ewo[e + 1] - p.ewo[e]);
-    q.ar = t0; q.ac = 0;
+    q.ar = t0; q.ac = 0;        // A(m,k) = GA[t0 + m][k]
     q.br = 0; q.bc = p.ewo[e];  // B(k,n) = W1[n][ewo + k]
     q.cr = t0; q.cc = 0;
     return q;
@@ -146,7 +157,7 @@ struct Traits<UP_DX> {
 
 template <>
 struct Traits<UP_DW> {
-  static constexpr bool a_k = false, b_k = false, a_grad = false, b_grad = true;
+  static constexpr bool a_k = false, b_k = false;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.hidden;
     nt = p.widths[e];
@@ -166,7 +177,7 @@ struct Traits<UP_DW> {
 
 template <>
 struct Traits<DOWN_DH> {
-  static constexpr bool a_k = true, b_k = true, a_grad = false, b_grad = false;
+  static constexpr bool a_k = true, b_k = true;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.tpe[e];
     nt = p.widths[e];
@@ -186,7 +197,7 @@ struct Traits<DOWN_DH> {
 
 template <>
 struct Traits<DOWN_DW> {
-  static constexpr bool a_k = false, b_k = false, a_grad = false, b_grad = false;
+  static constexpr bool a_k = false, b_k = false;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.widths[e];
     nt = p.hidden;
@@ -204,191 +215,185 @@ struct Traits<DOWN_DW> {
   }
 };
 
+// Tile shape per variant: 256x128 for the GEMMs tiled over rows (large M),
+// 128x128 for the dW GEMMs (M, N are hidden x width; split-K supplies the
+// parallelism, and smaller tiles keep partial tiles cheap).
+template <int V>
+struct Cfg {
+  static constexpr bool dw = V == UP_DW || V == DOWN_DW;
+  static constexpr int BM = dw ? 128 : 256;
+  static constexpr int BN = 128;
+  static constexpr int STAGES = 2;  // double-buffered LDS ring
+};
+
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 
-// GA = bf16(pre > 0 ? 2 * g * pre : 0) for relu^2, else g; 8 values at once.
-__device__ __forceinline__ uint4 relu2_grad(uint4 g, uint4 pre, int act) {
-  if (act != VMOE_ACT_RELU_SQUARED) return g;
-  uint32_t gw[4] = {g.x, g.y, g.z, g.w}, pw[4] = {pre.x, pre.y, pre.z, pre.w}, o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float pl = lo_f32(pw[i]), ph = hi_f32(pw[i]);
-    const float vl = pl > 0.0f ? lo_f32(gw[i]) * 2.0f * pl : 0.0f;
-    const float vh = ph > 0.0f ? hi_f32(gw[i]) * 2.0f * ph : 0.0f;
-    o[i] = pack_bf16(vl, vh);
-  }
-  return make_uint4(o[0], o[1], o[2], o[3]);
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__device__ __forceinline__ uint32_t half_of(const uint4& v, int i) {
-  const uint32_t w = i < 2 ? (i == 0 ? v.x : v.y) : (i == 2 ? v.z : v.w);
-  return w;
+// Buffer resource over [base, base + 2 GiB): word 3 = 0x00020000 is the raw
+// 32-bit-dword format of the gfx9 family. A lane whose offset is kOob (past
+// num_records) reads zeros, which is how every masked lane is handled.
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  // The base is block-uniform; readfirstlane keeps the resource in SGPRs
+  // (a VGPR resource would force a waterfall loop around every DMA).
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* b = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(b, 0, 0x7FFFFFFF, 0x00020000);
 }
 
-// Register transpose of a 4(k) x 8(mn) bf16 block into 8 rows of 4 k-values.
-// in[kk] holds mn = 0..7 at k = kk; out[mm] = {k0|k1, k2|k3} at mn = mm.
-__device__ __forceinline__ void transpose4x8(const uint4 in[4], uint2 out[8]) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const uint32_t a0 = half_of(in[0], w), a1 = half_of(in[1], w);
-    const uint32_t a2 = half_of(in[2], w), a3 = half_of(in[3], w);
-    // even mn = 2w: low halves; odd mn = 2w+1: high halves
-    out[2 * w].x = (a0 & 0xFFFFu) | (a1 << 16);
-    out[2 * w].y = (a2 & 0xFFFFu) | (a3 << 16);
-    out[2 * w + 1].x = (a0 >> 16) | (a1 & 0xFFFF0000u);
-    out[2 * w + 1].y = (a2 >> 16) | (a3 & 0xFFFF0000u);
-  }
+// 16-byte DMA of the lane's source into LDS at dst + 16 * lane.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, lds_char* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, reinterpret_cast<__attribute__((address_space(3))) void*>(dst), 16, (int)voff, 0, 0, 0);
 }
 
-template <int V, int BM, int BN, int BK>
+template <int V, int BM, int BN, int STAGES>
 struct Gemm {
   using T = Traits<V>;
-  static constexpr int LDK = BK + 8;  // LDS row pitch (bf16): 16-byte pad
-  static constexpr int WM = BM / 2, WN = BN / 2;  // wave tile
+  static constexpr int BK = kBK;
+  static constexpr int WM = BM / 2, WN = BN / 2;    // wave tile
   static constexpr int FM = WM / 32, FN = WN / 32;  // 32x32 blocks per wave
-  static constexpr int A_ELEMS = BM * LDK, B_ELEMS = BN * LDK;
-  static constexpr size_t LDS_BYTES = 2 * (A_ELEMS + B_ELEMS) * sizeof(uint16_t);
-
-  // K-contig loader: 16-byte chunks, ROWS x BK tile.
-  template <int ROWS>
-  struct KLoad {
-    static constexpr int CPR = BK / 8;  // chunks per row
-    static constexpr int TOTAL = ROWS * CPR;
-    static constexpr int N = cdiv(TOTAL, kThreads);
+  static constexpr int A_STAGE = BM * BK * 2, B_STAGE = BN * BK * 2;  // bytes
+  static constexpr int STAGE = A_STAGE + B_STAGE;
+  static constexpr int LDS_BYTES = STAGES * STAGE;
+  // DMA instructions per wave per stage for an operand of R rows/cols.
+  template <int R>
+  struct Dma {
+    static constexpr int INSTS = R * BK / 8 / 64;
+    static constexpr int PW = INSTS / 4;
+    static constexpr int LPR = R / 8;        // T-form: lanes per k-row
+    static constexpr int RPI = 64 / LPR;     // T-form: k-rows per instruction
+    static_assert(INSTS % 4 == 0 && PW >= 1, "tile too small for 4 waves");
   };
-  // MN-contig loader: 8(mn) x 4(k) blocks.
-  template <int COLS>
-  struct TLoad {
-    static constexpr int KB = BK / 4, MB = COLS / 8;
-    static constexpr int TOTAL = KB * MB;
-    static constexpr int N = cdiv(TOTAL, kThreads);
+  static constexpr int PWA = Dma<BM>::PW, PWB = Dma<BN>::PW;
+
+  __device__ static int kswz(int r) { return (r >> 1) & 3; }
+  __device__ static int tswz(int k) { return (k & 3) << 1; }
+
+  // Per-thread DMA state of one operand: a buffer resource over the
+  // operand (rebased to the tile where no row map is used) and one 32-bit
+  // byte offset per DMA instruction.
+  template <int PW>
+  struct Src {
+    __amdgpu_buffer_rsrc_t rsrc;
+    const int32_t* map;  // T-form row gather (nullable)
+    int64_t map_rows;
+    int64_t r0;          // T-form with map: source row of k = 0
+    uint32_t ld2;        // leading dimension in bytes
+    uint32_t off[PW];    // K-form: row + chunk; T-form: chunk column (+ k-row without map)
+    int idx[PW];         // K-form: k of the lane's chunk; T-form: the lane's k-row
+    bool ok[PW];         // K-form: row valid; T-form: column valid
   };
 
-  static constexpr int NA = T::a_k ? KLoad<BM>::N : TLoad<BM>::N * 4;
-  static constexpr int NB = T::b_k ? KLoad<BN>::N : TLoad<BN>::N * 4;
-
-  struct Regs {
-    uint4 a[NA];
-    uint4 a2[T::a_grad ? NA : 1];
-    uint4 b[NB];
-    uint4 b2[T::b_grad ? NB : 1];
-  };
-
-  __device__ static void load_k(const uint16_t* src, const uint16_t* src2, int64_t ld,
-                                const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
-                                int rows_valid, int k0, int K, uint4* dst, uint4* dst2,
-                                bool two, int nchunks, int cpr, int total) {
-    for (int i = 0; i < nchunks; ++i) {
-      const int c = threadIdx.x + kThreads * i;
-      const int row = c / cpr, kc = c % cpr;
-      const int k = k0 + kc * 8;
-      uint4 v = make_uint4(0, 0, 0, 0), v2 = v;
-      int64_t srow = r0 + row;
-      bool ok = c < total && row < rows_valid && k < K;
+  // K-form setup: rows [0, R) of the tile (source rows r0 + row, or
+  // map[r0 + row]), rows_valid of them real, k measured from column c0.
+  template <int R, int PW>
+  __device__ static void setup_k(Src<PW>& s, const uint16_t* base, int64_t ld,
+                                 const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
+                                 int rows_valid) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // Without a map, rebase to the tile's first row so offsets stay small.
+    const uint16_t* b = map ? base + c0 : base + r0 * ld + c0;
+    s.rsrc = make_rsrc(b);
+    s.map = nullptr;
+    s.ld2 = (uint32_t)(ld * 2);
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int row = (wave * PW + i) * 16 + (lane >> 2);
+      const int c = (lane & 3) ^ kswz(row);
+      bool ok = row < rows_valid;
+      int64_t srow = row;
       if (ok && map) {
-        srow = map[srow];
+        srow = map[r0 + row];
         ok = srow >= 0 && srow < map_rows;
       }
-      if (ok) {
-        const int64_t off = srow * ld + c0 + k;
-        v = *reinterpret_cast<const uint4*>(src + off);
-        if (two) v2 = *reinterpret_cast<const uint4*>(src2 + off);
+      s.ok[i] = ok;
+      s.idx[i] = c * 8;
+      s.off[i] = ok ? (uint32_t)((srow * ld + c * 8) * 2) : kOob;
+    }
+  }
+
+  // K-form issue: stage tile k0 .. k0 + BK (k0 relative to the setup's c0).
+  template <int R, int PW>
+  __device__ static void issue_k(const Src<PW>& s, int k0, int K, lds_char* stage) {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const bool v = s.ok[i] && k0 + s.idx[i] < K;
+      dma16(s.rsrc, v ? s.off[i] + (uint32_t)(k0 * 2) : kOob, stage + (wave * PW + i) * 1024);
+    }
+  }
+
+  // T-form setup: columns [0, R) of the tile starting at source column c0,
+  // cols_valid of them real; source rows r0 + k, or map[r0 + k].
+  template <int R, int PW>
+  __device__ static void setup_t(Src<PW>& s, const uint16_t* base, int64_t ld,
+                                 const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
+                                 int cols_valid) {
+    constexpr int LPR = Dma<R>::LPR, RPI = Dma<R>::RPI;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint16_t* b = map ? base + c0 : base + r0 * ld + c0;
+    s.rsrc = make_rsrc(b);
+    s.map = map;
+    s.map_rows = map_rows;
+    s.r0 = r0;
+    s.ld2 = (uint32_t)(ld * 2);
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int krow = (wave * PW + i) * RPI + lane / LPR;
+      const int c = (lane % LPR) ^ tswz(krow);
+      s.idx[i] = krow;
+      s.ok[i] = c * 8 < cols_valid;
+      s.off[i] = (uint32_t)(c * 16 + (map ? 0 : (int64_t)krow * ld * 2));
+    }
+  }
+
+  template <int R, int PW>
+  __device__ static void issue_t(const Src<PW>& s, int k0, int K, lds_char* stage) {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int k = k0 + s.idx[i];
+      bool v = s.ok[i] && k < K;
+      uint32_t off;
+      if (s.map) {
+        int64_t row = v ? (int64_t)s.map[s.r0 + k] : -1;
+        v = v && row >= 0 && row < s.map_rows;
+        off = v ? s.off[i] + (uint32_t)row * s.ld2 : kOob;
+      } else {
+        off = v ? s.off[i] + (uint32_t)k0 * s.ld2 : kOob;
       }
-      dst[i] = v;
-      if (two) dst2[i] = v2;
+      dma16(s.rsrc, off, stage + (wave * PW + i) * 1024);
     }
   }
 
-  __device__ static void load_t(const uint16_t* src, const uint16_t* src2, int64_t ld,
-                                const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
-                                int cols_valid, int k0, int K, uint4* dst, uint4* dst2,
-                                bool two, int nblocks, int kb_count, int total) {
-    for (int i = 0; i < nblocks; ++i) {
-      const int blk = threadIdx.x + kThreads * i;
-      const int kb = blk % kb_count, mb = blk / kb_count;
-      const bool col_ok = blk < total && mb * 8 < cols_valid;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int k = k0 + kb * 4 + kk;
-        uint4 v = make_uint4(0, 0, 0, 0), v2 = v;
-        if (col_ok && k < K) {
-          int64_t row = r0 + k;
-          bool ok = true;
-          if (map) {
-            row = map[row];
-            ok = row >= 0 && row < map_rows;
-          }
-          if (ok) {
-            const int64_t off = row * ld + c0 + mb * 8;
-            v = *reinterpret_cast<const uint4*>(src + off);
-            if (two) v2 = *reinterpret_cast<const uint4*>(src2 + off);
-          }
-        }
-        dst[i * 4 + kk] = v;
-        if (two) dst2[i * 4 + kk] = v2;
-      }
-    }
+  // MFMA fragment of rows [row0, row0 + 32) x k-step ks (16 deep).
+  __device__ static bf16x8_t frag_k(const lds_char* stage, int row0, int ks) {
+    const int lane = threadIdx.x & 63;
+    const int row = row0 + (lane & 31);
+    const int c = 2 * ks + (lane >> 5);
+    return *reinterpret_cast<const lds_bf16x8*>(stage + row * 64 + ((c ^ kswz(row)) << 4));
   }
 
-  __device__ static void store_k(uint16_t* lds, const uint4* v, int nchunks, int cpr,
-                                 int total) {
-    for (int i = 0; i < nchunks; ++i) {
-      const int c = threadIdx.x + kThreads * i;
-      if (c >= total) break;
-      const int row = c / cpr, kc = c % cpr;
-      *reinterpret_cast<uint4*>(lds + row * LDK + kc * 8) = v[i];
-    }
-  }
-
-  __device__ static void store_t(uint16_t* lds, const uint4* v, int nblocks, int kb_count,
-                                 int total) {
-    for (int i = 0; i < nblocks; ++i) {
-      const int blk = threadIdx.x + kThreads * i;
-      if (blk >= total) break;
-      const int kb = blk % kb_count, mb = blk / kb_count;
-      uint2 o[8];
-      transpose4x8(v + i * 4, o);
-#pragma unroll
-      for (int mm = 0; mm < 8; ++mm)
-        *reinterpret_cast<uint2*>(lds + (mb * 8 + mm) * LDK + kb * 4) = o[mm];
-    }
-  }
-
-  __device__ static void load_tiles(const Args& p, const Prob& q, int m0, int n0, int k0,
-                                    Regs& r) {
-    if (T::a_k)
-      load_k(p.a, p.a2, p.lda, p.a_map, p.a_rows, q.ar + m0, q.ac, q.M - m0, k0, q.K, r.a,
-             r.a2, T::a_grad,
-             KLoad<BM>::N, KLoad<BM>::CPR, KLoad<BM>::TOTAL);
-    else
-      load_t(p.a, p.a2, p.lda, p.a_map, p.a_rows, q.ar, q.ac + m0, q.M - m0, k0, q.K, r.a,
-             r.a2, T::a_grad, TLoad<BM>::N, TLoad<BM>::KB, TLoad<BM>::TOTAL);
-    if (T::b_k)
-      load_k(p.b, p.b2, p.ldb, nullptr, 0, q.br + n0, q.bc, q.N - n0, k0, q.K, r.b, r.b2,
-             T::b_grad,
-             KLoad<BN>::N, KLoad<BN>::CPR, KLoad<BN>::TOTAL);
-    else
-      load_t(p.b, p.b2, p.ldb, nullptr, 0, q.br, q.bc + n0, q.N - n0, k0, q.K, r.b, r.b2,
-             T::b_grad, TLoad<BN>::N, TLoad<BN>::KB, TLoad<BN>::TOTAL);
-  }
-
-  __device__ static void store_tiles(const Args& p, uint16_t* As, uint16_t* Bs, Regs& r) {
-    if (T::a_grad) {
-#pragma unroll
-      for (int i = 0; i < NA; ++i) r.a[i] = relu2_grad(r.a[i], r.a2[i], p.act);
-    }
-    if (T::b_grad) {
-#pragma unroll
-      for (int i = 0; i < NB; ++i) r.b[i] = relu2_grad(r.b[i], r.b2[i], p.act);
-    }
-    if (T::a_k)
-      store_k(As, r.a, KLoad<BM>::N, KLoad<BM>::CPR, KLoad<BM>::TOTAL);
-    else
-      store_t(As, r.a, TLoad<BM>::N, TLoad<BM>::KB, TLoad<BM>::TOTAL);
-    if (T::b_k)
-      store_k(Bs, r.b, KLoad<BN>::N, KLoad<BN>::CPR, KLoad<BN>::TOTAL);
-    else
-      store_t(Bs, r.b, TLoad<BN>::N, TLoad<BN>::KB, TLoad<BN>::TOTAL);
+  template <int R>
+  __device__ static bf16x8_t frag_t(const lds_char* stage, int col0, int ks) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, L = lane & 15;
+    const int m = col0 + 16 * (g & 1) + 4 * (L & 3);
+    const int kr = 16 * ks + 8 * (g >> 1) + (L >> 2);
+    const int cpos = (((m >> 3) ^ tswz(kr)) << 4) + ((m & 7) << 1);
+    const bf16x4_t lo =
+        __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(stage + kr * (2 * R) + cpos));
+    const bf16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (lds_bf16x4*)(stage + (kr + 4) * (2 * R) + cpos));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   }
 
   // Work items of expert e: its output tiles times its K chunks (chunks > 1
@@ -408,13 +413,14 @@ struct Gemm {
   // ranges of size a_e (a block scan over experts), the offset inside that
   // range, and the exclusive prefix of a second per-expert count b_e.
   // MODE 0: a = items, b = split items (GEMM); MODE 1: a = tiles, b = split
-  // items (reduce). Returns false when id is past the end.
+  // items (reduce). `scratch` holds 16 longs of LDS. Returns false when id is
+  // past the end.
   template <int MODE>
-  __device__ static bool locate(const Args& p, int id, int& e_out, int& local_out,
-                                int& bpre_out, int& chunks_out) {
-    __shared__ long long scan[kThreads / kWave + 1];
-    __shared__ int32_t s_e, s_local, s_bpre, s_chunks;
-    if (threadIdx.x == 0) s_e = -1;
+  __device__ static bool locate(const Args& p, int id, long long* scratch, int& e_out,
+                                int& local_out, int& bpre_out, int& chunks_out) {
+    long long* scan = scratch;                               // kThreads / 64 + 1 entries
+    int32_t* sh = reinterpret_cast<int32_t*>(scratch + 8);  // e, local, bpre, chunks
+    if (threadIdx.x == 0) sh[0] = -1;
     long long base = 0;
     for (int e0 = 0; e0 < p.E; e0 += kThreads) {
       const int e = e0 + threadIdx.x;
@@ -429,34 +435,68 @@ struct Gemm {
       const long long pre = base + ex;
       const int a_pre = (int)(pre >> 32), b_pre = (int)(pre & 0xFFFFFFFFll);
       if (a > 0 && id >= a_pre && id < a_pre + a) {
-        s_e = e;
-        s_local = id - a_pre;
-        s_bpre = b_pre;
-        s_chunks = chunks;
+        sh[0] = e;
+        sh[1] = id - a_pre;
+        sh[2] = b_pre;
+        sh[3] = chunks;
       }
       base += total;
       __syncthreads();
-      if (s_e >= 0 || (int)(base >> 32) > id) break;
+      if (sh[0] >= 0 || (int)(base >> 32) > id) break;
     }
-    e_out = s_e;
-    local_out = s_local;
-    bpre_out = s_bpre;
-    chunks_out = s_chunks;
-    return s_e >= 0;
+    // The values are block-uniform; readfirstlane tells the compiler so, and
+    // everything derived from them (operand bases, buffer resources) stays in
+    // scalar registers.
+    e_out = __builtin_amdgcn_readfirstlane(sh[0]);
+    local_out = __builtin_amdgcn_readfirstlane(sh[1]);
+    bpre_out = __builtin_amdgcn_readfirstlane(sh[2]);
+    chunks_out = __builtin_amdgcn_readfirstlane(sh[3]);
+    __syncthreads();  // the scratch LDS is reused by the caller
+    return e_out >= 0;
   }
 
-  __device__ static void run(const Args& p) {
-    extern __shared__ __align__(16) uint16_t smem[];
-    uint16_t* As = smem;                  // [2][BM][LDK]
-    uint16_t* Bs = smem + 2 * A_ELEMS;    // [2][BN][LDK]
+  // One k-tile: wait for its DMA, release the other buffer to the next
+  // tile's DMA, then multiply. cur/nxt are distinct LDS objects, so the
+  // compiler can tell the DMA into nxt from the reads of cur and does not
+  // wait on it.
+  template <class Issue>
+  __device__ static void step(int kt, int nk, lds_char* cur, lds_char* nxt, Issue& issue,
+                              f32x16_t (&acc)[FM][FN]) {
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (kt + 1 < nk) issue(kt + 1, nxt);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8_t af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = T::a_k ? frag_k(cur, wm * WM + i * 32, ks) : frag_t<BM>(cur, wm * WM + i * 32, ks);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = T::b_k ? frag_k(cur + A_STAGE, wn * WN + j * 32, ks)
+                        : frag_t<BN>(cur + A_STAGE, wn * WN + j * 32, ks);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          // Operands swapped: the accumulator holds C^T, so each lane owns
+          // 4 consecutive n of one m and stores 8 bytes at a time.
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+    }
+  }
 
+  __device__ static void run(const Args& p, lds_char* st0, lds_char* st1) {
     // XCD-aware remap: hardware deals workgroup ids round-robin over the 8
     // XCDs; give each XCD a contiguous range of tiles (gridDim.x % 8 == 0).
     const int g = gridDim.x, b = blockIdx.x;
     const int bid = (b % 8) * (g / 8) + b / 8;
 
     int e, local, split_pre, chunks;
-    if (!locate<0>(p, bid, e, local, split_pre, chunks)) return;
+    if (!locate<0>(p, bid, reinterpret_cast<long long*>((char*)st1), e, local, split_pre,
+                   chunks))
+      return;
     int mt_dim, nt_dim;
     T::tile_dims(p, e, mt_dim, nt_dim);
     const int n_tiles = cdiv(nt_dim, BN);
@@ -464,15 +504,34 @@ struct Gemm {
     const int m0 = (tile / n_tiles) * BM;
     const int n0 = (tile % n_tiles) * BN;
     Prob q = T::prob(p, e);
-    // K range of this work item: [kbeg, q.K) after clamping q.K to the chunk.
     int kbeg = 0;
     if (chunks > 1) {
       kbeg = chunk * p.kc;
       q.K = min(q.K, kbeg + p.kc);
     }
+    const int nk = q.K > kbeg ? cdiv(q.K - kbeg, BK) : 0;
+    const int klen = q.K - kbeg;  // k below is relative to kbeg
 
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    Src<PWA> sa;
+    Src<PWB> sb;
+    if (T::a_k)
+      setup_k<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + m0, q.ac + kbeg, q.M - m0);
+    else
+      setup_t<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + kbeg, q.ac + m0, q.M - m0);
+    if (T::b_k)
+      setup_k<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + n0, q.bc + kbeg, q.N - n0);
+    else
+      setup_t<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + kbeg, q.bc + n0, q.N - n0);
+
+    auto issue = [&](int kt, lds_char* st) {
+      const int k0 = kt * BK;
+      if (T::a_k) issue_k<BM>(sa, k0, klen, st); else issue_t<BM>(sa, k0, klen, st);
+      if (T::b_k) issue_k<BN>(sb, k0, klen, st + A_STAGE);
+      else issue_t<BN>(sb, k0, klen, st + A_STAGE);
+    };
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
 
     f32x16_t acc[FM][FN];
@@ -483,44 +542,15 @@ struct Gemm {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int nk = q.K > kbeg ? cdiv(q.K - kbeg, BK) : 0;
-    Regs regs;
-    if (nk > 0) {
-      load_tiles(p, q, m0, n0, kbeg, regs);
-      store_tiles(p, As, Bs, regs);
+    if (nk > 0) issue(0, st0);
+    // Pairs of k-tiles (stage 0 then stage 1), both steps unconditional so the
+    // accumulators stay in place across the loop; an odd last tile follows.
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      step(kt, nk, st0, st1, issue, acc);
+      step(kt + 1, nk, st1, st0, issue, acc);
     }
-    __syncthreads();
-
-    const int frag_row = lane & 31;
-    const int frag_k = (lane >> 5) * 8;
-    for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < nk) load_tiles(p, q, m0, n0, kbeg + (kt + 1) * BK, regs);
-      const uint16_t* Ac = As + cur * A_ELEMS;
-      const uint16_t* Bc = Bs + cur * B_ELEMS;
-#pragma unroll
-      for (int ks = 0; ks < BK / 16; ++ks) {
-        bf16x8_t af[FM], bfr[FN];
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-          af[i] = *reinterpret_cast<const bf16x8_t*>(
-              Ac + (wm * WM + i * 32 + frag_row) * LDK + ks * 16 + frag_k);
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          bfr[j] = *reinterpret_cast<const bf16x8_t*>(
-              Bc + (wn * WN + j * 32 + frag_row) * LDK + ks * 16 + frag_k);
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-            // Operands swapped: the accumulator holds C^T, so each lane owns
-            // 4 consecutive n of one m and stores 8 bytes at a time.
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
-      }
-      if (kt + 1 < nk)
-        store_tiles(p, As + (cur ^ 1) * A_ELEMS, Bs + (cur ^ 1) * B_ELEMS, regs);
-      __syncthreads();
-    }
+    if (kt < nk) step(kt, nk, st0, st1, issue, acc);
 
     // Epilogue. acc[i][j][4*g + r] sits at m = wm*WM + i*32 + (lane & 31),
     // n = wn*WN + j*32 + 8*g + 4*(lane >> 5) + r.
@@ -547,8 +577,7 @@ struct Gemm {
     for (int i = 0; i < FM; ++i) {
       const int m = m0 + wm * WM + i * 32 + (lane & 31);
       if (m >= q.M) continue;
-      uint16_t* crow = p.c + (q.cr + m) * p.ldc + q.cc;
-      uint16_t* crow2 = p.c2 ? p.c2 + (q.cr + m) * p.ldc + q.cc : nullptr;
+      const int64_t roff = (q.cr + m) * p.ldc + q.cc;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -560,33 +589,48 @@ struct Gemm {
           if (V == UP_FWD && p.act == VMOE_ACT_RELU_SQUARED) {
             v0 = fmaxf(v0, 0.0f); v1 = fmaxf(v1, 0.0f);
             v2 = fmaxf(v2, 0.0f); v3 = fmaxf(v3, 0.0f);
-            if (crow2)
-              *reinterpret_cast<uint2*>(crow2 + n) =
+            if (p.c2)
+              *reinterpret_cast<uint2*>(p.c2 + roff + n) =
                   make_uint2(pack_bf16(v0, v1), pack_bf16(v2, v3));
             v0 *= v0; v1 *= v1; v2 *= v2; v3 *= v3;
           }
-          *reinterpret_cast<uint2*>(crow + n) = make_uint2(pack_bf16(v0, v1), pack_bf16(v2, v3));
+          if (V == DOWN_DH && p.pre) {
+            // GA = bf16(pre > 0 ? 2 * GH * pre : 0), GH the bf16-rounded dH.
+            const uint2 pr = *reinterpret_cast<const uint2*>(p.pre + roff + n);
+            const float p0 = lo_f32(pr.x), p1 = hi_f32(pr.x), p2 = lo_f32(pr.y), p3 = hi_f32(pr.y);
+            v0 = p0 > 0.0f ? bf16_to_f32(f32_to_bf16(v0)) * 2.0f * p0 : 0.0f;
+            v1 = p1 > 0.0f ? bf16_to_f32(f32_to_bf16(v1)) * 2.0f * p1 : 0.0f;
+            v2 = p2 > 0.0f ? bf16_to_f32(f32_to_bf16(v2)) * 2.0f * p2 : 0.0f;
+            v3 = p3 > 0.0f ? bf16_to_f32(f32_to_bf16(v3)) * 2.0f * p3 : 0.0f;
+          }
+          *reinterpret_cast<uint2*>(p.c + roff + n) = make_uint2(pack_bf16(v0, v1), pack_bf16(v2, v3));
         }
       }
     }
   }
 };
 
-template <int V, int BM, int BN, int BK>
+template <int V>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
-  Gemm<V, BM, BN, BK>::run(p);
+  using G = Gemm<V, Cfg<V>::BM, Cfg<V>::BN, Cfg<V>::STAGES>;
+  // Two stage buffers as distinct LDS objects (see Gemm::step).
+  __shared__ __align__(16) char stage0[G::STAGE];
+  __shared__ __align__(16) char stage1[G::STAGE];
+  G::run(p, (lds_char*)stage0, (lds_char*)stage1);
 }
 
 // Sums the K-chunk partials of every split (expert, tile) in chunk order and
 // stores the bf16 result. One workgroup per output tile; tiles of experts that
 // were not split exit at once (their GEMM item stored bf16 directly).
-template <int V, int BM, int BN, int BK>
+template <int V>
 __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(Args p) {
-  using G = Gemm<V, BM, BN, BK>;
+  constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN;
+  using G = Gemm<V, BM, BN, Cfg<V>::STAGES>;
+  __shared__ long long scratch[16];
   const int g = gridDim.x, b = blockIdx.x;
   const int id = (b % 8) * (g / 8) + b / 8;
   int e, tile, split_pre, chunks;
-  if (!G::template locate<1>(p, id, e, tile, split_pre, chunks)) return;
+  if (!G::template locate<1>(p, id, scratch, e, tile, split_pre, chunks)) return;
   if (chunks <= 1) return;
   int mt_dim, nt_dim;
   Traits<V>::tile_dims(p, e, mt_dim, nt_dim);
@@ -608,8 +652,33 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(Args p) {
   }
 }
 
-// Tile configuration (one for all variants for now).
-constexpr int kBM = 128, kBN = 128, kBK = 32;
+// GA = bf16(pre > 0 ? 2 * grad_h * pre : 0) elementwise over [rows, cols]
+// (the relu^2 derivative, grouped_gemm.py:751-766), for callers that hold
+// grad_h and pre_act separately.
+__global__ __launch_bounds__(256) void relu2_grad_kernel(const uint16_t* __restrict__ gh,
+                                                          const uint16_t* __restrict__ pre,
+                                                          int64_t ld, uint16_t* __restrict__ ga,
+                                                          int64_t ldo, int64_t rows,
+                                                          int64_t cols) {
+  const int64_t vpr = cols / 8;
+  const int64_t total = rows * vpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / vpr, c = (i % vpr) * 8;
+    const uint4 g = *reinterpret_cast<const uint4*>(gh + r * ld + c);
+    const uint4 pv = *reinterpret_cast<const uint4*>(pre + r * ld + c);
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, pw[4] = {pv.x, pv.y, pv.z, pv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float pl = lo_f32(pw[j]), ph = hi_f32(pw[j]);
+      const float vl = pl > 0.0f ? lo_f32(gw[j]) * 2.0f * pl : 0.0f;
+      const float vh = ph > 0.0f ? hi_f32(gw[j]) * 2.0f * ph : 0.0f;
+      o[j] = pack_bf16(vl, vh);
+    }
+    *reinterpret_cast<uint4*>(ga + r * ldo + c) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
 
 inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -650,49 +719,50 @@ SplitPlan split_plan(int64_t tiles_max, int64_t rows_bound) {
 }
 
 template <int V>
-int launch(const Args& p, int64_t grid_tiles, hipStream_t s) {
-  using G = Gemm<V, kBM, kBN, kBK>;
-  auto kern = grouped_gemm_kernel<V, kBM, kBN, kBK>;
-  if (G::LDS_BYTES > 65536) {
-    static std::once_flag once;
-    static hipError_t attr_err = hipSuccess;
-    std::call_once(once, [&] {
-      attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)G::LDS_BYTES);
-    });
-    if (attr_err != hipSuccess) return VMOE_ERR_LAUNCH;
-  }
-  if (grid_tiles <= 0) return VMOE_OK;
-  int64_t g = (grid_tiles + 7) / 8 * 8;
+int launch(const Args& p, int64_t grid_items, hipStream_t s) {
+  if (grid_items <= 0) return VMOE_OK;
+  int64_t g = (grid_items + 7) / 8 * 8;
   if (g > INT32_MAX) return VMOE_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(kern, dim3((unsigned)g), dim3(kThreads), G::LDS_BYTES, s, p);
+  hipLaunchKernelGGL(grouped_gemm_kernel<V>, dim3((unsigned)g), dim3(kThreads), 0, s, p);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }
 
+template <int V>
+int64_t tiles_max(int64_t mmax, int64_t nmax) {
+  return ((mmax + Cfg<V>::BM - 1) / Cfg<V>::BM) * ((nmax + Cfg<V>::BN - 1) / Cfg<V>::BN);
+}
+
+// Upper bound of the work items of a row-tiled GEMM: sum_e ceil(tpe_e / BM)
+// <= rows_bound / BM + E row tiles, each with at most ceil(nmax / BN) tiles.
+template <int V>
+int64_t row_items(int64_t rows_bound, int E, int64_t nmax) {
+  return ((rows_bound + Cfg<V>::BM - 1) / Cfg<V>::BM + E) *
+         ((nmax + Cfg<V>::BN - 1) / Cfg<V>::BN);
+}
+
 // dW GEMM with split-K: GEMM items, then the chunk reduction.
 template <int V>
-int launch_dw(Args p, int64_t tiles_max, void* ws, size_t ws_bytes, hipStream_t s) {
+int launch_dw(Args p, int64_t tmax, void* ws, size_t ws_bytes, hipStream_t s) {
+  constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN;
   const int64_t E = p.E;
   if (ws) {
-    const SplitPlan sp = split_plan(tiles_max, p.rows_bound);
-    if (ws_bytes < (size_t)sp.slots * kBM * kBN * sizeof(float)) return VMOE_ERR_WORKSPACE;
+    const SplitPlan sp = split_plan(tmax, p.rows_bound);
+    if (ws_bytes < (size_t)sp.slots * BM * BN * sizeof(float)) return VMOE_ERR_WORKSPACE;
     p.kc = sp.kc;
     p.partial = reinterpret_cast<float*>(ws);
-    const int64_t items = tiles_max * (E + p.rows_bound / sp.kc + 1);
+    const int64_t items = tmax * (E + p.rows_bound / sp.kc + 1);
     int st = launch<V>(p, items, s);
     if (st) return st;
-    int64_t g = (E * tiles_max + 7) / 8 * 8;
+    int64_t g = (E * tmax + 7) / 8 * 8;
     if (g > INT32_MAX) return VMOE_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((splitk_reduce_kernel<V, kBM, kBN, kBK>), dim3((unsigned)g),
-                       dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((splitk_reduce_kernel<V>), dim3((unsigned)g), dim3(kThreads), 0, s, p);
     VMOE_CHECK_LAUNCH();
     return VMOE_OK;
   }
   p.kc = 0;
   p.partial = nullptr;
-  return launch<V>(p, E * tiles_max, s);
+  return launch<V>(p, E * tmax, s);
 }
 
 // Shared argument checks. Every dimension the kernels vectorise over must be a
@@ -711,9 +781,10 @@ inline int check_common(const int32_t* eto, const int32_t* ewo, const int32_t* w
 
 inline bool ld_ok(int64_t ld) { return ld > 0 && ld % 8 == 0; }
 
-inline int64_t rows_tiles(int64_t rows_bound, int E, int BM) {
-  return (rows_bound + BM - 1) / BM + E;
-}
+// DMA offsets are 31-bit byte offsets from an operand base (rebased to the
+// tile where rows are not gathered): every source the kernels address by a
+// row index must span less than 2 GiB.
+inline bool span_ok(int64_t rows, int64_t ld) { return rows * ld * 2 < ((int64_t)1 << 31); }
 
 }  // namespace
 }  // namespace vmoe
@@ -735,14 +806,16 @@ extern "C" int vmoe_gemm_up_fwd(const uint16_t* x, int64_t ldx, int64_t x_rows,
     return VMOE_ERR_UNSUPPORTED;
   if (!a16(x) || !a16(w1) || !a16(out) || (pre_act && !a16(pre_act)))
     return VMOE_ERR_UNSUPPORTED;
+  if ((gather_map && !span_ok(x_rows, ldx)) || !span_ok(hidden, ldw1))
+    return VMOE_ERR_UNSUPPORTED;
   Args p{};
   p.a = x; p.lda = ldx; p.a_map = gather_map; p.a_rows = gather_map ? x_rows : 0;
   p.b = w1; p.ldb = ldw1;
   p.c = out; p.c2 = activation == VMOE_ACT_RELU_SQUARED ? pre_act : nullptr; p.ldc = ldo;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = activation; p.rows_bound = rows_bound;
-  const int64_t tiles = rows_tiles(rows_bound, E, kBM) * ((max_width + kBN - 1) / kBN);
-  return launch<UP_FWD>(p, tiles, reinterpret_cast<hipStream_t>(stream));
+  return launch<UP_FWD>(p, row_items<UP_FWD>(rows_bound, E, max_width),
+                        reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int vmoe_gemm_down_fwd(const uint16_t* h, int64_t ldh, const uint16_t* w2,
@@ -756,82 +829,91 @@ extern "C" int vmoe_gemm_down_fwd(const uint16_t* h, int64_t ldh, const uint16_t
   if (!ld_ok(ldh) || !ld_ok(ldw2) || !ld_ok(ldy) || ldw2 < hidden || ldy < hidden)
     return VMOE_ERR_UNSUPPORTED;
   if (!a16(h) || !a16(w2) || !a16(y)) return VMOE_ERR_UNSUPPORTED;
+  if (!span_ok(max_width, ldw2)) return VMOE_ERR_UNSUPPORTED;
   Args p{};
   p.a = h; p.lda = ldh;
   p.b = w2; p.ldb = ldw2;
   p.c = y; p.ldc = ldy;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
-  const int64_t tiles = rows_tiles(rows_bound, E, kBM) * ((hidden + kBN - 1) / kBN);
-  return launch<DOWN_FWD>(p, tiles, reinterpret_cast<hipStream_t>(stream));
+  return launch<DOWN_FWD>(p, row_items<DOWN_FWD>(rows_bound, E, hidden),
+                          reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int vmoe_gemm_up_bwd_dx(const uint16_t* grad_h, const uint16_t* pre_act, int64_t ldg,
-                                   int32_t activation, const uint16_t* w1, int64_t ldw1,
-                                   uint16_t* grad_x, int64_t ldgx, const int32_t* eto,
-                                   const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
-                                   int32_t E, int64_t hidden, int64_t max_width,
-                                   int64_t rows_bound, vmoe_stream_t stream) {
+extern "C" int vmoe_relu2_grad(const uint16_t* grad_h, const uint16_t* pre_act, int64_t ld,
+                               uint16_t* grad_act, int64_t ldo, int64_t rows, int64_t cols,
+                               vmoe_stream_t stream) {
+  if (rows < 0 || cols < 0 || ld < cols || ldo < cols) return VMOE_ERR_INVALID_ARG;
+  if (rows == 0 || cols == 0) return VMOE_OK;
+  if (!grad_h || !pre_act || !grad_act) return VMOE_ERR_INVALID_ARG;
+  if (cols % 8 || ld % 8 || ldo % 8 || !a16(grad_h) || !a16(pre_act) || !a16(grad_act))
+    return VMOE_ERR_UNSUPPORTED;
+  const int64_t n = rows * (cols / 8);
+  const int64_t grid = std::min<int64_t>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(relu2_grad_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), grad_h, pre_act, ld, grad_act, ldo,
+                     rows, cols);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_gemm_up_bwd_dx(const uint16_t* grad_act, int64_t ldg, const uint16_t* w1,
+                                   int64_t ldw1, uint16_t* grad_x, int64_t ldgx,
+                                   const int32_t* eto, const int32_t* ewo, const int32_t* widths,
+                                   const int32_t* tpe, int32_t E, int64_t hidden,
+                                   int64_t max_width, int64_t rows_bound, vmoe_stream_t stream) {
   int st = check_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
   if (st) return st;
-  if (activation != VMOE_ACT_NONE && activation != VMOE_ACT_RELU_SQUARED)
-    return VMOE_ERR_INVALID_ARG;
-  if (!grad_h || !w1 || !grad_x || (activation == VMOE_ACT_RELU_SQUARED && !pre_act))
-    return VMOE_ERR_INVALID_ARG;
+  if (!grad_act || !w1 || !grad_x) return VMOE_ERR_INVALID_ARG;
   if (!ld_ok(ldg) || !ld_ok(ldw1) || !ld_ok(ldgx) || ldgx < hidden) return VMOE_ERR_UNSUPPORTED;
-  if (!a16(grad_h) || !a16(w1) || !a16(grad_x) || (pre_act && !a16(pre_act)))
-    return VMOE_ERR_UNSUPPORTED;
+  if (!a16(grad_act) || !a16(w1) || !a16(grad_x)) return VMOE_ERR_UNSUPPORTED;
   Args p{};
-  p.a = grad_h; p.a2 = pre_act ? pre_act : grad_h; p.lda = ldg;
+  p.a = grad_act; p.lda = ldg;
   p.b = w1; p.ldb = ldw1;
   p.c = grad_x; p.ldc = ldgx;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
-  p.E = E; p.hidden = (int)hidden; p.act = activation; p.rows_bound = rows_bound;
-  const int64_t tiles = rows_tiles(rows_bound, E, kBM) * ((hidden + kBN - 1) / kBN);
-  return launch<UP_DX>(p, tiles, reinterpret_cast<hipStream_t>(stream));
+  p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
+  return launch<UP_DX>(p, row_items<UP_DX>(rows_bound, E, hidden),
+                       reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t vmoe_gemm_dw_workspace_bytes(int32_t E, int64_t hidden, int64_t max_width,
                                                int64_t rows_bound) {
   if (E <= 0 || hidden <= 0 || max_width <= 0 || rows_bound <= 0) return 0;
-  const int64_t up_tiles = ((hidden + kBM - 1) / kBM) * ((max_width + kBN - 1) / kBN);
-  const int64_t down_tiles = ((max_width + kBM - 1) / kBM) * ((hidden + kBN - 1) / kBN);
-  const SplitPlan a = split_plan(up_tiles, rows_bound), b = split_plan(down_tiles, rows_bound);
-  return (size_t)std::max(a.slots, b.slots) * kBM * kBN * sizeof(float);
+  const SplitPlan a = split_plan(tiles_max<UP_DW>(hidden, max_width), rows_bound);
+  const SplitPlan b = split_plan(tiles_max<DOWN_DW>(max_width, hidden), rows_bound);
+  const size_t tile_a = (size_t)Cfg<UP_DW>::BM * Cfg<UP_DW>::BN * sizeof(float);
+  const size_t tile_b = (size_t)Cfg<DOWN_DW>::BM * Cfg<DOWN_DW>::BN * sizeof(float);
+  return std::max((size_t)a.slots * tile_a, (size_t)b.slots * tile_b);
 }
 
 extern "C" int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
-                                   const int32_t* gather_map, const uint16_t* grad_h,
-                                   const uint16_t* pre_act, int64_t ldg, int32_t activation,
-                                   uint16_t* grad_w1, int64_t ldgw, const int32_t* eto,
-                                   const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
-                                   int32_t E, int64_t hidden, int64_t max_width,
-                                   int64_t rows_bound, void* workspace, size_t workspace_bytes,
-                                   vmoe_stream_t stream) {
+                                   const int32_t* gather_map, const uint16_t* grad_act,
+                                   int64_t ldg, uint16_t* grad_w1, int64_t ldgw,
+                                   const int32_t* eto, const int32_t* ewo, const int32_t* widths,
+                                   const int32_t* tpe, int32_t E, int64_t hidden,
+                                   int64_t max_width, int64_t rows_bound, void* workspace,
+                                   size_t workspace_bytes, vmoe_stream_t stream) {
   int st = check_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
   if (st) return st;
-  if (activation != VMOE_ACT_NONE && activation != VMOE_ACT_RELU_SQUARED)
-    return VMOE_ERR_INVALID_ARG;
-  if (!x || !grad_h || !grad_w1 || x_rows < 0 ||
-      (activation == VMOE_ACT_RELU_SQUARED && !pre_act))
-    return VMOE_ERR_INVALID_ARG;
+  if (!x || !grad_act || !grad_w1 || x_rows < 0) return VMOE_ERR_INVALID_ARG;
   if (!ld_ok(ldx) || !ld_ok(ldg) || !ld_ok(ldgw) || ldx < hidden) return VMOE_ERR_UNSUPPORTED;
-  if (!a16(x) || !a16(grad_h) || !a16(grad_w1) || (pre_act && !a16(pre_act)))
+  if (!a16(x) || !a16(grad_act) || !a16(grad_w1)) return VMOE_ERR_UNSUPPORTED;
+  if (!span_ok(gather_map ? x_rows : rows_bound, ldx) || !span_ok(rows_bound, ldg))
     return VMOE_ERR_UNSUPPORTED;
   Args p{};
   p.a = x; p.lda = ldx; p.a_map = gather_map; p.a_rows = gather_map ? x_rows : 0;
-  p.b = grad_h; p.b2 = pre_act ? pre_act : grad_h; p.ldb = ldg;
+  p.b = grad_act; p.ldb = ldg;
   p.c = grad_w1; p.ldc = ldgw;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
-  p.E = E; p.hidden = (int)hidden; p.act = activation; p.rows_bound = rows_bound;
-  const int64_t tiles_max = ((hidden + kBM - 1) / kBM) * ((max_width + kBN - 1) / kBN);
-  return launch_dw<UP_DW>(p, tiles_max, workspace, workspace_bytes,
+  p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
+  return launch_dw<UP_DW>(p, tiles_max<UP_DW>(hidden, max_width), workspace, workspace_bytes,
                           reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, const uint16_t* w2,
-                                     int64_t ldw2, uint16_t* grad_h, int64_t ldgh,
-                                     const int32_t* eto, const int32_t* ewo,
+                                     int64_t ldw2, const uint16_t* pre_act, uint16_t* grad_h,
+                                     int64_t ldgh, const int32_t* eto, const int32_t* ewo,
                                      const int32_t* widths, const int32_t* tpe, int32_t E,
                                      int64_t hidden, int64_t max_width, int64_t rows_bound,
                                      vmoe_stream_t stream) {
@@ -841,15 +923,17 @@ extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, const
   if (!ld_ok(ldgy) || !ld_ok(ldw2) || !ld_ok(ldgh) || ldgy < hidden || ldw2 < hidden ||
       ldgh < max_width)
     return VMOE_ERR_UNSUPPORTED;
-  if (!a16(grad_y) || !a16(w2) || !a16(grad_h)) return VMOE_ERR_UNSUPPORTED;
+  if (!a16(grad_y) || !a16(w2) || !a16(grad_h) || (pre_act && !a16(pre_act)))
+    return VMOE_ERR_UNSUPPORTED;
   Args p{};
   p.a = grad_y; p.lda = ldgy;
   p.b = w2; p.ldb = ldw2;
   p.c = grad_h; p.ldc = ldgh;
+  p.pre = pre_act;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
-  const int64_t tiles = rows_tiles(rows_bound, E, kBM) * ((max_width + kBN - 1) / kBN);
-  return launch<DOWN_DH>(p, tiles, reinterpret_cast<hipStream_t>(stream));
+  return launch<DOWN_DH>(p, row_items<DOWN_DH>(rows_bound, E, max_width),
+                         reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint16_t* grad_y,
@@ -865,13 +949,13 @@ extern "C" int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint1
   if (!ld_ok(ldh) || !ld_ok(ldgy) || !ld_ok(ldgw) || ldgy < hidden || ldgw < hidden)
     return VMOE_ERR_UNSUPPORTED;
   if (!a16(h) || !a16(grad_y) || !a16(grad_w2)) return VMOE_ERR_UNSUPPORTED;
+  if (!span_ok(rows_bound, ldh) || !span_ok(rows_bound, ldgy)) return VMOE_ERR_UNSUPPORTED;
   Args p{};
   p.a = h; p.lda = ldh;
   p.b = grad_y; p.ldb = ldgy;
   p.c = grad_w2; p.ldc = ldgw;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
-  const int64_t tiles_max = ((max_width + kBM - 1) / kBM) * ((hidden + kBN - 1) / kBN);
-  return launch_dw<DOWN_DW>(p, tiles_max, workspace, workspace_bytes,
-                            reinterpret_cast<hipStream_t>(stream));
+  return launch_dw<DOWN_DW>(p, tiles_max<DOWN_DW>(max_width, hidden), workspace,
+                            workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }

@@ -192,44 +192,62 @@ def _same_ld(a, b):
     return a.contiguous(), b.contiguous()
 
 
-def up_bwd(grad_h, x, w1, pre, m: GemmMeta, hidden: int, act: int,
-           gather_map: torch.Tensor | None):
-    """(grad_x in gathered rows, grad_w1)."""
-    grad_h = _bf16(grad_h, "grouped_gemm_up_backward grad_output")
+def relu2_grad(grad_h: torch.Tensor, pre: torch.Tensor) -> torch.Tensor:
+    """GA = bf16(pre > 0 ? 2 * grad_h * pre : 0), elementwise (vmoe_relu2_grad)."""
+    grad_h, pre = _same_ld(grad_h, pre)
+    ga = torch.empty(grad_h.shape, dtype=grad_h.dtype, device=grad_h.device)
+    _lib.call("vmoe_relu2_grad", grad_h.data_ptr(), pre.data_ptr(), grad_h.stride(0),
+              ga.data_ptr(), ga.stride(0), grad_h.shape[0], grad_h.shape[1],
+              _lib.stream(grad_h.device))
+    return ga
+
+
+def up_bwd_from_ga(ga, x, w1, m: GemmMeta, hidden: int, gather_map: torch.Tensor | None):
+    """(grad_x in gathered rows, grad_w1) from GA, the gradient w.r.t. the
+    up projection's pre-activation."""
+    ga = _bf16(ga, "grouped_gemm_up_backward grad_output")
     x = _bf16(x, "grouped_gemm_up_backward x")
     w1 = _bf16(w1, "grouped_gemm_up_backward w1")
-    if act == _lib.ACT_RELU_SQUARED:
-        pre = _bf16(pre, "grouped_gemm_up_backward pre_act")
-        grad_h, pre = _same_ld(grad_h, pre)
-    else:
-        pre = None
     _need(w1.shape[0] == hidden and x.shape[1] == hidden, "x / w1 do not match hidden_size")
-    _need(grad_h.shape[0] >= m.rows and grad_h.shape[1] >= m.max_width,
+    _need(ga.shape[0] >= m.rows and ga.shape[1] >= m.max_width,
           "grad_output smaller than [rows, max_expert_width]")
-    if pre is not None:
-        _need(pre.shape == grad_h.shape, "pre_act and grad_output shapes differ")
     if gather_map is None:
         _need(x.shape[0] >= m.rows, "x has fewer rows than expert_token_offsets[-1]")
     else:
         _need(gather_map.numel() >= m.rows, "gather_map shorter than the padded row count")
-    grad_x = _alloc(m.rows, hidden, grad_h, not m.full_rows)
+    grad_x = _alloc(m.rows, hidden, ga, not m.full_rows)
     grad_w1 = torch.zeros_like(w1) if not m.full_cols else torch.empty_like(w1)
-    dev = grad_h.device
+    dev = ga.device
     if m.rows > 0:
-        _lib.call("vmoe_gemm_up_bwd_dx", grad_h.data_ptr(), _lib.ptr(pre), grad_h.stride(0),
-                  act, w1.data_ptr(), w1.stride(0), grad_x.data_ptr(), grad_x.stride(0),
-                  *_meta_args(m), hidden, m.max_width, m.rows, _lib.stream(dev))
+        _lib.call("vmoe_gemm_up_bwd_dx", ga.data_ptr(), ga.stride(0), w1.data_ptr(),
+                  w1.stride(0), grad_x.data_ptr(), grad_x.stride(0), *_meta_args(m), hidden,
+                  m.max_width, m.rows, _lib.stream(dev))
     gm = None if gather_map is None else _i32(gather_map)
     ws = _dw_workspace(m, hidden, dev)
     _lib.call("vmoe_gemm_up_bwd_dw", x.data_ptr(), x.stride(0), x.shape[0], _lib.ptr(gm),
-              grad_h.data_ptr(), _lib.ptr(pre), grad_h.stride(0), act, grad_w1.data_ptr(),
-              grad_w1.stride(0), *_meta_args(m), hidden, m.max_width, m.rows,
-              ws.data_ptr(), ws.numel(), _lib.stream(dev))
+              ga.data_ptr(), ga.stride(0), grad_w1.data_ptr(), grad_w1.stride(0),
+              *_meta_args(m), hidden, m.max_width, m.rows, ws.data_ptr(), ws.numel(),
+              _lib.stream(dev))
     return grad_x, grad_w1
 
 
-def down_bwd(grad_y, h, w2, m: GemmMeta, hidden: int, zero_tails: bool):
-    """(grad_intermediate [rows, max_width], grad_w2)."""
+def up_bwd(grad_h, x, w1, pre, m: GemmMeta, hidden: int, act: int,
+           gather_map: torch.Tensor | None):
+    """(grad_x in gathered rows, grad_w1) from the gradient of the activated output."""
+    grad_h = _bf16(grad_h, "grouped_gemm_up_backward grad_output")
+    if act == _lib.ACT_RELU_SQUARED:
+        pre = _bf16(pre, "grouped_gemm_up_backward pre_act")
+        _need(pre.shape == grad_h.shape, "pre_act and grad_output shapes differ")
+        ga = relu2_grad(grad_h, pre)
+    else:
+        ga = grad_h
+    return up_bwd_from_ga(ga, x, w1, m, hidden, gather_map)
+
+
+def down_bwd(grad_y, h, w2, m: GemmMeta, hidden: int, zero_tails: bool,
+             pre: torch.Tensor | None = None):
+    """(grad_intermediate [rows, max_width], grad_w2). With pre, the first
+    output is the relu^2 gradient GA instead (fused in the dH epilogue)."""
     grad_y = _bf16(grad_y, "grouped_gemm_down_backward grad_output")
     h = _bf16(h, "grouped_gemm_down_backward intermediate")
     w2 = _bf16(w2, "grouped_gemm_down_backward w2")
@@ -239,12 +257,16 @@ def down_bwd(grad_y, h, w2, m: GemmMeta, hidden: int, zero_tails: bool):
     _need(h.shape[0] >= m.rows and h.shape[1] >= m.max_width,
           "intermediate smaller than [rows, max_expert_width]")
     grad_h = _alloc(m.rows, m.max_width, grad_y, not m.full_rows)
+    if pre is not None:
+        pre = _bf16(pre, "pre_act")
+        _need(pre.shape[0] >= m.rows and pre.stride(0) == grad_h.stride(0),
+              "pre_act must match the [rows, max_expert_width] layout")
     grad_w2 = torch.zeros_like(w2) if not m.full_cols else torch.empty_like(w2)
     dev = grad_y.device
     if m.rows > 0:
         _lib.call("vmoe_gemm_down_bwd_dh", grad_y.data_ptr(), grad_y.stride(0), w2.data_ptr(),
-                  w2.stride(0), grad_h.data_ptr(), grad_h.stride(0), *_meta_args(m), hidden,
-                  m.max_width, m.rows, _lib.stream(dev))
+                  w2.stride(0), _lib.ptr(pre), grad_h.data_ptr(), grad_h.stride(0),
+                  *_meta_args(m), hidden, m.max_width, m.rows, _lib.stream(dev))
         if zero_tails:
             _zero_tails(grad_h, m)
     ws = _dw_workspace(m, hidden, dev)
@@ -418,40 +440,22 @@ def grouped_gemm_down_autograd(intermediate, w2, expert_token_offsets, expert_we
 # ---------------------------------------------------------------------------
 
 
-class RoutedUpOp(torch.autograd.Function):
-    """Up-projection for the module: metadata from the route, no host sync.
+class RoutedExpertsOp(torch.autograd.Function):
+    """Both grouped GEMMs of the module (up with relu^2, then down) as one
+    autograd node, with metadata from the route and no host sync.
 
-    Saves x_flat + gather_map for the dW backward, like the module's call of
-    grouped_gemm_up_autograd (triton_moe/moe.py:214-226).
+    Saves x_flat + gather_map for the up dW GEMM, like the module's call of
+    grouped_gemm_up_autograd (triton_moe/moe.py:214-226), plus H and PRE. Its
+    backward fuses the relu^2 gradient into the dH GEMM's epilogue, so the
+    gradient w.r.t. H is never materialised.
     """
 
     @staticmethod
     @custom_fwd(device_type="cuda")
-    def forward(ctx, x_gathered, w1, meta, x_flat, gather_map, hidden_size):
-        out, pre = up_fwd(x_gathered, w1, meta, _lib.ACT_RELU_SQUARED, True, zero_tails=False)
-        ctx.save_for_backward(x_flat, w1, pre, gather_map)
-        ctx.meta = meta
-        ctx.hidden_size = hidden_size
-        return out
-
-    @staticmethod
-    @custom_bwd(device_type="cuda")
-    @once_differentiable
-    def backward(ctx, grad_output):
-        x_flat, w1, pre, gm = ctx.saved_tensors
-        grad_x, grad_w1 = up_bwd(grad_output, x_flat, w1, pre, ctx.meta, ctx.hidden_size,
-                                 _lib.ACT_RELU_SQUARED, gm)
-        return grad_x, grad_w1, None, None, None, None
-
-
-class RoutedDownOp(torch.autograd.Function):
-    """Down-projection for the module: metadata from the route, no host sync."""
-
-    @staticmethod
-    @custom_fwd(device_type="cuda")
-    def forward(ctx, h, w2, meta, hidden_size):
+    def forward(ctx, x_gathered, w1, w2, meta, x_flat, gather_map, hidden_size):
+        h, pre = up_fwd(x_gathered, w1, meta, _lib.ACT_RELU_SQUARED, True, zero_tails=False)
         y = down_fwd(h, w2, meta, hidden_size)
-        ctx.save_for_backward(h, w2)
+        ctx.save_for_backward(x_flat, w1, w2, h, pre, gather_map)
         ctx.meta = meta
         ctx.hidden_size = hidden_size
         return y
@@ -459,8 +463,9 @@ class RoutedDownOp(torch.autograd.Function):
     @staticmethod
     @custom_bwd(device_type="cuda")
     @once_differentiable
-    def backward(ctx, grad_output):
-        h, w2 = ctx.saved_tensors
-        grad_h, grad_w2 = down_bwd(grad_output, h, w2, ctx.meta, ctx.hidden_size,
-                                   zero_tails=False)
-        return grad_h, grad_w2, None, None
+    def backward(ctx, grad_y):
+        x_flat, w1, w2, h, pre, gm = ctx.saved_tensors
+        ga, grad_w2 = down_bwd(grad_y, h, w2, ctx.meta, ctx.hidden_size, zero_tails=False,
+                               pre=pre)
+        grad_x, grad_w1 = up_bwd_from_ga(ga, x_flat, w1, ctx.meta, ctx.hidden_size, gm)
+        return grad_x, grad_w1, grad_w2, None, None, None, None

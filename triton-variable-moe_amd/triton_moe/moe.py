@@ -33,7 +33,7 @@ from .kernels import (
 )
 from .kernels.fused_cumsum import route_device
 from .kernels.gather import RoutedGatherOp
-from .kernels.grouped_gemm import GemmMeta, RoutedDownOp, RoutedUpOp
+from .kernels.grouped_gemm import GemmMeta, RoutedExpertsOp
 from .kernels.scatter import RoutedScatterOp
 
 
@@ -167,9 +167,8 @@ class TritonMoEMLP(nn.Module):
         num_rows_dev = r.info[0:1]
         x_gathered = RoutedGatherOp.apply(x_flat, r.row_src, r.assignment_row, k, r.rows_bound,
                                           num_rows_dev)
-        x_up = RoutedUpOp.apply(x_gathered, self.w1, meta, x_flat, r.gather_map,
-                                self.config.n_embd)
-        x_down = RoutedDownOp.apply(x_up, self.w2, meta, self.config.n_embd)
+        x_down = RoutedExpertsOp.apply(x_gathered, self.w1, self.w2, meta, x_flat,
+                                       r.gather_map, self.config.n_embd)
         output_flat = RoutedScatterOp.apply(x_down, r.row_src, r.assignment_row,
                                             top_k_weights_flat, k, x_flat.shape[0],
                                             num_rows_dev)
@@ -288,10 +287,13 @@ class TritonMoEMLP(nn.Module):
             x_gathered = RoutedGatherOp.apply(x_flat, r.row_src, r.assignment_row, k,
                                               r.rows_bound, nrd)
         with profiler.step("gemm_up"):
-            x_up = RoutedUpOp.apply(x_gathered, self.w1, meta, x_flat, r.gather_map,
-                                    self.config.n_embd)
+            # up and down run as one autograd node (their backward is fused);
+            # both forward GEMMs are timed under "gemm_up" and "gemm_down" stays
+            # as an (empty) step so the reference's step names are all present.
+            x_down = RoutedExpertsOp.apply(x_gathered, self.w1, self.w2, meta, x_flat,
+                                           r.gather_map, self.config.n_embd)
         with profiler.step("gemm_down"):
-            x_down = RoutedDownOp.apply(x_up, self.w2, meta, self.config.n_embd)
+            pass
         with profiler.step("scatter"):
             output_flat = RoutedScatterOp.apply(x_down, r.row_src, r.assignment_row,
                                                 top_k_weights_flat, k, x_flat.shape[0], nrd)
