@@ -97,6 +97,7 @@ struct Traits;
 
 template <>
 struct Traits<UP_FWD> {
+  static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = false;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.tpe[e];
@@ -117,6 +118,7 @@ struct Traits<UP_FWD> {
 
 template <>
 struct Traits<DOWN_FWD> {
+  static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = false;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.tpe[e];
@@ -137,6 +139,7 @@ struct Traits<DOWN_FWD> {
 
 template <>
 struct Traits<UP_DX> {
+  static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = true;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.tpe[e];
@@ -158,6 +161,7 @@ struct Traits<UP_DX> {
 template <>
 struct Traits<UP_DW> {
   static constexpr bool a_k = false, b_k = false;
+  static constexpr bool t_map = true;  // A rows may come through the gather map
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.hidden;
     nt = p.widths[e];
@@ -177,6 +181,7 @@ struct Traits<UP_DW> {
 
 template <>
 struct Traits<DOWN_DH> {
+  static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = true;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.tpe[e];
@@ -197,6 +202,7 @@ struct Traits<DOWN_DH> {
 
 template <>
 struct Traits<DOWN_DW> {
+  static constexpr bool t_map = false;
   static constexpr bool a_k = false, b_k = false;
   __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
     mt = p.widths[e];
@@ -223,7 +229,7 @@ struct Cfg {
   static constexpr bool dw = V == UP_DW || V == DOWN_DW;
   static constexpr int BM = dw ? 128 : 256;
   static constexpr int BN = 128;
-  static constexpr int STAGES = 2;  // double-buffered LDS ring
+  static constexpr int STAGES = 4;  // LDS ring: STAGES - 1 tiles in flight
 };
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
@@ -231,6 +237,18 @@ __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the release/acquire fences of __syncthreads(),
+// which would drain every outstanding DMA (vmcnt(0)) and empty the LDS ring.
+// LDS data are ordered explicitly instead: each wave waits for its own DMAs
+// (wait_vmcnt) before the barrier, and its LDS reads of a buffer are consumed
+// by MFMAs before it reaches the next barrier. The asm clobbers keep the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // Buffer resource over [base, base + 2 GiB): word 3 = 0x00020000 is the raw
@@ -248,10 +266,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(b, 0, 0x7FFFFFFF, 0x00020000);
 }
 
-// 16-byte DMA of the lane's source into LDS at dst + 16 * lane.
+// 16-byte DMA of the lane's source into LDS at dst + 16 * lane
+// (buffer_load_dwordx4 ... lds, LDS base in M0). Issued as inline asm so the
+// compiler does not track it: it would otherwise wait for every DMA before
+// any LDS read it cannot prove disjoint (at the loop head it cannot), which
+// empties the ring. The kernels order DMA completion themselves with
+// wait_vmcnt + block_barrier, and nothing else in them uses M0.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, lds_char* dst) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      r, reinterpret_cast<__attribute__((address_space(3))) void*>(dst), 16, (int)voff, 0, 0, 0);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(dst));
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(r), "s"(lds) : "memory");
 }
 
 template <int V, int BM, int BN, int STAGES>
@@ -363,7 +387,7 @@ struct Gemm {
       const int k = k0 + s.idx[i];
       bool v = s.ok[i] && k < K;
       uint32_t off;
-      if (s.map) {
+      if (T::t_map && s.map) {
         int64_t row = v ? (int64_t)s.map[s.r0 + k] : -1;
         v = v && row >= 0 && row < s.map_rows;
         off = v ? s.off[i] + (uint32_t)row * s.ld2 : kOob;
@@ -455,18 +479,26 @@ struct Gemm {
     return e_out >= 0;
   }
 
-  // One k-tile: wait for its DMA, release the other buffer to the next
-  // tile's DMA, then multiply. cur/nxt are distinct LDS objects, so the
-  // compiler can tell the DMA into nxt from the reads of cur and does not
-  // wait on it.
+  // One k-tile. Tiles kt+1 .. kt+STAGES-2 may still be in flight: wait until
+  // only their DMAs are outstanding (DMA completes in order), sync, hand the
+  // buffer read by the previous step to tile kt+STAGES-1, then multiply.
+  // Every stage buffer is a distinct LDS object, so the compiler can tell the
+  // DMAs into the other buffers from the reads of `cur` and adds no waits.
   template <class Issue>
-  __device__ static void step(int kt, int nk, lds_char* cur, lds_char* nxt, Issue& issue,
+  __device__ static void step(int kt, int nk, lds_char* cur, lds_char* refill, Issue& issue,
                               f32x16_t (&acc)[FM][FN]) {
+    constexpr int PT = PWA + PWB;  // DMA instructions per tile per thread
     const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    wait_vmcnt<0>();
-    __syncthreads();
-    if (kt + 1 < nk) issue(kt + 1, nxt);
+    const int after = min(nk - 1 - kt, STAGES - 2);
+    if (STAGES > 3 && after >= 2)
+      wait_vmcnt<(STAGES > 3 ? 2 : 0) * PT>();
+    else if (STAGES > 2 && after >= 1)
+      wait_vmcnt<(STAGES > 2 ? 1 : 0) * PT>();
+    else
+      wait_vmcnt<0>();
+    block_barrier();
+    if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, refill);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_t af[FM], bfr[FN];
@@ -487,14 +519,14 @@ struct Gemm {
     }
   }
 
-  __device__ static void run(const Args& p, lds_char* st0, lds_char* st1) {
+  __device__ static void run(const Args& p, lds_char* const (&st)[STAGES]) {
     // XCD-aware remap: hardware deals workgroup ids round-robin over the 8
     // XCDs; give each XCD a contiguous range of tiles (gridDim.x % 8 == 0).
     const int g = gridDim.x, b = blockIdx.x;
     const int bid = (b % 8) * (g / 8) + b / 8;
 
     int e, local, split_pre, chunks;
-    if (!locate<0>(p, bid, reinterpret_cast<long long*>((char*)st1), e, local, split_pre,
+    if (!locate<0>(p, bid, reinterpret_cast<long long*>((char*)st[STAGES - 1]), e, local, split_pre,
                    chunks))
       return;
     int mt_dim, nt_dim;
@@ -542,15 +574,20 @@ struct Gemm {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    if (nk > 0) issue(0, st0);
-    // Pairs of k-tiles (stage 0 then stage 1), both steps unconditional so the
-    // accumulators stay in place across the loop; an odd last tile follows.
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+      if (s < nk) issue(s, st[s]);
+    // Groups of STAGES k-tiles with every step unconditional (so the
+    // accumulators stay in their registers across the loop), then the tail.
     int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-      step(kt, nk, st0, st1, issue, acc);
-      step(kt + 1, nk, st1, st0, issue, acc);
+    for (; kt + STAGES - 1 < nk; kt += STAGES) {
+#pragma unroll
+      for (int j = 0; j < STAGES; ++j)
+        step(kt + j, nk, st[j], st[(j + STAGES - 1) % STAGES], issue, acc);
     }
-    if (kt < nk) step(kt, nk, st0, st1, issue, acc);
+#pragma unroll
+    for (int j = 0; j < STAGES - 1; ++j)
+      if (kt + j < nk) step(kt + j, nk, st[j], st[(j + STAGES - 1) % STAGES], issue, acc);
 
     // Epilogue. acc[i][j][4*g + r] sits at m = wm*WM + i*32 + (lane & 31),
     // n = wn*WN + j*32 + 8*g + 4*(lane >> 5) + r.
@@ -613,10 +650,15 @@ struct Gemm {
 template <int V>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
   using G = Gemm<V, Cfg<V>::BM, Cfg<V>::BN, Cfg<V>::STAGES>;
-  // Two stage buffers as distinct LDS objects (see Gemm::step).
+  static_assert(Cfg<V>::STAGES == 4, "the ring below declares four stage buffers");
+  // Stage buffers as distinct LDS objects (see Gemm::step).
   __shared__ __align__(16) char stage0[G::STAGE];
   __shared__ __align__(16) char stage1[G::STAGE];
-  G::run(p, (lds_char*)stage0, (lds_char*)stage1);
+  __shared__ __align__(16) char stage2[G::STAGE];
+  __shared__ __align__(16) char stage3[G::STAGE];
+  lds_char* const st[4] = {(lds_char*)stage0, (lds_char*)stage1, (lds_char*)stage2,
+                           (lds_char*)stage3};
+  G::run(p, st);
 }
 
 // Sums the K-chunk partials of every split (expert, tile) in chunk order and
