@@ -12,25 +12,27 @@
 //   DOWN_DW  _grouped_gemm_down_backward_dw_kernel   (grouped_gemm.py:1066-1162)
 //
 // Design:
-//  * Tile scheduler on the device: the grid is an upper bound of the work
-//    count; each workgroup scans the per-expert work counts (from the same
-//    metadata the reference reads) and finds its (expert, tile, K chunk), so
-//    no host sync is needed and empty experts cost nothing. Workgroup ids are
-//    remapped so that consecutive tiles (same expert, same weight slice) run
-//    on the same XCD and share its L2.
-//  * 256 threads = 4 waves in a 2x2 grid; each wave owns (BM/2)x(BN/2) of
-//    32x32 MFMA accumulators (fp32; 128x128 per wave for 256x256 tiles).
-//  * Every operand tile goes global -> LDS by DMA (global_load_lds, 16 bytes
-//    per lane), never through VGPRs, in a multi-stage ring: the loads of
-//    tile k+STAGES-1 fly while tile k is multiplied.
+//  * Persistent grid, one 512-thread workgroup per CU. Each workgroup builds
+//    the per-expert work table (tiles x K chunks, exclusive prefix) in LDS
+//    from the same metadata the reference reads, so no host sync is needed
+//    and empty experts cost nothing. XCD x owns a contiguous eighth of the
+//    work items (the tiles of one expert share that XCD's L2); its
+//    workgroups take every (grid / 8)-th item.
+//  * 8 waves in a 2x4 grid over a 256x256 tile, 128x64 fp32 accumulators
+//    per wave, two waves per SIMD.
+//  * Every operand tile goes global -> LDS by DMA (buffer_load ... lds, 16
+//    bytes per lane), never through VGPRs, in a 4-stage ring; the k-tiles of
+//    all items of a workgroup form one stream, so the next item's first
+//    stages load while the current item finishes and stores its tile.
 //      - K-contiguous sources (activations in the forward, W in dX/dH) land
 //        in "K-form": one 64-byte row per m (n), 16-byte chunk c of row r at
-//        c ^ ((r >> 1) & 3); MFMA fragments are one ds_read_b128.
+//        c ^ ((r >> 2) & 3); MFMA fragments are one ds_read_b128.
 //      - M/N-contiguous sources (W1/W2 in the forward, both dW operands)
 //        land as they are in memory ("T-form": one row per k), chunk c of
-//        k-row k at c ^ 2(k & 3); fragments are two ds_read_b64_tr_b16,
-//        the gfx950 LDS transpose read, so no operand is transposed in
-//        registers. Both swizzles make the fragment reads bank-conflict free.
+//        k-row k at c ^ (4 (k & 3) | 2 ((k >> 3) & 1)); fragments are two
+//        ds_read_b64_tr_b16, the gfx950 LDS transpose read, so no operand is
+//        transposed in registers. Both swizzles make the fragment reads
+//        bank-conflict free (64 banks of 4 bytes).
 //  * Epilogues: relu and relu^2 of the fp32 accumulator (PRE, H) for the up
 //    projection (grouped_gemm.py:336-346); for the down dH GEMM an optional
 //    fused relu^2 gradient GA = bf16(pre > 0 ? 2 * bf16(acc) * pre : 0)
@@ -51,8 +53,21 @@ typedef __attribute__((address_space(3))) char lds_char;
 typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4;
 typedef __attribute__((address_space(3))) bf16x8_t lds_bf16x8;
 
-constexpr int kThreads = 256;
-constexpr int kBK = 32;  // k per LDS stage: two 16-deep MFMA steps
+// Workgroup roles: consumer waves (two per SIMD, so one hides the other's
+// LDS latency) read the staged tiles, run the MFMAs and store the results;
+// producer waves (one per SIMD) issue every DMA and do every wait on it.
+// The wait counter of a wave (vmcnt) counts its loads and stores together,
+// so keeping the DMAs out of the consumers means their stores never hold
+// up the pipeline.
+constexpr int kConsumers = 8;
+constexpr int kProducers = 4;
+constexpr int kWaves = kConsumers + kProducers;
+constexpr int kThreads = kWaves * 64;
+constexpr int kBK = 32;        // k per LDS stage: two 16-deep MFMA steps
+constexpr int kStages = 4;     // LDS ring: kStages - 1 k-tiles in flight
+constexpr int kMaxExperts = 2048;  // per-expert work prefix held in LDS
+constexpr int kRecExperts = 512;   // per-expert metadata also held in LDS up to this E
+constexpr int kRedThreads = 256;   // split-K reduction kernel
 
 enum Variant { UP_FWD = 0, DOWN_FWD, UP_DX, UP_DW, DOWN_DH, DOWN_DW };
 
@@ -76,8 +91,27 @@ struct Args {
   int act;
   int64_t rows_bound;
   int kc;          // K rows per work item for the dW GEMMs (0 = whole K)
-  float* partial;  // fp32 partial tiles of split work items
+  float* partial;  // fp32 partial tiles of split tiles (2 slots per workgroup)
+  int grid;        // GEMM workgroups (the split-K reduce recomputes their ranges)
 };
+
+// Metadata of one expert as the GEMMs read it: its row range [t0, t1) in
+// the expert-sorted layout (t1 clipped to rows_bound), its routed-row count,
+// its weight column range [ew0, ew1) and its width.
+struct ExpertRec {
+  int t0, t1, tpe, ew0, ew1, w;
+};
+
+__device__ __forceinline__ ExpertRec rec_global(const Args& p, int e) {
+  ExpertRec r;
+  r.t0 = p.eto[e];
+  r.t1 = (int)min<int64_t>(p.eto[e + 1], p.rows_bound);
+  r.tpe = p.tpe[e];
+  r.ew0 = p.ewo[e];
+  r.ew1 = p.ewo[e + 1];
+  r.w = p.widths[e];
+  return r;
+}
 
 // Per-expert problem: valid extents and operand origins.
 //   A K-contig:  A(m,k) = a[(ar + m) * lda + ac + k]
@@ -87,10 +121,10 @@ struct Args {
 //   C(m,n) = c[(cr + m) * ldc + cc + n]
 struct Prob {
   int M, N, K;
-  int64_t ar, ac, br, bc, cr, cc;
+  int ar, ac, br, bc, cr, cc;
 };
 
-__device__ __forceinline__ int clamp0(int64_t v) { return (int)max<int64_t>(0, v); }
+__device__ __forceinline__ int clamp0(int v) { return max(0, v); }
 
 template <int V>
 struct Traits;
@@ -99,19 +133,14 @@ template <>
 struct Traits<UP_FWD> {
   static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = false;
-  __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
-    mt = p.tpe[e];
-    nt = p.widths[e];
-  }
-  __device__ static Prob prob(const Args& p, int e) {
-    const int64_t t0 = p.eto[e], t1 = min<int64_t>(p.eto[e + 1], p.rows_bound);
+  __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
-    q.M = clamp0(min<int64_t>(p.tpe[e], t1 - t0));
-    q.N = clamp0(p.widths[e]);
+    q.M = clamp0(min(r.tpe, r.t1 - r.t0));
+    q.N = clamp0(r.w);
     q.K = p.hidden;
-    q.ar = t0; q.ac = 0;
-    q.br = 0; q.bc = p.ewo[e];  // B(k,n) = W1[k][ewo + n]
-    q.cr = t0; q.cc = 0;
+    q.ar = r.t0; q.ac = 0;
+    q.br = 0; q.bc = r.ew0;  // B(k,n) = W1[k][ewo + n]
+    q.cr = r.t0; q.cc = 0;
     return q;
   }
 };
@@ -120,19 +149,14 @@ template <>
 struct Traits<DOWN_FWD> {
   static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = false;
-  __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
-    mt = p.tpe[e];
-    nt = p.hidden;
-  }
-  __device__ static Prob prob(const Args& p, int e) {
-    const int64_t t0 = p.eto[e], t1 = min<int64_t>(p.eto[e + 1], p.rows_bound);
+  __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
-    q.M = clamp0(min<int64_t>(p.tpe[e], t1 - t0));
+    q.M = clamp0(min(r.tpe, r.t1 - r.t0));
     q.N = p.hidden;
-    q.K = clamp0((int64_t)p.ewo[e + 1] - p.ewo[e]);
-    q.ar = t0; q.ac = 0;
-    q.br = p.ewo[e]; q.bc = 0;  // B(k,n) = W2[ewo + k][n]
-    q.cr = t0; q.cc = 0;
+    q.K = clamp0(r.ew1 - r.ew0);
+    q.ar = r.t0; q.ac = 0;
+    q.br = r.ew0; q.bc = 0;  // B(k,n) = W2[ewo + k][n]
+    q.cr = r.t0; q.cc = 0;
     return q;
   }
 };
@@ -141,19 +165,14 @@ template <>
 struct Traits<UP_DX> {
   static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = true;
-  __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
-    mt = p.tpe[e];
-    nt = p.hidden;
-  }
-  __device__ static Prob prob(const Args& p, int e) {
-    const int64_t t0 = p.eto[e], t1 = min<int64_t>(p.eto[e + 1], p.rows_bound);
+  __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
-    q.M = clamp0(min<int64_t>(p.tpe[e], t1 - t0));
+    q.M = clamp0(min(r.tpe, r.t1 - r.t0));
     q.N = p.hidden;
-    q.K = clamp0((int64_t)p.ewo[e + 1] - p.ewo[e]);
-    q.ar = t0; q.ac = 0;        // A(m,k) = GA[t0 + m][k]
-    q.br = 0; q.bc = p.ewo[e];  // B(k,n) = W1[n][ewo + k]
-    q.cr = t0; q.cc = 0;
+    q.K = clamp0(r.ew1 - r.ew0);
+    q.ar = r.t0; q.ac = 0;   // A(m,k) = GA[t0 + m][k]
+    q.br = 0; q.bc = r.ew0;  // B(k,n) = W1[n][ewo + k]
+    q.cr = r.t0; q.cc = 0;
     return q;
   }
 };
@@ -162,19 +181,14 @@ template <>
 struct Traits<UP_DW> {
   static constexpr bool a_k = false, b_k = false;
   static constexpr bool t_map = true;  // A rows may come through the gather map
-  __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
-    mt = p.hidden;
-    nt = p.widths[e];
-  }
-  __device__ static Prob prob(const Args& p, int e) {
-    const int64_t t0 = p.eto[e], t1 = min<int64_t>(p.eto[e + 1], p.rows_bound);
+  __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
     q.M = p.hidden;
-    q.N = clamp0(p.widths[e]);
-    q.K = clamp0(t1 - t0);
-    q.ar = t0; q.ac = 0;  // A(m,k) = X[row(t0 + k)][m]
-    q.br = t0; q.bc = 0;  // B(k,n) = GA[t0 + k][n]
-    q.cr = 0; q.cc = p.ewo[e];
+    q.N = clamp0(r.w);
+    q.K = clamp0(r.t1 - r.t0);
+    q.ar = r.t0; q.ac = 0;  // A(m,k) = X[row(t0 + k)][m]
+    q.br = r.t0; q.bc = 0;  // B(k,n) = GA[t0 + k][n]
+    q.cr = 0; q.cc = r.ew0;
     return q;
   }
 };
@@ -183,19 +197,14 @@ template <>
 struct Traits<DOWN_DH> {
   static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = true;
-  __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
-    mt = p.tpe[e];
-    nt = p.widths[e];
-  }
-  __device__ static Prob prob(const Args& p, int e) {
-    const int64_t t0 = p.eto[e], t1 = min<int64_t>(p.eto[e + 1], p.rows_bound);
+  __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
-    q.M = clamp0(min<int64_t>(p.tpe[e], t1 - t0));
-    q.N = clamp0(p.widths[e]);
+    q.M = clamp0(min(r.tpe, r.t1 - r.t0));
+    q.N = clamp0(r.w);
     q.K = p.hidden;
-    q.ar = t0; q.ac = 0;
-    q.br = p.ewo[e]; q.bc = 0;  // B(k,n) = W2[ewo + n][k]
-    q.cr = t0; q.cc = 0;
+    q.ar = r.t0; q.ac = 0;
+    q.br = r.ew0; q.bc = 0;  // B(k,n) = W2[ewo + n][k]
+    q.cr = r.t0; q.cc = 0;
     return q;
   }
 };
@@ -204,35 +213,42 @@ template <>
 struct Traits<DOWN_DW> {
   static constexpr bool t_map = false;
   static constexpr bool a_k = false, b_k = false;
-  __device__ static void tile_dims(const Args& p, int e, int& mt, int& nt) {
-    mt = p.widths[e];
-    nt = p.hidden;
-  }
-  __device__ static Prob prob(const Args& p, int e) {
-    const int64_t t0 = p.eto[e], t1 = min<int64_t>(p.eto[e + 1], p.rows_bound);
+  __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
-    q.M = clamp0(p.widths[e]);
+    q.M = clamp0(r.w);
     q.N = p.hidden;
-    q.K = clamp0(t1 - t0);
-    q.ar = t0; q.ac = 0;  // A(m,k) = H[t0 + k][m]
-    q.br = t0; q.bc = 0;  // B(k,n) = GY[t0 + k][n]
-    q.cr = p.ewo[e]; q.cc = 0;
+    q.K = clamp0(r.t1 - r.t0);
+    q.ar = r.t0; q.ac = 0;  // A(m,k) = H[t0 + k][m]
+    q.br = r.t0; q.bc = 0;  // B(k,n) = GY[t0 + k][n]
+    q.cr = r.ew0; q.cc = 0;
     return q;
   }
 };
 
-// Tile shape per variant: 256x128 for the GEMMs tiled over rows (large M),
-// 128x128 for the dW GEMMs (M, N are hidden x width; split-K supplies the
-// parallelism, and smaller tiles keep partial tiles cheap).
+// Tile shape: 128x256 output tiles, the 8 consumer waves in a 2 (m) x 4 (n)
+// grid of 64x64 fp32 accumulators each (64 registers, so three waves fit a
+// SIMD). N = 256 covers a whole 256-wide expert in the up projection. The
+// dW GEMMs split their long K (the expert's rows) into chunks and give each
+// workgroup a contiguous run of work items ("contig"), accumulating across
+// the chunks of a tile; the row-tiled GEMMs deal items round-robin.
 template <int V>
 struct Cfg {
-  static constexpr bool dw = V == UP_DW || V == DOWN_DW;
-  static constexpr int BM = dw ? 128 : 256;
-  static constexpr int BN = 128;
-  static constexpr int STAGES = 4;  // LDS ring: STAGES - 1 tiles in flight
+  static constexpr int BM = 128, BN = 256;
+  static constexpr int WGM = 2, WGN = 4;
+  static constexpr bool contig = V == UP_DW || V == DOWN_DW;
 };
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// Work items of expert e: its output tiles times its K chunks (chunks > 1
+// only for the split-K dW GEMMs, p.kc > 0).
+template <int V>
+__device__ __forceinline__ void expert_work(const Args& p, const Prob& q, int& tiles,
+                                            int& chunks) {
+  constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN;
+  tiles = (q.M > 0 && q.N > 0) ? cdiv(q.M, BM) * cdiv(q.N, BN) : 0;
+  chunks = (p.kc > 0 && tiles > 0 && q.K > p.kc) ? cdiv(q.K, p.kc) : 1;
+}
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -269,37 +285,90 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
 // 16-byte DMA of the lane's source into LDS at dst + 16 * lane
 // (buffer_load_dwordx4 ... lds, LDS base in M0). Issued as inline asm so the
 // compiler does not track it: it would otherwise wait for every DMA before
-// any LDS read it cannot prove disjoint (at the loop head it cannot), which
-// empties the ring. The kernels order DMA completion themselves with
-// wait_vmcnt + block_barrier, and nothing else in them uses M0.
+// any LDS read it cannot prove disjoint, which empties the ring. The kernels
+// order DMA completion themselves with wait_vmcnt + block_barrier, and
+// nothing else in them uses M0.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, lds_char* dst) {
   const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(dst));
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :: "v"(voff), "s"(r), "s"(lds) : "memory");
 }
 
-template <int V, int BM, int BN, int STAGES>
+// Per-expert tables of a launch, built once per workgroup: the exclusive
+// prefix of work items (pre[E] = total) and, for E <= kRecExperts, the
+// expert records themselves.
+struct Meta {
+  int pre[kMaxExperts + 1];
+  int rec[6][kRecExperts];
+};
+
+// Work-item range of workgroup b. Round-robin: XCD x (hardware deals
+// workgroup b to XCD b % 8) owns the contiguous range [x * total / 8,
+// (x + 1) * total / 8), so the tiles of one expert share an L2, and its
+// workgroups take every (grid / 8)-th item. Contig: workgroup with linear
+// index L = x * (grid / 8) + b / 8 owns [total * L / grid, total * (L + 1) / grid).
+struct Range {
+  int beg, end, stride, lin;
+};
+
+__host__ __device__ inline int contig_begin(int total, int lin, int grid) {
+  return (int)((int64_t)total * lin / grid);
+}
+
+template <bool CONTIG>
+__device__ __forceinline__ Range item_range(int total) {
+  const int G = gridDim.x, b = blockIdx.x;
+  const int xcd = b & 7, per = G >> 3, j = b >> 3;
+  Range r;
+  r.lin = xcd * per + j;
+  if (CONTIG) {
+    r.beg = contig_begin(total, r.lin, G);
+    r.end = contig_begin(total, r.lin + 1, G);
+    r.stride = 1;
+  } else {
+    r.beg = (int)((int64_t)total * xcd / 8) + j;
+    r.end = (int)((int64_t)total * (xcd + 1) / 8);
+    r.stride = per;
+  }
+  return r;
+}
+
+template <int V>
 struct Gemm {
   using T = Traits<V>;
+  static constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN;
+  static constexpr int WGM = Cfg<V>::WGM, WGN = Cfg<V>::WGN;
+  static_assert(WGM * WGN == kConsumers, "one consumer wave per wave-grid cell");
   static constexpr int BK = kBK;
-  static constexpr int WM = BM / 2, WN = BN / 2;    // wave tile
-  static constexpr int FM = WM / 32, FN = WN / 32;  // 32x32 blocks per wave
+  static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
+  static constexpr int FM = WM / 32, FN = WN / 32;    // 32x32 blocks per wave
   static constexpr int A_STAGE = BM * BK * 2, B_STAGE = BN * BK * 2;  // bytes
   static constexpr int STAGE = A_STAGE + B_STAGE;
-  static constexpr int LDS_BYTES = STAGES * STAGE;
-  // DMA instructions per wave per stage for an operand of R rows/cols.
+  static constexpr int RING = kStages * STAGE;
+  // DMA instructions per producer wave per stage for an operand of R rows/cols.
   template <int R>
   struct Dma {
-    static constexpr int INSTS = R * BK / 8 / 64;
-    static constexpr int PW = INSTS / 4;
-    static constexpr int LPR = R / 8;        // T-form: lanes per k-row
-    static constexpr int RPI = 64 / LPR;     // T-form: k-rows per instruction
-    static_assert(INSTS % 4 == 0 && PW >= 1, "tile too small for 4 waves");
+    static constexpr int INSTS = R * BK * 2 / 1024;
+    static constexpr int PW = INSTS / kProducers;
+    static constexpr int LPR = R / 8;     // T-form: lanes per k-row
+    static constexpr int RPI = 64 / LPR;  // T-form: k-rows per instruction
+    static_assert(INSTS % kProducers == 0 && PW >= 1, "tile too small for the producers");
+    static_assert(RPI >= 1, "T-form k-row wider than one DMA instruction");
   };
   static constexpr int PWA = Dma<BM>::PW, PWB = Dma<BN>::PW;
+  static constexpr int PT = PWA + PWB;  // DMA instructions per stage per producer thread
+  __device__ static int pwave() { return (threadIdx.x >> 6) - kConsumers; }
 
-  __device__ static int kswz(int r) { return (r >> 1) & 3; }
-  __device__ static int tswz(int k) { return (k & 3) << 1; }
+  // LDS is 64 banks x 4 bytes; a ds_read_b128 serves 16 lanes per cycle and
+  // a ds_read_b64_tr_b16 32 lanes per cycle. K-form: the 16 rows one phase
+  // reads sit four to a 256-byte bank line, so the chunk is XORed with
+  // (row / 4) to spread the four rows sharing a 64-byte slot. T-form: one
+  // phase reads k-rows k..k+3 at two column offsets 32 bytes apart, so the
+  // chunk is XORed with 4 * (k % 4) (distinct 64-byte slots per k-row) and
+  // with 2 * ((k / 8) % 2) for the other phase's k-rows.
+  __device__ static int kswz(int r) { return (r >> 2) & 3; }
+  __device__ static int tswz(int k) { return ((k & 3) << 2) | (((k >> 3) & 1) << 1); }
+  static_assert(BM >= 128 && BN >= 128, "T-form swizzle needs 16 chunks per k-row");
 
   // Per-thread DMA state of one operand: a buffer resource over the
   // operand (rebased to the tile where no row map is used) and one 32-bit
@@ -308,8 +377,8 @@ struct Gemm {
   struct Src {
     __amdgpu_buffer_rsrc_t rsrc;
     const int32_t* map;  // T-form row gather (nullable)
-    int64_t map_rows;
-    int64_t r0;          // T-form with map: source row of k = 0
+    int map_rows;
+    int r0;              // T-form with map: source row of k = 0
     uint32_t ld2;        // leading dimension in bytes
     uint32_t off[PW];    // K-form: row + chunk; T-form: chunk column (+ k-row without map)
     int idx[PW];         // K-form: k of the lane's chunk; T-form: the lane's k-row
@@ -322,7 +391,7 @@ struct Gemm {
   __device__ static void setup_k(Src<PW>& s, const uint16_t* base, int64_t ld,
                                  const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
                                  int rows_valid) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = pwave();
     // Without a map, rebase to the tile's first row so offsets stay small.
     const uint16_t* b = map ? base + c0 : base + r0 * ld + c0;
     s.rsrc = make_rsrc(b);
@@ -347,7 +416,7 @@ struct Gemm {
   // K-form issue: stage tile k0 .. k0 + BK (k0 relative to the setup's c0).
   template <int R, int PW>
   __device__ static void issue_k(const Src<PW>& s, int k0, int K, lds_char* stage) {
-    const int wave = threadIdx.x >> 6;
+    const int wave = pwave();
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const bool v = s.ok[i] && k0 + s.idx[i] < K;
@@ -362,12 +431,12 @@ struct Gemm {
                                  const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
                                  int cols_valid) {
     constexpr int LPR = Dma<R>::LPR, RPI = Dma<R>::RPI;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = pwave();
     const uint16_t* b = map ? base + c0 : base + r0 * ld + c0;
     s.rsrc = make_rsrc(b);
     s.map = map;
-    s.map_rows = map_rows;
-    s.r0 = r0;
+    s.map_rows = (int)map_rows;
+    s.r0 = (int)r0;
     s.ld2 = (uint32_t)(ld * 2);
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
@@ -381,7 +450,7 @@ struct Gemm {
 
   template <int R, int PW>
   __device__ static void issue_t(const Src<PW>& s, int k0, int K, lds_char* stage) {
-    const int wave = threadIdx.x >> 6;
+    const int wave = pwave();
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const int k = k0 + s.idx[i];
@@ -406,6 +475,8 @@ struct Gemm {
     return *reinterpret_cast<const lds_bf16x8*>(stage + row * 64 + ((c ^ kswz(row)) << 4));
   }
 
+  // Fragment of columns [col0, col0 + 32) x k-step ks from a T-form stage of
+  // R columns: two transposing reads of k-rows kr and kr + 4.
   template <int R>
   __device__ static bf16x8_t frag_t(const lds_char* stage, int col0, int ks) {
     const int lane = threadIdx.x & 63;
@@ -420,85 +491,114 @@ struct Gemm {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   }
 
-  // Work items of expert e: its output tiles times its K chunks (chunks > 1
-  // only for the split-K dW GEMMs, p.kc > 0).
-  __device__ static void expert_work(const Args& p, int e, int& tiles, int& chunks) {
-    int mt, nt;
-    T::tile_dims(p, e, mt, nt);
-    tiles = (mt > 0 && nt > 0) ? cdiv(mt, BM) * cdiv(nt, BN) : 0;
-    chunks = 1;
-    if (p.kc > 0 && tiles > 0) {
-      const int K = T::prob(p, e).K;
-      chunks = K > p.kc ? cdiv(K, p.kc) : 1;
-    }
-  }
-
-  // Finds the expert owning index `id` in the concatenation of per-expert
-  // ranges of size a_e (a block scan over experts), the offset inside that
-  // range, and the exclusive prefix of a second per-expert count b_e.
-  // MODE 0: a = items, b = split items (GEMM); MODE 1: a = tiles, b = split
-  // items (reduce). `scratch` holds 16 longs of LDS. Returns false when id is
-  // past the end.
-  template <int MODE>
-  __device__ static bool locate(const Args& p, int id, long long* scratch, int& e_out,
-                                int& local_out, int& bpre_out, int& chunks_out) {
-    long long* scan = scratch;                               // kThreads / 64 + 1 entries
-    int32_t* sh = reinterpret_cast<int32_t*>(scratch + 8);  // e, local, bpre, chunks
-    if (threadIdx.x == 0) sh[0] = -1;
+  // Builds the per-expert tables (all threads; `scan` is 16 longs of LDS).
+  // Returns the total number of work items.
+  __device__ static int build_meta(const Args& p, Meta& mt, long long* scan) {
     long long base = 0;
     for (int e0 = 0; e0 < p.E; e0 += kThreads) {
       const int e = e0 + threadIdx.x;
-      int tiles = 0, chunks = 1;
-      if (e < p.E) expert_work(p, e, tiles, chunks);
-      const int items = tiles * chunks;
-      const int a = MODE == 0 ? items : tiles;
-      const int b = chunks > 1 ? items : 0;
-      const long long packed = ((long long)a << 32) | (long long)b;
-      long long total;
-      const long long ex = block_exclusive_scan<long long, kThreads>(packed, scan, &total);
-      const long long pre = base + ex;
-      const int a_pre = (int)(pre >> 32), b_pre = (int)(pre & 0xFFFFFFFFll);
-      if (a > 0 && id >= a_pre && id < a_pre + a) {
-        sh[0] = e;
-        sh[1] = id - a_pre;
-        sh[2] = b_pre;
-        sh[3] = chunks;
+      int items = 0;
+      if (e < p.E) {
+        const ExpertRec r = rec_global(p, e);
+        if (p.E <= kRecExperts) {
+          mt.rec[0][e] = r.t0; mt.rec[1][e] = r.t1; mt.rec[2][e] = r.tpe;
+          mt.rec[3][e] = r.ew0; mt.rec[4][e] = r.ew1; mt.rec[5][e] = r.w;
+        }
+        int tiles, chunks;
+        expert_work<V>(p, T::prob(p, r), tiles, chunks);
+        items = tiles * chunks;
       }
+      long long total;
+      const long long ex = block_exclusive_scan<long long, kThreads>((long long)items, scan, &total);
+      if (e < p.E) mt.pre[e] = (int)(base + ex);
       base += total;
-      __syncthreads();
-      if (sh[0] >= 0 || (int)(base >> 32) > id) break;
+      __syncthreads();  // scan scratch reused by the next chunk
     }
-    // The values are block-uniform; readfirstlane tells the compiler so, and
-    // everything derived from them (operand bases, buffer resources) stays in
-    // scalar registers.
-    e_out = __builtin_amdgcn_readfirstlane(sh[0]);
-    local_out = __builtin_amdgcn_readfirstlane(sh[1]);
-    bpre_out = __builtin_amdgcn_readfirstlane(sh[2]);
-    chunks_out = __builtin_amdgcn_readfirstlane(sh[3]);
-    __syncthreads();  // the scratch LDS is reused by the caller
-    return e_out >= 0;
+    if (threadIdx.x == 0) mt.pre[p.E] = (int)base;
+    __syncthreads();
+    return (int)base;
   }
 
-  // One k-tile. Tiles kt+1 .. kt+STAGES-2 may still be in flight: wait until
-  // only their DMAs are outstanding (DMA completes in order), sync, hand the
-  // buffer read by the previous step to tile kt+STAGES-1, then multiply.
-  // Every stage buffer is a distinct LDS object, so the compiler can tell the
-  // DMAs into the other buffers from the reads of `cur` and adds no waits.
-  template <class Issue>
-  __device__ static void step(int kt, int nk, lds_char* cur, lds_char* refill, Issue& issue,
-                              f32x16_t (&acc)[FM][FN]) {
-    constexpr int PT = PWA + PWB;  // DMA instructions per tile per thread
-    const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int after = min(nk - 1 - kt, STAGES - 2);
-    if (STAGES > 3 && after >= 2)
-      wait_vmcnt<(STAGES > 3 ? 2 : 0) * PT>();
-    else if (STAGES > 2 && after >= 1)
-      wait_vmcnt<(STAGES > 2 ? 1 : 0) * PT>();
+  struct Work {
+    int m0, n0, kbeg, klen, nk, chunk, chunks;
+    Prob q;
+  };
+
+  // Work item `item` (ascending across calls with the same cursor): finds its
+  // expert with a wave-wide search of the prefix table from the cursor, then
+  // its tile and K chunk. Every field is workgroup-uniform.
+  __device__ static Work decode(const Args& p, const Meta& mt, int item, int& ecur) {
+    const int lane = threadIdx.x & 63;
+    int e = ecur;
+    for (;;) {
+      const int c = e + 1 + lane;
+      const bool past = c > p.E || mt.pre[c] > item;
+      const uint64_t mask = ballot64(past);
+      if (mask) {
+        e += __builtin_ctzll(mask);
+        break;
+      }
+      e += 64;
+    }
+    e = __builtin_amdgcn_readfirstlane(e);
+    ecur = e;
+    ExpertRec r;
+    if (p.E <= kRecExperts) {
+      r.t0 = __builtin_amdgcn_readfirstlane(mt.rec[0][e]);
+      r.t1 = __builtin_amdgcn_readfirstlane(mt.rec[1][e]);
+      r.tpe = __builtin_amdgcn_readfirstlane(mt.rec[2][e]);
+      r.ew0 = __builtin_amdgcn_readfirstlane(mt.rec[3][e]);
+      r.ew1 = __builtin_amdgcn_readfirstlane(mt.rec[4][e]);
+      r.w = __builtin_amdgcn_readfirstlane(mt.rec[5][e]);
+    } else {
+      r = rec_global(p, e);
+    }
+    Work w;
+    w.q = T::prob(p, r);
+    int tiles, chunks;
+    expert_work<V>(p, w.q, tiles, chunks);
+    const int local = item - __builtin_amdgcn_readfirstlane(mt.pre[e]);
+    const int tile = local / chunks, chunk = local % chunks;
+    const int n_tiles = cdiv(w.q.N, BN);
+    w.m0 = (tile / n_tiles) * BM;
+    w.n0 = (tile % n_tiles) * BN;
+    w.kbeg = 0;
+    w.chunk = chunk;
+    w.chunks = chunks;
+    int K = w.q.K;
+    if (chunks > 1) {
+      w.kbeg = chunk * p.kc;
+      K = min(K, w.kbeg + p.kc);
+    }
+    w.klen = K - w.kbeg;
+    w.nk = w.klen > 0 ? cdiv(w.klen, BK) : 0;
+    return w;
+  }
+
+  __device__ static void setup(const Args& p, const Work& w, Src<PWA>& sa, Src<PWB>& sb) {
+    const Prob& q = w.q;
+    if (T::a_k)
+      setup_k<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.m0, q.ac + w.kbeg, q.M - w.m0);
     else
-      wait_vmcnt<0>();
-    block_barrier();
-    if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, refill);
+      setup_t<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.kbeg, q.ac + w.m0, q.M - w.m0);
+    if (T::b_k)
+      setup_k<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg, q.N - w.n0);
+    else
+      setup_t<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + w.kbeg, q.bc + w.n0, q.N - w.n0);
+  }
+
+  __device__ static void issue(const Work& w, const Src<PWA>& sa, const Src<PWB>& sb, int kt,
+                               lds_char* st) {
+    const int k0 = kt * BK;
+    if (T::a_k) issue_k<BM>(sa, k0, w.klen, st); else issue_t<BM>(sa, k0, w.klen, st);
+    if (T::b_k) issue_k<BN>(sb, k0, w.klen, st + A_STAGE);
+    else issue_t<BN>(sb, k0, w.klen, st + A_STAGE);
+  }
+
+  // Multiplies one staged k-tile into the wave's accumulators.
+  __device__ static void compute(const lds_char* cur, f32x16_t (&acc)[FM][FN]) {
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_t af[FM], bfr[FN];
@@ -519,82 +619,19 @@ struct Gemm {
     }
   }
 
-  __device__ static void run(const Args& p, lds_char* const (&st)[STAGES]) {
-    // XCD-aware remap: hardware deals workgroup ids round-robin over the 8
-    // XCDs; give each XCD a contiguous range of tiles (gridDim.x % 8 == 0).
-    const int g = gridDim.x, b = blockIdx.x;
-    const int bid = (b % 8) * (g / 8) + b / 8;
-
-    int e, local, split_pre, chunks;
-    if (!locate<0>(p, bid, reinterpret_cast<long long*>((char*)st[STAGES - 1]), e, local, split_pre,
-                   chunks))
-      return;
-    int mt_dim, nt_dim;
-    T::tile_dims(p, e, mt_dim, nt_dim);
-    const int n_tiles = cdiv(nt_dim, BN);
-    const int tile = local / chunks, chunk = local % chunks;
-    const int m0 = (tile / n_tiles) * BM;
-    const int n0 = (tile % n_tiles) * BN;
-    Prob q = T::prob(p, e);
-    int kbeg = 0;
-    if (chunks > 1) {
-      kbeg = chunk * p.kc;
-      q.K = min(q.K, kbeg + p.kc);
-    }
-    const int nk = q.K > kbeg ? cdiv(q.K - kbeg, BK) : 0;
-    const int klen = q.K - kbeg;  // k below is relative to kbeg
-
-    Src<PWA> sa;
-    Src<PWB> sb;
-    if (T::a_k)
-      setup_k<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + m0, q.ac + kbeg, q.M - m0);
-    else
-      setup_t<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + kbeg, q.ac + m0, q.M - m0);
-    if (T::b_k)
-      setup_k<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + n0, q.bc + kbeg, q.N - n0);
-    else
-      setup_t<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + kbeg, q.bc + n0, q.N - n0);
-
-    auto issue = [&](int kt, lds_char* st) {
-      const int k0 = kt * BK;
-      if (T::a_k) issue_k<BM>(sa, k0, klen, st); else issue_t<BM>(sa, k0, klen, st);
-      if (T::b_k) issue_k<BN>(sb, k0, klen, st + A_STAGE);
-      else issue_t<BN>(sb, k0, klen, st + A_STAGE);
-    };
-
+  // Epilogue. acc[i][j][4*g + r] sits at m = wm*WM + i*32 + (lane & 31),
+  // n = wn*WN + j*32 + 8*g + 4*(lane >> 5) + r.
+  // `slot` >= 0: the accumulators are a partial sum over some of the tile's
+  // K chunks; the whole fp32 tile goes to that partial slot and the reduce
+  // kernel sums the segments in chunk order and rounds once.
+  __device__ static void epilogue(const Args& p, const Work& w, int pslot,
+                                  f32x16_t (&acc)[FM][FN]) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-
-    f32x16_t acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-      if (s < nk) issue(s, st[s]);
-    // Groups of STAGES k-tiles with every step unconditional (so the
-    // accumulators stay in their registers across the loop), then the tail.
-    int kt = 0;
-    for (; kt + STAGES - 1 < nk; kt += STAGES) {
-#pragma unroll
-      for (int j = 0; j < STAGES; ++j)
-        step(kt + j, nk, st[j], st[(j + STAGES - 1) % STAGES], issue, acc);
-    }
-#pragma unroll
-    for (int j = 0; j < STAGES - 1; ++j)
-      if (kt + j < nk) step(kt + j, nk, st[j], st[(j + STAGES - 1) % STAGES], issue, acc);
-
-    // Epilogue. acc[i][j][4*g + r] sits at m = wm*WM + i*32 + (lane & 31),
-    // n = wn*WN + j*32 + 8*g + 4*(lane >> 5) + r.
-    if (chunks > 1) {
-      // Split-K item: the whole fp32 tile goes to its partial slot; the
-      // reduce kernel sums the chunks in chunk order and rounds once.
-      float* slot = p.partial + (int64_t)(split_pre + local) * (BM * BN);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const Prob& q = w.q;
+    if (pslot >= 0) {
+      float* slot = p.partial + (int64_t)pslot * (BM * BN);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int ml = wm * WM + i * 32 + (lane & 31);
@@ -612,14 +649,14 @@ struct Gemm {
     }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int m = m0 + wm * WM + i * 32 + (lane & 31);
+      const int m = w.m0 + wm * WM + i * 32 + (lane & 31);
       if (m >= q.M) continue;
-      const int64_t roff = (q.cr + m) * p.ldc + q.cc;
+      const int64_t roff = ((int64_t)q.cr + m) * p.ldc + q.cc;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
-          const int n = n0 + wn * WN + j * 32 + 8 * gq + 4 * (lane >> 5);
+          const int n = w.n0 + wn * WN + j * 32 + 8 * gq + 4 * (lane >> 5);
           if (n >= q.N) continue;
           float v0 = acc[i][j][4 * gq + 0], v1 = acc[i][j][4 * gq + 1];
           float v2 = acc[i][j][4 * gq + 2], v3 = acc[i][j][4 * gq + 3];
@@ -645,52 +682,203 @@ struct Gemm {
       }
     }
   }
+
+  // Producer waves: stage the k-tiles of all of the workgroup's items, in
+  // item order, as one stream through the LDS ring (the first stages of the
+  // next item load while the current one finishes), waiting for each stage
+  // before the barrier that hands it to the consumers.
+  __device__ static void run_producer(const Args& p, lds_char* ring, const Meta& mt,
+                                      const Range& rg) {
+    int ec = 0, ei = 0;
+    Work wi = decode(p, mt, rg.beg, ei);
+    Src<PWA> sa;
+    Src<PWB> sb;
+    setup(p, wi, sa, sb);
+    int ikt = 0, inext = rg.beg + rg.stride;
+    int issued = 0;
+    auto issue_next = [&](lds_char* st) -> bool {
+      while (ikt >= wi.nk) {
+        if (inext >= rg.end) return false;
+        wi = decode(p, mt, inext, ei);
+        inext += rg.stride;
+        setup(p, wi, sa, sb);
+        ikt = 0;
+      }
+      issue(wi, sa, sb, ikt, st);
+      ++ikt;
+      return true;
+    };
+#pragma unroll
+    for (int s = 0; s < kStages - 1; ++s)
+      if (issue_next(ring + s * STAGE)) ++issued;
+    int s = 0;  // stage index in the workgroup's stream
+    for (int item = rg.beg; item < rg.end; item += rg.stride) {
+      const int nk = decode(p, mt, item, ec).nk;
+      for (int kt = 0; kt < nk; ++kt, ++s) {
+        // Stages s+1 .. issued-1 may still be in flight: wait until only
+        // their DMAs are outstanding (loads complete in order), sync (the
+        // consumers then read stage s), and refill the buffer the consumers
+        // read in the previous step, which every wave has left by now.
+        const int after = issued - 1 - s;
+        if (after >= 2)
+          wait_vmcnt<2 * PT>();
+        else if (after == 1)
+          wait_vmcnt<PT>();
+        else
+          wait_vmcnt<0>();
+        block_barrier();
+        if (issue_next(ring + ((s + kStages - 1) % kStages) * STAGE)) ++issued;
+      }
+    }
+  }
+
+  // Consumer waves: multiply each stage after the barrier that publishes it,
+  // and store a tile when its last K chunk in this workgroup is done. A
+  // contiguous range may start or end inside a split tile; such a segment
+  // is a partial sum and goes to slot 2 * lin (the range's first segment) or
+  // 2 * lin + 1 (its last).
+  __device__ static void run_consumer(const Args& p, const lds_char* ring, const Meta& mt,
+                                      const Range& rg) {
+    int ec = 0;
+    int s = 0;
+    int seg_item = rg.beg, seg_chunk = -1;
+    f32x16_t acc[FM][FN];
+    for (int item = rg.beg; item < rg.end; item += rg.stride) {
+      const Work w = decode(p, mt, item, ec);
+      if (seg_chunk < 0) {
+        seg_item = item;
+        seg_chunk = w.chunk;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      }
+      for (int kt = 0; kt < w.nk; ++kt, ++s) {
+        block_barrier();
+        compute(ring + (s % kStages) * STAGE, acc);
+      }
+      const bool last_chunk = w.chunk == w.chunks - 1;
+      if (rg.stride != 1 || last_chunk || item + 1 >= rg.end) {
+        int pslot = -1;
+        if (w.chunks > 1 && !(seg_chunk == 0 && last_chunk))
+          pslot = 2 * rg.lin + (seg_item == rg.beg ? 0 : 1);
+        epilogue(p, w, pslot, acc);
+        seg_chunk = -1;
+      }
+    }
+  }
+
+  __device__ static void run(const Args& p, lds_char* ring, Meta& mt) {
+    const int total = build_meta(p, mt, (long long*)(char*)ring);
+    const Range rg = item_range<Cfg<V>::contig>(total);
+    if (rg.beg >= rg.end) return;
+    if ((int)(threadIdx.x >> 6) >= kConsumers)
+      run_producer(p, ring, mt, rg);
+    else
+      run_consumer(p, ring, mt, rg);
+  }
 };
 
 template <int V>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
-  using G = Gemm<V, Cfg<V>::BM, Cfg<V>::BN, Cfg<V>::STAGES>;
-  static_assert(Cfg<V>::STAGES == 4, "the ring below declares four stage buffers");
-  // Stage buffers as distinct LDS objects (see Gemm::step).
-  __shared__ __align__(16) char stage0[G::STAGE];
-  __shared__ __align__(16) char stage1[G::STAGE];
-  __shared__ __align__(16) char stage2[G::STAGE];
-  __shared__ __align__(16) char stage3[G::STAGE];
-  lds_char* const st[4] = {(lds_char*)stage0, (lds_char*)stage1, (lds_char*)stage2,
-                           (lds_char*)stage3};
-  G::run(p, st);
+  using G = Gemm<V>;
+  __shared__ __align__(1024) char ring[G::RING];
+  __shared__ Meta meta;
+  static_assert(G::RING + sizeof(Meta) <= 160 * 1024, "LDS budget of a gfx950 CU");
+  G::run(p, (lds_char*)ring, meta);
 }
 
-// Sums the K-chunk partials of every split (expert, tile) in chunk order and
-// stores the bf16 result. One workgroup per output tile; tiles of experts that
-// were not split exit at once (their GEMM item stored bf16 directly).
+// Finds the expert owning tile `id` in the concatenation of per-expert tile
+// ranges (a block scan over experts), the exclusive prefix of work items
+// before that expert, and the total number of work items. Returns false
+// when id is past the end.
 template <int V>
-__global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(Args p) {
-  constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN;
-  using G = Gemm<V, BM, BN, Cfg<V>::STAGES>;
-  __shared__ long long scratch[16];
-  const int g = gridDim.x, b = blockIdx.x;
-  const int id = (b % 8) * (g / 8) + b / 8;
-  int e, tile, split_pre, chunks;
-  if (!G::template locate<1>(p, id, scratch, e, tile, split_pre, chunks)) return;
-  if (chunks <= 1) return;
-  int mt_dim, nt_dim;
-  Traits<V>::tile_dims(p, e, mt_dim, nt_dim);
-  const int n_tiles = cdiv(nt_dim, BN);
-  const int m0 = (tile / n_tiles) * BM, n0 = (tile % n_tiles) * BN;
-  const Prob q = Traits<V>::prob(p, e);
-  const float* base = p.partial + (int64_t)(split_pre + tile * chunks) * (BM * BN);
-  for (int idx = threadIdx.x * 4; idx < BM * BN; idx += kThreads * 4) {
-    const int ml = idx / BN, nl = idx % BN;
-    const int m = m0 + ml, n = n0 + nl;
-    if (m >= q.M || n >= q.N) continue;
-    float4 acc = *reinterpret_cast<const float4*>(base + idx);
-    for (int c = 1; c < chunks; ++c) {
-      const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)c * (BM * BN) + idx);
-      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+__device__ bool locate_tile(const Args& p, int id, long long* scan, int* sh, int& e_out,
+                            int& tile_out, int& ipre_out, int& chunks_out, int& total_out) {
+  if (threadIdx.x == 0) sh[0] = -1;
+  long long base = 0;  // (tiles << 32) | items
+  for (int e0 = 0; e0 < p.E; e0 += kRedThreads) {
+    const int e = e0 + threadIdx.x;
+    int tiles = 0, chunks = 1;
+    if (e < p.E) expert_work<V>(p, Traits<V>::prob(p, rec_global(p, e)), tiles, chunks);
+    const long long packed = ((long long)tiles << 32) | (long long)(tiles * chunks);
+    long long total;
+    const long long ex = block_exclusive_scan<long long, kRedThreads>(packed, scan, &total);
+    const long long pre = base + ex;
+    const int t_pre = (int)(pre >> 32), i_pre = (int)(pre & 0xFFFFFFFFll);
+    if (tiles > 0 && id >= t_pre && id < t_pre + tiles) {
+      sh[0] = e;
+      sh[1] = id - t_pre;
+      sh[2] = i_pre;
+      sh[3] = chunks;
     }
-    *reinterpret_cast<uint2*>(p.c + (q.cr + m) * p.ldc + q.cc + n) =
-        make_uint2(pack_bf16(acc.x, acc.y), pack_bf16(acc.z, acc.w));
+    base += total;
+    __syncthreads();
+  }
+  e_out = __builtin_amdgcn_readfirstlane(sh[0]);
+  tile_out = __builtin_amdgcn_readfirstlane(sh[1]);
+  ipre_out = __builtin_amdgcn_readfirstlane(sh[2]);
+  chunks_out = __builtin_amdgcn_readfirstlane(sh[3]);
+  total_out = (int)(base & 0xFFFFFFFFll);
+  return e_out >= 0;
+}
+
+// Split-K reduction of the contig GEMMs. A tile whose K chunks (items
+// [a, a + chunks)) were all done by one workgroup was stored directly; any
+// other tile has one partial segment per workgroup range it touches, in
+// slot 2L (the segment starts its range L) or 2L + 1 (it starts inside L).
+// This kernel sums the segments in chunk order and rounds once. Workgroup
+// (x, y) handles rows [16y, 16y + 16) of tile x.
+template <int V>
+__global__ __launch_bounds__(kRedThreads) void splitk_reduce_kernel(Args p) {
+  constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN, RB = 16;
+  constexpr int VEC = RB * BN / 4 / kRedThreads;  // float4 per thread
+  static_assert(VEC * kRedThreads * 4 == RB * BN, "row block must split evenly");
+  __shared__ long long scan[16];
+  __shared__ int sh[4];
+  int e, tile, ipre, chunks, total;
+  if (!locate_tile<V>(p, blockIdx.x, scan, sh, e, tile, ipre, chunks, total)) return;
+  if (chunks <= 1) return;
+  const int G = p.grid;
+  const int a = ipre + tile * chunks;
+  int L = (int)min<int64_t>(G - 1, (int64_t)a * G / total);
+  while (L + 1 < G && contig_begin(total, L + 1, G) <= a) ++L;
+  while (L > 0 && contig_begin(total, L, G) > a) --L;
+  if (contig_begin(total, L + 1, G) >= a + chunks) return;  // one range: stored directly
+  const Prob q = Traits<V>::prob(p, rec_global(p, e));
+  const int n_tiles = cdiv(q.N, BN);
+  const int m0 = (tile / n_tiles) * BM + blockIdx.y * RB, n0 = (tile % n_tiles) * BN;
+  float4 acc[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int row_off = blockIdx.y * RB * BN;
+  auto add_slot = [&](int slot) {
+    const float* src = p.partial + (int64_t)slot * (BM * BN) + row_off;
+    float4 v[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i)
+      v[i] = *reinterpret_cast<const float4*>(src + (threadIdx.x + i * kRedThreads) * 4);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      acc[i].x += v[i].x; acc[i].y += v[i].y; acc[i].z += v[i].z; acc[i].w += v[i].w;
+    }
+  };
+  add_slot(2 * L + (contig_begin(total, L, G) == a ? 0 : 1));
+  for (int l = L + 1; l < G; ++l) {
+    const int b0 = contig_begin(total, l, G);
+    if (b0 >= a + chunks) break;
+    if (contig_begin(total, l + 1, G) == b0) continue;  // empty range
+    add_slot(2 * l);
+  }
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const int idx = (threadIdx.x + i * kRedThreads) * 4;
+    const int m = m0 + idx / BN, n = n0 + idx % BN;
+    if (m >= q.M || n >= q.N) continue;
+    *reinterpret_cast<uint2*>(p.c + ((int64_t)q.cr + m) * p.ldc + q.cc + n) =
+        make_uint2(pack_bf16(acc[i].x, acc[i].y), pack_bf16(acc[i].z, acc[i].w));
   }
 }
 
@@ -739,35 +927,34 @@ int cu_count() {
   return cache[dev];
 }
 
-// Split-K plan of a dW GEMM: K rows per work item, and the partial-tile
-// capacity it can need. The chunk keeps a work item near a quarter of one
-// CU's share of the whole dW (tiles_max * rows_bound row-tiles), so one
-// heavily loaded expert is spread over many CUs; it never drops below 1024
-// rows, so lightly loaded layers do not pay for partials.
-struct SplitPlan {
-  int kc;
-  int64_t slots;  // partial tiles
-};
+// Split-K chunk of the dW GEMMs: K rows per work item. Small chunks let the
+// contiguous item ranges balance experts of very different row counts; the
+// chunks of one tile inside one range accumulate in registers, so the chunk
+// size does not change the partial traffic (at most two partial tiles per
+// workgroup).
+constexpr int kDwChunk = 256;
 
-SplitPlan split_plan(int64_t tiles_max, int64_t rows_bound) {
-  const int64_t cus = cu_count();
-  int64_t kc = (tiles_max * rows_bound) / (4 * cus);
-  kc = std::max<int64_t>(1024, (kc + kBK - 1) / kBK * kBK);
-  kc = std::min<int64_t>(kc, 1 << 30);
-  SplitPlan sp;
-  sp.kc = (int)kc;
-  sp.slots = tiles_max * (2 * ((rows_bound + kc - 1) / kc) + 1);
-  return sp;
+// Persistent grid: one workgroup per CU (the LDS ring and tables fill a CU),
+// never more than there are work items; a multiple of 8 so every XCD gets
+// the same number of workgroups.
+int gemm_grid(int64_t items_bound) {
+  const int64_t cus = std::max(8, cu_count() / 8 * 8);
+  return (int)std::min<int64_t>(cus, (items_bound + 7) / 8 * 8);
 }
 
 template <int V>
-int launch(const Args& p, int64_t grid_items, hipStream_t s) {
-  if (grid_items <= 0) return VMOE_OK;
-  int64_t g = (grid_items + 7) / 8 * 8;
-  if (g > INT32_MAX) return VMOE_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(grouped_gemm_kernel<V>, dim3((unsigned)g), dim3(kThreads), 0, s, p);
+int launch(Args p, int64_t items_bound, hipStream_t s) {
+  if (items_bound <= 0) return VMOE_OK;
+  p.grid = gemm_grid(items_bound);
+  hipLaunchKernelGGL(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
+}
+
+// Partial-tile workspace of a split dW launch: two tiles per workgroup.
+template <int V>
+size_t dw_workspace(int grid) {
+  return (size_t)2 * grid * Cfg<V>::BM * Cfg<V>::BN * sizeof(float);
 }
 
 template <int V>
@@ -783,28 +970,30 @@ int64_t row_items(int64_t rows_bound, int E, int64_t nmax) {
          ((nmax + Cfg<V>::BN - 1) / Cfg<V>::BN);
 }
 
-// dW GEMM with split-K: GEMM items, then the chunk reduction.
+// dW GEMM with split-K: GEMM items, then the segment reduction.
 template <int V>
 int launch_dw(Args p, int64_t tmax, void* ws, size_t ws_bytes, hipStream_t s) {
-  constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN;
+  constexpr int BM = Cfg<V>::BM;
   const int64_t E = p.E;
-  if (ws) {
-    const SplitPlan sp = split_plan(tmax, p.rows_bound);
-    if (ws_bytes < (size_t)sp.slots * BM * BN * sizeof(float)) return VMOE_ERR_WORKSPACE;
-    p.kc = sp.kc;
-    p.partial = reinterpret_cast<float*>(ws);
-    const int64_t items = tmax * (E + p.rows_bound / sp.kc + 1);
-    int st = launch<V>(p, items, s);
-    if (st) return st;
-    int64_t g = (E * tmax + 7) / 8 * 8;
-    if (g > INT32_MAX) return VMOE_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((splitk_reduce_kernel<V>), dim3((unsigned)g), dim3(kThreads), 0, s, p);
-    VMOE_CHECK_LAUNCH();
-    return VMOE_OK;
+  if (!ws) {
+    p.kc = 0;
+    p.partial = nullptr;
+    return launch<V>(p, E * tmax, s);
   }
-  p.kc = 0;
-  p.partial = nullptr;
-  return launch<V>(p, E * tmax, s);
+  // sum_e tiles_e * ceil(K_e / kc) <= tmax * (rows_bound / kc + E)
+  const int64_t items = tmax * (E + p.rows_bound / kDwChunk + 1);
+  if (items <= 0) return VMOE_OK;
+  if (items > INT32_MAX || E * tmax > INT32_MAX) return VMOE_ERR_UNSUPPORTED;
+  p.kc = kDwChunk;
+  p.grid = gemm_grid(items);
+  if (ws_bytes < dw_workspace<V>(p.grid)) return VMOE_ERR_WORKSPACE;
+  p.partial = reinterpret_cast<float*>(ws);
+  hipLaunchKernelGGL(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
+  VMOE_CHECK_LAUNCH();
+  hipLaunchKernelGGL((splitk_reduce_kernel<V>), dim3((unsigned)(E * tmax), BM / 16),
+                     dim3(kRedThreads), 0, s, p);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
 }
 
 // Shared argument checks. Every dimension the kernels vectorise over must be a
@@ -815,6 +1004,7 @@ inline int check_common(const int32_t* eto, const int32_t* ewo, const int32_t* w
   if (!eto || !ewo || !widths || !tpe || E <= 0 || hidden <= 0 || max_width < 0 ||
       rows_bound < 0)
     return VMOE_ERR_INVALID_ARG;
+  if (E > kMaxExperts) return VMOE_ERR_UNSUPPORTED;
   if (hidden % 8 != 0 || max_width % 8 != 0 || hidden > INT32_MAX / 2 ||
       rows_bound > INT32_MAX)
     return VMOE_ERR_UNSUPPORTED;
@@ -922,11 +1112,8 @@ extern "C" int vmoe_gemm_up_bwd_dx(const uint16_t* grad_act, int64_t ldg, const 
 extern "C" size_t vmoe_gemm_dw_workspace_bytes(int32_t E, int64_t hidden, int64_t max_width,
                                                int64_t rows_bound) {
   if (E <= 0 || hidden <= 0 || max_width <= 0 || rows_bound <= 0) return 0;
-  const SplitPlan a = split_plan(tiles_max<UP_DW>(hidden, max_width), rows_bound);
-  const SplitPlan b = split_plan(tiles_max<DOWN_DW>(max_width, hidden), rows_bound);
-  const size_t tile_a = (size_t)Cfg<UP_DW>::BM * Cfg<UP_DW>::BN * sizeof(float);
-  const size_t tile_b = (size_t)Cfg<DOWN_DW>::BM * Cfg<DOWN_DW>::BN * sizeof(float);
-  return std::max((size_t)a.slots * tile_a, (size_t)b.slots * tile_b);
+  const int grid = gemm_grid(INT32_MAX);
+  return std::max(dw_workspace<UP_DW>(grid), dw_workspace<DOWN_DW>(grid));
 }
 
 extern "C" int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
