@@ -54,7 +54,60 @@ def parse():
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--profile-steps", type=int, default=0,
                     help="only run this many steps (for rocprofv3), print nothing else")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy a 1 GiB device buffer 5 times: the known-size kernel that "
+                         "scales the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
+
+
+# Kernel symbol of each GEMM op (grouped_gemm_kernel<Variant>).
+GEMM_SYMBOL = {
+    "gemm_up_fwd": "grouped_gemm_kernel<0>",
+    "gemm_down_fwd": "grouped_gemm_kernel<1>",
+    "gemm_up_bwd_dx": "grouped_gemm_kernel<2>",
+    "gemm_up_bwd_dw": "grouped_gemm_kernel<3>",
+    "gemm_down_bwd_dh_ga": "grouped_gemm_kernel<4>",
+    "gemm_down_bwd_dw": "grouped_gemm_kernel<5>",
+}
+
+
+def gemm_bytes(op, A, d, nw, W):
+    """Minimal unique HBM bytes of one GEMM launch (bf16): its operands read
+    once and its outputs written once. A = routed rows, nw = sum_e n_e w_e,
+    W = total expert width."""
+    rows_d, inter, weights = 2 * A * d, 2 * nw, 2 * d * W
+    return {
+        "gemm_up_fwd": rows_d + weights + 2 * inter,          # Xg, W1 -> H, PRE
+        "gemm_down_fwd": inter + weights + rows_d,            # H, W2 -> Y
+        "gemm_down_bwd_dh_ga": rows_d + weights + 2 * inter,  # GY, W2, PRE -> GA
+        "gemm_up_bwd_dx": inter + weights + rows_d,           # GA, W1 -> GXg
+        "gemm_up_bwd_dw": rows_d + inter + weights,           # x[gm], GA -> GW1
+        "gemm_down_bwd_dw": inter + rows_d + weights,         # H, GY -> GW2
+    }[op]
+
+
+def measured_traffic(config, symbol):
+    """HBM bytes per launch of `symbol` from the committed rocprofv3 counter
+    summary (profiles/hbm_traffic_<config>.json), or None."""
+    path = REPO / "profiles" / f"hbm_traffic_{config}.json"
+    try:
+        data = json.loads(path.read_text())
+        k = data["kernels"][symbol]
+        return int(k["fetch_bytes"] + k["write_bytes"])
+    except (OSError, KeyError, ValueError, TypeError):
+        return None
+
+
+def copy_calibration():
+    import torch
+
+    n = 1 << 30
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 5}))
 
 
 def build_workload(name, device):
@@ -278,6 +331,9 @@ def main():
         print(json.dumps({"error": "no ROCm GPU visible"}))
         sys.exit(1)
     device = torch.device("cuda:0")
+    if args.copy_calibration:
+        copy_calibration()
+        return
     torch.manual_seed(0)
     m, xb, info = build_workload(args.config, device)
     flops, counts, sel = gemm_flops(m, xb)
@@ -300,6 +356,11 @@ def main():
     d, sizes, k, T, _ = CONFIGS[args.config]
     A = T * k
     E = m.num_experts
+    widths = [w for c, w in sizes for _ in range(c)]
+    nw = sum(int(n) * w for n, w in zip(counts, widths))
+    dom_bytes = gemm_bytes(dom, A, d, nw, sum(widths))
+    ai = per_gemm_flops / dom_bytes
+    ai_bound = min(PEAK_BF16_TFLOPS, ai * PEAK_HBM_GBS / 1e3)
     perm_bytes = {
         "gather": 2 * T * d + 2 * A * d + 8 * A,
         "combine": 2 * A * d + 2 * A + 2 * T * d + 8 * A,
@@ -335,7 +396,12 @@ def main():
         "kernel_us": {n: round(v, 2) for n, v in kern.items()},
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic(args.config, GEMM_SYMBOL[dom]),
+                     "algorithmic_bytes": dom_bytes,
+                     "ai_flop_per_byte": round(ai, 1),
+                     "ai_bound_tflops": round(ai_bound, 1),
+                     "frac_of_ai_bound": round(achieved / ai_bound, 4)},
     }
     if not args.no_cpu_baseline:
         sec, threads = cpu_baseline(m, xb, sel, args.cpu_iters)
