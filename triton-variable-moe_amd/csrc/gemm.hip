@@ -52,6 +52,8 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) char lds_char;
 typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4;
 typedef __attribute__((address_space(3))) bf16x8_t lds_bf16x8;
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // Workgroup roles: consumer waves (two per SIMD, so one hides the other's
 // LDS latency) read the staged tiles, run the MFMAs and store the results;
@@ -131,6 +133,7 @@ struct Traits;
 
 template <>
 struct Traits<UP_FWD> {
+  static constexpr bool k_map = true;  // A rows may come through the gather map
   static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = false;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
@@ -147,6 +150,7 @@ struct Traits<UP_FWD> {
 
 template <>
 struct Traits<DOWN_FWD> {
+  static constexpr bool k_map = false;
   static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = false;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
@@ -163,6 +167,7 @@ struct Traits<DOWN_FWD> {
 
 template <>
 struct Traits<UP_DX> {
+  static constexpr bool k_map = false;
   static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = true;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
@@ -179,6 +184,7 @@ struct Traits<UP_DX> {
 
 template <>
 struct Traits<UP_DW> {
+  static constexpr bool k_map = false;
   static constexpr bool a_k = false, b_k = false;
   static constexpr bool t_map = true;  // A rows may come through the gather map
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
@@ -195,6 +201,7 @@ struct Traits<UP_DW> {
 
 template <>
 struct Traits<DOWN_DH> {
+  static constexpr bool k_map = false;
   static constexpr bool t_map = false;
   static constexpr bool a_k = true, b_k = true;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
@@ -211,6 +218,7 @@ struct Traits<DOWN_DH> {
 
 template <>
 struct Traits<DOWN_DW> {
+  static constexpr bool k_map = false;
   static constexpr bool t_map = false;
   static constexpr bool a_k = false, b_k = false;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
@@ -272,26 +280,48 @@ __device__ __forceinline__ void block_barrier() {
 // num_records) reads zeros, which is how every masked lane is handled.
 constexpr uint32_t kOob = 0x80000000u;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
+                                                          int bytes = 0x7FFFFFFF) {
   // The base is block-uniform; readfirstlane keeps the resource in SGPRs
   // (a VGPR resource would force a waterfall loop around every DMA).
   const uint64_t a = reinterpret_cast<uint64_t>(base);
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
   void* b = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(b, 0, 0x7FFFFFFF, 0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc(b, 0, __builtin_amdgcn_readfirstlane(bytes),
+                                           0x00020000);
+}
+
+// Row-map entries for the producers come through the scalar cache: a load
+// from the constant address space at a uniform index compiles to s_load,
+// which completes on lgkmcnt, not vmcnt, so waiting for it never drains the
+// in-flight DMAs. The compiler tracks these loads itself. Callers clamp the
+// index into the rows the item owns, so every load stays inside the map.
+__device__ __forceinline__ int32_t sload_map(const int32_t* map, int idx) {
+  typedef __attribute__((address_space(4))) const int32_t cint;
+  return ((cint*)map)[__builtin_amdgcn_readfirstlane(idx)];
+}
+
+// v[idx] for a lane-varying idx over uniform (scalar) values.
+template <int N>
+__device__ __forceinline__ int32_t pick(const int32_t (&v)[N], int idx) {
+  int32_t r = v[0];
+#pragma unroll
+  for (int t = 1; t < N; ++t) r = idx == t ? v[t] : r;
+  return r;
 }
 
 // 16-byte DMA of the lane's source into LDS at dst + 16 * lane
 // (buffer_load_dwordx4 ... lds, LDS base in M0). Issued as inline asm so the
 // compiler does not track it: it would otherwise wait for every DMA before
 // any LDS read it cannot prove disjoint, which empties the ring. The kernels
-// order DMA completion themselves with wait_vmcnt + block_barrier, and
-// nothing else in them uses M0.
+// order DMA completion themselves with wait_vmcnt + block_barrier. The asm
+// has no register outputs (the data goes to LDS), so no register is written
+// behind the compiler's back; M0 is declared clobbered.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, lds_char* dst) {
   const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(dst));
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :: "v"(voff), "s"(r), "s"(lds) : "memory");
+               :: "v"(voff), "s"(r), "s"(lds) : "memory", "m0");
 }
 
 // Per-expert tables of a launch, built once per workgroup: the exclusive
@@ -376,13 +406,20 @@ struct Gemm {
   template <int PW>
   struct Src {
     __amdgpu_buffer_rsrc_t rsrc;
-    const int32_t* map;  // T-form row gather (nullable)
-    int map_rows;
-    int r0;              // T-form with map: source row of k = 0
     uint32_t ld2;        // leading dimension in bytes
     uint32_t off[PW];    // K-form: row + chunk; T-form: chunk column (+ k-row without map)
     int idx[PW];         // K-form: k of the lane's chunk; T-form: the lane's k-row
     bool ok[PW];         // K-form: row valid; T-form: column valid
+  };
+  // T-form row gather (the A operand of the up dW GEMM): the map entries of
+  // the item's k range, and those of the next stage's k-rows, loaded a stage
+  // ahead.
+  struct TMap {
+    const int32_t* base;  // map entry of the item's first k-row
+    int klen;             // k-rows of the item
+    int32_t nxt[8];       // entries of this wave's k-rows of the next stage
+    int rows;             // rows of the gathered source
+    bool on;
   };
 
   // K-form setup: rows [0, R) of the tile (source rows r0 + row, or
@@ -393,19 +430,24 @@ struct Gemm {
                                  int rows_valid) {
     const int lane = threadIdx.x & 63, wave = pwave();
     // Without a map, rebase to the tile's first row so offsets stay small.
+    if (!T::k_map) map = nullptr;
     const uint16_t* b = map ? base + c0 : base + r0 * ld + c0;
     s.rsrc = make_rsrc(b);
-    s.map = nullptr;
     s.ld2 = (uint32_t)(ld * 2);
+    const int last = max(0, min(rows_valid, R) - 1);  // clamp: entries the tile owns
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const int row = (wave * PW + i) * 16 + (lane >> 2);
       const int c = (lane & 3) ^ kswz(row);
       bool ok = row < rows_valid;
       int64_t srow = row;
-      if (ok && map) {
-        srow = map[r0 + row];
-        ok = srow >= 0 && srow < map_rows;
+      if (T::k_map && map) {
+        // This wave's 16 rows of instruction i, one scalar load each.
+        int32_t mv[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) mv[t] = sload_map(map + r0, min((wave * PW + i) * 16 + t, last));
+        srow = pick<16>(mv, lane >> 2);
+        ok = ok && srow >= 0 && srow < map_rows;
       }
       s.ok[i] = ok;
       s.idx[i] = c * 8;
@@ -427,17 +469,26 @@ struct Gemm {
   // T-form setup: columns [0, R) of the tile starting at source column c0,
   // cols_valid of them real; source rows r0 + k, or map[r0 + k].
   template <int R, int PW>
-  __device__ static void setup_t(Src<PW>& s, const uint16_t* base, int64_t ld,
+  __device__ static void setup_t(Src<PW>& s, TMap& tm, const uint16_t* base, int64_t ld,
                                  const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
-                                 int cols_valid) {
+                                 int cols_valid, int k_valid) {
     constexpr int LPR = Dma<R>::LPR, RPI = Dma<R>::RPI;
     const int lane = threadIdx.x & 63, wave = pwave();
+    if (!T::t_map) map = nullptr;
     const uint16_t* b = map ? base + c0 : base + r0 * ld + c0;
     s.rsrc = make_rsrc(b);
-    s.map = map;
-    s.map_rows = (int)map_rows;
-    s.r0 = (int)r0;
     s.ld2 = (uint32_t)(ld * 2);
+    tm.on = T::t_map && map;
+    if (T::t_map && map) {
+      // This wave's PW * RPI consecutive k-rows per stage, loaded a stage
+      // ahead (the first stage's here), indices clamped to the item's rows.
+      static_assert(!T::t_map || PW * RPI == 8, "map prefetch assumes 8 k-rows per wave");
+      tm.rows = (int)map_rows;
+      tm.base = map + r0;
+      tm.klen = max(1, k_valid);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) tm.nxt[t] = sload_map(tm.base, min(wave * 8 + t, tm.klen - 1));
+    }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const int krow = (wave * PW + i) * RPI + lane / LPR;
@@ -449,21 +500,32 @@ struct Gemm {
   }
 
   template <int R, int PW>
-  __device__ static void issue_t(const Src<PW>& s, int k0, int K, lds_char* stage) {
-    const int wave = pwave();
+  __device__ static void issue_t(const Src<PW>& s, TMap& tm, int k0, int K, lds_char* stage) {
+    constexpr int LPR = Dma<R>::LPR, RPI = Dma<R>::RPI;
+    const int wave = pwave(), lane = threadIdx.x & 63;
+    int32_t cur[8];
+    if (T::t_map && tm.on) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) cur[t] = tm.nxt[t];
+    }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const int k = k0 + s.idx[i];
       bool v = s.ok[i] && k < K;
       uint32_t off;
-      if (T::t_map && s.map) {
-        int64_t row = v ? (int64_t)s.map[s.r0 + k] : -1;
-        v = v && row >= 0 && row < s.map_rows;
+      if (T::t_map && tm.on) {
+        const int64_t row = pick<8>(cur, i * RPI + lane / LPR);
+        v = v && row >= 0 && row < tm.rows;
         off = v ? s.off[i] + (uint32_t)row * s.ld2 : kOob;
       } else {
         off = v ? s.off[i] + (uint32_t)k0 * s.ld2 : kOob;
       }
       dma16(s.rsrc, off, stage + (wave * PW + i) * 1024);
+    }
+    if (T::t_map && tm.on && k0 + BK < K) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        tm.nxt[t] = sload_map(tm.base, min(k0 + BK + wave * 8 + t, tm.klen - 1));
     }
   }
 
@@ -575,24 +637,34 @@ struct Gemm {
     return w;
   }
 
-  __device__ static void setup(const Args& p, const Work& w, Src<PWA>& sa, Src<PWB>& sb) {
+  __device__ static void setup(const Args& p, const Work& w, Src<PWA>& sa, Src<PWB>& sb,
+                               TMap& tm) {
     const Prob& q = w.q;
     if (T::a_k)
       setup_k<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.m0, q.ac + w.kbeg, q.M - w.m0);
     else
-      setup_t<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.kbeg, q.ac + w.m0, q.M - w.m0);
+      setup_t<BM>(sa, tm, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.kbeg, q.ac + w.m0, q.M - w.m0,
+                  w.klen);
     if (T::b_k)
       setup_k<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg, q.N - w.n0);
     else
-      setup_t<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + w.kbeg, q.bc + w.n0, q.N - w.n0);
+    {
+      TMap none;  // B is never gathered
+      setup_t<BN>(sb, none, p.b, p.ldb, nullptr, 0, q.br + w.kbeg, q.bc + w.n0, q.N - w.n0,
+                  w.klen);
+    }
   }
 
-  __device__ static void issue(const Work& w, const Src<PWA>& sa, const Src<PWB>& sb, int kt,
-                               lds_char* st) {
+  __device__ static void issue(const Work& w, const Src<PWA>& sa, const Src<PWB>& sb,
+                               TMap& tm, int kt, lds_char* st) {
     const int k0 = kt * BK;
-    if (T::a_k) issue_k<BM>(sa, k0, w.klen, st); else issue_t<BM>(sa, k0, w.klen, st);
+    if (T::a_k) issue_k<BM>(sa, k0, w.klen, st); else issue_t<BM>(sa, tm, k0, w.klen, st);
     if (T::b_k) issue_k<BN>(sb, k0, w.klen, st + A_STAGE);
-    else issue_t<BN>(sb, k0, w.klen, st + A_STAGE);
+    else {
+      TMap none;
+      none.on = false;
+      issue_t<BN>(sb, none, k0, w.klen, st + A_STAGE);
+    }
   }
 
   // Multiplies one staged k-tile into the wave's accumulators.
@@ -621,64 +693,116 @@ struct Gemm {
 
   // Epilogue. acc[i][j][4*g + r] sits at m = wm*WM + i*32 + (lane & 31),
   // n = wn*WN + j*32 + 8*g + 4*(lane >> 5) + r.
-  // `slot` >= 0: the accumulators are a partial sum over some of the tile's
-  // K chunks; the whole fp32 tile goes to that partial slot and the reduce
+  // Epilogue staging: each consumer wave turns one 32x64 accumulator block
+  // into bf16 in a private 4 KiB LDS scratch and reads it back as 128-byte
+  // row segments, so a store instruction writes 8 whole cache lines (the
+  // accumulator layout alone gives 8 bytes per lane over 32 rows). Row r
+  // holds its 16 8-byte half-chunks hc at position hc ^ ((r >> 1) & 15): the
+  // 32 lanes of one write phase (32 rows, same half-chunk) then hit 32
+  // distinct bank pairs, and a 16-lane read phase covers two whole rows.
+  static constexpr int EPI_BYTES = 32 * 64 * 2;
+  static_assert(WN == 64 && FN == 2, "epilogue staging assumes 64-column wave tiles");
+
+  __device__ static int epi_off(int r, int hc) { return r * 128 + ((hc ^ ((r >> 1) & 15)) << 3); }
+
+  // Block i of the accumulators, mapped through f, rounded to bf16 into the
+  // wave's scratch: lane (r = lane & 31, h = lane >> 5) holds for each (j, g)
+  // the 4 values at columns 32j + 8g + 4h .. +3 of row r.
+  template <class F>
+  __device__ static void epi_write(lds_char* scr, const f32x16_t (&acc)[FM][FN], int i, F f) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const u32x2_t v = {pack_bf16(f(acc[i][j][4 * g]), f(acc[i][j][4 * g + 1])),
+                           pack_bf16(f(acc[i][j][4 * g + 2]), f(acc[i][j][4 * g + 3]))};
+        *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(
+            scr + epi_off(r, 2 * (4 * j + g) + h)) = v;
+      }
+  }
+
+  // Row 8q + (lane >> 3), columns 8 (lane & 7) .. +7 of the scratch block.
+  __device__ static uint4 epi_read(const lds_char* scr, int q) {
+    const int lane = threadIdx.x & 63;
+    const int r = 8 * q + (lane >> 3), c = lane & 7;
+    const int f = (r >> 1) & 15;
+    const u32x4_t v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
+        scr + r * 128 + ((((2 * c) ^ f) >> 1) << 4));
+    // Half-chunks 2c and 2c + 1 sit swapped when f is odd.
+    return (f & 1) ? make_uint4(v.z, v.w, v.x, v.y) : make_uint4(v.x, v.y, v.z, v.w);
+  }
+
+  // `pslot` >= 0: the accumulators are a partial sum over some of the tile's
+  // K chunks; the fp32 tile goes to that partial slot in the accumulator
+  // layout (wave, i, j, g, lane: 1 KiB contiguous per store) and the reduce
   // kernel sums the segments in chunk order and rounds once.
   __device__ static void epilogue(const Args& p, const Work& w, int pslot,
-                                  f32x16_t (&acc)[FM][FN]) {
+                                  f32x16_t (&acc)[FM][FN], lds_char* scr) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
     const Prob& q = w.q;
     if (pslot >= 0) {
-      float* slot = p.partial + (int64_t)pslot * (BM * BN);
+      float* slot = p.partial + (int64_t)pslot * (BM * BN) + wave * (WM * WN);
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int ml = wm * WM + i * 32 + (lane & 31);
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            const int nl = wn * WN + j * 32 + 8 * gq + 4 * (lane >> 5);
-            *reinterpret_cast<float4*>(slot + ml * BN + nl) =
-                make_float4(acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
-                            acc[i][j][4 * gq + 3]);
-          }
-      }
+          for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<float4*>(slot + ((((i * FN + j) * 4 + g) * 64 + lane) << 2)) =
+                make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                            acc[i][j][4 * g + 3]);
       return;
     }
+    const int n = w.n0 + wn * WN + 8 * (lane & 7);
+    const bool n_ok = n < q.N;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int m = w.m0 + wm * WM + i * 32 + (lane & 31);
-      if (m >= q.M) continue;
-      const int64_t roff = ((int64_t)q.cr + m) * p.ldc + q.cc;
+      const int mb = w.m0 + wm * WM + i * 32;
+      if (mb >= q.M) break;
+      // Stores the staged block to `out` (rows mb + 8q + lane / 8).
+      auto flush = [&](uint16_t* out) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const int n = w.n0 + wn * WN + j * 32 + 8 * gq + 4 * (lane >> 5);
-          if (n >= q.N) continue;
-          float v0 = acc[i][j][4 * gq + 0], v1 = acc[i][j][4 * gq + 1];
-          float v2 = acc[i][j][4 * gq + 2], v3 = acc[i][j][4 * gq + 3];
-          if (V == UP_FWD && p.act == VMOE_ACT_RELU_SQUARED) {
-            v0 = fmaxf(v0, 0.0f); v1 = fmaxf(v1, 0.0f);
-            v2 = fmaxf(v2, 0.0f); v3 = fmaxf(v3, 0.0f);
-            if (p.c2)
-              *reinterpret_cast<uint2*>(p.c2 + roff + n) =
-                  make_uint2(pack_bf16(v0, v1), pack_bf16(v2, v3));
-            v0 *= v0; v1 *= v1; v2 *= v2; v3 *= v3;
-          }
-          if (V == DOWN_DH && p.pre) {
-            // GA = bf16(pre > 0 ? 2 * GH * pre : 0), GH the bf16-rounded dH.
-            const uint2 pr = *reinterpret_cast<const uint2*>(p.pre + roff + n);
-            const float p0 = lo_f32(pr.x), p1 = hi_f32(pr.x), p2 = lo_f32(pr.y), p3 = hi_f32(pr.y);
-            v0 = p0 > 0.0f ? bf16_to_f32(f32_to_bf16(v0)) * 2.0f * p0 : 0.0f;
-            v1 = p1 > 0.0f ? bf16_to_f32(f32_to_bf16(v1)) * 2.0f * p1 : 0.0f;
-            v2 = p2 > 0.0f ? bf16_to_f32(f32_to_bf16(v2)) * 2.0f * p2 : 0.0f;
-            v3 = p3 > 0.0f ? bf16_to_f32(f32_to_bf16(v3)) * 2.0f * p3 : 0.0f;
-          }
-          *reinterpret_cast<uint2*>(p.c + roff + n) = make_uint2(pack_bf16(v0, v1), pack_bf16(v2, v3));
+        for (int qq = 0; qq < 4; ++qq) {
+          const uint4 v = epi_read(scr, qq);
+          const int m = mb + 8 * qq + (lane >> 3);
+          if (m < q.M && n_ok)
+            *reinterpret_cast<uint4*>(out + ((int64_t)q.cr + m) * p.ldc + q.cc + n) = v;
         }
+      };
+      if (V == UP_FWD && p.act == VMOE_ACT_RELU_SQUARED) {
+        if (p.c2) {
+          epi_write(scr, acc, i, [](float v) { return fmaxf(v, 0.0f); });
+          flush(p.c2);
+        }
+        epi_write(scr, acc, i, [](float v) { v = fmaxf(v, 0.0f); return v * v; });
+        flush(p.c);
+      } else if (V == DOWN_DH && p.pre) {
+        // GA = bf16(pre > 0 ? 2 * GH * pre : 0), GH the bf16-rounded dH.
+        epi_write(scr, acc, i, [](float v) { return v; });
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const uint4 gh = epi_read(scr, qq);
+          const int m = mb + 8 * qq + (lane >> 3);
+          if (m >= q.M || !n_ok) continue;
+          const int64_t off = ((int64_t)q.cr + m) * p.ldc + q.cc + n;
+          const uint4 pr = *reinterpret_cast<const uint4*>(p.pre + off);
+          const uint32_t gw[4] = {gh.x, gh.y, gh.z, gh.w}, pw[4] = {pr.x, pr.y, pr.z, pr.w};
+          uint32_t o[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float pl = lo_f32(pw[t]), ph = hi_f32(pw[t]);
+            o[t] = pack_bf16(pl > 0.0f ? lo_f32(gw[t]) * 2.0f * pl : 0.0f,
+                             ph > 0.0f ? hi_f32(gw[t]) * 2.0f * ph : 0.0f);
+          }
+          *reinterpret_cast<uint4*>(p.c + off) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+      } else {
+        epi_write(scr, acc, i, [](float v) { return v; });
+        flush(p.c);
       }
     }
   }
@@ -693,7 +817,8 @@ struct Gemm {
     Work wi = decode(p, mt, rg.beg, ei);
     Src<PWA> sa;
     Src<PWB> sb;
-    setup(p, wi, sa, sb);
+    TMap tm;
+    setup(p, wi, sa, sb, tm);
     int ikt = 0, inext = rg.beg + rg.stride;
     int issued = 0;
     auto issue_next = [&](lds_char* st) -> bool {
@@ -701,10 +826,10 @@ struct Gemm {
         if (inext >= rg.end) return false;
         wi = decode(p, mt, inext, ei);
         inext += rg.stride;
-        setup(p, wi, sa, sb);
+        setup(p, wi, sa, sb, tm);
         ikt = 0;
       }
-      issue(wi, sa, sb, ikt, st);
+      issue(wi, sa, sb, tm, ikt, st);
       ++ikt;
       return true;
     };
@@ -738,7 +863,7 @@ struct Gemm {
   // is a partial sum and goes to slot 2 * lin (the range's first segment) or
   // 2 * lin + 1 (its last).
   __device__ static void run_consumer(const Args& p, const lds_char* ring, const Meta& mt,
-                                      const Range& rg) {
+                                      const Range& rg, lds_char* scr) {
     int ec = 0;
     int s = 0;
     int seg_item = rg.beg, seg_chunk = -1;
@@ -764,20 +889,21 @@ struct Gemm {
         int pslot = -1;
         if (w.chunks > 1 && !(seg_chunk == 0 && last_chunk))
           pslot = 2 * rg.lin + (seg_item == rg.beg ? 0 : 1);
-        epilogue(p, w, pslot, acc);
+        epilogue(p, w, pslot, acc, scr);
         seg_chunk = -1;
       }
     }
   }
 
-  __device__ static void run(const Args& p, lds_char* ring, Meta& mt) {
+  __device__ static void run(const Args& p, lds_char* ring, Meta& mt, lds_char* epi) {
     const int total = build_meta(p, mt, (long long*)(char*)ring);
     const Range rg = item_range<Cfg<V>::contig>(total);
     if (rg.beg >= rg.end) return;
-    if ((int)(threadIdx.x >> 6) >= kConsumers)
+    const int wave = threadIdx.x >> 6;
+    if (wave >= kConsumers)
       run_producer(p, ring, mt, rg);
     else
-      run_consumer(p, ring, mt, rg);
+      run_consumer(p, ring, mt, rg, epi + wave * EPI_BYTES);
   }
 };
 
@@ -785,9 +911,11 @@ template <int V>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
   using G = Gemm<V>;
   __shared__ __align__(1024) char ring[G::RING];
+  __shared__ __align__(16) char epi[kConsumers * G::EPI_BYTES];
   __shared__ Meta meta;
-  static_assert(G::RING + sizeof(Meta) <= 160 * 1024, "LDS budget of a gfx950 CU");
-  G::run(p, (lds_char*)ring, meta);
+  static_assert(G::RING + kConsumers * G::EPI_BYTES + sizeof(Meta) <= 160 * 1024,
+                "LDS budget of a gfx950 CU");
+  G::run(p, (lds_char*)ring, meta, (lds_char*)epi);
 }
 
 // Finds the expert owning tile `id` in the concatenation of per-expert tile
@@ -830,52 +958,56 @@ __device__ bool locate_tile(const Args& p, int id, long long* scan, int* sh, int
 // other tile has one partial segment per workgroup range it touches, in
 // slot 2L (the segment starts its range L) or 2L + 1 (it starts inside L).
 // This kernel sums the segments in chunk order and rounds once. Workgroup
-// (x, y) handles rows [16y, 16y + 16) of tile x.
+// (x, y) handles float4s [1024 y, 1024 (y + 1)) of tile x's slots, which
+// hold the accumulator layout of the GEMM's epilogue.
 template <int V>
 __global__ __launch_bounds__(kRedThreads) void splitk_reduce_kernel(Args p) {
-  constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN, RB = 16;
-  constexpr int VEC = RB * BN / 4 / kRedThreads;  // float4 per thread
-  static_assert(VEC * kRedThreads * 4 == RB * BN, "row block must split evenly");
+  using G = Gemm<V>;
+  constexpr int BM = G::BM, BN = G::BN, VEC = 4, PART = VEC * kRedThreads;
+  static_assert((BM * BN / 4) % PART == 0, "slot must split into whole parts");
   __shared__ long long scan[16];
   __shared__ int sh[4];
   int e, tile, ipre, chunks, total;
   if (!locate_tile<V>(p, blockIdx.x, scan, sh, e, tile, ipre, chunks, total)) return;
   if (chunks <= 1) return;
-  const int G = p.grid;
+  const int Gr = p.grid;
   const int a = ipre + tile * chunks;
-  int L = (int)min<int64_t>(G - 1, (int64_t)a * G / total);
-  while (L + 1 < G && contig_begin(total, L + 1, G) <= a) ++L;
-  while (L > 0 && contig_begin(total, L, G) > a) --L;
-  if (contig_begin(total, L + 1, G) >= a + chunks) return;  // one range: stored directly
+  int L = (int)min<int64_t>(Gr - 1, (int64_t)a * Gr / total);
+  while (L + 1 < Gr && contig_begin(total, L + 1, Gr) <= a) ++L;
+  while (L > 0 && contig_begin(total, L, Gr) > a) --L;
+  if (contig_begin(total, L + 1, Gr) >= a + chunks) return;  // one range: stored directly
   const Prob q = Traits<V>::prob(p, rec_global(p, e));
   const int n_tiles = cdiv(q.N, BN);
-  const int m0 = (tile / n_tiles) * BM + blockIdx.y * RB, n0 = (tile % n_tiles) * BN;
+  const int m0 = (tile / n_tiles) * BM, n0 = (tile % n_tiles) * BN;
+  const int f0 = blockIdx.y * PART + threadIdx.x;
   float4 acc[VEC];
 #pragma unroll
   for (int v = 0; v < VEC; ++v) acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
-  const int row_off = blockIdx.y * RB * BN;
   auto add_slot = [&](int slot) {
-    const float* src = p.partial + (int64_t)slot * (BM * BN) + row_off;
+    const float4* src = reinterpret_cast<const float4*>(p.partial + (int64_t)slot * (BM * BN));
     float4 v[VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i)
-      v[i] = *reinterpret_cast<const float4*>(src + (threadIdx.x + i * kRedThreads) * 4);
+    for (int i = 0; i < VEC; ++i) v[i] = src[f0 + i * kRedThreads];
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
       acc[i].x += v[i].x; acc[i].y += v[i].y; acc[i].z += v[i].z; acc[i].w += v[i].w;
     }
   };
-  add_slot(2 * L + (contig_begin(total, L, G) == a ? 0 : 1));
-  for (int l = L + 1; l < G; ++l) {
-    const int b0 = contig_begin(total, l, G);
+  add_slot(2 * L + (contig_begin(total, L, Gr) == a ? 0 : 1));
+  for (int l = L + 1; l < Gr; ++l) {
+    const int b0 = contig_begin(total, l, Gr);
     if (b0 >= a + chunks) break;
-    if (contig_begin(total, l + 1, G) == b0) continue;  // empty range
+    if (contig_begin(total, l + 1, Gr) == b0) continue;  // empty range
     add_slot(2 * l);
   }
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
-    const int idx = (threadIdx.x + i * kRedThreads) * 4;
-    const int m = m0 + idx / BN, n = n0 + idx % BN;
+    // float4 index -> (wave, i, j, g, lane) of the epilogue layout -> (m, n).
+    const int f = f0 + i * kRedThreads;
+    const int wave = f / (G::WM * G::WN / 4), rem = f % (G::WM * G::WN / 4);
+    const int lane = rem & 63, g = (rem >> 6) & 3, jj = (rem >> 8) % G::FN, ii = (rem >> 8) / G::FN;
+    const int m = m0 + (wave / G::WGN) * G::WM + ii * 32 + (lane & 31);
+    const int n = n0 + (wave % G::WGN) * G::WN + jj * 32 + 8 * g + 4 * (lane >> 5);
     if (m >= q.M || n >= q.N) continue;
     *reinterpret_cast<uint2*>(p.c + ((int64_t)q.cr + m) * p.ldc + q.cc + n) =
         make_uint2(pack_bf16(acc[i].x, acc[i].y), pack_bf16(acc[i].z, acc[i].w));
@@ -974,6 +1106,7 @@ int64_t row_items(int64_t rows_bound, int E, int64_t nmax) {
 template <int V>
 int launch_dw(Args p, int64_t tmax, void* ws, size_t ws_bytes, hipStream_t s) {
   constexpr int BM = Cfg<V>::BM;
+  static_assert(BM * Cfg<V>::BN % (16 * kRedThreads) == 0, "reduce parts");
   const int64_t E = p.E;
   if (!ws) {
     p.kc = 0;
@@ -990,7 +1123,8 @@ int launch_dw(Args p, int64_t tmax, void* ws, size_t ws_bytes, hipStream_t s) {
   p.partial = reinterpret_cast<float*>(ws);
   hipLaunchKernelGGL(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
   VMOE_CHECK_LAUNCH();
-  hipLaunchKernelGGL((splitk_reduce_kernel<V>), dim3((unsigned)(E * tmax), BM / 16),
+  hipLaunchKernelGGL((splitk_reduce_kernel<V>),
+                     dim3((unsigned)(E * tmax), BM * Cfg<V>::BN / 4 / (4 * kRedThreads)),
                      dim3(kRedThreads), 0, s, p);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
