@@ -225,8 +225,9 @@ def kernel_breakdown(m, xb, sel, reps):
                   meta.max_width, meta.rows, _lib.stream(x.device))
 
     def dw1_only():
+        # as the module calls it: A = the gathered activations, no row map
         gw = torch.empty_like(w1)
-        _lib.call("vmoe_gemm_up_bwd_dw", x.data_ptr(), x.stride(0), T, r.gather_map.data_ptr(),
+        _lib.call("vmoe_gemm_up_bwd_dw", xg.data_ptr(), xg.stride(0), xg.shape[0], None,
                   ga.data_ptr(), ga.stride(0), gw.data_ptr(), gw.stride(0),
                   *gg._meta_args(meta), d, meta.max_width, meta.rows, ws.data_ptr(), ws.numel(),
                   _lib.stream(x.device))

@@ -434,20 +434,17 @@ struct Gemm {
     const uint16_t* b = map ? base + c0 : base + r0 * ld + c0;
     s.rsrc = make_rsrc(b);
     s.ld2 = (uint32_t)(ld * 2);
-    const int last = max(0, min(rows_valid, R) - 1);  // clamp: entries the tile owns
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const int row = (wave * PW + i) * 16 + (lane >> 2);
       const int c = (lane & 3) ^ kswz(row);
       bool ok = row < rows_valid;
       int64_t srow = row;
-      if (T::k_map && map) {
-        // This wave's 16 rows of instruction i, one scalar load each.
-        int32_t mv[16];
-#pragma unroll
-        for (int t = 0; t < 16; ++t) mv[t] = sload_map(map + r0, min((wave * PW + i) * 16 + t, last));
-        srow = pick<16>(mv, lane >> 2);
-        ok = ok && srow >= 0 && srow < map_rows;
+      if (T::k_map && map && ok) {
+        // One entry per lane, once per item (the K-form rows are fixed for
+        // all of the item's k-tiles).
+        srow = map[r0 + row];
+        ok = srow >= 0 && srow < map_rows;
       }
       s.ok[i] = ok;
       s.idx[i] = c * 8;
@@ -709,8 +706,9 @@ struct Gemm {
   // wave's scratch: lane (r = lane & 31, h = lane >> 5) holds for each (j, g)
   // the 4 values at columns 32j + 8g + 4h .. +3 of row r.
   template <class F>
-  __device__ static void epi_write(lds_char* scr, const f32x16_t (&acc)[FM][FN], int i, F f) {
-    const int lane = threadIdx.x & 63;
+  __device__ static void epi_write(lds_char* scr, const f32x16_t (&acc)[FM][FN], int i, int lane,
+                                   F f) {
+    asm volatile("" : "+v"(lane));  // recompute the offsets per pass (see epilogue)
     const int r = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int j = 0; j < FN; ++j)
@@ -724,8 +722,7 @@ struct Gemm {
   }
 
   // Row 8q + (lane >> 3), columns 8 (lane & 7) .. +7 of the scratch block.
-  __device__ static uint4 epi_read(const lds_char* scr, int q) {
-    const int lane = threadIdx.x & 63;
+  __device__ static uint4 epi_read(const lds_char* scr, int q, int lane) {
     const int r = 8 * q + (lane >> 3), c = lane & 7;
     const int f = (r >> 1) & 15;
     const u32x4_t v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
@@ -740,7 +737,12 @@ struct Gemm {
   // kernel sums the segments in chunk order and rounds once.
   __device__ static void epilogue(const Args& p, const Work& w, int pslot,
                                   f32x16_t (&acc)[FM][FN], lds_char* scr) {
-    const int lane = threadIdx.x & 63;
+    // The lane index is made opaque here so that the epilogue's lane-only
+    // address arithmetic is not hoisted out of the item loop: live across the
+    // MFMA loop it would spill, and the spill reloads (scratch loads) would
+    // make every store pass wait for the previous one (vmcnt counts both).
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
     const int wave = threadIdx.x >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
     const Prob& q = w.q;
@@ -759,33 +761,44 @@ struct Gemm {
     }
     const int n = w.n0 + wn * WN + 8 * (lane & 7);
     const bool n_ok = n < q.N;
+    if (V == UP_FWD && p.act == VMOE_ACT_RELU_SQUARED) {
+      // relu in place: PRE = bf16(relu(z)), H = bf16(relu(z)^2) both read it
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaxf(acc[i][j][r], 0.0f);
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int mb = w.m0 + wm * WM + i * 32;
       if (mb >= q.M) break;
       // Stores the staged block to `out` (rows mb + 8q + lane / 8).
       auto flush = [&](uint16_t* out) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-          const uint4 v = epi_read(scr, qq);
-          const int m = mb + 8 * qq + (lane >> 3);
+          const uint4 v = epi_read(scr, qq, ln);
+          const int m = mb + 8 * qq + (ln >> 3);
           if (m < q.M && n_ok)
             *reinterpret_cast<uint4*>(out + ((int64_t)q.cr + m) * p.ldc + q.cc + n) = v;
         }
       };
       if (V == UP_FWD && p.act == VMOE_ACT_RELU_SQUARED) {
         if (p.c2) {
-          epi_write(scr, acc, i, [](float v) { return fmaxf(v, 0.0f); });
+          epi_write(scr, acc, i, lane, [](float v) { return v; });
           flush(p.c2);
         }
-        epi_write(scr, acc, i, [](float v) { v = fmaxf(v, 0.0f); return v * v; });
+        epi_write(scr, acc, i, lane, [](float v) { return v * v; });
         flush(p.c);
       } else if (V == DOWN_DH && p.pre) {
         // GA = bf16(pre > 0 ? 2 * GH * pre : 0), GH the bf16-rounded dH.
-        epi_write(scr, acc, i, [](float v) { return v; });
+        epi_write(scr, acc, i, lane, [](float v) { return v; });
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-          const uint4 gh = epi_read(scr, qq);
+          const uint4 gh = epi_read(scr, qq, lane);
           const int m = mb + 8 * qq + (lane >> 3);
           if (m >= q.M || !n_ok) continue;
           const int64_t off = ((int64_t)q.cr + m) * p.ldc + q.cc + n;
@@ -801,7 +814,7 @@ struct Gemm {
           *reinterpret_cast<uint4*>(p.c + off) = make_uint4(o[0], o[1], o[2], o[3]);
         }
       } else {
-        epi_write(scr, acc, i, [](float v) { return v; });
+        epi_write(scr, acc, i, lane, [](float v) { return v; });
         flush(p.c);
       }
     }

@@ -444,10 +444,10 @@ class RoutedExpertsOp(torch.autograd.Function):
     """Both grouped GEMMs of the module (up with relu^2, then down) as one
     autograd node, with metadata from the route and no host sync.
 
-    Saves x_flat + gather_map for the up dW GEMM, like the module's call of
-    grouped_gemm_up_autograd (triton_moe/moe.py:214-226), plus H and PRE. Its
-    backward fuses the relu^2 gradient into the dH GEMM's epilogue, so the
-    gradient w.r.t. H is never materialised.
+    Saves the gathered activations (already materialised for the forward) for
+    the up dW GEMM, whose A operand then streams without a row map, plus H and
+    PRE. Its backward fuses the relu^2 gradient into the dH GEMM's epilogue,
+    so the gradient w.r.t. H is never materialised.
     """
 
     @staticmethod
@@ -455,7 +455,7 @@ class RoutedExpertsOp(torch.autograd.Function):
     def forward(ctx, x_gathered, w1, w2, meta, x_flat, gather_map, hidden_size):
         h, pre = up_fwd(x_gathered, w1, meta, _lib.ACT_RELU_SQUARED, True, zero_tails=False)
         y = down_fwd(h, w2, meta, hidden_size)
-        ctx.save_for_backward(x_flat, w1, w2, h, pre, gather_map)
+        ctx.save_for_backward(x_gathered, w1, w2, h, pre)
         ctx.meta = meta
         ctx.hidden_size = hidden_size
         return y
@@ -464,8 +464,8 @@ class RoutedExpertsOp(torch.autograd.Function):
     @custom_bwd(device_type="cuda")
     @once_differentiable
     def backward(ctx, grad_y):
-        x_flat, w1, w2, h, pre, gm = ctx.saved_tensors
+        xg, w1, w2, h, pre = ctx.saved_tensors
         ga, grad_w2 = down_bwd(grad_y, h, w2, ctx.meta, ctx.hidden_size, zero_tails=False,
                                pre=pre)
-        grad_x, grad_w1 = up_bwd_from_ga(ga, x_flat, w1, ctx.meta, ctx.hidden_size, gm)
+        grad_x, grad_w1 = up_bwd_from_ga(ga, xg, w1, ctx.meta, ctx.hidden_size, None)
         return grad_x, grad_w1, grad_w2, None, None, None, None
