@@ -70,6 +70,7 @@ constexpr int kStages = 4;     // LDS ring: kStages - 1 k-tiles in flight
 constexpr int kMaxExperts = 2048;  // per-expert work prefix held in LDS
 constexpr int kRecExperts = 512;   // per-expert metadata also held in LDS up to this E
 constexpr int kRedThreads = 256;   // split-K reduction kernel
+constexpr int kLane = 8;           // dW GEMMs: workgroups of one XCD that share each K chunk
 
 enum Variant { UP_FWD = 0, DOWN_FWD, UP_DX, UP_DW, DOWN_DH, DOWN_DW };
 
@@ -236,9 +237,9 @@ struct Traits<DOWN_DW> {
 // Tile shape: 128x256 output tiles, the 8 consumer waves in a 2 (m) x 4 (n)
 // grid of 64x64 fp32 accumulators each (64 registers, so three waves fit a
 // SIMD). N = 256 covers a whole 256-wide expert in the up projection. The
-// dW GEMMs split their long K (the expert's rows) into chunks and give each
-// workgroup a contiguous run of work items ("contig"), accumulating across
-// the chunks of a tile; the row-tiled GEMMs deal items round-robin.
+// dW GEMMs split their long K (the expert's rows) into chunks and accumulate
+// a tile across consecutive chunks ("contig"); the row-tiled GEMMs deal
+// items round-robin.
 template <int V>
 struct Cfg {
   static constexpr int BM = 128, BN = 256;
@@ -248,8 +249,8 @@ struct Cfg {
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 
-// Work items of expert e: its output tiles times its K chunks (chunks > 1
-// only for the split-K dW GEMMs, p.kc > 0).
+// Output tiles and K chunks of expert e (chunks > 1 only for the split-K dW
+// GEMMs, p.kc > 0).
 template <int V>
 __device__ __forceinline__ void expert_work(const Args& p, const Prob& q, int& tiles,
                                             int& chunks) {
@@ -324,6 +325,16 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, l
                :: "v"(voff), "s"(r), "s"(lds) : "memory", "m0");
 }
 
+// Work items of an expert with `tiles` output tiles and `chunks` K chunks.
+// Row-tiled GEMMs: one item per tile. dW GEMMs: the tiles form groups of
+// kLane and an item is (tile group, chunk); the kLane workgroups of a lane
+// (all on one XCD) each take one tile of the group, so they read the same
+// K chunk of the shared operand at the same time and it comes from HBM once.
+template <int V>
+__host__ __device__ __forceinline__ int work_items(int tiles, int chunks) {
+  return Cfg<V>::contig ? cdiv(tiles, kLane) * chunks : tiles * chunks;
+}
+
 // Per-expert tables of a launch, built once per workgroup: the exclusive
 // prefix of work items (pre[E] = total) and, for E <= kRecExperts, the
 // expert records themselves.
@@ -335,10 +346,14 @@ struct Meta {
 // Work-item range of workgroup b. Round-robin: XCD x (hardware deals
 // workgroup b to XCD b % 8) owns the contiguous range [x * total / 8,
 // (x + 1) * total / 8), so the tiles of one expert share an L2, and its
-// workgroups take every (grid / 8)-th item. Contig: workgroup with linear
-// index L = x * (grid / 8) + b / 8 owns [total * L / grid, total * (L + 1) / grid).
+// workgroups take every (grid / 8)-th item. Contig (grid a multiple of
+// 8 * kLane): the j-th workgroup of XCD x (j = b / 8) is slot j % kLane of
+// lane l = x * (grid / 8 / kLane) + j / kLane; lane l owns items
+// [total * l / NL, total * (l + 1) / NL) of the NL = grid / kLane lanes, and
+// its slot s works on tile kLane * group + s of each. lin = kLane * l + s
+// names the workgroup's split-K partial slots.
 struct Range {
-  int beg, end, stride, lin;
+  int beg, end, stride, lin, slot;
 };
 
 __host__ __device__ inline int contig_begin(int total, int lin, int grid) {
@@ -351,9 +366,14 @@ __device__ __forceinline__ Range item_range(int total) {
   const int xcd = b & 7, per = G >> 3, j = b >> 3;
   Range r;
   r.lin = xcd * per + j;
+  r.slot = 0;
   if (CONTIG) {
-    r.beg = contig_begin(total, r.lin, G);
-    r.end = contig_begin(total, r.lin + 1, G);
+    const int NL = G / kLane;
+    const int lane = xcd * (NL >> 3) + j / kLane;
+    r.slot = j % kLane;
+    r.lin = lane * kLane + r.slot;
+    r.beg = contig_begin(total, lane, NL);
+    r.end = contig_begin(total, lane + 1, NL);
     r.stride = 1;
   } else {
     r.beg = (int)((int64_t)total * xcd / 8) + j;
@@ -565,7 +585,7 @@ struct Gemm {
         }
         int tiles, chunks;
         expert_work<V>(p, T::prob(p, r), tiles, chunks);
-        items = tiles * chunks;
+        items = work_items<V>(tiles, chunks);
       }
       long long total;
       const long long ex = block_exclusive_scan<long long, kThreads>((long long)items, scan, &total);
@@ -580,13 +600,15 @@ struct Gemm {
 
   struct Work {
     int m0, n0, kbeg, klen, nk, chunk, chunks;
+    bool skip;  // contig: the item's tile group has no tile for this slot
     Prob q;
   };
 
   // Work item `item` (ascending across calls with the same cursor): finds its
   // expert with a wave-wide search of the prefix table from the cursor, then
-  // its tile and K chunk. Every field is workgroup-uniform.
-  __device__ static Work decode(const Args& p, const Meta& mt, int item, int& ecur) {
+  // its tile (for contig, that of lane slot `slot`) and K chunk. Every field
+  // is workgroup-uniform.
+  __device__ static Work decode(const Args& p, const Meta& mt, int item, int& ecur, int slot) {
     const int lane = threadIdx.x & 63;
     int e = ecur;
     for (;;) {
@@ -617,7 +639,9 @@ struct Gemm {
     int tiles, chunks;
     expert_work<V>(p, w.q, tiles, chunks);
     const int local = item - __builtin_amdgcn_readfirstlane(mt.pre[e]);
-    const int tile = local / chunks, chunk = local % chunks;
+    const int chunk = local % chunks;
+    const int tile = Cfg<V>::contig ? (local / chunks) * kLane + slot : local / chunks;
+    w.skip = tile >= tiles;
     const int n_tiles = cdiv(w.q.N, BN);
     w.m0 = (tile / n_tiles) * BM;
     w.n0 = (tile % n_tiles) * BN;
@@ -630,7 +654,7 @@ struct Gemm {
       K = min(K, w.kbeg + p.kc);
     }
     w.klen = K - w.kbeg;
-    w.nk = w.klen > 0 ? cdiv(w.klen, BK) : 0;
+    w.nk = w.klen > 0 && !w.skip ? cdiv(w.klen, BK) : 0;
     return w;
   }
 
@@ -690,39 +714,59 @@ struct Gemm {
 
   // Epilogue. acc[i][j][4*g + r] sits at m = wm*WM + i*32 + (lane & 31),
   // n = wn*WN + j*32 + 8*g + 4*(lane >> 5) + r.
-  // Epilogue staging: each consumer wave turns one 32x64 accumulator block
-  // into bf16 in a private 4 KiB LDS scratch and reads it back as 128-byte
-  // row segments, so a store instruction writes 8 whole cache lines (the
-  // accumulator layout alone gives 8 bytes per lane over 32 rows). Row r
-  // holds its 16 8-byte half-chunks hc at position hc ^ ((r >> 1) & 15): the
-  // 32 lanes of one write phase (32 rows, same half-chunk) then hit 32
-  // distinct bank pairs, and a 16-lane read phase covers two whole rows.
+  //
+  // Deferred stores: when a tile's last K chunk is done, each consumer wave
+  // rounds its accumulators to packed bf16 in registers (the "pending"
+  // tile, 32 registers per output) and goes on with the next item; the
+  // pending tile is stored one 32x64 block at a time between the MFMA
+  // k-steps of that next item. The stores of one tile thus overlap the
+  // loads and MFMAs of the next instead of stalling the whole workgroup
+  // (all consumer waves reach a tile end together). Split-K partial tiles
+  // are stored at once in fp32.
+  //
+  // Store staging: a block goes through the wave's private 4 KiB LDS
+  // scratch and is read back as 128-byte row segments, so a store
+  // instruction writes 8 whole cache lines (the accumulator layout alone
+  // gives 8 bytes per lane over 32 rows). Row r holds its 16 8-byte
+  // half-chunks hc at position hc ^ ((r >> 1) & 15): the 32 lanes of one
+  // write phase (32 rows, same half-chunk) then hit 32 distinct bank pairs,
+  // and a 16-lane read phase covers two whole rows.
   static constexpr int EPI_BYTES = 32 * 64 * 2;
-  static_assert(WN == 64 && FN == 2, "epilogue staging assumes 64-column wave tiles");
+  static_assert(WN == 64 && FN == 2 && FM == 2, "epilogue assumes 64x64 wave tiles");
+  // UP_FWD with relu^2 stores PRE and H; every other variant one output.
+  static constexpr int NOUT = V == UP_FWD ? 2 : 1;
+
+  // Pending blocks are units u = out * FM + i (output-major, row block i);
+  // every unit index is a compile-time constant where the block is used, so
+  // the pending tile stays in registers.
+  static constexpr int UNITS = NOUT * FM;
+  struct Pending {
+    uint32_t pk[NOUT][FM][FN][8];  // bf16 pairs of block (i, j): (g, half) -> 2 g + half
+    int mb, nb;                    // first row / column of the wave tile in the problem
+    int M, N, cr, cc;              // the tile's problem extents and output origin
+    int mask;                      // bit u: unit u still to be stored
+  };
 
   __device__ static int epi_off(int r, int hc) { return r * 128 + ((hc ^ ((r >> 1) & 15)) << 3); }
 
-  // Block i of the accumulators, mapped through f, rounded to bf16 into the
-  // wave's scratch: lane (r = lane & 31, h = lane >> 5) holds for each (j, g)
-  // the 4 values at columns 32j + 8g + 4h .. +3 of row r.
-  template <class F>
-  __device__ static void epi_write(lds_char* scr, const f32x16_t (&acc)[FM][FN], int i, int lane,
-                                   F f) {
-    asm volatile("" : "+v"(lane));  // recompute the offsets per pass (see epilogue)
+  // Packed block (out, i) into the wave's scratch: lane (r = lane & 31,
+  // h = lane >> 5) holds for each (j, g) the 4 values at columns
+  // 32j + 8g + 4h .. +3 of row r.
+  template <int OUT, int I>
+  __device__ __forceinline__ static void epi_write(lds_char* scr, const Pending& pd, int lane) {
     const int r = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const u32x2_t v = {pack_bf16(f(acc[i][j][4 * g]), f(acc[i][j][4 * g + 1])),
-                           pack_bf16(f(acc[i][j][4 * g + 2]), f(acc[i][j][4 * g + 3]))};
+        const u32x2_t v = {pd.pk[OUT][I][j][2 * g], pd.pk[OUT][I][j][2 * g + 1]};
         *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(
             scr + epi_off(r, 2 * (4 * j + g) + h)) = v;
       }
   }
 
   // Row 8q + (lane >> 3), columns 8 (lane & 7) .. +7 of the scratch block.
-  __device__ static uint4 epi_read(const lds_char* scr, int q, int lane) {
+  __device__ __forceinline__ static uint4 epi_read(const lds_char* scr, int q, int lane) {
     const int r = 8 * q + (lane >> 3), c = lane & 7;
     const int f = (r >> 1) & 15;
     const u32x4_t v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
@@ -731,93 +775,121 @@ struct Gemm {
     return (f & 1) ? make_uint4(v.z, v.w, v.x, v.y) : make_uint4(v.x, v.y, v.z, v.w);
   }
 
+  // Rounds the finished tile of this wave into `pd` (the previous pending
+  // tile must be fully stored): relu / relu^2 for the up projection
+  // (PRE = bf16(relu(z)), H = bf16(relu(z)^2), grouped_gemm.py:336-346),
+  // the accumulators as they are otherwise.
+  __device__ __forceinline__ static void stash(const Args& p, const Work& w, const f32x16_t (&acc)[FM][FN],
+                               Pending& pd) {
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const Prob& q = w.q;
+    pd.mb = w.m0 + wm * WM;
+    pd.nb = w.n0 + wn * WN;
+    pd.M = q.M; pd.N = q.N; pd.cr = q.cr; pd.cc = q.cc;
+    const bool two = V == UP_FWD && p.act == VMOE_ACT_RELU_SQUARED && p.c2;
+    // Row blocks starting inside the problem (wave-uniform): none, the first, or both.
+    const int rows = pd.mb >= q.M ? 0 : (pd.mb + 32 >= q.M ? 1 : 3);
+    pd.mask = (rows << (FM * (NOUT - 1))) | (two ? rows : 0);
+    if (pd.mask == 0) return;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const float a = acc[i][j][4 * g + 2 * hh], b = acc[i][j][4 * g + 2 * hh + 1];
+            if (NOUT == 2) {
+              // Selects, not branches: every store below goes to a fixed
+              // element, which keeps the pending tile in registers.
+              const bool r2 = p.act == VMOE_ACT_RELU_SQUARED;
+              const float ra = r2 ? fmaxf(a, 0.0f) : a, rb = r2 ? fmaxf(b, 0.0f) : b;
+              pd.pk[0][i][j][2 * g + hh] = pack_bf16(ra, rb);
+              pd.pk[NOUT - 1][i][j][2 * g + hh] =
+                  pack_bf16(r2 ? ra * ra : ra, r2 ? rb * rb : rb);
+            } else {
+              pd.pk[NOUT - 1][i][j][2 * g + hh] = pack_bf16(a, b);
+            }
+          }
+  }
+
+  // Stores block (OUT, I) of the pending tile: rows pd.mb + 32 I .. +31.
+  template <int OUT, int I>
+  __device__ __forceinline__ static void flush_unit(const Args& p, const Pending& pd, lds_char* scr) {
+    // The lane index is made opaque so that this lane-only address math is
+    // recomputed here instead of being hoisted out of the k-loop, where it
+    // would stay live (and spill) across the MFMAs.
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    const int mb = pd.mb + I * 32;
+    epi_write<OUT, I>(scr, pd, lane);
+    const int n = pd.nb + 8 * (lane & 7);
+    const bool n_ok = n < pd.N;
+    if (V == DOWN_DH && p.pre) {
+      // GA = bf16(pre > 0 ? 2 * GH * pre : 0), GH the bf16-rounded dH
+      // (grouped_gemm.py:751-766). PRE is read for all four row groups
+      // before any is used.
+      uint4 pr[4];
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int m = mb + 8 * qq + (lane >> 3);
+        pr[qq] = make_uint4(0, 0, 0, 0);
+        if (m < pd.M && n_ok)
+          pr[qq] = *reinterpret_cast<const uint4*>(p.pre + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n);
+      }
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const uint4 gh = epi_read(scr, qq, lane);
+        const int m = mb + 8 * qq + (lane >> 3);
+        if (m >= pd.M || !n_ok) continue;
+        const uint32_t gw[4] = {gh.x, gh.y, gh.z, gh.w};
+        const uint32_t pw[4] = {pr[qq].x, pr[qq].y, pr[qq].z, pr[qq].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float pl = lo_f32(pw[t]), ph = hi_f32(pw[t]);
+          o[t] = pack_bf16(pl > 0.0f ? lo_f32(gw[t]) * 2.0f * pl : 0.0f,
+                           ph > 0.0f ? hi_f32(gw[t]) * 2.0f * ph : 0.0f);
+        }
+        *reinterpret_cast<uint4*>(p.c + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n) =
+            make_uint4(o[0], o[1], o[2], o[3]);
+      }
+      return;
+    }
+    uint16_t* out = (NOUT == 2 && OUT == 0) ? p.c2 : p.c;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const uint4 v = epi_read(scr, qq, lane);
+      const int m = mb + 8 * qq + (lane >> 3);
+      if (m < pd.M && n_ok)
+        *reinterpret_cast<uint4*>(out + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n) = v;
+    }
+  }
+
+  // Stores unit U of the pending tile if it is still pending.
+  template <int U>
+  __device__ __forceinline__ static void flush_slot(const Args& p, Pending& pd, lds_char* scr) {
+    if (pd.mask & (1 << U)) flush_unit<U / FM, U % FM>(p, pd, scr);
+  }
+
   // `pslot` >= 0: the accumulators are a partial sum over some of the tile's
   // K chunks; the fp32 tile goes to that partial slot in the accumulator
   // layout (wave, i, j, g, lane: 1 KiB contiguous per store) and the reduce
   // kernel sums the segments in chunk order and rounds once.
-  __device__ static void epilogue(const Args& p, const Work& w, int pslot,
-                                  f32x16_t (&acc)[FM][FN], lds_char* scr) {
-    // The lane index is made opaque here so that the epilogue's lane-only
-    // address arithmetic is not hoisted out of the item loop: live across the
-    // MFMA loop it would spill, and the spill reloads (scratch loads) would
-    // make every store pass wait for the previous one (vmcnt counts both).
-    int lane = threadIdx.x & 63;
-    asm volatile("" : "+v"(lane));
-    const int wave = threadIdx.x >> 6;
-    const int wm = wave / WGN, wn = wave % WGN;
-    const Prob& q = w.q;
-    if (pslot >= 0) {
-      float* slot = p.partial + (int64_t)pslot * (BM * BN) + wave * (WM * WN);
+  __device__ __forceinline__ static void store_partial(const Args& p, int pslot, const f32x16_t (&acc)[FM][FN]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* slot = p.partial + (int64_t)pslot * (BM * BN) + wave * (WM * WN);
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int g = 0; g < 4; ++g)
-            *reinterpret_cast<float4*>(slot + ((((i * FN + j) * 4 + g) * 64 + lane) << 2)) =
-                make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                            acc[i][j][4 * g + 3]);
-      return;
-    }
-    const int n = w.n0 + wn * WN + 8 * (lane & 7);
-    const bool n_ok = n < q.N;
-    if (V == UP_FWD && p.act == VMOE_ACT_RELU_SQUARED) {
-      // relu in place: PRE = bf16(relu(z)), H = bf16(relu(z)^2) both read it
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaxf(acc[i][j][r], 0.0f);
-    }
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int mb = w.m0 + wm * WM + i * 32;
-      if (mb >= q.M) break;
-      // Stores the staged block to `out` (rows mb + 8q + lane / 8).
-      auto flush = [&](uint16_t* out) {
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const uint4 v = epi_read(scr, qq, ln);
-          const int m = mb + 8 * qq + (ln >> 3);
-          if (m < q.M && n_ok)
-            *reinterpret_cast<uint4*>(out + ((int64_t)q.cr + m) * p.ldc + q.cc + n) = v;
-        }
-      };
-      if (V == UP_FWD && p.act == VMOE_ACT_RELU_SQUARED) {
-        if (p.c2) {
-          epi_write(scr, acc, i, lane, [](float v) { return v; });
-          flush(p.c2);
-        }
-        epi_write(scr, acc, i, lane, [](float v) { return v * v; });
-        flush(p.c);
-      } else if (V == DOWN_DH && p.pre) {
-        // GA = bf16(pre > 0 ? 2 * GH * pre : 0), GH the bf16-rounded dH.
-        epi_write(scr, acc, i, lane, [](float v) { return v; });
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const uint4 gh = epi_read(scr, qq, lane);
-          const int m = mb + 8 * qq + (lane >> 3);
-          if (m >= q.M || !n_ok) continue;
-          const int64_t off = ((int64_t)q.cr + m) * p.ldc + q.cc + n;
-          const uint4 pr = *reinterpret_cast<const uint4*>(p.pre + off);
-          const uint32_t gw[4] = {gh.x, gh.y, gh.z, gh.w}, pw[4] = {pr.x, pr.y, pr.z, pr.w};
-          uint32_t o[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float pl = lo_f32(pw[t]), ph = hi_f32(pw[t]);
-            o[t] = pack_bf16(pl > 0.0f ? lo_f32(gw[t]) * 2.0f * pl : 0.0f,
-                             ph > 0.0f ? hi_f32(gw[t]) * 2.0f * ph : 0.0f);
-          }
-          *reinterpret_cast<uint4*>(p.c + off) = make_uint4(o[0], o[1], o[2], o[3]);
-        }
-      } else {
-        epi_write(scr, acc, i, lane, [](float v) { return v; });
-        flush(p.c);
-      }
-    }
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4*>(slot + ((((i * FN + j) * 4 + g) * 64 + lane) << 2)) =
+              make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                          acc[i][j][4 * g + 3]);
   }
 
   // Producer waves: stage the k-tiles of all of the workgroup's items, in
@@ -827,7 +899,7 @@ struct Gemm {
   __device__ static void run_producer(const Args& p, lds_char* ring, const Meta& mt,
                                       const Range& rg) {
     int ec = 0, ei = 0;
-    Work wi = decode(p, mt, rg.beg, ei);
+    Work wi = decode(p, mt, rg.beg, ei, rg.slot);
     Src<PWA> sa;
     Src<PWB> sb;
     TMap tm;
@@ -837,7 +909,7 @@ struct Gemm {
     auto issue_next = [&](lds_char* st) -> bool {
       while (ikt >= wi.nk) {
         if (inext >= rg.end) return false;
-        wi = decode(p, mt, inext, ei);
+        wi = decode(p, mt, inext, ei, rg.slot);
         inext += rg.stride;
         setup(p, wi, sa, sb, tm);
         ikt = 0;
@@ -851,7 +923,7 @@ struct Gemm {
       if (issue_next(ring + s * STAGE)) ++issued;
     int s = 0;  // stage index in the workgroup's stream
     for (int item = rg.beg; item < rg.end; item += rg.stride) {
-      const int nk = decode(p, mt, item, ec).nk;
+      const int nk = decode(p, mt, item, ec, rg.slot).nk;
       for (int kt = 0; kt < nk; ++kt, ++s) {
         // Stages s+1 .. issued-1 may still be in flight: wait until only
         // their DMAs are outstanding (loads complete in order), sync (the
@@ -870,19 +942,23 @@ struct Gemm {
     }
   }
 
-  // Consumer waves: multiply each stage after the barrier that publishes it,
-  // and store a tile when its last K chunk in this workgroup is done. A
-  // contiguous range may start or end inside a split tile; such a segment
-  // is a partial sum and goes to slot 2 * lin (the range's first segment) or
-  // 2 * lin + 1 (its last).
+  // Consumer waves: multiply each stage after the barrier that publishes it.
+  // A tile is finished when its last K chunk in this workgroup is done; its
+  // results become the pending tile, stored during the next item's k-steps
+  // (spread evenly over them) or at the end. A contiguous range may start or
+  // end inside a split tile; such a segment is a partial sum and goes to
+  // slot 2 * lin (the range's first segment) or 2 * lin + 1 (its last).
   __device__ static void run_consumer(const Args& p, const lds_char* ring, const Meta& mt,
                                       const Range& rg, lds_char* scr) {
     int ec = 0;
     int s = 0;
     int seg_item = rg.beg, seg_chunk = -1;
     f32x16_t acc[FM][FN];
+    Pending pd;
+    pd.mask = 0;
     for (int item = rg.beg; item < rg.end; item += rg.stride) {
-      const Work w = decode(p, mt, item, ec);
+      const Work w = decode(p, mt, item, ec, rg.slot);
+      if (w.skip) continue;
       if (seg_chunk < 0) {
         seg_item = item;
         seg_chunk = w.chunk;
@@ -893,18 +969,51 @@ struct Gemm {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
       }
-      for (int kt = 0; kt < w.nk; ++kt, ++s) {
+      // Pending unit u goes out after k-step min(u * gap, nk - 1) of this item
+      // (right away when the item has no k-steps), so the previous tile's
+      // stores are spread over this item's MFMAs. The dW GEMMs finish few
+      // tiles per workgroup and store them at once (pending stays empty),
+      // which keeps their registers for the accumulators.
+      const int gap = max(1, w.nk / UNITS);
+      int kt = 0;
+#pragma unroll
+      for (int u = 0; u < (Cfg<V>::contig ? 0 : UNITS); ++u) {
+        const int at = min(u * gap, w.nk - 1);
+        for (; kt <= at; ++kt, ++s) {
+          block_barrier();
+          compute(ring + (s % kStages) * STAGE, acc);
+        }
+        if (u == 0) flush_slot<0>(p, pd, scr);
+        if (u == 1) flush_slot<1>(p, pd, scr);
+        if (u == 2) flush_slot<2 % UNITS>(p, pd, scr);
+        if (u == 3) flush_slot<3 % UNITS>(p, pd, scr);
+      }
+      pd.mask = 0;
+      for (; kt < w.nk; ++kt, ++s) {
         block_barrier();
         compute(ring + (s % kStages) * STAGE, acc);
       }
       const bool last_chunk = w.chunk == w.chunks - 1;
       if (rg.stride != 1 || last_chunk || item + 1 >= rg.end) {
-        int pslot = -1;
-        if (w.chunks > 1 && !(seg_chunk == 0 && last_chunk))
-          pslot = 2 * rg.lin + (seg_item == rg.beg ? 0 : 1);
-        epilogue(p, w, pslot, acc, scr);
+        if (w.chunks > 1 && !(seg_chunk == 0 && last_chunk)) {
+          store_partial(p, 2 * rg.lin + (seg_item == rg.beg ? 0 : 1), acc);
+        } else {
+          stash(p, w, acc, pd);
+          if (Cfg<V>::contig) {
+            flush_slot<0>(p, pd, scr);
+            flush_slot<1>(p, pd, scr);
+            pd.mask = 0;
+          }
+        }
         seg_chunk = -1;
       }
+    }
+    // The last tile has no next item to hide behind.
+    flush_slot<0>(p, pd, scr);
+    flush_slot<1>(p, pd, scr);
+    if (UNITS > 2) {
+      flush_slot<2 % UNITS>(p, pd, scr);
+      flush_slot<3 % UNITS>(p, pd, scr);
     }
   }
 
@@ -944,7 +1053,7 @@ __device__ bool locate_tile(const Args& p, int id, long long* scan, int* sh, int
     const int e = e0 + threadIdx.x;
     int tiles = 0, chunks = 1;
     if (e < p.E) expert_work<V>(p, Traits<V>::prob(p, rec_global(p, e)), tiles, chunks);
-    const long long packed = ((long long)tiles << 32) | (long long)(tiles * chunks);
+    const long long packed = ((long long)tiles << 32) | (long long)work_items<V>(tiles, chunks);
     long long total;
     const long long ex = block_exclusive_scan<long long, kRedThreads>(packed, scan, &total);
     const long long pre = base + ex;
@@ -966,13 +1075,15 @@ __device__ bool locate_tile(const Args& p, int id, long long* scan, int* sh, int
   return e_out >= 0;
 }
 
-// Split-K reduction of the contig GEMMs. A tile whose K chunks (items
-// [a, a + chunks)) were all done by one workgroup was stored directly; any
-// other tile has one partial segment per workgroup range it touches, in
-// slot 2L (the segment starts its range L) or 2L + 1 (it starts inside L).
-// This kernel sums the segments in chunk order and rounds once. Workgroup
-// (x, y) handles float4s [1024 y, 1024 (y + 1)) of tile x's slots, which
-// hold the accumulator layout of the GEMM's epilogue.
+// Split-K reduction of the contig GEMMs. The K chunks of tile t are items
+// [a, a + chunks) of the lane ranges, done by slot t % kLane of each lane
+// whose range they touch. A tile inside one lane range was stored directly;
+// any other tile has one partial segment per lane range it touches, in slot
+// 2 lin (the segment starts that range) or 2 lin + 1 (it starts inside it),
+// lin = kLane * lane + t % kLane. This kernel sums the segments in chunk
+// order and rounds once. Workgroup (x, y) handles float4s
+// [1024 y, 1024 (y + 1)) of tile x's slots, which hold the accumulator
+// layout of the GEMM's epilogue.
 template <int V>
 __global__ __launch_bounds__(kRedThreads) void splitk_reduce_kernel(Args p) {
   using G = Gemm<V>;
@@ -983,8 +1094,8 @@ __global__ __launch_bounds__(kRedThreads) void splitk_reduce_kernel(Args p) {
   int e, tile, ipre, chunks, total;
   if (!locate_tile<V>(p, blockIdx.x, scan, sh, e, tile, ipre, chunks, total)) return;
   if (chunks <= 1) return;
-  const int Gr = p.grid;
-  const int a = ipre + tile * chunks;
+  const int Gr = p.grid / kLane;  // lanes
+  const int a = ipre + (tile / kLane) * chunks, ts = tile % kLane;
   int L = (int)min<int64_t>(Gr - 1, (int64_t)a * Gr / total);
   while (L + 1 < Gr && contig_begin(total, L + 1, Gr) <= a) ++L;
   while (L > 0 && contig_begin(total, L, Gr) > a) --L;
@@ -1006,12 +1117,12 @@ __global__ __launch_bounds__(kRedThreads) void splitk_reduce_kernel(Args p) {
       acc[i].x += v[i].x; acc[i].y += v[i].y; acc[i].z += v[i].z; acc[i].w += v[i].w;
     }
   };
-  add_slot(2 * L + (contig_begin(total, L, Gr) == a ? 0 : 1));
+  add_slot(2 * (L * kLane + ts) + (contig_begin(total, L, Gr) == a ? 0 : 1));
   for (int l = L + 1; l < Gr; ++l) {
     const int b0 = contig_begin(total, l, Gr);
     if (b0 >= a + chunks) break;
     if (contig_begin(total, l + 1, Gr) == b0) continue;  // empty range
-    add_slot(2 * l);
+    add_slot(2 * (l * kLane + ts));
   }
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
@@ -1087,10 +1198,14 @@ int gemm_grid(int64_t items_bound) {
   return (int)std::min<int64_t>(cus, (items_bound + 7) / 8 * 8);
 }
 
+// Grid of the dW GEMMs: whole lanes on every XCD (a multiple of 8 * kLane),
+// one workgroup per CU where the device allows.
+int lane_grid() { return std::max(8 * kLane, cu_count() / (8 * kLane) * (8 * kLane)); }
+
 template <int V>
 int launch(Args p, int64_t items_bound, hipStream_t s) {
   if (items_bound <= 0) return VMOE_OK;
-  p.grid = gemm_grid(items_bound);
+  p.grid = Cfg<V>::contig ? lane_grid() : gemm_grid(items_bound);
   hipLaunchKernelGGL(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
@@ -1131,7 +1246,7 @@ int launch_dw(Args p, int64_t tmax, void* ws, size_t ws_bytes, hipStream_t s) {
   if (items <= 0) return VMOE_OK;
   if (items > INT32_MAX || E * tmax > INT32_MAX) return VMOE_ERR_UNSUPPORTED;
   p.kc = kDwChunk;
-  p.grid = gemm_grid(items);
+  p.grid = lane_grid();
   if (ws_bytes < dw_workspace<V>(p.grid)) return VMOE_ERR_WORKSPACE;
   p.partial = reinterpret_cast<float*>(ws);
   hipLaunchKernelGGL(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
@@ -1259,7 +1374,7 @@ extern "C" int vmoe_gemm_up_bwd_dx(const uint16_t* grad_act, int64_t ldg, const 
 extern "C" size_t vmoe_gemm_dw_workspace_bytes(int32_t E, int64_t hidden, int64_t max_width,
                                                int64_t rows_bound) {
   if (E <= 0 || hidden <= 0 || max_width <= 0 || rows_bound <= 0) return 0;
-  const int grid = gemm_grid(INT32_MAX);
+  const int grid = lane_grid();
   return std::max(dw_workspace<UP_DW>(grid), dw_workspace<DOWN_DW>(grid));
 }
 
