@@ -207,11 +207,13 @@ def kernel_breakdown(m, xb, sel, reps):
     meta = gg.GemmMeta(eto, m.expert_weight_offsets_t, m.expert_widths_t, tpe, E,
                        m.max_expert_width, r.rows_bound)
     nrd = r.info[0:1]
-    xg = gather_rows(x, r.row_src, k, r.rows_bound, num_rows_dev=nrd)
+    ar = r.assignment_row
+    xg = gather_rows(x, r.row_src, k, r.rows_bound, num_rows_dev=nrd, assignment_row=ar)
     h, pre = gg.up_fwd(xg, m.w1.detach(), meta, 1, True, False)
     y = gg.down_fwd(h, m.w2.detach(), meta, d)
     G = torch.ones(T, d, dtype=torch.bfloat16, device=x.device)
-    gy = gather_rows(G, r.row_src, k, r.rows_bound, weights=wts, num_rows_dev=nrd)
+    gy = gather_rows(G, r.row_src, k, r.rows_bound, weights=wts, num_rows_dev=nrd,
+                     assignment_row=ar)
     w1, w2 = m.w1.detach(), m.w2.detach()
     ga, _ = gg.down_bwd(gy, h, w2, meta, d, False, pre=pre)
     gxg, _ = gg.up_bwd_from_ga(ga, x, w1, meta, d, r.gather_map)
@@ -246,12 +248,13 @@ def kernel_breakdown(m, xb, sel, reps):
 
     ops = {
         "route": lambda: route_device(selv, E, k, b),
-        "gather": lambda: gather_rows(x, r.row_src, k, r.rows_bound, num_rows_dev=nrd),
+        "gather": lambda: gather_rows(x, r.row_src, k, r.rows_bound, num_rows_dev=nrd,
+                                      assignment_row=ar),
         "gemm_up_fwd": lambda: gg.up_fwd(xg, w1, meta, 1, True, False),
         "gemm_down_fwd": lambda: gg.down_fwd(h, w2, meta, d),
         "combine": lambda: combine_rows(y, r.assignment_row, k, T, weights=wts),
         "scatter_bwd_gather": lambda: gather_rows(G, r.row_src, k, r.rows_bound, weights=wts,
-                                                  num_rows_dev=nrd),
+                                                  num_rows_dev=nrd, assignment_row=ar),
         "gemm_down_bwd_dh_ga": dh_only,
         "gemm_down_bwd_dw": dw2_only,
         "gemm_up_bwd_dx": dx_only,

@@ -100,6 +100,20 @@ int vmoe_gather(const uint16_t* x, int64_t x_rows, int64_t ldx, const int32_t* r
                 int64_t ldo, int64_t num_rows, const int32_t* num_rows_dev, int64_t hidden,
                 vmoe_stream_t stream);
 
+/* vmoe_gather_tokens: the same output as vmoe_gather for maps produced
+ * together by vmoe_route, computed token by token: for t < num_tokens and
+ * j < top_k, out[assignment_row[t*k+j]] = x[t] (times weights[t*k+j] when
+ * weights != NULL, rounded to bf16); rows r < num_rows with row_src[r] < 0
+ * are zeroed. x is read once per token instead of once per row, and ldx may
+ * be 0 (one row broadcast to every token, e.g. the gradient of out.sum()).
+ * Replaces the same reference functions as vmoe_gather
+ * (triton_moe/kernels/gather.py:63-115, 177-218). Requires hidden, ldx and
+ * ldo multiples of 8, 16-byte aligned x and out, and top_k <= 64. */
+int vmoe_gather_tokens(const uint16_t* x, int64_t ldx, const int32_t* assignment_row,
+                       int64_t num_tokens, int32_t top_k, const uint16_t* weights,
+                       const int32_t* row_src, uint16_t* out, int64_t ldo, int64_t num_rows,
+                       const int32_t* num_rows_dev, int64_t hidden, vmoe_stream_t stream);
+
 /* vmoe_combine: out[t] = bf16( sum_j f32( bf16( y[assignment_row[t*k+j]] * w[t*k+j] ) ) ),
  * j = 0..top_k-1 in order, slots with assignment_row < 0 contribute 0.
  *   - weighted:   padded_scatter + intermediate.sum(1)

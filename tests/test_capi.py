@@ -25,7 +25,7 @@ def test_header_declares_expected_entry_points():
     for must in ("vmoe_route", "vmoe_row_maps", "vmoe_gather", "vmoe_combine",
                  "vmoe_gemm_up_fwd", "vmoe_gemm_down_fwd", "vmoe_gemm_up_bwd_dx",
                  "vmoe_gemm_up_bwd_dw", "vmoe_gemm_down_bwd_dh", "vmoe_gemm_down_bwd_dw",
-                 "vmoe_zero_tail_cols", "vmoe_status_string"):
+                 "vmoe_zero_tail_cols", "vmoe_status_string", "vmoe_gather_tokens"):
         assert must in names
 
 
@@ -58,6 +58,11 @@ def test_argument_checks_return_invalid_arg():
     assert lib.vmoe_gather(None, 0, 0, None, 1, None, 0, None, 8, -1, None, 8,
                            None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_combine(None, 0, 0, None, None, 0, None, 8, 1, 8, None) == _lib.ERR_INVALID_ARG
+    # token-major gather: top_k above one wave is rejected, unaligned widths unsupported
+    assert lib.vmoe_gather_tokens(1, 8, 1, 4, 65, None, 1, 1, 8, 4, None, 8,
+                                  None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gather_tokens(1, 12, 1, 4, 2, None, 1, 1, 12, 4, None, 12,
+                                  None) == _lib.ERR_UNSUPPORTED
     # unaligned hidden size is unsupported, not silently wrong
     assert lib.vmoe_gemm_up_fwd(None, 8, 0, None, None, 8, None, None, 8, 1, 1, 1, 1, 1, 4, 12,
                                 16, 64, None) == _lib.ERR_UNSUPPORTED

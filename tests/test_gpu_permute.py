@@ -136,3 +136,39 @@ def test_route_maps_feed_permutation(device):
     assert bits_equal(got, _ref_gather(x, maps, k))
     pub = fused_route(sel.reshape(-1).to(device), E, block_size=64)
     assert torch.equal(pub[1].cpu(), torch.from_numpy(r["indices"]))
+
+
+@pytest.mark.parametrize("T,d,E,k,b", [(128, 128, 4, 2, 128), (1024, 256, 8, 2, 128),
+                                       (2048, 768, 16, 2, 64), (1024, 1024, 64, 8, 64),
+                                       (300, 104, 5, 2, 8), (257, 2056, 7, 3, 64),
+                                       (300, 100, 5, 2, 8)])
+def test_token_major_gather_exact(T, d, E, k, b, device):
+    """The token-by-token gather (x read once per token) writes the same rows,
+    weighted or not, with zero pad rows (d = 100 takes the row-by-row path)."""
+    x, sel, wts, r, maps = _setup(T, d, E, k, b, device, seed=9)
+    P = int(r["padded_bins"][-1])
+    rs = torch.as_tensor(maps["row_src"]).to(device)
+    ar = torch.as_tensor(maps["assignment_row"]).to(device)
+    # fill the output allocator with garbage first: every row must be written
+    torch.full((P + 64, d), 7.0, dtype=torch.bfloat16, device=device)
+    got = gather_rows(x.to(device), rs, k, P, assignment_row=ar)
+    assert bits_equal(got, _ref_gather(x, maps, k))
+    gw = gather_rows(x.to(device), rs, k, P, weights=wts.reshape(-1).to(device),
+                     assignment_row=ar)
+    assert bits_equal(gw, _ref_gather(x, maps, k, wts))
+
+
+def test_token_major_gather_broadcast_and_row_cap(device):
+    """A stride-0 input is read from one row; a device row count caps the output."""
+    T, d, E, k, b = 512, 256, 8, 4, 64
+    x, sel, wts, r, maps = _setup(T, d, E, k, b, device, seed=10)
+    rd = route_device(sel.reshape(-1).to(device), E, k, b)
+    P, _ = check_route(rd)
+    row = torch.randn(1, d, generator=torch.Generator().manual_seed(11)).to(torch.bfloat16)
+    full = row.expand(T, d)
+    for xin in (row.to(device).expand(T, d), torch.ones((), dtype=torch.bfloat16,
+                                                         device=device).expand(T, d)):
+        ref_x = full if xin.stride(1) == 1 else torch.ones(T, d, dtype=torch.bfloat16)
+        got = gather_rows(xin, rd.row_src, k, rd.rows_bound, weights=wts.reshape(-1).to(device),
+                          num_rows_dev=rd.info[0:1], assignment_row=rd.assignment_row)
+        assert bits_equal(got[:P], _ref_gather(ref_x, maps, k, wts))

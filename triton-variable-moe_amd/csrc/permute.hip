@@ -92,6 +92,81 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
   }
 }
 
+// Token-major form of the same gather: wave-blocks [0, tok_blocks) take
+// tokens, read x[t] once and write it (times w[t*k+j] when weighted) to each
+// of its rows assignment_row[t*k+j] < rows; the remaining blocks write zeros
+// to the pad rows (row_src < 0), found 64 rows at a time with a wave ballot.
+// x is read once instead of top_k times. CHUNKS 16-byte vectors per lane stay
+// in registers between the top_k stores.
+template <bool WEIGHTED, int CHUNKS>
+__global__ __launch_bounds__(kThreads) void gather_tokens_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const int32_t* __restrict__ assignment_row,
+    int64_t num_tokens, int top_k, const uint16_t* __restrict__ w,
+    const int32_t* __restrict__ row_src, uint16_t* __restrict__ out, int64_t ldo,
+    int64_t num_rows, const int32_t* __restrict__ num_rows_dev, int64_t hidden, int tok_blocks) {
+  using V = Vec<8>;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  int64_t rows = num_rows;
+  if (num_rows_dev) rows = min(rows, (int64_t)*num_rows_dev);
+  const int64_t nvec = hidden / 8;
+  if ((int)blockIdx.x < tok_blocks) {
+    for (int64_t t = (int64_t)blockIdx.x * kRowsPerBlock + wv; t < num_tokens;
+         t += (int64_t)tok_blocks * kRowsPerBlock) {
+      // Lane j < top_k holds the row (and weight) of slot j.
+      const int64_t a0 = t * top_k;
+      int32_t my_row = -1;
+      float my_w = 1.0f;
+      if (lane < top_k) {
+        my_row = assignment_row[a0 + lane];
+        if (WEIGHTED) my_w = bf16_to_f32(w[a0 + lane]);
+      }
+      const uint16_t* xrow = x + t * ldx;
+      for (int64_t c0 = 0; c0 < nvec; c0 += (int64_t)CHUNKS * kWave) {
+        V::T v[CHUNKS];
+#pragma unroll
+        for (int ch = 0; ch < CHUNKS; ++ch) {
+          const int64_t c = c0 + ch * kWave + lane;
+          v[ch] = c < nvec ? V::load(xrow + c * 8) : V::zero();
+        }
+        for (int j = 0; j < top_k; ++j) {
+          const int32_t r = __shfl(my_row, j, kWave);
+          if (r < 0 || r >= rows) continue;
+          const float scale = WEIGHTED ? __shfl(my_w, j, kWave) : 1.0f;
+          uint16_t* orow = out + (int64_t)r * ldo;
+#pragma unroll
+          for (int ch = 0; ch < CHUNKS; ++ch) {
+            const int64_t c = c0 + ch * kWave + lane;
+            if (c >= nvec) continue;
+            typename V::T o = v[ch];
+            if (WEIGHTED) {
+              float f[8];
+              V::to_f32(o, f);
+#pragma unroll
+              for (int i = 0; i < 8; ++i) f[i] *= scale;
+              o = V::from_f32(f);
+            }
+            V::store(orow + c * 8, o);
+          }
+        }
+      }
+    }
+    return;
+  }
+  const int pad_blocks = (int)gridDim.x - tok_blocks;
+  for (int64_t r0 = ((int64_t)(blockIdx.x - tok_blocks) * kRowsPerBlock + wv) * kWave; r0 < rows;
+       r0 += (int64_t)pad_blocks * kRowsPerBlock * kWave) {
+    const int64_t r = r0 + lane;
+    uint64_t pad = ballot64(r < rows && row_src[r] < 0);
+    while (pad) {
+      const int b = __builtin_ctzll(pad);
+      pad &= pad - 1;
+      uint16_t* orow = out + (r0 + b) * ldo;
+      for (int64_t c = lane; c < nvec; c += kWave) V::store(orow + c * 8, V::zero());
+    }
+  }
+}
+
 // out[t] = bf16(sum_j f32(bf16(y[row(t,j)] * w[t*k+j]))). Each lane keeps up
 // to CHUNKS vectors of the row in fp32 registers.
 template <int VEC, bool WEIGHTED, int CHUNKS>
@@ -203,6 +278,37 @@ extern "C" int vmoe_gather(const uint16_t* x, int64_t x_rows, int64_t ldx,
       hipLaunchKernelGGL((gather_kernel<1, false>), grid, block, 0, s, x, x_rows, ldx, row_src,
                          top_k, weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
   }
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_gather_tokens(const uint16_t* x, int64_t ldx,
+                                  const int32_t* assignment_row, int64_t num_tokens,
+                                  int32_t top_k, const uint16_t* weights,
+                                  const int32_t* row_src, uint16_t* out, int64_t ldo,
+                                  int64_t num_rows, const int32_t* num_rows_dev, int64_t hidden,
+                                  vmoe_stream_t stream) {
+  if (num_rows < 0 || hidden < 0 || num_tokens < 0 || top_k <= 0 || top_k > kWave || ldx < 0 ||
+      ldo < hidden)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_rows == 0 || hidden == 0) return VMOE_OK;
+  if (!out || !row_src || (num_tokens > 0 && (!x || !assignment_row)))
+    return VMOE_ERR_INVALID_ARG;
+  if (hidden % 8 != 0 || ldx % 8 != 0 || ldo % 8 != 0 || !aligned16(x) || !aligned16(out))
+    return VMOE_ERR_UNSUPPORTED;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int tok_blocks = num_tokens > 0 ? std::min(row_grid(num_tokens), 8192) : 0;
+  const int pad_blocks = (int)std::min<int64_t>(
+      1024, std::max<int64_t>(1, (num_rows + kRowsPerBlock * kWave - 1) / (kRowsPerBlock * kWave)));
+  const dim3 grid(tok_blocks + pad_blocks), block(kThreads);
+  if (weights)
+    hipLaunchKernelGGL((gather_tokens_kernel<true, 2>), grid, block, 0, s, x, ldx,
+                       assignment_row, num_tokens, top_k, weights, row_src, out, ldo, num_rows,
+                       num_rows_dev, hidden, tok_blocks);
+  else
+    hipLaunchKernelGGL((gather_tokens_kernel<false, 2>), grid, block, 0, s, x, ldx,
+                       assignment_row, num_tokens, top_k, weights, row_src, out, ldo, num_rows,
+                       num_rows_dev, hidden, tok_blocks);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }

@@ -30,6 +30,8 @@ _SIGNATURES = {
                    _i64, _vp, _vp, _vp, ctypes.c_size_t, _vp],
     "vmoe_row_maps": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _i64, _vp, _vp, _vp, _vp],
     "vmoe_gather": [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp],
+    "vmoe_gather_tokens": [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _vp, _i64, _i64, _vp, _i64,
+                           _vp],
     "vmoe_combine": [_vp, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp],
     "vmoe_gemm_up_fwd": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp,
                          _vp, _i32, _i64, _i64, _i64, _vp],

@@ -52,18 +52,36 @@ def row_maps(indices, bin_ids, bins, padded_bins, top_k: int, num_rows: int,
 
 def gather_rows(x: torch.Tensor, row_src: torch.Tensor, top_k: int, num_rows: int,
                 weights: torch.Tensor | None = None,
-                num_rows_dev: torch.Tensor | None = None) -> torch.Tensor:
-    """out[r] = x[row_src[r] // top_k] (* weights[row_src[r]]), zeros where row_src < 0."""
+                num_rows_dev: torch.Tensor | None = None,
+                assignment_row: torch.Tensor | None = None) -> torch.Tensor:
+    """out[r] = x[row_src[r] // top_k] (* weights[row_src[r]]), zeros where row_src < 0.
+
+    With assignment_row (the map vmoe_route produces with row_src) the copy
+    runs token by token and reads each row of x once; a row-broadcast x (row
+    stride 0, such as the gradient of out.sum()) is then read from a single row.
+    """
     _require_bf16(x, "gather")
-    x = _row_major(x)
     hidden = x.shape[1]
+    tokens = x.shape[0]
+    token_major = (assignment_row is not None and hidden % 8 == 0
+                   and assignment_row.numel() == tokens * top_k and top_k <= 64)
+    if token_major and tokens > 0 and x.stride(0) == 0:
+        x, ldx = (x[:1] if x.stride(1) == 1 else x[:1].contiguous()), 0
+    else:
+        x = _row_major(x)
+        ldx = x.stride(0)
     out = torch.empty(num_rows, hidden, dtype=x.dtype, device=x.device)
     if num_rows == 0 or hidden == 0:
         return out
     w = None
     if weights is not None:
         w = weights.to(x.dtype).contiguous()
-    _lib.call("vmoe_gather", x.data_ptr(), x.shape[0], x.stride(0), row_src.data_ptr(),
+    if token_major and ldx % 8 == 0 and x.data_ptr() % 16 == 0:
+        _lib.call("vmoe_gather_tokens", x.data_ptr(), ldx, assignment_row.data_ptr(), tokens,
+                  int(top_k), _lib.ptr(w), row_src.data_ptr(), out.data_ptr(), out.stride(0),
+                  num_rows, _lib.ptr(num_rows_dev), hidden, _lib.stream(x.device))
+        return out
+    _lib.call("vmoe_gather", x.data_ptr(), tokens, ldx, row_src.data_ptr(),
               int(top_k), _lib.ptr(w), 0 if w is None else w.numel(), out.data_ptr(),
               out.stride(0), num_rows, _lib.ptr(num_rows_dev), hidden, _lib.stream(x.device))
     return out
@@ -166,7 +184,8 @@ class RoutedGatherOp(torch.autograd.Function):
         ctx.save_for_backward(assignment_row)
         ctx.top_k = top_k
         ctx.num_tokens = x.shape[0]
-        return gather_rows(x, row_src, top_k, rows, num_rows_dev=num_rows_dev)
+        return gather_rows(x, row_src, top_k, rows, num_rows_dev=num_rows_dev,
+                           assignment_row=assignment_row)
 
     @staticmethod
     @custom_bwd(device_type="cuda")

@@ -87,7 +87,7 @@ class RoutedScatterOp(torch.autograd.Function):
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx, y, row_src, assignment_row, weights, top_k, num_tokens, num_rows_dev):
-        ctx.save_for_backward(row_src, weights, num_rows_dev)
+        ctx.save_for_backward(row_src, assignment_row, weights, num_rows_dev)
         ctx.top_k = top_k
         ctx.rows = y.shape[0]
         return combine_rows(y, assignment_row, top_k, num_tokens, weights=weights)
@@ -96,7 +96,7 @@ class RoutedScatterOp(torch.autograd.Function):
     @custom_bwd(device_type="cuda")
     @once_differentiable
     def backward(ctx, grad_output):
-        rs, weights, nrd = ctx.saved_tensors
+        rs, ar, weights, nrd = ctx.saved_tensors
         grad_y = gather_rows(grad_output, rs, ctx.top_k, ctx.rows, weights=weights,
-                             num_rows_dev=nrd)
+                             num_rows_dev=nrd, assignment_row=ar)
         return grad_y, None, None, None, None, None, None
