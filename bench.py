@@ -201,11 +201,8 @@ def kernel_breakdown(m, xb, sel, reps):
     wts = torch.rand(T * k, device=x.device).to(torch.bfloat16)
     selv = sel.reshape(-1)
     r = route_device(selv, E, k, b)
-    pb = r.padded_bins
-    eto = torch.cat([torch.zeros(1, dtype=torch.int32, device=x.device), pb])
-    tpe = torch.cat([pb[:1], pb[1:] - pb[:-1]])
-    meta = gg.GemmMeta(eto, m.expert_weight_offsets_t, m.expert_widths_t, tpe, E,
-                       m.max_expert_width, r.rows_bound)
+    meta = gg.GemmMeta(r.expert_offsets, m.expert_weight_offsets_t, m.expert_widths_t,
+                       r.padded_counts, E, m.max_expert_width, r.rows_bound)
     nrd = r.info[0:1]
     ar = r.assignment_row
     xg = gather_rows(x, r.row_src, k, r.rows_bound, num_rows_dev=nrd, assignment_row=ar)

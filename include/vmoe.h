@@ -60,6 +60,10 @@ int vmoe_route_max_experts(void);
  *   gather_map  [row_capacity] int32: padded row -> token (assignment / top_k), 0 = pad
  *   assignment_row [A] int32: assignment -> padded row, -1 = dropped
  *   info        [VMOE_INFO_LEN] int32: rows P, kept count, error bits
+ *   expert_offsets [E+1] int32 (nullable): [0, padded_bins], the module's
+ *               expert_token_offsets (triton_moe/moe.py:193-197)
+ *   padded_counts  [E] int32 (nullable): rounded counts, diff(padded_bins),
+ *               the module's padded tokens_per_expert (moe.py:198-202)
  * Only the first P = padded_bins[E-1] rows of row_src/gather_map are written;
  * row_capacity >= A + E*(block_size-1) always suffices.
  * ---------------------------------------------------------------------- */
@@ -69,8 +73,9 @@ int vmoe_route(const void* selected_experts, int32_t selected_is_int64,
                int32_t block_size, int32_t rounding, int32_t* bin_ids, int32_t* indices,
                int32_t* tokens_per_expert, int32_t* bins, int32_t* padded_bins,
                int32_t* row_src, int32_t* gather_map, int64_t row_capacity,
-               int32_t* assignment_row, int32_t* info, void* workspace,
-               size_t workspace_bytes, vmoe_stream_t stream);
+               int32_t* assignment_row, int32_t* info, int32_t* expert_offsets,
+               int32_t* padded_counts, void* workspace, size_t workspace_bytes,
+               vmoe_stream_t stream);
 
 /* Row maps from caller-supplied routing arrays, for the stand-alone
  * gather/scatter/gather-map entry points. Follows the per-sorted-position

@@ -43,6 +43,10 @@ def test_route_golden(case, dtype, device):
     np.testing.assert_array_equal(_np(r.row_src[:P]), exp["row_src"])
     np.testing.assert_array_equal(_np(r.gather_map[:P]), exp["gather_map"])
     np.testing.assert_array_equal(_np(r.assignment_row), exp["assignment_row"])
+    # the module's expert_token_offsets and padded counts (moe.py:193-202)
+    pb = np.asarray(exp["padded_bins"], dtype=np.int64)
+    np.testing.assert_array_equal(_np(r.expert_offsets), np.concatenate([[0], pb]))
+    np.testing.assert_array_equal(_np(r.padded_counts), np.diff(np.concatenate([[0], pb])))
     # public entry point
     out = fused_route(sel, E, block_size=b, rounding=mode)
     for t, key in zip(out, ("bin_ids", "indices", "tokens_per_expert", "bins", "padded_bins")):

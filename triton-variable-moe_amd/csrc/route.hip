@@ -107,7 +107,8 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     RouteWs ws, int E, int ntiles, int block, int mode, int32_t* __restrict__ tpe,
     int32_t* __restrict__ bins, int32_t* __restrict__ padded_bins,
     int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int64_t row_capacity,
-    int32_t* __restrict__ info) {
+    int32_t* __restrict__ info, int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ padded_counts) {
   __shared__ int32_t scan_smem[kScanThreads / kWave + 1];
   __shared__ int32_t carry_kept, carry_rounded, any_bad;
   extern __shared__ int32_t lds[];
@@ -170,6 +171,13 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
       ps_lds[e] = br + er;
       kept_lds[e] = k;
       rounded_lds[e] = r;
+      // The module's expert_token_offsets = [0, padded_bins] and padded
+      // tokens_per_expert = diff(padded_bins) (moe.py:193-202).
+      if (expert_offsets) {
+        expert_offsets[e + 1] = br + er + r;
+        if (e == 0) expert_offsets[0] = 0;
+      }
+      if (padded_counts) padded_counts[e] = r;
     }
     __syncthreads();
     if (tid == 0) {
@@ -329,7 +337,8 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
                           int32_t block, int32_t rounding, int32_t* bin_ids, int32_t* indices,
                           int32_t* tpe, int32_t* bins, int32_t* padded_bins, int32_t* row_src,
                           int32_t* gather_map, int64_t row_capacity, int32_t* assignment_row,
-                          int32_t* info, void* workspace, size_t ws_bytes, vmoe_stream_t stream) {
+                          int32_t* info, int32_t* expert_offsets, int32_t* padded_counts,
+                          void* workspace, size_t ws_bytes, vmoe_stream_t stream) {
   if (A < 0 || E <= 0 || top_k <= 0 || block <= 0 || row_capacity < 0)
     return VMOE_ERR_INVALID_ARG;
   if (rounding < VMOE_ROUND_UP || rounding > VMOE_ROUND_NEAREST) return VMOE_ERR_INVALID_ARG;
@@ -349,7 +358,7 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
   }
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), sizeof(int32_t) * (4 * E + 1),
                      s, ws, E, ntiles, block, rounding, tpe, bins, padded_bins, row_src,
-                     gather_map, row_capacity, info);
+                     gather_map, row_capacity, info, expert_offsets, padded_counts);
   VMOE_CHECK_LAUNCH();
   if (ntiles > 0) {
     int nbits = 1;

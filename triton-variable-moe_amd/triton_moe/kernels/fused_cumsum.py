@@ -31,6 +31,8 @@ class Route:
     gather_map: torch.Tensor       # [rows_bound] int32, 0 = pad row
     assignment_row: torch.Tensor   # [A] int32, -1 = dropped
     info: torch.Tensor             # [4] int32: rows P, kept, error bits
+    expert_offsets: torch.Tensor   # [E+1] int32: [0, padded_bins]
+    padded_counts: torch.Tensor    # [E] int32: diff(padded_bins)
     rows_bound: int                # host upper bound of P
     num_assignments: int
     num_experts: int
@@ -65,25 +67,25 @@ def route_device(selected: torch.Tensor, num_experts: int, top_k: int, block_siz
     A = sel.numel()
     E = int(num_experts)
     cap = rows_upper_bound(A, E, block_size, rounding)
-    i32 = dict(dtype=torch.int32, device=dev)
-    bin_ids = torch.empty(max(A, 1), **i32)
-    indices = torch.empty(max(A, 1), **i32)
-    tpe = torch.empty(E, **i32)
-    bins = torch.empty(E, **i32)
-    padded = torch.empty(E, **i32)
-    row_src = torch.empty(max(cap, 1), **i32)
-    gmap = torch.empty(max(cap, 1), **i32)
-    arow = torch.empty(max(A, 1), **i32)
-    info = torch.empty(_lib.INFO_LEN, **i32)
     ws_bytes = int(_lib.lib().vmoe_route_workspace_bytes(A, E))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    # One allocation carved into 16-byte aligned int32 views (one allocator
+    # call per routing instead of twelve).
+    sizes = [max(A, 1), max(A, 1), E, E, E, max(cap, 1), max(cap, 1), max(A, 1), _lib.INFO_LEN,
+             E + 1, E, (ws_bytes + 3) // 4]
+    offs, n = [], 0
+    for sz in sizes:
+        offs.append(n)
+        n += (sz + 3) // 4 * 4
+    buf = torch.empty(n, dtype=torch.int32, device=dev)
+    (bin_ids, indices, tpe, bins, padded, row_src, gmap, arow, info, eto, ptpe,
+     ws) = (buf[o:o + sz] for o, sz in zip(offs, sizes))
     _lib.call("vmoe_route", sel.data_ptr(), int(sel.dtype == torch.int64), A, E, int(top_k),
               int(block_size), _lib.ROUNDING[rounding], bin_ids.data_ptr(), indices.data_ptr(),
               tpe.data_ptr(), bins.data_ptr(), padded.data_ptr(), row_src.data_ptr(),
-              gmap.data_ptr(), cap, arow.data_ptr(), info.data_ptr(), ws.data_ptr(), ws_bytes,
-              _lib.stream(dev))
+              gmap.data_ptr(), cap, arow.data_ptr(), info.data_ptr(), eto.data_ptr(),
+              ptpe.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream(dev))
     return Route(bin_ids[:A], indices[:A], tpe, bins, padded, row_src[:cap], gmap[:cap],
-                 arow[:A], info, cap, A, E, int(top_k))
+                 arow[:A], info, eto, ptpe, cap, A, E, int(top_k))
 
 
 def check_route(r: Route) -> tuple[int, int]:

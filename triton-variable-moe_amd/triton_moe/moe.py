@@ -155,14 +155,10 @@ class TritonMoEMLP(nn.Module):
         """Routing + expert MLP + combine on the HIP kernels, no host sync."""
         k = self.num_active_experts
         r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up")
-        device = x_flat.device
-        padded_bins = r.padded_bins
-        expert_token_offsets = torch.cat(
-            [torch.zeros(1, device=device, dtype=torch.int32), padded_bins])
-        padded_tokens_per_expert = torch.cat(
-            [padded_bins[:1], padded_bins[1:] - padded_bins[:-1]])
-        meta = GemmMeta(expert_token_offsets, self.expert_weight_offsets_t,
-                        self.expert_widths_t, padded_tokens_per_expert, self.num_experts,
+        # expert_token_offsets = [0, padded_bins] and the padded counts come
+        # out of the routing kernel (moe.py:193-202 of the reference).
+        meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
+                        self.expert_widths_t, r.padded_counts, self.num_experts,
                         self.max_expert_width, r.rows_bound)
         num_rows_dev = r.info[0:1]
         x_gathered = RoutedGatherOp.apply(x_flat, r.row_src, r.assignment_row, k, r.rows_bound,
@@ -274,13 +270,8 @@ class TritonMoEMLP(nn.Module):
         k = self.num_active_experts
         with profiler.step("fused_route"):
             r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up")
-            padded_bins = r.padded_bins
-            expert_token_offsets = torch.cat(
-                [torch.zeros(1, device=x.device, dtype=torch.int32), padded_bins])
-            padded_tokens_per_expert = torch.cat(
-                [padded_bins[:1], padded_bins[1:] - padded_bins[:-1]])
-            meta = GemmMeta(expert_token_offsets, self.expert_weight_offsets_t,
-                            self.expert_widths_t, padded_tokens_per_expert, self.num_experts,
+            meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
+                            self.expert_widths_t, r.padded_counts, self.num_experts,
                             self.max_expert_width, r.rows_bound)
             nrd = r.info[0:1]
         with profiler.step("gather"):
