@@ -92,6 +92,43 @@ int vmoe_row_maps(const int32_t* indices, const int32_t* bin_ids, const int32_t*
                   vmoe_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Router front end (TritonMoEMLP.forward, triton_moe/moe.py:166-182 and the
+ * auxiliary losses at moe.py:253-303).
+ * vmoe_router_topk: from bf16 router logits L [T, E] (row stride ld_logits)
+ *   p = sigmoid(float(L)); top_k of p per token, values descending, equal
+ *   values by ascending expert index; weights[t*k+j] = bf16(v_j / (sum v +
+ *   1e-20)) (normalize != 0) or bf16(v_j); selected_i32 / selected_i64 (either
+ *   may be NULL, not both) the expert ids; probs (nullable) p as fp32 [T, E];
+ *   lse [T] fp32 = bf16-rounded logsumexp_e L[t, e]; partial = per-workgroup
+ *   sums for vmoe_router_aux (vmoe_router_partial_floats(T, E) floats; the
+ *   row count is returned in *num_partial_rows). Limits: E <= 2048, k <= 64.
+ * vmoe_router_aux: after routing, z_loss (bf16), [load_balance, compute] (fp32
+ *   in losses[0..1]), f_i = bf16(tpe / sum tpe) (bf16 and fp32 copies) and
+ *   p_i = mean_t p [E] fp32. coef[e] is the load-balance weight of expert e:
+ *   E for uniform widths, 1 without expert groups, else
+ *   group_size / num_groups for experts in a group and 0 otherwise
+ *   (moe.py:276-303); widths_normalized is the module's buffer as fp32.
+ * vmoe_router_aux_bwd: grad_logits[t, e] = bf16(g_z 2 lse_t softmax(L[t])_e / T
+ *   + (g_lb coef_e f_e + g_cl wn_e) / T p (1 - p)); g_* are device fp32
+ *   scalars (nullable = 0). The top-k weights get no gradient (scatter.py:176).
+ * ---------------------------------------------------------------------- */
+size_t vmoe_router_partial_floats(int64_t num_tokens, int32_t num_experts);
+int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
+                     int32_t num_experts, int32_t top_k, int32_t normalize, uint16_t* weights,
+                     int32_t* selected_i32, int64_t* selected_i64, float* probs, float* lse,
+                     float* partial, size_t partial_floats, int32_t* num_partial_rows,
+                     vmoe_stream_t stream);
+int vmoe_router_aux(const float* partial, int32_t num_partial_rows, int64_t num_tokens,
+                    int32_t num_experts, const int32_t* tokens_per_expert, const float* coef,
+                    const float* widths_normalized, uint16_t* f_i, float* f_i_f32, float* p_i,
+                    uint16_t* z_loss, float* losses, vmoe_stream_t stream);
+int vmoe_router_aux_bwd(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
+                        int32_t num_experts, const float* lse, const float* f_i_f32,
+                        const float* coef, const float* widths_normalized, const float* grad_z,
+                        const float* grad_lb, const float* grad_cl, uint16_t* grad_logits,
+                        int64_t ld_grad, vmoe_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Token permutation (bf16).
  * vmoe_gather: out[r] = x[row_src[r] / top_k] (times weights[row_src[r]] when
  * weights != NULL, product rounded to bf16), zero where row_src[r] < 0.

@@ -63,6 +63,16 @@ def test_argument_checks_return_invalid_arg():
                                   None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_gather_tokens(1, 12, 1, 4, 2, None, 1, 1, 12, 4, None, 12,
                                   None) == _lib.ERR_UNSUPPORTED
+    # router: k > E is invalid, more than 2048 experts unsupported
+    assert lib.vmoe_router_topk(1, 8, 4, 8, 9, 1, 1, 1, None, None, 1, 1, 1 << 20, None,
+                                None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_router_topk(1, 4096, 4, 4096, 8, 1, 1, 1, None, None, 1, 1, 1 << 20, None,
+                                None) == _lib.ERR_UNSUPPORTED
+    assert lib.vmoe_router_topk(1, 8, 4, 8, 2, 1, 1, 1, None, None, 1, 1, 0, None,
+                                None) == _lib.ERR_WORKSPACE
+    assert lib.vmoe_router_partial_floats(16384, 64) % 65 == 0
+    assert lib.vmoe_router_aux(None, 1, 4, 8, None, None, None, None, None, None, None, None,
+                               None) == _lib.ERR_INVALID_ARG
     # unaligned hidden size is unsupported, not silently wrong
     assert lib.vmoe_gemm_up_fwd(None, 8, 0, None, None, 8, None, None, 8, 1, 1, 1, 1, 1, 4, 12,
                                 16, 64, None) == _lib.ERR_UNSUPPORTED

@@ -1,0 +1,398 @@
+// Router front end on gfx950: sigmoid, top-k, weight normalisation and the
+// auxiliary-loss reductions of TritonMoEMLP.forward, plus the gradient of
+// the auxiliary losses with respect to the router logits.
+//
+// Semantics (triton_moe/moe.py:166-182, 253-303 of the reference):
+//   p[t, e]   = sigmoid(float(L[t, e]))                    L = router logits (bf16)
+//   (v, s)    = topk(p[t], k): values descending; equal values are ordered
+//               by ascending expert index (torch leaves the tie order open)
+//   w[t, j]   = bf16(v_j / (sum_j v_j + 1e-20))  (norm) or bf16(v_j)
+//   z_loss    = bf16(mean_t bf16(bf16(logsumexp_e L[t, e])^2))
+//   p_i[e]    = mean_t p[t, e]
+//   f_i[e]    = bf16(tokens_per_expert[e] / sum tokens_per_expert)
+//   lb_loss   = sum_e coef[e] * f_i[e] * p_i[e]   (coef folds the reference's
+//               uniform / ungrouped / grouped formulas, moe.py:276-303)
+//   cl_loss   = sum_e wn[e] * p_i[e]  (= mean_t p[t] . wn, moe.py:266-268)
+// Gradients (the weights w get none, as in the reference, scatter.py:176):
+//   dL[t, e] = g_z * 2 lse_t softmax(L[t])[e] / T
+//            + (g_lb coef[e] f_i[e] + g_cl wn[e]) / T * p (1 - p)
+//
+// One wave per token: lane l holds experts l, l + 64, ... (VPL of them), so
+// the top-k is k rounds of a wave-wide arg-max over 64-bit keys
+// (value bits << 32 | ~expert), and the per-expert column sums of p stay in
+// registers until a fixed-order block reduction writes one partial row per
+// workgroup. The final sums run over those rows in a fixed order, so every
+// result is the same from run to run.
+
+#include <algorithm>
+
+#include "vmoe_common.h"
+
+namespace vmoe {
+namespace {
+
+constexpr int kRtThreads = 256;
+constexpr int kRtWaves = kRtThreads / kWave;
+constexpr int kRtMaxExperts = 2048;
+constexpr int kRtMaxBlocks = 1024;
+constexpr int kAuxThreads = 1024;
+constexpr int kAuxWaves = kAuxThreads / kWave;
+
+// Tokens whose logits a wave loads together before working on them (their
+// loads are in flight at once): 8 / (experts per lane), at least 1.
+template <int VPL>
+struct TokBatch {
+  static constexpr int value = VPL >= 8 ? 1 : 8 / VPL;
+};
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, off, kWave);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off, kWave);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// sigmoid as torch evaluates it for fp32 (1 / (1 + exp(-x)), precise exp).
+__device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Block b handles tokens [b * per, min(T, (b + 1) * per)); its waves take
+// batches of TB consecutive tokens in turn. partial[b][e] = sum of p[t][e]
+// over the block's tokens (e < E); partial[b][E] = sum of bf16(bf16(lse_t)^2).
+template <int VPL>
+__global__ __launch_bounds__(kRtThreads) void router_topk_kernel(
+    const uint16_t* __restrict__ logits, int64_t ldl, int64_t T, int E, int k, int norm,
+    uint16_t* __restrict__ weights, int32_t* __restrict__ selected32,
+    int64_t* __restrict__ selected64, float* __restrict__ probs, float* __restrict__ lse_out,
+    float* __restrict__ partial, int64_t per) {
+  constexpr int TB = TokBatch<VPL>::value;
+  __shared__ float red[kRtWaves][kRtMaxExperts + 1];
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  float col[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) col[v] = 0.0f;
+  float zsum = 0.0f;
+  const int64_t t_beg = (int64_t)blockIdx.x * per, t_end = min(T, t_beg + per);
+  for (int64_t tb = t_beg + (int64_t)wv * TB; tb < t_end; tb += (int64_t)kRtWaves * TB) {
+    float lgb[TB][VPL];
+#pragma unroll
+    for (int u = 0; u < TB; ++u)
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int e = lane + v * kWave;
+        lgb[u][v] = (tb + u < t_end && e < E) ? bf16_to_f32(logits[(tb + u) * ldl + e])
+                                               : -INFINITY;
+      }
+#pragma unroll
+    for (int u = 0; u < TB; ++u) {
+      const int64_t t = tb + u;
+      if (t >= t_end) break;
+      float p[VPL];
+      float m = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int e = lane + v * kWave;
+        m = fmaxf(m, lgb[u][v]);
+        p[v] = e < E ? sigmoidf(lgb[u][v]) : 0.0f;
+        col[v] += p[v];
+        if (probs && e < E) probs[t * E + e] = p[v];
+      }
+      // logsumexp in fp32, rounded to bf16 as torch.logsumexp on bf16 logits.
+      m = wave_max_f32(m);
+      float se = 0.0f;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+        if (lane + v * kWave < E) se += expf(lgb[u][v] - m);
+      se = wave_sum_f32(se);
+      const float lse = bf16_to_f32(f32_to_bf16(logf(se) + m));
+      if (lse_out && lane == 0) lse_out[t] = lse;
+      zsum += bf16_to_f32(f32_to_bf16(lse * lse));
+      // top-k: k rounds of a wave arg-max; keys order by value, then by the
+      // lower expert index. p >= 0, so its bits order like its value.
+      uint32_t taken = 0;
+      float my_v = 0.0f;
+      int my_e = 0;
+      float vsum = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+          const int e = lane + v * kWave;
+          if (e < E && !((taken >> v) & 1u)) {
+            const uint64_t key = ((uint64_t)__float_as_uint(p[v]) << 32) | (uint32_t)(~e);
+            best = key > best ? key : best;
+          }
+        }
+        best = wave_max_u64(best);
+        const int e_sel = (int)(~(uint32_t)best);
+        const float v_sel = __uint_as_float((uint32_t)(best >> 32));
+        if ((e_sel & (kWave - 1)) == lane) taken |= 1u << (e_sel / kWave);
+        if (lane == j) {
+          my_v = v_sel;
+          my_e = e_sel;
+        }
+        vsum += v_sel;  // j ascending
+      }
+      if (lane < k) {
+        const float wv_ = norm ? my_v / (vsum + 1e-20f) : my_v;
+        weights[t * k + lane] = (uint16_t)f32_to_bf16(wv_);
+        if (selected32) selected32[t * k + lane] = my_e;
+        if (selected64) selected64[t * k + lane] = my_e;
+      }
+    }
+  }
+  // Block partials: fixed order over waves.
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int e = lane + v * kWave;
+    if (e < E) red[wv][e] = col[v];
+  }
+  if (lane == 0) red[wv][E] = zsum;
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += kRtThreads) {
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kRtWaves; ++w) s += red[w][e];
+    partial[(int64_t)blockIdx.x * (E + 1) + e] = s;
+  }
+}
+
+// One workgroup: sums the block partials in a fixed order and forms the
+// losses: z_out (bf16) = z_loss, out_scalars[0] = load balance, [1] = compute
+// loss. Columns go 64 at a time (one per lane); wave w adds rows w, w + 16, ...
+// with 8 independent loads in flight, then the 16 wave sums are added in
+// wave order.
+__global__ __launch_bounds__(kAuxThreads) void router_aux_kernel(
+    const float* __restrict__ partial, int nblk, int64_t T, int E,
+    const int32_t* __restrict__ tokens_per_expert, const float* __restrict__ coef,
+    const float* __restrict__ wn, uint16_t* __restrict__ f_i, float* __restrict__ f_i32,
+    float* __restrict__ p_i, uint16_t* __restrict__ z_out, float* __restrict__ out_scalars) {
+  __shared__ float wsum[kAuxWaves][kWave];
+  __shared__ float sh_lb[kAuxThreads / kWave], sh_cl[kAuxThreads / kWave];
+  __shared__ long long sh_cnt[kAuxWaves];
+  __shared__ float sh_z;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  // total routed assignments
+  long long cnt = 0;
+  for (int e = tid; e < E; e += kAuxThreads) cnt += tokens_per_expert[e];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, kWave);
+  if (lane == 0) sh_cnt[wv] = cnt;
+  __syncthreads();
+  long long total_i = 0;
+#pragma unroll
+  for (int w = 0; w < kAuxWaves; ++w) total_i += sh_cnt[w];
+  const float total = (float)total_i;
+  const float invT = T > 0 ? 1.0f / (float)T : 0.0f;
+  float lb = 0.0f, cl = 0.0f;
+  for (int c0 = 0; c0 <= E; c0 += kWave) {
+    const int c = c0 + lane;
+    float s = 0.0f;
+    if (c <= E) {
+      float acc[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+      int b = wv;
+      for (; b + 7 * kAuxWaves < nblk; b += 8 * kAuxWaves) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += partial[(int64_t)(b + i * kAuxWaves) * (E + 1) + c];
+      }
+      for (int i = 0; b < nblk; b += kAuxWaves, ++i) acc[i] += partial[(int64_t)b * (E + 1) + c];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += acc[i];
+    }
+    wsum[wv][lane] = s;
+    __syncthreads();
+    if (wv == 0 && c <= E) {
+      float col = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kAuxWaves; ++w) col += wsum[w][lane];
+      if (c == E) {
+        sh_z = col;
+      } else {
+        const float pe = col * invT;
+        // f_i = (tpe.float() / tpe.sum()).to(bf16)
+        const float fe = bf16_to_f32(f32_to_bf16((float)tokens_per_expert[c] / total));
+        f_i[c] = (uint16_t)f32_to_bf16(fe);
+        f_i32[c] = fe;
+        p_i[c] = pe;
+        lb += coef[c] * fe * pe;
+        cl += wn[c] * pe;
+      }
+    }
+    __syncthreads();
+  }
+  if (wv == 0) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      lb += __shfl_xor(lb, off, kWave);
+      cl += __shfl_xor(cl, off, kWave);
+    }
+    if (lane == 0) {
+      *z_out = (uint16_t)f32_to_bf16(sh_z * invT);
+      out_scalars[0] = lb;
+      out_scalars[1] = cl;
+    }
+  }
+}
+
+// dL for every logit (one wave per token).
+template <int VPL>
+__global__ __launch_bounds__(kRtThreads) void router_aux_bwd_kernel(
+    const uint16_t* __restrict__ logits, int64_t ldl, int64_t T, int E,
+    const float* __restrict__ lse, const float* __restrict__ f_i32,
+    const float* __restrict__ coef, const float* __restrict__ wn,
+    const float* __restrict__ g_z, const float* __restrict__ g_lb,
+    const float* __restrict__ g_cl, uint16_t* __restrict__ grad, int64_t ldg) {
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  const float invT = 1.0f / (float)T;
+  const float gz = g_z ? *g_z : 0.0f, glb = g_lb ? *g_lb : 0.0f, gcl = g_cl ? *g_cl : 0.0f;
+  float ce[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int e = lane + v * kWave;
+    ce[v] = e < E ? (glb * coef[e] * f_i32[e] + gcl * wn[e]) * invT : 0.0f;
+  }
+  for (int64_t t = (int64_t)blockIdx.x * kRtWaves + wv; t < T;
+       t += (int64_t)gridDim.x * kRtWaves) {
+    const float l = lse[t];
+    const float zt = gz * 2.0f * l * invT;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int e = lane + v * kWave;
+      if (e >= E) continue;
+      const float x = bf16_to_f32(logits[t * ldl + e]);
+      const float p = sigmoidf(x);
+      const float d = zt * expf(x - l) + ce[v] * p * (1.0f - p);
+      grad[t * ldg + e] = (uint16_t)f32_to_bf16(d);
+    }
+  }
+}
+
+inline int router_blocks(int64_t T) {
+  // About 8 tokens per wave, at most kRtMaxBlocks partial rows.
+  const int64_t b = (T + 8 * kRtWaves - 1) / (8 * kRtWaves);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(b, kRtMaxBlocks));
+}
+
+inline int vpl_of(int E) {
+  int v = 1;
+  while (v * kWave < E) v <<= 1;
+  return v;
+}
+
+}  // namespace
+}  // namespace vmoe
+
+using namespace vmoe;
+
+extern "C" size_t vmoe_router_partial_floats(int64_t num_tokens, int32_t num_experts) {
+  if (num_tokens < 0 || num_experts <= 0) return 0;
+  return (size_t)router_blocks(num_tokens) * (size_t)(num_experts + 1);
+}
+
+extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
+                                int32_t num_experts, int32_t top_k, int32_t normalize,
+                                uint16_t* weights, int32_t* selected_i32, int64_t* selected_i64,
+                                float* probs, float* lse, float* partial, size_t partial_floats,
+                                int32_t* num_partial_rows, vmoe_stream_t stream) {
+  if (num_tokens < 0 || num_experts <= 0 || top_k <= 0 || top_k > num_experts ||
+      ld_logits < num_experts)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_experts > kRtMaxExperts || top_k > kWave) return VMOE_ERR_UNSUPPORTED;
+  if (!weights || !partial || !lse || (!selected_i32 && !selected_i64) ||
+      (num_tokens > 0 && !logits))
+    return VMOE_ERR_INVALID_ARG;
+  const int nblk = router_blocks(num_tokens);
+  if (partial_floats < (size_t)nblk * (size_t)(num_experts + 1)) return VMOE_ERR_WORKSPACE;
+  if (num_partial_rows) *num_partial_rows = nblk;
+  const int64_t per = (num_tokens + nblk - 1) / nblk;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (vpl_of(num_experts)) {
+#define VMOE_RT_CASE(V)                                                                      \
+  case V:                                                                                    \
+    hipLaunchKernelGGL(router_topk_kernel<V>, dim3(nblk), dim3(kRtThreads), 0, s, logits,    \
+                       ld_logits, num_tokens, num_experts, top_k, normalize, weights,         \
+                       selected_i32, selected_i64, probs, lse, partial, per);                \
+    break;
+    VMOE_RT_CASE(1)
+    VMOE_RT_CASE(2)
+    VMOE_RT_CASE(4)
+    VMOE_RT_CASE(8)
+    VMOE_RT_CASE(16)
+    VMOE_RT_CASE(32)
+#undef VMOE_RT_CASE
+    default:
+      return VMOE_ERR_UNSUPPORTED;
+  }
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_router_aux(const float* partial, int32_t num_partial_rows,
+                               int64_t num_tokens, int32_t num_experts,
+                               const int32_t* tokens_per_expert, const float* coef,
+                               const float* widths_normalized, uint16_t* f_i, float* f_i_f32,
+                               float* p_i, uint16_t* z_loss, float* losses,
+                               vmoe_stream_t stream) {
+  if (num_partial_rows <= 0 || num_tokens < 0 || num_experts <= 0) return VMOE_ERR_INVALID_ARG;
+  if (!partial || !tokens_per_expert || !coef || !widths_normalized || !f_i || !f_i_f32 ||
+      !p_i || !z_loss || !losses)
+    return VMOE_ERR_INVALID_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(router_aux_kernel, dim3(1), dim3(kAuxThreads), 0, s, partial,
+                     num_partial_rows, num_tokens, num_experts, tokens_per_expert, coef,
+                     widths_normalized, f_i, f_i_f32, p_i, z_loss, losses);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_router_aux_bwd(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
+                                   int32_t num_experts, const float* lse, const float* f_i_f32,
+                                   const float* coef, const float* widths_normalized,
+                                   const float* grad_z, const float* grad_lb,
+                                   const float* grad_cl, uint16_t* grad_logits, int64_t ld_grad,
+                                   vmoe_stream_t stream) {
+  if (num_tokens < 0 || num_experts <= 0 || ld_logits < num_experts || ld_grad < num_experts)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_experts > kRtMaxExperts) return VMOE_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return VMOE_OK;
+  if (!logits || !lse || !f_i_f32 || !coef || !widths_normalized || !grad_logits)
+    return VMOE_ERR_INVALID_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t g = std::min<int64_t>((num_tokens + kRtWaves - 1) / kRtWaves, 4096);
+  switch (vpl_of(num_experts)) {
+#define VMOE_RB_CASE(V)                                                                       \
+  case V:                                                                                     \
+    hipLaunchKernelGGL(router_aux_bwd_kernel<V>, dim3((unsigned)g), dim3(kRtThreads), 0, s,   \
+                       logits, ld_logits, num_tokens, num_experts, lse, f_i_f32, coef,         \
+                       widths_normalized, grad_z, grad_lb, grad_cl, grad_logits, ld_grad);    \
+    break;
+    VMOE_RB_CASE(1)
+    VMOE_RB_CASE(2)
+    VMOE_RB_CASE(4)
+    VMOE_RB_CASE(8)
+    VMOE_RB_CASE(16)
+    VMOE_RB_CASE(32)
+#undef VMOE_RB_CASE
+    default:
+      return VMOE_ERR_UNSUPPORTED;
+  }
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}

@@ -48,11 +48,18 @@ _SIGNATURES = {
     "vmoe_gemm_down_bwd_dw": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
                               _i64, _i64, _vp, ctypes.c_size_t, _vp],
     "vmoe_zero_tail_cols": [_vp, _i64, _vp, _vp, _i32, _i64, _i64, _vp],
+    "vmoe_router_partial_floats": [_i64, _i32],
+    "vmoe_router_topk": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                         ctypes.c_size_t, _vp, _vp],
+    "vmoe_router_aux": [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "vmoe_router_aux_bwd": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                            _vp],
 }
 _RESTYPES = {
     "vmoe_status_string": ctypes.c_char_p,
     "vmoe_route_workspace_bytes": ctypes.c_size_t,
     "vmoe_gemm_dw_workspace_bytes": ctypes.c_size_t,
+    "vmoe_router_partial_floats": ctypes.c_size_t,
 }
 
 # Status codes (include/vmoe.h).

@@ -1,0 +1,121 @@
+"""Router front end on the gfx950 router kernels (csrc/router.hip).
+
+The reference computes, in TritonMoEMLP.forward (triton_moe/moe.py:166-182,
+253-303), sigmoid -> torch.topk -> normalise -> bf16 for the routing, and
+logsumexp / mean / matmul chains for the auxiliary losses: about thirty
+PyTorch launches per step. Here one kernel does the routing and the
+per-token reductions, and one single-workgroup kernel finishes the losses
+after the routing counts exist. The losses are differentiable with respect
+to the router logits (their gradient is one elementwise kernel); the top-k
+weights are not, as in the reference (scatter.py:176).
+
+Top-k order: values descending; equal values by ascending expert index
+(torch.topk leaves the order of equal values unspecified).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch.amp import custom_bwd, custom_fwd
+from torch.autograd.function import once_differentiable
+
+from .. import _lib
+
+
+@dataclass
+class RouterState:
+    """Outputs of router_topk."""
+
+    weights: torch.Tensor      # [T, k] bf16 (normalised when requested)
+    selected: torch.Tensor     # [T, k] int32 or int64 expert ids
+    probs: torch.Tensor | None  # [T, E] fp32 sigmoid(logits), when requested
+    lse: torch.Tensor          # [T] fp32, bf16-rounded logsumexp of each row
+    partial: torch.Tensor      # per-workgroup sums for the auxiliary losses
+    partial_rows: int
+
+
+def router_topk(logits: torch.Tensor, top_k: int, normalize: bool = True,
+                want_probs: bool = False, index_dtype=torch.int32) -> RouterState:
+    """sigmoid + top-k + normalisation of bf16 router logits [T, E] (no host sync)."""
+    _lib.require_gpu(logits)
+    if logits.dtype != torch.bfloat16:
+        raise NotImplementedError(f"router logits must be bfloat16 (got {logits.dtype})")
+    if logits.dim() != 2 or logits.stride(-1) != 1:
+        logits = logits.reshape(-1, logits.shape[-1]).contiguous()
+    T, E = logits.shape
+    dev = logits.device
+    nfl = int(_lib.lib().vmoe_router_partial_floats(T, E))
+    rows = nfl // (E + 1)
+    f32 = torch.float32
+    weights = torch.empty(T, top_k, dtype=torch.bfloat16, device=dev)
+    selected = torch.empty(T, top_k, dtype=index_dtype, device=dev)
+    probs = torch.empty(T, E, dtype=f32, device=dev) if want_probs else None
+    scratch = torch.empty(T + nfl, dtype=f32, device=dev)
+    lse, partial = scratch[:T], scratch[T:]
+    is64 = index_dtype == torch.int64
+    _lib.call("vmoe_router_topk", logits.data_ptr(), logits.stride(0), T, E, int(top_k),
+              int(bool(normalize)), weights.data_ptr(), None if is64 else selected.data_ptr(),
+              selected.data_ptr() if is64 else None, _lib.ptr(probs), lse.data_ptr(),
+              partial.data_ptr(), nfl, None, _lib.stream(dev))
+    return RouterState(weights, selected, probs, lse, partial, rows)
+
+
+class RouterAuxOp(torch.autograd.Function):
+    """(z_loss, load_balance_loss, compute_loss, f_i) from the router state and
+    the routing counts; backward gives the router-logit gradient."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, logits, lse, partial, partial_rows, tokens_per_expert, coef, wn):
+        T, E = logits.shape
+        dev = logits.device
+        f_i = torch.empty(E, dtype=torch.bfloat16, device=dev)
+        f32 = torch.empty(2 * E + 2, dtype=torch.float32, device=dev)
+        f_i32, p_i, losses = f32[:E], f32[E:2 * E], f32[2 * E:]
+        z = torch.empty((), dtype=torch.bfloat16, device=dev)
+        tpe = tokens_per_expert.to(torch.int32).contiguous()
+        _lib.call("vmoe_router_aux", partial.data_ptr(), int(partial_rows), T, E,
+                  tpe.data_ptr(), coef.data_ptr(), wn.data_ptr(), f_i.data_ptr(),
+                  f_i32.data_ptr(), p_i.data_ptr(), z.data_ptr(), losses.data_ptr(),
+                  _lib.stream(dev))
+        ctx.save_for_backward(logits, lse, f_i32, coef, wn)
+        ctx.mark_non_differentiable(f_i)
+        return z, losses[0], losses[1], f_i
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, g_z, g_lb, g_cl, _g_fi):
+        logits, lse, f_i32, coef, wn = ctx.saved_tensors
+        T, E = logits.shape
+
+        def scalar(g):
+            return None if g is None else g.detach().to(torch.float32).reshape(()).contiguous()
+
+        gz, glb, gcl = scalar(g_z), scalar(g_lb), scalar(g_cl)
+        grad = torch.empty_like(logits)
+        _lib.call("vmoe_router_aux_bwd", logits.data_ptr(), logits.stride(0), T, E,
+                  lse.data_ptr(), f_i32.data_ptr(), coef.data_ptr(), wn.data_ptr(),
+                  _lib.ptr(gz), _lib.ptr(glb), _lib.ptr(gcl), grad.data_ptr(), grad.stride(0),
+                  _lib.stream(logits.device))
+        return grad, None, None, None, None, None, None
+
+
+def load_balance_coef(expert_sizes) -> list[float]:
+    """Per-expert weights that turn the reference's three load-balance formulas
+    (moe.py:276-303) into one dot product sum_e coef[e] f_i[e] p_i[e]:
+    uniform widths -> E; no group with more than one expert -> 1; otherwise
+    group_size / num_groups for experts of a group, 0 for lone experts."""
+    widths = [w for c, w in expert_sizes for _ in range(c)]
+    E = len(widths)
+    if len(set(widths)) == 1:
+        return [float(E)] * E
+    groups = [c for c, _ in expert_sizes if c > 1]
+    if not groups:
+        return [1.0] * E
+    coef = []
+    for c, _w in expert_sizes:
+        coef += [float(c) / len(groups) if c > 1 else 0.0] * c
+    return coef

@@ -5,13 +5,14 @@ TritonMoEMLP (:42-518) with the same constructor (parameter names, shapes,
 init order router -> w1 -> w2, buffers), forward returning
 (output, aux_loss, f_i), forward_with_intermediates and forward_profiled.
 
-The router Linear, sigmoid, top-k, weight normalisation and auxiliary losses
-stay in PyTorch as in the reference (moe.py:166-182, 253-274). Everything
-between them runs on libvmoe.so: routing (counting sort + scans + maps),
-gather, grouped up GEMM with fused relu^2, grouped down GEMM and weighted
-combine, and their backward. The forward and backward issue no host sync:
-buffers are sized from an upper bound of the padded row count and the kernels
-read the true counts on the device.
+The router Linear stays a PyTorch (hipBLASLt) GEMM. Everything after it runs
+on libvmoe.so: sigmoid / top-k / normalisation and the auxiliary-loss
+reductions (one router kernel, moe.py:166-182, 253-303 of the reference),
+routing (counting sort + scans + maps), gather, grouped up GEMM with fused
+relu^2, grouped down GEMM and weighted combine, and their backward. The
+forward and backward issue no host sync: buffers are sized from an upper
+bound of the padded row count and the kernels read the true counts on the
+device.
 """
 
 from __future__ import annotations
@@ -34,6 +35,7 @@ from .kernels import (
 from .kernels.fused_cumsum import route_device
 from .kernels.gather import RoutedGatherOp
 from .kernels.grouped_gemm import GemmMeta, RoutedExpertsOp
+from .kernels.router import RouterAuxOp, load_balance_coef, router_topk
 from .kernels.scatter import RoutedScatterOp
 
 
@@ -125,31 +127,40 @@ class TritonMoEMLP(nn.Module):
                                  persistent=False)
 
     # ------------------------------------------------------------------
-    # routing front end (PyTorch, as in the reference moe.py:166-182)
+    # routing front end (moe.py:166-182 of the reference) on the router kernel
     # ------------------------------------------------------------------
 
     def _router(self, x_flat: torch.Tensor):
+        """(router_logits, router_probs fp32, top_k_weights bf16, selected_experts
+        int64), the reference's four routing tensors."""
         router_logits = self.router(x_flat)
-        router_probs = F.sigmoid(router_logits.float())
-        top_k_weights, selected_experts = torch.topk(
-            router_probs, self.num_active_experts, dim=-1)
-        if self.norm_topk_prob:
-            top_k_weights = top_k_weights / (top_k_weights.sum(dim=-1, keepdim=True) + 1e-20)
-        top_k_weights = top_k_weights.to(x_flat.dtype)
-        return router_logits, router_probs, top_k_weights, selected_experts
+        st = router_topk(router_logits, self.num_active_experts, self.norm_topk_prob,
+                         want_probs=True, index_dtype=torch.int64)
+        return router_logits, st.probs, st.weights.to(x_flat.dtype), st.selected
 
-    def _aux(self, router_logits, router_probs, tokens_per_expert, dtype):
-        router_z_loss = torch.logsumexp(router_logits, dim=-1).pow(2).mean()
-        f_i = (tokens_per_expert.float() / tokens_per_expert.sum()).to(dtype)
-        load_balance_loss = self._compute_load_balance_loss(router_probs, f_i)
-        compute_loss = (
-            router_probs @ self.expert_widths_normalized.to(router_probs.dtype)).mean()
+    def _aux_tables(self, device):
+        """fp32 load-balance coefficients and normalised widths on `device`."""
+        key = (str(device), self.expert_widths_normalized.dtype)
+        cache = getattr(self, "_aux_cache", None)
+        if cache is None or cache[0] != key:
+            coef = torch.tensor(load_balance_coef(self.config.expert_sizes),
+                                dtype=torch.float32, device=device)
+            wn = self.expert_widths_normalized.to(device=device, dtype=torch.float32)
+            self._aux_cache = cache = (key, coef, wn)
+        return cache[1], cache[2]
+
+    def _aux(self, router_logits, state, tokens_per_expert, dtype):
+        """router_z_loss, load_balance_loss, compute_loss and f_i
+        (moe.py:253-303), differentiable with respect to the router logits."""
+        coef, wn = self._aux_tables(router_logits.device)
+        z, lb, cl, f_i = RouterAuxOp.apply(router_logits, state.lse, state.partial,
+                                           state.partial_rows, tokens_per_expert, coef, wn)
         aux_loss = {
-            "router_z_loss": router_z_loss,
-            "load_balance_loss": load_balance_loss,
-            "compute_loss": compute_loss,
+            "router_z_loss": z,
+            "load_balance_loss": lb,
+            "compute_loss": cl,
         }
-        return aux_loss, f_i
+        return aux_loss, f_i.to(dtype)
 
     def _experts(self, x_flat, top_k_weights_flat, selected_experts_flat):
         """Routing + expert MLP + combine on the HIP kernels, no host sync."""
@@ -177,17 +188,18 @@ class TritonMoEMLP(nn.Module):
         """x [batch, seq, n_embd] -> (output [batch, seq, n_embd], aux_loss dict, f_i)."""
         batch_size, _seq_len, _n_embd = x.shape
         x_flat = rearrange(x, "b s d -> (b s) d")
-        router_logits, router_probs, top_k_weights, selected_experts = self._router(x_flat)
-        top_k_weights_flat = rearrange(top_k_weights, "... -> (...)")
-        selected_experts_flat = rearrange(selected_experts, "... -> (...)")
+        router_logits = self.router(x_flat)
+        state = router_topk(router_logits, self.num_active_experts, self.norm_topk_prob)
         output_flat, tokens_per_expert = self._experts(
-            x_flat, top_k_weights_flat, selected_experts_flat)
+            x_flat, state.weights.reshape(-1), state.selected.reshape(-1))
         output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
-        aux_loss, f_i = self._aux(router_logits, router_probs, tokens_per_expert, x.dtype)
+        aux_loss, f_i = self._aux(router_logits, state, tokens_per_expert, x.dtype)
         return output, aux_loss, f_i
 
     def _compute_load_balance_loss(self, router_probs: torch.Tensor,
                                    f_i: torch.Tensor) -> torch.Tensor:
+        # Kept with the reference's formula (the module itself uses the router
+        # kernel's equivalent coefficient form, kernels/router.py).
         """Load balance loss within expert groups (reference moe.py:276-303)."""
         p_i = router_probs.mean(dim=0)
         if len(set(self.expert_widths)) == 1:
@@ -264,9 +276,10 @@ class TritonMoEMLP(nn.Module):
         with profiler.step("flatten"):
             x_flat = rearrange(x, "b s d -> (b s) d")
         with profiler.step("routing"):
-            router_logits, router_probs, top_k_weights, selected_experts = self._router(x_flat)
-            top_k_weights_flat = rearrange(top_k_weights, "... -> (...)")
-            selected_experts_flat = rearrange(selected_experts, "... -> (...)")
+            router_logits = self.router(x_flat)
+            state = router_topk(router_logits, self.num_active_experts, self.norm_topk_prob)
+            top_k_weights_flat = state.weights.reshape(-1)
+            selected_experts_flat = state.selected.reshape(-1)
         k = self.num_active_experts
         with profiler.step("fused_route"):
             r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up")
@@ -291,6 +304,5 @@ class TritonMoEMLP(nn.Module):
         with profiler.step("reshape"):
             output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
         with profiler.step("aux_loss"):
-            aux_loss, f_i = self._aux(router_logits, router_probs, r.tokens_per_expert,
-                                      x.dtype)
+            aux_loss, f_i = self._aux(router_logits, state, r.tokens_per_expert, x.dtype)
         return output, aux_loss, f_i
