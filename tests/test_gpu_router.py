@@ -118,7 +118,7 @@ def test_aux_losses_vs_oracle(name, device):
     # relative); the other two are fp32 sums of the same terms.
     for key, tol in (("router_z_loss", 1e-2), ("load_balance_loss", 1e-4),
                      ("compute_loss", 1e-4)):
-        got, want = float(aux[key]), float(ref[key])
+        got, want = float(aux[key].detach()), float(ref[key])
         assert abs(got - want) <= tol * abs(want) + 1e-7, (key, got, want)
     # the coefficient form equals the reference's three formulas
     coef = torch.tensor(load_balance_coef(sizes), dtype=torch.float64)

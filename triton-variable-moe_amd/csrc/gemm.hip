@@ -65,8 +65,6 @@ constexpr int kConsumers = 8;
 constexpr int kProducers = 4;
 constexpr int kWaves = kConsumers + kProducers;
 constexpr int kThreads = kWaves * 64;
-constexpr int kBK = 32;        // k per LDS stage: two 16-deep MFMA steps
-constexpr int kStages = 4;     // LDS ring: kStages - 1 k-tiles in flight
 constexpr int kMaxExperts = 2048;  // per-expert work prefix held in LDS
 constexpr int kRecExperts = 512;   // per-expert metadata also held in LDS up to this E
 constexpr int kRedThreads = 256;   // split-K reduction kernel
@@ -240,11 +238,19 @@ struct Traits<DOWN_DW> {
 // dW GEMMs split their long K (the expert's rows) into chunks and accumulate
 // a tile across consecutive chunks ("contig"); the row-tiled GEMMs deal
 // items round-robin.
+//
+// k per LDS stage (BK) and ring depth. A K-contiguous ("K-form") operand row
+// of a stage is BK * 2 bytes; 128-byte rows (BK = 64) would halve the L2
+// requests per byte, but within the LDS budget they allow only a 2-deep
+// ring of 48 KiB stages, and that measured slower on every variant than
+// BK = 32 in a 4-deep ring of 24 KiB stages (the per-stage wait is exposed).
 template <int V>
 struct Cfg {
   static constexpr int BM = 128, BN = 256;
   static constexpr int WGM = 2, WGN = 4;
   static constexpr bool contig = V == UP_DW || V == DOWN_DW;
+  static constexpr int BK = 32;
+  static constexpr int STAGES = 4;
 };
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
@@ -389,7 +395,7 @@ struct Gemm {
   static constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN;
   static constexpr int WGM = Cfg<V>::WGM, WGN = Cfg<V>::WGN;
   static_assert(WGM * WGN == kConsumers, "one consumer wave per wave-grid cell");
-  static constexpr int BK = kBK;
+  static constexpr int BK = Cfg<V>::BK, kStages = Cfg<V>::STAGES;
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
   static constexpr int FM = WM / 32, FN = WN / 32;    // 32x32 blocks per wave
   static constexpr int A_STAGE = BM * BK * 2, B_STAGE = BN * BK * 2;  // bytes
@@ -410,13 +416,17 @@ struct Gemm {
   __device__ static int pwave() { return (threadIdx.x >> 6) - kConsumers; }
 
   // LDS is 64 banks x 4 bytes; a ds_read_b128 serves 16 lanes per cycle and
-  // a ds_read_b64_tr_b16 32 lanes per cycle. K-form: the 16 rows one phase
-  // reads sit four to a 256-byte bank line, so the chunk is XORed with
-  // (row / 4) to spread the four rows sharing a 64-byte slot. T-form: one
-  // phase reads k-rows k..k+3 at two column offsets 32 bytes apart, so the
-  // chunk is XORed with 4 * (k % 4) (distinct 64-byte slots per k-row) and
-  // with 2 * ((k / 8) % 2) for the other phase's k-rows.
-  __device__ static int kswz(int r) { return (r >> 2) & 3; }
+  // a ds_read_b64_tr_b16 32 lanes per cycle. K-form: a row is KCH 16-byte
+  // chunks and the 16 rows one phase reads share 256-byte bank lines
+  // (KCH = 4: four rows per line; KCH = 8: two), so the chunk is XORed with
+  // (row / (16 / KCH)) mod KCH to give the 16 rows distinct 16-byte slots.
+  // T-form: one phase reads k-rows k..k+3 at two column offsets 32 bytes
+  // apart, so the chunk is XORed with 4 * (k % 4) (distinct 64-byte slots
+  // per k-row) and with 2 * ((k / 8) % 2) for the other phase's k-rows.
+  static constexpr int KCH = BK * 2 / 16;  // 16-byte chunks per K-form row
+  static constexpr int KRPI = 64 / KCH;    // K-form rows per DMA instruction
+  static_assert(KCH == 4 || KCH == 8, "K-form rows of 64 or 128 bytes");
+  __device__ static int kswz(int r) { return KCH == 4 ? (r >> 2) & 3 : (r >> 1) & 7; }
   __device__ static int tswz(int k) { return ((k & 3) << 2) | (((k >> 3) & 1) << 1); }
   static_assert(BM >= 128 && BN >= 128, "T-form swizzle needs 16 chunks per k-row");
 
@@ -456,8 +466,8 @@ struct Gemm {
     s.ld2 = (uint32_t)(ld * 2);
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-      const int row = (wave * PW + i) * 16 + (lane >> 2);
-      const int c = (lane & 3) ^ kswz(row);
+      const int row = (wave * PW + i) * KRPI + lane / KCH;
+      const int c = (lane % KCH) ^ kswz(row);
       bool ok = row < rows_valid;
       int64_t srow = row;
       if (T::k_map && map && ok) {
@@ -551,7 +561,8 @@ struct Gemm {
     const int lane = threadIdx.x & 63;
     const int row = row0 + (lane & 31);
     const int c = 2 * ks + (lane >> 5);
-    return *reinterpret_cast<const lds_bf16x8*>(stage + row * 64 + ((c ^ kswz(row)) << 4));
+    return *reinterpret_cast<const lds_bf16x8*>(stage + row * (BK * 2) +
+                                                ((c ^ kswz(row)) << 4));
   }
 
   // Fragment of columns [col0, col0 + 32) x k-step ks from a T-form stage of
