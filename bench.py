@@ -243,7 +243,13 @@ def kernel_breakdown(m, xb, sel, reps):
                   gy.stride(0), gw.data_ptr(), gw.stride(0), *gg._meta_args(meta), d,
                   meta.max_width, meta.rows, ws.data_ptr(), ws.numel(), _lib.stream(x.device))
 
+    from triton_moe.kernels.router import router_topk
+
+    with torch.no_grad():
+        logits = m.router(x)
+
     ops = {
+        "router_topk": lambda: router_topk(logits, k, m.norm_topk_prob),
         "route": lambda: route_device(selv, E, k, b),
         "gather": lambda: gather_rows(x, r.row_src, k, r.rows_bound, num_rows_dev=nrd,
                                       assignment_row=ar),

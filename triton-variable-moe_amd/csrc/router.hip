@@ -31,41 +31,81 @@
 namespace vmoe {
 namespace {
 
-constexpr int kRtThreads = 256;
+constexpr int kRtThreads = 256;   // aux backward
 constexpr int kRtWaves = kRtThreads / kWave;
+
+// Top-k workgroup: 16 waves (many tokens in flight per CU) while a lane's
+// experts fit in the 128 registers that leaves a wave; 4 waves beyond.
+__host__ __device__ constexpr int topk_threads(int vpl) { return vpl <= 8 ? 1024 : 256; }
 constexpr int kRtMaxExperts = 2048;
 constexpr int kRtMaxBlocks = 1024;
 constexpr int kAuxThreads = 1024;
 constexpr int kAuxWaves = kAuxThreads / kWave;
 
 // Tokens whose logits a wave loads together before working on them (their
-// loads are in flight at once): 8 / (experts per lane), at least 1.
+// loads are in flight at once).
 template <int VPL>
 struct TokBatch {
-  static constexpr int value = VPL >= 8 ? 1 : 8 / VPL;
+  static constexpr int value = VPL >= 4 ? 1 : 2;
 };
 
+// Wave-wide reductions on DPP moves (no LDS round trip): xor 1 and xor 2
+// inside quads, the half-row and row mirrors, then row broadcasts 15 and 31
+// leave the full result in lane 63, which is read back for every lane.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp(uint32_t old, uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+constexpr int kDppBcast15 = 0x142;
+constexpr int kDppBcast31 = 0x143;
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint64_t max_step_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  const uint64_t o = ((uint64_t)dpp<CTRL, ROW_MASK>(hi, hi) << 32) | dpp<CTRL, ROW_MASK>(lo, lo);
+  return o > v ? o : v;
+}
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, off, kWave);
-    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off, kWave);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = o > v ? o : v;
-  }
-  return v;
+  v = max_step_u64<kDppXor1>(v);
+  v = max_step_u64<kDppXor2>(v);
+  v = max_step_u64<kDppHalfMirror>(v);
+  v = max_step_u64<kDppMirror>(v);
+  v = max_step_u64<kDppBcast15, 0xA>(v);
+  v = max_step_u64<kDppBcast31, 0xC>(v);
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float fdpp(float v) {
+  return __uint_as_float(dpp<CTRL, ROW_MASK>(__float_as_uint(v), __float_as_uint(v)));
 }
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  v += fdpp<kDppXor1>(v);
+  v += fdpp<kDppXor2>(v);
+  v += fdpp<kDppHalfMirror>(v);
+  v += fdpp<kDppMirror>(v);
+  // rows outside the mask keep their value and add 0
+  v += __uint_as_float(dpp<kDppBcast15, 0xA>(0u, __float_as_uint(v)));
+  v += __uint_as_float(dpp<kDppBcast31, 0xC>(0u, __float_as_uint(v)));
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
+  v = fmaxf(v, fdpp<kDppXor1>(v));
+  v = fmaxf(v, fdpp<kDppXor2>(v));
+  v = fmaxf(v, fdpp<kDppHalfMirror>(v));
+  v = fmaxf(v, fdpp<kDppMirror>(v));
+  v = fmaxf(v, fdpp<kDppBcast15, 0xA>(v));
+  v = fmaxf(v, fdpp<kDppBcast31, 0xC>(v));
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
 }
 
 // sigmoid as torch evaluates it for fp32 (1 / (1 + exp(-x)), precise exp).
@@ -75,20 +115,21 @@ __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(
 // batches of TB consecutive tokens in turn. partial[b][e] = sum of p[t][e]
 // over the block's tokens (e < E); partial[b][E] = sum of bf16(bf16(lse_t)^2).
 template <int VPL>
-__global__ __launch_bounds__(kRtThreads) void router_topk_kernel(
+__global__ __launch_bounds__(topk_threads(VPL)) void router_topk_kernel(
     const uint16_t* __restrict__ logits, int64_t ldl, int64_t T, int E, int k, int norm,
     uint16_t* __restrict__ weights, int32_t* __restrict__ selected32,
     int64_t* __restrict__ selected64, float* __restrict__ probs, float* __restrict__ lse_out,
     float* __restrict__ partial, int64_t per) {
   constexpr int TB = TokBatch<VPL>::value;
-  __shared__ float red[kRtWaves][kRtMaxExperts + 1];
+  constexpr int NW = topk_threads(VPL) / kWave;
+  extern __shared__ float red[];  // [NW][E + 1]
   const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
   float col[VPL];
 #pragma unroll
   for (int v = 0; v < VPL; ++v) col[v] = 0.0f;
   float zsum = 0.0f;
   const int64_t t_beg = (int64_t)blockIdx.x * per, t_end = min(T, t_beg + per);
-  for (int64_t tb = t_beg + (int64_t)wv * TB; tb < t_end; tb += (int64_t)kRtWaves * TB) {
+  for (int64_t tb = t_beg + (int64_t)wv * TB; tb < t_end; tb += (int64_t)NW * TB) {
     float lgb[TB][VPL];
 #pragma unroll
     for (int u = 0; u < TB; ++u)
@@ -160,14 +201,14 @@ __global__ __launch_bounds__(kRtThreads) void router_topk_kernel(
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int e = lane + v * kWave;
-    if (e < E) red[wv][e] = col[v];
+    if (e < E) red[wv * (E + 1) + e] = col[v];
   }
-  if (lane == 0) red[wv][E] = zsum;
+  if (lane == 0) red[wv * (E + 1) + E] = zsum;
   __syncthreads();
-  for (int e = threadIdx.x; e <= E; e += kRtThreads) {
+  for (int e = threadIdx.x; e <= E; e += NW * kWave) {
     float s = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kRtWaves; ++w) s += red[w][e];
+    for (int w = 0; w < NW; ++w) s += red[w * (E + 1) + e];
     partial[(int64_t)blockIdx.x * (E + 1) + e] = s;
   }
 }
@@ -284,16 +325,17 @@ __global__ __launch_bounds__(kRtThreads) void router_aux_bwd_kernel(
   }
 }
 
-inline int router_blocks(int64_t T) {
-  // About 8 tokens per wave, at most kRtMaxBlocks partial rows.
-  const int64_t b = (T + 8 * kRtWaves - 1) / (8 * kRtWaves);
-  return (int)std::max<int64_t>(1, std::min<int64_t>(b, kRtMaxBlocks));
-}
-
 inline int vpl_of(int E) {
   int v = 1;
   while (v * kWave < E) v <<= 1;
   return v;
+}
+
+inline int router_blocks(int64_t T, int E) {
+  // About 2 tokens per wave, at most kRtMaxBlocks partial rows.
+  const int per = 2 * topk_threads(vpl_of(E)) / kWave;
+  const int64_t b = (T + per - 1) / per;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(b, kRtMaxBlocks));
 }
 
 }  // namespace
@@ -303,7 +345,7 @@ using namespace vmoe;
 
 extern "C" size_t vmoe_router_partial_floats(int64_t num_tokens, int32_t num_experts) {
   if (num_tokens < 0 || num_experts <= 0) return 0;
-  return (size_t)router_blocks(num_tokens) * (size_t)(num_experts + 1);
+  return (size_t)router_blocks(num_tokens, num_experts) * (size_t)(num_experts + 1);
 }
 
 extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
@@ -318,15 +360,18 @@ extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64
   if (!weights || !partial || !lse || (!selected_i32 && !selected_i64) ||
       (num_tokens > 0 && !logits))
     return VMOE_ERR_INVALID_ARG;
-  const int nblk = router_blocks(num_tokens);
+  const int nblk = router_blocks(num_tokens, num_experts);
   if (partial_floats < (size_t)nblk * (size_t)(num_experts + 1)) return VMOE_ERR_WORKSPACE;
   if (num_partial_rows) *num_partial_rows = nblk;
   const int64_t per = (num_tokens + nblk - 1) / nblk;
+  const int vpl = vpl_of(num_experts);
+  const size_t lds = sizeof(float) * (topk_threads(vpl) / kWave) * (num_experts + 1);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (vpl_of(num_experts)) {
+  switch (vpl) {
 #define VMOE_RT_CASE(V)                                                                      \
   case V:                                                                                    \
-    hipLaunchKernelGGL(router_topk_kernel<V>, dim3(nblk), dim3(kRtThreads), 0, s, logits,    \
+    hipLaunchKernelGGL(router_topk_kernel<V>, dim3(nblk), dim3(topk_threads(V)), lds, s,      \
+                       logits,                                                                \
                        ld_logits, num_tokens, num_experts, top_k, normalize, weights,         \
                        selected_i32, selected_i64, probs, lse, partial, per);                \
     break;
