@@ -7,9 +7,10 @@ logits biased by a Zipf(s=1.2) rank profile (alpha = smallest integer giving an
 empty expert and a hottest expert above 4x the mean). Synthetic data: one CPU
 torch.Generator(0) draws x ~ N(0,1), then router, w1, w2 ~ N(0, 0.02).
 
-A step is one forward + out.sum().backward() of the layer (routing, gather,
-grouped GEMM up + relu^2, grouped GEMM down, weighted combine and the full
-backward including both dW GEMMs).
+A step is one forward + out.sum().backward() of the layer (router, routing,
+token gather (fused into the up GEMM's operand staging), grouped GEMM up +
+relu^2, grouped GEMM down, weighted combine and the full backward including
+both dW GEMMs).
 
 Prints one JSON line: value = grouped-GEMM TFLOP/s of the whole step
 (12 * d * sum_e n_e * w_e over the step's wall time), plus ms_per_step, the
@@ -71,17 +72,18 @@ GEMM_SYMBOL = {
 }
 
 
-def gemm_bytes(op, A, d, nw, W):
+def gemm_bytes(op, A, T, d, nw, W):
     """Minimal unique HBM bytes of one GEMM launch (bf16): its operands read
-    once and its outputs written once. A = routed rows, nw = sum_e n_e w_e,
-    W = total expert width."""
-    rows_d, inter, weights = 2 * A * d, 2 * nw, 2 * d * W
+    once and its outputs written once. A = routed rows, T = tokens (the up
+    GEMM and its dW read the token rows x through the row map), nw =
+    sum_e n_e w_e, W = total expert width."""
+    rows_d, tok_d, inter, weights = 2 * A * d, 2 * T * d, 2 * nw, 2 * d * W
     return {
-        "gemm_up_fwd": rows_d + weights + 2 * inter,          # Xg, W1 -> H, PRE
+        "gemm_up_fwd": tok_d + weights + 2 * inter,           # x[gm], W1 -> H, PRE
         "gemm_down_fwd": inter + weights + rows_d,            # H, W2 -> Y
         "gemm_down_bwd_dh_ga": rows_d + weights + 2 * inter,  # GY, W2, PRE -> GA
         "gemm_up_bwd_dx": inter + weights + rows_d,           # GA, W1 -> GXg
-        "gemm_up_bwd_dw": rows_d + inter + weights,           # x[gm], GA -> GW1
+        "gemm_up_bwd_dw": tok_d + inter + weights,            # x[gm], GA -> GW1
         "gemm_down_bwd_dw": inter + rows_d + weights,         # H, GY -> GW2
     }[op]
 
@@ -200,20 +202,22 @@ def kernel_breakdown(m, xb, sel, reps):
     T = x.shape[0]
     wts = torch.rand(T * k, device=x.device).to(torch.bfloat16)
     selv = sel.reshape(-1)
-    r = route_device(selv, E, k, b)
+    # the module's launches: pad rows of the row map are -1 and the up GEMM
+    # and its dW read the tokens x through it (no gathered copy of x)
+    r = route_device(selv, E, k, b, map_pad=-1)
     meta = gg.GemmMeta(r.expert_offsets, m.expert_weight_offsets_t, m.expert_widths_t,
                        r.padded_counts, E, m.max_expert_width, r.rows_bound)
     nrd = r.info[0:1]
     ar = r.assignment_row
-    xg = gather_rows(x, r.row_src, k, r.rows_bound, num_rows_dev=nrd, assignment_row=ar)
-    h, pre = gg.up_fwd(xg, m.w1.detach(), meta, 1, True, False)
+    gm = r.gather_map
+    h, pre = gg.up_fwd(x, m.w1.detach(), meta, 1, True, False, gather_map=gm)
     y = gg.down_fwd(h, m.w2.detach(), meta, d)
     G = torch.ones(T, d, dtype=torch.bfloat16, device=x.device)
     gy = gather_rows(G, r.row_src, k, r.rows_bound, weights=wts, num_rows_dev=nrd,
                      assignment_row=ar)
     w1, w2 = m.w1.detach(), m.w2.detach()
     ga, _ = gg.down_bwd(gy, h, w2, meta, d, False, pre=pre)
-    gxg, _ = gg.up_bwd_from_ga(ga, x, w1, meta, d, r.gather_map)
+    gxg, _ = gg.up_bwd_from_ga(ga, x, w1, meta, d, gm)
     ws = gg._dw_workspace(meta, d, x.device)
     from triton_moe import _lib
 
@@ -224,9 +228,9 @@ def kernel_breakdown(m, xb, sel, reps):
                   meta.max_width, meta.rows, _lib.stream(x.device))
 
     def dw1_only():
-        # as the module calls it: A = the gathered activations, no row map
+        # as the module calls it: A = the tokens x through the row map
         gw = torch.empty_like(w1)
-        _lib.call("vmoe_gemm_up_bwd_dw", xg.data_ptr(), xg.stride(0), xg.shape[0], None,
+        _lib.call("vmoe_gemm_up_bwd_dw", x.data_ptr(), x.stride(0), T, gm.data_ptr(),
                   ga.data_ptr(), ga.stride(0), gw.data_ptr(), gw.stride(0),
                   *gg._meta_args(meta), d, meta.max_width, meta.rows, ws.data_ptr(), ws.numel(),
                   _lib.stream(x.device))
@@ -250,10 +254,8 @@ def kernel_breakdown(m, xb, sel, reps):
 
     ops = {
         "router_topk": lambda: router_topk(logits, k, m.norm_topk_prob),
-        "route": lambda: route_device(selv, E, k, b),
-        "gather": lambda: gather_rows(x, r.row_src, k, r.rows_bound, num_rows_dev=nrd,
-                                      assignment_row=ar),
-        "gemm_up_fwd": lambda: gg.up_fwd(xg, w1, meta, 1, True, False),
+        "route": lambda: route_device(selv, E, k, b, map_pad=-1),
+        "gemm_up_fwd": lambda: gg.up_fwd(x, w1, meta, 1, True, False, gather_map=gm),
         "gemm_down_fwd": lambda: gg.down_fwd(h, w2, meta, d),
         "combine": lambda: combine_rows(y, r.assignment_row, k, T, weights=wts),
         "scatter_bwd_gather": lambda: gather_rows(G, r.row_src, k, r.rows_bound, weights=wts,
@@ -365,11 +367,10 @@ def main():
     E = m.num_experts
     widths = [w for c, w in sizes for _ in range(c)]
     nw = sum(int(n) * w for n, w in zip(counts, widths))
-    dom_bytes = gemm_bytes(dom, A, d, nw, sum(widths))
+    dom_bytes = gemm_bytes(dom, A, T, d, nw, sum(widths))
     ai = per_gemm_flops / dom_bytes
     ai_bound = min(PEAK_BF16_TFLOPS, ai * PEAK_HBM_GBS / 1e3)
     perm_bytes = {
-        "gather": 2 * T * d + 2 * A * d + 8 * A,
         "combine": 2 * A * d + 2 * A + 2 * T * d + 8 * A,
         "scatter_bwd_gather": 2 * T * d + 2 * A + 2 * A * d + 8 * A,
         "gather_bwd_combine": 2 * A * d + 2 * T * d + 8 * A,

@@ -57,7 +57,9 @@ int vmoe_route_max_experts(void);
  *                     the first info[VMOE_INFO_KEPT] entries are valid
  *   tokens_per_expert, bins, padded_bins  [E] int32
  *   row_src     [row_capacity] int32: padded row -> assignment index, -1 = pad
- *   gather_map  [row_capacity] int32: padded row -> token (assignment / top_k), 0 = pad
+ *   gather_map  [row_capacity] int32: padded row -> token (assignment / top_k); pad rows
+ *               hold gather_map_pad (0 in the reference's precompute_gather_map; -1
+ *               makes the GEMMs' row gather read zeros for them)
  *   assignment_row [A] int32: assignment -> padded row, -1 = dropped
  *   info        [VMOE_INFO_LEN] int32: rows P, kept count, error bits
  *   expert_offsets [E+1] int32 (nullable): [0, padded_bins], the module's
@@ -72,8 +74,9 @@ int vmoe_route(const void* selected_experts, int32_t selected_is_int64,
                int64_t num_assignments, int32_t num_experts, int32_t top_k,
                int32_t block_size, int32_t rounding, int32_t* bin_ids, int32_t* indices,
                int32_t* tokens_per_expert, int32_t* bins, int32_t* padded_bins,
-               int32_t* row_src, int32_t* gather_map, int64_t row_capacity,
-               int32_t* assignment_row, int32_t* info, int32_t* expert_offsets,
+               int32_t* row_src, int32_t* gather_map, int32_t gather_map_pad,
+               int64_t row_capacity, int32_t* assignment_row, int32_t* info,
+               int32_t* expert_offsets,
                int32_t* padded_counts, void* workspace, size_t workspace_bytes,
                vmoe_stream_t stream);
 

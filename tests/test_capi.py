@@ -52,9 +52,9 @@ def test_argument_checks_return_invalid_arg():
     lib = _lib.lib()
     # negative sizes / bad enums are rejected before any launch
     assert lib.vmoe_route(None, 0, -1, 4, 1, 64, 0, None, None, None, None, None, None, None,
-                          0, None, None, None, None, None, 0, None) == _lib.ERR_INVALID_ARG
+                          0, 0, None, None, None, None, None, 0, None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_route(None, 0, 0, 4, 1, 64, 7, None, None, None, None, None, None, None,
-                          0, None, None, None, None, None, 0, None) == _lib.ERR_INVALID_ARG
+                          0, 0, None, None, None, None, None, 0, None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_gather(None, 0, 0, None, 1, None, 0, None, 8, -1, None, 8,
                            None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_combine(None, 0, 0, None, None, 0, None, 8, 1, 8, None) == _lib.ERR_INVALID_ARG

@@ -218,6 +218,47 @@ def test_up_fwd_gather_map_path(device):
     assert_close_norm(out, h_ref, TIGHT, "H gm")
 
 
+@pytest.mark.parametrize("with_workspace", [True, False], ids=["splitk", "no_workspace"])
+def test_up_dw_row_map(with_workspace, device):
+    """dW1 = x[map]^T @ GA through the row map, called through the C ABI: the
+    split-K path (K chunks of 256 rows) and the workspace-free path (whole
+    experts of ~1000 rows per item). Map entries outside [0, x_rows), -1 as
+    the module's pad rows, read zeros."""
+    from triton_moe import _lib
+    from triton_moe.kernels.grouped_gemm import _dw_workspace, host_meta
+
+    c = _case(2048, 256, [(2, 256), (2, 128)], 2, 64, False, seed=4)
+    eto, ewo, wid, tpe = _meta_dev(c, device)
+    P, d, max_w, W = c["P"], c["d"], c["max_w"], c["W"]
+    g = torch.Generator().manual_seed(5)
+    T = 1500
+    x_flat = torch.randn(T, d, generator=g).to(torch.bfloat16)
+    gm = torch.randint(0, T, (P,), generator=g, dtype=torch.int32)
+    bad = torch.rand(P, generator=g)
+    gm[bad < 0.05] = -1
+    gm[(bad >= 0.05) & (bad < 0.08)] = T + 7
+    ga = (torch.randn(P, max_w, generator=g) * 0.1).to(torch.bfloat16)
+    for e, (r0, r1) in enumerate(c["rows"]):
+        ga[r0:r1, c["widths"][e]:] = 0
+    m = host_meta(eto, ewo, wid, tpe, max_w, d, P, W)
+    gw = torch.full((d, W), float("nan"), dtype=torch.bfloat16, device=device)
+    ws = _dw_workspace(m, d, device) if with_workspace else None
+    xd, gmd, gad = x_flat.to(device), gm.to(device), ga.to(device)
+    _lib.call("vmoe_gemm_up_bwd_dw", xd.data_ptr(), xd.stride(0), T, gmd.data_ptr(),
+              gad.data_ptr(), gad.stride(0), gw.data_ptr(), gw.stride(0), eto.data_ptr(),
+              ewo.data_ptr(), wid.data_ptr(), tpe.data_ptr(), c["E"], d, max_w, P,
+              None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+              _lib.stream(xd.device))
+    valid = (gm >= 0) & (gm < T)
+    xs = torch.where(valid[:, None], x_flat[gm.clamp(0, T - 1).long()], torch.zeros(()))
+    ref = torch.zeros(d, W)
+    for e, (r0, r1) in enumerate(c["rows"]):
+        w, o = c["widths"][e], c["offsets"][e]
+        assert r1 - r0 > 8 * 32, "each expert spans more than one map window"
+        ref[:, o:o + w] = bf(xs[r0:r1].float().T @ ga[r0:r1, :w].float())
+    assert_close_norm(gw, ref, TIGHT, f"GW1 map ws={with_workspace}")
+
+
 def test_autograd_entry_points(device):
     """grouped_gemm_up_autograd -> grouped_gemm_down_autograd -> sum().backward()
     (the reference's test_grouped_gemm_backward flow, in bf16)."""

@@ -85,6 +85,11 @@ def test_route_random_topk(T, k, E, b, mode, device):
     np.testing.assert_array_equal(_np(r.row_src[:P]), maps["row_src"])
     np.testing.assert_array_equal(_np(r.gather_map[:P]), maps["gather_map"])
     np.testing.assert_array_equal(_np(r.assignment_row), maps["assignment_row"])
+    # the module's map: pad rows -1 (read as zeros by the GEMMs' row gather)
+    r2 = route_device(sel, E, k, b, mode, map_pad=-1)
+    gm2 = np.where(maps["row_src"] < 0, -1, maps["gather_map"])
+    np.testing.assert_array_equal(_np(r2.gather_map[:P]), gm2)
+    np.testing.assert_array_equal(_np(r2.row_src[:P]), maps["row_src"])
 
 
 def test_route_deterministic_and_large(device):

@@ -299,25 +299,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
                                            0x00020000);
 }
 
-// Row-map entries for the producers come through the scalar cache: a load
-// from the constant address space at a uniform index compiles to s_load,
-// which completes on lgkmcnt, not vmcnt, so waiting for it never drains the
-// in-flight DMAs. The compiler tracks these loads itself. Callers clamp the
-// index into the rows the item owns, so every load stays inside the map.
-__device__ __forceinline__ int32_t sload_map(const int32_t* map, int idx) {
-  typedef __attribute__((address_space(4))) const int32_t cint;
-  return ((cint*)map)[__builtin_amdgcn_readfirstlane(idx)];
-}
-
-// v[idx] for a lane-varying idx over uniform (scalar) values.
-template <int N>
-__device__ __forceinline__ int32_t pick(const int32_t (&v)[N], int idx) {
-  int32_t r = v[0];
-#pragma unroll
-  for (int t = 1; t < N; ++t) r = idx == t ? v[t] : r;
-  return r;
-}
-
 // 16-byte DMA of the lane's source into LDS at dst + 16 * lane
 // (buffer_load_dwordx4 ... lds, LDS base in M0). Issued as inline asm so the
 // compiler does not track it: it would otherwise wait for every DMA before
@@ -328,6 +309,14 @@ __device__ __forceinline__ int32_t pick(const int32_t (&v)[N], int idx) {
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, lds_char* dst) {
   const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(dst));
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(r), "s"(lds) : "memory", "m0");
+}
+
+// 4-byte DMA of the lane's source into LDS at dst + 4 * lane (the row-map
+// windows of the T-form gather), under the same rules as dma16.
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, lds_char* dst) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(dst));
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds"
                :: "v"(voff), "s"(r), "s"(lds) : "memory", "m0");
 }
 
@@ -441,16 +430,24 @@ struct Gemm {
     int idx[PW];         // K-form: k of the lane's chunk; T-form: the lane's k-row
     bool ok[PW];         // K-form: row valid; T-form: column valid
   };
-  // T-form row gather (the A operand of the up dW GEMM): the map entries of
-  // the item's k range, and those of the next stage's k-rows, loaded a stage
-  // ahead.
+  // T-form row gather (the A operand of the up dW GEMM). Each producer wave
+  // stages the map entries of its k-rows for kWinStages stages of an item
+  // in a 256-byte LDS window (lane l of the window DMA fetches the entry of
+  // stage l / 8, row 8 * wave + l % 8), by DMA like the operand tiles, so
+  // the ring's vmcnt waits order it too. The window of the next item loads
+  // while the current one streams (two windows per wave); a scalar load of
+  // the entries instead waits on the scalar cache once per stage.
+  static constexpr int kWinStages = 8;
   struct TMap {
-    const int32_t* base;  // map entry of the item's first k-row
-    int klen;             // k-rows of the item
-    int32_t nxt[8];       // entries of this wave's k-rows of the next stage
-    int rows;             // rows of the gathered source
+    __amdgpu_buffer_rsrc_t mrs;  // over the row map
+    lds_char* win;               // this wave's window of the current item
+    int64_t mbase;               // map index of the item's first k-row
+    int klen;                    // k-rows of the item
+    uint32_t rows;               // rows of the gathered source
     bool on;
   };
+  static_assert(BK / kProducers == 8 && kWinStages * 8 == 64,
+                "window: 8 k-rows per producer wave per stage, one DMA instruction");
 
   // K-form setup: rows [0, R) of the tile (source rows r0 + row, or
   // map[r0 + row]), rows_valid of them real, k measured from column c0.
@@ -494,27 +491,22 @@ struct Gemm {
   }
 
   // T-form setup: columns [0, R) of the tile starting at source column c0,
-  // cols_valid of them real; source rows r0 + k, or map[r0 + k].
-  template <int R, int PW>
+  // cols_valid of them real; source rows r0 + k, or map[r0 + k] (a map entry
+  // outside [0, map_rows) reads zeros).
+  template <int R, int PW, bool MAP>
   __device__ static void setup_t(Src<PW>& s, TMap& tm, const uint16_t* base, int64_t ld,
                                  const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
                                  int cols_valid, int k_valid) {
     constexpr int LPR = Dma<R>::LPR, RPI = Dma<R>::RPI;
     const int lane = threadIdx.x & 63, wave = pwave();
-    if (!T::t_map) map = nullptr;
-    const uint16_t* b = map ? base + c0 : base + r0 * ld + c0;
-    s.rsrc = make_rsrc(b);
+    if (!MAP) map = nullptr;
+    s.rsrc = make_rsrc(map ? base + c0 : base + r0 * ld + c0);
     s.ld2 = (uint32_t)(ld * 2);
-    tm.on = T::t_map && map;
-    if (T::t_map && map) {
-      // This wave's PW * RPI consecutive k-rows per stage, loaded a stage
-      // ahead (the first stage's here), indices clamped to the item's rows.
-      static_assert(!T::t_map || PW * RPI == 8, "map prefetch assumes 8 k-rows per wave");
-      tm.rows = (int)map_rows;
-      tm.base = map + r0;
-      tm.klen = max(1, k_valid);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) tm.nxt[t] = sload_map(tm.base, min(wave * 8 + t, tm.klen - 1));
+    tm.on = MAP && map;
+    if (MAP && map) {
+      tm.mbase = r0;
+      tm.klen = k_valid;
+      tm.rows = (uint32_t)map_rows;
     }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
@@ -526,33 +518,40 @@ struct Gemm {
     }
   }
 
-  template <int R, int PW>
-  __device__ static void issue_t(const Src<PW>& s, TMap& tm, int k0, int K, lds_char* stage) {
+  // DMA of this wave's map entries for stages [kw / BK, kw / BK + kWinStages)
+  // of the item into window `win`; entries past the item's rows read 0.
+  __device__ static void load_window(const TMap& tm, int kw, lds_char* win) {
+    const int lane = threadIdx.x & 63, wave = pwave();
+    const int k = kw + (lane >> 3) * BK + wave * 8 + (lane & 7);
+    dma4(tm.mrs, k < tm.klen ? (uint32_t)((tm.mbase + k) * 4) : kOob, win);
+  }
+
+  template <int R, int PW, bool MAP>
+  __device__ static void issue_t(const Src<PW>& s, TMap& tm, int kt, int K, lds_char* stage) {
     constexpr int LPR = Dma<R>::LPR, RPI = Dma<R>::RPI;
     const int wave = pwave(), lane = threadIdx.x & 63;
-    int32_t cur[8];
-    if (T::t_map && tm.on) {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) cur[t] = tm.nxt[t];
+    const int k0 = kt * BK;
+    if constexpr (MAP) {
+      if (tm.on && kt > 0 && kt % kWinStages == 0) {
+        // Items longer than the window (no split-K): refill it in place.
+        load_window(tm, k0, tm.win);
+        wait_vmcnt<0>();
+      }
     }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-      const int k = k0 + s.idx[i];
-      bool v = s.ok[i] && k < K;
-      uint32_t off;
-      if (T::t_map && tm.on) {
-        const int64_t row = pick<8>(cur, i * RPI + lane / LPR);
-        v = v && row >= 0 && row < tm.rows;
-        off = v ? s.off[i] + (uint32_t)row * s.ld2 : kOob;
-      } else {
-        off = v ? s.off[i] + (uint32_t)k0 * s.ld2 : kOob;
+      const bool v = s.ok[i] && k0 + s.idx[i] < K;
+      uint32_t off = v ? s.off[i] + (uint32_t)k0 * s.ld2 : kOob;
+      if constexpr (MAP) {
+        static_assert(RPI == 4, "map window assumes 4 k-rows per DMA instruction");
+        if (tm.on) {
+          const int e = (kt % kWinStages) * 8 + i * RPI + lane / LPR;
+          const int32_t row = reinterpret_cast<const __attribute__((address_space(3))) int32_t*>(
+              tm.win)[e];
+          off = v && (uint32_t)row < tm.rows ? s.off[i] + (uint32_t)row * s.ld2 : kOob;
+        }
       }
       dma16(s.rsrc, off, stage + (wave * PW + i) * 1024);
-    }
-    if (T::t_map && tm.on && k0 + BK < K) {
-#pragma unroll
-      for (int t = 0; t < 8; ++t)
-        tm.nxt[t] = sload_map(tm.base, min(k0 + BK + wave * 8 + t, tm.klen - 1));
     }
   }
 
@@ -669,33 +668,41 @@ struct Gemm {
     return w;
   }
 
+  // Map fields of the A operand of work w (T-form gather).
+  __device__ static void setup_map(const Args& p, const Work& w, TMap& tm) {
+    tm.mbase = w.q.ar + w.kbeg;
+    tm.klen = w.klen;
+    tm.rows = (uint32_t)p.a_rows;
+    tm.on = true;
+  }
+
   __device__ static void setup(const Args& p, const Work& w, Src<PWA>& sa, Src<PWB>& sb,
                                TMap& tm) {
     const Prob& q = w.q;
     if (T::a_k)
       setup_k<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.m0, q.ac + w.kbeg, q.M - w.m0);
     else
-      setup_t<BM>(sa, tm, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.kbeg, q.ac + w.m0, q.M - w.m0,
-                  w.klen);
+      setup_t<BM, PWA, T::t_map>(sa, tm, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.kbeg,
+                                 q.ac + w.m0, q.M - w.m0, w.klen);
     if (T::b_k)
       setup_k<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg, q.N - w.n0);
     else
     {
       TMap none;  // B is never gathered
-      setup_t<BN>(sb, none, p.b, p.ldb, nullptr, 0, q.br + w.kbeg, q.bc + w.n0, q.N - w.n0,
-                  w.klen);
+      setup_t<BN, PWB, false>(sb, none, p.b, p.ldb, nullptr, 0, q.br + w.kbeg, q.bc + w.n0,
+                              q.N - w.n0, w.klen);
     }
   }
 
   __device__ static void issue(const Work& w, const Src<PWA>& sa, const Src<PWB>& sb,
                                TMap& tm, int kt, lds_char* st) {
     const int k0 = kt * BK;
-    if (T::a_k) issue_k<BM>(sa, k0, w.klen, st); else issue_t<BM>(sa, tm, k0, w.klen, st);
+    if (T::a_k) issue_k<BM>(sa, k0, w.klen, st); else issue_t<BM, PWA, T::t_map>(sa, tm, kt, w.klen, st);
     if (T::b_k) issue_k<BN>(sb, k0, w.klen, st + A_STAGE);
     else {
       TMap none;
       none.on = false;
-      issue_t<BN>(sb, none, k0, w.klen, st + A_STAGE);
+      issue_t<BN, PWB, false>(sb, none, kt, w.klen, st + A_STAGE);
     }
   }
 
@@ -907,23 +914,69 @@ struct Gemm {
   // item order, as one stream through the LDS ring (the first stages of the
   // next item load while the current one finishes), waiting for each stage
   // before the barrier that hands it to the consumers.
-  __device__ static void run_producer(const Args& p, lds_char* ring, const Meta& mt,
-                                      const Range& rg) {
-    int ec = 0, ei = 0;
+  //
+  // Row-map windows (T-form gather): when an item starts, the window of the
+  // next item with k-steps is requested into the wave's other window. The
+  // wait before stage s's barrier completes every DMA issued before stage
+  // s + 1's, so a window requested after stage j was issued is in LDS once
+  // the loop has waited for stage j; an item that starts earlier than that
+  // (an item of fewer stages than the ring is deep, or the first one)
+  // waits for its window explicitly.
+  __device__ static void run_producer(const Args& p, lds_char* ring, lds_char* wins,
+                                      const Meta& mt, const Range& rg) {
+    int ec = 0, ei = 0, ela = 0;
     Work wi = decode(p, mt, rg.beg, ei, rg.slot);
     Src<PWA> sa;
     Src<PWB> sb;
     TMap tm;
-    setup(p, wi, sa, sb, tm);
-    int ikt = 0, inext = rg.beg + rg.stride;
+    const bool mapped = T::t_map && p.a_map;
+    if (mapped) tm.mrs = make_rsrc(p.a_map);
+    lds_char* const win0 = wins + pwave() * 256;
+    lds_char* const win1 = win0 + kProducers * 256;
+    int wcur = 0;           // window of the current item (0: win0, 1: win1)
+    int la_item = -1;       // item whose window was requested into the other one
+    int la_stage = 0;       // last stage issued before that request
+    int done = -2;          // every DMA issued before stage done + 1's is complete
+    int ikt = 0, inext = rg.beg + rg.stride, witem = rg.beg;
     int issued = 0;
+    bool fresh = true;      // wi not set up yet
+    auto begin_item = [&]() {
+      setup(p, wi, sa, sb, tm);
+      if (!mapped) return;
+      if (la_item == witem) {
+        wcur ^= 1;
+        tm.win = wcur ? win1 : win0;
+        if (la_stage > done) wait_vmcnt<0>();
+      } else {
+        tm.win = wcur ? win1 : win0;
+        load_window(tm, 0, tm.win);
+        wait_vmcnt<0>();
+      }
+      la_item = -1;
+      for (int nx = witem + rg.stride; nx < rg.end; nx += rg.stride) {
+        const Work wn = decode(p, mt, nx, ela, rg.slot);
+        if (wn.nk > 0) {
+          TMap tn = tm;
+          setup_map(p, wn, tn);
+          load_window(tn, 0, wcur ? win0 : win1);
+          la_item = nx;
+          la_stage = issued - 1;
+          break;
+        }
+      }
+    };
     auto issue_next = [&](lds_char* st) -> bool {
       while (ikt >= wi.nk) {
         if (inext >= rg.end) return false;
+        witem = inext;
         wi = decode(p, mt, inext, ei, rg.slot);
         inext += rg.stride;
-        setup(p, wi, sa, sb, tm);
         ikt = 0;
+        fresh = true;
+      }
+      if (fresh) {
+        begin_item();
+        fresh = false;
       }
       issue(wi, sa, sb, tm, ikt, st);
       ++ikt;
@@ -947,6 +1000,7 @@ struct Gemm {
           wait_vmcnt<PT>();
         else
           wait_vmcnt<0>();
+        done = s;
         block_barrier();
         if (issue_next(ring + ((s + kStages - 1) % kStages) * STAGE)) ++issued;
       }
@@ -1028,13 +1082,14 @@ struct Gemm {
     }
   }
 
-  __device__ static void run(const Args& p, lds_char* ring, Meta& mt, lds_char* epi) {
+  __device__ static void run(const Args& p, lds_char* ring, Meta& mt, lds_char* epi,
+                             lds_char* wins) {
     const int total = build_meta(p, mt, (long long*)(char*)ring);
     const Range rg = item_range<Cfg<V>::contig>(total);
     if (rg.beg >= rg.end) return;
     const int wave = threadIdx.x >> 6;
     if (wave >= kConsumers)
-      run_producer(p, ring, mt, rg);
+      run_producer(p, ring, wins, mt, rg);
     else
       run_consumer(p, ring, mt, rg, epi + wave * EPI_BYTES);
   }
@@ -1046,9 +1101,12 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
   __shared__ __align__(1024) char ring[G::RING];
   __shared__ __align__(16) char epi[kConsumers * G::EPI_BYTES];
   __shared__ Meta meta;
-  static_assert(G::RING + kConsumers * G::EPI_BYTES + sizeof(Meta) <= 160 * 1024,
+  // Row-map windows of the producers (two per wave), for the T-form gather.
+  constexpr int WIN_BYTES = Traits<V>::t_map ? 2 * kProducers * 256 : 16;
+  __shared__ __align__(16) char wins[WIN_BYTES];
+  static_assert(G::RING + kConsumers * G::EPI_BYTES + sizeof(Meta) + WIN_BYTES <= 160 * 1024,
                 "LDS budget of a gfx950 CU");
-  G::run(p, (lds_char*)ring, meta, (lds_char*)epi);
+  G::run(p, (lds_char*)ring, meta, (lds_char*)epi, (lds_char*)wins);
 }
 
 // Finds the expert owning tile `id` in the concatenation of per-expert tile

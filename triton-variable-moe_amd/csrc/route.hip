@@ -106,8 +106,8 @@ __device__ __forceinline__ int32_t round_count(int32_t c, int32_t b, int mode) {
 __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     RouteWs ws, int E, int ntiles, int block, int mode, int32_t* __restrict__ tpe,
     int32_t* __restrict__ bins, int32_t* __restrict__ padded_bins,
-    int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int64_t row_capacity,
-    int32_t* __restrict__ info, int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int32_t map_pad,
+    int64_t row_capacity, int32_t* __restrict__ info, int32_t* __restrict__ expert_offsets,
     int32_t* __restrict__ padded_counts) {
   __shared__ int32_t scan_smem[kScanThreads / kWave + 1];
   __shared__ int32_t carry_kept, carry_rounded, any_bad;
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
       const int64_t row = ps + q;
       if (row < row_capacity) {
         row_src[row] = -1;
-        gather_map[row] = 0;
+        gather_map[row] = map_pad;
       }
     }
   }
@@ -336,9 +336,10 @@ extern "C" size_t vmoe_route_workspace_bytes(int64_t A, int32_t E) {
 extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_k,
                           int32_t block, int32_t rounding, int32_t* bin_ids, int32_t* indices,
                           int32_t* tpe, int32_t* bins, int32_t* padded_bins, int32_t* row_src,
-                          int32_t* gather_map, int64_t row_capacity, int32_t* assignment_row,
-                          int32_t* info, int32_t* expert_offsets, int32_t* padded_counts,
-                          void* workspace, size_t ws_bytes, vmoe_stream_t stream) {
+                          int32_t* gather_map, int32_t gather_map_pad, int64_t row_capacity,
+                          int32_t* assignment_row, int32_t* info, int32_t* expert_offsets,
+                          int32_t* padded_counts, void* workspace, size_t ws_bytes,
+                          vmoe_stream_t stream) {
   if (A < 0 || E <= 0 || top_k <= 0 || block <= 0 || row_capacity < 0)
     return VMOE_ERR_INVALID_ARG;
   if (rounding < VMOE_ROUND_UP || rounding > VMOE_ROUND_NEAREST) return VMOE_ERR_INVALID_ARG;
@@ -358,7 +359,8 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
   }
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), sizeof(int32_t) * (4 * E + 1),
                      s, ws, E, ntiles, block, rounding, tpe, bins, padded_bins, row_src,
-                     gather_map, row_capacity, info, expert_offsets, padded_counts);
+                     gather_map, gather_map_pad, row_capacity, info, expert_offsets,
+                     padded_counts);
   VMOE_CHECK_LAUNCH();
   if (ntiles > 0) {
     int nbits = 1;

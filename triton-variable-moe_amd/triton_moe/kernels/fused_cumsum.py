@@ -50,8 +50,12 @@ def rows_upper_bound(num_assignments: int, num_experts: int, block_size: int,
 
 
 def route_device(selected: torch.Tensor, num_experts: int, top_k: int, block_size: int,
-                 rounding: str = "up") -> Route:
-    """Runs the routing chain on the current stream; never syncs."""
+                 rounding: str = "up", map_pad: int = 0) -> Route:
+    """Runs the routing chain on the current stream; never syncs.
+
+    map_pad is the gather_map entry of pad rows: 0 as in the reference's
+    precompute_gather_map, -1 for the module's fused row gather (the GEMMs
+    read zeros for it)."""
     _lib.require_gpu(selected)
     if rounding not in _lib.ROUNDING:
         raise AssertionError(f"Invalid rounding mode: {rounding}")
@@ -82,7 +86,7 @@ def route_device(selected: torch.Tensor, num_experts: int, top_k: int, block_siz
     _lib.call("vmoe_route", sel.data_ptr(), int(sel.dtype == torch.int64), A, E, int(top_k),
               int(block_size), _lib.ROUNDING[rounding], bin_ids.data_ptr(), indices.data_ptr(),
               tpe.data_ptr(), bins.data_ptr(), padded.data_ptr(), row_src.data_ptr(),
-              gmap.data_ptr(), cap, arow.data_ptr(), info.data_ptr(), eto.data_ptr(),
+              gmap.data_ptr(), int(map_pad), cap, arow.data_ptr(), info.data_ptr(), eto.data_ptr(),
               ptpe.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream(dev))
     return Route(bin_ids[:A], indices[:A], tpe, bins, padded, row_src[:cap], gmap[:cap],
                  arow[:A], info, eto, ptpe, cap, A, E, int(top_k))

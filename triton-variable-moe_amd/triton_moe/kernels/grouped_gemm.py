@@ -441,31 +441,41 @@ def grouped_gemm_down_autograd(intermediate, w2, expert_token_offsets, expert_we
 
 
 class RoutedExpertsOp(torch.autograd.Function):
-    """Both grouped GEMMs of the module (up with relu^2, then down) as one
-    autograd node, with metadata from the route and no host sync.
+    """Token gather, both grouped GEMMs of the module (up with relu^2, then
+    down) and the gather's backward as one autograd node, with metadata from
+    the route and no host sync.
 
-    Saves the gathered activations (already materialised for the forward) for
-    the up dW GEMM, whose A operand then streams without a row map, plus H and
-    PRE. Its backward fuses the relu^2 gradient into the dH GEMM's epilogue,
-    so the gradient w.r.t. H is never materialised.
+    The up GEMM and its dW read the token activations x_flat through the row
+    map (row -> token, -1 for pad rows, which read zeros), so the gathered
+    copy of x (rows x hidden) is never written: the reference's padded_gather
+    (gather.py:63-115) is fused into the GEMMs' operand staging. The backward
+    fuses the relu^2 gradient into the dH GEMM's epilogue (the gradient with
+    respect to H is never materialised) and returns the gradient with respect
+    to x_flat: dX in expert-row order, summed over each token's k rows by the
+    unweighted combine (PaddedGatherOp's backward, gather.py:253-265).
     """
 
     @staticmethod
     @custom_fwd(device_type="cuda")
-    def forward(ctx, x_gathered, w1, w2, meta, x_flat, gather_map, hidden_size):
-        h, pre = up_fwd(x_gathered, w1, meta, _lib.ACT_RELU_SQUARED, True, zero_tails=False)
+    def forward(ctx, x_flat, w1, w2, meta, gather_map, assignment_row, top_k, hidden_size):
+        h, pre = up_fwd(x_flat, w1, meta, _lib.ACT_RELU_SQUARED, True, zero_tails=False,
+                        gather_map=gather_map)
         y = down_fwd(h, w2, meta, hidden_size)
-        ctx.save_for_backward(x_gathered, w1, w2, h, pre)
+        ctx.save_for_backward(x_flat, w1, w2, h, pre, gather_map, assignment_row)
         ctx.meta = meta
         ctx.hidden_size = hidden_size
+        ctx.top_k = top_k
         return y
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     @once_differentiable
     def backward(ctx, grad_y):
-        xg, w1, w2, h, pre = ctx.saved_tensors
+        from .gather import combine_rows
+
+        x_flat, w1, w2, h, pre, gm, ar = ctx.saved_tensors
         ga, grad_w2 = down_bwd(grad_y, h, w2, ctx.meta, ctx.hidden_size, zero_tails=False,
                                pre=pre)
-        grad_x, grad_w1 = up_bwd_from_ga(ga, xg, w1, ctx.meta, ctx.hidden_size, None)
-        return grad_x, grad_w1, grad_w2, None, None, None, None
+        grad_xg, grad_w1 = up_bwd_from_ga(ga, x_flat, w1, ctx.meta, ctx.hidden_size, gm)
+        grad_x = combine_rows(grad_xg, ar, ctx.top_k, x_flat.shape[0])
+        return grad_x, grad_w1, grad_w2, None, None, None, None, None

@@ -8,8 +8,9 @@ init order router -> w1 -> w2, buffers), forward returning
 The router Linear stays a PyTorch (hipBLASLt) GEMM. Everything after it runs
 on libvmoe.so: sigmoid / top-k / normalisation and the auxiliary-loss
 reductions (one router kernel, moe.py:166-182, 253-303 of the reference),
-routing (counting sort + scans + maps), gather, grouped up GEMM with fused
-relu^2, grouped down GEMM and weighted combine, and their backward. The
+routing (counting sort + scans + maps), grouped up GEMM with the token
+gather fused into its operand staging and relu^2 fused into its epilogue,
+grouped down GEMM and weighted combine, and their backward. The
 forward and backward issue no host sync: buffers are sized from an upper
 bound of the padded row count and the kernels read the true counts on the
 device.
@@ -33,7 +34,6 @@ from .kernels import (
     padded_scatter,
 )
 from .kernels.fused_cumsum import route_device
-from .kernels.gather import RoutedGatherOp
 from .kernels.grouped_gemm import GemmMeta, RoutedExpertsOp
 from .kernels.router import RouterAuxOp, load_balance_coef, router_topk
 from .kernels.scatter import RoutedScatterOp
@@ -165,17 +165,17 @@ class TritonMoEMLP(nn.Module):
     def _experts(self, x_flat, top_k_weights_flat, selected_experts_flat):
         """Routing + expert MLP + combine on the HIP kernels, no host sync."""
         k = self.num_active_experts
-        r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up")
+        # Pad rows of the row map are -1: the GEMMs' fused gather reads zeros.
+        r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
+                         map_pad=-1)
         # expert_token_offsets = [0, padded_bins] and the padded counts come
         # out of the routing kernel (moe.py:193-202 of the reference).
         meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
                         self.expert_widths_t, r.padded_counts, self.num_experts,
                         self.max_expert_width, r.rows_bound)
         num_rows_dev = r.info[0:1]
-        x_gathered = RoutedGatherOp.apply(x_flat, r.row_src, r.assignment_row, k, r.rows_bound,
-                                          num_rows_dev)
-        x_down = RoutedExpertsOp.apply(x_gathered, self.w1, self.w2, meta, x_flat,
-                                       r.gather_map, self.config.n_embd)
+        x_down = RoutedExpertsOp.apply(x_flat, self.w1, self.w2, meta, r.gather_map,
+                                       r.assignment_row, k, self.config.n_embd)
         output_flat = RoutedScatterOp.apply(x_down, r.row_src, r.assignment_row,
                                             top_k_weights_flat, k, x_flat.shape[0],
                                             num_rows_dev)
@@ -282,20 +282,20 @@ class TritonMoEMLP(nn.Module):
             selected_experts_flat = state.selected.reshape(-1)
         k = self.num_active_experts
         with profiler.step("fused_route"):
-            r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up")
+            r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
+                             map_pad=-1)
             meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
                             self.expert_widths_t, r.padded_counts, self.num_experts,
                             self.max_expert_width, r.rows_bound)
             nrd = r.info[0:1]
         with profiler.step("gather"):
-            x_gathered = RoutedGatherOp.apply(x_flat, r.row_src, r.assignment_row, k,
-                                              r.rows_bound, nrd)
+            pass  # fused into the up GEMM's operand staging (row map)
         with profiler.step("gemm_up"):
-            # up and down run as one autograd node (their backward is fused);
-            # both forward GEMMs are timed under "gemm_up" and "gemm_down" stays
-            # as an (empty) step so the reference's step names are all present.
-            x_down = RoutedExpertsOp.apply(x_gathered, self.w1, self.w2, meta, x_flat,
-                                           r.gather_map, self.config.n_embd)
+            # gather, up and down run as one autograd node; both forward GEMMs
+            # are timed under "gemm_up", and "gather" and "gemm_down" stay as
+            # (empty) steps so the reference's step names are all present.
+            x_down = RoutedExpertsOp.apply(x_flat, self.w1, self.w2, meta, r.gather_map,
+                                           r.assignment_row, k, self.config.n_embd)
         with profiler.step("gemm_down"):
             pass
         with profiler.step("scatter"):
