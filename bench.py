@@ -75,16 +75,18 @@ GEMM_SYMBOL = {
 def gemm_bytes(op, A, T, d, nw, W):
     """Minimal unique HBM bytes of one GEMM launch (bf16): its operands read
     once and its outputs written once. A = routed rows, T = tokens (the up
-    GEMM and its dW read the token rows x through the row map), nw =
-    sum_e n_e w_e, W = total expert width."""
+    GEMM and its dW read the token rows x, the dH and dW2 GEMMs the token
+    gradient G, through the row map), nw = sum_e n_e w_e, W = total expert
+    width. G counts as T rows (a real upstream gradient; the bench's
+    out.sum() gradient is one broadcast row)."""
     rows_d, tok_d, inter, weights = 2 * A * d, 2 * T * d, 2 * nw, 2 * d * W
     return {
-        "gemm_up_fwd": tok_d + weights + 2 * inter,           # x[gm], W1 -> H, PRE
-        "gemm_down_fwd": inter + weights + rows_d,            # H, W2 -> Y
-        "gemm_down_bwd_dh_ga": rows_d + weights + 2 * inter,  # GY, W2, PRE -> GA
+        "gemm_up_fwd": tok_d + weights + 2 * inter,           # x[gm], W1 -> H', PRE
+        "gemm_down_fwd": inter + weights + rows_d,            # H', W2 -> Y'
+        "gemm_down_bwd_dh_ga": tok_d + weights + 2 * inter,   # G[gm], W2, PRE -> GA
         "gemm_up_bwd_dx": inter + weights + rows_d,           # GA, W1 -> GXg
         "gemm_up_bwd_dw": tok_d + inter + weights,            # x[gm], GA -> GW1
-        "gemm_down_bwd_dw": inter + rows_d + weights,         # H, GY -> GW2
+        "gemm_down_bwd_dw": inter + tok_d + weights,          # H', G[gm] -> GW2
     }[op]
 
 
@@ -194,7 +196,7 @@ def kernel_breakdown(m, xb, sel, reps):
 
     from triton_moe.kernels import grouped_gemm as gg
     from triton_moe.kernels.fused_cumsum import route_device
-    from triton_moe.kernels.gather import combine_rows, gather_rows
+    from triton_moe.kernels.gather import combine_rows
 
     k, E, b = m.num_active_experts, m.num_experts, m.block_size
     d = xb.shape[-1]
@@ -202,21 +204,21 @@ def kernel_breakdown(m, xb, sel, reps):
     T = x.shape[0]
     wts = torch.rand(T * k, device=x.device).to(torch.bfloat16)
     selv = sel.reshape(-1)
-    # the module's launches: pad rows of the row map are -1 and the up GEMM
-    # and its dW read the tokens x through it (no gathered copy of x)
-    r = route_device(selv, E, k, b, map_pad=-1)
+    # the module's launches: pad rows of the row map are -1, the up GEMM and
+    # its dW read the tokens x through it (no gathered copy of x), the up
+    # GEMM scales H by each row's routing weight (row_weight), so the combine
+    # is unweighted and the dH / dW2 GEMMs read the output gradient G through
+    # the map. G is the step's: the gradient of out.sum(), one broadcast row.
+    r = route_device(selv, E, k, b, map_pad=-1, weights=wts)
     meta = gg.GemmMeta(r.expert_offsets, m.expert_weight_offsets_t, m.expert_widths_t,
                        r.padded_counts, E, m.max_expert_width, r.rows_bound)
-    nrd = r.info[0:1]
-    ar = r.assignment_row
-    gm = r.gather_map
-    h, pre = gg.up_fwd(x, m.w1.detach(), meta, 1, True, False, gather_map=gm)
+    gm, rw = r.gather_map, r.row_weight
+    h, pre = gg.up_fwd(x, m.w1.detach(), meta, 1, True, False, gather_map=gm, row_scale=rw)
     y = gg.down_fwd(h, m.w2.detach(), meta, d)
-    G = torch.ones(T, d, dtype=torch.bfloat16, device=x.device)
-    gy = gather_rows(G, r.row_src, k, r.rows_bound, weights=wts, num_rows_dev=nrd,
-                     assignment_row=ar)
+    G1 = torch.ones(1, d, dtype=torch.bfloat16, device=x.device)  # ld 0: one row for all
     w1, w2 = m.w1.detach(), m.w2.detach()
-    ga, _ = gg.down_bwd(gy, h, w2, meta, d, False, pre=pre)
+    ga, _ = gg.down_bwd(G1.expand(T, d), h, w2, meta, d, False, pre=pre, gather_map=gm,
+                        row_scale=rw)
     gxg, _ = gg.up_bwd_from_ga(ga, x, w1, meta, d, gm)
     ws = gg._dw_workspace(meta, d, x.device)
     from triton_moe import _lib
@@ -237,14 +239,14 @@ def kernel_breakdown(m, xb, sel, reps):
 
     def dh_only():
         o = torch.empty(meta.rows, meta.max_width, dtype=torch.bfloat16, device=x.device)
-        _lib.call("vmoe_gemm_down_bwd_dh", gy.data_ptr(), gy.stride(0), w2.data_ptr(),
-                  w2.stride(0), pre.data_ptr(), o.data_ptr(), o.stride(0), *gg._meta_args(meta),
-                  d, meta.max_width, meta.rows, _lib.stream(x.device))
+        _lib.call("vmoe_gemm_down_bwd_dh", G1.data_ptr(), 0, T, gm.data_ptr(), w2.data_ptr(),
+                  w2.stride(0), pre.data_ptr(), rw.data_ptr(), o.data_ptr(), o.stride(0),
+                  *gg._meta_args(meta), d, meta.max_width, meta.rows, _lib.stream(x.device))
 
     def dw2_only():
         gw = torch.empty_like(w2)
-        _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), gy.data_ptr(),
-                  gy.stride(0), gw.data_ptr(), gw.stride(0), *gg._meta_args(meta), d,
+        _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), G1.data_ptr(), 0, T,
+                  gm.data_ptr(), gw.data_ptr(), gw.stride(0), *gg._meta_args(meta), d,
                   meta.max_width, meta.rows, ws.data_ptr(), ws.numel(), _lib.stream(x.device))
 
     from triton_moe.kernels.router import router_topk
@@ -254,12 +256,11 @@ def kernel_breakdown(m, xb, sel, reps):
 
     ops = {
         "router_topk": lambda: router_topk(logits, k, m.norm_topk_prob),
-        "route": lambda: route_device(selv, E, k, b, map_pad=-1),
-        "gemm_up_fwd": lambda: gg.up_fwd(x, w1, meta, 1, True, False, gather_map=gm),
+        "route": lambda: route_device(selv, E, k, b, map_pad=-1, weights=wts),
+        "gemm_up_fwd": lambda: gg.up_fwd(x, w1, meta, 1, True, False, gather_map=gm,
+                                         row_scale=rw),
         "gemm_down_fwd": lambda: gg.down_fwd(h, w2, meta, d),
-        "combine": lambda: combine_rows(y, r.assignment_row, k, T, weights=wts),
-        "scatter_bwd_gather": lambda: gather_rows(G, r.row_src, k, r.rows_bound, weights=wts,
-                                                  num_rows_dev=nrd, assignment_row=ar),
+        "combine": lambda: combine_rows(y, r.assignment_row, k, T),
         "gemm_down_bwd_dh_ga": dh_only,
         "gemm_down_bwd_dw": dw2_only,
         "gemm_up_bwd_dx": dx_only,
@@ -371,9 +372,8 @@ def main():
     ai = per_gemm_flops / dom_bytes
     ai_bound = min(PEAK_BF16_TFLOPS, ai * PEAK_HBM_GBS / 1e3)
     perm_bytes = {
-        "combine": 2 * A * d + 2 * A + 2 * T * d + 8 * A,
-        "scatter_bwd_gather": 2 * T * d + 2 * A + 2 * A * d + 8 * A,
-        "gather_bwd_combine": 2 * A * d + 2 * T * d + 8 * A,
+        "combine": 2 * A * d + 2 * T * d + 4 * A,
+        "gather_bwd_combine": 2 * A * d + 2 * T * d + 4 * A,
     }
     perm_us = sum(kern[n] for n in perm_bytes)
     perm_gbs = sum(perm_bytes.values()) / (perm_us * 1e-6) / 1e9

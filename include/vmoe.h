@@ -66,6 +66,10 @@ int vmoe_route_max_experts(void);
  *               expert_token_offsets (triton_moe/moe.py:193-197)
  *   padded_counts  [E] int32 (nullable): rounded counts, diff(padded_bins),
  *               the module's padded tokens_per_expert (moe.py:198-202)
+ *   weights     [A] bf16 (nullable): routing weights in the order of
+ *               selected_experts; with row_weight [row_capacity] fp32 (nullable)
+ *               row_weight[row] = weights[row_src[row]], 0 for pad rows: the
+ *               per-row factor the module's up GEMM and dH GEMM apply
  * Only the first P = padded_bins[E-1] rows of row_src/gather_map are written;
  * row_capacity >= A + E*(block_size-1) always suffices.
  * ---------------------------------------------------------------------- */
@@ -76,8 +80,8 @@ int vmoe_route(const void* selected_experts, int32_t selected_is_int64,
                int32_t* tokens_per_expert, int32_t* bins, int32_t* padded_bins,
                int32_t* row_src, int32_t* gather_map, int32_t gather_map_pad,
                int64_t row_capacity, int32_t* assignment_row, int32_t* info,
-               int32_t* expert_offsets,
-               int32_t* padded_counts, void* workspace, size_t workspace_bytes,
+               int32_t* expert_offsets, int32_t* padded_counts, const uint16_t* weights,
+               float* row_weight, void* workspace, size_t workspace_bytes,
                vmoe_stream_t stream);
 
 /* Row maps from caller-supplied routing arrays, for the stand-alone
@@ -186,15 +190,21 @@ int vmoe_combine(const uint16_t* y, int64_t y_rows, int64_t ldy, const int32_t* 
 
 /* out = act(x_e @ W1[:, ewo[e]:ewo[e]+w_e]); pre_act = relu(z) (nullable).
  * Rows of x_e are x[gather_map[row]] when gather_map != NULL (the reference's
- * USE_GATHER_MAP path; x then has x_rows rows), else x[row].
+ * USE_GATHER_MAP path; x then has x_rows rows, ldx = 0 reads one row for all;
+ * map entries outside [0, x_rows), such as -1 for pad rows, read zeros), else
+ * x[row]. row_scale [rows_bound] fp32 (nullable): out[row] =
+ * bf16(row_scale[row] * act(z)) (pre_act is not scaled); the module passes
+ * each row's routing weight (vmoe_route's row_weight), which moves the
+ * weight of the combine onto H.
  * Replaces grouped_gemm_up / _grouped_gemm_up_kernel
  * (triton_moe/kernels/grouped_gemm.py:212-368, 379-477). */
 int vmoe_gemm_up_fwd(const uint16_t* x, int64_t ldx, int64_t x_rows, const int32_t* gather_map,
                      const uint16_t* w1, int64_t ldw1,
                      uint16_t* out, uint16_t* pre_act, int64_t ldo, int32_t activation,
-                     const int32_t* eto, const int32_t* ewo, const int32_t* widths,
-                     const int32_t* tpe, int32_t num_experts, int64_t hidden,
-                     int64_t max_width, int64_t rows_bound, vmoe_stream_t stream);
+                     const float* row_scale, const int32_t* eto, const int32_t* ewo,
+                     const int32_t* widths, const int32_t* tpe, int32_t num_experts,
+                     int64_t hidden, int64_t max_width, int64_t rows_bound,
+                     vmoe_stream_t stream);
 
 /* y = h_e[:, :w_e] @ W2[ewo[e]:ewo[e+1], :].
  * Replaces grouped_gemm_down / _grouped_gemm_down_kernel
@@ -246,20 +256,30 @@ int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
  * (same leading dimension as grad_h) the output is instead the relu^2
  * gradient GA = bf16(pre_act > 0 ? 2 * bf16(grad_h) * pre_act : 0), computed in
  * the epilogue, which is what the up-projection backward consumes.
+ * gather_map (nullable): rows of grad_y are grad_y[gather_map[row]] (grad_y
+ * has gy_rows rows; ldgy = 0 reads one row for all; entries outside
+ * [0, gy_rows) read zeros), e.g. the token gradient of the combine, read
+ * without materialising its per-row copy. row_scale (nullable, fp32
+ * [rows_bound]): grad_h[row] = bf16(row_scale[row] * (grad_y @ W2_e^T)[row])
+ * before the relu^2 rule.
  * Replaces _grouped_gemm_down_backward_dintermediate_kernel
  * (triton_moe/kernels/grouped_gemm.py:970-1063, launched at 1336-1362). */
-int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, const uint16_t* w2,
-                          int64_t ldw2, const uint16_t* pre_act, uint16_t* grad_h,
+int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64_t gy_rows,
+                          const int32_t* gather_map, const uint16_t* w2, int64_t ldw2,
+                          const uint16_t* pre_act, const float* row_scale, uint16_t* grad_h,
                           int64_t ldgh, const int32_t* eto, const int32_t* ewo,
                           const int32_t* widths, const int32_t* tpe, int32_t num_experts,
                           int64_t hidden, int64_t max_width, int64_t rows_bound,
                           vmoe_stream_t stream);
 
-/* grad_w2[ewo[e]:+w_e, :] = H_e^T @ grad_y_e.
+/* grad_w2[ewo[e]:+w_e, :] = H_e^T @ grad_y_e; rows of grad_y_e are
+ * grad_y[gather_map[row]] when gather_map != NULL (gy_rows, ldgy = 0 and
+ * out-of-range entries as for vmoe_gemm_down_bwd_dh), else grad_y[row].
  * Replaces _grouped_gemm_down_backward_dw_kernel
  * (triton_moe/kernels/grouped_gemm.py:1066-1162, launched at 1364-1390). */
 int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint16_t* grad_y,
-                          int64_t ldgy, uint16_t* grad_w2, int64_t ldgw, const int32_t* eto,
+                          int64_t ldgy, int64_t gy_rows, const int32_t* gather_map,
+                          uint16_t* grad_w2, int64_t ldgw, const int32_t* eto,
                           const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
                           int32_t num_experts, int64_t hidden, int64_t max_width,
                           int64_t rows_bound, void* workspace, size_t workspace_bytes,

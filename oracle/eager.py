@@ -17,6 +17,14 @@ Runs on the CPU in float32 (or float64 for pinning tests). Two numerics modes:
     GXg = bf16(GA @ W1^T), GW1 = bf16(Xg^T @ GA) (grouped_gemm.py:793-802, 947-967)
     Gx = bf16(sum_j GXg[row(t, j)])        (gather.py:256-263 via padded_scatter)
   The only remaining difference to a GPU run is fp32 summation order.
+* mode="bf16w": the same products with the routing weight w of each row
+  applied to H instead of to Y, the order the HIP module path rounds in
+  (its up GEMM scales H, so the combine and the backward need no weighted
+  copies of Y or of the output gradient G):
+    H' = bf16(w * relu(z)^2), Y' = bf16(H' @ W2), out = bf16(sum_j Y'[row(t, j)])
+    GH = bf16(w * (G[t] @ W2^T)), GW2 = bf16(H'^T @ G[t]); GA, GXg, GW1, Gx as above.
+  In exact arithmetic all three modes agree: w (H @ W2) = (w H) @ W2 and
+  H^T (w G) = (w H)^T G.
 
 Routing weights get no gradient, as in the reference (scatter.py:176).
 """
@@ -86,10 +94,20 @@ def _rows(r: dict, e: int) -> tuple[int, int]:
     return r0, int(pb[e])
 
 
+def _row_weights(prob: Problem, row_src: torch.Tensor, dt) -> torch.Tensor:
+    """w[row] = weights[row_src[row]], 0 on pad rows (column vector)."""
+    w_flat = prob.weights.to(dt).reshape(-1)
+    valid = row_src >= 0
+    rw = torch.zeros(row_src.numel(), dtype=dt)
+    rw[valid] = w_flat[row_src[valid]]
+    return rw[:, None]
+
+
 def forward(prob: Problem, mode: str = "fp32", r: dict | None = None) -> dict:
-    """Forward of the MoE MLP. Returns out [T, d] and the padded intermediates."""
-    assert mode in ("fp32", "bf16")
-    rb = bf if mode == "bf16" else (lambda t: t)
+    """Forward of the MoE MLP. Returns out [T, d] and the padded intermediates
+    (in mode "bf16w", h and y are the row-weighted H' and Y')."""
+    assert mode in ("fp32", "bf16", "bf16w")
+    rb = bf if mode != "fp32" else (lambda t: t)
     dt = prob.x.dtype
     r = route(prob) if r is None else r
     T, d = prob.x.shape
@@ -100,6 +118,7 @@ def forward(prob: Problem, mode: str = "fp32", r: dict | None = None) -> dict:
     valid = row_src >= 0
     xg = torch.zeros(P, d, dtype=dt)
     xg[valid] = prob.x[row_src[valid] // k]
+    rw = _row_weights(prob, row_src, dt) if mode == "bf16w" else None
     z = torch.zeros(P, max_w, dtype=dt)
     pre = torch.zeros(P, max_w, dtype=dt)
     h = torch.zeros(P, max_w, dtype=dt)
@@ -112,9 +131,10 @@ def forward(prob: Problem, mode: str = "fp32", r: dict | None = None) -> dict:
         z[r0:r1, :w] = ze
         relu = torch.clamp_min(ze, 0)
         pre[r0:r1, :w] = rb(relu)
-        h[r0:r1, :w] = rb(relu * relu)
+        h[r0:r1, :w] = rb(relu * relu if rw is None else rw[r0:r1] * (relu * relu))
         y[r0:r1] = rb(h[r0:r1, :w] @ prob.w2[o:o + w])
-    out = combine(y, r["assignment_row"], prob.weights.to(dt).reshape(-1), k, T, mode)
+    wc = None if mode == "bf16w" else prob.weights.to(dt).reshape(-1)
+    out = combine(y, r["assignment_row"], wc, k, T, mode)
     return {"out": out, "x_gathered": xg, "z": z, "pre_act": pre, "h": h, "y": y, "route": r}
 
 
@@ -122,7 +142,7 @@ def combine(y: torch.Tensor, assignment_row, weights_flat, k: int, T: int,
             mode: str) -> torch.Tensor:
     """out[t] = sum_j slot(t, j), slot = y[row] * w (rounded to bf16 in bf16 mode),
     summed in fp32 in ascending j (scatter.py:61-69, 133)."""
-    rb = bf if mode == "bf16" else (lambda t: t)
+    rb = bf if mode != "fp32" else (lambda t: t)
     ar = torch.as_tensor(np.asarray(assignment_row, np.int64)).view(T, k)
     out = torch.zeros(T, y.shape[1], dtype=y.dtype)
     for j in range(k):
@@ -139,9 +159,10 @@ def combine(y: torch.Tensor, assignment_row, weights_flat, k: int, T: int,
 
 
 def backward(prob: Problem, fwd: dict, grad_out: torch.Tensor, mode: str = "fp32") -> dict:
-    """Gradients of the forward above for upstream grad_out [T, d]."""
-    assert mode in ("fp32", "bf16")
-    rb = bf if mode == "bf16" else (lambda t: t)
+    """Gradients of the forward above for upstream grad_out [T, d] (fwd from
+    forward() in the same mode)."""
+    assert mode in ("fp32", "bf16", "bf16w")
+    rb = bf if mode != "fp32" else (lambda t: t)
     r = fwd["route"]
     dt = prob.x.dtype
     T, d = prob.x.shape
@@ -153,7 +174,12 @@ def backward(prob: Problem, fwd: dict, grad_out: torch.Tensor, mode: str = "fp32
     row_src = torch.from_numpy(r["row_src"].astype(np.int64))
     valid = row_src >= 0
     gy = torch.zeros(P, d, dtype=dt)
-    gy[valid] = rb(g[row_src[valid] // k] * w_flat[row_src[valid], None])
+    rw = None
+    if mode == "bf16w":
+        gy[valid] = g[row_src[valid] // k]  # G[t], the weight goes on GH
+        rw = _row_weights(prob, row_src, dt)
+    else:
+        gy[valid] = rb(g[row_src[valid] // k] * w_flat[row_src[valid], None])
     gh = torch.zeros(P, max_w, dtype=dt)
     ga = torch.zeros(P, max_w, dtype=dt)
     gxg = torch.zeros(P, d, dtype=dt)
@@ -163,7 +189,8 @@ def backward(prob: Problem, fwd: dict, grad_out: torch.Tensor, mode: str = "fp32
         r0, r1 = _rows(r, e)
         if r1 == r0:
             continue
-        ghe = rb(gy[r0:r1] @ prob.w2[o:o + w].T)
+        ghe = gy[r0:r1] @ prob.w2[o:o + w].T
+        ghe = rb(ghe if rw is None else rw[r0:r1] * ghe)
         gh[r0:r1, :w] = ghe
         gw2[o:o + w] = rb(fwd["h"][r0:r1, :w].T @ gy[r0:r1])
         pre = fwd["pre_act"][r0:r1, :w]

@@ -52,9 +52,11 @@ def test_argument_checks_return_invalid_arg():
     lib = _lib.lib()
     # negative sizes / bad enums are rejected before any launch
     assert lib.vmoe_route(None, 0, -1, 4, 1, 64, 0, None, None, None, None, None, None, None,
-                          0, 0, None, None, None, None, None, 0, None) == _lib.ERR_INVALID_ARG
+                          0, 0, None, None, None, None, None, None, None, 0,
+                          None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_route(None, 0, 0, 4, 1, 64, 7, None, None, None, None, None, None, None,
-                          0, 0, None, None, None, None, None, 0, None) == _lib.ERR_INVALID_ARG
+                          0, 0, None, None, None, None, None, None, None, 0,
+                          None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_gather(None, 0, 0, None, 1, None, 0, None, 8, -1, None, 8,
                            None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_combine(None, 0, 0, None, None, 0, None, 8, 1, 8, None) == _lib.ERR_INVALID_ARG
@@ -74,12 +76,15 @@ def test_argument_checks_return_invalid_arg():
     assert lib.vmoe_router_aux(None, 1, 4, 8, None, None, None, None, None, None, None, None,
                                None) == _lib.ERR_INVALID_ARG
     # unaligned hidden size is unsupported, not silently wrong
-    assert lib.vmoe_gemm_up_fwd(None, 8, 0, None, None, 8, None, None, 8, 1, 1, 1, 1, 1, 4, 12,
-                                16, 64, None) == _lib.ERR_UNSUPPORTED
+    assert lib.vmoe_gemm_up_fwd(None, 8, 0, None, None, 8, None, None, 8, 1, None, 1, 1, 1, 1,
+                                4, 12, 16, 64, None) == _lib.ERR_UNSUPPORTED
     assert lib.vmoe_gemm_down_fwd(None, 8, None, 8, None, 8, None, None, None, None, 4, 16, 16,
                                   64, None) == _lib.ERR_INVALID_ARG
-    assert lib.vmoe_gemm_up_fwd(1, 8, 0, None, 1, 8, 1, None, 8, 5, 1, 1, 1, 1, 4, 16, 16, 64,
-                                None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gemm_up_fwd(1, 8, 0, None, 1, 8, 1, None, 8, 5, None, 1, 1, 1, 1, 4, 16,
+                                16, 64, None) == _lib.ERR_INVALID_ARG
+    # a row-weight output without the weights it is read from
+    assert lib.vmoe_route(1, 0, 4, 4, 1, 64, 0, 1, 1, 1, 1, 1, 1, 1, 0, 8, 1, 1, None, None,
+                          None, 1, 1, 4096, None) == _lib.ERR_INVALID_ARG
 
 
 def test_check_maps_status_to_exceptions():

@@ -259,6 +259,58 @@ def test_up_dw_row_map(with_workspace, device):
     assert_close_norm(gw, ref, TIGHT, f"GW1 map ws={with_workspace}")
 
 
+@pytest.mark.parametrize("broadcast", [False, True], ids=["token_rows", "broadcast_row"])
+def test_weighted_rows_through_map(broadcast, device):
+    """The module's fused path: H' = bf16(w_r relu(z)^2) from x_flat[map]
+    (up GEMM with row map and row factor), then from the token gradient G read
+    through the map: GA = relu^2 rule of bf16(w_r (G[map] @ W2^T)) (dH GEMM)
+    and dW2 = H'^T G[map] (dW GEMM). Map entries -1 (pad rows) read zeros;
+    a row-broadcast G (stride 0, the gradient of out.sum()) is one row."""
+    from triton_moe.kernels.grouped_gemm import down_bwd, host_meta, up_fwd
+
+    c = _case(2048, 256, [(2, 256), (2, 128), (2, 64)], 2, 64, False, seed=6)
+    eto, ewo, wid, tpe = _meta_dev(c, device)
+    P, d, max_w, W = c["P"], c["d"], c["max_w"], c["W"]
+    g = torch.Generator().manual_seed(7)
+    T = 1200
+    x_flat = torch.randn(T, d, generator=g).to(torch.bfloat16)
+    gm = torch.randint(0, T, (P,), generator=g, dtype=torch.int32)
+    gm[torch.rand(P, generator=g) < 0.05] = -1
+    w = torch.rand(P, generator=g).to(torch.bfloat16).float()
+    w[gm < 0] = 0.0
+    m = host_meta(eto, ewo, wid, tpe, max_w, d, P, W)
+    h, pre = up_fwd(x_flat.to(device), c["w1"].to(device), m, 1, True, True,
+                    gather_map=gm.to(device), row_scale=w.to(device))
+    xs = torch.where((gm >= 0)[:, None], x_flat[gm.clamp(min=0).long()], torch.zeros(()))
+    h_ref = torch.zeros(P, max_w)
+    pre_ref = torch.zeros(P, max_w)
+    for e, (r0, r1) in enumerate(c["rows"]):
+        wd, o = c["widths"][e], c["offsets"][e]
+        z = torch.relu(xs[r0:r1].float() @ c["w1"][:, o:o + wd].float())
+        pre_ref[r0:r1, :wd] = bf(z)
+        h_ref[r0:r1, :wd] = bf(w[r0:r1, None] * z ** 2)
+    assert_close_norm(h, h_ref, TIGHT, "H' (row-scaled)")
+    assert_close_norm(pre, pre_ref, TIGHT, "PRE")
+    if broadcast:
+        G = torch.randn(1, d, generator=g).to(torch.bfloat16).expand(T, d)
+    else:
+        G = torch.randn(T, d, generator=g).to(torch.bfloat16)
+    hb, preb = h_ref.to(torch.bfloat16), pre_ref.to(torch.bfloat16)
+    ga, gw2 = down_bwd(G.to(device), hb.to(device), c["w2"].to(device), m, d, True,
+                       pre=preb.to(device), gather_map=gm.to(device), row_scale=w.to(device))
+    Gs = torch.where((gm >= 0)[:, None], G[gm.clamp(min=0).long()], torch.zeros(())).float()
+    ga_ref = torch.zeros(P, max_w)
+    gw2_ref = torch.zeros(W, d)
+    for e, (r0, r1) in enumerate(c["rows"]):
+        wd, o = c["widths"][e], c["offsets"][e]
+        gh = bf(w[r0:r1, None] * (Gs[r0:r1] @ c["w2"][o:o + wd].float().T))
+        p_ = preb[r0:r1, :wd].float()
+        ga_ref[r0:r1, :wd] = bf(torch.where(p_ > 0, 2.0 * gh * p_, torch.zeros(())))
+        gw2_ref[o:o + wd] = bf(hb[r0:r1, :wd].float().T @ Gs[r0:r1])
+    assert_close_norm(ga, ga_ref, TIGHT, "GA (mapped, row-scaled)")
+    assert_close_norm(gw2, gw2_ref, TIGHT, "GW2 (mapped)")
+
+
 def test_autograd_entry_points(device):
     """grouped_gemm_up_autograd -> grouped_gemm_down_autograd -> sum().backward()
     (the reference's test_grouped_gemm_backward flow, in bf16)."""

@@ -5,7 +5,9 @@ Protocol: the oracle consumes the device module's own routing decision
 the same inputs), upcasts the bf16 parameters exactly to fp32, and detaches
 the routing weights (the reference gives them no gradient, scatter.py:176).
 Tolerances are normwise (max|d|/max|ref|, mean|d|/mean|ref|): TIGHT against
-the bf16-faithful oracle, LOOSE against the unrounded fp32 oracle.
+the oracle rounding to bf16 where the module does (mode "bf16w": the routing
+weight applied to H, the same products as the reference with other rounding
+points), LOOSE against the unrounded fp32 oracle.
 """
 
 from __future__ import annotations
@@ -64,10 +66,14 @@ def test_forward_backward_vs_oracle(name, device):
     m, x, out, aux, f_i, prob = _run(name, device)
     T, d = prob.x.shape
     assert out.shape == x.shape and out.dtype == torch.bfloat16
-    fb = eager.forward(prob, "bf16")
+    # The module rounds in the "bf16w" order (routing weight applied to H,
+    # so the combine and the backward need no weighted copies): held to the
+    # oracle in that order with only summation order free, and to the
+    # unrounded fp32 oracle with the bf16 tolerance.
+    fb = eager.forward(prob, "bf16w")
     ff = eager.forward(prob, "fp32")
     o = out.detach().reshape(T, d)
-    assert_close_norm(o, fb["out"], TIGHT, f"{name} out vs bf16 oracle")
+    assert_close_norm(o, fb["out"], TIGHT, f"{name} out vs bf16w oracle")
     assert_close_norm(o, ff["out"], LOOSE, f"{name} out vs fp32 oracle")
     # upstream gradient: random (exercises the weighted gather) for small
     # configs, ones (out.sum()) for the large ones
@@ -77,11 +83,11 @@ def test_forward_backward_vs_oracle(name, device):
     else:
         G = torch.ones(T, d, dtype=torch.bfloat16)
         out.sum().backward()
-    bb = eager.backward(prob, fb, G.float(), "bf16")
+    bb = eager.backward(prob, fb, G.float(), "bf16w")
     bf_ = eager.backward(prob, ff, G.float(), "fp32")
     for got, key in ((x.grad.reshape(T, d), "grad_x"), (m.w1.grad, "grad_w1"),
                      (m.w2.grad, "grad_w2")):
-        assert_close_norm(got, bb[key], TIGHT, f"{name} {key} vs bf16 oracle")
+        assert_close_norm(got, bb[key], TIGHT, f"{name} {key} vs bf16w oracle")
         assert_close_norm(got, bf_[key], LOOSE, f"{name} {key} vs fp32 oracle")
     assert m.router.weight.grad is None
 
@@ -114,8 +120,10 @@ def test_forward_with_intermediates(device):
     assert_close_norm(inter["x_after_up"], fb["h"], TIGHT, "x_after_up")
     assert_close_norm(inter["x_after_down"], fb["y"], TIGHT, "x_after_down")
     assert_close_norm(inter["output"].reshape(fb["out"].shape), fb["out"], TIGHT, "output")
-    # the sync-free module path and the public-API path agree bit for bit
-    assert bits_equal(inter["output"], out.detach())
+    # the public-API path rounds in the reference's order, the fused module
+    # path with the routing weight on H: the same products, to bf16 accuracy
+    assert_close_norm(out.detach().reshape(fb["out"].shape), fb["out"], LOOSE,
+                      "module vs public-API order")
     assert set(inter) >= {"x_flat", "router_logits", "router_probs", "top_k_weights",
                           "top_k_weights_flat", "selected_experts", "selected_experts_flat",
                           "x_scattered"}
@@ -171,9 +179,9 @@ def test_config4_full_size_sampled(device):
     tok = torch.randperm(S, generator=g)[:192].sort().values
     sub = eager.Problem(p["x"][tok].float(), p["w1"].float(), p["w2"].float(), p["widths"],
                         p["offsets"], sel.cpu()[tok], wts.cpu()[tok].float(), b)
-    fb = eager.forward(sub, "bf16")
+    fb = eager.forward(sub, "bf16w")
     assert_close_norm(out.detach().reshape(S, d)[tok.to(device)], fb["out"], TIGHT, "cfg4 out")
-    bb = eager.backward(sub, fb, torch.ones(len(tok), d), "bf16")
+    bb = eager.backward(sub, fb, torch.ones(len(tok), d), "bf16w")
     assert_close_norm(x.grad.reshape(S, d)[tok.to(device)], bb["grad_x"], TIGHT, "cfg4 x.grad")
     # weight gradients: full oracle on a few experts' columns (all their tokens)
     full = eager.Problem(p["x"].float(), p["w1"].float(), p["w2"].float(), p["widths"],
@@ -190,12 +198,14 @@ def test_config4_full_size_sampled(device):
         we = torch.zeros(r1 - r0)
         we[ok] = wts.cpu().float().reshape(-1)[rs[ok]]
         z = xe @ p["w1"][:, o:o + w].float()
+        # the "bf16w" order: H' = bf16(w relu(z)^2), GH = bf16(w (G @ W2^T))
         pre = eager.bf(torch.relu(z))
-        h = eager.bf(torch.relu(z) ** 2)
-        gy = eager.bf(torch.ones(r1 - r0, d) * we[:, None])
-        gh = eager.bf(gy @ p["w2"][o:o + w].float().T)
+        h = eager.bf(we[:, None] * torch.relu(z) ** 2)
+        g_rows = torch.zeros(r1 - r0, d)
+        g_rows[ok] = 1.0
+        gh = eager.bf(we[:, None] * (g_rows @ p["w2"][o:o + w].float().T))
         ga = eager.bf(torch.where(pre > 0, gh * 2.0 * pre, torch.zeros_like(pre)))
-        gw2 = eager.bf(h.T @ gy)
+        gw2 = eager.bf(h.T @ g_rows)
         gw1 = eager.bf(xe.T @ ga)
         assert_close_norm(m.w2.grad[o:o + w], gw2, TIGHT, f"cfg4 gw2 e{e}")
         assert_close_norm(m.w1.grad[:, o:o + w], gw1, TIGHT, f"cfg4 gw1 e{e}")

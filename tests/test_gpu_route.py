@@ -85,11 +85,16 @@ def test_route_random_topk(T, k, E, b, mode, device):
     np.testing.assert_array_equal(_np(r.row_src[:P]), maps["row_src"])
     np.testing.assert_array_equal(_np(r.gather_map[:P]), maps["gather_map"])
     np.testing.assert_array_equal(_np(r.assignment_row), maps["assignment_row"])
-    # the module's map: pad rows -1 (read as zeros by the GEMMs' row gather)
-    r2 = route_device(sel, E, k, b, mode, map_pad=-1)
+    # the module's map: pad rows -1 (read as zeros by the GEMMs' row gather),
+    # and each row's routing weight (0 on pad rows)
+    wts = torch.rand(sel.numel(), generator=g, device=device).to(torch.bfloat16)
+    r2 = route_device(sel, E, k, b, mode, map_pad=-1, weights=wts)
     gm2 = np.where(maps["row_src"] < 0, -1, maps["gather_map"])
     np.testing.assert_array_equal(_np(r2.gather_map[:P]), gm2)
     np.testing.assert_array_equal(_np(r2.row_src[:P]), maps["row_src"])
+    rs = torch.from_numpy(maps["row_src"]).long()
+    rw_ref = torch.where(rs >= 0, wts.cpu().float()[rs.clamp(min=0)], torch.zeros(()))
+    assert torch.equal(r2.row_weight[:P].cpu(), rw_ref)
 
 
 def test_route_deterministic_and_large(device):

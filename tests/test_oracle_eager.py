@@ -108,6 +108,54 @@ def test_bf16_mode_close_to_fp32_mode():
     assert (a - b).abs().mean() / a.abs().mean() < 1e-2
 
 
+def test_bf16w_rounding_points_by_hand():
+    """Mode "bf16w" puts the routing weight on H: H' = bf16(w relu(z)^2),
+    out = bf16(H' @ W2) (unweighted combine), GH = bf16(w (G @ W2^T))."""
+    f = torch.float32
+    a = 1.0 + 2.0 ** -7  # exact in bf16
+    x = torch.tensor([[1.0]], dtype=f)
+    one = torch.tensor([[1.0]], dtype=f)
+    # relu(z) = 1, w = a: H' = a exactly; W2 = a: out = bf16(a * a) = 1 + 2^-6
+    prob = eager.Problem(x, one, torch.tensor([[a]], dtype=f), [1], [0, 1],
+                         torch.tensor([[0]]), torch.tensor([[a]], dtype=f), 1)
+    fw = eager.forward(prob, "bf16w")
+    assert fw["h"][0, 0].item() == a
+    assert fw["out"].item() == 1.0 + 2.0 ** -6
+    # the reference order rounds y = a first, then bf16(y * w): the same here
+    assert eager.forward(prob, "bf16")["out"].item() == 1.0 + 2.0 ** -6
+    # G = a: GH = bf16(w * (G @ W2^T)) = bf16(a^3) = 1 + 3 * 2^-7 (exact: 1 + 3*2^-7
+    # + 3*2^-14 + 2^-21 rounds down), and the reference's GY = bf16(a * a) = 1 + 2^-6,
+    # GH = bf16(GY * a) = bf16(1 + 3*2^-7 + 2^-13) = 1 + 3 * 2^-7: same, by another path
+    bw = eager.backward(prob, fw, torch.tensor([[a]], dtype=f), "bf16w")
+    assert bw["grad_h"][0, 0].item() == 1.0 + 3 * 2.0 ** -7
+    # dW2 = H'^T G = a * a -> bf16 1 + 2^-6
+    assert bw["grad_w2"][0, 0].item() == 1.0 + 2.0 ** -6
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_bf16w_mode_no_less_accurate_than_bf16(seed):
+    """Both bf16 orders against the unrounded fp32 mode: the row-weighted
+    order (fewer roundings per product) is within bf16 tolerance and no
+    worse than the reference's order by more than a little."""
+    prob = _problem(seed, 128, 64, [(2, 64), (4, 32)], 2, 8, dtype=torch.float32)
+    prob.x = prob.x.to(torch.bfloat16).float()
+    prob.w1 = prob.w1.to(torch.bfloat16).float()
+    prob.w2 = prob.w2.to(torch.bfloat16).float()
+    ff, fb, fw = (eager.forward(prob, m) for m in ("fp32", "bf16", "bf16w"))
+    G = torch.randn(prob.x.shape, generator=torch.Generator().manual_seed(seed + 3))
+    bf_, bb, bw = (eager.backward(prob, f_, G, m)
+                   for f_, m in ((ff, "fp32"), (fb, "bf16"), (fw, "bf16w")))
+
+    def mean_err(a, b):
+        return ((a - b).abs().mean() / b.abs().mean()).item()
+
+    pairs = [(fw["out"], fb["out"], ff["out"])] + [
+        (bw[key], bb[key], bf_[key]) for key in ("grad_x", "grad_w1", "grad_w2")]
+    for w_, b_, ref in pairs:
+        assert mean_err(w_, ref) < 6e-3
+        assert mean_err(w_, ref) <= 1.1 * mean_err(b_, ref) + 1e-4
+
+
 def test_aux_losses_uniform_and_grouped():
     g = torch.Generator().manual_seed(0)
     L = torch.randn(50, 8, generator=g)

@@ -83,6 +83,9 @@ struct Args {
   int64_t ldc;
   uint16_t* c2;          // UP_FWD: pre_act output (nullable)
   const uint16_t* pre;   // DOWN_DH: pre_act input -> fused relu^2 gradient (nullable)
+  const int32_t* b_map;  // row gather for B (T-form, DOWN_DW), nullable
+  int64_t b_rows;        // rows of B's gathered source
+  const float* row_scale;  // UP_FWD / DOWN_DH: per-row factor of the output (nullable)
   const int32_t* eto;
   const int32_t* ewo;
   const int32_t* widths;
@@ -133,7 +136,7 @@ struct Traits;
 template <>
 struct Traits<UP_FWD> {
   static constexpr bool k_map = true;  // A rows may come through the gather map
-  static constexpr bool t_map = false;
+  static constexpr bool t_map = false, t_map_b = false;
   static constexpr bool a_k = true, b_k = false;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
@@ -150,7 +153,7 @@ struct Traits<UP_FWD> {
 template <>
 struct Traits<DOWN_FWD> {
   static constexpr bool k_map = false;
-  static constexpr bool t_map = false;
+  static constexpr bool t_map = false, t_map_b = false;
   static constexpr bool a_k = true, b_k = false;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
@@ -167,7 +170,7 @@ struct Traits<DOWN_FWD> {
 template <>
 struct Traits<UP_DX> {
   static constexpr bool k_map = false;
-  static constexpr bool t_map = false;
+  static constexpr bool t_map = false, t_map_b = false;
   static constexpr bool a_k = true, b_k = true;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
@@ -186,6 +189,7 @@ struct Traits<UP_DW> {
   static constexpr bool k_map = false;
   static constexpr bool a_k = false, b_k = false;
   static constexpr bool t_map = true;  // A rows may come through the gather map
+  static constexpr bool t_map_b = false;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
     q.M = p.hidden;
@@ -200,8 +204,8 @@ struct Traits<UP_DW> {
 
 template <>
 struct Traits<DOWN_DH> {
-  static constexpr bool k_map = false;
-  static constexpr bool t_map = false;
+  static constexpr bool k_map = true;  // A (the output gradient) may come through the map
+  static constexpr bool t_map = false, t_map_b = false;
   static constexpr bool a_k = true, b_k = true;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
@@ -219,6 +223,7 @@ template <>
 struct Traits<DOWN_DW> {
   static constexpr bool k_map = false;
   static constexpr bool t_map = false;
+  static constexpr bool t_map_b = true;  // B (the output gradient) may come through the map
   static constexpr bool a_k = false, b_k = false;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
@@ -438,6 +443,11 @@ struct Gemm {
   // while the current one streams (two windows per wave); a scalar load of
   // the entries instead waits on the scalar cache once per stage.
   static constexpr int kWinStages = 8;
+  // Row factors of the output (UP_FWD, DOWN_DH): one slot of BM floats per
+  // item, as many slots as the producers can run items ahead (each item has
+  // at least one stage and they run at most kStages - 1 stages ahead).
+  static constexpr bool kScaled = V == UP_FWD || V == DOWN_DH;
+  static constexpr int kScaleSlots = kStages;
   struct TMap {
     __amdgpu_buffer_rsrc_t mrs;  // over the row map
     lds_char* win;               // this wave's window of the current item
@@ -496,13 +506,13 @@ struct Gemm {
   template <int R, int PW, bool MAP>
   __device__ static void setup_t(Src<PW>& s, TMap& tm, const uint16_t* base, int64_t ld,
                                  const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
-                                 int cols_valid, int k_valid) {
+                                 int cols_valid, int k_valid, bool owns_map = true) {
     constexpr int LPR = Dma<R>::LPR, RPI = Dma<R>::RPI;
     const int lane = threadIdx.x & 63, wave = pwave();
     if (!MAP) map = nullptr;
     s.rsrc = make_rsrc(map ? base + c0 : base + r0 * ld + c0);
     s.ld2 = (uint32_t)(ld * 2);
-    tm.on = MAP && map;
+    if (owns_map) tm.on = MAP && map;
     if (MAP && map) {
       tm.mbase = r0;
       tm.klen = k_valid;
@@ -543,7 +553,6 @@ struct Gemm {
       const bool v = s.ok[i] && k0 + s.idx[i] < K;
       uint32_t off = v ? s.off[i] + (uint32_t)k0 * s.ld2 : kOob;
       if constexpr (MAP) {
-        static_assert(RPI == 4, "map window assumes 4 k-rows per DMA instruction");
         if (tm.on) {
           const int e = (kt % kWinStages) * 8 + i * RPI + lane / LPR;
           const int32_t row = reinterpret_cast<const __attribute__((address_space(3))) int32_t*>(
@@ -668,11 +677,12 @@ struct Gemm {
     return w;
   }
 
-  // Map fields of the A operand of work w (T-form gather).
+  // Map fields of work w for the gathered T-form operand (A of UP_DW, B of
+  // DOWN_DW).
   __device__ static void setup_map(const Args& p, const Work& w, TMap& tm) {
-    tm.mbase = w.q.ar + w.kbeg;
+    tm.mbase = (T::t_map_b ? w.q.br : w.q.ar) + w.kbeg;
     tm.klen = w.klen;
-    tm.rows = (uint32_t)p.a_rows;
+    tm.rows = (uint32_t)(T::t_map_b ? p.b_rows : p.a_rows);
     tm.on = true;
   }
 
@@ -683,15 +693,12 @@ struct Gemm {
       setup_k<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.m0, q.ac + w.kbeg, q.M - w.m0);
     else
       setup_t<BM, PWA, T::t_map>(sa, tm, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.kbeg,
-                                 q.ac + w.m0, q.M - w.m0, w.klen);
+                                 q.ac + w.m0, q.M - w.m0, w.klen, !T::t_map_b);
     if (T::b_k)
       setup_k<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg, q.N - w.n0);
     else
-    {
-      TMap none;  // B is never gathered
-      setup_t<BN, PWB, false>(sb, none, p.b, p.ldb, nullptr, 0, q.br + w.kbeg, q.bc + w.n0,
-                              q.N - w.n0, w.klen);
-    }
+      setup_t<BN, PWB, T::t_map_b>(sb, tm, p.b, p.ldb, p.b_map, p.b_rows, q.br + w.kbeg,
+                                   q.bc + w.n0, q.N - w.n0, w.klen, T::t_map_b);
   }
 
   __device__ static void issue(const Work& w, const Src<PWA>& sa, const Src<PWB>& sb,
@@ -699,11 +706,7 @@ struct Gemm {
     const int k0 = kt * BK;
     if (T::a_k) issue_k<BM>(sa, k0, w.klen, st); else issue_t<BM, PWA, T::t_map>(sa, tm, kt, w.klen, st);
     if (T::b_k) issue_k<BN>(sb, k0, w.klen, st + A_STAGE);
-    else {
-      TMap none;
-      none.on = false;
-      issue_t<BN, PWB, false>(sb, none, kt, w.klen, st + A_STAGE);
-    }
+    else issue_t<BN, PWB, T::t_map_b>(sb, tm, kt, w.klen, st + A_STAGE);
   }
 
   // Multiplies one staged k-tile into the wave's accumulators.
@@ -797,10 +800,24 @@ struct Gemm {
   // tile must be fully stored): relu / relu^2 for the up projection
   // (PRE = bf16(relu(z)), H = bf16(relu(z)^2), grouped_gemm.py:336-346),
   // the accumulators as they are otherwise.
-  __device__ __forceinline__ static void stash(const Args& p, const Work& w, const f32x16_t (&acc)[FM][FN],
-                               Pending& pd) {
+  __device__ __forceinline__ static void stash(const Args& p, const Work& w,
+                                              const f32x16_t (&acc)[FM][FN], Pending& pd,
+                                              const lds_char* scale) {
     const int wave = threadIdx.x >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
+    // Row factors (UP_FWD: the output H, not PRE; DOWN_DH: the gradient
+    // before the relu^2 rule): acc row wm * WM + 32 i + (lane & 31).
+    float sc[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) sc[i] = 1.0f;
+    if constexpr (kScaled) {
+      if (scale) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          sc[i] = reinterpret_cast<const __attribute__((address_space(3))) float*>(scale)
+              [wm * WM + i * 32 + (threadIdx.x & 31)];
+      }
+    }
     const Prob& q = w.q;
     pd.mb = w.m0 + wm * WM;
     pd.nb = w.n0 + wn * WN;
@@ -826,9 +843,9 @@ struct Gemm {
               const float ra = r2 ? fmaxf(a, 0.0f) : a, rb = r2 ? fmaxf(b, 0.0f) : b;
               pd.pk[0][i][j][2 * g + hh] = pack_bf16(ra, rb);
               pd.pk[NOUT - 1][i][j][2 * g + hh] =
-                  pack_bf16(r2 ? ra * ra : ra, r2 ? rb * rb : rb);
+                  pack_bf16(sc[i] * (r2 ? ra * ra : ra), sc[i] * (r2 ? rb * rb : rb));
             } else {
-              pd.pk[NOUT - 1][i][j][2 * g + hh] = pack_bf16(a, b);
+              pd.pk[NOUT - 1][i][j][2 * g + hh] = pack_bf16(sc[i] * a, sc[i] * b);
             }
           }
   }
@@ -923,14 +940,18 @@ struct Gemm {
   // (an item of fewer stages than the ring is deep, or the first one)
   // waits for its window explicitly.
   __device__ static void run_producer(const Args& p, lds_char* ring, lds_char* wins,
-                                      const Meta& mt, const Range& rg) {
+                                      lds_char* scl, const Meta& mt, const Range& rg) {
     int ec = 0, ei = 0, ela = 0;
     Work wi = decode(p, mt, rg.beg, ei, rg.slot);
     Src<PWA> sa;
     Src<PWB> sb;
     TMap tm;
-    const bool mapped = T::t_map && p.a_map;
-    if (mapped) tm.mrs = make_rsrc(p.a_map);
+    const bool mapped = (T::t_map && p.a_map) || (T::t_map_b && p.b_map);
+    if (mapped) tm.mrs = make_rsrc(T::t_map_b ? p.b_map : p.a_map);
+    const bool scaled = kScaled && p.row_scale;
+    __amdgpu_buffer_rsrc_t srs;
+    if (scaled) srs = make_rsrc(p.row_scale);
+    int nbegun = 0;         // items begun (their row factors go to slot nbegun % 4)
     lds_char* const win0 = wins + pwave() * 256;
     lds_char* const win1 = win0 + kProducers * 256;
     int wcur = 0;           // window of the current item (0: win0, 1: win1)
@@ -942,6 +963,19 @@ struct Gemm {
     bool fresh = true;      // wi not set up yet
     auto begin_item = [&]() {
       setup(p, wi, sa, sb, tm);
+      if (scaled && pwave() == 0) {
+        // The tile's BM row factors into the item's slot; the consumers read
+        // them when they round the tile, many barriers after this DMA.
+        const int lane = threadIdx.x & 63;
+        const int64_t r0 = (int64_t)wi.q.cr + wi.m0;
+        lds_char* slot = scl + (nbegun % kScaleSlots) * (BM * 4);
+#pragma unroll
+        for (int h = 0; h < BM / 64; ++h) {
+          const int m = wi.m0 + h * 64 + lane;
+          dma4(srs, m < wi.q.M ? (uint32_t)((r0 + h * 64 + lane) * 4) : kOob, slot + h * 256);
+        }
+      }
+      ++nbegun;
       if (!mapped) return;
       if (la_item == witem) {
         wcur ^= 1;
@@ -1014,9 +1048,10 @@ struct Gemm {
   // end inside a split tile; such a segment is a partial sum and goes to
   // slot 2 * lin (the range's first segment) or 2 * lin + 1 (its last).
   __device__ static void run_consumer(const Args& p, const lds_char* ring, const Meta& mt,
-                                      const Range& rg, lds_char* scr) {
+                                      const Range& rg, lds_char* scr, const lds_char* scl) {
     int ec = 0;
     int s = 0;
+    int nbegun = 0;  // items with k-steps so far (the producers' slot count)
     int seg_item = rg.beg, seg_chunk = -1;
     f32x16_t acc[FM][FN];
     Pending pd;
@@ -1024,6 +1059,11 @@ struct Gemm {
     for (int item = rg.beg; item < rg.end; item += rg.stride) {
       const Work w = decode(p, mt, item, ec, rg.slot);
       if (w.skip) continue;
+      int slot = 0;
+      if constexpr (kScaled) {
+        slot = nbegun % kScaleSlots;
+        if (w.nk > 0) ++nbegun;
+      }
       if (seg_chunk < 0) {
         seg_item = item;
         seg_chunk = w.chunk;
@@ -1063,7 +1103,8 @@ struct Gemm {
         if (w.chunks > 1 && !(seg_chunk == 0 && last_chunk)) {
           store_partial(p, 2 * rg.lin + (seg_item == rg.beg ? 0 : 1), acc);
         } else {
-          stash(p, w, acc, pd);
+          stash(p, w, acc, pd, kScaled && p.row_scale && w.nk > 0 ? scl + slot * (BM * 4)
+                                                                  : nullptr);
           if (Cfg<V>::contig) {
             flush_slot<0>(p, pd, scr);
             flush_slot<1>(p, pd, scr);
@@ -1083,15 +1124,15 @@ struct Gemm {
   }
 
   __device__ static void run(const Args& p, lds_char* ring, Meta& mt, lds_char* epi,
-                             lds_char* wins) {
+                             lds_char* wins, lds_char* scl) {
     const int total = build_meta(p, mt, (long long*)(char*)ring);
     const Range rg = item_range<Cfg<V>::contig>(total);
     if (rg.beg >= rg.end) return;
     const int wave = threadIdx.x >> 6;
     if (wave >= kConsumers)
-      run_producer(p, ring, wins, mt, rg);
+      run_producer(p, ring, wins, scl, mt, rg);
     else
-      run_consumer(p, ring, mt, rg, epi + wave * EPI_BYTES);
+      run_consumer(p, ring, mt, rg, epi + wave * EPI_BYTES, scl);
   }
 };
 
@@ -1102,11 +1143,16 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
   __shared__ __align__(16) char epi[kConsumers * G::EPI_BYTES];
   __shared__ Meta meta;
   // Row-map windows of the producers (two per wave), for the T-form gather.
-  constexpr int WIN_BYTES = Traits<V>::t_map ? 2 * kProducers * 256 : 16;
+  constexpr int WIN_BYTES =
+      Traits<V>::t_map || Traits<V>::t_map_b ? 2 * kProducers * 256 : 16;
   __shared__ __align__(16) char wins[WIN_BYTES];
-  static_assert(G::RING + kConsumers * G::EPI_BYTES + sizeof(Meta) + WIN_BYTES <= 160 * 1024,
+  // Per-row output factors, kScaleSlots slots of BM floats.
+  constexpr int SCL_BYTES = G::kScaled ? G::kScaleSlots * G::BM * 4 : 16;
+  __shared__ __align__(16) char scl[SCL_BYTES];
+  static_assert(G::RING + kConsumers * G::EPI_BYTES + sizeof(Meta) + WIN_BYTES + SCL_BYTES <=
+                    160 * 1024,
                 "LDS budget of a gfx950 CU");
-  G::run(p, (lds_char*)ring, meta, (lds_char*)epi, (lds_char*)wins);
+  G::run(p, (lds_char*)ring, meta, (lds_char*)epi, (lds_char*)wins, (lds_char*)scl);
 }
 
 // Finds the expert owning tile `id` in the concatenation of per-expert tile
@@ -1344,6 +1390,12 @@ inline int check_common(const int32_t* eto, const int32_t* ewo, const int32_t* w
 
 inline bool ld_ok(int64_t ld) { return ld > 0 && ld % 8 == 0; }
 
+// Leading dimension of a source of `cols` columns; a source read through a
+// row map may also be one row broadcast to all (ld = 0).
+inline bool src_ld_ok(int64_t ld, int64_t cols, const int32_t* map) {
+  return (map && ld == 0) || (ld_ok(ld) && ld >= cols);
+}
+
 // DMA offsets are 31-bit byte offsets from an operand base (rebased to the
 // tile where rows are not gathered): every source the kernels address by a
 // row index must span less than 2 GiB.
@@ -1357,15 +1409,16 @@ using namespace vmoe;
 extern "C" int vmoe_gemm_up_fwd(const uint16_t* x, int64_t ldx, int64_t x_rows,
                                 const int32_t* gather_map, const uint16_t* w1, int64_t ldw1,
                                 uint16_t* out, uint16_t* pre_act, int64_t ldo, int32_t activation,
-                                const int32_t* eto, const int32_t* ewo, const int32_t* widths,
-                                const int32_t* tpe, int32_t E, int64_t hidden, int64_t max_width,
-                                int64_t rows_bound, vmoe_stream_t stream) {
+                                const float* row_scale, const int32_t* eto, const int32_t* ewo,
+                                const int32_t* widths, const int32_t* tpe, int32_t E,
+                                int64_t hidden, int64_t max_width, int64_t rows_bound,
+                                vmoe_stream_t stream) {
   int st = check_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
   if (st) return st;
   if (activation != VMOE_ACT_NONE && activation != VMOE_ACT_RELU_SQUARED)
     return VMOE_ERR_INVALID_ARG;
   if (!x || !w1 || !out || x_rows < 0) return VMOE_ERR_INVALID_ARG;
-  if (!ld_ok(ldx) || !ld_ok(ldw1) || !ld_ok(ldo) || ldx < hidden || ldo < max_width)
+  if (!src_ld_ok(ldx, hidden, gather_map) || !ld_ok(ldw1) || !ld_ok(ldo) || ldo < max_width)
     return VMOE_ERR_UNSUPPORTED;
   if (!a16(x) || !a16(w1) || !a16(out) || (pre_act && !a16(pre_act)))
     return VMOE_ERR_UNSUPPORTED;
@@ -1375,6 +1428,7 @@ extern "C" int vmoe_gemm_up_fwd(const uint16_t* x, int64_t ldx, int64_t x_rows,
   p.a = x; p.lda = ldx; p.a_map = gather_map; p.a_rows = gather_map ? x_rows : 0;
   p.b = w1; p.ldb = ldw1;
   p.c = out; p.c2 = activation == VMOE_ACT_RELU_SQUARED ? pre_act : nullptr; p.ldc = ldo;
+  p.row_scale = row_scale;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = activation; p.rows_bound = rows_bound;
   return launch<UP_FWD>(p, row_items<UP_FWD>(rows_bound, E, max_width),
@@ -1457,7 +1511,8 @@ extern "C" int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_row
   int st = check_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
   if (st) return st;
   if (!x || !grad_act || !grad_w1 || x_rows < 0) return VMOE_ERR_INVALID_ARG;
-  if (!ld_ok(ldx) || !ld_ok(ldg) || !ld_ok(ldgw) || ldx < hidden) return VMOE_ERR_UNSUPPORTED;
+  if (!src_ld_ok(ldx, hidden, gather_map) || !ld_ok(ldg) || !ld_ok(ldgw))
+    return VMOE_ERR_UNSUPPORTED;
   if (!a16(x) || !a16(grad_act) || !a16(grad_w1)) return VMOE_ERR_UNSUPPORTED;
   if (!span_ok(gather_map ? x_rows : rows_bound, ldx) || !span_ok(rows_bound, ldg))
     return VMOE_ERR_UNSUPPORTED;
@@ -1471,25 +1526,29 @@ extern "C" int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_row
                           reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, const uint16_t* w2,
-                                     int64_t ldw2, const uint16_t* pre_act, uint16_t* grad_h,
-                                     int64_t ldgh, const int32_t* eto, const int32_t* ewo,
+extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64_t gy_rows,
+                                     const int32_t* gather_map, const uint16_t* w2,
+                                     int64_t ldw2, const uint16_t* pre_act,
+                                     const float* row_scale, uint16_t* grad_h, int64_t ldgh,
+                                     const int32_t* eto, const int32_t* ewo,
                                      const int32_t* widths, const int32_t* tpe, int32_t E,
                                      int64_t hidden, int64_t max_width, int64_t rows_bound,
                                      vmoe_stream_t stream) {
   int st = check_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
   if (st) return st;
-  if (!grad_y || !w2 || !grad_h) return VMOE_ERR_INVALID_ARG;
-  if (!ld_ok(ldgy) || !ld_ok(ldw2) || !ld_ok(ldgh) || ldgy < hidden || ldw2 < hidden ||
+  if (!grad_y || !w2 || !grad_h || gy_rows < 0) return VMOE_ERR_INVALID_ARG;
+  if (!src_ld_ok(ldgy, hidden, gather_map) || !ld_ok(ldw2) || !ld_ok(ldgh) || ldw2 < hidden ||
       ldgh < max_width)
     return VMOE_ERR_UNSUPPORTED;
   if (!a16(grad_y) || !a16(w2) || !a16(grad_h) || (pre_act && !a16(pre_act)))
     return VMOE_ERR_UNSUPPORTED;
+  if (gather_map && !span_ok(gy_rows, ldgy)) return VMOE_ERR_UNSUPPORTED;
   Args p{};
-  p.a = grad_y; p.lda = ldgy;
+  p.a = grad_y; p.lda = ldgy; p.a_map = gather_map; p.a_rows = gather_map ? gy_rows : 0;
   p.b = w2; p.ldb = ldw2;
   p.c = grad_h; p.ldc = ldgh;
   p.pre = pre_act;
+  p.row_scale = row_scale;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
   return launch<DOWN_DH>(p, row_items<DOWN_DH>(rows_bound, E, max_width),
@@ -1497,22 +1556,23 @@ extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, const
 }
 
 extern "C" int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint16_t* grad_y,
-                                     int64_t ldgy, uint16_t* grad_w2, int64_t ldgw,
-                                     const int32_t* eto, const int32_t* ewo,
-                                     const int32_t* widths, const int32_t* tpe, int32_t E,
-                                     int64_t hidden, int64_t max_width, int64_t rows_bound,
-                                     void* workspace, size_t workspace_bytes,
-                                     vmoe_stream_t stream) {
+                                     int64_t ldgy, int64_t gy_rows, const int32_t* gather_map,
+                                     uint16_t* grad_w2, int64_t ldgw, const int32_t* eto,
+                                     const int32_t* ewo, const int32_t* widths,
+                                     const int32_t* tpe, int32_t E, int64_t hidden,
+                                     int64_t max_width, int64_t rows_bound, void* workspace,
+                                     size_t workspace_bytes, vmoe_stream_t stream) {
   int st = check_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
   if (st) return st;
-  if (!h || !grad_y || !grad_w2) return VMOE_ERR_INVALID_ARG;
-  if (!ld_ok(ldh) || !ld_ok(ldgy) || !ld_ok(ldgw) || ldgy < hidden || ldgw < hidden)
+  if (!h || !grad_y || !grad_w2 || gy_rows < 0) return VMOE_ERR_INVALID_ARG;
+  if (!ld_ok(ldh) || !src_ld_ok(ldgy, hidden, gather_map) || !ld_ok(ldgw) || ldgw < hidden)
     return VMOE_ERR_UNSUPPORTED;
   if (!a16(h) || !a16(grad_y) || !a16(grad_w2)) return VMOE_ERR_UNSUPPORTED;
-  if (!span_ok(rows_bound, ldh) || !span_ok(rows_bound, ldgy)) return VMOE_ERR_UNSUPPORTED;
+  if (!span_ok(rows_bound, ldh) || !span_ok(gather_map ? gy_rows : rows_bound, ldgy))
+    return VMOE_ERR_UNSUPPORTED;
   Args p{};
   p.a = h; p.lda = ldh;
-  p.b = grad_y; p.ldb = ldgy;
+  p.b = grad_y; p.ldb = ldgy; p.b_map = gather_map; p.b_rows = gather_map ? gy_rows : 0;
   p.c = grad_w2; p.ldc = ldgw;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;

@@ -107,8 +107,8 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     RouteWs ws, int E, int ntiles, int block, int mode, int32_t* __restrict__ tpe,
     int32_t* __restrict__ bins, int32_t* __restrict__ padded_bins,
     int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int32_t map_pad,
-    int64_t row_capacity, int32_t* __restrict__ info, int32_t* __restrict__ expert_offsets,
-    int32_t* __restrict__ padded_counts) {
+    float* __restrict__ row_weight, int64_t row_capacity, int32_t* __restrict__ info,
+    int32_t* __restrict__ expert_offsets, int32_t* __restrict__ padded_counts) {
   __shared__ int32_t scan_smem[kScanThreads / kWave + 1];
   __shared__ int32_t carry_kept, carry_rounded, any_bad;
   extern __shared__ int32_t lds[];
@@ -196,6 +196,7 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
       if (row < row_capacity) {
         row_src[row] = -1;
         gather_map[row] = map_pad;
+        if (row_weight) row_weight[row] = 0.0f;
       }
     }
   }
@@ -216,7 +217,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_place_kernel(
     const void* __restrict__ sel, int is64, int64_t A, int E, int nbits, int ntiles,
     int top_k, RouteWs ws, int32_t* __restrict__ bin_ids, int32_t* __restrict__ indices,
     int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int64_t row_capacity,
-    int32_t* __restrict__ assignment_row) {
+    int32_t* __restrict__ assignment_row, const uint16_t* __restrict__ weights,
+    float* __restrict__ row_weight) {
   extern __shared__ int32_t wbase[];  // [kRouteWaves][E]
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) wbase[i] = 0;
@@ -275,6 +277,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_place_kernel(
         if (row < row_capacity) {
           row_src[row] = (int32_t)p;
           gather_map[row] = (int32_t)(p / top_k);
+          if (row_weight) row_weight[row] = __uint_as_float((uint32_t)weights[p] << 16);
         }
       } else {
         assignment_row[p] = -1;
@@ -338,8 +341,8 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
                           int32_t* tpe, int32_t* bins, int32_t* padded_bins, int32_t* row_src,
                           int32_t* gather_map, int32_t gather_map_pad, int64_t row_capacity,
                           int32_t* assignment_row, int32_t* info, int32_t* expert_offsets,
-                          int32_t* padded_counts, void* workspace, size_t ws_bytes,
-                          vmoe_stream_t stream) {
+                          int32_t* padded_counts, const uint16_t* weights, float* row_weight,
+                          void* workspace, size_t ws_bytes, vmoe_stream_t stream) {
   if (A < 0 || E <= 0 || top_k <= 0 || block <= 0 || row_capacity < 0)
     return VMOE_ERR_INVALID_ARG;
   if (rounding < VMOE_ROUND_UP || rounding > VMOE_ROUND_NEAREST) return VMOE_ERR_INVALID_ARG;
@@ -347,6 +350,7 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
   if (!tpe || !bins || !padded_bins || !info || !workspace) return VMOE_ERR_INVALID_ARG;
   if (A > 0 && (!sel || !bin_ids || !indices || !assignment_row)) return VMOE_ERR_INVALID_ARG;
   if (row_capacity > 0 && (!row_src || !gather_map)) return VMOE_ERR_INVALID_ARG;
+  if (row_weight && !weights) return VMOE_ERR_INVALID_ARG;
   if (ws_bytes < vmoe_route_workspace_bytes(A, E)) return VMOE_ERR_WORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
@@ -359,8 +363,8 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
   }
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), sizeof(int32_t) * (4 * E + 1),
                      s, ws, E, ntiles, block, rounding, tpe, bins, padded_bins, row_src,
-                     gather_map, gather_map_pad, row_capacity, info, expert_offsets,
-                     padded_counts);
+                     gather_map, gather_map_pad, row_weight, row_capacity, info,
+                     expert_offsets, padded_counts);
   VMOE_CHECK_LAUNCH();
   if (ntiles > 0) {
     int nbits = 1;
@@ -368,7 +372,7 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
     hipLaunchKernelGGL(route_place_kernel, dim3(ntiles), dim3(kRouteThreads),
                        sizeof(int32_t) * kRouteWaves * E, s, sel, is64, A, E, nbits, ntiles,
                        top_k, ws, bin_ids, indices, row_src, gather_map, row_capacity,
-                       assignment_row);
+                       assignment_row, weights, row_weight);
     VMOE_CHECK_LAUNCH();
   }
   return VMOE_OK;

@@ -27,14 +27,14 @@ _SIGNATURES = {
     "vmoe_route_max_experts": [],
     "vmoe_route_workspace_bytes": [_i64, _i32],
     "vmoe_route": [_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                   _i32, _i64, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp],
+                   _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp],
     "vmoe_row_maps": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _i64, _vp, _vp, _vp, _vp],
     "vmoe_gather": [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp],
     "vmoe_gather_tokens": [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _vp, _i64, _i64, _vp, _i64,
                            _vp],
     "vmoe_combine": [_vp, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp],
     "vmoe_gemm_up_fwd": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp,
-                         _vp, _i32, _i64, _i64, _i64, _vp],
+                         _vp, _vp, _i32, _i64, _i64, _i64, _vp],
     "vmoe_gemm_down_fwd": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
                            _i64, _i64, _vp],
     "vmoe_relu2_grad": [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp],
@@ -43,10 +43,10 @@ _SIGNATURES = {
     "vmoe_gemm_dw_workspace_bytes": [_i32, _i64, _i64, _i64],
     "vmoe_gemm_up_bwd_dw": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp,
                             _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
-    "vmoe_gemm_down_bwd_dh": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i32,
-                              _i64, _i64, _i64, _vp],
-    "vmoe_gemm_down_bwd_dw": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
-                              _i64, _i64, _vp, ctypes.c_size_t, _vp],
+    "vmoe_gemm_down_bwd_dh": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp,
+                              _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "vmoe_gemm_down_bwd_dw": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
+                              _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
     "vmoe_zero_tail_cols": [_vp, _i64, _vp, _vp, _i32, _i64, _i64, _vp],
     "vmoe_router_partial_floats": [_i64, _i32],
     "vmoe_router_topk": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,

@@ -28,7 +28,7 @@ class Route:
     bins: torch.Tensor             # [E] int32
     padded_bins: torch.Tensor      # [E] int32
     row_src: torch.Tensor          # [rows_bound] int32, -1 = pad row
-    gather_map: torch.Tensor       # [rows_bound] int32, 0 = pad row
+    gather_map: torch.Tensor       # [rows_bound] int32, map_pad (0 or -1) = pad row
     assignment_row: torch.Tensor   # [A] int32, -1 = dropped
     info: torch.Tensor             # [4] int32: rows P, kept, error bits
     expert_offsets: torch.Tensor   # [E+1] int32: [0, padded_bins]
@@ -37,6 +37,7 @@ class Route:
     num_assignments: int
     num_experts: int
     top_k: int
+    row_weight: torch.Tensor | None = None  # [rows_bound] fp32 routing weight, 0 = pad row
 
 
 def rows_upper_bound(num_assignments: int, num_experts: int, block_size: int,
@@ -50,12 +51,14 @@ def rows_upper_bound(num_assignments: int, num_experts: int, block_size: int,
 
 
 def route_device(selected: torch.Tensor, num_experts: int, top_k: int, block_size: int,
-                 rounding: str = "up", map_pad: int = 0) -> Route:
+                 rounding: str = "up", map_pad: int = 0,
+                 weights: torch.Tensor | None = None) -> Route:
     """Runs the routing chain on the current stream; never syncs.
 
     map_pad is the gather_map entry of pad rows: 0 as in the reference's
     precompute_gather_map, -1 for the module's fused row gather (the GEMMs
-    read zeros for it)."""
+    read zeros for it). With weights (bf16, one per assignment) the route
+    also holds row_weight[row] = weights[row_src[row]] (0 on pad rows)."""
     _lib.require_gpu(selected)
     if rounding not in _lib.ROUNDING:
         raise AssertionError(f"Invalid rounding mode: {rounding}")
@@ -74,22 +77,30 @@ def route_device(selected: torch.Tensor, num_experts: int, top_k: int, block_siz
     ws_bytes = int(_lib.lib().vmoe_route_workspace_bytes(A, E))
     # One allocation carved into 16-byte aligned int32 views (one allocator
     # call per routing instead of twelve).
+    if weights is not None:
+        if weights.dtype != torch.bfloat16 or weights.numel() != A:
+            raise ValueError("weights must be bf16 with one entry per assignment")
+        weights = weights.reshape(-1).contiguous()
+    nrw = max(cap, 1) if weights is not None else 0
     sizes = [max(A, 1), max(A, 1), E, E, E, max(cap, 1), max(cap, 1), max(A, 1), _lib.INFO_LEN,
-             E + 1, E, (ws_bytes + 3) // 4]
+             E + 1, E, nrw, (ws_bytes + 3) // 4]
     offs, n = [], 0
     for sz in sizes:
         offs.append(n)
         n += (sz + 3) // 4 * 4
     buf = torch.empty(n, dtype=torch.int32, device=dev)
-    (bin_ids, indices, tpe, bins, padded, row_src, gmap, arow, info, eto, ptpe,
+    (bin_ids, indices, tpe, bins, padded, row_src, gmap, arow, info, eto, ptpe, rw,
      ws) = (buf[o:o + sz] for o, sz in zip(offs, sizes))
+    rw = rw.view(torch.float32) if weights is not None else None
     _lib.call("vmoe_route", sel.data_ptr(), int(sel.dtype == torch.int64), A, E, int(top_k),
               int(block_size), _lib.ROUNDING[rounding], bin_ids.data_ptr(), indices.data_ptr(),
               tpe.data_ptr(), bins.data_ptr(), padded.data_ptr(), row_src.data_ptr(),
               gmap.data_ptr(), int(map_pad), cap, arow.data_ptr(), info.data_ptr(), eto.data_ptr(),
-              ptpe.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream(dev))
+              ptpe.data_ptr(), _lib.ptr(weights), _lib.ptr(rw), ws.data_ptr(), ws_bytes,
+              _lib.stream(dev))
     return Route(bin_ids[:A], indices[:A], tpe, bins, padded, row_src[:cap], gmap[:cap],
-                 arow[:A], info, eto, ptpe, cap, A, E, int(top_k))
+                 arow[:A], info, eto, ptpe, cap, A, E, int(top_k),
+                 None if rw is None else rw[:cap])
 
 
 def check_route(r: Route) -> tuple[int, int]:

@@ -169,28 +169,3 @@ class PaddedGatherOp(torch.autograd.Function):
 def padded_gather_autograd(x, indices, bin_ids, bins, padded_bins, top_k):
     """Padded gather with autograd support."""
     return PaddedGatherOp.apply(x, indices, bin_ids, bins, padded_bins, top_k)
-
-
-class RoutedGatherOp(torch.autograd.Function):
-    """Gather through precomputed route maps (no host sync).
-
-    forward: out[r] = x[row_src[r] // top_k] for r < rows (rows counted on the
-    device by num_rows_dev); backward: grad_x[t] = sum_j grad[row(t, j)].
-    """
-
-    @staticmethod
-    @custom_fwd(device_type="cuda")
-    def forward(ctx, x, row_src, assignment_row, top_k, rows, num_rows_dev):
-        ctx.save_for_backward(assignment_row)
-        ctx.top_k = top_k
-        ctx.num_tokens = x.shape[0]
-        return gather_rows(x, row_src, top_k, rows, num_rows_dev=num_rows_dev,
-                           assignment_row=assignment_row)
-
-    @staticmethod
-    @custom_bwd(device_type="cuda")
-    @once_differentiable
-    def backward(ctx, grad_output):
-        (ar,) = ctx.saved_tensors
-        grad_x = combine_rows(grad_output, ar, ctx.top_k, ctx.num_tokens)
-        return grad_x, None, None, None, None, None

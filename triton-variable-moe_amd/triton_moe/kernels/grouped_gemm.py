@@ -14,7 +14,7 @@ side in columns, W2 [total_width, hidden] stacked in rows, intermediates
 
 The public functions read the small metadata arrays back once (the
 reference does several .item() syncs) to size outputs and validate; the
-Routed*Op functions used by the module take a prebuilt GemmMeta and never
+RoutedMoEOp node used by the module takes a prebuilt GemmMeta and never
 sync: the kernels find their tiles on the device.
 """
 
@@ -114,6 +114,32 @@ def _need(cond: bool, msg: str) -> None:
         raise ValueError(msg)
 
 
+def _token_source(g: torch.Tensor):
+    """(tensor, leading dimension) of a bf16 [T, d] source read through a row
+    map; a row-broadcast source (row stride 0, such as the gradient of
+    out.sum()) is passed as its first row with leading dimension 0."""
+    g = _bf16_any(g, "token source")
+    if g.shape[0] > 0 and g.stride(0) == 0:
+        row = g[:1] if g.stride(1) == 1 and g.data_ptr() % 16 == 0 else g[:1].contiguous()
+        return row, 0
+    g = _bf16(g, "token source")
+    return g, g.stride(0)
+
+
+def _bf16_any(t: torch.Tensor, what: str) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise NotImplementedError(f"{what}: only bfloat16 is supported (got {t.dtype})")
+    return t
+
+
+def _f32_rows(t: torch.Tensor | None, rows: int, what: str) -> torch.Tensor | None:
+    if t is None:
+        return None
+    _need(t.dtype == torch.float32 and t.is_contiguous() and t.numel() >= rows,
+          f"{what} must be contiguous fp32 with one entry per row")
+    return t
+
+
 def _alloc(rows, cols, like, zero):
     f = torch.zeros if zero else torch.empty
     return f(rows, cols, dtype=like.dtype, device=like.device)
@@ -144,8 +170,9 @@ def _zero_tails(buf: torch.Tensor, m: GemmMeta):
 
 
 def up_fwd(x, w1, m: GemmMeta, act: int, save_pre: bool, zero_tails: bool,
-           gather_map: torch.Tensor | None = None):
-    """out = act(x_e @ W1_e) and pre_act = relu(z) (or zeros for act none)."""
+           gather_map: torch.Tensor | None = None, row_scale: torch.Tensor | None = None):
+    """out = act(x_e @ W1_e) and pre_act = relu(z) (or zeros for act none).
+    With row_scale (fp32 per row) out[row] = bf16(row_scale[row] * act(z))."""
     x = _bf16(x, "grouped_gemm_up x")
     w1 = _bf16(w1, "grouped_gemm_up w1")
     hidden = x.shape[1]
@@ -163,8 +190,8 @@ def up_fwd(x, w1, m: GemmMeta, act: int, save_pre: bool, zero_tails: bool,
         _lib.call("vmoe_gemm_up_fwd", x.data_ptr(), x.stride(0), x.shape[0], _lib.ptr(gm),
                   w1.data_ptr(), w1.stride(0),
                   out.data_ptr(), _lib.ptr(pre) if act == _lib.ACT_RELU_SQUARED else None,
-                  out.stride(0), act, *_meta_args(m), hidden, m.max_width, m.rows,
-                  _lib.stream(x.device))
+                  out.stride(0), act, _lib.ptr(_f32_rows(row_scale, m.rows, "row_scale")),
+                  *_meta_args(m), hidden, m.max_width, m.rows, _lib.stream(x.device))
         if zero_tails:
             _zero_tails(out, m)
             if pre is not None and act == _lib.ACT_RELU_SQUARED:
@@ -245,15 +272,26 @@ def up_bwd(grad_h, x, w1, pre, m: GemmMeta, hidden: int, act: int,
 
 
 def down_bwd(grad_y, h, w2, m: GemmMeta, hidden: int, zero_tails: bool,
-             pre: torch.Tensor | None = None):
+             pre: torch.Tensor | None = None, gather_map: torch.Tensor | None = None,
+             row_scale: torch.Tensor | None = None):
     """(grad_intermediate [rows, max_width], grad_w2). With pre, the first
-    output is the relu^2 gradient GA instead (fused in the dH epilogue)."""
-    grad_y = _bf16(grad_y, "grouped_gemm_down_backward grad_output")
+    output is the relu^2 gradient GA instead (fused in the dH epilogue).
+    With gather_map, grad_y holds one row per token and row r of the
+    gradient is grad_y[gather_map[r]] (-1: zeros); with row_scale (fp32 per
+    row) the gradient w.r.t. H is scaled by it before the relu^2 rule."""
+    gy_rows = grad_y.shape[0]
+    if gather_map is None:
+        grad_y = _bf16(grad_y, "grouped_gemm_down_backward grad_output")
+        ldgy = grad_y.stride(0)
+        _need(gy_rows >= m.rows, "grad_output has fewer rows than the padded row count")
+    else:
+        grad_y, ldgy = _token_source(grad_y)
+        _need(gather_map.numel() >= m.rows, "gather_map shorter than the padded row count")
+    gm = None if gather_map is None else _i32(gather_map)
     h = _bf16(h, "grouped_gemm_down_backward intermediate")
     w2 = _bf16(w2, "grouped_gemm_down_backward w2")
     _need(w2.shape[1] == hidden and grad_y.shape[1] == hidden,
           "grad_output / w2 do not match hidden_size")
-    _need(grad_y.shape[0] >= m.rows, "grad_output has fewer rows than the padded row count")
     _need(h.shape[0] >= m.rows and h.shape[1] >= m.max_width,
           "intermediate smaller than [rows, max_expert_width]")
     grad_h = _alloc(m.rows, m.max_width, grad_y, not m.full_rows)
@@ -264,15 +302,17 @@ def down_bwd(grad_y, h, w2, m: GemmMeta, hidden: int, zero_tails: bool,
     grad_w2 = torch.zeros_like(w2) if not m.full_cols else torch.empty_like(w2)
     dev = grad_y.device
     if m.rows > 0:
-        _lib.call("vmoe_gemm_down_bwd_dh", grad_y.data_ptr(), grad_y.stride(0), w2.data_ptr(),
-                  w2.stride(0), _lib.ptr(pre), grad_h.data_ptr(), grad_h.stride(0),
-                  *_meta_args(m), hidden, m.max_width, m.rows, _lib.stream(dev))
+        _lib.call("vmoe_gemm_down_bwd_dh", grad_y.data_ptr(), ldgy, gy_rows, _lib.ptr(gm),
+                  w2.data_ptr(), w2.stride(0), _lib.ptr(pre),
+                  _lib.ptr(_f32_rows(row_scale, m.rows, "row_scale")), grad_h.data_ptr(),
+                  grad_h.stride(0), *_meta_args(m), hidden, m.max_width, m.rows,
+                  _lib.stream(dev))
         if zero_tails:
             _zero_tails(grad_h, m)
     ws = _dw_workspace(m, hidden, dev)
-    _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), grad_y.data_ptr(),
-              grad_y.stride(0), grad_w2.data_ptr(), grad_w2.stride(0), *_meta_args(m), hidden,
-              m.max_width, m.rows, ws.data_ptr(), ws.numel(), _lib.stream(dev))
+    _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), grad_y.data_ptr(), ldgy,
+              gy_rows, _lib.ptr(gm), grad_w2.data_ptr(), grad_w2.stride(0), *_meta_args(m),
+              hidden, m.max_width, m.rows, ws.data_ptr(), ws.numel(), _lib.stream(dev))
     return grad_h, grad_w2
 
 
@@ -440,42 +480,53 @@ def grouped_gemm_down_autograd(intermediate, w2, expert_token_offsets, expert_we
 # ---------------------------------------------------------------------------
 
 
-class RoutedExpertsOp(torch.autograd.Function):
-    """Token gather, both grouped GEMMs of the module (up with relu^2, then
-    down) and the gather's backward as one autograd node, with metadata from
-    the route and no host sync.
+class RoutedMoEOp(torch.autograd.Function):
+    """The module's expert path after routing, as one autograd node: token
+    gather, grouped GEMM up with relu^2, grouped GEMM down, weighted combine,
+    and their backward (reference: padded_gather, grouped_gemm_up/down and
+    padded_scatter as called by TritonMoEMLP.forward, moe.py:203-240).
 
-    The up GEMM and its dW read the token activations x_flat through the row
-    map (row -> token, -1 for pad rows, which read zeros), so the gathered
-    copy of x (rows x hidden) is never written: the reference's padded_gather
-    (gather.py:63-115) is fused into the GEMMs' operand staging. The backward
-    fuses the relu^2 gradient into the dH GEMM's epilogue (the gradient with
-    respect to H is never materialised) and returns the gradient with respect
-    to x_flat: dX in expert-row order, summed over each token's k rows by the
-    unweighted combine (PaddedGatherOp's backward, gather.py:253-265).
+    The gather is fused into the GEMMs' operand staging: the up GEMM and its
+    dW read x_flat through the row map (row -> token, -1 on pad rows, which
+    read zeros), so the gathered copy of x is never written.
+
+    The routing weight of each row is applied to H instead of to the down
+    projection's output: the up GEMM writes H' = bf16(w_row * relu(z)^2), so
+    Y' = H' @ W2 = w * Y and the combine is the plain sum over a token's k
+    rows. The backward then needs no weighted copy of the output gradient
+    G (the reference's GY = bf16(G * w), scatter.py:141-189): the dH GEMM
+    reads G through the row map and scales row r by w_r before the relu^2
+    rule (w_r (G @ W2^T) = GY @ W2^T), and the dW2 GEMM reads G through the
+    map against H' (H'^T G = H^T GY). The products are the reference's; only
+    where they round to bf16 moves. The routing weights get no gradient, as
+    in the reference (scatter.py:176).
     """
 
     @staticmethod
     @custom_fwd(device_type="cuda")
-    def forward(ctx, x_flat, w1, w2, meta, gather_map, assignment_row, top_k, hidden_size):
+    def forward(ctx, x_flat, w1, w2, meta, gather_map, row_weight, assignment_row, top_k,
+                hidden_size):
+        from .gather import combine_rows
+
         h, pre = up_fwd(x_flat, w1, meta, _lib.ACT_RELU_SQUARED, True, zero_tails=False,
-                        gather_map=gather_map)
+                        gather_map=gather_map, row_scale=row_weight)
         y = down_fwd(h, w2, meta, hidden_size)
-        ctx.save_for_backward(x_flat, w1, w2, h, pre, gather_map, assignment_row)
+        out = combine_rows(y, assignment_row, top_k, x_flat.shape[0])
+        ctx.save_for_backward(x_flat, w1, w2, h, pre, gather_map, row_weight, assignment_row)
         ctx.meta = meta
         ctx.hidden_size = hidden_size
         ctx.top_k = top_k
-        return y
+        return out
 
     @staticmethod
     @custom_bwd(device_type="cuda")
     @once_differentiable
-    def backward(ctx, grad_y):
+    def backward(ctx, grad_out):
         from .gather import combine_rows
 
-        x_flat, w1, w2, h, pre, gm, ar = ctx.saved_tensors
-        ga, grad_w2 = down_bwd(grad_y, h, w2, ctx.meta, ctx.hidden_size, zero_tails=False,
-                               pre=pre)
+        x_flat, w1, w2, h, pre, gm, rw, ar = ctx.saved_tensors
+        ga, grad_w2 = down_bwd(grad_out, h, w2, ctx.meta, ctx.hidden_size, zero_tails=False,
+                               pre=pre, gather_map=gm, row_scale=rw)
         grad_xg, grad_w1 = up_bwd_from_ga(ga, x_flat, w1, ctx.meta, ctx.hidden_size, gm)
         grad_x = combine_rows(grad_xg, ar, ctx.top_k, x_flat.shape[0])
-        return grad_x, grad_w1, grad_w2, None, None, None, None, None
+        return grad_x, grad_w1, grad_w2, None, None, None, None, None, None

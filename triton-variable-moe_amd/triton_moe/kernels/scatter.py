@@ -74,29 +74,3 @@ class PaddedScatterOp(torch.autograd.Function):
 def padded_scatter_autograd(x, indices, bin_ids, weights, bins, padded_bins, top_k):
     """Padded scatter with autograd support."""
     return PaddedScatterOp.apply(x, indices, bin_ids, weights, bins, padded_bins, top_k)
-
-
-class RoutedScatterOp(torch.autograd.Function):
-    """Weighted combine through precomputed route maps (no host sync).
-
-    forward: out[t] = sum_j bf16(y[row(t, j)] * w[t*k + j]);
-    backward: grad_y[r] = bf16(grad[t(r)] * w[row_src[r]]), zeros on pad rows,
-    for r < rows (counted on the device by num_rows_dev).
-    """
-
-    @staticmethod
-    @custom_fwd(device_type="cuda")
-    def forward(ctx, y, row_src, assignment_row, weights, top_k, num_tokens, num_rows_dev):
-        ctx.save_for_backward(row_src, assignment_row, weights, num_rows_dev)
-        ctx.top_k = top_k
-        ctx.rows = y.shape[0]
-        return combine_rows(y, assignment_row, top_k, num_tokens, weights=weights)
-
-    @staticmethod
-    @custom_bwd(device_type="cuda")
-    @once_differentiable
-    def backward(ctx, grad_output):
-        rs, ar, weights, nrd = ctx.saved_tensors
-        grad_y = gather_rows(grad_output, rs, ctx.top_k, ctx.rows, weights=weights,
-                             num_rows_dev=nrd, assignment_row=ar)
-        return grad_y, None, None, None, None, None, None

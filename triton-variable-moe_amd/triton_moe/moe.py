@@ -34,9 +34,8 @@ from .kernels import (
     padded_scatter,
 )
 from .kernels.fused_cumsum import route_device
-from .kernels.grouped_gemm import GemmMeta, RoutedExpertsOp
+from .kernels.grouped_gemm import GemmMeta, RoutedMoEOp
 from .kernels.router import RouterAuxOp, load_balance_coef, router_topk
-from .kernels.scatter import RoutedScatterOp
 
 
 @dataclass
@@ -165,20 +164,17 @@ class TritonMoEMLP(nn.Module):
     def _experts(self, x_flat, top_k_weights_flat, selected_experts_flat):
         """Routing + expert MLP + combine on the HIP kernels, no host sync."""
         k = self.num_active_experts
-        # Pad rows of the row map are -1: the GEMMs' fused gather reads zeros.
+        # Pad rows of the row map are -1 (the GEMMs' fused gather reads zeros
+        # for them); row_weight holds each row's routing weight.
         r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
-                         map_pad=-1)
+                         map_pad=-1, weights=top_k_weights_flat)
         # expert_token_offsets = [0, padded_bins] and the padded counts come
         # out of the routing kernel (moe.py:193-202 of the reference).
         meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
                         self.expert_widths_t, r.padded_counts, self.num_experts,
                         self.max_expert_width, r.rows_bound)
-        num_rows_dev = r.info[0:1]
-        x_down = RoutedExpertsOp.apply(x_flat, self.w1, self.w2, meta, r.gather_map,
-                                       r.assignment_row, k, self.config.n_embd)
-        output_flat = RoutedScatterOp.apply(x_down, r.row_src, r.assignment_row,
-                                            top_k_weights_flat, k, x_flat.shape[0],
-                                            num_rows_dev)
+        output_flat = RoutedMoEOp.apply(x_flat, self.w1, self.w2, meta, r.gather_map,
+                                        r.row_weight, r.assignment_row, k, self.config.n_embd)
         return output_flat, r.tokens_per_expert
 
     @torch.compiler.disable
@@ -283,24 +279,23 @@ class TritonMoEMLP(nn.Module):
         k = self.num_active_experts
         with profiler.step("fused_route"):
             r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
-                             map_pad=-1)
+                             map_pad=-1, weights=top_k_weights_flat)
             meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
                             self.expert_widths_t, r.padded_counts, self.num_experts,
                             self.max_expert_width, r.rows_bound)
-            nrd = r.info[0:1]
         with profiler.step("gather"):
             pass  # fused into the up GEMM's operand staging (row map)
         with profiler.step("gemm_up"):
-            # gather, up and down run as one autograd node; both forward GEMMs
-            # are timed under "gemm_up", and "gather" and "gemm_down" stay as
-            # (empty) steps so the reference's step names are all present.
-            x_down = RoutedExpertsOp.apply(x_flat, self.w1, self.w2, meta, r.gather_map,
-                                           r.assignment_row, k, self.config.n_embd)
+            # gather, both GEMMs and the combine run as one autograd node and
+            # are timed under "gemm_up"; "gather", "gemm_down" and "scatter"
+            # stay as (empty) steps so the reference's step names are present.
+            output_flat = RoutedMoEOp.apply(x_flat, self.w1, self.w2, meta, r.gather_map,
+                                            r.row_weight, r.assignment_row, k,
+                                            self.config.n_embd)
         with profiler.step("gemm_down"):
             pass
         with profiler.step("scatter"):
-            output_flat = RoutedScatterOp.apply(x_down, r.row_src, r.assignment_row,
-                                                top_k_weights_flat, k, x_flat.shape[0], nrd)
+            pass
         with profiler.step("reshape"):
             output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
         with profiler.step("aux_loss"):
