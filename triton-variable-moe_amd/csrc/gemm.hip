@@ -304,15 +304,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
                                            0x00020000);
 }
 
-// 16-byte DMA of the lane's source into LDS at dst + 16 * lane
-// (buffer_load_dwordx4 ... lds, LDS base in M0). Issued as inline asm so the
+// 16-byte DMA of the lane's source into LDS at lds + 16 * lane
+// (buffer_load_dwordx4 ... lds; lds is a uniform LDS byte address, written to
+// M0). Issued as inline asm so the
 // compiler does not track it: it would otherwise wait for every DMA before
 // any LDS read it cannot prove disjoint, which empties the ring. The kernels
 // order DMA completion themselves with wait_vmcnt + block_barrier. The asm
 // has no register outputs (the data goes to LDS), so no register is written
 // behind the compiler's back; M0 is declared clobbered.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, lds_char* dst) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(dst));
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :: "v"(voff), "s"(r), "s"(lds) : "memory", "m0");
 }
@@ -409,6 +409,17 @@ struct Gemm {
   static constexpr int PT = PWA + PWB;  // DMA instructions per stage per producer thread
   __device__ static int pwave() { return (threadIdx.x >> 6) - kConsumers; }
 
+  // LDS address of this wave's first DMA slot of an operand stage, uniform:
+  // DMA i of the wave then writes at lds_slot + 1024 i (scalar adds). Every
+  // vector instruction a producer issues between a barrier and its DMAs
+  // competes with the consumers' MFMAs for the SIMD and delays the stage, so
+  // the per-DMA work is one vector op (the offset) where possible.
+  template <int PW>
+  __device__ static uint32_t lds_slot(lds_char* stage) {
+    return __builtin_amdgcn_readfirstlane(
+        (uint32_t)reinterpret_cast<uintptr_t>(stage + pwave() * PW * 1024));
+  }
+
   // LDS is 64 banks x 4 bytes; a ds_read_b128 serves 16 lanes per cycle and
   // a ds_read_b64_tr_b16 32 lanes per cycle. K-form: a row is KCH 16-byte
   // chunks and the 16 rows one phase reads share 256-byte bank lines
@@ -454,6 +465,8 @@ struct Gemm {
     int64_t mbase;               // map index of the item's first k-row
     int klen;                    // k-rows of the item
     uint32_t rows;               // rows of the gathered source
+    int pf_kt;                   // stage whose entries are in pf (-1: none)
+    int32_t pf[4];               // the lane's entries of stage pf_kt, read a stage ahead
     bool on;
   };
   static_assert(BK / kProducers == 8 && kWinStages * 8 == 64,
@@ -490,13 +503,20 @@ struct Gemm {
   }
 
   // K-form issue: stage tile k0 .. k0 + BK (k0 relative to the setup's c0).
+  // Invalid rows hold offset kOob, which stays out of range after adding k0
+  // (offsets are below 2^31), so a stage inside K needs one add per DMA.
   template <int R, int PW>
   __device__ static void issue_k(const Src<PW>& s, int k0, int K, lds_char* stage) {
-    const int wave = pwave();
+    const uint32_t m0 = lds_slot<PW>(stage);
+    if (k0 + BK <= K) {
+#pragma unroll
+      for (int i = 0; i < PW; ++i) dma16(s.rsrc, s.off[i] + (uint32_t)(k0 * 2), m0 + i * 1024);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-      const bool v = s.ok[i] && k0 + s.idx[i] < K;
-      dma16(s.rsrc, v ? s.off[i] + (uint32_t)(k0 * 2) : kOob, stage + (wave * PW + i) * 1024);
+      const bool v = s.ok[i] & (k0 + s.idx[i] < K);
+      dma16(s.rsrc, v ? s.off[i] + (uint32_t)(k0 * 2) : kOob, m0 + i * 1024);
     }
   }
 
@@ -517,6 +537,7 @@ struct Gemm {
       tm.mbase = r0;
       tm.klen = k_valid;
       tm.rows = (uint32_t)map_rows;
+      tm.pf_kt = -1;
     }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
@@ -524,7 +545,10 @@ struct Gemm {
       const int c = (lane % LPR) ^ tswz(krow);
       s.idx[i] = krow;
       s.ok[i] = c * 8 < cols_valid;
-      s.off[i] = (uint32_t)(c * 16 + (map ? 0 : (int64_t)krow * ld * 2));
+      // Without a map an invalid column holds kOob (see issue_k); with one,
+      // the column offset, to which the gathered row's offset is added.
+      s.off[i] = map ? (uint32_t)(c * 16)
+                     : (s.ok[i] ? (uint32_t)(c * 16 + (int64_t)krow * ld * 2) : kOob);
     }
   }
 
@@ -536,31 +560,69 @@ struct Gemm {
     dma4(tm.mrs, k < tm.klen ? (uint32_t)((tm.mbase + k) * 4) : kOob, win);
   }
 
+  // The lane's map entries (one per DMA instruction) of stage kt from the
+  // current window.
+  template <int R, int PW>
+  __device__ static void window_rows(const TMap& tm, int kt, int32_t (&rows)[PW]) {
+    constexpr int LPR = Dma<R>::LPR, RPI = Dma<R>::RPI;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < PW; ++i)
+      rows[i] = reinterpret_cast<const __attribute__((address_space(3))) int32_t*>(
+          tm.win)[(kt % kWinStages) * 8 + i * RPI + lane / LPR];
+  }
+
   template <int R, int PW, bool MAP>
   __device__ static void issue_t(const Src<PW>& s, TMap& tm, int kt, int K, lds_char* stage) {
-    constexpr int LPR = Dma<R>::LPR, RPI = Dma<R>::RPI;
-    const int wave = pwave(), lane = threadIdx.x & 63;
+    const uint32_t m0 = lds_slot<PW>(stage);
     const int k0 = kt * BK;
     if constexpr (MAP) {
-      if (tm.on && kt > 0 && kt % kWinStages == 0) {
-        // Items longer than the window (no split-K): refill it in place.
-        load_window(tm, k0, tm.win);
-        wait_vmcnt<0>();
+      static_assert(PW <= 4, "prefetched map entries per lane");
+      if (tm.on) {
+        if (kt > 0 && kt % kWinStages == 0) {
+          // Items longer than the window (no split-K): refill it in place.
+          load_window(tm, k0, tm.win);
+          wait_vmcnt<0>();
+          tm.pf_kt = -1;
+        }
+        // Entries of this stage, read from LDS during the previous stage's
+        // issue when it was in the same window (the read's latency then
+        // overlaps the wait for the ring), else now.
+        int32_t rows[PW];
+        if (tm.pf_kt == kt) {
+#pragma unroll
+          for (int i = 0; i < PW; ++i) rows[i] = tm.pf[i];
+        } else {
+          window_rows<R, PW>(tm, kt, rows);
+        }
+        const bool kin = k0 + BK <= K;  // uniform: every k-row of the stage is in K
+#pragma unroll
+        for (int i = 0; i < PW; ++i) {
+          const bool v = s.ok[i] & (kin | (k0 + s.idx[i] < K)) & ((uint32_t)rows[i] < tm.rows);
+          dma16(s.rsrc, v ? s.off[i] + (uint32_t)rows[i] * s.ld2 : kOob, m0 + i * 1024);
+        }
+        const int kn = kt + 1;
+        tm.pf_kt = -1;
+        if (kn * BK < K && kn % kWinStages != 0) {
+          int32_t nx[PW];
+          window_rows<R, PW>(tm, kn, nx);
+#pragma unroll
+          for (int i = 0; i < PW; ++i) tm.pf[i] = nx[i];
+          tm.pf_kt = kn;
+        }
+        return;
       }
+    }
+    if (k0 + BK <= K) {
+#pragma unroll
+      for (int i = 0; i < PW; ++i)
+        dma16(s.rsrc, s.off[i] + (uint32_t)k0 * s.ld2, m0 + i * 1024);
+      return;
     }
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-      const bool v = s.ok[i] && k0 + s.idx[i] < K;
-      uint32_t off = v ? s.off[i] + (uint32_t)k0 * s.ld2 : kOob;
-      if constexpr (MAP) {
-        if (tm.on) {
-          const int e = (kt % kWinStages) * 8 + i * RPI + lane / LPR;
-          const int32_t row = reinterpret_cast<const __attribute__((address_space(3))) int32_t*>(
-              tm.win)[e];
-          off = v && (uint32_t)row < tm.rows ? s.off[i] + (uint32_t)row * s.ld2 : kOob;
-        }
-      }
-      dma16(s.rsrc, off, stage + (wave * PW + i) * 1024);
+      const bool v = s.ok[i] & (k0 + s.idx[i] < K);
+      dma16(s.rsrc, v ? s.off[i] + (uint32_t)k0 * s.ld2 : kOob, m0 + i * 1024);
     }
   }
 
