@@ -106,6 +106,27 @@ struct ExpertRec {
   int t0, t1, tpe, ew0, ew1, w;
 };
 
+// The same through the scalar cache, for a uniform e: a load from the
+// constant address space at a uniform index compiles to s_load, which
+// completes on lgkmcnt. Vector loads in a producer wave would make the
+// compiler wait for them with vmcnt(0), which also drains the DMAs in flight
+// (the compiler does not count them).
+__device__ __forceinline__ int32_t sload(const int32_t* ptr, int idx) {
+  typedef __attribute__((address_space(4))) const int32_t cint;
+  return ((cint*)ptr)[__builtin_amdgcn_readfirstlane(idx)];
+}
+
+__device__ __forceinline__ ExpertRec rec_scalar(const Args& p, int e) {
+  ExpertRec r;
+  r.t0 = sload(p.eto, e);
+  r.t1 = (int)min<int64_t>(sload(p.eto, e + 1), p.rows_bound);
+  r.tpe = sload(p.tpe, e);
+  r.ew0 = sload(p.ewo, e);
+  r.ew1 = sload(p.ewo, e + 1);
+  r.w = sload(p.widths, e);
+  return r;
+}
+
 __device__ __forceinline__ ExpertRec rec_global(const Args& p, int e) {
   ExpertRec r;
   r.t0 = p.eto[e];
@@ -455,10 +476,12 @@ struct Gemm {
   // the entries instead waits on the scalar cache once per stage.
   static constexpr int kWinStages = 8;
   // Row factors of the output (UP_FWD, DOWN_DH): one slot of BM floats per
-  // item, as many slots as the producers can run items ahead (each item has
-  // at least one stage and they run at most kStages - 1 stages ahead).
+  // item. The producers set an item up right after issuing the previous
+  // item's last stage, kStages - 1 stages ahead of the consumers, and every
+  // item has at least one stage, so the slot of item n - kStages - 1 is the
+  // newest one a consumer can still be reading.
   static constexpr bool kScaled = V == UP_FWD || V == DOWN_DH;
-  static constexpr int kScaleSlots = kStages;
+  static constexpr int kScaleSlots = kStages + 1;
   struct TMap {
     __amdgpu_buffer_rsrc_t mrs;  // over the row map
     lds_char* win;               // this wave's window of the current item
@@ -477,7 +500,7 @@ struct Gemm {
   template <int R, int PW>
   __device__ static void setup_k(Src<PW>& s, const uint16_t* base, int64_t ld,
                                  const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
-                                 int rows_valid) {
+                                 int rows_valid, const lds_char* win) {
     const int lane = threadIdx.x & 63, wave = pwave();
     // Without a map, rebase to the tile's first row so offsets stay small.
     if (!T::k_map) map = nullptr;
@@ -492,8 +515,9 @@ struct Gemm {
       int64_t srow = row;
       if (T::k_map && map && ok) {
         // One entry per lane, once per item (the K-form rows are fixed for
-        // all of the item's k-tiles).
-        srow = map[r0 + row];
+        // all of the item's k-tiles), from the wave's map window.
+        srow = reinterpret_cast<const __attribute__((address_space(3))) int32_t*>(
+            win)[i * KRPI + lane / KCH];
         ok = srow >= 0 && srow < map_rows;
       }
       s.ok[i] = ok;
@@ -554,10 +578,19 @@ struct Gemm {
 
   // DMA of this wave's map entries for stages [kw / BK, kw / BK + kWinStages)
   // of the item into window `win`; entries past the item's rows read 0.
+  // K-form gather (A of UP_FWD and DOWN_DH): the window holds the entries of
+  // the wave's PWA * KRPI tile rows instead (tm.klen = valid rows).
   __device__ static void load_window(const TMap& tm, int kw, lds_char* win) {
     const int lane = threadIdx.x & 63, wave = pwave();
-    const int k = kw + (lane >> 3) * BK + wave * 8 + (lane & 7);
-    dma4(tm.mrs, k < tm.klen ? (uint32_t)((tm.mbase + k) * 4) : kOob, win);
+    if constexpr (T::k_map) {
+      static_assert(PWA * KRPI <= 64, "one 4-byte DMA covers the wave's tile rows");
+      const int row = wave * PWA * KRPI + lane;
+      const bool v = lane < PWA * KRPI && row < tm.klen;
+      dma4(tm.mrs, v ? (uint32_t)((tm.mbase + row) * 4) : kOob, win);
+    } else {
+      const int k = kw + (lane >> 3) * BK + wave * 8 + (lane & 7);
+      dma4(tm.mrs, k < tm.klen ? (uint32_t)((tm.mbase + k) * 4) : kOob, win);
+    }
   }
 
   // The lane's map entries (one per DMA instruction) of stage kt from the
@@ -713,7 +746,7 @@ struct Gemm {
       r.ew1 = __builtin_amdgcn_readfirstlane(mt.rec[4][e]);
       r.w = __builtin_amdgcn_readfirstlane(mt.rec[5][e]);
     } else {
-      r = rec_global(p, e);
+      r = rec_scalar(p, e);
     }
     Work w;
     w.q = T::prob(p, r);
@@ -742,8 +775,13 @@ struct Gemm {
   // Map fields of work w for the gathered T-form operand (A of UP_DW, B of
   // DOWN_DW).
   __device__ static void setup_map(const Args& p, const Work& w, TMap& tm) {
-    tm.mbase = (T::t_map_b ? w.q.br : w.q.ar) + w.kbeg;
-    tm.klen = w.klen;
+    if constexpr (T::k_map) {
+      tm.mbase = w.q.ar + w.m0;  // map index of the tile's first row
+      tm.klen = w.q.M - w.m0;    // rows of the tile that exist
+    } else {
+      tm.mbase = (T::t_map_b ? w.q.br : w.q.ar) + w.kbeg;
+      tm.klen = w.klen;
+    }
     tm.rows = (uint32_t)(T::t_map_b ? p.b_rows : p.a_rows);
     tm.on = true;
   }
@@ -752,12 +790,13 @@ struct Gemm {
                                TMap& tm) {
     const Prob& q = w.q;
     if (T::a_k)
-      setup_k<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.m0, q.ac + w.kbeg, q.M - w.m0);
+      setup_k<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.m0, q.ac + w.kbeg, q.M - w.m0,
+                  tm.win);
     else
       setup_t<BM, PWA, T::t_map>(sa, tm, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.kbeg,
                                  q.ac + w.m0, q.M - w.m0, w.klen, !T::t_map_b);
     if (T::b_k)
-      setup_k<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg, q.N - w.n0);
+      setup_k<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg, q.N - w.n0, nullptr);
     else
       setup_t<BN, PWB, T::t_map_b>(sb, tm, p.b, p.ldb, p.b_map, p.b_rows, q.br + w.kbeg,
                                    q.bc + w.n0, q.N - w.n0, w.klen, T::t_map_b);
@@ -1003,27 +1042,45 @@ struct Gemm {
   // waits for its window explicitly.
   __device__ static void run_producer(const Args& p, lds_char* ring, lds_char* wins,
                                       lds_char* scl, const Meta& mt, const Range& rg) {
-    int ec = 0, ei = 0, ela = 0;
-    Work wi = decode(p, mt, rg.beg, ei, rg.slot);
+    int ei = 0, ela = 0;
+    Work wi;
     Src<PWA> sa;
     Src<PWB> sb;
     TMap tm;
-    const bool mapped = (T::t_map && p.a_map) || (T::t_map_b && p.b_map);
+    const bool mapped = ((T::t_map || T::k_map) && p.a_map) || (T::t_map_b && p.b_map);
     if (mapped) tm.mrs = make_rsrc(T::t_map_b ? p.b_map : p.a_map);
     const bool scaled = kScaled && p.row_scale;
     __amdgpu_buffer_rsrc_t srs;
     if (scaled) srs = make_rsrc(p.row_scale);
-    int nbegun = 0;         // items begun (their row factors go to slot nbegun % 4)
+    int nbegun = 0;         // items begun (row factors go to slot nbegun % kScaleSlots)
     lds_char* const win0 = wins + pwave() * 256;
     lds_char* const win1 = win0 + kProducers * 256;
     int wcur = 0;           // window of the current item (0: win0, 1: win1)
     int la_item = -1;       // item whose window was requested into the other one
     int la_stage = 0;       // last stage issued before that request
+    int win_stage = -2;     // the same for the current item's window
     int done = -2;          // every DMA issued before stage done + 1's is complete
-    int ikt = 0, inext = rg.beg + rg.stride, witem = rg.beg;
-    int issued = 0;
-    bool fresh = true;      // wi not set up yet
+    int issued = 0;         // stages issued
+    int ikt = 0, inext = rg.beg, witem = rg.beg;
     auto begin_item = [&]() {
+      if (mapped) {
+        if (la_item == witem) {
+          wcur ^= 1;
+          tm.win = wcur ? win1 : win0;
+          win_stage = la_stage;
+        } else {
+          tm.win = wcur ? win1 : win0;
+          setup_map(p, wi, tm);
+          load_window(tm, 0, tm.win);
+          wait_vmcnt<0>();
+          win_stage = -2;
+        }
+        // The K-form gather reads its entries when the item is set up.
+        if (T::k_map && win_stage > done) {
+          wait_vmcnt<0>();
+          win_stage = -2;
+        }
+      }
       setup(p, wi, sa, sb, tm);
       if (scaled && pwave() == 0) {
         // The tile's BM row factors into the item's slot; the consumers read
@@ -1039,15 +1096,6 @@ struct Gemm {
       }
       ++nbegun;
       if (!mapped) return;
-      if (la_item == witem) {
-        wcur ^= 1;
-        tm.win = wcur ? win1 : win0;
-        if (la_stage > done) wait_vmcnt<0>();
-      } else {
-        tm.win = wcur ? win1 : win0;
-        load_window(tm, 0, tm.win);
-        wait_vmcnt<0>();
-      }
       la_item = -1;
       for (int nx = witem + rg.stride; nx < rg.end; nx += rg.stride) {
         const Work wn = decode(p, mt, nx, ela, rg.slot);
@@ -1061,45 +1109,50 @@ struct Gemm {
         }
       }
     };
-    auto issue_next = [&](lds_char* st) -> bool {
-      while (ikt >= wi.nk) {
-        if (inext >= rg.end) return false;
+    // Moves to the next item with k-steps and sets it up (decode, operand
+    // offsets, row factors, the next map window); false at the range's end.
+    auto advance = [&]() -> bool {
+      while (inext < rg.end) {
         witem = inext;
         wi = decode(p, mt, inext, ei, rg.slot);
         inext += rg.stride;
-        ikt = 0;
-        fresh = true;
+        if (wi.nk > 0) {
+          ikt = 0;
+          begin_item();
+          return true;
+        }
       }
-      if (fresh) {
-        begin_item();
-        fresh = false;
-      }
+      return false;
+    };
+    bool have = advance();
+    // Issues the stream's next stage into `st`; after an item's last stage
+    // the next item is set up right away, so that work runs before the next
+    // wait instead of between a barrier and the DMAs it would delay.
+    auto issue_one = [&](lds_char* st) {
+      if (!have) return;
+      if (mapped && ikt == 0 && win_stage > done) wait_vmcnt<0>();  // window not yet in LDS
       issue(wi, sa, sb, tm, ikt, st);
-      ++ikt;
-      return true;
+      ++issued;
+      if (++ikt >= wi.nk) have = advance();
     };
 #pragma unroll
-    for (int s = 0; s < kStages - 1; ++s)
-      if (issue_next(ring + s * STAGE)) ++issued;
-    int s = 0;  // stage index in the workgroup's stream
-    for (int item = rg.beg; item < rg.end; item += rg.stride) {
-      const int nk = decode(p, mt, item, ec, rg.slot).nk;
-      for (int kt = 0; kt < nk; ++kt, ++s) {
-        // Stages s+1 .. issued-1 may still be in flight: wait until only
-        // their DMAs are outstanding (loads complete in order), sync (the
-        // consumers then read stage s), and refill the buffer the consumers
-        // read in the previous step, which every wave has left by now.
-        const int after = issued - 1 - s;
-        if (after >= 2)
-          wait_vmcnt<2 * PT>();
-        else if (after == 1)
-          wait_vmcnt<PT>();
-        else
-          wait_vmcnt<0>();
-        done = s;
-        block_barrier();
-        if (issue_next(ring + ((s + kStages - 1) % kStages) * STAGE)) ++issued;
-      }
+    for (int s = 0; s < kStages - 1; ++s) issue_one(ring + s * STAGE);
+    // One barrier per issued stage, as the consumers take one per stage.
+    for (int s = 0; s < issued; ++s) {
+      // Stages s+1 .. issued-1 may still be in flight: wait until only
+      // their DMAs are outstanding (loads complete in order), sync (the
+      // consumers then read stage s), and refill the buffer the consumers
+      // read in the previous step, which every wave has left by now.
+      const int after = issued - 1 - s;
+      if (after >= 2)
+        wait_vmcnt<2 * PT>();
+      else if (after == 1)
+        wait_vmcnt<PT>();
+      else
+        wait_vmcnt<0>();
+      done = s;
+      block_barrier();
+      issue_one(ring + ((s + kStages - 1) % kStages) * STAGE);
     }
   }
 
@@ -1206,7 +1259,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
   __shared__ Meta meta;
   // Row-map windows of the producers (two per wave), for the T-form gather.
   constexpr int WIN_BYTES =
-      Traits<V>::t_map || Traits<V>::t_map_b ? 2 * kProducers * 256 : 16;
+      Traits<V>::t_map || Traits<V>::t_map_b || Traits<V>::k_map ? 2 * kProducers * 256 : 16;
   __shared__ __align__(16) char wins[WIN_BYTES];
   // Per-row output factors, kScaleSlots slots of BM floats.
   constexpr int SCL_BYTES = G::kScaled ? G::kScaleSlots * G::BM * 4 : 16;
