@@ -15,7 +15,7 @@ side in columns, W2 [total_width, hidden] stacked in rows, intermediates
 The public functions read the small metadata arrays back once (the
 reference does several .item() syncs) to size outputs and validate; the
 RoutedMoEOp node used by the module takes a prebuilt GemmMeta and never
-sync: the kernels find their tiles on the device.
+syncs: the kernels find their tiles on the device.
 """
 
 from __future__ import annotations
@@ -229,33 +229,49 @@ def relu2_grad(grad_h: torch.Tensor, pre: torch.Tensor) -> torch.Tensor:
     return ga
 
 
-def up_bwd_from_ga(ga, x, w1, m: GemmMeta, hidden: int, gather_map: torch.Tensor | None):
-    """(grad_x in gathered rows, grad_w1) from GA, the gradient w.r.t. the
+def up_bwd_dx(ga, w1, m: GemmMeta, hidden: int):
+    """grad_x in gathered rows = GA_e @ W1_e^T, from GA, the gradient w.r.t. the
     up projection's pre-activation."""
+    ga = _bf16(ga, "grouped_gemm_up_backward grad_output")
+    w1 = _bf16(w1, "grouped_gemm_up_backward w1")
+    _need(w1.shape[0] == hidden, "w1 does not match hidden_size")
+    _need(ga.shape[0] >= m.rows and ga.shape[1] >= m.max_width,
+          "grad_output smaller than [rows, max_expert_width]")
+    grad_x = _alloc(m.rows, hidden, ga, not m.full_rows)
+    if m.rows > 0:
+        _lib.call("vmoe_gemm_up_bwd_dx", ga.data_ptr(), ga.stride(0), w1.data_ptr(),
+                  w1.stride(0), grad_x.data_ptr(), grad_x.stride(0), *_meta_args(m), hidden,
+                  m.max_width, m.rows, _lib.stream(ga.device))
+    return grad_x
+
+
+def up_bwd_dw(ga, x, w1, m: GemmMeta, hidden: int, gather_map: torch.Tensor | None):
+    """grad_w1 = X_e^T @ GA_e, X_e read through gather_map when given."""
     ga = _bf16(ga, "grouped_gemm_up_backward grad_output")
     x = _bf16(x, "grouped_gemm_up_backward x")
     w1 = _bf16(w1, "grouped_gemm_up_backward w1")
     _need(w1.shape[0] == hidden and x.shape[1] == hidden, "x / w1 do not match hidden_size")
-    _need(ga.shape[0] >= m.rows and ga.shape[1] >= m.max_width,
-          "grad_output smaller than [rows, max_expert_width]")
     if gather_map is None:
         _need(x.shape[0] >= m.rows, "x has fewer rows than expert_token_offsets[-1]")
     else:
         _need(gather_map.numel() >= m.rows, "gather_map shorter than the padded row count")
-    grad_x = _alloc(m.rows, hidden, ga, not m.full_rows)
     grad_w1 = torch.zeros_like(w1) if not m.full_cols else torch.empty_like(w1)
     dev = ga.device
-    if m.rows > 0:
-        _lib.call("vmoe_gemm_up_bwd_dx", ga.data_ptr(), ga.stride(0), w1.data_ptr(),
-                  w1.stride(0), grad_x.data_ptr(), grad_x.stride(0), *_meta_args(m), hidden,
-                  m.max_width, m.rows, _lib.stream(dev))
     gm = None if gather_map is None else _i32(gather_map)
     ws = _dw_workspace(m, hidden, dev)
     _lib.call("vmoe_gemm_up_bwd_dw", x.data_ptr(), x.stride(0), x.shape[0], _lib.ptr(gm),
               ga.data_ptr(), ga.stride(0), grad_w1.data_ptr(), grad_w1.stride(0),
               *_meta_args(m), hidden, m.max_width, m.rows, ws.data_ptr(), ws.numel(),
               _lib.stream(dev))
-    return grad_x, grad_w1
+    return grad_w1
+
+
+def up_bwd_from_ga(ga, x, w1, m: GemmMeta, hidden: int, gather_map: torch.Tensor | None):
+    """(grad_x in gathered rows, grad_w1) from GA, the gradient w.r.t. the
+    up projection's pre-activation."""
+    _need(x.shape[1] == hidden, "x / w1 do not match hidden_size")
+    grad_x = up_bwd_dx(ga, w1, m, hidden)
+    return grad_x, up_bwd_dw(ga, x, w1, m, hidden, gather_map)
 
 
 def up_bwd(grad_h, x, w1, pre, m: GemmMeta, hidden: int, act: int,
@@ -527,6 +543,10 @@ class RoutedMoEOp(torch.autograd.Function):
         x_flat, w1, w2, h, pre, gm, rw, ar = ctx.saved_tensors
         ga, grad_w2 = down_bwd(grad_out, h, w2, ctx.meta, ctx.hidden_size, zero_tails=False,
                                pre=pre, gather_map=gm, row_scale=rw)
-        grad_xg, grad_w1 = up_bwd_from_ga(ga, x_flat, w1, ctx.meta, ctx.hidden_size, gm)
+        # the combine right after the dX GEMM, while its output is still in
+        # the caches, then dW1
+        grad_xg = up_bwd_dx(ga, w1, ctx.meta, ctx.hidden_size)
         grad_x = combine_rows(grad_xg, ar, ctx.top_k, x_flat.shape[0])
+        del grad_xg
+        grad_w1 = up_bwd_dw(ga, x_flat, w1, ctx.meta, ctx.hidden_size, gm)
         return grad_x, grad_w1, grad_w2, None, None, None, None, None, None
