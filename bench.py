@@ -141,11 +141,12 @@ def build_workload(name, device):
         ranks = np.random.default_rng(0).permutation(E) + 1
         base = torch.tensor(-1.2 * np.log(ranks), dtype=torch.float32, device=device)
         state = {"bias": None}
+        # the bias is held in the logits' dtype (bf16), converted once per alpha
         m.router.register_forward_hook(
-            lambda mod, inp, out: out if state["bias"] is None else out + state["bias"].to(out.dtype))
+            lambda mod, inp, out: out if state["bias"] is None else out + state["bias"])
         with torch.no_grad():
             for alpha in range(1, 20):
-                state["bias"] = alpha * base
+                state["bias"] = (alpha * base).to(torch.bfloat16)
                 _, _, f_i = m(xb)
                 logits = m.router(xb.reshape(-1, d))
                 sel = torch.topk(torch.sigmoid(logits.float()), k, dim=-1).indices
