@@ -61,7 +61,10 @@ def test_route_golden(case, dtype, device):
 # test fixtures (b=128), random top-k routing on the device.
 SHAPES = [(2 * 64, 2, 4, 128), (4 * 256, 2, 8, 128), (8 * 512, 2, 8, 64),
           (8 * 1024, 2, 8, 64), (8 * 2048, 2, 16, 64), (16384, 8, 64, 64),
-          (32768, 8, 128, 64), (4096, 8, 1000, 16)]
+          (32768, 8, 128, 64), (4096, 8, 1000, 16),
+          # past the two-launch path's limits (E * tiles > 65536, E > 1024):
+          # the three-launch path with the single-workgroup scan
+          (65536, 8, 256, 64), (4096, 4, 2048, 16)]
 
 
 @pytest.mark.parametrize("T,k,E,b", SHAPES)

@@ -210,33 +210,65 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
   }
 }
 
-// Launch 3: stable placement. Each wave walks its kWaveSpan assignments in
-// order, 64 at a time; lanes holding the same expert id find each other with
-// ballots over the id bits, and rank = number of equal lanes below.
-__global__ __launch_bounds__(kRouteThreads) void route_place_kernel(
-    const void* __restrict__ sel, int is64, int64_t A, int E, int nbits, int ntiles,
-    int top_k, RouteWs ws, int32_t* __restrict__ bin_ids, int32_t* __restrict__ indices,
-    int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int64_t row_capacity,
-    int32_t* __restrict__ assignment_row, const uint16_t* __restrict__ weights,
-    float* __restrict__ row_weight) {
-  extern __shared__ int32_t wbase[];  // [kRouteWaves][E]
+constexpr int kSpanSteps = kWaveSpan / kWave;
+
+// One wave's span of a tile, held in registers from the start of the
+// placement kernels so the loads overlap the prefix work: expert id per
+// assignment (-1 past A or out of range) and its bf16 routing weight.
+struct TileSel {
+  int32_t e[kSpanSteps];
+  uint16_t w[kSpanSteps];
+};
+
+__device__ __forceinline__ TileSel load_tile(const void* __restrict__ sel, int is64, int64_t A,
+                                             int E, int tile,
+                                             const uint16_t* __restrict__ weights) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int64_t w0 = (int64_t)tile * kTile + (int64_t)wave * kWaveSpan;
+  TileSel t;
+#pragma unroll
+  for (int i = 0; i < kSpanSteps; ++i) {
+    const int64_t p = w0 + i * kWave + lane;
+    int64_t ev = -1;
+    uint16_t wv = 0;
+    if (p < A) {
+      ev = load_sel(sel, is64, p);
+      if (weights) wv = weights[p];
+    }
+    t.e[i] = ev >= 0 && ev < E ? (int32_t)ev : -1;
+    t.w[i] = wv;
+  }
+  return t;
+}
+
+// Stable placement of tile `tile` (kTile assignments). Each wave walks its
+// kWaveSpan assignments in order, 64 at a time; lanes holding the same
+// expert id find each other with ballots over the id bits, and rank = number
+// of equal lanes below. tile_start[e] is the sorted position of the tile's
+// first assignment of expert e; start/kept/bs/ps are per expert (the sorted
+// position of the expert's first assignment, its kept count, bins[e-1] and
+// padded_bins[e-1]). wbase is kRouteWaves * E ints of LDS.
+__device__ void place_tile(const TileSel& ts, int E, int nbits, int tile, int top_k,
+                           const int32_t* tile_start, const int32_t* start,
+                           const int32_t* kept, const int32_t* bs, const int32_t* ps,
+                           int32_t* wbase, int32_t* __restrict__ bin_ids,
+                           int32_t* __restrict__ indices, int32_t* __restrict__ row_src,
+                           int32_t* __restrict__ gather_map, int64_t row_capacity,
+                           int32_t* __restrict__ assignment_row,
+                           float* __restrict__ row_weight) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) wbase[i] = 0;
   __syncthreads();
 
-  const int64_t w0 = (int64_t)blockIdx.x * kTile + (int64_t)wave * kWaveSpan;
+  const int64_t w0 = (int64_t)tile * kTile + (int64_t)wave * kWaveSpan;
   // Per-wave histogram of this wave's span.
-  for (int s = 0; s < kWaveSpan; s += kWave) {
-    const int64_t p = w0 + s + lane;
-    if (p < A) {
-      int64_t e = load_sel(sel, is64, p);
-      if (e >= 0 && e < E) atomicAdd(&wbase[wave * E + (int)e], 1);
-    }
-  }
+#pragma unroll
+  for (int i = 0; i < kSpanSteps; ++i)
+    if (ts.e[i] >= 0) atomicAdd(&wbase[wave * E + ts.e[i]], 1);
   __syncthreads();
   // Turn the per-wave counts into per-wave first sorted positions.
   for (int e = tid; e < E; e += kRouteThreads) {
-    int32_t run = ws.counts[(int64_t)e * ntiles + blockIdx.x];
+    int32_t run = tile_start[e];
 #pragma unroll
     for (int w = 0; w < kRouteWaves; ++w) {
       int32_t c = wbase[w * E + e];
@@ -247,15 +279,11 @@ __global__ __launch_bounds__(kRouteThreads) void route_place_kernel(
   __syncthreads();
 
   int32_t* base = wbase + wave * E;
-  for (int s = 0; s < kWaveSpan; s += kWave) {
-    const int64_t p = w0 + s + lane;
-    int e = 0;
-    bool valid = false;
-    if (p < A) {
-      int64_t ev = load_sel(sel, is64, p);
-      valid = ev >= 0 && ev < E;
-      e = valid ? (int)ev : 0;
-    }
+#pragma unroll
+  for (int st = 0; st < kSpanSteps; ++st) {
+    const int64_t p = w0 + st * kWave + lane;
+    const bool valid = ts.e[st] >= 0;
+    const int e = valid ? ts.e[st] : 0;
     uint64_t same = ballot64(valid);
     for (int b = 0; b < nbits; ++b) {
       const bool bit = (e >> b) & 1;
@@ -267,17 +295,17 @@ __global__ __launch_bounds__(kRouteThreads) void route_place_kernel(
     if (valid) first = base[e];
     __builtin_amdgcn_wave_barrier();
     if (valid) {
-      const int32_t q = first + rank - ws.start[e];  // rank inside expert e
-      if (q < ws.kept[e]) {
-        const int32_t i = ws.bs[e] + q;
-        const int64_t row = (int64_t)ws.ps[e] + q;
+      const int32_t q = first + rank - start[e];  // rank inside expert e
+      if (q < kept[e]) {
+        const int32_t i = bs[e] + q;
+        const int64_t row = (int64_t)ps[e] + q;
         bin_ids[i] = e;
         indices[i] = (int32_t)p;
         assignment_row[p] = (int32_t)row;
         if (row < row_capacity) {
           row_src[row] = (int32_t)p;
           gather_map[row] = (int32_t)(p / top_k);
-          if (row_weight) row_weight[row] = __uint_as_float((uint32_t)weights[p] << 16);
+          if (row_weight) row_weight[row] = __uint_as_float((uint32_t)ts.w[st] << 16);
         }
       } else {
         assignment_row[p] = -1;
@@ -286,6 +314,161 @@ __global__ __launch_bounds__(kRouteThreads) void route_place_kernel(
     }
     __builtin_amdgcn_wave_barrier();
   }
+}
+
+// Launch 3 (three-launch path): placement from the scan's in-place prefix.
+__global__ __launch_bounds__(kRouteThreads) void route_place_kernel(
+    const void* __restrict__ sel, int is64, int64_t A, int E, int nbits, int ntiles,
+    int top_k, RouteWs ws, int32_t* __restrict__ bin_ids, int32_t* __restrict__ indices,
+    int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int64_t row_capacity,
+    int32_t* __restrict__ assignment_row, const uint16_t* __restrict__ weights,
+    float* __restrict__ row_weight) {
+  extern __shared__ int32_t lds[];
+  int32_t* wbase = lds;                        // [kRouteWaves][E]
+  int32_t* tile_start = wbase + kRouteWaves * E;  // [E]
+  const TileSel ts = load_tile(sel, is64, A, E, blockIdx.x, row_weight ? weights : nullptr);
+  for (int e = threadIdx.x; e < E; e += kRouteThreads)
+    tile_start[e] = ws.counts[(int64_t)e * ntiles + blockIdx.x];
+  place_tile(ts, E, nbits, blockIdx.x, top_k, tile_start, ws.start, ws.kept, ws.bs, ws.ps,
+             wbase, bin_ids, indices, row_src, gather_map, row_capacity, assignment_row,
+             row_weight);
+}
+
+// Launch 2 of the two-launch path (E <= kFusedMaxExperts and E * tiles <=
+// kFusedMaxCounts): every workgroup derives what the scan would give it from
+// the per-tile histograms (E * tiles counts, from L2): per-expert totals and
+// the prefix of its own tile (one wave per expert), then the rounded counts
+// and the scans over experts; workgroup 0 writes the per-expert outputs and
+// info[], workgroup b the pad rows of experts e = b (mod grid), and workgroup
+// b < tiles places tile b. This saves the single-workgroup scan launch.
+constexpr int kFusedMaxExperts = 1024;
+constexpr int64_t kFusedMaxCounts = 65536;
+
+__global__ __launch_bounds__(kRouteThreads) void route_fused_kernel(
+    const void* __restrict__ sel, int is64, int64_t A, int E, int nbits, int ntiles,
+    int block, int mode, int top_k, RouteWs ws, int32_t* __restrict__ tpe,
+    int32_t* __restrict__ bins, int32_t* __restrict__ padded_bins,
+    int32_t* __restrict__ bin_ids, int32_t* __restrict__ indices,
+    int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int32_t map_pad,
+    int64_t row_capacity, int32_t* __restrict__ assignment_row,
+    const uint16_t* __restrict__ weights, float* __restrict__ row_weight,
+    int32_t* __restrict__ info, int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ padded_counts) {
+  __shared__ int32_t scan_smem[kRouteWaves + 1];
+  __shared__ int32_t tot_k, tot_r, any_bad;
+  extern __shared__ int32_t lds[];
+  int32_t* wbase = lds;                       // [kRouteWaves][E]
+  int32_t* cnt = wbase + kRouteWaves * E;     // [E] tokens per expert
+  int32_t* tstart = cnt + E;                  // [E] count in tiles before this one, then start
+  int32_t* start = tstart + E;                // [E]
+  int32_t* kept = start + E;                  // [E]
+  int32_t* rnd = kept + E;                    // [E]
+  int32_t* bs = rnd + E;                      // [E]
+  int32_t* ps = bs + E;                       // [E]
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int b = blockIdx.x;
+  if (tid == 0) any_bad = 0;
+  const TileSel ts = load_tile(sel, is64, A, E, b, row_weight ? weights : nullptr);
+
+  // Totals and this tile's prefix: G lanes per expert (a power of two that
+  // divides the wave), each summing every G-th tile, so a thread has all of
+  // its counts loads in flight at once; then a butterfly over the G lanes.
+  int G = kWave;
+  while (G > 1 && G * E > kRouteThreads) G >>= 1;
+  const int j = tid & (G - 1);
+  for (int e = tid / G; e < E; e += kRouteThreads / G) {
+    const int32_t* c = ws.counts + (int64_t)e * ntiles;
+    int32_t tot = 0, pre = 0;
+#pragma unroll 8
+    for (int t = j; t < ntiles; t += G) {
+      const int32_t v = c[t];
+      tot += v;
+      pre += t < b ? v : 0;
+    }
+    for (int off = G / 2; off > 0; off >>= 1) {
+      tot += __shfl_xor(tot, off, kWave);
+      pre += __shfl_xor(pre, off, kWave);
+    }
+    if (j == 0) {
+      cnt[e] = tot;
+      tstart[e] = pre;
+    }
+  }
+  __syncthreads();
+  // Scans over experts (E <= 1024: up to 4 consecutive experts per thread).
+  const int per = (E + kRouteThreads - 1) / kRouteThreads;
+  const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
+  int32_t sc = 0, sk = 0, sr = 0;
+  for (int e = e0; e < e1; ++e) {
+    const int32_t c = cnt[e], r = round_count(c, block, mode);
+    rnd[e] = r;
+    kept[e] = min(c, r);
+    sc += c;
+    sk += min(c, r);
+    sr += r;
+  }
+  int32_t t_c, t_k, t_r;
+  int32_t xc = block_exclusive_scan<int32_t, kRouteThreads>(sc, scan_smem, &t_c);
+  __syncthreads();
+  int32_t xk = block_exclusive_scan<int32_t, kRouteThreads>(sk, scan_smem, &t_k);
+  __syncthreads();
+  int32_t xr = block_exclusive_scan<int32_t, kRouteThreads>(sr, scan_smem, &t_r);
+  for (int e = e0; e < e1; ++e) {
+    start[e] = xc;
+    tstart[e] += xc;
+    bs[e] = xk;
+    ps[e] = xr;
+    xc += cnt[e];
+    xk += kept[e];
+    xr += rnd[e];
+  }
+  if (tid == 0) {
+    tot_k = t_k;
+    tot_r = t_r;
+  }
+  if (b == 0) {
+    bool bad = false;
+    for (int t = tid; t < ntiles; t += kRouteThreads) bad |= ws.bad[t] != 0;
+    if (bad) any_bad = 1;
+  }
+  __syncthreads();
+
+  if (b == 0) {
+    for (int e = tid; e < E; e += kRouteThreads) {
+      tpe[e] = cnt[e];
+      bins[e] = bs[e] + kept[e];
+      padded_bins[e] = ps[e] + rnd[e];
+      // The module's expert_token_offsets = [0, padded_bins] and padded
+      // tokens_per_expert = diff(padded_bins) (moe.py:193-202).
+      if (expert_offsets) {
+        expert_offsets[e + 1] = ps[e] + rnd[e];
+        if (e == 0) expert_offsets[0] = 0;
+      }
+      if (padded_counts) padded_counts[e] = rnd[e];
+    }
+    if (tid == 0) {
+      int32_t err = any_bad ? (int32_t)VMOE_ROUTE_BAD_EXPERT_ID : 0;
+      if ((int64_t)tot_r > row_capacity) err |= (int32_t)VMOE_ROUTE_ROW_OVERFLOW;
+      info[VMOE_INFO_ROWS] = tot_r;
+      info[VMOE_INFO_KEPT] = tot_k;
+      info[VMOE_INFO_ERRORS] = err;
+      info[3] = 0;
+    }
+  }
+  // Pad rows [ps + kept, ps + rounded) of the experts this workgroup owns.
+  for (int e = b + (int)gridDim.x * wave; e < E; e += (int)gridDim.x * kRouteWaves) {
+    for (int32_t q = kept[e] + lane; q < rnd[e]; q += kWave) {
+      const int64_t row = (int64_t)ps[e] + q;
+      if (row < row_capacity) {
+        row_src[row] = -1;
+        gather_map[row] = map_pad;
+        if (row_weight) row_weight[row] = 0.0f;
+      }
+    }
+  }
+  if (b < ntiles)
+    place_tile(ts, E, nbits, b, top_k, tstart, start, kept, bs, ps, wbase, bin_ids, indices,
+               row_src, gather_map, row_capacity, assignment_row, row_weight);
 }
 
 // Row maps from caller arrays (vmoe_row_maps): init, then place.
@@ -361,16 +544,27 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
                        sizeof(int32_t) * E, s, sel, is64, A, E, ntiles, ws.counts, ws.bad);
     VMOE_CHECK_LAUNCH();
   }
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  if (E <= kFusedMaxExperts && (int64_t)E * ntiles <= kFusedMaxCounts) {
+    hipLaunchKernelGGL(route_fused_kernel, dim3(std::max(ntiles, 1)), dim3(kRouteThreads),
+                       sizeof(int32_t) * (kRouteWaves + 7) * E, s, sel, is64, A, E, nbits,
+                       ntiles, block, rounding, top_k, ws, tpe, bins, padded_bins, bin_ids,
+                       indices, row_src, gather_map, gather_map_pad, row_capacity,
+                       assignment_row, weights, row_weight, info, expert_offsets,
+                       padded_counts);
+    VMOE_CHECK_LAUNCH();
+    return VMOE_OK;
+  }
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), sizeof(int32_t) * (4 * E + 1),
                      s, ws, E, ntiles, block, rounding, tpe, bins, padded_bins, row_src,
                      gather_map, gather_map_pad, row_weight, row_capacity, info,
                      expert_offsets, padded_counts);
   VMOE_CHECK_LAUNCH();
   if (ntiles > 0) {
-    int nbits = 1;
-    while ((1 << nbits) < E) ++nbits;
     hipLaunchKernelGGL(route_place_kernel, dim3(ntiles), dim3(kRouteThreads),
-                       sizeof(int32_t) * kRouteWaves * E, s, sel, is64, A, E, nbits, ntiles,
+                       sizeof(int32_t) * (kRouteWaves + 1) * E, s, sel, is64, A, E, nbits,
+                       ntiles,
                        top_k, ws, bin_ids, indices, row_src, gather_map, row_capacity,
                        assignment_row, weights, row_weight);
     VMOE_CHECK_LAUNCH();

@@ -3,10 +3,12 @@
 Mirrors fused_route (triton_moe/kernels/fused_cumsum.py:85-171 of the
 reference): same arguments, same five outputs, same errors. The reference runs
 torch.sort + torch.bincount + a one-program cumsum kernel and, for token
-dropping, a host loop with 2E syncs; here one three-launch HIP chain produces
-the sorted arrays, histogram, both cumulative sums, the padded-row maps and
-the gather map at once, and only "down"/"nearest" rounding (whose output length
-is data dependent) reads anything back to the host.
+dropping, a host loop with 2E syncs; here one HIP chain (a per-tile histogram,
+then placement; a single-workgroup scan in between for more than 1024 experts
+or 65,536 tile counts) produces the sorted arrays, histogram, both cumulative
+sums, the padded-row maps and the gather map at once, and only "down"/"nearest"
+rounding (whose output length is data dependent) reads anything back to the
+host.
 """
 
 from __future__ import annotations
