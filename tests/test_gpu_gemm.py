@@ -259,6 +259,78 @@ def test_up_dw_row_map(with_workspace, device):
     assert_close_norm(gw, ref, TIGHT, f"GW1 map ws={with_workspace}")
 
 
+def test_dw_split_tiles_across_many_lanes(device):
+    """One expert holds almost every row, so its tiles' K chunks span many
+    workgroup lanes (three or more segments per tile): the wave finishing a
+    tile's last segment sums the partials in lane order. Checked against the
+    per-expert reference, for bitwise determinism over repeated calls (the
+    arrival words are left zero for the next call), and against the split-K
+    free path within the summation-order tolerance."""
+    from triton_moe import _lib
+    from triton_moe.kernels.grouped_gemm import _dw_workspace, host_meta
+
+    g = torch.Generator().manual_seed(11)
+    d, widths = 512, [256, 128, 256]
+    E = len(widths)
+    offsets = [0]
+    for w in widths:
+        offsets.append(offsets[-1] + w)
+    counts = [30000, 64, 0]          # hot, small, empty
+    pad = [(c + 63) // 64 * 64 for c in counts]
+    eto = torch.tensor([0] + list(torch.tensor(pad).cumsum(0)), dtype=torch.int32)
+    P, W, max_w = int(eto[-1]), offsets[-1], max(widths)
+    tpe = torch.diff(eto)
+    ewo = torch.tensor(offsets, dtype=torch.int32)
+    wid = torch.tensor(widths, dtype=torch.int32)
+    xg = torch.randn(P, d, generator=g).to(torch.bfloat16)
+    ga = (torch.randn(P, max_w, generator=g) * 0.1).to(torch.bfloat16)
+    h = torch.randn(P, max_w, generator=g).abs().to(torch.bfloat16)
+    gy = (torch.randn(P, d, generator=g) * 0.1).to(torch.bfloat16)
+    for e in range(E):
+        r0, r1 = int(eto[e]), int(eto[e + 1])
+        ga[r0:r1, widths[e]:] = 0
+        h[r0:r1, widths[e]:] = 0
+        ga[r0 + counts[e]:r1] = 0
+        h[r0 + counts[e]:r1] = 0
+    dev = [t.to(device) for t in (eto, ewo, wid, tpe)]
+    m = host_meta(*dev, max_w, d, P, W)
+    xd, gad, hd, gyd = (t.to(device) for t in (xg, ga, h, gy))
+    ws = _dw_workspace(m, d, device)
+
+    def dw1(workspace):
+        out = torch.full((d, W), float("nan"), dtype=torch.bfloat16, device=device)
+        _lib.call("vmoe_gemm_up_bwd_dw", xd.data_ptr(), xd.stride(0), 0, None, gad.data_ptr(),
+                  gad.stride(0), out.data_ptr(), out.stride(0), *(t.data_ptr() for t in dev),
+                  E, d, max_w, P, None if workspace is None else workspace.data_ptr(),
+                  0 if workspace is None else workspace.numel(), _lib.stream(xd.device))
+        return out
+
+    def dw2(workspace):
+        out = torch.full((W, d), float("nan"), dtype=torch.bfloat16, device=device)
+        _lib.call("vmoe_gemm_down_bwd_dw", hd.data_ptr(), hd.stride(0), gyd.data_ptr(),
+                  gyd.stride(0), 0, None, out.data_ptr(), out.stride(0),
+                  *(t.data_ptr() for t in dev), E, d, max_w, P,
+                  None if workspace is None else workspace.data_ptr(),
+                  0 if workspace is None else workspace.numel(), _lib.stream(xd.device))
+        return out
+
+    ref1 = torch.zeros(d, W)
+    ref2 = torch.zeros(W, d)
+    for e in range(E):
+        r0, r1 = int(eto[e]), int(eto[e + 1])
+        w, o = widths[e], offsets[e]
+        ref1[:, o:o + w] = bf(xg[r0:r1].float().T @ ga[r0:r1, :w].float())
+        ref2[o:o + w] = bf(h[r0:r1, :w].float().T @ gy[r0:r1].float())
+    a1, a2 = dw1(ws), dw2(ws)
+    assert_close_norm(a1, ref1, TIGHT, "dW1 split across lanes")
+    assert_close_norm(a2, ref2, TIGHT, "dW2 split across lanes")
+    for _ in range(3):
+        assert torch.equal(dw1(ws), a1) and torch.equal(dw2(ws), a2)
+    assert int(ws[:256].count_nonzero()) == 0, "arrival words left non-zero"
+    assert_close_norm(dw1(None), ref1, TIGHT, "dW1 without split-K")
+    assert_close_norm(dw2(None), ref2, TIGHT, "dW2 without split-K")
+
+
 @pytest.mark.parametrize("broadcast", [False, True], ids=["token_rows", "broadcast_row"])
 def test_weighted_rows_through_map(broadcast, device):
     """The module's fused path: H' = bf16(w_r relu(z)^2) from x_flat[map]

@@ -37,7 +37,8 @@
 //    projection (grouped_gemm.py:336-346); for the down dH GEMM an optional
 //    fused relu^2 gradient GA = bf16(pre > 0 ? 2 * bf16(acc) * pre : 0)
 //    (grouped_gemm.py:751-766), so dX and dW read GA directly; split-K fp32
-//    partial tiles for the dW GEMMs, summed in chunk order by a second pass.
+//    partial tiles for the dW GEMMs, summed in chunk order by the wave that
+//    finishes a tile's last segment.
 
 #include <algorithm>
 
@@ -67,7 +68,6 @@ constexpr int kWaves = kConsumers + kProducers;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxExperts = 2048;  // per-expert work prefix held in LDS
 constexpr int kRecExperts = 512;   // per-expert metadata also held in LDS up to this E
-constexpr int kRedThreads = 256;   // split-K reduction kernel
 constexpr int kLane = 8;           // dW GEMMs: workgroups of one XCD that share each K chunk
 
 enum Variant { UP_FWD = 0, DOWN_FWD, UP_DX, UP_DW, DOWN_DH, DOWN_DW };
@@ -95,8 +95,9 @@ struct Args {
   int act;
   int64_t rows_bound;
   int kc;          // K rows per work item for the dW GEMMs (0 = whole K)
-  float* partial;  // fp32 partial tiles of split tiles (2 slots per workgroup)
-  int grid;        // GEMM workgroups (the split-K reduce recomputes their ranges)
+  float* partial;    // fp32 partial tiles of split tiles (2 slots per workgroup)
+  uint32_t* arrive;  // split-K arrival words, kConsumers per workgroup (zero between launches)
+  int grid;          // GEMM workgroups
 };
 
 // Metadata of one expert as the GEMMs read it: its row range [t0, t1) in
@@ -1010,23 +1011,113 @@ struct Gemm {
     if (pd.mask & (1 << U)) flush_unit<U / FM, U % FM>(p, pd, scr);
   }
 
-  // `pslot` >= 0: the accumulators are a partial sum over some of the tile's
-  // K chunks; the fp32 tile goes to that partial slot in the accumulator
-  // layout (wave, i, j, g, lane: 1 KiB contiguous per store) and the reduce
-  // kernel sums the segments in chunk order and rounds once.
-  __device__ __forceinline__ static void store_partial(const Args& p, int pslot, const f32x16_t (&acc)[FM][FN]) {
+  // Partial tiles travel between XCDs, whose L2s are not coherent with one
+  // another: they are written and read with device-scope cache policy (sc1),
+  // so stores reach the device-coherent level and loads do not hit a stale
+  // line, without flushing or invalidating a whole L2.
+  static constexpr int kScDevice = 16;  // buffer cache policy: sc1
+
+  // The accumulators as a partial sum over some of the tile's K chunks: the
+  // wave's fp32 values go to partial slot `pslot` in the accumulator layout
+  // (wave, i, j, g, lane: 1 KiB contiguous per store).
+  __device__ __forceinline__ static void store_partial(const Args& p, int pslot,
+                                                       const f32x16_t (&acc)[FM][FN]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float* slot = p.partial + (int64_t)pslot * (BM * BN) + wave * (WM * WN);
+    const auto r = make_rsrc(p.partial + (int64_t)pslot * (BM * BN) + wave * (WM * WN));
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<float4*>(slot + ((((i * FN + j) * 4 + g) * 64 + lane) << 2)) =
-              make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                          acc[i][j][4 * g + 3]);
+        for (int g = 0; g < 4; ++g) {
+          const u32x4_t v = {__float_as_uint(acc[i][j][4 * g]),
+                             __float_as_uint(acc[i][j][4 * g + 1]),
+                             __float_as_uint(acc[i][j][4 * g + 2]),
+                             __float_as_uint(acc[i][j][4 * g + 3])};
+          __builtin_amdgcn_raw_buffer_store_b128(v, r, (((i * FN + j) * 4 + g) * 64 + lane) << 4,
+                                                 0, kScDevice);
+        }
   }
+
+  // Adds (FIRST: copies) the wave's values of partial slot `pslot` into acc,
+  // one 32x32 block at a time to bound the registers in flight.
+  template <bool FIRST>
+  __device__ __forceinline__ static void add_partial(const Args& p, int pslot,
+                                                     f32x16_t (&acc)[FM][FN]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const auto r = make_rsrc(p.partial + (int64_t)pslot * (BM * BN) + wave * (WM * WN));
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        // Keeps the next block's loads below this block's additions.
+        asm volatile("" ::: "memory");
+        u32x4_t v[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          v[g] = __builtin_amdgcn_raw_buffer_load_b128(
+              r, (((i * FN + j) * 4 + g) * 64 + lane) << 4, 0, kScDevice);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const float x = __uint_as_float(v[g][c]);
+            acc[i][j][4 * g + c] = FIRST ? x : acc[i][j][4 * g + c] + x;
+          }
+      }
+  }
+
+  // Split-K, per consumer wave. The K chunks [a, a + chunks) of a split tile
+  // are segments of consecutive non-empty lane ranges L0, L0 + 1, ...; the
+  // wave of each segment stores its fp32 partial (slot 2 lin for a range's
+  // first segment, 2 lin + 1 for its last), waits until the stores are
+  // complete and counts itself in the tile's arrival word with a wrapping
+  // increment, which the last arrival puts back to zero. The last wave sums
+  // the segments in lane order, s0 + s1 + s2 + ...; its own term comes from
+  // registers when it is s0 or s1 (the first addition commutes), else from
+  // its slot, so the sum does not depend on which wave arrives last. Returns
+  // true for that wave: acc then holds the whole tile for the normal
+  // epilogue. No wave waits for another.
+  __device__ static bool split_arrive(const Args& p, const Range& rg, int total, int a,
+                                      int chunks, int seg_item, f32x16_t (&acc)[FM][FN]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int NL = (int)gridDim.x / kLane, me = rg.lin / kLane, ts = rg.slot;
+    int L0 = me;
+    while (L0 > 0 && contig_begin(total, L0, NL) > a) --L0;
+    const bool l0_inside = contig_begin(total, L0, NL) != a;  // L0's segment starts mid-range
+    store_partial(p, 2 * rg.lin + (seg_item == rg.beg ? 0 : 1), acc);
+    int nseg = 0, own = 0;
+    for (int l = L0; l < NL; ++l) {
+      const int b0 = contig_begin(total, l, NL);
+      if (b0 >= a + chunks) break;
+      if (contig_begin(total, l + 1, NL) == b0) continue;  // empty range
+      if (l == me) own = nseg;
+      ++nseg;
+    }
+    wait_vmcnt<0>();  // the partial is at the device-coherent level
+    uint32_t old = 0;
+    if (lane == 0)
+      old = __builtin_amdgcn_atomic_inc32(
+          p.arrive + ((int64_t)(L0 * kLane + ts) * kConsumers + wave), (uint32_t)(nseg - 1),
+          __ATOMIC_RELAXED, "agent");
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != (uint32_t)(nseg - 1)) return false;
+    asm volatile("" ::: "memory");  // the loads below follow the arrival
+    int t = 0;
+    for (int l = L0; l < NL && t < nseg; ++l) {
+      const int b0 = contig_begin(total, l, NL);
+      if (contig_begin(total, l + 1, NL) == b0) continue;
+      const int slot = 2 * (l * kLane + ts) + (l == L0 && l0_inside ? 1 : 0);
+      // own >= 2: the sum is rebuilt from the slots, own included.
+      if (own >= 2 && t == 0)
+        add_partial<true>(p, slot, acc);
+      else if (t != own || own >= 2)
+        add_partial<false>(p, slot, acc);
+      ++t;
+    }
+    return true;
+  }
+
 
   // Producer waves: stage the k-tiles of all of the workgroup's items, in
   // item order, as one stream through the LDS ring (the first stages of the
@@ -1160,10 +1251,11 @@ struct Gemm {
   // A tile is finished when its last K chunk in this workgroup is done; its
   // results become the pending tile, stored during the next item's k-steps
   // (spread evenly over them) or at the end. A contiguous range may start or
-  // end inside a split tile; such a segment is a partial sum and goes to
-  // slot 2 * lin (the range's first segment) or 2 * lin + 1 (its last).
+  // end inside a split tile; such a segment is a partial sum, and the wave
+  // that completes the tile's last segment stores the tile (split_arrive).
   __device__ static void run_consumer(const Args& p, const lds_char* ring, const Meta& mt,
-                                      const Range& rg, lds_char* scr, const lds_char* scl) {
+                                      const Range& rg, int total, lds_char* scr,
+                                      const lds_char* scl) {
     int ec = 0;
     int s = 0;
     int nbegun = 0;  // items with k-steps so far (the producers' slot count)
@@ -1215,9 +1307,12 @@ struct Gemm {
       }
       const bool last_chunk = w.chunk == w.chunks - 1;
       if (rg.stride != 1 || last_chunk || item + 1 >= rg.end) {
-        if (w.chunks > 1 && !(seg_chunk == 0 && last_chunk)) {
-          store_partial(p, 2 * rg.lin + (seg_item == rg.beg ? 0 : 1), acc);
-        } else {
+        bool whole = true;
+        if constexpr (Cfg<V>::contig) {
+          if (w.chunks > 1 && !(seg_chunk == 0 && last_chunk))
+            whole = split_arrive(p, rg, total, item - w.chunk, w.chunks, seg_item, acc);
+        }
+        if (whole) {
           stash(p, w, acc, pd, kScaled && p.row_scale && w.nk > 0 ? scl + slot * (BM * 4)
                                                                   : nullptr);
           if (Cfg<V>::contig) {
@@ -1247,7 +1342,7 @@ struct Gemm {
     if (wave >= kConsumers)
       run_producer(p, ring, wins, scl, mt, rg);
     else
-      run_consumer(p, ring, mt, rg, epi + wave * EPI_BYTES, scl);
+      run_consumer(p, ring, mt, rg, total, epi + wave * EPI_BYTES, scl);
   }
 };
 
@@ -1268,104 +1363,6 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
                     160 * 1024,
                 "LDS budget of a gfx950 CU");
   G::run(p, (lds_char*)ring, meta, (lds_char*)epi, (lds_char*)wins, (lds_char*)scl);
-}
-
-// Finds the expert owning tile `id` in the concatenation of per-expert tile
-// ranges (a block scan over experts), the exclusive prefix of work items
-// before that expert, and the total number of work items. Returns false
-// when id is past the end.
-template <int V>
-__device__ bool locate_tile(const Args& p, int id, long long* scan, int* sh, int& e_out,
-                            int& tile_out, int& ipre_out, int& chunks_out, int& total_out) {
-  if (threadIdx.x == 0) sh[0] = -1;
-  long long base = 0;  // (tiles << 32) | items
-  for (int e0 = 0; e0 < p.E; e0 += kRedThreads) {
-    const int e = e0 + threadIdx.x;
-    int tiles = 0, chunks = 1;
-    if (e < p.E) expert_work<V>(p, Traits<V>::prob(p, rec_global(p, e)), tiles, chunks);
-    const long long packed = ((long long)tiles << 32) | (long long)work_items<V>(tiles, chunks);
-    long long total;
-    const long long ex = block_exclusive_scan<long long, kRedThreads>(packed, scan, &total);
-    const long long pre = base + ex;
-    const int t_pre = (int)(pre >> 32), i_pre = (int)(pre & 0xFFFFFFFFll);
-    if (tiles > 0 && id >= t_pre && id < t_pre + tiles) {
-      sh[0] = e;
-      sh[1] = id - t_pre;
-      sh[2] = i_pre;
-      sh[3] = chunks;
-    }
-    base += total;
-    __syncthreads();
-  }
-  e_out = __builtin_amdgcn_readfirstlane(sh[0]);
-  tile_out = __builtin_amdgcn_readfirstlane(sh[1]);
-  ipre_out = __builtin_amdgcn_readfirstlane(sh[2]);
-  chunks_out = __builtin_amdgcn_readfirstlane(sh[3]);
-  total_out = (int)(base & 0xFFFFFFFFll);
-  return e_out >= 0;
-}
-
-// Split-K reduction of the contig GEMMs. The K chunks of tile t are items
-// [a, a + chunks) of the lane ranges, done by slot t % kLane of each lane
-// whose range they touch. A tile inside one lane range was stored directly;
-// any other tile has one partial segment per lane range it touches, in slot
-// 2 lin (the segment starts that range) or 2 lin + 1 (it starts inside it),
-// lin = kLane * lane + t % kLane. This kernel sums the segments in chunk
-// order and rounds once. Workgroup (x, y) handles float4s
-// [1024 y, 1024 (y + 1)) of tile x's slots, which hold the accumulator
-// layout of the GEMM's epilogue.
-template <int V>
-__global__ __launch_bounds__(kRedThreads) void splitk_reduce_kernel(Args p) {
-  using G = Gemm<V>;
-  constexpr int BM = G::BM, BN = G::BN, VEC = 4, PART = VEC * kRedThreads;
-  static_assert((BM * BN / 4) % PART == 0, "slot must split into whole parts");
-  __shared__ long long scan[16];
-  __shared__ int sh[4];
-  int e, tile, ipre, chunks, total;
-  if (!locate_tile<V>(p, blockIdx.x, scan, sh, e, tile, ipre, chunks, total)) return;
-  if (chunks <= 1) return;
-  const int Gr = p.grid / kLane;  // lanes
-  const int a = ipre + (tile / kLane) * chunks, ts = tile % kLane;
-  int L = (int)min<int64_t>(Gr - 1, (int64_t)a * Gr / total);
-  while (L + 1 < Gr && contig_begin(total, L + 1, Gr) <= a) ++L;
-  while (L > 0 && contig_begin(total, L, Gr) > a) --L;
-  if (contig_begin(total, L + 1, Gr) >= a + chunks) return;  // one range: stored directly
-  const Prob q = Traits<V>::prob(p, rec_global(p, e));
-  const int n_tiles = cdiv(q.N, BN);
-  const int m0 = (tile / n_tiles) * BM, n0 = (tile % n_tiles) * BN;
-  const int f0 = blockIdx.y * PART + threadIdx.x;
-  float4 acc[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
-  auto add_slot = [&](int slot) {
-    const float4* src = reinterpret_cast<const float4*>(p.partial + (int64_t)slot * (BM * BN));
-    float4 v[VEC];
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) v[i] = src[f0 + i * kRedThreads];
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      acc[i].x += v[i].x; acc[i].y += v[i].y; acc[i].z += v[i].z; acc[i].w += v[i].w;
-    }
-  };
-  add_slot(2 * (L * kLane + ts) + (contig_begin(total, L, Gr) == a ? 0 : 1));
-  for (int l = L + 1; l < Gr; ++l) {
-    const int b0 = contig_begin(total, l, Gr);
-    if (b0 >= a + chunks) break;
-    if (contig_begin(total, l + 1, Gr) == b0) continue;  // empty range
-    add_slot(2 * (l * kLane + ts));
-  }
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    // float4 index -> (wave, i, j, g, lane) of the epilogue layout -> (m, n).
-    const int f = f0 + i * kRedThreads;
-    const int wave = f / (G::WM * G::WN / 4), rem = f % (G::WM * G::WN / 4);
-    const int lane = rem & 63, g = (rem >> 6) & 3, jj = (rem >> 8) % G::FN, ii = (rem >> 8) / G::FN;
-    const int m = m0 + (wave / G::WGN) * G::WM + ii * 32 + (lane & 31);
-    const int n = n0 + (wave % G::WGN) * G::WN + jj * 32 + 8 * g + 4 * (lane >> 5);
-    if (m >= q.M || n >= q.N) continue;
-    *reinterpret_cast<uint2*>(p.c + ((int64_t)q.cr + m) * p.ldc + q.cc + n) =
-        make_uint2(pack_bf16(acc[i].x, acc[i].y), pack_bf16(acc[i].z, acc[i].w));
-  }
 }
 
 // GA = bf16(pre > 0 ? 2 * grad_h * pre : 0) elementwise over [rows, cols]
@@ -1441,10 +1438,15 @@ int launch(Args p, int64_t items_bound, hipStream_t s) {
   return VMOE_OK;
 }
 
-// Partial-tile workspace of a split dW launch: two tiles per workgroup.
+// Workspace of a split dW launch: the arrival words (kConsumers per
+// workgroup, 256-byte aligned region), then two partial tiles per workgroup.
+inline size_t dw_arrive_bytes(int grid) {
+  return ((size_t)grid * kConsumers * sizeof(uint32_t) + 255) / 256 * 256;
+}
+
 template <int V>
 size_t dw_workspace(int grid) {
-  return (size_t)2 * grid * Cfg<V>::BM * Cfg<V>::BN * sizeof(float);
+  return dw_arrive_bytes(grid) + (size_t)2 * grid * Cfg<V>::BM * Cfg<V>::BN * sizeof(float);
 }
 
 template <int V>
@@ -1460,15 +1462,14 @@ int64_t row_items(int64_t rows_bound, int E, int64_t nmax) {
          ((nmax + Cfg<V>::BN - 1) / Cfg<V>::BN);
 }
 
-// dW GEMM with split-K: GEMM items, then the segment reduction.
+// dW GEMM with split-K (one launch; split tiles are summed in the kernel).
 template <int V>
 int launch_dw(Args p, int64_t tmax, void* ws, size_t ws_bytes, hipStream_t s) {
-  constexpr int BM = Cfg<V>::BM;
-  static_assert(BM * Cfg<V>::BN % (16 * kRedThreads) == 0, "reduce parts");
   const int64_t E = p.E;
   if (!ws) {
     p.kc = 0;
     p.partial = nullptr;
+    p.arrive = nullptr;
     return launch<V>(p, E * tmax, s);
   }
   // sum_e tiles_e * ceil(K_e / kc) <= tmax * (rows_bound / kc + E)
@@ -1478,12 +1479,9 @@ int launch_dw(Args p, int64_t tmax, void* ws, size_t ws_bytes, hipStream_t s) {
   p.kc = kDwChunk;
   p.grid = lane_grid();
   if (ws_bytes < dw_workspace<V>(p.grid)) return VMOE_ERR_WORKSPACE;
-  p.partial = reinterpret_cast<float*>(ws);
+  p.arrive = reinterpret_cast<uint32_t*>(ws);
+  p.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + dw_arrive_bytes(p.grid));
   hipLaunchKernelGGL(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
-  VMOE_CHECK_LAUNCH();
-  hipLaunchKernelGGL((splitk_reduce_kernel<V>),
-                     dim3((unsigned)(E * tmax), BM * Cfg<V>::BN / 4 / (4 * kRedThreads)),
-                     dim3(kRedThreads), 0, s, p);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }

@@ -150,10 +150,25 @@ def _meta_args(m: GemmMeta):
             m.num_experts)
 
 
+_DW_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
 def _dw_workspace(m: GemmMeta, hidden: int, device) -> torch.Tensor:
-    n = int(_lib.lib().vmoe_gemm_dw_workspace_bytes(m.num_experts, hidden, m.max_width,
-                                                    max(m.rows, 1)))
-    return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
+    """Split-K workspace of the dW GEMMs. Its arrival words must be zero when
+    a launch starts, and every launch leaves them zero, so one zero-filled
+    buffer per (device, stream) is kept and reused: calls on one stream run
+    in order, and calls on different streams get different buffers."""
+    n = max(int(_lib.lib().vmoe_gemm_dw_workspace_bytes(m.num_experts, hidden, m.max_width,
+                                                        max(m.rows, 1))), 16)
+    device = torch.device(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           _lib.stream(device))
+    ws = _DW_WORKSPACES.get(key)
+    if ws is None or ws.numel() < n:
+        # zero_() is a fill kernel, so this also holds under graph capture
+        ws = torch.empty(n, dtype=torch.uint8, device=device).zero_()
+        _DW_WORKSPACES[key] = ws
+    return ws
 
 
 def _zero_tails(buf: torch.Tensor, m: GemmMeta):
@@ -567,6 +582,10 @@ class RoutedMoEOp(torch.autograd.Function):
 
         x_flat, w1, w2, h, pre, gm, rw, ar = ctx.saved_tensors
         m, d = ctx.meta, ctx.hidden_size
+        if grad_out.shape[0] > 0 and grad_out.stride(0) == 0 and grad_out.stride(1) != 1:
+            # A broadcast scalar (the gradient of out.sum()): both GEMMs read
+            # one materialised row with leading dimension 0; make it once.
+            grad_out = grad_out[:1].contiguous().expand(grad_out.shape)
         # GA (written by dH) is read by dW1 and dX back to back while it is
         # cached, the combine follows dX for the same reason, dW2 (H' and G)
         # goes last: 8 us per cfg3 step against dH, dW2, dX, dW1.
