@@ -213,6 +213,158 @@ __global__ __launch_bounds__(topk_threads(VPL)) void router_topk_kernel(
   }
 }
 
+// Top-k with G lanes per token, 8 experts per lane (E % 8 == 0, E <= 8 G,
+// k <= 8): lane (s, r) of a wave holds experts 8r .. 8r + 7 of token slot s
+// (one 16-byte load), so a wave works on 64 / G tokens at once instead of
+// one. Each lane sorts its 8 keys with a 19-comparator network, then log2 G
+// butterfly steps merge the sorted lists of partner lanes (the larger of
+// A[j] and B[7 - j] is a bitonic sequence holding the top 8 of A and B; three
+// half-cleaner stages sort it), after which every lane of the group holds the
+// token's top 8. Keys, sigmoid, weights (v_j / (sum_j v_j + 1e-20), j
+// ascending) and the tie rule are those of router_topk_kernel; logsumexp and
+// the column sums reduce in a different fixed order.
+constexpr int kGrpMaxExperts = 128;
+constexpr int kGrpThreads = 256;
+constexpr int kGrpWaves = kGrpThreads / kWave;
+
+__device__ __forceinline__ void cs_desc(uint64_t& a, uint64_t& b) {
+  const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+  a = hi;
+  b = lo;
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, kWave);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, kWave);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int G>
+__global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
+    const uint16_t* __restrict__ logits, int64_t ldl, int64_t T, int E, int k, int norm,
+    uint16_t* __restrict__ weights, int32_t* __restrict__ selected32,
+    int64_t* __restrict__ selected64, float* __restrict__ probs, float* __restrict__ lse_out,
+    float* __restrict__ partial, int64_t per) {
+  constexpr int TPW = kWave / G;  // tokens per wave and batch
+  __shared__ float red[kGrpWaves][kGrpMaxExperts + 1];
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  const int r = lane & (G - 1), slot = lane / G;
+  const int e0 = 8 * r;
+  const bool part_ok = e0 < E;
+  float col[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) col[v] = 0.0f;
+  float zsum = 0.0f;
+  const int64_t t_beg = (int64_t)blockIdx.x * per, t_end = min(T, t_beg + per);
+  for (int64_t tb = t_beg + (int64_t)wv * TPW; tb < t_end; tb += (int64_t)kGrpWaves * TPW) {
+    const int64_t t = tb + slot;
+    const bool ok = t < t_end && part_ok;
+    float x[8];
+    if (ok) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(logits + t * ldl + e0);
+      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        x[2 * v] = __uint_as_float(w4[v] << 16);
+        x[2 * v + 1] = __uint_as_float(w4[v] & 0xFFFF0000u);
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) x[v] = -INFINITY;
+    }
+    float p[8];
+    float m = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      m = fmaxf(m, x[v]);
+      p[v] = ok ? sigmoidf(x[v]) : 0.0f;
+      col[v] += p[v];
+    }
+    if (probs && ok) {
+      float4* dst = reinterpret_cast<float4*>(probs + t * E + e0);
+      dst[0] = make_float4(p[0], p[1], p[2], p[3]);
+      dst[1] = make_float4(p[4], p[5], p[6], p[7]);
+    }
+    // logsumexp in fp32 over the group, rounded to bf16 as torch.logsumexp
+    // on bf16 logits.
+#pragma unroll
+    for (int st = 1; st < G; st <<= 1) m = fmaxf(m, __shfl_xor(m, st, kWave));
+    float se = 0.0f;
+    if (ok) {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) se += expf(x[v] - m);
+    }
+#pragma unroll
+    for (int st = 1; st < G; st <<= 1) se += __shfl_xor(se, st, kWave);
+    const float lse = bf16_to_f32(f32_to_bf16(logf(se) + m));
+    const bool tok = t < t_end;
+    if (tok && r == 0) {
+      if (lse_out) lse_out[t] = lse;
+      zsum += bf16_to_f32(f32_to_bf16(lse * lse));
+    }
+    // keys: value bits, then the lower expert index (p >= 0 orders like its
+    // bits); 0 for no expert, below every real key.
+    uint64_t key[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v)
+      key[v] = ok ? ((uint64_t)__float_as_uint(p[v]) << 32) | (uint32_t)(~(e0 + v)) : 0ull;
+    cs_desc(key[0], key[1]); cs_desc(key[2], key[3]); cs_desc(key[4], key[5]); cs_desc(key[6], key[7]);
+    cs_desc(key[0], key[2]); cs_desc(key[1], key[3]); cs_desc(key[4], key[6]); cs_desc(key[5], key[7]);
+    cs_desc(key[1], key[2]); cs_desc(key[5], key[6]);
+    cs_desc(key[0], key[4]); cs_desc(key[1], key[5]); cs_desc(key[2], key[6]); cs_desc(key[3], key[7]);
+    cs_desc(key[2], key[4]); cs_desc(key[3], key[5]);
+    cs_desc(key[1], key[2]); cs_desc(key[3], key[4]); cs_desc(key[5], key[6]);
+#pragma unroll
+    for (int st = 1; st < G; st <<= 1) {
+      uint64_t b[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) b[j] = shfl_xor_u64(key[j], st);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) key[j] = key[j] > b[7 - j] ? key[j] : b[7 - j];
+#pragma unroll
+      for (int d = 4; d >= 1; d >>= 1)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if ((j & d) == 0) cs_desc(key[j], key[j + d]);
+    }
+    if (tok) {
+      float vsum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < k) vsum += __uint_as_float((uint32_t)(key[j] >> 32));  // j ascending
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j < k && (j & (G - 1)) == r) {
+          const float v = __uint_as_float((uint32_t)(key[j] >> 32));
+          const int e = (int)(~(uint32_t)key[j]);
+          weights[t * k + j] = (uint16_t)f32_to_bf16(norm ? v / (vsum + 1e-20f) : v);
+          if (selected32) selected32[t * k + j] = e;
+          if (selected64) selected64[t * k + j] = e;
+        }
+      }
+    }
+  }
+  // Column sums: lanes with the same r hold the same experts; add over the
+  // token slots, then one partial row per workgroup in wave order.
+#pragma unroll
+  for (int st = G; st < kWave; st <<= 1)
+#pragma unroll
+    for (int v = 0; v < 8; ++v) col[v] += __shfl_xor(col[v], st, kWave);
+  if (slot == 0 && part_ok) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) red[wv][e0 + v] = col[v];
+  }
+  zsum = wave_sum_f32(zsum);
+  if (lane == 0) red[wv][E] = zsum;
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += kGrpThreads) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kGrpWaves; ++w) sum += red[w][e];
+    partial[(int64_t)blockIdx.x * (E + 1) + e] = sum;
+  }
+}
+
 // One workgroup: sums the block partials in a fixed order and forms the
 // losses: z_out (bf16) = z_loss, out_scalars[0] = load balance, [1] = compute
 // loss. Columns go 64 at a time (one per lane); wave w adds rows w, w + 16, ...
@@ -224,7 +376,6 @@ __global__ __launch_bounds__(kAuxThreads) void router_aux_kernel(
     const float* __restrict__ wn, uint16_t* __restrict__ f_i, float* __restrict__ f_i32,
     float* __restrict__ p_i, uint16_t* __restrict__ z_out, float* __restrict__ out_scalars) {
   __shared__ float wsum[kAuxWaves][kWave];
-  __shared__ float sh_lb[kAuxThreads / kWave], sh_cl[kAuxThreads / kWave];
   __shared__ long long sh_cnt[kAuxWaves];
   __shared__ float sh_z;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
@@ -364,9 +515,33 @@ extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64
   if (partial_floats < (size_t)nblk * (size_t)(num_experts + 1)) return VMOE_ERR_WORKSPACE;
   if (num_partial_rows) *num_partial_rows = nblk;
   const int64_t per = (num_tokens + nblk - 1) / nblk;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (num_experts % 8 == 0 && num_experts <= kGrpMaxExperts && top_k <= 8 &&
+      ld_logits % 8 == 0 && reinterpret_cast<uintptr_t>(logits) % 16 == 0 &&
+      (!probs || reinterpret_cast<uintptr_t>(probs) % 16 == 0)) {
+    int g = 1;
+    while (8 * g < num_experts) g <<= 1;
+    switch (g) {
+#define VMOE_RT_GRP(G)                                                                      \
+  case G:                                                                                   \
+    hipLaunchKernelGGL(router_topk_group_kernel<G>, dim3(nblk), dim3(kGrpThreads), 0, s,     \
+                       logits, ld_logits, num_tokens, num_experts, top_k, normalize, weights, \
+                       selected_i32, selected_i64, probs, lse, partial, per);                \
+    break;
+      VMOE_RT_GRP(1)
+      VMOE_RT_GRP(2)
+      VMOE_RT_GRP(4)
+      VMOE_RT_GRP(8)
+      VMOE_RT_GRP(16)
+#undef VMOE_RT_GRP
+      default:
+        return VMOE_ERR_UNSUPPORTED;
+    }
+    VMOE_CHECK_LAUNCH();
+    return VMOE_OK;
+  }
   const int vpl = vpl_of(num_experts);
   const size_t lds = sizeof(float) * (topk_threads(vpl) / kWave) * (num_experts + 1);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (vpl) {
 #define VMOE_RT_CASE(V)                                                                      \
   case V:                                                                                    \
