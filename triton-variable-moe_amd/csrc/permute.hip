@@ -219,6 +219,71 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(
   }
 }
 
+// The same combine for top_k <= KMAX on 16-byte vectors: lane j reads slot
+// j's row index (and weight) once and the wave takes them by readlane, then
+// every slot's loads are issued before any is summed, so a wave has k rows
+// in flight instead of one. The sum is the same: slot order, invalid rows
+// skipped.
+template <int KMAX, bool WEIGHTED, int CHUNKS>
+__global__ __launch_bounds__(kThreads) void combine_k_kernel(
+    const uint16_t* __restrict__ y, int64_t y_rows, int64_t ldy,
+    const int32_t* __restrict__ assignment_row, const uint16_t* __restrict__ w, int top_k,
+    uint16_t* __restrict__ out, int64_t ldo, int64_t num_tokens, int64_t hidden) {
+  using V = Vec<8>;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t nvec = hidden / 8;
+  for (int64_t t = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; t < num_tokens;
+       t += (int64_t)gridDim.x * kRowsPerBlock) {
+    int32_t my_row = -1;
+    uint32_t my_w = 0;
+    if (lane < top_k) {
+      my_row = assignment_row[t * top_k + lane];
+      if (WEIGHTED) my_w = __float_as_uint(bf16_to_f32(w[t * top_k + lane]));
+    }
+    int32_t rows[KMAX];
+    bool ok[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      rows[j] = __builtin_amdgcn_readlane(my_row, j);
+      ok[j] = j < top_k && rows[j] >= 0 && rows[j] < y_rows;
+    }
+    for (int64_t c0 = 0; c0 < nvec; c0 += (int64_t)CHUNKS * kWave) {
+      V::T v[KMAX][CHUNKS];
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j)
+#pragma unroll
+        for (int ch = 0; ch < CHUNKS; ++ch) {
+          const int64_t c = c0 + ch * kWave + lane;
+          v[j][ch] = ok[j] && c < nvec ? V::load(y + (int64_t)rows[j] * ldy + c * 8) : V::zero();
+        }
+      float acc[CHUNKS][8];
+#pragma unroll
+      for (int ch = 0; ch < CHUNKS; ++ch)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[ch][i] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) {
+        if (!ok[j]) continue;
+        const float scale =
+            WEIGHTED ? __uint_as_float(__builtin_amdgcn_readlane(my_w, j)) : 1.0f;
+#pragma unroll
+        for (int ch = 0; ch < CHUNKS; ++ch) {
+          float f[8];
+          V::to_f32(v[j][ch], f);
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            acc[ch][i] += WEIGHTED ? bf16_to_f32(f32_to_bf16(f[i] * scale)) : f[i];
+        }
+      }
+#pragma unroll
+      for (int ch = 0; ch < CHUNKS; ++ch) {
+        const int64_t c = c0 + ch * kWave + lane;
+        if (c < nvec) V::store(out + t * ldo + c * 8, V::from_f32(acc[ch]));
+      }
+    }
+  }
+}
+
 // Zero columns [widths[e], max_width) of expert e's rows [eto[e], eto[e+1]).
 __global__ __launch_bounds__(kThreads) void zero_tail_kernel(
     uint16_t* __restrict__ buf, int64_t ld, const int32_t* __restrict__ eto,
@@ -325,7 +390,14 @@ extern "C" int vmoe_combine(const uint16_t* y, int64_t y_rows, int64_t ldy,
   const bool vec = hidden % 8 == 0 && ldy % 8 == 0 && ldo % 8 == 0 && aligned16(y) &&
                    aligned16(out);
   const dim3 grid(row_grid(num_tokens)), block(kThreads);
-  if (vec) {
+  if (vec && top_k <= 8) {
+    if (weights)
+      hipLaunchKernelGGL((combine_k_kernel<8, true, 2>), grid, block, 0, s, y, y_rows, ldy,
+                         assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
+    else
+      hipLaunchKernelGGL((combine_k_kernel<8, false, 2>), grid, block, 0, s, y, y_rows, ldy,
+                         assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
+  } else if (vec) {
     // Two 16-byte chunks per lane cover d <= 1024 in one pass.
     if (weights)
       hipLaunchKernelGGL((combine_kernel<8, true, 2>), grid, block, 0, s, y, y_rows, ldy,

@@ -224,7 +224,7 @@ __global__ __launch_bounds__(topk_threads(VPL)) void router_topk_kernel(
 // ascending) and the tie rule are those of router_topk_kernel; logsumexp and
 // the column sums reduce in a different fixed order.
 constexpr int kGrpMaxExperts = 128;
-constexpr int kGrpThreads = 256;
+constexpr int kGrpThreads = 1024;
 constexpr int kGrpWaves = kGrpThreads / kWave;
 
 __device__ __forceinline__ void cs_desc(uint64_t& a, uint64_t& b) {
@@ -482,10 +482,28 @@ inline int vpl_of(int E) {
   return v;
 }
 
+inline int group_size(int E) {
+  int g = 1;
+  while (8 * g < E) g <<= 1;
+  return g;
+}
+
+// Workgroups of the top-k launch = partial rows for the aux kernel (both
+// top-k kernels take any count; each workgroup handles a contiguous token
+// range). Experts the grouped kernel can take: one token batch per wave
+// (16 waves of 64 / G tokens), but at least min(256, T / (64 / G))
+// workgroups so small T still spreads over the device. Otherwise about
+// 2 tokens per wave. At most kRtMaxBlocks.
 inline int router_blocks(int64_t T, int E) {
-  // About 2 tokens per wave, at most kRtMaxBlocks partial rows.
-  const int per = 2 * topk_threads(vpl_of(E)) / kWave;
-  const int64_t b = (T + per - 1) / per;
+  int64_t b;
+  if (E % 8 == 0 && E <= kGrpMaxExperts) {
+    const int64_t tpw = kWave / group_size(E);
+    b = (T + kGrpWaves * tpw - 1) / (kGrpWaves * tpw);
+    b = std::max(b, std::min<int64_t>(256, (T + tpw - 1) / tpw));
+  } else {
+    const int per = 2 * topk_threads(vpl_of(E)) / kWave;
+    b = (T + per - 1) / per;
+  }
   return (int)std::max<int64_t>(1, std::min<int64_t>(b, kRtMaxBlocks));
 }
 
@@ -519,9 +537,7 @@ extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64
   if (num_experts % 8 == 0 && num_experts <= kGrpMaxExperts && top_k <= 8 &&
       ld_logits % 8 == 0 && reinterpret_cast<uintptr_t>(logits) % 16 == 0 &&
       (!probs || reinterpret_cast<uintptr_t>(probs) % 16 == 0)) {
-    int g = 1;
-    while (8 * g < num_experts) g <<= 1;
-    switch (g) {
+    switch (group_size(num_experts)) {
 #define VMOE_RT_GRP(G)                                                                      \
   case G:                                                                                   \
     hipLaunchKernelGGL(router_topk_group_kernel<G>, dim3(nblk), dim3(kGrpThreads), 0, s,     \
