@@ -12,14 +12,17 @@
 //   DOWN_DW  _grouped_gemm_down_backward_dw_kernel   (grouped_gemm.py:1066-1162)
 //
 // Design:
-//  * Persistent grid, one 512-thread workgroup per CU. Each workgroup builds
+//  * Persistent grid, one 768-thread workgroup per CU. Each workgroup builds
 //    the per-expert work table (tiles x K chunks, exclusive prefix) in LDS
 //    from the same metadata the reference reads, so no host sync is needed
-//    and empty experts cost nothing. XCD x owns a contiguous eighth of the
-//    work items (the tiles of one expert share that XCD's L2); its
-//    workgroups take every (grid / 8)-th item.
-//  * 8 waves in a 2x4 grid over a 256x256 tile, 128x64 fp32 accumulators
-//    per wave, two waves per SIMD.
+//    and empty experts cost nothing. Row-tiled GEMMs: XCD x owns a
+//    contiguous eighth of the work items (the tiles of one expert share that
+//    XCD's L2) and its workgroups take every (grid / 8)-th item. dW GEMMs:
+//    lanes of kLane workgroups on one XCD take contiguous item ranges (see
+//    item_range).
+//  * 128x256 output tiles; 8 consumer waves in a 2x4 grid, 64x64 fp32
+//    accumulators per wave (two consumer waves per SIMD), and 4 producer
+//    waves that issue every DMA.
 //  * Every operand tile goes global -> LDS by DMA (buffer_load ... lds, 16
 //    bytes per lane), never through VGPRs, in a 4-stage ring; the k-tiles of
 //    all items of a workgroup form one stream, so the next item's first
