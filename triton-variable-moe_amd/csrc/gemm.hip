@@ -955,9 +955,32 @@ struct Gemm {
           }
   }
 
+  // DOWN_DH with pre: the PRE values unit I of the pending tile combines
+  // with, loaded a few k-steps before its flush so the load latency does not
+  // stall the wave (and with it the next barrier) at every flush.
+  template <int I>
+  __device__ __forceinline__ static void load_pre(const Args& p, const Pending& pd,
+                                                  uint4 (&pr)[4]) {
+    if constexpr (V == DOWN_DH) {
+      if (!p.pre) return;
+      int lane = threadIdx.x & 63;
+      asm volatile("" : "+v"(lane));
+      const int mb = pd.mb + I * 32;
+      const int n = pd.nb + 8 * (lane & 7);
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int m = mb + 8 * qq + (lane >> 3);
+        pr[qq] = make_uint4(0, 0, 0, 0);
+        if (m < pd.M && n < pd.N)
+          pr[qq] = *reinterpret_cast<const uint4*>(p.pre + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n);
+      }
+    }
+  }
+
   // Stores block (OUT, I) of the pending tile: rows pd.mb + 32 I .. +31.
   template <int OUT, int I>
-  __device__ __forceinline__ static void flush_unit(const Args& p, const Pending& pd, lds_char* scr) {
+  __device__ __forceinline__ static void flush_unit(const Args& p, const Pending& pd, lds_char* scr,
+                                                    const uint4 (&pr)[4]) {
     // The lane index is made opaque so that this lane-only address math is
     // recomputed here instead of being hoisted out of the k-loop, where it
     // would stay live (and spill) across the MFMAs.
@@ -969,16 +992,7 @@ struct Gemm {
     const bool n_ok = n < pd.N;
     if (V == DOWN_DH && p.pre) {
       // GA = bf16(pre > 0 ? 2 * GH * pre : 0), GH the bf16-rounded dH
-      // (grouped_gemm.py:751-766). PRE is read for all four row groups
-      // before any is used.
-      uint4 pr[4];
-#pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int m = mb + 8 * qq + (lane >> 3);
-        pr[qq] = make_uint4(0, 0, 0, 0);
-        if (m < pd.M && n_ok)
-          pr[qq] = *reinterpret_cast<const uint4*>(p.pre + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n);
-      }
+      // (grouped_gemm.py:751-766), with PRE from load_pre.
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const uint4 gh = epi_read(scr, qq, lane);
@@ -1010,8 +1024,9 @@ struct Gemm {
 
   // Stores unit U of the pending tile if it is still pending.
   template <int U>
-  __device__ __forceinline__ static void flush_slot(const Args& p, Pending& pd, lds_char* scr) {
-    if (pd.mask & (1 << U)) flush_unit<U / FM, U % FM>(p, pd, scr);
+  __device__ __forceinline__ static void flush_slot(const Args& p, Pending& pd, lds_char* scr,
+                                                    const uint4 (&pr)[4]) {
+    if (pd.mask & (1 << U)) flush_unit<U / FM, U % FM>(p, pd, scr, pr);
   }
 
   // Partial tiles travel between XCDs, whose L2s are not coherent with one
@@ -1266,6 +1281,11 @@ struct Gemm {
     f32x16_t acc[FM][FN];
     Pending pd;
     pd.mask = 0;
+    uint4 pr[4];  // DOWN_DH: PRE of the next unit to flush
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) pr[qq] = make_uint4(0, 0, 0, 0);
+    // Units flush kLead k-steps after their PRE loads are issued.
+    constexpr int kLead = V == DOWN_DH ? 2 : 0;
     for (int item = rg.beg; item < rg.end; item += rg.stride) {
       const Work w = decode(p, mt, item, ec, rg.slot);
       if (w.skip) continue;
@@ -1291,17 +1311,19 @@ struct Gemm {
       // which keeps their registers for the accumulators.
       const int gap = max(1, w.nk / UNITS);
       int kt = 0;
+      if (pd.mask & 1) load_pre<0>(p, pd, pr);
 #pragma unroll
       for (int u = 0; u < (Cfg<V>::contig ? 0 : UNITS); ++u) {
-        const int at = min(u * gap, w.nk - 1);
+        const int at = min(u * gap + kLead, w.nk - 1);
         for (; kt <= at; ++kt, ++s) {
           block_barrier();
           compute(ring + (s % kStages) * STAGE, acc);
         }
-        if (u == 0) flush_slot<0>(p, pd, scr);
-        if (u == 1) flush_slot<1>(p, pd, scr);
-        if (u == 2) flush_slot<2 % UNITS>(p, pd, scr);
-        if (u == 3) flush_slot<3 % UNITS>(p, pd, scr);
+        if (u == 0) flush_slot<0>(p, pd, scr, pr);
+        if (u == 1) flush_slot<1>(p, pd, scr, pr);
+        if (u == 2) flush_slot<2 % UNITS>(p, pd, scr, pr);
+        if (u == 3) flush_slot<3 % UNITS>(p, pd, scr, pr);
+        if (V == DOWN_DH && u == 0 && (pd.mask & 2)) load_pre<1 % FM>(p, pd, pr);
       }
       pd.mask = 0;
       for (; kt < w.nk; ++kt, ++s) {
@@ -1319,8 +1341,8 @@ struct Gemm {
           stash(p, w, acc, pd, kScaled && p.row_scale && w.nk > 0 ? scl + slot * (BM * 4)
                                                                   : nullptr);
           if (Cfg<V>::contig) {
-            flush_slot<0>(p, pd, scr);
-            flush_slot<1>(p, pd, scr);
+            flush_slot<0>(p, pd, scr, pr);
+            flush_slot<1>(p, pd, scr, pr);
             pd.mask = 0;
           }
         }
@@ -1328,11 +1350,13 @@ struct Gemm {
       }
     }
     // The last tile has no next item to hide behind.
-    flush_slot<0>(p, pd, scr);
-    flush_slot<1>(p, pd, scr);
+    if (pd.mask & 1) load_pre<0>(p, pd, pr);
+    flush_slot<0>(p, pd, scr, pr);
+    if (V == DOWN_DH && (pd.mask & 2)) load_pre<1 % FM>(p, pd, pr);
+    flush_slot<1>(p, pd, scr, pr);
     if (UNITS > 2) {
-      flush_slot<2 % UNITS>(p, pd, scr);
-      flush_slot<3 % UNITS>(p, pd, scr);
+      flush_slot<2 % UNITS>(p, pd, scr, pr);
+      flush_slot<3 % UNITS>(p, pd, scr, pr);
     }
   }
 
