@@ -14,7 +14,8 @@ both dW GEMMs).
 
 Prints one JSON line: value = grouped-GEMM TFLOP/s of the whole step
 (12 * d * sum_e n_e * w_e over the step's wall time), plus ms_per_step, the
-per-kernel breakdown (HIP events on the launch stream), the roofline of the
+per-kernel breakdown (HIP events around each launch inside real steps, on the
+launch stream), the roofline of the
 dominant kernel and the CPU baseline (the fp32 eager per-expert-loop oracle on
 the host cores).
 """
@@ -50,7 +51,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
-    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--kernel-steps", type=int, default=10,
+                    help="steps run with a HIP event pair around every launch (per-kernel times)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--profile-steps", type=int, default=0,
@@ -171,8 +173,8 @@ def gemm_flops(m, xb):
     return 12.0 * d * snw, counts, sel
 
 
-def time_steps(m, xb, steps, warmup):
-    import torch
+def make_step(m, xb):
+    """One training step of the layer: forward, loss out.sum(), backward."""
 
     def step():
         m.zero_grad(set_to_none=True)
@@ -180,6 +182,13 @@ def time_steps(m, xb, steps, warmup):
         out, _, _ = m(xb)
         out.sum().backward()
 
+    return step
+
+
+def time_steps(m, xb, steps, warmup):
+    import torch
+
+    step = make_step(m, xb)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -190,98 +199,77 @@ def time_steps(m, xb, steps, warmup):
     return (time.perf_counter() - t0) / steps * 1e3
 
 
-def kernel_breakdown(m, xb, sel, reps):
-    """Average duration of every kernel launch of a step, each timed alone in a
-    loop of `reps` launches between two HIP events on the launch stream."""
+# Entry point -> op name of the per-kernel breakdown; the combine runs twice
+# per step (forward, then the backward gather of dX).
+OP_OF = {
+    "vmoe_router_topk": ("router_topk",),
+    "vmoe_route": ("route",),
+    "vmoe_gemm_up_fwd": ("gemm_up_fwd",),
+    "vmoe_gemm_down_fwd": ("gemm_down_fwd",),
+    "vmoe_combine": ("combine", "gather_bwd_combine"),
+    "vmoe_router_aux": ("router_aux",),
+    "vmoe_gemm_down_bwd_dh": ("gemm_down_bwd_dh_ga",),
+    "vmoe_gemm_up_bwd_dw": ("gemm_up_bwd_dw",),
+    "vmoe_gemm_up_bwd_dx": ("gemm_up_bwd_dx",),
+    "vmoe_gemm_down_bwd_dw": ("gemm_down_bwd_dw",),
+}
+
+
+class LaunchTimer:
+    """HIP events recorded on the current (launch) stream right before and
+    after every C-ABI launch of a step, so each kernel is timed where it runs
+    in the real step (after the kernels that precede it, with their caches
+    and write-backs), not in a loop of its own."""
+
+    def __init__(self):
+        import torch
+
+        self.torch = torch
+        self.marks = []
+        self.seen = {}
+        self.open = None
+
+    def new_step(self):
+        self.seen = {}
+
+    def begin(self, name):
+        e0 = self.torch.cuda.Event(enable_timing=True)
+        e0.record()
+        self.open = e0
+
+    def end(self, name):
+        e1 = self.torch.cuda.Event(enable_timing=True)
+        e1.record()
+        n = self.seen.get(name, 0)
+        self.seen[name] = n + 1
+        ops = OP_OF.get(name, (name,))
+        self.marks.append((ops[min(n, len(ops) - 1)], self.open, e1))
+
+
+def kernel_breakdown(m, xb, steps):
+    """Average duration (us) of each launch of the step, from HIP events
+    around the launches of `steps` real steps (the timed steps run without
+    the events)."""
     import torch
 
-    from triton_moe.kernels import grouped_gemm as gg
-    from triton_moe.kernels.fused_cumsum import route_device
-    from triton_moe.kernels.gather import combine_rows
-
-    k, E, b = m.num_active_experts, m.num_experts, m.block_size
-    d = xb.shape[-1]
-    x = xb.detach().reshape(-1, d)
-    T = x.shape[0]
-    wts = torch.rand(T * k, device=x.device).to(torch.bfloat16)
-    selv = sel.reshape(-1)
-    # the module's launches: pad rows of the row map are -1, the up GEMM and
-    # its dW read the tokens x through it (no gathered copy of x), the up
-    # GEMM scales H by each row's routing weight (row_weight), so the combine
-    # is unweighted and the dH / dW2 GEMMs read the output gradient G through
-    # the map. G is the step's: the gradient of out.sum(), one broadcast row.
-    r = route_device(selv, E, k, b, map_pad=-1, weights=wts)
-    meta = gg.GemmMeta(r.expert_offsets, m.expert_weight_offsets_t, m.expert_widths_t,
-                       r.padded_counts, E, m.max_expert_width, r.rows_bound)
-    gm, rw = r.gather_map, r.row_weight
-    h, pre = gg.up_fwd(x, m.w1.detach(), meta, 1, True, False, gather_map=gm, row_scale=rw)
-    y = gg.down_fwd(h, m.w2.detach(), meta, d)
-    G1 = torch.ones(1, d, dtype=torch.bfloat16, device=x.device)  # ld 0: one row for all
-    w1, w2 = m.w1.detach(), m.w2.detach()
-    ga, _ = gg.down_bwd(G1.expand(T, d), h, w2, meta, d, False, pre=pre, gather_map=gm,
-                        row_scale=rw)
-    gxg, _ = gg.up_bwd_from_ga(ga, x, w1, meta, d, gm)
-    ws = gg._dw_workspace(meta, d, x.device)
     from triton_moe import _lib
 
-    def dx_only():
-        gx = torch.empty(meta.rows, d, dtype=torch.bfloat16, device=x.device)
-        _lib.call("vmoe_gemm_up_bwd_dx", ga.data_ptr(), ga.stride(0), w1.data_ptr(),
-                  w1.stride(0), gx.data_ptr(), gx.stride(0), *gg._meta_args(meta), d,
-                  meta.max_width, meta.rows, _lib.stream(x.device))
-
-    def dw1_only():
-        # as the module calls it: A = the tokens x through the row map
-        gw = torch.empty_like(w1)
-        _lib.call("vmoe_gemm_up_bwd_dw", x.data_ptr(), x.stride(0), T, gm.data_ptr(),
-                  ga.data_ptr(), ga.stride(0), gw.data_ptr(), gw.stride(0),
-                  *gg._meta_args(meta), d, meta.max_width, meta.rows, ws.data_ptr(), ws.numel(),
-                  _lib.stream(x.device))
-
-    def dh_only():
-        o = torch.empty(meta.rows, meta.max_width, dtype=torch.bfloat16, device=x.device)
-        _lib.call("vmoe_gemm_down_bwd_dh", G1.data_ptr(), 0, T, gm.data_ptr(), w2.data_ptr(),
-                  w2.stride(0), pre.data_ptr(), rw.data_ptr(), o.data_ptr(), o.stride(0),
-                  *gg._meta_args(meta), d, meta.max_width, meta.rows, _lib.stream(x.device))
-
-    def dw2_only():
-        gw = torch.empty_like(w2)
-        _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), G1.data_ptr(), 0, T,
-                  gm.data_ptr(), gw.data_ptr(), gw.stride(0), *gg._meta_args(meta), d,
-                  meta.max_width, meta.rows, ws.data_ptr(), ws.numel(), _lib.stream(x.device))
-
-    from triton_moe.kernels.router import router_topk
-
-    with torch.no_grad():
-        logits = m.router(x)
-
-    ops = {
-        "router_topk": lambda: router_topk(logits, k, m.norm_topk_prob),
-        "route": lambda: route_device(selv, E, k, b, map_pad=-1, weights=wts),
-        "gemm_up_fwd": lambda: gg.up_fwd(x, w1, meta, 1, True, False, gather_map=gm,
-                                         row_scale=rw),
-        "gemm_down_fwd": lambda: gg.down_fwd(h, w2, meta, d),
-        "combine": lambda: combine_rows(y, r.assignment_row, k, T),
-        "gemm_down_bwd_dh_ga": dh_only,
-        "gemm_down_bwd_dw": dw2_only,
-        "gemm_up_bwd_dx": dx_only,
-        "gemm_up_bwd_dw": dw1_only,
-        "gather_bwd_combine": lambda: combine_rows(gxg, r.assignment_row, k, T),
-    }
-    out = {}
-    stream = torch.cuda.current_stream()
-    for name, fn in ops.items():
-        fn()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            fn()
-        e1.record(stream)
-        e1.synchronize()
-        out[name] = e0.elapsed_time(e1) / reps * 1e3  # microseconds
-    return out
+    step = make_step(m, xb)
+    step()
+    timer = LaunchTimer()
+    _lib.set_launch_timer(timer)
+    try:
+        for _ in range(steps):
+            timer.new_step()
+            step()
+    finally:
+        _lib.set_launch_timer(None)
+    torch.cuda.synchronize()
+    tot, cnt = {}, {}
+    for op, e0, e1 in timer.marks:
+        tot[op] = tot.get(op, 0.0) + e0.elapsed_time(e1) * 1e3
+        cnt[op] = cnt.get(op, 0) + 1
+    return {op: tot[op] / cnt[op] for op in tot}
 
 
 def cpu_baseline(m, xb, sel, iters):
@@ -356,7 +344,7 @@ def main():
 
     ms = time_steps(m, xb, args.steps, args.warmup)
     value = flops / (ms * 1e-3) / 1e12
-    kern = kernel_breakdown(m, xb, sel, args.kernel_reps)
+    kern = kernel_breakdown(m, xb, args.kernel_steps)
     gemm_names = [n for n in kern if n.startswith("gemm_")]
     gemm_us = sum(kern[n] for n in gemm_names)
     per_gemm_flops = flops / 6.0

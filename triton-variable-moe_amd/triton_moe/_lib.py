@@ -106,8 +106,26 @@ def check(status: int, what: str) -> None:
         raise RuntimeError(f"{what}: {msg} (status {status})")
 
 
+# Optional observer of every launch (bench.py's per-kernel timing): an object
+# with begin(name) and end(name), called around each entry point on the
+# calling thread; None in normal use.
+_launch_timer = None
+
+
+def set_launch_timer(timer) -> None:
+    global _launch_timer
+    _launch_timer = timer
+
+
 def call(name: str, *args) -> None:
-    check(getattr(lib(), name)(*args), name)
+    timer = _launch_timer
+    if timer is None:
+        check(getattr(lib(), name)(*args), name)
+        return
+    timer.begin(name)
+    status = getattr(lib(), name)(*args)
+    timer.end(name)
+    check(status, name)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
