@@ -95,3 +95,27 @@ def test_check_maps_status_to_exceptions():
     with pytest.raises(RuntimeError):
         _lib.check(_lib.ERR_LAUNCH, "x")
     _lib.check(_lib.OK, "x")
+
+
+def test_launch_timer_sees_every_call():
+    """The observer hook (bench.py's per-launch timing) is called around each
+    entry point, also when the call fails its argument checks."""
+
+    class Rec:
+        def __init__(self):
+            self.log = []
+
+        def begin(self, name):
+            self.log.append(("begin", name))
+
+        def end(self, name):
+            self.log.append(("end", name))
+
+    rec = Rec()
+    _lib.set_launch_timer(rec)
+    try:
+        with pytest.raises(ValueError):
+            _lib.call("vmoe_combine", None, 0, 0, None, None, 0, None, 8, 1, 8, None)
+    finally:
+        _lib.set_launch_timer(None)
+    assert rec.log == [("begin", "vmoe_combine"), ("end", "vmoe_combine")]
