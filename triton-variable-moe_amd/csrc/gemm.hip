@@ -70,7 +70,7 @@ constexpr int kProducers = 4;
 constexpr int kWaves = kConsumers + kProducers;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxExperts = 2048;  // per-expert work prefix held in LDS
-constexpr int kRecExperts = 512;   // per-expert metadata also held in LDS up to this E
+constexpr int kRecExperts = 256;   // per-expert metadata also held in LDS up to this E
 constexpr int kLane = 8;           // dW GEMMs: workgroups of one XCD that share each K chunk
 
 enum Variant { UP_FWD = 0, DOWN_FWD, UP_DX, UP_DW, DOWN_DH, DOWN_DW };
@@ -419,7 +419,29 @@ struct Gemm {
   static constexpr int FM = WM / 32, FN = WN / 32;    // 32x32 blocks per wave
   static constexpr int A_STAGE = BM * BK * 2, B_STAGE = BN * BK * 2;  // bytes
   static constexpr int STAGE = A_STAGE + B_STAGE;
-  static constexpr int RING = kStages * STAGE;
+  // The GEMMs that store a [rows, d] output (DOWN_FWD, UP_DX) stage their
+  // K-contiguous A operand two k-steps at a time: one 128-byte request per
+  // row instead of two 64-byte ones, which halves the address-queue slots
+  // those loads take from the epilogue stores (2-3 us each at cfg3; the
+  // other row-tiled GEMMs gain nothing from it). A pair slot holds blocks of 8 rows, each the 8 rows' 64 bytes of
+  // the even k-step, then of the odd one; kPairSlots slots keep the ring's
+  // lookahead (a pair is refilled kStages - 1 stages ahead, as one stage
+  // is). Items then have an even number of k-steps (an odd one gets a k-step
+  // of zeros), so pairs never straddle items. The ring is the A pair slots,
+  // then kStages B stages; otherwise kStages stages of A then B.
+  static constexpr bool PAIR_A = V == DOWN_FWD || V == UP_DX;
+  static constexpr int kPairSlots = 3;
+  static constexpr int A_RING = PAIR_A ? kPairSlots * 2 * A_STAGE : 0;
+  static constexpr int RING = PAIR_A ? A_RING + kStages * B_STAGE : kStages * STAGE;
+  template <typename P>
+  __device__ static P* a_at(P* ring, int s) {
+    return PAIR_A ? ring + ((s >> 1) % kPairSlots) * (2 * A_STAGE) : ring + (s % kStages) * STAGE;
+  }
+  template <typename P>
+  __device__ static P* b_at(P* ring, int s) {
+    return PAIR_A ? ring + A_RING + (s % kStages) * B_STAGE
+                  : ring + (s % kStages) * STAGE + A_STAGE;
+  }
   // DMA instructions per producer wave per stage for an operand of R rows/cols.
   template <int R>
   struct Dma {
@@ -432,6 +454,7 @@ struct Gemm {
   };
   static constexpr int PWA = Dma<BM>::PW, PWB = Dma<BN>::PW;
   static constexpr int PT = PWA + PWB;  // DMA instructions per stage per producer thread
+  static constexpr int PWA_S = PAIR_A ? 2 * PWA : PWA;  // A DMAs per issue (a pair: two stages)
   __device__ static int pwave() { return (threadIdx.x >> 6) - kConsumers; }
 
   // LDS address of this wave's first DMA slot of an operand stage, uniform:
@@ -501,7 +524,7 @@ struct Gemm {
 
   // K-form setup: rows [0, R) of the tile (source rows r0 + row, or
   // map[r0 + row]), rows_valid of them real, k measured from column c0.
-  template <int R, int PW>
+  template <int R, int PW, bool PAIR>
   __device__ static void setup_k(Src<PW>& s, const uint16_t* base, int64_t ld,
                                  const int32_t* map, int64_t map_rows, int64_t r0, int64_t c0,
                                  int rows_valid, const lds_char* win) {
@@ -513,30 +536,33 @@ struct Gemm {
     s.ld2 = (uint32_t)(ld * 2);
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-      const int row = (wave * PW + i) * KRPI + lane / KCH;
-      const int c = (lane % KCH) ^ kswz(row);
+      // PAIR: instruction i covers rows 8 (wave PW + i) .. +7; lanes 0-31
+      // the even k-step's 64 bytes of them, lanes 32-63 the odd one's.
+      const int lr = PAIR ? i * 8 + ((lane & 31) >> 2) : i * KRPI + lane / KCH;  // wave-local row
+      const int row = wave * (PAIR ? PW * 8 : PW * KRPI) + lr;
+      const int c = PAIR ? (lane & 3) ^ ((row >> 2) & 3) : (lane % KCH) ^ kswz(row);
+      const int k = PAIR ? (lane >> 5) * BK + c * 8 : c * 8;
       bool ok = row < rows_valid;
       int64_t srow = row;
       if (T::k_map && map && ok) {
         // One entry per lane, once per item (the K-form rows are fixed for
         // all of the item's k-tiles), from the wave's map window.
-        srow = reinterpret_cast<const __attribute__((address_space(3))) int32_t*>(
-            win)[i * KRPI + lane / KCH];
+        srow = reinterpret_cast<const __attribute__((address_space(3))) int32_t*>(win)[lr];
         ok = srow >= 0 && srow < map_rows;
       }
       s.ok[i] = ok;
-      s.idx[i] = c * 8;
-      s.off[i] = ok ? (uint32_t)((srow * ld + c * 8) * 2) : kOob;
+      s.idx[i] = k;
+      s.off[i] = ok ? (uint32_t)((srow * ld + k) * 2) : kOob;
     }
   }
 
   // K-form issue: stage tile k0 .. k0 + BK (k0 relative to the setup's c0).
   // Invalid rows hold offset kOob, which stays out of range after adding k0
   // (offsets are below 2^31), so a stage inside K needs one add per DMA.
-  template <int R, int PW>
+  template <int R, int PW, bool PAIR>
   __device__ static void issue_k(const Src<PW>& s, int k0, int K, lds_char* stage) {
     const uint32_t m0 = lds_slot<PW>(stage);
-    if (k0 + BK <= K) {
+    if (k0 + (PAIR ? 2 * BK : BK) <= K) {
 #pragma unroll
       for (int i = 0; i < PW; ++i) dma16(s.rsrc, s.off[i] + (uint32_t)(k0 * 2), m0 + i * 1024);
       return;
@@ -664,6 +690,16 @@ struct Gemm {
   }
 
   // MFMA fragment of rows [row0, row0 + 32) x k-step ks (16 deep).
+  // Fragment of rows [row0, row0 + 32) x k-step ks of half h of an A pair
+  // slot (the layout setup_k's PAIR mapping writes).
+  __device__ static bf16x8_t frag_kp(const lds_char* pair, int h, int row0, int ks) {
+    const int lane = threadIdx.x & 63;
+    const int row = row0 + (lane & 31);
+    const int c = 2 * ks + (lane >> 5);
+    return *reinterpret_cast<const lds_bf16x8*>(pair + (row >> 3) * 1024 + h * 512 +
+                                                (row & 7) * 64 + ((c ^ ((row >> 2) & 3)) << 4));
+  }
+
   __device__ static bf16x8_t frag_k(const lds_char* stage, int row0, int ks) {
     const int lane = threadIdx.x & 63;
     const int row = row0 + (lane & 31);
@@ -773,6 +809,7 @@ struct Gemm {
     }
     w.klen = K - w.kbeg;
     w.nk = w.klen > 0 && !w.skip ? cdiv(w.klen, BK) : 0;
+    if (PAIR_A) w.nk = (w.nk + 1) & ~1;  // pairs of k-steps
     return w;
   }
 
@@ -790,44 +827,52 @@ struct Gemm {
     tm.on = true;
   }
 
-  __device__ static void setup(const Args& p, const Work& w, Src<PWA>& sa, Src<PWB>& sb,
+  __device__ static void setup(const Args& p, const Work& w, Src<PWA_S>& sa, Src<PWB>& sb,
                                TMap& tm) {
     const Prob& q = w.q;
-    if (T::a_k)
-      setup_k<BM>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.m0, q.ac + w.kbeg, q.M - w.m0,
-                  tm.win);
+    if constexpr (T::a_k)
+      setup_k<BM, PWA_S, PAIR_A>(sa, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.m0, q.ac + w.kbeg,
+                                 q.M - w.m0, tm.win);
     else
       setup_t<BM, PWA, T::t_map>(sa, tm, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.kbeg,
                                  q.ac + w.m0, q.M - w.m0, w.klen, !T::t_map_b);
     if (T::b_k)
-      setup_k<BN>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg, q.N - w.n0, nullptr);
+      setup_k<BN, PWB, false>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg, q.N - w.n0,
+                              nullptr);
     else
       setup_t<BN, PWB, T::t_map_b>(sb, tm, p.b, p.ldb, p.b_map, p.b_rows, q.br + w.kbeg,
                                    q.bc + w.n0, q.N - w.n0, w.klen, T::t_map_b);
   }
 
-  __device__ static void issue(const Work& w, const Src<PWA>& sa, const Src<PWB>& sb,
-                               TMap& tm, int kt, lds_char* st) {
+  // Issues k-step kt of item w as global stage s (A of a pair: on even kt).
+  __device__ static void issue(const Work& w, const Src<PWA_S>& sa, const Src<PWB>& sb,
+                               TMap& tm, int kt, lds_char* ring, int s) {
     const int k0 = kt * BK;
-    if (T::a_k) issue_k<BM>(sa, k0, w.klen, st); else issue_t<BM, PWA, T::t_map>(sa, tm, kt, w.klen, st);
-    if (T::b_k) issue_k<BN>(sb, k0, w.klen, st + A_STAGE);
-    else issue_t<BN, PWB, T::t_map_b>(sb, tm, kt, w.klen, st + A_STAGE);
+    if constexpr (T::a_k) {
+      if (!PAIR_A || (kt & 1) == 0) issue_k<BM, PWA_S, PAIR_A>(sa, k0, w.klen, a_at(ring, s));
+    } else {
+      issue_t<BM, PWA, T::t_map>(sa, tm, kt, w.klen, a_at(ring, s));
+    }
+    if (T::b_k) issue_k<BN, PWB, false>(sb, k0, w.klen, b_at(ring, s));
+    else issue_t<BN, PWB, T::t_map_b>(sb, tm, kt, w.klen, b_at(ring, s));
   }
 
   // Multiplies one staged k-tile into the wave's accumulators.
-  __device__ static void compute(const lds_char* cur, f32x16_t (&acc)[FM][FN]) {
+  __device__ static void compute(const lds_char* ring, int s, f32x16_t (&acc)[FM][FN]) {
     const int wave = threadIdx.x >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
+    const lds_char* ca = a_at(ring, s);
+    const lds_char* cb = b_at(ring, s);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_t af[FM], bfr[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[i] = T::a_k ? frag_k(cur, wm * WM + i * 32, ks) : frag_t<BM>(cur, wm * WM + i * 32, ks);
+        af[i] = PAIR_A ? frag_kp(ca, s & 1, wm * WM + i * 32, ks)
+                : T::a_k ? frag_k(ca, wm * WM + i * 32, ks) : frag_t<BM>(ca, wm * WM + i * 32, ks);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = T::b_k ? frag_k(cur + A_STAGE, wn * WN + j * 32, ks)
-                        : frag_t<BN>(cur + A_STAGE, wn * WN + j * 32, ks);
+        bfr[j] = T::b_k ? frag_k(cb, wn * WN + j * 32, ks) : frag_t<BN>(cb, wn * WN + j * 32, ks);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1153,7 +1198,7 @@ struct Gemm {
                                       lds_char* scl, const Meta& mt, const Range& rg) {
     int ei = 0, ela = 0;
     Work wi;
-    Src<PWA> sa;
+    Src<PWA_S> sa;
     Src<PWB> sb;
     TMap tm;
     const bool mapped = ((T::t_map || T::k_map) && p.a_map) || (T::t_map_b && p.b_map);
@@ -1237,31 +1282,39 @@ struct Gemm {
     // Issues the stream's next stage into `st`; after an item's last stage
     // the next item is set up right away, so that work runs before the next
     // wait instead of between a barrier and the DMAs it would delay.
-    auto issue_one = [&](lds_char* st) {
+    auto issue_one = [&]() {
       if (!have) return;
       if (mapped && ikt == 0 && win_stage > done) wait_vmcnt<0>();  // window not yet in LDS
-      issue(wi, sa, sb, tm, ikt, st);
+      issue(wi, sa, sb, tm, ikt, ring, issued);
       ++issued;
       if (++ikt >= wi.nk) have = advance();
     };
 #pragma unroll
-    for (int s = 0; s < kStages - 1; ++s) issue_one(ring + s * STAGE);
+    for (int s = 0; s < kStages - 1; ++s) issue_one();
     // One barrier per issued stage, as the consumers take one per stage.
     for (int s = 0; s < issued; ++s) {
       // Stages s+1 .. issued-1 may still be in flight: wait until only
       // their DMAs are outstanding (loads complete in order), sync (the
       // consumers then read stage s), and refill the buffer the consumers
       // read in the previous step, which every wave has left by now.
+      // With A pairs an even stage issues 2 PWA + PWB DMAs and an odd one
+      // PWB, so two consecutive stages still issue 2 PT.
       const int after = issued - 1 - s;
-      if (after >= 2)
+      if (after >= 2) {
         wait_vmcnt<2 * PT>();
-      else if (after == 1)
-        wait_vmcnt<PT>();
-      else
+      } else if (after == 1) {
+        if (!PAIR_A)
+          wait_vmcnt<PT>();
+        else if ((s & 1) == 1)
+          wait_vmcnt<2 * PWA + PWB>();  // stage s + 1 is even
+        else
+          wait_vmcnt<PWB>();
+      } else {
         wait_vmcnt<0>();
+      }
       done = s;
       block_barrier();
-      issue_one(ring + ((s + kStages - 1) % kStages) * STAGE);
+      issue_one();
     }
   }
 
@@ -1317,7 +1370,7 @@ struct Gemm {
         const int at = min(u * gap + kLead, w.nk - 1);
         for (; kt <= at; ++kt, ++s) {
           block_barrier();
-          compute(ring + (s % kStages) * STAGE, acc);
+          compute(ring, s, acc);
         }
         if (u == 0) flush_slot<0>(p, pd, scr, pr);
         if (u == 1) flush_slot<1>(p, pd, scr, pr);
@@ -1328,7 +1381,7 @@ struct Gemm {
       pd.mask = 0;
       for (; kt < w.nk; ++kt, ++s) {
         block_barrier();
-        compute(ring + (s % kStages) * STAGE, acc);
+        compute(ring, s, acc);
       }
       const bool last_chunk = w.chunk == w.chunks - 1;
       if (rg.stride != 1 || last_chunk || item + 1 >= rg.end) {
