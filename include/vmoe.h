@@ -119,6 +119,15 @@ int vmoe_row_maps(const int32_t* indices, const int32_t* bin_ids, const int32_t*
  *   + (g_lb coef_e f_e + g_cl wn_e) / T p (1 - p)); g_* are device fp32
  *   scalars (nullable = 0). The top-k weights get no gradient (scatter.py:176).
  * ---------------------------------------------------------------------- */
+/* Router logits: logits[T, E] = bf16(x[T, hidden] @ weight[E, hidden]^T), fp32
+ * accumulation (nn.Linear(n_embd, num_experts, bias=False), triton_moe/moe.py:78
+ * and its call at moe.py:166). Supports E % 8 == 0, E <= 128, hidden % 256 == 0,
+ * 16-byte aligned x / weight rows and 8-byte aligned logits rows; other shapes
+ * return VMOE_ERR_UNSUPPORTED (the caller's own linear layer covers them). */
+int vmoe_router_logits(const uint16_t* x, int64_t ldx, int64_t num_tokens, int64_t hidden,
+                       const uint16_t* weight, int64_t ldw, int32_t num_experts,
+                       uint16_t* logits, int64_t ld_logits, vmoe_stream_t stream);
+
 size_t vmoe_router_partial_floats(int64_t num_tokens, int32_t num_experts);
 int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
                      int32_t num_experts, int32_t top_k, int32_t normalize, uint16_t* weights,

@@ -73,6 +73,9 @@ def test_argument_checks_return_invalid_arg():
     assert lib.vmoe_router_topk(1, 8, 4, 8, 2, 1, 1, 1, None, None, 1, 1, 0, None,
                                 None) == _lib.ERR_WORKSPACE
     assert lib.vmoe_router_partial_floats(16384, 64) % 65 == 0
+    # router logits: ld below the row is invalid; E % 8 != 0 is unsupported
+    assert lib.vmoe_router_logits(1, 32, 4, 64, 1, 64, 8, 1, 8, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_router_logits(16, 256, 4, 256, 16, 256, 7, 8, 8, None) == _lib.ERR_UNSUPPORTED
     assert lib.vmoe_router_aux(None, 1, 4, 8, None, None, None, None, None, None, None, None,
                                None) == _lib.ERR_INVALID_ARG
     # unaligned hidden size is unsupported, not silently wrong

@@ -15,7 +15,7 @@ import torch
 
 from oracle import eager
 from triton_moe import TritonMoEConfig, TritonMoEMLP
-from triton_moe.kernels.router import load_balance_coef, router_topk
+from triton_moe.kernels.router import RouterLinear, load_balance_coef, router_topk
 
 from _util import LOOSE, assert_close_norm, bits_equal, make_problem
 
@@ -158,3 +158,34 @@ def test_router_deterministic(device):
     b = router_topk(L, 8, True)
     assert torch.equal(a.selected, b.selected) and bits_equal(a.weights, b.weights)
     assert torch.equal(a.partial, b.partial) and torch.equal(a.lse, b.lse)
+
+
+@pytest.mark.parametrize("T,d,E", [(16384, 1024, 64), (1000, 768, 8), (333, 2048, 128),
+                                   (512, 256, 16), (97, 512, 24), (64, 64, 8), (4096, 768, 7)])
+def test_router_linear(T, d, E, device):
+    """RouterLinear = nn.Linear(d, E, bias=False): the kernel's logits are one
+    bf16 rounding of the fp32 product (E = 7 is outside the kernel's shapes and
+    runs nn.Linear's own path); gradients as the linear layer's; forward hooks
+    still apply."""
+    g = torch.Generator().manual_seed(T + d + E)
+    x = torch.randn(T, d, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, d, generator=g) * 0.05).to(torch.bfloat16)
+    lin = RouterLinear(d, E, bias=False).to(device).to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(w)
+    xd = x.to(device).requires_grad_(True)
+    out = lin(xd)
+    assert out.shape == (T, E) and out.dtype == torch.bfloat16
+    ref = x.float() @ w.float().t()
+    bound = ref.abs() * 2.0 ** -8 + (x.float().abs() @ w.float().abs().t()) * 2.0 ** -20
+    assert bool(((out.float().cpu() - ref).abs() <= bound).all())
+    gout = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    out.backward(gout.to(device))
+    assert_close_norm(xd.grad, gout.float() @ w.float(), LOOSE, "router x.grad")
+    assert_close_norm(lin.weight.grad, gout.float().t() @ x.float(), LOOSE, "router weight.grad")
+    h = lin.register_forward_hook(lambda mod, inp, o: o + 1.0)
+    with torch.no_grad():
+        assert torch.equal(lin(xd), (out + 1.0).detach())
+    h.remove()
+    # a [B, S, d] input keeps its leading shape
+    assert lin(xd.detach().reshape(1, T, d)).shape == (1, T, E)

@@ -507,6 +507,124 @@ inline int router_blocks(int64_t T, int E) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(b, kRtMaxBlocks));
 }
 
+// Router logits L = bf16(x W^T) (nn.Linear without bias) for E <= 32 NT
+// experts: a workgroup takes 32 tokens and its 4 waves split K into quarters.
+// A wave walks its quarter in chunks of 64 k (one 128-byte line per row):
+// global loads of 8 rows x 128 bytes per instruction (the next chunk's in
+// registers while the current one is used), a wave-private swizzled LDS copy
+// (chunk c of row r at c ^ ((r >> 1) & 7): conflict-free 16-lane phases both
+// ways), then v_mfma_f32_32x32x16_bf16 with the expert rows as the first
+// operand (each lane then holds 4 consecutive experts of one token). Rows
+// past T or E read a valid row and their results are never stored. Waves 1-3
+// leave their partial sums in LDS; wave 0 adds them in wave order and rounds
+// once.
+typedef __bf16 rl_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float rl_f32x16 __attribute__((ext_vector_type(16)));
+constexpr int kRlThreads = 256;
+constexpr int kRlWaves = kRlThreads / kWave;
+constexpr int kRlTokens = 32;
+constexpr int kRlChunk = 64;  // k per chunk: 128 bytes of a row
+typedef __attribute__((address_space(3))) char rl_lds;
+typedef uint32_t rl_u32x4 __attribute__((ext_vector_type(4)));
+
+template <int NT>
+__global__ __launch_bounds__(kRlThreads) void router_logits_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t T, int K, const uint16_t* __restrict__ w,
+    int64_t ldw, int E, uint16_t* __restrict__ out, int64_t ldo) {
+  constexpr int XI = kRlTokens / 8, WI = 32 * NT / 8;  // load instructions per chunk
+  __shared__ __align__(16) char stage[kRlWaves][(kRlTokens + 32 * NT) * 128];
+  __shared__ float red[kRlWaves - 1][NT][16][kWave];
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  const int64_t t0 = (int64_t)blockIdx.x * kRlTokens;
+  const int kq = K / kRlWaves;
+  const int k0 = wv * kq;
+  // Loads: instruction u covers rows 8u .. 8u + 7, lane -> (row 8u + lane/8, 16 bytes lane%8).
+  const rl_u32x4* xs[XI];
+  const rl_u32x4* ws[WI];
+#pragma unroll
+  for (int u = 0; u < XI; ++u) {
+    const int64_t t = min(t0 + 8 * u + (lane >> 3), T - 1);
+    xs[u] = reinterpret_cast<const rl_u32x4*>(x + t * ldx + k0) + (lane & 7);
+  }
+#pragma unroll
+  for (int u = 0; u < WI; ++u) {
+    const int e = min(8 * u + (lane >> 3), E - 1);
+    ws[u] = reinterpret_cast<const rl_u32x4*>(w + (int64_t)e * ldw + k0) + (lane & 7);
+  }
+  // An LDS pointer, so the compiler knows these stores cannot touch the
+  // lane's registers-in-memory (a generic pointer keeps xa / wa in scratch).
+  rl_lds* st = (rl_lds*)stage[wv];
+  auto spos = [](int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); };
+  rl_f32x16 acc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
+  rl_u32x4 xa[XI], wa[WI];
+#pragma unroll
+  for (int u = 0; u < XI; ++u) xa[u] = xs[u][0];
+#pragma unroll
+  for (int u = 0; u < WI; ++u) wa[u] = ws[u][0];
+  const int nch = kq / kRlChunk;
+  for (int ch = 0; ch < nch; ++ch) {
+    // the chunk into LDS, then the next chunk's loads
+#pragma unroll
+    for (int u = 0; u < XI; ++u)
+      *reinterpret_cast<__attribute__((address_space(3))) rl_u32x4*>(st + spos(8 * u + (lane >> 3), lane & 7)) = xa[u];
+#pragma unroll
+    for (int u = 0; u < WI; ++u)
+      *reinterpret_cast<__attribute__((address_space(3))) rl_u32x4*>(st + kRlTokens * 128 + spos(8 * u + (lane >> 3), lane & 7)) = wa[u];
+    {
+      // the last chunk reloads itself (unused) so the loads are unconditional
+      const int off = min(ch + 1, nch - 1) * (kRlChunk / 8);  // uint4 per chunk of a row
+#pragma unroll
+      for (int u = 0; u < XI; ++u) xa[u] = xs[u][off];
+#pragma unroll
+      for (int u = 0; u < WI; ++u) wa[u] = ws[u][off];
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int s4 = 0; s4 < kRlChunk / 16; ++s4) {
+      const int c = 2 * s4 + (lane >> 5);
+      const rl_u32x4 a = *reinterpret_cast<const __attribute__((address_space(3))) rl_u32x4*>(st + spos(lane & 31, c));
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const rl_u32x4 b = *reinterpret_cast<const __attribute__((address_space(3))) rl_u32x4*>(
+            st + kRlTokens * 128 + spos(32 * j + (lane & 31), c));
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(rl_bf16x8, b),
+                                                         __builtin_bit_cast(rl_bf16x8, a), acc[j],
+                                                         0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the next chunk overwrites the wave's stage
+  }
+  if (wv > 0) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) red[wv - 1][j][v][lane] = acc[j][v];
+  }
+  __syncthreads();
+  const int64_t t = t0 + (lane & 31);
+  if (wv != 0 || t >= T) return;
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+#pragma unroll
+    for (int w2 = 0; w2 < kRlWaves - 1; ++w2)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[j][v] += red[w2][j][v][lane];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      // experts 32 j + 8 g + 4 (lane / 32) + r, r = 0..3
+      const int e = 32 * j + 8 * g + 4 * (lane >> 5);
+      if (e < E)
+        *reinterpret_cast<uint2*>(out + t * ldo + e) =
+            make_uint2(pack_bf16(acc[j][4 * g], acc[j][4 * g + 1]),
+                       pack_bf16(acc[j][4 * g + 2], acc[j][4 * g + 3]));
+    }
+  }
+}
+
 }  // namespace
 }  // namespace vmoe
 
@@ -626,6 +744,40 @@ extern "C" int vmoe_router_aux_bwd(const uint16_t* logits, int64_t ld_logits, in
     VMOE_RB_CASE(16)
     VMOE_RB_CASE(32)
 #undef VMOE_RB_CASE
+    default:
+      return VMOE_ERR_UNSUPPORTED;
+  }
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_router_logits(const uint16_t* x, int64_t ldx, int64_t num_tokens,
+                                  int64_t hidden, const uint16_t* weight, int64_t ldw,
+                                  int32_t num_experts, uint16_t* logits, int64_t ld_logits,
+                                  vmoe_stream_t stream) {
+  if (num_tokens < 0 || hidden <= 0 || num_experts <= 0 || ldx < hidden || ldw < hidden ||
+      ld_logits < num_experts)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_tokens == 0) return VMOE_OK;
+  if (!x || !weight || !logits) return VMOE_ERR_INVALID_ARG;
+  if (num_experts > 4 * 32 || num_experts % 8 != 0 || hidden % (kRlChunk * kRlWaves) != 0 ||
+      hidden > INT32_MAX || ldx % 8 != 0 || ldw % 8 != 0 || ld_logits % 4 != 0 ||
+      reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(weight) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(logits) % 8 != 0)
+    return VMOE_ERR_UNSUPPORTED;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((num_tokens + kRlTokens - 1) / kRlTokens));
+  switch ((num_experts + 31) / 32) {
+#define VMOE_RL_CASE(N)                                                                   \
+  case N:                                                                                 \
+    hipLaunchKernelGGL(router_logits_kernel<N>, grid, dim3(kRlThreads), 0, s, x, ldx,      \
+                       num_tokens, (int)hidden, weight, ldw, num_experts, logits, ld_logits); \
+    break;
+    VMOE_RL_CASE(1)
+    VMOE_RL_CASE(2)
+    VMOE_RL_CASE(3)
+    VMOE_RL_CASE(4)
+#undef VMOE_RL_CASE
     default:
       return VMOE_ERR_UNSUPPORTED;
   }

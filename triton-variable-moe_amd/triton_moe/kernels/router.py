@@ -18,6 +18,8 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 import torch
+import torch.nn as nn
+import torch.nn.functional as F
 from torch.amp import custom_bwd, custom_fwd
 from torch.autograd.function import once_differentiable
 
@@ -60,6 +62,59 @@ def router_topk(logits: torch.Tensor, top_k: int, normalize: bool = True,
               selected.data_ptr() if is64 else None, _lib.ptr(probs), lse.data_ptr(),
               partial.data_ptr(), nfl, None, _lib.stream(dev))
     return RouterState(weights, selected, probs, lse, partial, rows)
+
+
+def router_logits_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Shapes and layouts vmoe_router_logits takes (bf16 on the GPU, E % 8 == 0,
+    E <= 128, hidden % 256 == 0, contiguous 16-byte aligned rows)."""
+    if not (x.is_cuda and weight.is_cuda and x.dtype == torch.bfloat16 and
+            weight.dtype == torch.bfloat16 and x.dim() >= 1 and weight.dim() == 2):
+        return False
+    E, d = weight.shape
+    return (x.shape[-1] == d and E % 8 == 0 and E <= 128 and d % 256 == 0 and
+            weight.stride(1) == 1 and weight.stride(0) % 8 == 0 and
+            weight.data_ptr() % 16 == 0)
+
+
+class RouterLogitsOp(torch.autograd.Function):
+    """logits = bf16(x @ W^T) on the router-logits kernel; the backward is the
+    linear layer's (two bf16 matmuls with fp32 accumulation)."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, x2d, weight):
+        T, d = x2d.shape
+        E = weight.shape[0]
+        if x2d.stride(1) != 1 or x2d.stride(0) % 8 != 0 or x2d.data_ptr() % 16 != 0:
+            x2d = x2d.contiguous()
+        out = torch.empty(T, E, dtype=torch.bfloat16, device=x2d.device)
+        _lib.call("vmoe_router_logits", x2d.data_ptr(), x2d.stride(0), T, d, weight.data_ptr(),
+                  weight.stride(0), E, out.data_ptr(), out.stride(0), _lib.stream(x2d.device))
+        ctx.save_for_backward(x2d, weight)
+        return out
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, g):
+        x2d, weight = ctx.saved_tensors
+        g = g.contiguous()
+        gx = g @ weight if ctx.needs_input_grad[0] else None
+        gw = g.t().contiguous() @ x2d if ctx.needs_input_grad[1] else None
+        return gx, gw
+
+
+class RouterLinear(nn.Linear):
+    """The router of TritonMoEMLP: nn.Linear(n_embd, num_experts, bias=False)
+    (moe.py:78 of the reference) -- same parameter, initialisation, state-dict
+    key and hooks -- whose forward runs the router-logits kernel on the inputs
+    it supports and is nn.Linear's otherwise."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.bias is None and router_logits_supported(x, self.weight):
+            out = RouterLogitsOp.apply(x.reshape(-1, x.shape[-1]), self.weight)
+            return out.reshape(*x.shape[:-1], out.shape[-1])
+        return F.linear(x, self.weight, self.bias)
 
 
 class RouterAuxOp(torch.autograd.Function):

@@ -35,7 +35,7 @@ from .kernels import (
 )
 from .kernels.fused_cumsum import route_device
 from .kernels.grouped_gemm import GemmMeta, RoutedMoEOp
-from .kernels.router import RouterAuxOp, load_balance_coef, router_topk
+from .kernels.router import RouterAuxOp, RouterLinear, load_balance_coef, router_topk
 
 
 @dataclass
@@ -77,7 +77,7 @@ class TritonMoEMLP(nn.Module):
         self.total_expert_width = self.expert_offsets[-1]
         self.max_expert_width = max(self.expert_widths)
 
-        self.router = nn.Linear(config.n_embd, self.num_experts, bias=False)
+        self.router = RouterLinear(config.n_embd, self.num_experts, bias=False)
         self.w1 = nn.Parameter(torch.empty(config.n_embd, self.total_expert_width))
         self.w2 = nn.Parameter(torch.empty(self.total_expert_width, config.n_embd))
         nn.init.trunc_normal_(self.w1, mean=0.0, std=0.02, a=-0.06, b=0.06)
