@@ -275,11 +275,14 @@ int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
  * [0, gy_rows) read zeros), e.g. the token gradient of the combine, read
  * without materialising its per-row copy. row_scale (nullable, fp32
  * [rows_bound]): grad_h[row] = bf16(row_scale[row] * (grad_y @ W2_e^T)[row])
- * before the relu^2 rule.
+ * before the relu^2 rule. grad_scale (nullable, one bf16 on the device): the
+ * output is scaled by it, so a broadcast gradient c * ones (out.sum(),
+ * out.mean()) is passed as a row of ones (ldgy = 0) and grad_scale = &c.
  * Replaces _grouped_gemm_down_backward_dintermediate_kernel
  * (triton_moe/kernels/grouped_gemm.py:970-1063, launched at 1336-1362). */
 int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64_t gy_rows,
-                          const int32_t* gather_map, const uint16_t* w2, int64_t ldw2,
+                          const int32_t* gather_map, const uint16_t* grad_scale,
+                          const uint16_t* w2, int64_t ldw2,
                           const uint16_t* pre_act, const float* row_scale, uint16_t* grad_h,
                           int64_t ldgh, const int32_t* eto, const int32_t* ewo,
                           const int32_t* widths, const int32_t* tpe, int32_t num_experts,
@@ -288,12 +291,13 @@ int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64_t gy_rows,
 
 /* grad_w2[ewo[e]:+w_e, :] = H_e^T @ grad_y_e; rows of grad_y_e are
  * grad_y[gather_map[row]] when gather_map != NULL (gy_rows, ldgy = 0 and
- * out-of-range entries as for vmoe_gemm_down_bwd_dh), else grad_y[row].
+ * out-of-range entries as for vmoe_gemm_down_bwd_dh), else grad_y[row];
+ * grad_scale as for vmoe_gemm_down_bwd_dh.
  * Replaces _grouped_gemm_down_backward_dw_kernel
  * (triton_moe/kernels/grouped_gemm.py:1066-1162, launched at 1364-1390). */
 int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint16_t* grad_y,
                           int64_t ldgy, int64_t gy_rows, const int32_t* gather_map,
-                          uint16_t* grad_w2, int64_t ldgw, const int32_t* eto,
+                          const uint16_t* grad_scale, uint16_t* grad_w2, int64_t ldgw, const int32_t* eto,
                           const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
                           int32_t num_experts, int64_t hidden, int64_t max_width,
                           int64_t rows_bound, void* workspace, size_t workspace_bytes,

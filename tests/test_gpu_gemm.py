@@ -308,7 +308,7 @@ def test_dw_split_tiles_across_many_lanes(device):
     def dw2(workspace):
         out = torch.full((W, d), float("nan"), dtype=torch.bfloat16, device=device)
         _lib.call("vmoe_gemm_down_bwd_dw", hd.data_ptr(), hd.stride(0), gyd.data_ptr(),
-                  gyd.stride(0), 0, None, out.data_ptr(), out.stride(0),
+                  gyd.stride(0), 0, None, None, out.data_ptr(), out.stride(0),
                   *(t.data_ptr() for t in dev), E, d, max_w, P,
                   None if workspace is None else workspace.data_ptr(),
                   0 if workspace is None else workspace.numel(), _lib.stream(xd.device))

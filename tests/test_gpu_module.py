@@ -92,6 +92,21 @@ def test_forward_backward_vs_oracle(name, device):
     assert m.router.weight.grad is None
 
 
+@pytest.mark.parametrize("name", ["ref_variable", "cfg1"])
+def test_broadcast_gradient_scale(name, device):
+    """A loss c * out.sum() hands the backward a broadcast scalar c: the dH
+    and dW2 GEMMs read a row of ones and scale by c on the device. Held to the
+    oracle with G = c everywhere (c = 0.75, not a power of two)."""
+    m, x, out, aux, f_i, prob = _run(name, device)
+    T, d = prob.x.shape
+    (out.sum() * 0.75).backward()
+    fb = eager.forward(prob, "bf16w")
+    bb = eager.backward(prob, fb, torch.full((T, d), 0.75), "bf16w")
+    for got, key in ((x.grad.reshape(T, d), "grad_x"), (m.w1.grad, "grad_w1"),
+                     (m.w2.grad, "grad_w2")):
+        assert_close_norm(got, bb[key], TIGHT, f"{name} {key} with c = 0.75")
+
+
 def test_aux_losses_and_f_i(device):
     m, x, out, aux, f_i, prob = _run("cfg2", device)
     with torch.no_grad():

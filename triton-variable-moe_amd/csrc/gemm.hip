@@ -89,6 +89,7 @@ struct Args {
   const int32_t* b_map;  // row gather for B (T-form, DOWN_DW), nullable
   int64_t b_rows;        // rows of B's gathered source
   const float* row_scale;  // UP_FWD / DOWN_DH: per-row factor of the output (nullable)
+  const uint16_t* gscale;  // DOWN_DH / DOWN_DW: bf16 scalar factor of the output (nullable)
   const int32_t* eto;
   const int32_t* ewo;
   const int32_t* widths;
@@ -968,6 +969,15 @@ struct Gemm {
               [wm * WM + i * 32 + (threadIdx.x & 31)];
       }
     }
+    if constexpr (V == DOWN_DH || V == DOWN_DW) {
+      // A broadcast output gradient c * ones: the GEMM read the ones row, c
+      // scales the result here.
+      if (p.gscale) {
+        const float gs = bf16_to_f32(*p.gscale);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) sc[i] *= gs;
+      }
+    }
     const Prob& q = w.q;
     pd.mb = w.m0 + wm * WM;
     pd.nb = w.n0 + wn * WN;
@@ -1720,7 +1730,8 @@ extern "C" int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_row
 }
 
 extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64_t gy_rows,
-                                     const int32_t* gather_map, const uint16_t* w2,
+                                     const int32_t* gather_map, const uint16_t* grad_scale,
+                                     const uint16_t* w2,
                                      int64_t ldw2, const uint16_t* pre_act,
                                      const float* row_scale, uint16_t* grad_h, int64_t ldgh,
                                      const int32_t* eto, const int32_t* ewo,
@@ -1742,6 +1753,7 @@ extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64
   p.c = grad_h; p.ldc = ldgh;
   p.pre = pre_act;
   p.row_scale = row_scale;
+  p.gscale = grad_scale;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
   return launch<DOWN_DH>(p, row_items<DOWN_DH>(rows_bound, E, max_width),
@@ -1750,7 +1762,7 @@ extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64
 
 extern "C" int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint16_t* grad_y,
                                      int64_t ldgy, int64_t gy_rows, const int32_t* gather_map,
-                                     uint16_t* grad_w2, int64_t ldgw, const int32_t* eto,
+                                     const uint16_t* grad_scale, uint16_t* grad_w2, int64_t ldgw, const int32_t* eto,
                                      const int32_t* ewo, const int32_t* widths,
                                      const int32_t* tpe, int32_t E, int64_t hidden,
                                      int64_t max_width, int64_t rows_bound, void* workspace,
@@ -1766,6 +1778,7 @@ extern "C" int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint1
   Args p{};
   p.a = h; p.lda = ldh;
   p.b = grad_y; p.ldb = ldgy; p.b_map = gather_map; p.b_rows = gather_map ? gy_rows : 0;
+  p.gscale = grad_scale;
   p.c = grad_w2; p.ldc = ldgw;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;

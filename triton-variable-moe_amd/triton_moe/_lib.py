@@ -43,10 +43,10 @@ _SIGNATURES = {
     "vmoe_gemm_dw_workspace_bytes": [_i32, _i64, _i64, _i64],
     "vmoe_gemm_up_bwd_dw": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp,
                             _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
-    "vmoe_gemm_down_bwd_dh": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp,
-                              _vp, _vp, _i32, _i64, _i64, _i64, _vp],
-    "vmoe_gemm_down_bwd_dw": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
-                              _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
+    "vmoe_gemm_down_bwd_dh": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp,
+                              _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "vmoe_gemm_down_bwd_dw": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+                              _vp, _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
     "vmoe_zero_tail_cols": [_vp, _i64, _vp, _vp, _i32, _i64, _i64, _vp],
     "vmoe_router_logits": [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp],
     "vmoe_router_partial_floats": [_i64, _i32],

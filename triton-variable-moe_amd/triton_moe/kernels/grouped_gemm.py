@@ -302,16 +302,33 @@ def up_bwd(grad_h, x, w1, pre, m: GemmMeta, hidden: int, act: int,
     return up_bwd_from_ga(ga, x, w1, m, hidden, gather_map)
 
 
+_ONES_ROWS: dict[tuple[str, int], torch.Tensor] = {}
+
+
+def _ones_row(d: int, device) -> torch.Tensor:
+    key = (str(device), d)
+    row = _ONES_ROWS.get(key)
+    if row is None:
+        row = _ONES_ROWS[key] = torch.ones(1, d, dtype=torch.bfloat16, device=device)
+    return row
+
+
 def _grad_source(grad_y, m: GemmMeta, gather_map):
-    """(tensor, leading dimension, rows) of the output-gradient operand."""
+    """(tensor, leading dimension, rows, scale) of the output-gradient operand.
+    Read through a row map, a broadcast scalar c (both strides 0: the gradient
+    of out.sum() or out.mean()) becomes a row of ones with ld 0 and the scale
+    c, which the GEMM applies to its output; scale is None otherwise."""
     gy_rows = grad_y.shape[0]
     if gather_map is None:
         grad_y = _bf16(grad_y, "grouped_gemm_down_backward grad_output")
         _need(gy_rows >= m.rows, "grad_output has fewer rows than the padded row count")
-        return grad_y, grad_y.stride(0), gy_rows
+        return grad_y, grad_y.stride(0), gy_rows, None
     _need(gather_map.numel() >= m.rows, "gather_map shorter than the padded row count")
+    if (grad_y.dtype == torch.bfloat16 and gy_rows > 0 and grad_y.stride(0) == 0 and
+            grad_y.stride(1) == 0):
+        return _ones_row(grad_y.shape[1], grad_y.device), 0, gy_rows, grad_y
     g, ld = _token_source(grad_y)
-    return g, ld, gy_rows
+    return g, ld, gy_rows, None
 
 
 def down_bwd_dh(grad_y, w2, m: GemmMeta, hidden: int, zero_tails: bool,
@@ -322,7 +339,7 @@ def down_bwd_dh(grad_y, w2, m: GemmMeta, hidden: int, zero_tails: bool,
     grad_y holds one row per token and row r is grad_y[gather_map[r]] (-1:
     zeros); with row_scale (fp32 per row) the gradient w.r.t. H is scaled by
     it before the relu^2 rule."""
-    g, ldg, g_rows = _grad_source(grad_y, m, gather_map)
+    g, ldg, g_rows, gs = _grad_source(grad_y, m, gather_map)
     w2 = _bf16(w2, "grouped_gemm_down_backward w2")
     _need(w2.shape[1] == hidden and g.shape[1] == hidden,
           "grad_output / w2 do not match hidden_size")
@@ -334,7 +351,7 @@ def down_bwd_dh(grad_y, w2, m: GemmMeta, hidden: int, zero_tails: bool,
     gm = None if gather_map is None else _i32(gather_map)
     if m.rows > 0:
         _lib.call("vmoe_gemm_down_bwd_dh", g.data_ptr(), ldg, g_rows, _lib.ptr(gm),
-                  w2.data_ptr(), w2.stride(0), _lib.ptr(pre),
+                  _lib.ptr(gs), w2.data_ptr(), w2.stride(0), _lib.ptr(pre),
                   _lib.ptr(_f32_rows(row_scale, m.rows, "row_scale")), grad_h.data_ptr(),
                   grad_h.stride(0), *_meta_args(m), hidden, m.max_width, m.rows,
                   _lib.stream(g.device))
@@ -346,7 +363,7 @@ def down_bwd_dh(grad_y, w2, m: GemmMeta, hidden: int, zero_tails: bool,
 def down_bwd_dw(grad_y, h, w2, m: GemmMeta, hidden: int,
                 gather_map: torch.Tensor | None = None):
     """grad_w2 = H_e^T @ grad_y_e (grad_y through gather_map when given)."""
-    g, ldg, g_rows = _grad_source(grad_y, m, gather_map)
+    g, ldg, g_rows, gs = _grad_source(grad_y, m, gather_map)
     h = _bf16(h, "grouped_gemm_down_backward intermediate")
     w2 = _bf16(w2, "grouped_gemm_down_backward w2")
     _need(w2.shape[1] == hidden and g.shape[1] == hidden,
@@ -358,7 +375,7 @@ def down_bwd_dw(grad_y, h, w2, m: GemmMeta, hidden: int,
     dev = g.device
     ws = _dw_workspace(m, hidden, dev)
     _lib.call("vmoe_gemm_down_bwd_dw", h.data_ptr(), h.stride(0), g.data_ptr(), ldg, g_rows,
-              _lib.ptr(gm), grad_w2.data_ptr(), grad_w2.stride(0), *_meta_args(m), hidden,
+              _lib.ptr(gm), _lib.ptr(gs), grad_w2.data_ptr(), grad_w2.stride(0), *_meta_args(m), hidden,
               m.max_width, m.rows, ws.data_ptr(), ws.numel(), _lib.stream(dev))
     return grad_w2
 
@@ -582,10 +599,6 @@ class RoutedMoEOp(torch.autograd.Function):
 
         x_flat, w1, w2, h, pre, gm, rw, ar = ctx.saved_tensors
         m, d = ctx.meta, ctx.hidden_size
-        if grad_out.shape[0] > 0 and grad_out.stride(0) == 0 and grad_out.stride(1) != 1:
-            # A broadcast scalar (the gradient of out.sum()): both GEMMs read
-            # one materialised row with leading dimension 0; make it once.
-            grad_out = grad_out[:1].contiguous().expand(grad_out.shape)
         # GA (written by dH) is read by dW1 and dX back to back while it is
         # cached, the combine follows dX for the same reason, dW2 (H' and G)
         # goes last: 8 us per cfg3 step against dH, dW2, dX, dW1.
