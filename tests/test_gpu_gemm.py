@@ -221,7 +221,7 @@ def test_up_fwd_gather_map_path(device):
 @pytest.mark.parametrize("with_workspace", [True, False], ids=["splitk", "no_workspace"])
 def test_up_dw_row_map(with_workspace, device):
     """dW1 = x[map]^T @ GA through the row map, called through the C ABI: the
-    split-K path (K chunks of 256 rows) and the workspace-free path (whole
+    split-K path (K chunks of 512 rows) and the workspace-free path (whole
     experts of ~1000 rows per item). Map entries outside [0, x_rows), -1 as
     the module's pad rows, read zeros."""
     from triton_moe import _lib

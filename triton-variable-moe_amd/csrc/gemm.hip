@@ -1505,7 +1505,7 @@ int cu_count() {
 // chunks of one tile inside one range accumulate in registers, so the chunk
 // size does not change the partial traffic (at most two partial tiles per
 // workgroup).
-constexpr int kDwChunk = 256;
+constexpr int kDwChunk = 512;
 
 // Persistent grid: one workgroup per CU (the LDS ring and tables fill a CU),
 // never more than there are work items; a multiple of 8 so every XCD gets
