@@ -202,6 +202,7 @@ def time_steps(m, xb, steps, warmup):
 # Entry point -> op name of the per-kernel breakdown; the combine runs twice
 # per step (forward, then the backward gather of dX).
 OP_OF = {
+    "vmoe_router_logits": ("router_logits",),
     "vmoe_router_topk": ("router_topk",),
     "vmoe_route": ("route",),
     "vmoe_gemm_up_fwd": ("gemm_up_fwd",),
