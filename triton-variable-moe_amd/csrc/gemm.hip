@@ -495,14 +495,17 @@ struct Gemm {
     int idx[PW];         // K-form: k of the lane's chunk; T-form: the lane's k-row
     bool ok[PW];         // K-form: row valid; T-form: column valid
   };
-  // T-form row gather (the A operand of the up dW GEMM). Each producer wave
-  // stages the map entries of its k-rows for kWinStages stages of an item
-  // in a 256-byte LDS window (lane l of the window DMA fetches the entry of
-  // stage l / 8, row 8 * wave + l % 8), by DMA like the operand tiles, so
-  // the ring's vmcnt waits order it too. The window of the next item loads
-  // while the current one streams (two windows per wave); a scalar load of
-  // the entries instead waits on the scalar cache once per stage.
-  static constexpr int kWinStages = 8;
+  // T-form row gather (the A operand of the up dW GEMM, B of the down dW
+  // GEMM). Each producer wave stages the map entries of its k-rows for
+  // kWinStages stages of an item in a 512-byte LDS window (lane l of window
+  // DMA h fetches the entry of stage 8 h + l / 8, row 8 * wave + l % 8), by
+  // DMA like the operand tiles, so the ring's vmcnt waits order it too. The
+  // window of the next item loads while the current one streams (two windows
+  // per wave); a scalar load of the entries instead waits on the scalar cache
+  // once per stage. A split-K item (kDwChunk rows) fits one window: refilling
+  // a window in the middle of an item has to drain every DMA in flight.
+  static constexpr int kWinStages = 16;
+  static constexpr int kWinBytes = kWinStages * 8 * 4;
   // Row factors of the output (UP_FWD, DOWN_DH): one slot of BM floats per
   // item. The producers set an item up right after issuing the previous
   // item's last stage, kStages - 1 stages ahead of the consumers, and every
@@ -520,8 +523,8 @@ struct Gemm {
     int32_t pf[4];               // the lane's entries of stage pf_kt, read a stage ahead
     bool on;
   };
-  static_assert(BK / kProducers == 8 && kWinStages * 8 == 64,
-                "window: 8 k-rows per producer wave per stage, one DMA instruction");
+  static_assert(BK / kProducers == 8 && kWinStages * 8 == 128,
+                "window: 8 k-rows per producer wave per stage, two DMA instructions");
 
   // K-form setup: rows [0, R) of the tile (source rows r0 + row, or
   // map[r0 + row]), rows_valid of them real, k measured from column c0.
@@ -619,8 +622,11 @@ struct Gemm {
       const bool v = lane < PWA * KRPI && row < tm.klen;
       dma4(tm.mrs, v ? (uint32_t)((tm.mbase + row) * 4) : kOob, win);
     } else {
-      const int k = kw + (lane >> 3) * BK + wave * 8 + (lane & 7);
-      dma4(tm.mrs, k < tm.klen ? (uint32_t)((tm.mbase + k) * 4) : kOob, win);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = kw + (8 * h + (lane >> 3)) * BK + wave * 8 + (lane & 7);
+        dma4(tm.mrs, k < tm.klen ? (uint32_t)((tm.mbase + k) * 4) : kOob, win + h * 256);
+      }
     }
   }
 
@@ -1217,8 +1223,8 @@ struct Gemm {
     __amdgpu_buffer_rsrc_t srs;
     if (scaled) srs = make_rsrc(p.row_scale);
     int nbegun = 0;         // items begun (row factors go to slot nbegun % kScaleSlots)
-    lds_char* const win0 = wins + pwave() * 256;
-    lds_char* const win1 = win0 + kProducers * 256;
+    lds_char* const win0 = wins + pwave() * kWinBytes;
+    lds_char* const win1 = win0 + kProducers * kWinBytes;
     int wcur = 0;           // window of the current item (0: win0, 1: win1)
     int la_item = -1;       // item whose window was requested into the other one
     int la_stage = 0;       // last stage issued before that request
@@ -1444,7 +1450,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
   __shared__ Meta meta;
   // Row-map windows of the producers (two per wave), for the T-form gather.
   constexpr int WIN_BYTES =
-      Traits<V>::t_map || Traits<V>::t_map_b || Traits<V>::k_map ? 2 * kProducers * 256 : 16;
+      Traits<V>::t_map || Traits<V>::t_map_b || Traits<V>::k_map ? 2 * kProducers * G::kWinBytes
+                                                                  : 16;
   __shared__ __align__(16) char wins[WIN_BYTES];
   // Per-row output factors, kScaleSlots slots of BM floats.
   constexpr int SCL_BYTES = G::kScaled ? G::kScaleSlots * G::BM * 4 : 16;
@@ -1506,6 +1513,9 @@ int cu_count() {
 // size does not change the partial traffic (at most two partial tiles per
 // workgroup).
 constexpr int kDwChunk = 512;
+static_assert(kDwChunk % Cfg<UP_DW>::BK == 0 &&
+                  kDwChunk / Cfg<UP_DW>::BK <= Gemm<UP_DW>::kWinStages,
+              "a split-K item fits one map window");
 
 // Persistent grid: one workgroup per CU (the LDS ring and tables fill a CU),
 // never more than there are work items; a multiple of 8 so every XCD gets
