@@ -86,7 +86,7 @@ struct Args {
   int64_t ldc;
   uint16_t* c2;          // UP_FWD: pre_act output (nullable)
   const uint16_t* pre;   // DOWN_DH: pre_act input -> fused relu^2 gradient (nullable)
-  const int32_t* b_map;  // row gather for B (T-form, DOWN_DW), nullable
+  const int32_t* b_map;  // row gather for B (T-form; no variant uses it), nullable
   int64_t b_rows;        // rows of B's gathered source
   const float* row_scale;  // UP_FWD / DOWN_DH: per-row factor of the output (nullable)
   const uint16_t* gscale;  // DOWN_DH / DOWN_DW: bf16 scalar factor of the output (nullable)
@@ -246,19 +246,23 @@ struct Traits<DOWN_DH> {
 };
 
 template <>
+// grad_w2 is computed transposed, C' = GY^T H (m over hidden, n over the
+// expert's width), so the row-mapped operand is A, the narrower one (two
+// DMAs per producer wave per stage instead of four), as in UP_DW; the
+// epilogue stores C' transposed into grad_w2[ew0 + n][m].
 struct Traits<DOWN_DW> {
   static constexpr bool k_map = false;
-  static constexpr bool t_map = false;
-  static constexpr bool t_map_b = true;  // B (the output gradient) may come through the map
+  static constexpr bool t_map = true;  // A (the output gradient) may come through the map
+  static constexpr bool t_map_b = false;
   static constexpr bool a_k = false, b_k = false;
   __device__ static Prob prob(const Args& p, const ExpertRec& r) {
     Prob q;
-    q.M = clamp0(r.w);
-    q.N = p.hidden;
+    q.M = p.hidden;
+    q.N = clamp0(r.w);
     q.K = clamp0(r.t1 - r.t0);
-    q.ar = r.t0; q.ac = 0;  // A(m,k) = H[t0 + k][m]
-    q.br = r.t0; q.bc = 0;  // B(k,n) = GY[t0 + k][n]
-    q.cr = r.ew0; q.cc = 0;
+    q.ar = r.t0; q.ac = 0;  // A(m,k) = GY[row(t0 + k)][m]
+    q.br = r.t0; q.bc = 0;  // B(k,n) = H[t0 + k][n]
+    q.cr = r.ew0; q.cc = 0;  // C'(m,n) -> grad_w2[cr + n][cc + m]
     return q;
   }
 };
@@ -985,6 +989,36 @@ struct Gemm {
       }
     }
     const Prob& q = w.q;
+    if constexpr (V == DOWN_DW) {
+      // Transposed store: for each (i, j, g, r) lanes 0-31 hold 32
+      // consecutive m of column n and lanes 32-63 of column n + 4, i.e. two
+      // 64-byte runs of output rows n and n + 4.
+      pd.mask = 0;
+      const int lane = threadIdx.x & 63;
+      const int n0 = w.n0 + wn * WN + 4 * (lane >> 5);  // this lane's first column
+      const int m0 = w.m0 + wm * WM + (lane & 31);
+      // One buffer resource over the expert's rows of grad_w2, 32-bit byte
+      // offsets per store.
+      const auto rc = make_rsrc(p.c + (int64_t)q.cr * p.ldc + q.cc);
+      const uint32_t ld2 = (uint32_t)p.ldc * 2;
+      const uint32_t base = (uint32_t)n0 * ld2 + (uint32_t)m0 * 2;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int dn = j * 32 + 8 * g + r;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+              const bool ok = n0 + dn < q.N && m0 + i * 32 < q.M;
+              __builtin_amdgcn_raw_buffer_store_b16(
+                  (uint16_t)f32_to_bf16(sc[i] * acc[i][j][4 * g + r]), rc,
+                  ok ? base + (uint32_t)dn * ld2 + i * 64 : kOob, 0, 0);
+            }
+          }
+      return;
+    }
     pd.mb = w.m0 + wm * WM;
     pd.nb = w.n0 + wn * WN;
     pd.M = q.M; pd.N = q.N; pd.cr = q.cr; pd.cc = q.cc;
@@ -1786,12 +1820,12 @@ extern "C" int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint1
   if (!span_ok(rows_bound, ldh) || !span_ok(gather_map ? gy_rows : rows_bound, ldgy))
     return VMOE_ERR_UNSUPPORTED;
   Args p{};
-  p.a = h; p.lda = ldh;
-  p.b = grad_y; p.ldb = ldgy; p.b_map = gather_map; p.b_rows = gather_map ? gy_rows : 0;
+  p.a = grad_y; p.lda = ldgy; p.a_map = gather_map; p.a_rows = gather_map ? gy_rows : 0;
+  p.b = h; p.ldb = ldh;
   p.gscale = grad_scale;
   p.c = grad_w2; p.ldc = ldgw;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
-  return launch_dw<DOWN_DW>(p, tiles_max<DOWN_DW>(max_width, hidden), workspace,
+  return launch_dw<DOWN_DW>(p, tiles_max<DOWN_DW>(hidden, max_width), workspace,
                             workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
