@@ -182,6 +182,18 @@ int vmoe_combine(const uint16_t* y, int64_t y_rows, int64_t ldy, const int32_t* 
                  const uint16_t* weights, int32_t top_k, uint16_t* out, int64_t ldo,
                  int64_t num_tokens, int64_t hidden, vmoe_stream_t stream);
 
+/* vmoe_combine_weight_grad: gradient of vmoe_combine's routing weights,
+ *   grad_weights[t*k+j] = sum_c f32(grad[t, c]) * f32(y[assignment_row[t*k+j], c])
+ * in fp32, 0 for slots with assignment_row < 0 (the per-slot bf16 rounding is
+ * taken as identity). Opt-in: the reference's PaddedScatterOp.backward returns
+ * None for the weights (triton_moe/kernels/scatter.py:176); this is the
+ * routing-weight gradient its padded_scatter lacks. grad may be a broadcast
+ * row (ldg = 0). */
+int vmoe_combine_weight_grad(const uint16_t* grad, int64_t ldg, const uint16_t* y, int64_t y_rows,
+                             int64_t ldy, const int32_t* assignment_row, int32_t top_k,
+                             float* grad_weights, int64_t num_tokens, int64_t hidden,
+                             vmoe_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Variable-width grouped GEMMs (bf16 in, fp32 MFMA accumulate, bf16 out).
  * Per-expert metadata as in the reference kernels:

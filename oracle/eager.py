@@ -26,7 +26,9 @@ Runs on the CPU in float32 (or float64 for pinning tests). Two numerics modes:
   In exact arithmetic all three modes agree: w (H @ W2) = (w H) @ W2 and
   H^T (w G) = (w H)^T G.
 
-Routing weights get no gradient, as in the reference (scatter.py:176).
+Routing weights get no gradient, as in the reference (scatter.py:176); the
+opt-in routing-weight gradient of the weighted combine, which the reference
+lacks, is combine_weight_grad below (pinned against torch autograd of combine).
 """
 
 from __future__ import annotations
@@ -156,6 +158,21 @@ def combine(y: torch.Tensor, assignment_row, weights_flat, k: int, T: int,
             slot[ok] = rb(y[rows[ok]] * wj[ok, None])
         out = out + slot
     return rb(out)
+
+
+def combine_weight_grad(grad: torch.Tensor, y: torch.Tensor, assignment_row, k: int,
+                        T: int) -> torch.Tensor:
+    """d(sum out * grad)/dw of combine in fp32 mode: gw[t*k+j] = sum_c grad[t, c] *
+    y[row(t, j), c], 0 for slots with row < 0; float64 accumulation.
+    The reference has no such gradient (scatter.py:176 returns None)."""
+    ar = torch.as_tensor(np.asarray(assignment_row, np.int64)).view(T, k)
+    g64, y64 = grad.double(), y.double()
+    gw = torch.zeros(T, k, dtype=torch.float64)
+    for j in range(k):
+        rows = ar[:, j]
+        ok = rows >= 0
+        gw[ok, j] = (g64[ok] * y64[rows[ok]]).sum(dim=1)
+    return gw.reshape(-1)
 
 
 def backward(prob: Problem, fwd: dict, grad_out: torch.Tensor, mode: str = "fp32") -> dict:

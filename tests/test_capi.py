@@ -60,6 +60,15 @@ def test_argument_checks_return_invalid_arg():
     assert lib.vmoe_gather(None, 0, 0, None, 1, None, 0, None, 8, -1, None, 8,
                            None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_combine(None, 0, 0, None, None, 0, None, 8, 1, 8, None) == _lib.ERR_INVALID_ARG
+    # routing-weight gradient: bad top_k, negative stride, missing output
+    assert lib.vmoe_combine_weight_grad(1, 8, 1, 4, 8, 1, 0, 1, 4, 8,
+                                        None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_combine_weight_grad(1, -8, 1, 4, 8, 1, 2, 1, 4, 8,
+                                        None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_combine_weight_grad(1, 8, 1, 4, 8, 1, 2, None, 4, 8,
+                                        None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_combine_weight_grad(None, 0, None, 0, 0, None, 2, None, 0, 8,
+                                        None) == _lib.OK
     # token-major gather: top_k above one wave is rejected, unaligned widths unsupported
     assert lib.vmoe_gather_tokens(1, 8, 1, 4, 65, None, 1, 1, 8, 4, None, 8,
                                   None) == _lib.ERR_INVALID_ARG

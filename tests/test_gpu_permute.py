@@ -172,3 +172,60 @@ def test_token_major_gather_broadcast_and_row_cap(device):
         got = gather_rows(xin, rd.row_src, k, rd.rows_bound, weights=wts.reshape(-1).to(device),
                           num_rows_dev=rd.info[0:1], assignment_row=rd.assignment_row)
         assert bits_equal(got[:P], _ref_gather(ref_x, maps, k, wts))
+
+
+def _abs_dot(G, y, ar, k, T):
+    """Per-slot sum |g| |y| (scales the fp32 summation-order tolerance)."""
+    return eager.combine_weight_grad(G.float().abs(), y.float().abs(), ar, k, T)
+
+
+@pytest.mark.parametrize("T,d,E,k,b", [(512, 256, 8, 2, 64), (300, 100, 6, 3, 32),
+                                       (1024, 1024, 64, 8, 128), (1, 8, 2, 2, 16)])
+def test_combine_weight_grad(T, d, E, k, b, device):
+    """Opt-in routing-weight gradient (absent in the reference, scatter.py:176)
+    against the float64 oracle, slots without a row included. Tolerance: the
+    kernel sums in fp32 in another order, so |got - ref| <= 1e-5 * sum|g||y|."""
+    from triton_moe.kernels.gather import combine_weight_grad
+
+    x, sel, wts, r, maps = _setup(T, d, E, k, b, device, seed=11)
+    P = int(r["padded_bins"][-1])
+    gen = torch.Generator().manual_seed(12)
+    y = torch.randn(P, d, generator=gen).to(torch.bfloat16)
+    G = torch.randn(T, d, generator=gen).to(torch.bfloat16)
+    ar = torch.as_tensor(maps["assignment_row"]).clone()
+    ar[::5] = -1  # unplaced slots (dropped tokens) give 0
+    ref = eager.combine_weight_grad(G.float(), y.float(), ar.numpy(), k, T)
+    got = combine_weight_grad(G.to(device), y.to(device), ar.to(device), k).cpu().double()
+    tol = 1e-5 * _abs_dot(G, y, ar.numpy(), k, T) + 1e-30
+    assert got.shape == ref.shape
+    assert bool(((got - ref).abs() <= tol).all())
+    assert bool((got[::5] == 0).all())
+
+
+def test_padded_scatter_weight_grad_opt_in(device):
+    """padded_scatter_autograd(..., weight_grad=True): the routing weights get the
+    gradient (bf16, at most one bf16 rounding step from the oracle); the input
+    gradient is unchanged; a broadcast output gradient (out.sum()) works."""
+    T, d, E, k, b = 512, 256, 8, 4, 64
+    x, sel, wts, r, maps = _setup(T, d, E, k, b, device, seed=13)
+    dev = lambda a: torch.as_tensor(a).to(device)  # noqa: E731
+    idx, bid, bins, pb = (dev(r["indices"]), dev(r["bin_ids"]), dev(r["bins"]),
+                          dev(r["padded_bins"]))
+    P = int(r["padded_bins"][-1])
+    y = torch.randn(P, d, generator=torch.Generator().manual_seed(14)).to(torch.bfloat16)
+    ar = maps["assignment_row"]
+    for G in (torch.randn(T, d, generator=torch.Generator().manual_seed(15)).to(torch.bfloat16),
+              None):
+        yd = y.to(device).requires_grad_(True)
+        wd = wts.reshape(-1).to(device).requires_grad_(True)
+        out = padded_scatter_autograd(yd, idx, bid, wd, bins, pb, k, weight_grad=True)
+        if G is None:
+            out.sum().backward()
+            G = torch.ones(T, d, dtype=torch.bfloat16)
+        else:
+            out.backward(G.to(device))
+        ref = eager.combine_weight_grad(G.float(), y.float(), ar, k, T)
+        tol = ref.abs() * 2.0 ** -8 + 1e-5 * _abs_dot(G, y, ar, k, T) + 1e-30
+        assert wd.grad is not None and wd.grad.dtype == torch.bfloat16
+        assert bool(((wd.grad.cpu().double() - ref).abs() <= tol).all())
+        assert bits_equal(yd.grad, _ref_gather(G, maps, k, wts))

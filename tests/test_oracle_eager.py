@@ -167,3 +167,21 @@ def test_aux_losses_uniform_and_grouped():
     b = eager.aux_losses(L, tpe, [64] * 4 + [32] * 4, [(4, 64), (4, 32)])
     fp = f * p.mean(0)
     assert torch.allclose(b["load_balance_loss"], (4 * fp[:4].sum() + 4 * fp[4:].sum()) / 2)
+
+
+@pytest.mark.parametrize("T,k,d,P", [(7, 3, 5, 30), (64, 8, 32, 700)])
+def test_combine_weight_grad_matches_autograd(T, k, d, P):
+    """The opt-in routing-weight gradient equals torch autograd of the fp32
+    combine with respect to the weights (float64), slots without a row
+    included; a transposed operand or a wrong slot index fails it."""
+    g = torch.Generator().manual_seed(T * 31 + k)
+    y = torch.randn(P, d, generator=g, dtype=torch.float64)
+    G = torch.randn(T, d, generator=g, dtype=torch.float64)
+    ar = torch.randperm(P, generator=g)[:T * k].clone()
+    ar[::4] = -1
+    w = torch.rand(T * k, generator=g, dtype=torch.float64).requires_grad_(True)
+    out = eager.combine(y, ar.numpy(), w, k, T, "fp32")
+    (out * G).sum().backward()
+    got = eager.combine_weight_grad(G, y, ar.numpy(), k, T)
+    assert torch.allclose(got, w.grad, rtol=1e-12, atol=1e-12)
+    assert bool((got[::4] == 0).all())

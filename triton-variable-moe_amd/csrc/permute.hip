@@ -303,6 +303,45 @@ __global__ __launch_bounds__(kThreads) void zero_tail_kernel(
   }
 }
 
+// Routing-weight gradient of the weighted combine (opt-in; the reference
+// returns None for the weights, triton_moe/kernels/scatter.py:176):
+//   gw[t*k+j] = sum_c f32(g[t, c]) * f32(y[row(t, j), c]), 0 for slots with no row.
+// The rounding to bf16 of each slot is taken as identity (straight-through),
+// as for the other gradients. One wave per token; the token's gradient row is
+// re-read per slot from cache, y rows once from HBM. Lane partial sums are
+// added by a butterfly, so the result is fp32 with a fixed summation order.
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void combine_wgrad_kernel(
+    const uint16_t* __restrict__ g, int64_t ldg, const uint16_t* __restrict__ y, int64_t y_rows,
+    int64_t ldy, const int32_t* __restrict__ assignment_row, int top_k,
+    float* __restrict__ gw, int64_t num_tokens, int64_t hidden) {
+  using V = Vec<VEC>;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t nvec = hidden / VEC;
+  for (int64_t t = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave; t < num_tokens;
+       t += (int64_t)gridDim.x * kRowsPerBlock) {
+    const uint16_t* grow = g + t * ldg;
+    for (int j = 0; j < top_k; ++j) {
+      const int64_t a = t * top_k + j;
+      const int32_t row = assignment_row[a];
+      float s = 0.0f;
+      if (row >= 0 && row < y_rows) {
+        const uint16_t* yrow = y + (int64_t)row * ldy;
+        for (int64_t c = lane; c < nvec; c += kWave) {
+          float fg[VEC], fy[VEC];
+          V::to_f32(V::load(grow + c * VEC), fg);
+          V::to_f32(V::load(yrow + c * VEC), fy);
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) s = fmaf(fg[i], fy[i], s);
+        }
+      }
+#pragma unroll
+      for (int off = kWave / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, kWave);
+      if (lane == 0) gw[a] = s;
+    }
+  }
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 inline int row_grid(int64_t rows) {
@@ -413,6 +452,30 @@ extern "C" int vmoe_combine(const uint16_t* y, int64_t y_rows, int64_t ldy,
       hipLaunchKernelGGL((combine_kernel<1, false, 4>), grid, block, 0, s, y, y_rows, ldy,
                          assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
   }
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_combine_weight_grad(const uint16_t* grad, int64_t ldg, const uint16_t* y,
+                                        int64_t y_rows, int64_t ldy,
+                                        const int32_t* assignment_row, int32_t top_k,
+                                        float* grad_weights, int64_t num_tokens, int64_t hidden,
+                                        vmoe_stream_t stream) {
+  if (num_tokens < 0 || hidden < 0 || y_rows < 0 || top_k <= 0 || ldy < 0 || ldg < 0)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_tokens == 0) return VMOE_OK;
+  if (!grad_weights || !assignment_row || (hidden > 0 && (!grad || (y_rows > 0 && !y))))
+    return VMOE_ERR_INVALID_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = hidden % 8 == 0 && ldy % 8 == 0 && ldg % 8 == 0 && aligned16(y) &&
+                   aligned16(grad);
+  const dim3 grid(row_grid(num_tokens)), block(kThreads);
+  if (vec)
+    hipLaunchKernelGGL((combine_wgrad_kernel<8>), grid, block, 0, s, grad, ldg, y, y_rows, ldy,
+                       assignment_row, top_k, grad_weights, num_tokens, hidden);
+  else
+    hipLaunchKernelGGL((combine_wgrad_kernel<1>), grid, block, 0, s, grad, ldg, y, y_rows, ldy,
+                       assignment_row, top_k, grad_weights, num_tokens, hidden);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }

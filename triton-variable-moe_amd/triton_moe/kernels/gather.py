@@ -105,6 +105,31 @@ def combine_rows(y: torch.Tensor, assignment_row: torch.Tensor, top_k: int, num_
     return out
 
 
+def combine_weight_grad(grad: torch.Tensor, y: torch.Tensor, assignment_row: torch.Tensor,
+                        top_k: int) -> torch.Tensor:
+    """fp32 [T*k]: gw[t*k+j] = sum_c grad[t, c] * y[row(t, j), c], 0 for unplaced slots.
+
+    The routing-weight gradient of combine_rows(y, ..., weights=w), with each
+    slot's bf16 rounding taken as identity. A row-broadcast grad (row stride
+    0, the gradient of out.sum()) is read from its single row."""
+    _require_bf16(y, "combine weight gradient")
+    _require_bf16(grad, "combine weight gradient")
+    y = _row_major(y)
+    tokens, hidden = grad.shape
+    if tokens > 0 and grad.stride(0) == 0:
+        grad, ldg = (grad[:1] if grad.stride(1) == 1 else grad[:1].contiguous()), 0
+    else:
+        grad = _row_major(grad)
+        ldg = grad.stride(0)
+    gw = torch.empty(tokens * top_k, dtype=torch.float32, device=y.device)
+    if gw.numel() == 0:
+        return gw
+    _lib.call("vmoe_combine_weight_grad", grad.data_ptr(), ldg, y.data_ptr(), y.shape[0],
+              y.stride(0), assignment_row.data_ptr(), int(top_k), gw.data_ptr(), tokens, hidden,
+              _lib.stream(y.device))
+    return gw
+
+
 @torch.compiler.disable
 def padded_gather(
     x: torch.Tensor,

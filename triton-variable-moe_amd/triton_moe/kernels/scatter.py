@@ -6,7 +6,9 @@ The reference writes bf16(y * w) into a zero-filled [T, k, d] intermediate and
 sums it with torch; here one kernel reads the k rows of each token through an
 assignment -> row map and sums the bf16-rounded products in fp32 registers,
 which gives the same value with a third of the HBM traffic. As in the
-reference, the routing weights receive no gradient.
+reference, the routing weights receive no gradient by default;
+padded_scatter_autograd(..., weight_grad=True) adds it (the reference returns
+None for them, scatter.py:176): gw[t*k+j] = sum_c G[t, c] * x[row(t, j), c].
 """
 
 from __future__ import annotations
@@ -16,7 +18,7 @@ from torch.amp import custom_bwd, custom_fwd
 from torch.autograd.function import once_differentiable
 
 from .. import _lib
-from .gather import combine_rows, gather_rows, row_maps
+from .gather import combine_rows, combine_weight_grad, gather_rows, row_maps
 
 
 @torch.compiler.disable
@@ -51,13 +53,18 @@ class PaddedScatterOp(torch.autograd.Function):
 
     @staticmethod
     @custom_fwd(device_type="cuda")
-    def forward(ctx, x, indices, bin_ids, weights, bins, padded_bins, top_k):
+    def forward(ctx, x, indices, bin_ids, weights, bins, padded_bins, top_k,
+                weight_grad=False):
         _lib.require_gpu(x)
         total_padded = x.shape[0]
         num_tokens = len(weights) // top_k
         rs, _, ar = row_maps(indices, bin_ids, bins, padded_bins, top_k, total_padded,
                              num_tokens * top_k, want_assignment_row=True)
-        ctx.save_for_backward(rs, weights)
+        ctx.weight_grad = bool(weight_grad)
+        if ctx.weight_grad:
+            ctx.save_for_backward(rs, weights, x, ar)
+        else:
+            ctx.save_for_backward(rs, weights)
         ctx.top_k = top_k
         ctx.total_padded = total_padded
         return combine_rows(x, ar, top_k, num_tokens, weights=weights)
@@ -66,11 +73,23 @@ class PaddedScatterOp(torch.autograd.Function):
     @custom_bwd(device_type="cuda")
     @once_differentiable
     def backward(ctx, grad_output):
-        rs, weights = ctx.saved_tensors
-        grad_x = gather_rows(grad_output, rs, ctx.top_k, ctx.total_padded, weights=weights)
-        return grad_x, None, None, None, None, None, None
+        rs, weights = ctx.saved_tensors[:2]
+        grad_x = None
+        if ctx.needs_input_grad[0]:
+            grad_x = gather_rows(grad_output, rs, ctx.top_k, ctx.total_padded, weights=weights)
+        grad_w = None
+        if ctx.weight_grad and ctx.needs_input_grad[3]:
+            x, ar = ctx.saved_tensors[2:]
+            grad_w = combine_weight_grad(grad_output, x, ar, ctx.top_k).to(weights.dtype)
+            grad_w = grad_w.reshape(weights.shape)
+        return grad_x, None, None, grad_w, None, None, None, None
 
 
-def padded_scatter_autograd(x, indices, bin_ids, weights, bins, padded_bins, top_k):
-    """Padded scatter with autograd support."""
-    return PaddedScatterOp.apply(x, indices, bin_ids, weights, bins, padded_bins, top_k)
+def padded_scatter_autograd(x, indices, bin_ids, weights, bins, padded_bins, top_k,
+                            weight_grad: bool = False):
+    """Padded scatter with autograd support.
+
+    weight_grad=True (opt-in, not in the reference) also returns the gradient
+    of the routing weights when they require it."""
+    return PaddedScatterOp.apply(x, indices, bin_ids, weights, bins, padded_bins, top_k,
+                                 weight_grad)
