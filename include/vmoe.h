@@ -244,6 +244,22 @@ int vmoe_relu2_grad(const uint16_t* grad_h, const uint16_t* pre_act, int64_t ld,
                     uint16_t* grad_act, int64_t ldo, int64_t rows, int64_t cols,
                     vmoe_stream_t stream);
 
+/* SwiGLU activation for activation="swiglu": the gate and up halves of an
+ * expert's W1 columns (gate at ewo_e + c, up at ewo_e + w_e + c, the
+ * reference's layout, triton_moe/kernels/grouped_gemm.py:295-297) are run as
+ * two grouped GEMMs without activation, then
+ *   vmoe_swiglu:      H = bf16(silu(gate) * up)   (grouped_gemm.py:347-349)
+ *   vmoe_swiglu_grad: grad_gate = bf16(gh * up * s * (1 + gate * (1 - s))),
+ *                     grad_up = bf16(gh * gate * s), s = sigmoid(gate)
+ * The reference's swiglu backward is an unfinished placeholder
+ * (grouped_gemm.py:768-790); vmoe_swiglu_grad is the derivative of its
+ * forward. Elementwise over [rows, cols]; cols, ld, ldo, ldgh multiples of 8. */
+int vmoe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t ld, uint16_t* h, int64_t ldo,
+                int64_t rows, int64_t cols, vmoe_stream_t stream);
+int vmoe_swiglu_grad(const uint16_t* grad_h, int64_t ldgh, const uint16_t* gate,
+                     const uint16_t* up, int64_t ld, uint16_t* grad_gate, uint16_t* grad_up,
+                     int64_t ldo, int64_t rows, int64_t cols, vmoe_stream_t stream);
+
 /* grad_x = GA_e @ W1_e^T, GA = gradient w.r.t. the pre-activation (the output
  * of vmoe_relu2_grad, or grad_h itself for activation "none").
  * Replaces _grouped_gemm_up_backward_dx_kernel

@@ -160,6 +160,29 @@ def combine(y: torch.Tensor, assignment_row, weights_flat, k: int, T: int,
     return rb(out)
 
 
+def swiglu_up(xg: torch.Tensor, w1: torch.Tensor, rows, widths, offsets,
+              max_w: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(H, gate) of the grouped up projection with swiglu, unrounded, per-expert
+    loop: gate = X_e W1[:, o_e : o_e + w_e], up = X_e W1[:, o_e + w_e : o_e + 2 w_e],
+    H = silu(gate) * up (reference grouped_gemm.py:295-297, 323-330, 347-349).
+    Differentiable (torch autograd gives the backward the reference leaves
+    unfinished, grouped_gemm.py:768-790)."""
+    P = xg.shape[0]
+    h = torch.zeros(P, max_w, dtype=xg.dtype)
+    gate = torch.zeros(P, max_w, dtype=xg.dtype)
+    hs, gs = [], []
+    for e, (r0, r1) in enumerate(rows):
+        w, o = widths[e], offsets[e]
+        g = xg[r0:r1] @ w1[:, o:o + w]
+        u = xg[r0:r1] @ w1[:, o + w:o + 2 * w]
+        hs.append((e, r0, r1, w, g * torch.sigmoid(g) * u))
+        gs.append(g)
+    for (e, r0, r1, w, he), g in zip(hs, gs):
+        h = h.index_put((torch.arange(r0, r1)[:, None], torch.arange(w)[None, :]), he)
+        gate = gate.index_put((torch.arange(r0, r1)[:, None], torch.arange(w)[None, :]), g)
+    return h, gate
+
+
 def combine_weight_grad(grad: torch.Tensor, y: torch.Tensor, assignment_row, k: int,
                         T: int) -> torch.Tensor:
     """d(sum out * grad)/dw of combine in fp32 mode: gw[t*k+j] = sum_c grad[t, c] *

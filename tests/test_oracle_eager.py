@@ -185,3 +185,22 @@ def test_combine_weight_grad_matches_autograd(T, k, d, P):
     got = eager.combine_weight_grad(G, y, ar.numpy(), k, T)
     assert torch.allclose(got, w.grad, rtol=1e-12, atol=1e-12)
     assert bool((got[::4] == 0).all())
+
+
+def test_swiglu_oracle_layout_and_silu():
+    """swiglu_up against torch.nn.functional.silu on a dense single-expert
+    problem and, for two experts of different widths, against column slices
+    taken by hand: a swapped gate/up half or a wrong column offset fails it."""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(12, 16, generator=g, dtype=torch.float64)
+    w1 = torch.randn(16, 2 * 8 + 2 * 16, generator=g, dtype=torch.float64)
+    h, gate = eager.swiglu_up(x[:5], w1[:, :16], [(0, 5)], [8], [0], 8)
+    ref = torch.nn.functional.silu(x[:5] @ w1[:, :8]) * (x[:5] @ w1[:, 8:16])
+    assert torch.allclose(h, ref, rtol=1e-12, atol=1e-12)
+    assert torch.allclose(gate, x[:5] @ w1[:, :8], rtol=1e-12, atol=1e-12)
+    rows, widths, offs = [(0, 5), (5, 12)], [8, 16], [0, 16]
+    h2, _ = eager.swiglu_up(x, w1, rows, widths, offs, 16)
+    ref1 = torch.nn.functional.silu(x[5:] @ w1[:, 16:32]) * (x[5:] @ w1[:, 32:48])
+    assert torch.allclose(h2[5:], ref1, rtol=1e-12, atol=1e-12)
+    assert torch.allclose(h2[:5, :8], ref, rtol=1e-12, atol=1e-12)
+    assert (h2[:5, 8:] == 0).all()

@@ -1496,6 +1496,56 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
   G::run(p, (lds_char*)ring, meta, (lds_char*)epi, (lds_char*)wins, (lds_char*)scl);
 }
 
+// SwiGLU on [rows, cols] bf16 pairs (gate g, up u) from the two halves of an
+// expert's W1 columns (the reference's layout, grouped_gemm.py:295-297 and its
+// epilogue silu(gate) * up, :347-349):
+//   forward   H  = bf16(silu(g) * u),            silu(g) = g * sigmoid(g)
+//   backward  dG = bf16(gh * u * s * (1 + g (1 - s))), dU = bf16(gh * g * s),
+//             s = sigmoid(g)
+// The reference's backward for it is an unfinished placeholder
+// (grouped_gemm.py:768-790); this is the derivative of the forward above.
+__device__ __forceinline__ float sigm(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+template <bool BWD>
+__global__ __launch_bounds__(256) void swiglu_kernel(
+    const uint16_t* __restrict__ gh, int64_t ldgh, const uint16_t* __restrict__ gate,
+    const uint16_t* __restrict__ up, int64_t ld, uint16_t* __restrict__ o0,
+    uint16_t* __restrict__ o1, int64_t ldo, int64_t rows, int64_t cols) {
+  const int64_t vpr = cols / 8;
+  const int64_t total = rows * vpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / vpr, c = (i % vpr) * 8;
+    const uint4 gv = *reinterpret_cast<const uint4*>(gate + r * ld + c);
+    const uint4 uv = *reinterpret_cast<const uint4*>(up + r * ld + c);
+    uint4 hv = make_uint4(0, 0, 0, 0);
+    if (BWD) hv = *reinterpret_cast<const uint4*>(gh + r * ldgh + c);
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    uint32_t a[4], b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float gf[2] = {lo_f32(gw[j]), hi_f32(gw[j])}, uf[2] = {lo_f32(uw[j]), hi_f32(uw[j])};
+      float hf[2] = {lo_f32(hw[j]), hi_f32(hw[j])}, ra[2], rb[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float sg = sigm(gf[h]);
+        if (BWD) {
+          ra[h] = hf[h] * uf[h] * sg * (1.0f + gf[h] * (1.0f - sg));
+          rb[h] = hf[h] * gf[h] * sg;
+        } else {
+          ra[h] = gf[h] * sg * uf[h];
+          rb[h] = 0.0f;
+        }
+      }
+      a[j] = pack_bf16(ra[0], ra[1]);
+      b[j] = pack_bf16(rb[0], rb[1]);
+    }
+    *reinterpret_cast<uint4*>(o0 + r * ldo + c) = make_uint4(a[0], a[1], a[2], a[3]);
+    if (BWD) *reinterpret_cast<uint4*>(o1 + r * ldo + c) = make_uint4(b[0], b[1], b[2], b[3]);
+  }
+}
+
 // GA = bf16(pre > 0 ? 2 * grad_h * pre : 0) elementwise over [rows, cols]
 // (the relu^2 derivative, grouped_gemm.py:751-766), for callers that hold
 // grad_h and pre_act separately.
@@ -1702,6 +1752,42 @@ extern "C" int vmoe_gemm_down_fwd(const uint16_t* h, int64_t ldh, const uint16_t
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
   return launch<DOWN_FWD>(p, row_items<DOWN_FWD>(rows_bound, E, hidden),
                           reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int vmoe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t ld, uint16_t* h,
+                           int64_t ldo, int64_t rows, int64_t cols, vmoe_stream_t stream) {
+  if (rows < 0 || cols < 0 || ld < cols || ldo < cols) return VMOE_ERR_INVALID_ARG;
+  if (rows == 0 || cols == 0) return VMOE_OK;
+  if (!gate || !up || !h) return VMOE_ERR_INVALID_ARG;
+  if (cols % 8 || ld % 8 || ldo % 8 || !a16(gate) || !a16(up) || !a16(h))
+    return VMOE_ERR_UNSUPPORTED;
+  const int64_t n = rows * (cols / 8);
+  const int64_t grid = std::min<int64_t>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(swiglu_kernel<false>, dim3((unsigned)grid), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), nullptr, 0, gate, up, ld, h,
+                     nullptr, ldo, rows, cols);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_swiglu_grad(const uint16_t* grad_h, int64_t ldgh, const uint16_t* gate,
+                                const uint16_t* up, int64_t ld, uint16_t* grad_gate,
+                                uint16_t* grad_up, int64_t ldo, int64_t rows, int64_t cols,
+                                vmoe_stream_t stream) {
+  if (rows < 0 || cols < 0 || ld < cols || ldo < cols || ldgh < cols)
+    return VMOE_ERR_INVALID_ARG;
+  if (rows == 0 || cols == 0) return VMOE_OK;
+  if (!grad_h || !gate || !up || !grad_gate || !grad_up) return VMOE_ERR_INVALID_ARG;
+  if (cols % 8 || ld % 8 || ldo % 8 || ldgh % 8 || !a16(grad_h) || !a16(gate) || !a16(up) ||
+      !a16(grad_gate) || !a16(grad_up))
+    return VMOE_ERR_UNSUPPORTED;
+  const int64_t n = rows * (cols / 8);
+  const int64_t grid = std::min<int64_t>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(swiglu_kernel<true>, dim3((unsigned)grid), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), grad_h, ldgh, gate, up, ld,
+                     grad_gate, grad_up, ldo, rows, cols);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
 }
 
 extern "C" int vmoe_relu2_grad(const uint16_t* grad_h, const uint16_t* pre_act, int64_t ld,

@@ -32,11 +32,12 @@ from .gather import row_maps
 _ACTIVATIONS = {"none": _lib.ACT_NONE, "relu_squared": _lib.ACT_RELU_SQUARED}
 
 
+ACT_SWIGLU = 2  # host-side only: two grouped GEMMs without activation + vmoe_swiglu
+
+
 def _activation_code(activation: str) -> int:
     if activation == "swiglu":
-        raise NotImplementedError(
-            "swiglu is an incomplete placeholder in the reference and is not provided")
-    # The reference maps unknown names to "none" (grouped_gemm.py:435).
+        return ACT_SWIGLU
     return _ACTIVATIONS.get(activation, _lib.ACT_NONE)
 
 
@@ -404,6 +405,84 @@ def precompute_gather_map(indices, bin_ids, bins, padded_bins, top_k):
     return gm
 
 
+# ---------------------------------------------------------------------------
+# SwiGLU: expert e's gate columns are W1[:, ewo_e : ewo_e + w_e] and its up
+# columns W1[:, ewo_e + w_e : ewo_e + 2 w_e] (the reference's layout,
+# grouped_gemm.py:295-297). The halves are gathered into two contiguous
+# weight matrices, each run as a plain grouped GEMM, and combined by the
+# elementwise vmoe_swiglu / vmoe_swiglu_grad kernels.
+# ---------------------------------------------------------------------------
+
+
+def swiglu_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, w1_cols: int):
+    """(GemmMeta over the compacted halves, gate column index, up column index)."""
+    E = int(torch.as_tensor(widths).numel())
+    if E == 0:
+        raise ValueError("expert_widths is empty")
+    h_ewo = _i32(ewo)[:E + 1].cpu().tolist()
+    h_w = _i32(widths)[:E].cpu().tolist()
+    if any(w < 0 or o < 0 or o + 2 * w > w1_cols for o, w in zip(h_ewo, h_w)):
+        raise ValueError("swiglu: expert gate/up columns exceed the weight matrix")
+    cum = [0]
+    for w in h_w:
+        cum.append(cum[-1] + w)
+    dev = torch.as_tensor(widths).device
+    gate = torch.cat([torch.arange(o, o + w) for o, w in zip(h_ewo, h_w)] or
+                     [torch.zeros(0, dtype=torch.long)]).to(dev)
+    up = torch.cat([torch.arange(o + w, o + 2 * w) for o, w in zip(h_ewo, h_w)] or
+                   [torch.zeros(0, dtype=torch.long)]).to(dev)
+    m = host_meta(eto, torch.tensor(cum, dtype=torch.int32, device=dev), widths, tpe,
+                  max_width, hidden, None, cum[-1])
+    return m, gate, up
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """H = bf16(silu(gate) * up) elementwise (vmoe_swiglu)."""
+    gate, up = _same_ld(gate, up)
+    h = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
+    _lib.call("vmoe_swiglu", gate.data_ptr(), up.data_ptr(), gate.stride(0), h.data_ptr(),
+              h.stride(0), gate.shape[0], gate.shape[1], _lib.stream(gate.device))
+    return h
+
+
+def swiglu_grad(grad_h: torch.Tensor, gate: torch.Tensor, up: torch.Tensor):
+    """(grad_gate, grad_up) of swiglu (vmoe_swiglu_grad)."""
+    grad_h = _bf16(grad_h, "swiglu grad_output")
+    gate, up = _same_ld(gate, up)
+    gg = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
+    gu = torch.empty_like(gg)
+    _lib.call("vmoe_swiglu_grad", grad_h.data_ptr(), grad_h.stride(0), gate.data_ptr(),
+              up.data_ptr(), gate.stride(0), gg.data_ptr(), gu.data_ptr(), gg.stride(0),
+              gate.shape[0], gate.shape[1], _lib.stream(gate.device))
+    return gg, gu
+
+
+def swiglu_fwd(x, w1, m: GemmMeta, gate_idx, up_idx, gather_map=None):
+    """(H, gate, up), each [rows, max_width] with zero column tails."""
+    w1 = _bf16(w1, "grouped_gemm_up w1")
+    g, _ = up_fwd(x, w1.index_select(1, gate_idx), m, _lib.ACT_NONE, False, zero_tails=True,
+                  gather_map=gather_map)
+    u, _ = up_fwd(x, w1.index_select(1, up_idx), m, _lib.ACT_NONE, False, zero_tails=True,
+                  gather_map=gather_map)
+    return swiglu(g, u), g, u
+
+
+def swiglu_bwd(grad_h, x, w1, gate, up, m: GemmMeta, gate_idx, up_idx, hidden: int,
+               gather_map=None):
+    """(grad_x in gathered rows, grad_w1 in W1's gate/up layout)."""
+    w1 = _bf16(w1, "grouped_gemm_up_backward w1")
+    _need(grad_h.shape == gate.shape, "grad_output and pre_act shapes differ")
+    gg, gu = swiglu_grad(grad_h, gate, up)
+    w1g, w1u = w1.index_select(1, gate_idx), w1.index_select(1, up_idx)
+    # one bf16 rounding of the fp32 sum of the two bf16 halves
+    grad_x = up_bwd_dx(gg, w1g, m, hidden).float()
+    grad_x = (grad_x + up_bwd_dx(gu, w1u, m, hidden).float()).to(torch.bfloat16)
+    grad_w1 = torch.zeros_like(w1)
+    grad_w1.index_copy_(1, gate_idx, up_bwd_dw(gg, x, w1g, m, hidden, gather_map))
+    grad_w1.index_copy_(1, up_idx, up_bwd_dw(gu, x, w1u, m, hidden, gather_map))
+    return grad_x, grad_w1
+
+
 @torch.compiler.disable
 def grouped_gemm_up(x, w1, expert_token_offsets, expert_weight_offsets, expert_widths,
                     tokens_per_expert, max_expert_width, activation="relu_squared",
@@ -415,6 +494,12 @@ def grouped_gemm_up(x, w1, expert_token_offsets, expert_weight_offsets, expert_w
     """
     _lib.require_gpu(x)
     act = _activation_code(activation)
+    if act == ACT_SWIGLU:
+        m, gi, ui = swiglu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                                tokens_per_expert, int(max_expert_width), x.shape[1],
+                                w1.shape[1])
+        h, g, _ = swiglu_fwd(x, w1, m, gi, ui, gather_map)
+        return (h, g) if save_pre_act else h
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1])
     # With gather_map, rows are read as x[gather_map[row]] inside the kernel
@@ -443,6 +528,19 @@ def grouped_gemm_up_backward(grad_output, x, w1, pre_act, expert_token_offsets,
     """(grad_x [total_tokens, hidden] in gathered space, grad_w1 like w1)."""
     _lib.require_gpu(grad_output)
     act = _activation_code(activation)
+    if act == ACT_SWIGLU:
+        # pre_act holds the gate; the up half is recomputed from x (the
+        # reference keeps only the gate and leaves this backward unfinished,
+        # grouped_gemm.py:768-790).
+        m, gi, ui = swiglu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                                tokens_per_expert, grad_output.shape[1], int(hidden_size),
+                                w1.shape[1])
+        w1b = _bf16(w1, "grouped_gemm_up_backward w1")
+        up, _ = up_fwd(x, w1b.index_select(1, ui), m, _lib.ACT_NONE, False, zero_tails=True,
+                       gather_map=gather_map)
+        gate = _bf16(pre_act, "grouped_gemm_up_backward pre_act")
+        return swiglu_bwd(grad_output, x, w1b, gate, up, m, gi, ui, int(hidden_size),
+                          gather_map)
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, grad_output.shape[1], int(hidden_size), None,
                   w1.shape[1])
@@ -476,15 +574,24 @@ class GroupedGemmUp(torch.autograd.Function):
         _lib.require_gpu(x)
         x = x.to(w1.dtype)
         act = _activation_code(activation)
+        use_gm = x_flat is not None and gather_map is not None
+        ctx.use_gather_map = use_gm
+        xs = (x_flat.to(w1.dtype), w1) if use_gm else (x, w1)
+        if act == ACT_SWIGLU:
+            m, gi, ui = swiglu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                                    tokens_per_expert, int(max_expert_width), x.shape[1],
+                                    w1.shape[1])
+            out, gate, up = swiglu_fwd(x, w1, m, gi, ui)
+            ctx.swiglu = (gi, ui)
+            ctx.save_for_backward(*xs, gate, up, *((gather_map,) if use_gm else ()))
+            ctx.meta = m
+            ctx.hidden_size = hidden_size
+            ctx.act = act
+            return out
         m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                       tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1])
         out, pre = up_fwd(x, w1, m, act, True, zero_tails=True)
-        use_gm = x_flat is not None and gather_map is not None
-        ctx.use_gather_map = use_gm
-        if use_gm:
-            ctx.save_for_backward(x_flat.to(w1.dtype), w1, pre, gather_map)
-        else:
-            ctx.save_for_backward(x, w1, pre)
+        ctx.save_for_backward(*xs, pre, *((gather_map,) if use_gm else ()))
         ctx.meta = m
         ctx.hidden_size = hidden_size
         ctx.act = act
@@ -494,6 +601,13 @@ class GroupedGemmUp(torch.autograd.Function):
     @custom_bwd(device_type="cuda")
     @once_differentiable
     def backward(ctx, grad_output):
+        if ctx.act == ACT_SWIGLU:
+            saved = ctx.saved_tensors
+            x_for_dw, w1, gate, up = saved[:4]
+            gm = saved[4] if ctx.use_gather_map else None
+            grad_x, grad_w1 = swiglu_bwd(grad_output, x_for_dw, w1, gate, up, ctx.meta,
+                                         *ctx.swiglu, int(ctx.hidden_size), gm)
+            return grad_x, grad_w1, None, None, None, None, None, None, None, None, None
         if ctx.use_gather_map:
             x_for_dw, w1, pre, gm = ctx.saved_tensors
         else:
