@@ -428,8 +428,9 @@ def test_fp32_inputs_not_supported(device):
         grouped_gemm_up(x, w1, eto, eto, wid, wid, 128)
 
 
-def _swiglu_case(seed=31):
-    c = _case(512, 256, [(2, 128), (2, 64)], 2, 64, False, seed=seed)
+def _swiglu_case(seed=31, skew=False):
+    sizes = [(4, 128), (4, 64)] if skew else [(2, 128), (2, 64)]
+    c = _case(512, 256, sizes, 2, 64, skew, seed=seed)
     g = torch.Generator().manual_seed(seed + 1)
     offs2 = [0]
     for w in c["widths"]:
@@ -440,8 +441,8 @@ def _swiglu_case(seed=31):
     return c
 
 
-@pytest.mark.parametrize("public_backward", [False, True])
-def test_swiglu_forward_backward(public_backward, device):
+@pytest.mark.parametrize("public_backward,skew", [(False, False), (True, False), (False, True)])
+def test_swiglu_forward_backward(public_backward, skew, device):
     """activation="swiglu" (gate at ewo_e + c, up at ewo_e + w_e + c, as the
     reference's forward, grouped_gemm.py:295-349) against float64 autograd of
     the oracle; the backward the reference leaves unfinished (:768-790) is
@@ -450,7 +451,7 @@ def test_swiglu_forward_backward(public_backward, device):
     from oracle import eager
     from triton_moe.kernels import grouped_gemm_up_autograd, grouped_gemm_up_backward
 
-    c = _swiglu_case()
+    c = _swiglu_case(skew=skew)  # skew: hot experts and four that receive no rows
     eto, _, wid, tpe = _meta_dev(c, device)
     ewo2 = c["ewo2"].to(device)
     xg64 = c["xg"].double().requires_grad_(True)

@@ -202,6 +202,17 @@ def test_combine_weight_grad(T, d, E, k, b, device):
     assert bool((got[::5] == 0).all())
 
 
+def test_combine_weight_grad_empty(device):
+    """No tokens: an empty fp32 gradient, no launch."""
+    from triton_moe.kernels.gather import combine_weight_grad
+
+    y = torch.zeros(4, 16, dtype=torch.bfloat16, device=device)
+    g = torch.zeros(0, 16, dtype=torch.bfloat16, device=device)
+    ar = torch.zeros(0, dtype=torch.int32, device=device)
+    got = combine_weight_grad(g, y, ar, 2)
+    assert got.shape == (0,) and got.dtype == torch.float32
+
+
 def test_padded_scatter_weight_grad_opt_in(device):
     """padded_scatter_autograd(..., weight_grad=True): the routing weights get the
     gradient (bf16, at most one bf16 rounding step from the oracle); the input
