@@ -478,3 +478,34 @@ def test_swiglu_forward_backward(public_backward, skew, device):
         gx, gw1 = xr.grad, w1r.grad
     assert_close_norm(gx, xg64.grad, LOOSE, "swiglu grad_x")
     assert_close_norm(gw1, w164.grad, LOOSE, "swiglu grad_w1")
+
+
+def test_swiglu_gather_map_path(device):
+    """activation="swiglu" with gather_map: forward reads x_flat[gm[row]] for both
+    halves, and the public backward (which recomputes the up half through the
+    map) gives grad_w1 of the gathered rows; grad_x stays in gathered rows."""
+    from oracle import eager
+    from triton_moe.kernels import grouped_gemm_up_backward
+
+    c = _swiglu_case(seed=41)
+    eto, _, wid, tpe = _meta_dev(c, device)
+    ewo2 = c["ewo2"].to(device)
+    T = 300
+    x_flat = torch.randn(T, c["d"], generator=torch.Generator().manual_seed(42)).to(torch.bfloat16)
+    gm = torch.randint(0, T, (c["P"],), dtype=torch.int32,
+                       generator=torch.Generator().manual_seed(43))
+    xg64 = x_flat[gm.long()].double().requires_grad_(True)
+    w164 = c["w1s"].double().requires_grad_(True)
+    h_ref, gate_ref = eager.swiglu_up(xg64, w164, c["rows"], c["widths"], c["offs2"][:-1],
+                                      c["max_w"])
+    G = torch.randn(h_ref.shape, generator=torch.Generator().manual_seed(44)).to(torch.bfloat16)
+    h_ref.backward(G.double())
+    xd, w1, gmd = x_flat.to(device), c["w1s"].to(device), gm.to(device)
+    out, pre = grouped_gemm_up(xd, w1, eto, ewo2, wid, tpe, c["max_w"], activation="swiglu",
+                               save_pre_act=True, gather_map=gmd)
+    assert_close_norm(out, h_ref, LOOSE, "swiglu H gm")
+    assert_close_norm(pre, gate_ref, TIGHT, "swiglu gate gm")
+    gx, gw1 = grouped_gemm_up_backward(G.to(device), xd, w1, pre, eto, ewo2, wid, tpe, c["d"],
+                                       activation="swiglu", gather_map=gmd)
+    assert_close_norm(gx, xg64.grad, LOOSE, "swiglu grad_x gm")
+    assert_close_norm(gw1, w164.grad, LOOSE, "swiglu grad_w1 gm")
