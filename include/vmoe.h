@@ -84,6 +84,25 @@ int vmoe_route(const void* selected_experts, int32_t selected_is_int64,
                float* row_weight, void* workspace, size_t workspace_bytes,
                vmoe_stream_t stream);
 
+/* vmoe_route without a workspace argument and without any allocation: the
+ * workspace is a file-scope device array of 1 MiB per GPU (each GPU the
+ * library runs on holds it until the process ends). No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code
+ * under graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Arguments, outputs and status codes are those of vmoe_route; a call whose
+ * vmoe_route_workspace_bytes(num_assignments, num_experts) exceeds 1 MiB
+ * returns VMOE_ERR_WORKSPACE without launching anything (1 MiB holds, e.g.,
+ * 262144 assignments over 512 experts). Calls that overlap on one GPU share
+ * the array and race: run them in one stream. */
+int vmoe_route_static(const void* selected_experts, int32_t selected_is_int64,
+                      int64_t num_assignments, int32_t num_experts, int32_t top_k,
+                      int32_t block_size, int32_t rounding, int32_t* bin_ids, int32_t* indices,
+                      int32_t* tokens_per_expert, int32_t* bins, int32_t* padded_bins,
+                      int32_t* row_src, int32_t* gather_map, int32_t gather_map_pad,
+                      int64_t row_capacity, int32_t* assignment_row, int32_t* info,
+                      int32_t* expert_offsets, int32_t* padded_counts, const uint16_t* weights,
+                      float* row_weight, vmoe_stream_t stream);
+
 /* Row maps from caller-supplied routing arrays, for the stand-alone
  * gather/scatter/gather-map entry points. Follows the per-sorted-position
  * placement of _padded_gather_kernel (triton_moe/kernels/gather.py:34-60) and

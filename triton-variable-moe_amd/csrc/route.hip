@@ -22,6 +22,7 @@
 // comparison sort.
 
 #include <algorithm>
+#include <mutex>
 
 #include "vmoe_common.h"
 
@@ -570,6 +571,60 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
     VMOE_CHECK_LAUNCH();
   }
   return VMOE_OK;
+}
+
+// vmoe_route_static: vmoe_route with its workspace in a file-scope device
+// array, for callers that cannot allocate. Each GPU the library runs on holds
+// its own copy of `scratch` (kRouteStaticBytes) until the process ends. In
+// host code the array's name is only a stand-in for the symbol: its device
+// address is looked up once per device, with that device current, by
+// hipGetSymbolAddress, and only that address is passed to the kernels.
+// vmoe_route rewrites every word of the workspace it reads (the per-tile
+// counts and error flags, then the per-expert starts), so nothing has to be
+// cleared between calls. Calls that overlap on one GPU share the array and
+// race.
+constexpr size_t kRouteStaticBytes = 1u << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kRouteStaticBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on first use).
+int static_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return VMOE_ERR_LAUNCH;
+  if (dev < 0 || dev >= kMaxDevices) return VMOE_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
+      return VMOE_ERR_LAUNCH;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return VMOE_OK;
+}
+}  // namespace
+
+extern "C" int vmoe_route_static(const void* sel, int32_t is64, int64_t A, int32_t E,
+                                 int32_t top_k, int32_t block, int32_t rounding,
+                                 int32_t* bin_ids, int32_t* indices, int32_t* tpe, int32_t* bins,
+                                 int32_t* padded_bins, int32_t* row_src, int32_t* gather_map,
+                                 int32_t gather_map_pad, int64_t row_capacity,
+                                 int32_t* assignment_row, int32_t* info, int32_t* expert_offsets,
+                                 int32_t* padded_counts, const uint16_t* weights,
+                                 float* row_weight, vmoe_stream_t stream) {
+  if (A < 0 || E <= 0) return VMOE_ERR_INVALID_ARG;
+  if (vmoe_route_workspace_bytes(A, E) > kRouteStaticBytes) return VMOE_ERR_WORKSPACE;
+  void* ws = nullptr;
+  const int st = static_scratch(&ws);
+  if (st) return st;
+  return vmoe_route(sel, is64, A, E, top_k, block, rounding, bin_ids, indices, tpe, bins,
+                    padded_bins, row_src, gather_map, gather_map_pad, row_capacity,
+                    assignment_row, info, expert_offsets, padded_counts, weights, row_weight, ws,
+                    kRouteStaticBytes, stream);
 }
 
 extern "C" int vmoe_row_maps(const int32_t* indices, const int32_t* bin_ids,

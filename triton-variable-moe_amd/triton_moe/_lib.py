@@ -28,6 +28,8 @@ _SIGNATURES = {
     "vmoe_route_workspace_bytes": [_i64, _i32],
     "vmoe_route": [_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                    _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp],
+    "vmoe_route_static": [_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                          _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "vmoe_row_maps": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _i64, _vp, _vp, _vp, _vp],
     "vmoe_gather": [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp],
     "vmoe_gather_tokens": [_vp, _i64, _vp, _i64, _i32, _vp, _vp, _vp, _i64, _i64, _vp, _i64,
