@@ -11,6 +11,8 @@ Contents:
                forward and backward, in two modes: "fp32" (no intermediate
                rounding; the tolerance oracle) and "bf16" (rounds to bf16
                exactly where the reference's kernels do; the tight oracle).
+  topk.py   -- the reference router's top-k chain (torch.topk order of equal
+               values and torch.sum order on the GPU, normalisation, bf16).
 
 Pinning (what checks each function against something other than itself):
   route / row maps: numpy stable argsort + bincount + cumsum (library
@@ -19,4 +21,7 @@ Pinning (what checks each function against something other than itself):
   eager forward/backward: a dense all-experts formulation with a routing
       weight matrix and torch autograd for the gradients, float64 on small
       inputs (tests/test_oracle_eager.py).
+  topk chain: torch.topk / torch.sum outputs recorded on a ROCm GPU
+      (tests/golden/topk_cases.json) and a lexicographic sort for the
+      selected set (tests/test_oracle_topk.py).
 """

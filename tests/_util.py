@@ -45,7 +45,9 @@ def bits_equal(got: torch.Tensor, ref: torch.Tensor) -> bool:
 
 def make_problem(T, d, sizes, k, block_size=64, seed=0, skew=None, device="cuda"):
     """Seeded bf16 inputs on the CPU (so the oracle sees identical bits), routing
-    decided on the device exactly as TritonMoEMLP does (sigmoid -> topk -> norm)."""
+    decided on the device by the reference's own chain (moe.py:166-176):
+    nn.Linear logits (+ skew, as a forward hook on the router adds it),
+    sigmoid, torch.topk, normalisation, bf16."""
     g = torch.Generator().manual_seed(seed)
     widths, offsets = eager.expert_layout(sizes)
     E, W = len(widths), offsets[-1]
@@ -53,7 +55,7 @@ def make_problem(T, d, sizes, k, block_size=64, seed=0, skew=None, device="cuda"
     wr = (torch.randn(E, d, generator=g) * 0.02).to(torch.bfloat16)
     w1 = (torch.randn(d, W, generator=g) * 0.02).to(torch.bfloat16)
     w2 = (torch.randn(W, d, generator=g) * 0.02).to(torch.bfloat16)
-    logits = (x.to(device) @ wr.to(device).T)
+    logits = torch.nn.functional.linear(x.to(device), wr.to(device))
     if skew is not None:
         logits = logits + skew.to(device=device, dtype=logits.dtype)
     probs = torch.sigmoid(logits.float())

@@ -418,6 +418,88 @@ def test_autograd_entry_points(device):
     assert_close_norm(w2.grad, gw2_ref, TIGHT, "w2.grad")
 
 
+@pytest.mark.parametrize("activation", ["relu_squared", "swiglu"])
+def test_reference_module_chain_autograd(activation, device):
+    """The reference module's call chain (moe.py:184-250) through the public API:
+    fused_route -> precompute_gather_map -> padded_gather_autograd ->
+    grouped_gemm_up_autograd(..., x_flat=x_flat, gather_map=gather_map) ->
+    grouped_gemm_down_autograd -> padded_scatter_autograd, forward and
+    backward. relu_squared is held to the oracle rounding where the
+    reference's kernels do (mode "bf16") at TIGHT; swiglu (whose backward the
+    reference leaves unfinished) runs the up stage with x_flat and gather_map
+    against float64 autograd at LOOSE."""
+    from oracle import eager
+    from triton_moe.kernels import (
+        fused_route,
+        padded_gather_autograd,
+        padded_scatter_autograd,
+        precompute_gather_map,
+    )
+
+    from _util import make_problem
+
+    T, d, sizes, k, b = 768, 256, [(4, 256), (4, 128)], 2, 64
+    p = make_problem(T, d, sizes, k, b, seed=21, device=device)
+    E = p["E"]
+    sel = p["sel"].reshape(-1)
+    wts = p["wts"].reshape(-1)
+    bin_ids, indices, _tpe, bins, padded_bins = fused_route(sel, E, block_size=b, rounding="up")
+    eto = torch.cat([torch.zeros(1, device=device, dtype=torch.int32), padded_bins])
+    ptpe = torch.cat([padded_bins[:1], padded_bins[1:] - padded_bins[:-1]])
+    gm = precompute_gather_map(indices, bin_ids, bins, padded_bins, k)
+    wid = torch.tensor(p["widths"], dtype=torch.int32, device=device)
+    max_w = max(p["widths"])
+    x_flat = p["x"].to(device).requires_grad_(True)
+    G = torch.randn(T, d, generator=torch.Generator().manual_seed(22)).to(torch.bfloat16)
+    if activation == "relu_squared":
+        ewo = torch.tensor(p["offsets"], dtype=torch.int32, device=device)
+        w1 = p["w1"].to(device).requires_grad_(True)
+        w2 = p["w2"].to(device).requires_grad_(True)
+        xg = padded_gather_autograd(x_flat, indices, bin_ids, bins, padded_bins, k)
+        h = grouped_gemm_up_autograd(xg, w1, eto, ewo, wid, ptpe, max_w, d, "relu_squared",
+                                     x_flat=x_flat, gather_map=gm)
+        y = grouped_gemm_down_autograd(h, w2, eto, ewo, wid, ptpe, d, max_w)
+        out = padded_scatter_autograd(y, indices, bin_ids, wts, bins, padded_bins, k)
+        out.backward(G.to(device))
+        prob = eager.Problem(p["x"].float(), p["w1"].float(), p["w2"].float(), p["widths"],
+                             p["offsets"], p["sel"].cpu(), p["wts"].cpu().float(), b)
+        fb = eager.forward(prob, "bf16")
+        bb = eager.backward(prob, fb, G.float(), "bf16")
+        assert_close_norm(out, fb["out"], TIGHT, "chain out")
+        for got, key in ((x_flat.grad, "grad_x"), (w1.grad, "grad_w1"), (w2.grad, "grad_w2")):
+            assert_close_norm(got, bb[key], TIGHT, f"chain {key}")
+        return
+    # swiglu: W1 holds gate and up halves per expert
+    g = torch.Generator().manual_seed(23)
+    offs2 = [0]
+    for w in p["widths"]:
+        offs2.append(offs2[-1] + 2 * w)
+    w1s = (torch.randn(d, offs2[-1], generator=g) * 0.05).to(torch.bfloat16)
+    ewo2 = torch.tensor(offs2, dtype=torch.int32, device=device)
+    w1 = w1s.to(device).requires_grad_(True)
+    xg = padded_gather_autograd(x_flat, indices, bin_ids, bins, padded_bins, k)
+    h = grouped_gemm_up_autograd(xg, w1, eto, ewo2, wid, ptpe, max_w, d, "swiglu",
+                                 x_flat=x_flat, gather_map=gm)
+    Gh = torch.randn(h.shape, generator=g).to(torch.bfloat16)
+    h.backward(Gh.to(device))
+    # float64 reference: the padded gather (zeros on pad rows), then swiglu
+    pb = [0] + padded_bins.cpu().tolist()
+    rows = [(pb[e], pb[e + 1]) for e in range(E)]
+    gmap = gm.cpu().long()
+    r = eager.route(eager.Problem(p["x"].float(), p["w1"].float(), p["w2"].float(),
+                                  p["widths"], p["offsets"], p["sel"].cpu(),
+                                  p["wts"].cpu().float(), b))
+    pad = torch.from_numpy(r["row_src"]) < 0
+    x64 = p["x"].double().requires_grad_(True)
+    xg64 = torch.where(pad[:, None], torch.zeros((), dtype=torch.float64), x64[gmap])
+    w164 = w1s.double().requires_grad_(True)
+    h_ref, _ = eager.swiglu_up(xg64, w164, rows, p["widths"], offs2[:-1], max_w)
+    h_ref.backward(Gh.double())
+    assert_close_norm(h, h_ref, LOOSE, "chain swiglu H")
+    assert_close_norm(x_flat.grad, x64.grad, LOOSE, "chain swiglu grad_x")
+    assert_close_norm(w1.grad, w164.grad, LOOSE, "chain swiglu grad_w1")
+
+
 def test_fp32_inputs_not_supported(device):
     """The reference also accepts fp32 (tf32 tl.dot); here bf16 only, loudly."""
     eto = torch.tensor([0, 128, 256], dtype=torch.int32, device=device)

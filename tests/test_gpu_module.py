@@ -1,8 +1,10 @@
 """TritonMoEMLP on the GPU against the eager per-expert-loop oracle.
 
-Protocol: the oracle consumes the device module's own routing decision
-(selected experts and bf16 weights, recomputed with the module's router on
-the same inputs), upcasts the bf16 parameters exactly to fp32, and detaches
+Protocol: the module's routing (logits, expert ids in slot order, bf16
+weights) is first checked bit for bit against the reference's routing chain
+run by PyTorch on the same inputs (nn.Linear, sigmoid, torch.topk,
+normalisation, moe.py:166-176); the oracle then consumes that decision,
+upcasts the bf16 parameters exactly to fp32, and detaches
 the routing weights (the reference gives them no gradient, scatter.py:176).
 Tolerances are normwise (max|d|/max|ref|, mean|d|/mean|ref|): TIGHT against
 the oracle rounding to bf16 where the module does (mode "bf16w": the routing
@@ -11,6 +13,8 @@ points), LOOSE against the unrounded fp32 oracle.
 """
 
 from __future__ import annotations
+
+import contextlib
 
 import pytest
 import torch
@@ -22,15 +26,16 @@ from _util import LOOSE, TIGHT, assert_close_norm, bits_equal, make_problem, zip
 
 pytestmark = pytest.mark.gpu
 
-# name: (batch, seq, n_embd, expert_sizes, top_k, block_size, zipf)
+# name: (batch, seq, n_embd, expert_sizes, top_k, block_size, Zipf alpha or None)
 CONFIGS = {
-    "ref_small": (2, 64, 128, [(4, 256)], 2, 128, False),
-    "ref_uniform": (4, 256, 256, [(8, 512)], 2, 128, False),
-    "ref_variable": (4, 256, 256, [(4, 512), (4, 256)], 2, 128, False),
-    "cfg0_shape": (8, 512, 256, [(8, 512)], 2, 64, False),
-    "cfg1": (8, 1024, 768, [(8, 512)], 2, 64, False),
-    "cfg2": (8, 2048, 768, [(4, 512), (8, 256), (4, 128)], 2, 64, False),
-    "cfg3": (1, 16384, 1024, [(64, 256)], 8, 64, True),
+    "ref_small": (2, 64, 128, [(4, 256)], 2, 128, None),
+    "ref_uniform": (4, 256, 256, [(8, 512)], 2, 128, None),
+    "ref_variable": (4, 256, 256, [(4, 512), (4, 256)], 2, 128, None),
+    "cfg0_shape": (8, 512, 256, [(8, 512)], 2, 64, None),
+    "cfg1": (8, 1024, 768, [(8, 512)], 2, 64, None),
+    "cfg2": (8, 2048, 768, [(4, 512), (8, 256), (4, 128)], 2, 64, None),
+    "cfg3": (1, 16384, 1024, [(64, 256)], 8, 64, 3.0),
+    "cfg3_a1": (1, 16384, 1024, [(64, 256)], 8, 64, 1.0),  # the benchmark's alpha
 }
 
 
@@ -45,9 +50,9 @@ def _module(p, d, sizes, k, b, device):
 
 
 def _run(name, device, seed=0):
-    B, S, d, sizes, k, b, zipf = CONFIGS[name]
+    B, S, d, sizes, k, b, alpha = CONFIGS[name]
     E = sum(c for c, _ in sizes)
-    bias = zipf_bias(E, alpha=3.0) if zipf else None
+    bias = zipf_bias(E, alpha=alpha) if alpha is not None else None
     p = make_problem(B * S, d, sizes, k, b, seed=seed, skew=bias, device=device)
     m = _module(p, d, sizes, k, b, device)
     if bias is not None:
@@ -55,9 +60,16 @@ def _run(name, device, seed=0):
     x = p["x"].view(B, S, d).to(device).requires_grad_(True)
     out, aux, f_i = m(x)
     with torch.no_grad():
-        _, _, wts, sel = m._router(x.detach().reshape(-1, d))
+        logits, _, wts, sel = m._router(x.detach().reshape(-1, d))
+    # The module routes exactly as the reference's chain on the same inputs
+    # (logits, expert ids in slot order, bf16 weights); the oracle is fed
+    # that chain's decision.
+    assert bits_equal(logits, p["logits"]), f"{name}: router logits"
+    bad = int((sel != p["sel"]).any(dim=1).sum())
+    assert bad == 0, f"{name}: {bad} tokens routed differently from the reference chain"
+    assert bits_equal(wts, p["wts"]), f"{name}: routing weights"
     prob = eager.Problem(p["x"].float(), p["w1"].float(), p["w2"].float(), p["widths"],
-                         p["offsets"], sel.cpu(), wts.cpu().float(), b)
+                         p["offsets"], p["sel"].cpu(), p["wts"].cpu().float(), b)
     return m, x, out, aux, f_i, prob
 
 
@@ -161,20 +173,34 @@ def test_forward_profiled(device):
     m, x, out, aux, f_i, _ = _run("ref_small", device)
 
     class StepRecorder:
+        """Event-timed steps, as the reference's CUDAStepProfiler."""
+
         def __init__(self):
-            self.names = []
+            self.steps = []
 
+        @contextlib.contextmanager
         def step(self, name):
-            import contextlib
-
-            self.names.append(name)
-            return contextlib.nullcontext()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            try:
+                yield
+            finally:
+                e1.record()
+                self.steps.append((name, e0, e1))
 
     rec = StepRecorder()
     out2, aux2, f2 = m.forward_profiled(x.detach(), rec)
-    assert rec.names == ["flatten", "routing", "fused_route", "gather", "gemm_up", "gemm_down",
-                         "scatter", "reshape", "aux_loss"]
+    torch.cuda.synchronize()
+    names = [n for n, _, _ in rec.steps]
+    assert names == ["flatten", "routing", "fused_route", "gather+gemm_up", "gemm_down",
+                     "scatter", "reshape", "aux_loss"]
+    ms = {n: a.elapsed_time(b) for n, a, b in rec.steps}
+    # each expert-path step holds a launch of its own
+    for n in ("gather+gemm_up", "gemm_down", "scatter"):
+        assert ms[n] > 0.0, (n, ms)
     assert bits_equal(out2, out.detach()) and torch.equal(f2, f_i)
+    assert not out2.requires_grad
 
 
 def test_config4_full_size_sampled(device):
@@ -189,15 +215,24 @@ def test_config4_full_size_sampled(device):
     out, _, _ = m(x)
     out.sum().backward()
     with torch.no_grad():
-        _, _, wts, sel = m._router(x.detach().reshape(-1, d))
+        logits, _, wts, sel = m._router(x.detach().reshape(-1, d))
+    assert bits_equal(logits, p["logits"]) and torch.equal(sel, p["sel"])
+    assert bits_equal(wts, p["wts"])
     g = torch.Generator().manual_seed(0)
     tok = torch.randperm(S, generator=g)[:192].sort().values
     sub = eager.Problem(p["x"][tok].float(), p["w1"].float(), p["w2"].float(), p["widths"],
                         p["offsets"], sel.cpu()[tok], wts.cpu()[tok].float(), b)
+    out_s = out.detach().reshape(S, d)[tok.to(device)]
+    gx_s = x.grad.reshape(S, d)[tok.to(device)]
+    ones = torch.ones(len(tok), d)
     fb = eager.forward(sub, "bf16w")
-    assert_close_norm(out.detach().reshape(S, d)[tok.to(device)], fb["out"], TIGHT, "cfg4 out")
-    bb = eager.backward(sub, fb, torch.ones(len(tok), d), "bf16w")
-    assert_close_norm(x.grad.reshape(S, d)[tok.to(device)], bb["grad_x"], TIGHT, "cfg4 x.grad")
+    assert_close_norm(out_s, fb["out"], TIGHT, "cfg4 out")
+    bb = eager.backward(sub, fb, ones, "bf16w")
+    assert_close_norm(gx_s, bb["grad_x"], TIGHT, "cfg4 x.grad")
+    ff = eager.forward(sub, "fp32")
+    assert_close_norm(out_s, ff["out"], LOOSE, "cfg4 out vs fp32 oracle")
+    bf_ = eager.backward(sub, ff, ones, "fp32")
+    assert_close_norm(gx_s, bf_["grad_x"], LOOSE, "cfg4 x.grad vs fp32 oracle")
     # weight gradients: full oracle on a few experts' columns (all their tokens)
     full = eager.Problem(p["x"].float(), p["w1"].float(), p["w2"].float(), p["widths"],
                          p["offsets"], sel.cpu(), wts.cpu().float(), b)
@@ -224,3 +259,9 @@ def test_config4_full_size_sampled(device):
         gw1 = eager.bf(xe.T @ ga)
         assert_close_norm(m.w2.grad[o:o + w], gw2, TIGHT, f"cfg4 gw2 e{e}")
         assert_close_norm(m.w1.grad[:, o:o + w], gw1, TIGHT, f"cfg4 gw1 e{e}")
+        # unrounded fp32 chain (the tolerance oracle)
+        h32 = we[:, None] * torch.relu(z) ** 2
+        gh32 = we[:, None] * (g_rows @ p["w2"][o:o + w].float().T)
+        ga32 = torch.where(z > 0, gh32 * 2.0 * torch.relu(z), torch.zeros_like(z))
+        assert_close_norm(m.w2.grad[o:o + w], h32.T @ g_rows, LOOSE, f"cfg4 gw2 e{e} fp32")
+        assert_close_norm(m.w1.grad[:, o:o + w], xe.T @ ga32, LOOSE, f"cfg4 gw1 e{e} fp32")

@@ -4,9 +4,10 @@
 //
 // Semantics (triton_moe/moe.py:166-182, 253-303 of the reference):
 //   p[t, e]   = sigmoid(float(L[t, e]))                    L = router logits (bf16)
-//   (v, s)    = topk(p[t], k): values descending; equal values are ordered
-//               by ascending expert index (torch leaves the tie order open)
-//   w[t, j]   = bf16(v_j / (sum_j v_j + 1e-20))  (norm) or bf16(v_j)
+//   (v, s)    = topk(p[t], k) in torch.topk's order on ROCm, ties included
+//               (torch_topk_order below)
+//   w[t, j]   = bf16(v_j / (sum_j v_j + 1e-20))  (norm) or bf16(v_j), the sum
+//               in the order of torch's row reduction (torch_row_sum)
 //   z_loss    = bf16(mean_t bf16(bf16(logsumexp_e L[t, e])^2))
 //   p_i[e]    = mean_t p[t, e]
 //   f_i[e]    = bf16(tokens_per_expert[e] / sum tokens_per_expert)
@@ -111,6 +112,147 @@ __device__ __forceinline__ float wave_max_f32(float v) {
 // sigmoid as torch evaluates it for fp32 (1 / (1 + exp(-x)), precise exp).
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// ---- torch.topk's output order and torch.sum's order, for one token ----
+//
+// The reference takes torch.topk(sigmoid(L.float()), k) (moe.py:168-170).
+// On ROCm (PyTorch 2.x, aten/src/ATen/native/cuda/TensorTopK.cu, Sort.cu,
+// SortUtils.cuh) a row of up to a few thousand values goes through the
+// single-block selection, which writes the values above the k-th largest in
+// ascending index order and then the values equal to it, also by ascending
+// index, until k are written; for 1 < k <= 32 an in-place 32-slot bitonic
+// sort (descending, slots past k marked unused and sorted to the end) then
+// orders them, and for k > 32 a stable radix sort does. The bitonic sort is
+// not stable: equal values come out in the order its network leaves them,
+// so that network is replayed here. Slots >= N (N = 8, 16 or 32, the
+// smallest >= k) hold no entry through the whole network and a slot below N
+// never swaps with one above, so N slots replay it exactly: the sizes 2 .. N
+// with direction bit (pos & size), then one descending merge pass over the N
+// slots for each wider size up to 32. An unused slot is key -1, below every
+// probability's bits (p >= 0); such slots are interchangeable.
+//
+// Input: pb / ex hold the k largest values (float bits) and their expert
+// indices in the selection order of this file's kernels (value descending,
+// equal values by ascending index); entries at j >= k are ignored. Output:
+// the same k entries in torch.topk's order.
+__device__ __forceinline__ void cx_select(uint32_t& ka, int32_t& va, uint32_t& kb, int32_t& vb,
+                                          bool swap) {
+  const uint32_t k0 = ka, k1 = kb;
+  const int32_t v0 = va, v1 = vb;
+  ka = swap ? k1 : k0;
+  kb = swap ? k0 : k1;
+  va = swap ? v1 : v0;
+  vb = swap ? v0 : v1;
+}
+
+template <int N>
+__device__ __forceinline__ void torch_topk_order(uint32_t (&pb)[N], int32_t (&ex)[N], int k) {
+  static_assert(N == 8 || N == 16 || N == 32, "N slots");
+  uint32_t kth = pb[0];
+#pragma unroll
+  for (int j = 1; j < N; ++j)
+    if (j == k - 1) kth = pb[j];
+  // Selection order: ascending (value == kth, index); the index (< 65536)
+  // stays in the low bits of the sort key, the value bits ride along.
+  uint32_t ck[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j)
+    ck[j] = j < k ? ((pb[j] == kth ? 1u << 16 : 0u) | (uint32_t)ex[j]) : 0xFFFFFFFFu;
+#pragma unroll
+  for (int size = 2; size <= N; size *= 2)
+#pragma unroll
+    for (int stride = size / 2; stride > 0; stride /= 2)
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int l = i ^ stride;
+        if (l > i) {
+          const bool up = (i & size) == 0;
+          const bool swap = up ? ck[i] > ck[l] : ck[i] < ck[l];
+          const uint32_t c0 = ck[i], c1 = ck[l], p0 = pb[i], p1 = pb[l];
+          ck[i] = swap ? c1 : c0;
+          ck[l] = swap ? c0 : c1;
+          pb[i] = swap ? p1 : p0;
+          pb[l] = swap ? p0 : p1;
+        }
+      }
+  // torch's network: swap when (key_a > key_b) == dir, keys signed.
+  uint32_t key[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    key[j] = j < k ? pb[j] : 0xFFFFFFFFu;  // -1 as int32
+    ex[j] = (int32_t)(ck[j] & 0xFFFFu);
+  }
+#pragma unroll
+  for (int size = 2; size <= 32; size *= 2) {
+    // sizes above N: one descending pass with strides N / 2 .. 1
+    const int smax = size <= N ? size / 2 : N / 2;
+#pragma unroll
+    for (int stride = smax; stride > 0; stride /= 2)
+#pragma unroll
+      for (int t = 0; t < N / 2; ++t) {
+        const int pos = 2 * t - (t & (stride - 1));
+        const bool dir = size <= N && (pos & size) != 0;
+        const bool gt = (int32_t)key[pos] > (int32_t)key[pos + stride];
+        cx_select(key[pos], ex[pos], key[pos + stride], ex[pos + stride], gt == dir);
+      }
+  }
+#pragma unroll
+  for (int j = 0; j < N; ++j) pb[j] = key[j];
+}
+
+// sum(dim=-1) of the k values as torch's reduction kernel orders it for a
+// contiguous row of k: block width bw = the largest power of two <= k
+// (k <= 64, the wave size), thread x adds x, x + bw (from 0), then the
+// threads are combined by shfl_down with offsets 1, 2, .., bw / 2. Values
+// at j >= k count as 0 (adding +0 to a non-negative sum is exact).
+template <int BW, int N>
+__device__ __forceinline__ float torch_tree_sum(const float (&v)[N]) {
+  float acc[BW];
+#pragma unroll
+  for (int x = 0; x < BW; ++x) {
+    acc[x] = v[x];
+#pragma unroll
+    for (int m = x + BW; m < N; m += BW) acc[x] += v[m];
+  }
+#pragma unroll
+  for (int off = 1; off < BW; off *= 2)
+#pragma unroll
+    for (int x = 0; x < BW; x += 2 * off) acc[x] += acc[x + off];
+  return acc[0];
+}
+
+template <int N>
+__device__ __forceinline__ float torch_row_sum(const uint32_t (&pb)[N], int k) {
+  float v[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] = j < k ? __uint_as_float(pb[j]) : 0.0f;
+  if (k >= 32) return torch_tree_sum<(N < 32 ? N : 32), N>(v);
+  if (k >= 16) return torch_tree_sum<(N < 16 ? N : 16), N>(v);
+  if (k >= 8) return torch_tree_sum<8, N>(v);
+  if (k >= 4) return torch_tree_sum<4, N>(v);
+  if (k >= 2) return torch_tree_sum<2, N>(v);
+  return v[0];
+}
+
+// Lane j < k holds the j-th selected entry (selection order); afterwards it
+// holds torch.topk's j-th entry. Every lane replays the network on copies.
+template <int N>
+__device__ __forceinline__ void topk_order_lanes(float& my_v, int& my_e, int k, int lane) {
+  uint32_t pb[N];
+  int32_t ex[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    pb[j] = __builtin_amdgcn_readlane(__float_as_uint(my_v), j);
+    ex[j] = __builtin_amdgcn_readlane(my_e, j);
+  }
+  torch_topk_order<N>(pb, ex, k);
+#pragma unroll
+  for (int j = 0; j < N; ++j)
+    if (lane == j) {
+      my_v = __uint_as_float(pb[j]);
+      my_e = ex[j];
+    }
+}
+
 // Block b handles tokens [b * per, min(T, (b + 1) * per)); its waves take
 // batches of TB consecutive tokens in turn. partial[b][e] = sum of p[t][e]
 // over the block's tokens (e < E); partial[b][E] = sum of bf16(bf16(lse_t)^2).
@@ -168,7 +310,6 @@ __global__ __launch_bounds__(topk_threads(VPL)) void router_topk_kernel(
       uint32_t taken = 0;
       float my_v = 0.0f;
       int my_e = 0;
-      float vsum = 0.0f;
       for (int j = 0; j < k; ++j) {
         uint64_t best = 0;
 #pragma unroll
@@ -187,8 +328,23 @@ __global__ __launch_bounds__(topk_threads(VPL)) void router_topk_kernel(
           my_v = v_sel;
           my_e = e_sel;
         }
-        vsum += v_sel;  // j ascending
       }
+      // sum in torch's order: lane x < bw adds lanes x and x + bw, then
+      // shfl_down steps 1 .. bw / 2 (lane 0 ends with the total)
+      int bw = 1;
+      while (2 * bw <= k) bw *= 2;
+      float part = lane < k ? my_v : 0.0f;
+      const float upper = __shfl(part, (lane + bw) & (kWave - 1), kWave);
+      if (lane + bw < k) part += upper;
+      for (int off = 1; off < bw; off *= 2) part += __shfl_down(part, off, kWave);
+      const float vsum = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(part), 0));
+      if (k <= 8) {
+        topk_order_lanes<8>(my_v, my_e, k, lane);
+      } else if (k <= 16) {
+        topk_order_lanes<16>(my_v, my_e, k, lane);
+      } else if (k <= 32) {
+        topk_order_lanes<32>(my_v, my_e, k, lane);
+      }  // k > 32: a stable sort, the selection order
       if (lane < k) {
         const float wv_ = norm ? my_v / (vsum + 1e-20f) : my_v;
         weights[t * k + lane] = (uint16_t)f32_to_bf16(wv_);
@@ -220,9 +376,10 @@ __global__ __launch_bounds__(topk_threads(VPL)) void router_topk_kernel(
 // butterfly steps merge the sorted lists of partner lanes (the larger of
 // A[j] and B[7 - j] is a bitonic sequence holding the top 8 of A and B; three
 // half-cleaner stages sort it), after which every lane of the group holds the
-// token's top 8. Keys, sigmoid, weights (v_j / (sum_j v_j + 1e-20), j
-// ascending) and the tie rule are those of router_topk_kernel; logsumexp and
-// the column sums reduce in a different fixed order.
+// token's top 8, in the selection order, which torch_topk_order turns into
+// torch.topk's. Keys, sigmoid, weights and output order are those of
+// router_topk_kernel; logsumexp and the column sums reduce in a different
+// fixed order.
 constexpr int kGrpMaxExperts = 128;
 constexpr int kGrpThreads = 1024;
 constexpr int kGrpWaves = kGrpThreads / kWave;
@@ -328,18 +485,22 @@ __global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
           if ((j & d) == 0) cs_desc(key[j], key[j + d]);
     }
     if (tok) {
-      float vsum = 0.0f;
+      uint32_t pb[8];
+      int32_t ex[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (j < k) vsum += __uint_as_float((uint32_t)(key[j] >> 32));  // j ascending
+      for (int j = 0; j < 8; ++j) {
+        pb[j] = (uint32_t)(key[j] >> 32);
+        ex[j] = (int32_t)(~(uint32_t)key[j]);
+      }
+      const float vsum = torch_row_sum<8>(pb, k);
+      torch_topk_order<8>(pb, ex, k);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         if (j < k && (j & (G - 1)) == r) {
-          const float v = __uint_as_float((uint32_t)(key[j] >> 32));
-          const int e = (int)(~(uint32_t)key[j]);
+          const float v = __uint_as_float(pb[j]);
           weights[t * k + j] = (uint16_t)f32_to_bf16(norm ? v / (vsum + 1e-20f) : v);
-          if (selected32) selected32[t * k + j] = e;
-          if (selected64) selected64[t * k + j] = e;
+          if (selected32) selected32[t * k + j] = ex[j];
+          if (selected64) selected64[t * k + j] = ex[j];
         }
       }
     }

@@ -9,8 +9,10 @@ after the routing counts exist. The losses are differentiable with respect
 to the router logits (their gradient is one elementwise kernel); the top-k
 weights are not, as in the reference (scatter.py:176).
 
-Top-k order: values descending; equal values by ascending expert index
-(torch.topk leaves the order of equal values unspecified).
+Top-k: the expert ids come out in torch.topk's order on ROCm, ties
+included, and the normalised weights carry the bits of the reference's
+torch chain (the sum in torch's reduction order); both are held to PyTorch
+on the same logits by the GPU tests.
 """
 
 from __future__ import annotations
@@ -107,11 +109,23 @@ class RouterLogitsOp(torch.autograd.Function):
 class RouterLinear(nn.Linear):
     """The router of TritonMoEMLP: nn.Linear(n_embd, num_experts, bias=False)
     (moe.py:78 of the reference) -- same parameter, initialisation, state-dict
-    key and hooks -- whose forward runs the router-logits kernel on the inputs
-    it supports and is nn.Linear's otherwise."""
+    key and hooks.
+
+    Its forward is nn.Linear's own (F.linear, hipBLASLt on ROCm), so the
+    logits carry the same bits as the reference module's on the same GPU and
+    the routing decisions downstream (top-k of their sigmoid, which the
+    router kernel reproduces bit for bit) are the reference's. With
+    use_logits_kernel = True the inputs vmoe_router_logits supports go to that
+    kernel instead: one bf16 rounding of the fp32 product, in its own
+    summation order, which can move a logit by one bf16 step (about 0.02 %
+    of them at the benchmark shapes) and with it a near-tied routing choice.
+    """
+
+    use_logits_kernel: bool = False
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.bias is None and router_logits_supported(x, self.weight):
+        if (self.use_logits_kernel and self.bias is None and
+                router_logits_supported(x, self.weight)):
             out = RouterLogitsOp.apply(x.reshape(-1, x.shape[-1]), self.weight)
             return out.reshape(*x.shape[:-1], out.shape[-1])
         return F.linear(x, self.weight, self.bias)

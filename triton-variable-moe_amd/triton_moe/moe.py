@@ -33,8 +33,10 @@ from .kernels import (
     padded_gather,
     padded_scatter,
 )
+from . import _lib
 from .kernels.fused_cumsum import route_device
-from .kernels.grouped_gemm import GemmMeta, RoutedMoEOp
+from .kernels.gather import combine_rows
+from .kernels.grouped_gemm import GemmMeta, RoutedMoEOp, down_fwd, up_fwd
 from .kernels.router import RouterAuxOp, RouterLinear, load_balance_coef, router_topk
 
 
@@ -192,30 +194,6 @@ class TritonMoEMLP(nn.Module):
         aux_loss, f_i = self._aux(router_logits, state, tokens_per_expert, x.dtype)
         return output, aux_loss, f_i
 
-    def _compute_load_balance_loss(self, router_probs: torch.Tensor,
-                                   f_i: torch.Tensor) -> torch.Tensor:
-        # Kept with the reference's formula (the module itself uses the router
-        # kernel's equivalent coefficient form, kernels/router.py).
-        """Load balance loss within expert groups (reference moe.py:276-303)."""
-        p_i = router_probs.mean(dim=0)
-        if len(set(self.expert_widths)) == 1:
-            return self.num_experts * (f_i.float() @ p_i.float())
-        if self._num_valid_groups == 0:
-            return f_i.float() @ p_i.float()
-        fi_pi = f_i.float() * p_i.float()
-        membership = self.group_membership.to(fi_pi.dtype)
-        if self._all_experts_valid:
-            group_sums = fi_pi @ membership
-        else:
-            fi_pi_valid = fi_pi.index_select(0, self.valid_expert_indices)
-            membership_valid = membership.index_select(0, self.valid_expert_indices)
-            group_sums = fi_pi_valid @ membership_valid
-        group_losses = self.group_sizes.to(fi_pi.dtype) * group_sums
-        return group_losses.mean()
-
-    def _expert_tensors(self, device):
-        return self.expert_weight_offsets_t, self.expert_widths_t
-
     def forward_with_intermediates(self, x: torch.Tensor) -> dict[str, Any]:
         """Forward returning every intermediate (reference moe.py:305-409), exact shapes."""
         batch_size = x.shape[0]
@@ -283,19 +261,19 @@ class TritonMoEMLP(nn.Module):
             meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
                             self.expert_widths_t, r.padded_counts, self.num_experts,
                             self.max_expert_width, r.rows_bound)
-        with profiler.step("gather"):
-            pass  # fused into the up GEMM's operand staging (row map)
-        with profiler.step("gemm_up"):
-            # gather, both GEMMs and the combine run as one autograd node and
-            # are timed under "gemm_up"; "gather", "gemm_down" and "scatter"
-            # stay as (empty) steps so the reference's step names are present.
-            output_flat = RoutedMoEOp.apply(x_flat, self.w1, self.w2, meta, r.gather_map,
-                                            r.row_weight, r.assignment_row, k,
-                                            self.config.n_embd)
-        with profiler.step("gemm_down"):
-            pass
-        with profiler.step("scatter"):
-            pass
+        # Forward only, as the reference's (its GEMM calls carry no autograd):
+        # the three launches of RoutedMoEOp.forward, each timed on its own.
+        # The token gather has no launch of its own (the up GEMM reads x_flat
+        # through the gather map), so its step is "gather+gemm_up".
+        with torch.no_grad():
+            with profiler.step("gather+gemm_up"):
+                h, _pre = up_fwd(x_flat, self.w1, meta, _lib.ACT_RELU_SQUARED, False,
+                                 zero_tails=False, gather_map=r.gather_map,
+                                 row_scale=r.row_weight)
+            with profiler.step("gemm_down"):
+                y = down_fwd(h, self.w2, meta, self.config.n_embd)
+            with profiler.step("scatter"):
+                output_flat = combine_rows(y, r.assignment_row, k, x_flat.shape[0])
         with profiler.step("reshape"):
             output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
         with profiler.step("aux_loss"):
