@@ -361,9 +361,16 @@ def main():
     dom_bytes = gemm_bytes(dom, A, T, d, nw, sum(widths))
     ai = per_gemm_flops / dom_bytes
     ai_bound = min(PEAK_BF16_TFLOPS, ai * PEAK_HBM_GBS / 1e3)
+    # Permutation and routing bytes: each combine reads the k rows of every
+    # token and the row of each assignment and writes the token rows; the
+    # routing reads the ids (int32) and bf16 weights and writes bin_ids,
+    # indices and assignment_row per assignment and row_src, gather_map and
+    # the fp32 row weight per padded row (+ five E-long arrays).
+    P = sum(-(-int(n) // 64) * 64 for n in counts)
     perm_bytes = {
         "combine": 2 * A * d + 2 * T * d + 4 * A,
         "gather_bwd_combine": 2 * A * d + 2 * T * d + 4 * A,
+        "route": 6 * A + 12 * A + 12 * P + 20 * E,
     }
     perm_us = sum(kern[n] for n in perm_bytes)
     perm_gbs = sum(perm_bytes.values()) / (perm_us * 1e-6) / 1e9
@@ -391,6 +398,9 @@ def main():
         "gemm_pct_mfma_peak": round(100 * gemm_tflops / PEAK_BF16_TFLOPS, 2),
         "permutation_gbs": round(perm_gbs, 1),
         "permutation_pct_hbm_peak": round(100 * perm_gbs / PEAK_HBM_GBS, 2),
+        "permutation_scope": "both combines + routing (vmoe_route), bytes and time",
+        "routing_us": round(kern["route"], 2),
+        "router_topk_us": round(kern.get("router_topk", 0.0), 2),
         "kernel_us": {n: round(v, 2) for n, v in kern.items()},
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",

@@ -290,14 +290,32 @@ struct Cfg {
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// Split-K chunk of the dW GEMMs: K rows per work item (p.kc is 0 or this).
+// Small chunks let the contiguous item ranges balance experts of very
+// different row counts; the chunks of one tile inside one range accumulate
+// in registers, so the chunk size does not change the partial traffic (at
+// most two partial tiles per workgroup).
+constexpr int kDwChunk = 512;
+
 // Output tiles and K chunks of expert e (chunks > 1 only for the split-K dW
-// GEMMs, p.kc > 0).
+// GEMMs, p.kc > 0). Every divisor is a compile-time power of two.
 template <int V>
 __device__ __forceinline__ void expert_work(const Args& p, const Prob& q, int& tiles,
                                             int& chunks) {
   constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN;
   tiles = (q.M > 0 && q.N > 0) ? cdiv(q.M, BM) * cdiv(q.N, BN) : 0;
-  chunks = (p.kc > 0 && tiles > 0 && q.K > p.kc) ? cdiv(q.K, p.kc) : 1;
+  chunks = (Cfg<V>::contig && p.kc > 0 && tiles > 0 && q.K > kDwChunk) ? cdiv(q.K, kDwChunk) : 1;
+}
+
+// x / d for 0 <= x < 2^22 and 1 <= d < 2^22: the float reciprocal estimate
+// is within one of the quotient and one correction each way makes it exact
+// (a 32-bit integer division is a long instruction sequence, and the work
+// decoder runs on the critical path of every item).
+__device__ __forceinline__ int udiv_small(int x, int d) {
+  int q = (int)((float)x * __builtin_amdgcn_rcpf((float)d));
+  q -= q * d > x ? 1 : 0;
+  q += (q + 1) * d <= x ? 1 : 0;
+  return q;
 }
 
 template <int N>
@@ -804,12 +822,14 @@ struct Gemm {
     int tiles, chunks;
     expert_work<V>(p, w.q, tiles, chunks);
     const int local = item - __builtin_amdgcn_readfirstlane(mt.pre[e]);
-    const int chunk = local % chunks;
-    const int tile = Cfg<V>::contig ? (local / chunks) * kLane + slot : local / chunks;
+    const int group = chunks == 1 ? local : udiv_small(local, chunks);
+    const int chunk = local - group * chunks;
+    const int tile = Cfg<V>::contig ? group * kLane + slot : group;
     w.skip = tile >= tiles;
     const int n_tiles = cdiv(w.q.N, BN);
-    w.m0 = (tile / n_tiles) * BM;
-    w.n0 = (tile % n_tiles) * BN;
+    const int mt_idx = n_tiles == 1 ? tile : udiv_small(tile, n_tiles);
+    w.m0 = mt_idx * BM;
+    w.n0 = (tile - mt_idx * n_tiles) * BN;
     w.kbeg = 0;
     w.chunk = chunk;
     w.chunks = chunks;
@@ -1266,6 +1286,7 @@ struct Gemm {
     int done = -2;          // every DMA issued before stage done + 1's is complete
     int issued = 0;         // stages issued
     int ikt = 0, inext = rg.beg, witem = rg.beg;
+    Work wla;  // decode of la_item, reused when that item begins
     auto begin_item = [&]() {
       if (mapped) {
         if (la_item == witem) {
@@ -1302,10 +1323,10 @@ struct Gemm {
       if (!mapped) return;
       la_item = -1;
       for (int nx = witem + rg.stride; nx < rg.end; nx += rg.stride) {
-        const Work wn = decode(p, mt, nx, ela, rg.slot);
-        if (wn.nk > 0) {
+        wla = decode(p, mt, nx, ela, rg.slot);
+        if (wla.nk > 0) {
           TMap tn = tm;
-          setup_map(p, wn, tn);
+          setup_map(p, wla, tn);
           load_window(tn, 0, wcur ? win0 : win1);
           la_item = nx;
           la_stage = issued - 1;
@@ -1318,7 +1339,7 @@ struct Gemm {
     auto advance = [&]() -> bool {
       while (inext < rg.end) {
         witem = inext;
-        wi = decode(p, mt, inext, ei, rg.slot);
+        wi = inext == la_item ? wla : decode(p, mt, inext, ei, rg.slot);
         inext += rg.stride;
         if (wi.nk > 0) {
           ikt = 0;
@@ -1413,11 +1434,15 @@ struct Gemm {
       // tiles per workgroup and store them at once (pending stays empty),
       // which keeps their registers for the accumulators.
       const int gap = max(1, w.nk / UNITS);
+      // Workgroups offset their flush k-steps by (b / 8) mod gap, so that the
+      // chip's workgroups, which reach their k-steps nearly together, do not
+      // all store in the same k-step (measured: 2-4 % faster at cfg3).
+      const int stagger = (int)((blockIdx.x >> 3) % (unsigned)gap);
       int kt = 0;
       if (pd.mask & 1) load_pre<0>(p, pd, pr);
 #pragma unroll
       for (int u = 0; u < (Cfg<V>::contig ? 0 : UNITS); ++u) {
-        const int at = min(u * gap + kLead, w.nk - 1);
+        const int at = min(u * gap + kLead + stagger, w.nk - 1);
         for (; kt <= at; ++kt, ++s) {
           block_barrier();
           compute(ring, s, acc);
@@ -1591,12 +1616,6 @@ int cu_count() {
   return cache[dev];
 }
 
-// Split-K chunk of the dW GEMMs: K rows per work item. Small chunks let the
-// contiguous item ranges balance experts of very different row counts; the
-// chunks of one tile inside one range accumulate in registers, so the chunk
-// size does not change the partial traffic (at most two partial tiles per
-// workgroup).
-constexpr int kDwChunk = 512;
 static_assert(kDwChunk % Cfg<UP_DW>::BK == 0 &&
                   kDwChunk / Cfg<UP_DW>::BK <= Gemm<UP_DW>::kWinStages,
               "a split-K item fits one map window");
