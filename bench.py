@@ -255,16 +255,23 @@ def kernel_breakdown(m, xb, steps):
 
     from triton_moe import _lib
 
+    from triton_moe.kernels import grouped_gemm as gg
+
     step = make_step(m, xb)
     step()
     timer = LaunchTimer()
     _lib.set_launch_timer(timer)
+    # one stream, so that no two timed launches overlap (the timed steps
+    # run the weight-gradient GEMMs beside the others on a second stream)
+    side = gg.BACKWARD_SIDE_STREAM
+    gg.BACKWARD_SIDE_STREAM = False
     try:
         for _ in range(steps):
             timer.new_step()
             step()
     finally:
         _lib.set_launch_timer(None)
+        gg.BACKWARD_SIDE_STREAM = side
     torch.cuda.synchronize()
     tot, cnt = {}, {}
     for op, e0, e1 in timer.marks:

@@ -169,6 +169,38 @@ def test_forward_deterministic(device):
         assert bits_equal(a, b)
 
 
+@pytest.mark.parametrize("name", ["cfg1", "cfg3"])
+def test_backward_side_stream_same_bits(name, device):
+    """The backward runs its weight-gradient GEMMs on a second stream; the
+    gradients are bit-identical to the single-stream order, over three
+    steps in a row (stream reuse, workspaces per stream)."""
+    from triton_moe.kernels import grouped_gemm as gg
+
+    m, x, _, _, _, _ = _run(name, device)
+    G = torch.randn(x.shape, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    G = G.to(device)
+
+    def grads(side):
+        gg.BACKWARD_SIDE_STREAM = side
+        try:
+            out = []
+            for _ in range(3):
+                x.grad = None
+                m.zero_grad(set_to_none=True)
+                y, _, _ = m(x)
+                y.backward(G)
+                out.append((x.grad.clone(), m.w1.grad.clone(), m.w2.grad.clone()))
+            torch.cuda.synchronize()
+            return out
+        finally:
+            gg.BACKWARD_SIDE_STREAM = True
+
+    one, two = grads(False), grads(True)
+    for a, b in zip(one, two):
+        for ga, gb in zip(a, b):
+            assert bits_equal(ga, gb)
+
+
 def test_forward_profiled(device):
     m, x, out, aux, f_i, _ = _run("ref_small", device)
 

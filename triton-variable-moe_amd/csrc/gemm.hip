@@ -72,6 +72,7 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kMaxExperts = 2048;  // per-expert work prefix held in LDS
 constexpr int kRecExperts = 256;   // per-expert metadata also held in LDS up to this E
 constexpr int kLane = 8;           // dW GEMMs: workgroups of one XCD that share each K chunk
+constexpr int kMaxLanes = 64;      // dW GEMMs: lanes (grid / kLane) a launch may have
 
 enum Variant { UP_FWD = 0, DOWN_FWD, UP_DX, UP_DW, DOWN_DH, DOWN_DW };
 
@@ -389,6 +390,7 @@ __host__ __device__ __forceinline__ int work_items(int tiles, int chunks) {
 struct Meta {
   int pre[kMaxExperts + 1];
   int rec[6][kRecExperts];
+  int lane_beg[kMaxLanes + 1];  // dW GEMMs: first item of each lane (lane_beg[NL] = total)
 };
 
 // Work-item range of workgroup b. Round-robin: XCD x (hardware deals
@@ -397,19 +399,16 @@ struct Meta {
 // workgroups take every (grid / 8)-th item. Contig (grid a multiple of
 // 8 * kLane): the j-th workgroup of XCD x (j = b / 8) is slot j % kLane of
 // lane l = x * (grid / 8 / kLane) + j / kLane; lane l owns items
-// [total * l / NL, total * (l + 1) / NL) of the NL = grid / kLane lanes, and
-// its slot s works on tile kLane * group + s of each. lin = kLane * l + s
-// names the workgroup's split-K partial slots.
+// [lane_beg[l], lane_beg[l + 1]) of the NL = grid / kLane lanes (equal
+// shares of the k-steps, see build_meta), and its slot s works on tile
+// kLane * group + s of each. lin = kLane * l + s names the workgroup's
+// split-K partial slots.
 struct Range {
   int beg, end, stride, lin, slot;
 };
 
-__host__ __device__ inline int contig_begin(int total, int lin, int grid) {
-  return (int)((int64_t)total * lin / grid);
-}
-
 template <bool CONTIG>
-__device__ __forceinline__ Range item_range(int total) {
+__device__ __forceinline__ Range item_range(int total, const int* lane_beg) {
   const int G = gridDim.x, b = blockIdx.x;
   const int xcd = b & 7, per = G >> 3, j = b >> 3;
   Range r;
@@ -420,8 +419,8 @@ __device__ __forceinline__ Range item_range(int total) {
     const int lane = xcd * (NL >> 3) + j / kLane;
     r.slot = j % kLane;
     r.lin = lane * kLane + r.slot;
-    r.beg = contig_begin(total, lane, NL);
-    r.end = contig_begin(total, lane + 1, NL);
+    r.beg = lane_beg[lane];
+    r.end = lane_beg[lane + 1];
     r.stride = 1;
   } else {
     r.beg = (int)((int64_t)total * xcd / 8) + j;
@@ -755,29 +754,88 @@ struct Gemm {
 
   // Builds the per-expert tables (all threads; `scan` is 16 longs of LDS).
   // Returns the total number of work items.
-  __device__ static int build_meta(const Args& p, Meta& mt, long long* scan) {
-    long long base = 0;
+  // Contig (dW) GEMMs also split the items into NL = grid / kLane lane
+  // ranges of equal estimated cost, in k-step units: an item costs its
+  // chunk's k-steps (1 .. kDwChunk / BK) plus kItemCost for starting it, and
+  // a tile group kEpiCost more for its epilogue (measured: an item start
+  // about 2 k-steps, a tile's rounding and stores about 4). Equal item
+  // counts left the lanes of large experts three times as busy as the
+  // lanes of the many small ones. Lane l starts at the first item at or
+  // after cumulative cost cost_total * l / NL. `cpre` is LDS scratch for
+  // E + 1 ints (the ring, before its first use).
+  static constexpr int kItemCost = 2, kEpiCost = 4;
+  __device__ static int build_meta(const Args& p, Meta& mt, long long* scan,
+                                   __attribute__((address_space(3))) int* cpre) {
+    constexpr bool CONTIG = Cfg<V>::contig;
+    long long base = 0, cbase = 0;
     for (int e0 = 0; e0 < p.E; e0 += kThreads) {
       const int e = e0 + threadIdx.x;
-      int items = 0;
+      int items = 0, cost = 0;
       if (e < p.E) {
         const ExpertRec r = rec_global(p, e);
         if (p.E <= kRecExperts) {
           mt.rec[0][e] = r.t0; mt.rec[1][e] = r.t1; mt.rec[2][e] = r.tpe;
           mt.rec[3][e] = r.ew0; mt.rec[4][e] = r.ew1; mt.rec[5][e] = r.w;
         }
+        const Prob q = T::prob(p, r);
         int tiles, chunks;
-        expert_work<V>(p, T::prob(p, r), tiles, chunks);
+        expert_work<V>(p, q, tiles, chunks);
         items = work_items<V>(tiles, chunks);
+        if (CONTIG)
+          cost = cdiv(tiles, kLane) * (cdiv(q.K, BK) + kItemCost * chunks + kEpiCost);
       }
+      // One scan of (cost << 32 | items): both prefixes stay below 2^31.
       long long total;
-      const long long ex = block_exclusive_scan<long long, kThreads>((long long)items, scan, &total);
-      if (e < p.E) mt.pre[e] = (int)(base + ex);
-      base += total;
+      const long long ex = block_exclusive_scan<long long, kThreads>(
+          ((long long)cost << 32) | (long long)items, scan, &total);
+      if (e < p.E) {
+        mt.pre[e] = (int)(base + (ex & 0xFFFFFFFFll));
+        if (CONTIG) cpre[e] = (int)(cbase + (ex >> 32));
+      }
+      base += total & 0xFFFFFFFFll;
+      cbase += total >> 32;
       __syncthreads();  // scan scratch reused by the next chunk
     }
-    if (threadIdx.x == 0) mt.pre[p.E] = (int)base;
+    if (threadIdx.x == 0) {
+      mt.pre[p.E] = (int)base;
+      if (CONTIG) cpre[p.E] = (int)cbase;
+    }
     __syncthreads();
+    if (CONTIG) {
+      const int NL = (int)gridDim.x / kLane;
+      for (int l = threadIdx.x; l <= NL; l += kThreads) {
+        int item = (int)base;
+        if (l == 0 || cbase == 0) {
+          item = l == NL ? (int)base : 0;
+        } else if (l < NL) {
+          // any monotone split will do: float, no 64-bit division
+          const int target = min((int)cbase - 1, (int)((float)cbase * ((float)l / (float)NL)));
+          // first expert e with cpre[e + 1] > target (zero-cost experts skipped)
+          int lo = 0, hi = p.E - 1;
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (cpre[mid + 1] > target) hi = mid; else lo = mid + 1;
+          }
+          const int e = lo;
+          const ExpertRec r = p.E <= kRecExperts
+              ? ExpertRec{mt.rec[0][e], mt.rec[1][e], mt.rec[2][e], mt.rec[3][e], mt.rec[4][e],
+                          mt.rec[5][e]}
+              : rec_global(p, e);
+          const Prob q = T::prob(p, r);
+          int tiles, chunks;
+          expert_work<V>(p, q, tiles, chunks);
+          const int gcost = cdiv(q.K, BK) + kItemCost * chunks + kEpiCost;
+          const int o = target - cpre[e];
+          const int g = udiv_small(o, gcost), rem = o - g * gcost;
+          // first item of group g starting at or after rem: chunk c starts
+          // at cost c * (kDwChunk / BK + kItemCost); past the last chunk,
+          // the next group's first item
+          item = mt.pre[e] + g * chunks + min(chunks, cdiv(rem, kDwChunk / BK + kItemCost));
+        }
+        mt.lane_beg[l] = item;
+      }
+      __syncthreads();
+    }
     return (int)base;
   }
 
@@ -1173,7 +1231,8 @@ struct Gemm {
   }
 
   // Adds (FIRST: copies) the wave's values of partial slot `pslot` into acc,
-  // one 32x32 block at a time to bound the registers in flight.
+  // one 32x32 block at a time to bound the registers in flight (two blocks
+  // per round trip measured 20 % slower on the up-projection dW GEMM).
   template <bool FIRST>
   __device__ __forceinline__ static void add_partial(const Args& p, int pslot,
                                                      f32x16_t (&acc)[FM][FN]) {
@@ -1211,19 +1270,20 @@ struct Gemm {
   // its slot, so the sum does not depend on which wave arrives last. Returns
   // true for that wave: acc then holds the whole tile for the normal
   // epilogue. No wave waits for another.
-  __device__ static bool split_arrive(const Args& p, const Range& rg, int total, int a,
+  __device__ static bool split_arrive(const Args& p, const Meta& mt, const Range& rg, int a,
                                       int chunks, int seg_item, f32x16_t (&acc)[FM][FN]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int NL = (int)gridDim.x / kLane, me = rg.lin / kLane, ts = rg.slot;
+    const int* lb = mt.lane_beg;
     int L0 = me;
-    while (L0 > 0 && contig_begin(total, L0, NL) > a) --L0;
-    const bool l0_inside = contig_begin(total, L0, NL) != a;  // L0's segment starts mid-range
+    while (L0 > 0 && lb[L0] > a) --L0;
+    const bool l0_inside = lb[L0] != a;  // L0's segment starts mid-range
     store_partial(p, 2 * rg.lin + (seg_item == rg.beg ? 0 : 1), acc);
     int nseg = 0, own = 0;
     for (int l = L0; l < NL; ++l) {
-      const int b0 = contig_begin(total, l, NL);
+      const int b0 = lb[l];
       if (b0 >= a + chunks) break;
-      if (contig_begin(total, l + 1, NL) == b0) continue;  // empty range
+      if (lb[l + 1] == b0) continue;  // empty range
       if (l == me) own = nseg;
       ++nseg;
     }
@@ -1238,8 +1298,8 @@ struct Gemm {
     asm volatile("" ::: "memory");  // the loads below follow the arrival
     int t = 0;
     for (int l = L0; l < NL && t < nseg; ++l) {
-      const int b0 = contig_begin(total, l, NL);
-      if (contig_begin(total, l + 1, NL) == b0) continue;
+      const int b0 = lb[l];
+      if (lb[l + 1] == b0) continue;
       const int slot = 2 * (l * kLane + ts) + (l == L0 && l0_inside ? 1 : 0);
       // own >= 2: the sum is rebuilt from the slots, own included.
       if (own >= 2 && t == 0)
@@ -1463,7 +1523,7 @@ struct Gemm {
         bool whole = true;
         if constexpr (Cfg<V>::contig) {
           if (w.chunks > 1 && !(seg_chunk == 0 && last_chunk))
-            whole = split_arrive(p, rg, total, item - w.chunk, w.chunks, seg_item, acc);
+            whole = split_arrive(p, mt, rg, item - w.chunk, w.chunks, seg_item, acc);
         }
         if (whole) {
           stash(p, w, acc, pd, kScaled && p.row_scale && w.nk > 0 ? scl + slot * (BM * 4)
@@ -1490,8 +1550,9 @@ struct Gemm {
 
   __device__ static void run(const Args& p, lds_char* ring, Meta& mt, lds_char* epi,
                              lds_char* wins, lds_char* scl) {
-    const int total = build_meta(p, mt, (long long*)(char*)ring);
-    const Range rg = item_range<Cfg<V>::contig>(total);
+    const int total = build_meta(p, mt, (long long*)(char*)ring,
+                                 (__attribute__((address_space(3))) int*)(ring + 256));
+    const Range rg = item_range<Cfg<V>::contig>(total, mt.lane_beg);
     if (rg.beg >= rg.end) return;
     const int wave = threadIdx.x >> 6;
     if (wave >= kConsumers)

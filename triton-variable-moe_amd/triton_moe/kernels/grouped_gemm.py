@@ -667,6 +667,24 @@ def grouped_gemm_down_autograd(intermediate, w2, expert_token_offsets, expert_we
 # ---------------------------------------------------------------------------
 
 
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+# RoutedMoEOp.backward runs its weight-gradient GEMMs on a side stream when
+# True; False keeps every launch on the current stream (per-kernel timing).
+BACKWARD_SIDE_STREAM = True
+
+
+def _side_stream(device) -> torch.cuda.Stream:
+    """One extra stream per device (default priority) for GEMMs that can run
+    beside the ones on the current stream."""
+    device = torch.device(device)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    st = _SIDE_STREAMS.get(idx)
+    if st is None:
+        st = torch.cuda.Stream(device=idx)
+        _SIDE_STREAMS[idx] = st
+    return st
+
+
 class RoutedMoEOp(torch.autograd.Function):
     """The module's expert path after routing, as one autograd node: token
     gather, grouped GEMM up with relu^2, grouped GEMM down, weighted combine,
@@ -713,14 +731,27 @@ class RoutedMoEOp(torch.autograd.Function):
 
         x_flat, w1, w2, h, pre, gm, rw, ar = ctx.saved_tensors
         m, d = ctx.meta, ctx.hidden_size
-        # GA (written by dH) is read by dW1 and dX back to back while it is
-        # cached, the combine follows dX for the same reason, dW2 (H' and G)
-        # goes last: 8 us per cfg3 step against dH, dW2, dX, dW1.
+        # Two streams: the weight-gradient GEMMs run on a side stream, dW2
+        # (it needs only G and H') beside dH, dW1 beside dX once GA exists.
+        # Each GEMM keeps every CU busy until its last tiles, which are
+        # fewer than the CUs; the other stream's workgroups take the CUs
+        # those tails leave idle.
+        main = torch.cuda.current_stream(grad_out.device)
+        side = _side_stream(grad_out.device) if BACKWARD_SIDE_STREAM else main
+        side.wait_stream(main)
         ga = down_bwd_dh(grad_out, w2, m, d, False, pre=pre, gather_map=gm, row_scale=rw)
-        grad_w1 = up_bwd_dw(ga, x_flat, w1, m, d, gm)
+        with torch.cuda.stream(side):
+            grad_w2 = down_bwd_dw(grad_out, h, w2, m, d, gather_map=gm)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            grad_w1 = up_bwd_dw(ga, x_flat, w1, m, d, gm)
         grad_xg = up_bwd_dx(ga, w1, m, d)
-        del ga
         grad_x = combine_rows(grad_xg, ar, ctx.top_k, x_flat.shape[0])
-        del grad_xg
-        grad_w2 = down_bwd_dw(grad_out, h, w2, m, d, gather_map=gm)
+        main.wait_stream(side)
+        # Cross-stream lifetimes for the caching allocator: main's tensors
+        # read on the side stream, the side stream's results used on main.
+        for t in (grad_out, ga, h, x_flat, gm, w1, w2):
+            t.record_stream(side)
+        for t in (grad_w1, grad_w2):
+            t.record_stream(main)
         return grad_x, grad_w1, grad_w2, None, None, None, None, None, None
