@@ -1186,23 +1186,12 @@ struct Gemm {
       return;
     }
     uint16_t* out = (NOUT == 2 && OUT == 0) ? p.c2 : p.c;
-    // The [rows, d] outputs of DOWN_FWD and UP_DX (268 MB at cfg3, read
-    // once by the combine) are stored non-temporally, so they do not evict
-    // the operands the GEMM re-reads from L2 (measured: UP_DX 142 -> 113 us
-    // at cfg3); the other outputs are read right after by the next GEMM.
-    constexpr bool kStream = V == DOWN_FWD || V == UP_DX;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const uint4 v = epi_read(scr, qq, lane);
       const int m = mb + 8 * qq + (lane >> 3);
-      if (m < pd.M && n_ok) {
-        u32x4_t* dst = reinterpret_cast<u32x4_t*>(out + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n);
-        const u32x4_t val = {v.x, v.y, v.z, v.w};
-        if (kStream)
-          __builtin_nontemporal_store(val, dst);
-        else
-          *dst = val;
-      }
+      if (m < pd.M && n_ok)
+        *reinterpret_cast<uint4*>(out + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n) = v;
     }
   }
 
