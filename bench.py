@@ -57,6 +57,10 @@ def parse():
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--profile-steps", type=int, default=0,
                     help="only run this many steps (for rocprofv3), print nothing else")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="only measure the box's practical ceilings: dense bf16 torch.matmul "
+                         "(hipBLASLt) at square and MoE-like shapes, and device copy / fill "
+                         "bandwidth")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 1 GiB device buffer 5 times: the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -102,6 +106,53 @@ def measured_traffic(config, symbol):
         return int(k["fetch_bytes"] + k["write_bytes"])
     except (OSError, KeyError, ValueError, TypeError):
         return None
+
+
+def ceiling():
+    """Practical ceilings of this GPU: dense bf16 GEMMs through torch.matmul
+    (hipBLASLt) on random and on all-zero operands (the power draw of random
+    data lowers the clock), at square sizes and at the dense equivalents of
+    cfg3's GEMMs (rows = T k, the expert dimension folded), and copy / fill
+    bandwidth of a 1 GiB buffer."""
+    import torch
+
+    dev = torch.device("cuda:0")
+
+    def timed(fn, iters):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters * 1e-3
+
+    out = {"gemm_tflops": {}, "bandwidth_tbs": {}}
+    g = torch.Generator(device=dev).manual_seed(0)
+    for M, N, K, zero, ta in [(8192, 8192, 8192, False, False), (8192, 8192, 8192, True, False),
+                              (16384, 16384, 16384, False, False),
+                              (131072, 256, 1024, False, False), (131072, 1024, 256, False, False),
+                              (1024, 256, 131072, False, True)]:
+        a = (torch.randn(K, M, device=dev, dtype=torch.bfloat16, generator=g).t() if ta else
+             torch.randn(M, K, device=dev, dtype=torch.bfloat16, generator=g))
+        b = torch.randn(K, N, device=dev, dtype=torch.bfloat16, generator=g)
+        if zero:
+            a.zero_()
+            b.zero_()
+        sec = timed(lambda: a @ b, 20 if M * N * K < 2 ** 40 else 5)
+        key = f"{M}x{N}x{K}" + ("_zeros" if zero else "") + ("_At" if ta else "")
+        out["gemm_tflops"][key] = round(2.0 * M * N * K / sec / 1e12, 1)
+        del a, b
+    n = 1 << 30
+    x = torch.empty(n, dtype=torch.uint8, device=dev)
+    y = torch.empty_like(x)
+    out["bandwidth_tbs"]["copy_read_plus_write"] = round(2 * n / timed(lambda: y.copy_(x), 20) / 1e12, 2)
+    out["bandwidth_tbs"]["fill_write"] = round(n / timed(lambda: y.fill_(1), 20) / 1e12, 2)
+    print(json.dumps({"ceiling": out, "device": torch.cuda.get_device_name(0)}))
 
 
 def copy_calibration():
@@ -340,6 +391,9 @@ def main():
     device = torch.device("cuda:0")
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.ceiling:
+        ceiling()
         return
     torch.manual_seed(0)
     m, xb, info = build_workload(args.config, device)
