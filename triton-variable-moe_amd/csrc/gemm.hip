@@ -1494,10 +1494,13 @@ struct Gemm {
       // tiles per workgroup and store them at once (pending stays empty),
       // which keeps their registers for the accumulators.
       const int gap = max(1, w.nk / UNITS);
-      // Workgroups offset their flush k-steps by (b / 8) mod gap, so that the
-      // chip's workgroups, which reach their k-steps nearly together, do not
-      // all store in the same k-step (measured: 2-4 % faster at cfg3).
-      const int stagger = (int)((blockIdx.x >> 3) % (unsigned)gap);
+      // The GEMMs with K = hidden (up fwd, dH) offset their flush k-steps by
+      // (b / 8) mod gap, so that the chip's workgroups, which reach their
+      // k-steps nearly together, do not all store in the same k-step
+      // (measured at cfg3, same box, three runs: up fwd -6 us, dH -1.6 us;
+      // on the down projection, with 8 k-steps per item, +14 us).
+      const int stagger =
+          (V == UP_FWD || V == DOWN_DH) ? (int)((blockIdx.x >> 3) % (unsigned)gap) : 0;
       int kt = 0;
       if (pd.mask & 1) load_pre<0>(p, pd, pr);
 #pragma unroll
