@@ -71,7 +71,7 @@ constexpr int kWaves = kConsumers + kProducers;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxExperts = 2048;  // per-expert work prefix held in LDS
 constexpr int kRecExperts = 256;   // per-expert metadata also held in LDS up to this E
-constexpr int kLane = 8;           // dW GEMMs: workgroups of one XCD that share each K chunk
+constexpr int kLane = 4;           // dW GEMMs: workgroups of one XCD that share each K chunk
 constexpr int kMaxLanes = 64;      // dW GEMMs: lanes (grid / kLane) a launch may have
 
 enum Variant { UP_FWD = 0, DOWN_FWD, UP_DX, UP_DW, DOWN_DH, DOWN_DW };
@@ -1694,7 +1694,11 @@ int gemm_grid(int64_t items_bound) {
 
 // Grid of the dW GEMMs: whole lanes on every XCD (a multiple of 8 * kLane),
 // one workgroup per CU where the device allows.
-int lane_grid() { return std::max(8 * kLane, cu_count() / (8 * kLane) * (8 * kLane)); }
+int lane_grid() {
+  const int g = std::max(8 * kLane, cu_count() / (8 * kLane) * (8 * kLane));
+  return std::min(g, kMaxLanes * kLane);  // lane_beg[] holds kMaxLanes + 1 entries
+}
+static_assert(kMaxLanes * kLane % (8 * kLane) == 0, "whole lanes on every XCD");
 
 template <int V>
 int launch(Args p, int64_t items_bound, hipStream_t s) {
