@@ -121,8 +121,8 @@ int vmoe_row_maps(const int32_t* indices, const int32_t* bin_ids, const int32_t*
  * Router front end (TritonMoEMLP.forward, triton_moe/moe.py:166-182 and the
  * auxiliary losses at moe.py:253-303).
  * vmoe_router_topk: from bf16 router logits L [T, E] (row stride ld_logits)
- *   p = sigmoid(float(L)); top_k of p per token, values descending, equal
- *   values by ascending expert index; weights[t*k+j] = bf16(v_j / (sum v +
+ *   p = sigmoid(float(L)); top_k of p per token in torch.topk's output order
+ *   on ROCm (equal values included); weights[t*k+j] = bf16(v_j / (sum v +
  *   1e-20)) (normalize != 0) or bf16(v_j); selected_i32 / selected_i64 (either
  *   may be NULL, not both) the expert ids; probs (nullable) p as fp32 [T, E];
  *   lse [T] fp32 = bf16-rounded logsumexp_e L[t, e]; partial = per-workgroup
@@ -162,6 +162,21 @@ int vmoe_router_aux_bwd(const uint16_t* logits, int64_t ld_logits, int64_t num_t
                         const float* coef, const float* widths_normalized, const float* grad_z,
                         const float* grad_lb, const float* grad_cl, uint16_t* grad_logits,
                         int64_t ld_grad, vmoe_stream_t stream);
+
+/* vmoe_router_weight_bwd: opt-in gradient of the routing weights with respect
+ * to the logits, which the reference does not compute (its padded_scatter
+ * returns None for the weights, triton_moe/kernels/scatter.py:176; the chain
+ * is moe.py:168-176). For token t, slot j with expert s_j, p_j =
+ * sigmoid(float(L[t, s_j])) and g_j = grad_weights[t * ld_grad_weights + j]
+ * (bf16): dp_j = (g_j - sum_i g_i p_i / S) / S with S = sum_j p_j + 1e-20
+ * when normalize != 0, else dp_j = g_j; grad_logits[t, s_j] =
+ * bf16(dp_j p_j (1 - p_j)) and 0 for every other expert (the whole row is
+ * written). selected_i32 / selected_i64 as for vmoe_router_topk. */
+int vmoe_router_weight_bwd(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
+                           int32_t num_experts, int32_t top_k, int32_t normalize,
+                           const int32_t* selected_i32, const int64_t* selected_i64,
+                           const uint16_t* grad_weights, int64_t ld_grad_weights,
+                           uint16_t* grad_logits, int64_t ld_grad, vmoe_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Token permutation (bf16).
@@ -212,6 +227,18 @@ int vmoe_combine_weight_grad(const uint16_t* grad, int64_t ldg, const uint16_t* 
                              int64_t ldy, const int32_t* assignment_row, int32_t top_k,
                              float* grad_weights, int64_t num_tokens, int64_t hidden,
                              vmoe_stream_t stream);
+
+/* vmoe_routing_weight_grad: the routing-weight gradient of the module path
+ * (opt-in; the reference has none, scatter.py:176), which scales H by the
+ * weight in the up GEMM (H' = bf16(w * relu(z)^2)), so that
+ * dL/dw = sum_c dL/dH'[c] relu(z)[c]^2:
+ *   grad_weights[a] = bf16( sum_{b < num_blocks} row_dot[row][b] / row_weight[row] ),
+ *   row = assignment_row[a], with row_dot from vmoe_gemm_down_bwd_dh; 0 when
+ *   row < 0, row >= rows or row_weight[row] == 0. */
+int vmoe_routing_weight_grad(const float* row_dot, int64_t ld_row_dot, int32_t num_blocks,
+                             int64_t rows, const float* row_weight,
+                             const int32_t* assignment_row, int64_t num_assignments,
+                             uint16_t* grad_weights, vmoe_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Variable-width grouped GEMMs (bf16 in, fp32 MFMA accumulate, bf16 out).
@@ -325,6 +352,12 @@ int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
  * before the relu^2 rule. grad_scale (nullable, one bf16 on the device): the
  * output is scaled by it, so a broadcast gradient c * ones (out.sum(),
  * out.mean()) is passed as a row of ones (ldgy = 0) and grad_scale = &c.
+ * row_dot (nullable; needs pre_act; fp32 [rows_bound, ld_row_dot] with
+ * ld_row_dot >= ceil(max_width / 64)): row_dot[row][b] = sum over the
+ * columns c of 64-column block b of GH[row][c] * pre_act[row][c]^2, GH the
+ * bf16 (scaled) gradient before the relu^2 rule; blocks at or past an
+ * expert's width are not written. It is the module's routing-weight
+ * gradient before division by the weight (vmoe_routing_weight_grad).
  * Replaces _grouped_gemm_down_backward_dintermediate_kernel
  * (triton_moe/kernels/grouped_gemm.py:970-1063, launched at 1336-1362). */
 int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64_t gy_rows,
@@ -334,7 +367,7 @@ int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64_t gy_rows,
                           int64_t ldgh, const int32_t* eto, const int32_t* ewo,
                           const int32_t* widths, const int32_t* tpe, int32_t num_experts,
                           int64_t hidden, int64_t max_width, int64_t rows_bound,
-                          vmoe_stream_t stream);
+                          float* row_dot, int64_t ld_row_dot, vmoe_stream_t stream);
 
 /* grad_w2[ewo[e]:+w_e, :] = H_e^T @ grad_y_e; rows of grad_y_e are
  * grad_y[gather_map[row]] when gather_map != NULL (gy_rows, ldgy = 0 and

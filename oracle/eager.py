@@ -28,7 +28,9 @@ Runs on the CPU in float32 (or float64 for pinning tests). Two numerics modes:
 
 Routing weights get no gradient, as in the reference (scatter.py:176); the
 opt-in routing-weight gradient of the weighted combine, which the reference
-lacks, is combine_weight_grad below (pinned against torch autograd of combine).
+lacks, is combine_weight_grad below (pinned against torch autograd of combine),
+and its chain into the router logits router_weight_logit_grad (float64
+autograd of the reference's sigmoid / normalise, pinned by gradcheck).
 """
 
 from __future__ import annotations
@@ -241,6 +243,28 @@ def backward(prob: Problem, fwd: dict, grad_out: torch.Tensor, mode: str = "fp32
     gx = combine(gxg, r["assignment_row"], None, k, T, mode)
     return {"grad_x": gx, "grad_w1": gw1, "grad_w2": gw2, "grad_y": gy, "grad_h": gh,
             "grad_a": ga, "grad_xg": gxg}
+
+
+def router_weights(logits: torch.Tensor, selected: torch.Tensor,
+                   normalize: bool = True) -> torch.Tensor:
+    """The reference's routing weights for a given selection (moe.py:168-176):
+    v = sigmoid(L)[selected], normalised by (sum v + 1e-20); unrounded and
+    differentiable in L (the selection itself is piecewise constant)."""
+    v = torch.sigmoid(logits).gather(1, selected.long())
+    if normalize:
+        v = v / (v.sum(dim=-1, keepdim=True) + 1e-20)
+    return v
+
+
+def router_weight_logit_grad(logits: torch.Tensor, selected: torch.Tensor,
+                             grad_weights: torch.Tensor, normalize: bool = True) -> torch.Tensor:
+    """dL/dlogits of sum(router_weights(logits) * grad_weights), float64 torch
+    autograd. The reference computes no such gradient (scatter.py:176); this
+    is the opt-in routing-weight gradient's chain into the router."""
+    L = logits.detach().to(torch.float64).requires_grad_(True)
+    v = router_weights(L, selected, normalize)
+    (v * grad_weights.detach().to(torch.float64).reshape(v.shape)).sum().backward()
+    return L.grad
 
 
 def aux_losses(router_logits: torch.Tensor, tokens_per_expert, widths, expert_sizes,

@@ -69,6 +69,17 @@ def test_argument_checks_return_invalid_arg():
                                         None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_combine_weight_grad(None, 0, None, 0, 0, None, 2, None, 0, 8,
                                         None) == _lib.OK
+    # module-path routing-weight gradient: ld below the block count, missing inputs
+    assert lib.vmoe_routing_weight_grad(1, 2, 4, 8, 1, 1, 16, 1, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_routing_weight_grad(1, 4, 4, 8, None, 1, 16, 1, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_routing_weight_grad(None, 4, 4, 8, 1, None, 0, None, None) == _lib.OK
+    # its logit gradient: both or neither index arrays, k above one wave
+    assert lib.vmoe_router_weight_bwd(1, 8, 4, 8, 2, 1, 1, 1, 1, 2, 1, 8,
+                                      None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_router_weight_bwd(1, 8, 4, 8, 2, 1, None, None, 1, 2, 1, 8,
+                                      None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_router_weight_bwd(1, 128, 4, 128, 65, 1, 1, None, 1, 65, 1, 128,
+                                      None) == _lib.ERR_UNSUPPORTED
     # token-major gather: top_k above one wave is rejected, unaligned widths unsupported
     assert lib.vmoe_gather_tokens(1, 8, 1, 4, 65, None, 1, 1, 8, 4, None, 8,
                                   None) == _lib.ERR_INVALID_ARG
@@ -94,6 +105,11 @@ def test_argument_checks_return_invalid_arg():
                                   64, None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_gemm_up_fwd(1, 8, 0, None, 1, 8, 1, None, 8, 5, None, 1, 1, 1, 1, 4, 16,
                                 16, 64, None) == _lib.ERR_INVALID_ARG
+    # dH row sums need pre_act and a row stride of at least ceil(max_width / 64)
+    assert lib.vmoe_gemm_down_bwd_dh(1, 16, 4, None, None, 1, 16, None, None, 1, 128, 1, 1, 1,
+                                     1, 4, 16, 128, 64, 1, 2, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gemm_down_bwd_dh(1, 16, 4, None, None, 1, 16, 1, None, 1, 128, 1, 1, 1,
+                                     1, 4, 16, 128, 64, 1, 1, None) == _lib.ERR_INVALID_ARG
     # a row-weight output without the weights it is read from
     assert lib.vmoe_route(1, 0, 4, 4, 1, 64, 0, 1, 1, 1, 1, 1, 1, 1, 0, 8, 1, 1, None, None,
                           None, 1, 1, 4096, None) == _lib.ERR_INVALID_ARG

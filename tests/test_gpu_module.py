@@ -297,3 +297,78 @@ def test_config4_full_size_sampled(device):
         ga32 = torch.where(z > 0, gh32 * 2.0 * torch.relu(z), torch.zeros_like(z))
         assert_close_norm(m.w2.grad[o:o + w], h32.T @ g_rows, LOOSE, f"cfg4 gw2 e{e} fp32")
         assert_close_norm(m.w1.grad[:, o:o + w], xe.T @ ga32, LOOSE, f"cfg4 gw1 e{e} fp32")
+
+
+def _norm_err(got, ref):
+    d = (got.double() - ref.double()).abs()
+    return (d.max() / ref.abs().max()).item(), (d.mean() / ref.abs().mean()).item()
+
+
+@pytest.mark.parametrize("name", ["ref_small", "ref_variable", "cfg1", "cfg3_a1"])
+def test_routing_weight_grad(name, device):
+    """TritonMoEConfig(routing_weight_grad=True) differentiates the output
+    through the routing weights into the router (the reference's weights get
+    no gradient, scatter.py:176). The logit gradient is held to the float64
+    chain of the fp32 oracle's weight gradient (combine_weight_grad of the
+    unrounded Y, then router_weight_logit_grad): its normwise error must stay
+    within twice that of the same chain fed the reference's rounding order
+    (Y = bf16(H W2), bf16 H), the yardstick of what bf16 storage costs here.
+    W1 and W2 gradients are unchanged, bit for bit."""
+    B, S, d, sizes, k, b, alpha = CONFIGS[name]
+    E = sum(c for c, _ in sizes)
+    bias = zipf_bias(E, alpha=alpha) if alpha is not None else None
+    p = make_problem(B * S, d, sizes, k, b, seed=0, skew=bias, device=device)
+    T = B * S
+    G = torch.randn(T, d, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    grads = {}
+    for flag in (False, True):
+        cfg = TritonMoEConfig(n_embd=d, expert_sizes=sizes, num_active_experts=k, block_size=b,
+                              routing_weight_grad=flag)
+        m = TritonMoEMLP(cfg).to(device).to(torch.bfloat16)
+        with torch.no_grad():
+            m.router.weight.copy_(p["wr"])
+            m.w1.copy_(p["w1"])
+            m.w2.copy_(p["w2"])
+        store = {}
+
+        def hook(mod, inp, out):
+            out = out + bias.to(out.device, out.dtype) if bias is not None else out
+            if out.requires_grad:
+                out.register_hook(lambda g: store.__setitem__("glogits", g))
+            store["logits"] = out.detach()
+            return out
+
+        m.router.register_forward_hook(hook)
+        x = p["x"].view(B, S, d).to(device).requires_grad_(True)
+        out, _, _ = m(x)
+        out.backward(G.to(device).view_as(out))
+        grads[flag] = (x.grad, m.w1.grad, m.w2.grad, m.router.weight.grad, store)
+    for a, b_ in zip(grads[False][1:3], grads[True][1:3]):
+        assert bits_equal(a, b_)
+    assert grads[False][3] is None and grads[True][3] is not None
+    store = grads[True][4]
+    # x also reaches the loss through the router Linear now: x.grad gains
+    # dlogits @ Wr (the two bf16 contributions summed by autograd)
+    xr = store["glogits"].float() @ p["wr"].to(device).float()
+    assert_close_norm(grads[True][0].reshape(T, d).float(),
+                      grads[False][0].reshape(T, d).float() + xr, TIGHT, f"{name} x.grad")
+    assert bits_equal(store["logits"], p["logits"])
+    prob = eager.Problem(p["x"].float(), p["w1"].float(), p["w2"].float(), p["widths"],
+                         p["offsets"], p["sel"].cpu(), p["wts"].cpu().float(), b)
+    ff = eager.forward(prob, "fp32")
+    f16 = eager.forward(prob, "bf16")
+    ar = ff["route"]["assignment_row"]
+    Gf = G.float()
+    L = p["logits"].float().cpu()
+    ref = eager.router_weight_logit_grad(
+        L, prob.selected, eager.combine_weight_grad(Gf, ff["y"], ar, k, T).view(T, k))
+    yard = eager.router_weight_logit_grad(
+        L, prob.selected, eager.combine_weight_grad(Gf, f16["y"], ar, k, T).view(T, k))
+    got = store["glogits"].float().cpu()
+    e_got, e_yard = _norm_err(got, ref), _norm_err(yard, ref)
+    # + 4e-3: the two bf16 roundings the yardstick leaves out (the bf16
+    # weight gradient autograd hands the router, and the bf16 logit gradient)
+    assert e_got[0] <= 2 * e_yard[0] + 4e-3 and e_got[1] <= 2 * e_yard[1] + 4e-3, (e_got, e_yard)
+    # the router weight's gradient is the linear layer's backward of it
+    wr_ref = store["glogits"].float().t() @ p["x"].to(device).float()
+    assert_close_norm(grads[True][3], wr_ref, TIGHT, f"{name} router weight grad")

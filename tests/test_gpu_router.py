@@ -243,3 +243,32 @@ def test_router_linear(T, d, E, device):
     h.remove()
     # a [B, S, d] input keeps its leading shape
     assert lin(xd.detach().reshape(1, T, d)).shape == (1, T, E)
+
+
+@pytest.mark.parametrize("T,E,k,norm", [(300, 64, 8, True), (257, 16, 2, True),
+                                        (128, 40, 5, False), (64, 128, 33, True)])
+def test_router_weight_bwd_vs_oracle(T, E, k, norm, device):
+    """Opt-in routing-weight gradient into the logits (the reference has none,
+    scatter.py:176) against float64 autograd of the reference's chain
+    (sigmoid, gather of the selected, normalisation; moe.py:168-176) for the
+    kernel's own selection: non-zero exactly on the selected experts, within
+    bf16 rounding of the output elsewhere."""
+    from triton_moe.kernels.router import RouterWeightOp
+
+    L = _logits(T, E, seed=T + E, ties=False).to(device)
+    for dt in (torch.int32, torch.int64):
+        st = router_topk(L, k, norm, index_dtype=dt)
+        Lg = L.clone().requires_grad_(True)
+        w = RouterWeightOp.apply(Lg, st.weights, st.selected, norm)
+        assert bits_equal(w, st.weights)
+        gw = torch.randn(T, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
+        w.backward(gw.to(device))
+        ref = eager.router_weight_logit_grad(L.float().cpu(), st.selected.cpu(), gw.float(), norm)
+        got = Lg.grad.float().cpu()
+        mask = torch.zeros(T, E, dtype=torch.bool).scatter_(1, st.selected.long().cpu(), True)
+        assert bool((got[~mask] == 0).all())
+        # one bf16 rounding of an fp32 value, |d| <= 2^-8 |ref|, plus fp32
+        # cancellation in g_j - sum_i g_i w_i, bounded by the gradient's scale
+        d = (got - ref.float()).abs()
+        bound = ref.abs().float() * 2.0 ** -8 + 1e-5 * ref.abs().max().float()
+        assert bool((d <= bound).all()), float((d - bound).max())

@@ -187,6 +187,48 @@ def test_combine_weight_grad_matches_autograd(T, k, d, P):
     assert bool((got[::4] == 0).all())
 
 
+def test_router_weight_logit_grad_gradcheck():
+    """The routing weights' chain into the logits: torch.autograd.gradcheck
+    (finite differences) of the weights for a fixed selection, normalised and
+    not, and the closed form dp_j = (g_j - sum_i g_i w_i) / S, dL = dp p (1 - p)
+    on the selected experts (0 elsewhere)."""
+    g = torch.Generator().manual_seed(5)
+    L = torch.randn(6, 10, generator=g, dtype=torch.float64)
+    sel = torch.topk(L, 3, dim=-1).indices
+    gw = torch.randn(6, 3, generator=g, dtype=torch.float64)
+    for norm in (True, False):
+        assert torch.autograd.gradcheck(
+            lambda x: eager.router_weights(x, sel, norm), (L.clone().requires_grad_(True),))
+        got = eager.router_weight_logit_grad(L, sel, gw, norm)
+        p = torch.sigmoid(L).gather(1, sel)
+        S = p.sum(-1, keepdim=True) + 1e-20
+        dp = (gw - (gw * p / S).sum(-1, keepdim=True)) / S if norm else gw
+        want = torch.zeros_like(L).scatter_(1, sel, dp * p * (1 - p))
+        assert torch.allclose(got, want, rtol=1e-12, atol=1e-14)
+        assert bool((got.gather(1, sel) != 0).all())
+        assert int((got != 0).sum()) == sel.numel()
+
+
+def test_module_weight_gradient_decomposes():
+    """dL/dlogits of sum(out * G) through the fp32 oracle's forward with the
+    weights a function of the logits equals router_weight_logit_grad of
+    combine_weight_grad(G, y): the per-row gradient the module computes from
+    the dH GEMM, then the router chain."""
+    prob = _problem(3, 29, 12, [(2, 24), (3, 8)], 2, 8)
+    g = torch.Generator().manual_seed(4)
+    L = torch.randn(29, 5, generator=g, dtype=torch.float64)
+    sel = prob.selected
+    Lr = L.clone().requires_grad_(True)
+    prob.weights = eager.router_weights(Lr, sel)
+    fwd = eager.forward(prob, "fp32")
+    G = torch.randn(fwd["out"].shape, generator=g, dtype=torch.float64)
+    (fwd["out"] * G).sum().backward()
+    r = fwd["route"]
+    gw = eager.combine_weight_grad(G, fwd["y"].detach(), r["assignment_row"], 2, 29)
+    got = eager.router_weight_logit_grad(L, sel, gw.view(29, 2))
+    assert torch.allclose(got, Lr.grad, rtol=1e-10, atol=1e-12)
+
+
 def test_swiglu_oracle_layout_and_silu():
     """swiglu_up against torch.nn.functional.silu on a dense single-expert
     problem and, for two experts of different widths, against column slices

@@ -103,6 +103,8 @@ struct Args {
   float* partial;    // fp32 partial tiles of split tiles (2 slots per workgroup)
   uint32_t* arrive;  // split-K arrival words, kConsumers per workgroup (zero between launches)
   int grid;          // GEMM workgroups
+  float* row_dot;    // DOWN_DH with pre: per (row, 64-column block) sum of GH * PRE^2 (nullable)
+  int64_t ld_rd;     // its leading dimension (floats)
 };
 
 // Metadata of one expert as the GEMMs read it: its row range [t0, t1) in
@@ -988,9 +990,11 @@ struct Gemm {
   // scratch and is read back as 128-byte row segments, so a store
   // instruction writes 8 whole cache lines (the accumulator layout alone
   // gives 8 bytes per lane over 32 rows). Row r holds its 16 8-byte
-  // half-chunks hc at position hc ^ ((r >> 1) & 15): the 32 lanes of one
-  // write phase (32 rows, same half-chunk) then hit 32 distinct bank pairs,
-  // and a 16-lane read phase covers two whole rows.
+  // half-chunks hc at position hc ^ (r & 15). ds_write_b64 serves 16
+  // consecutive lanes per cycle over 32 dword banks (128 B; measured: a
+  // (r >> 1) swizzle conflicts 2-way there and takes twice the cycles), and
+  // 16 rows with one half-chunk then fill the 32 banks exactly; a 16-lane
+  // ds_read_b128 phase covers two whole rows over all 64 banks.
   static constexpr int EPI_BYTES = 32 * 64 * 2;
   static_assert(WN == 64 && FN == 2 && FM == 2, "epilogue assumes 64x64 wave tiles");
   // UP_FWD with relu^2 stores PRE and H; every other variant one output.
@@ -1007,7 +1011,7 @@ struct Gemm {
     int mask;                      // bit u: unit u still to be stored
   };
 
-  __device__ static int epi_off(int r, int hc) { return r * 128 + ((hc ^ ((r >> 1) & 15)) << 3); }
+  __device__ static int epi_off(int r, int hc) { return r * 128 + ((hc ^ (r & 15)) << 3); }
 
   // Packed block (out, i) into the wave's scratch: lane (r = lane & 31,
   // h = lane >> 5) holds for each (j, g) the 4 values at columns
@@ -1028,7 +1032,7 @@ struct Gemm {
   // Row 8q + (lane >> 3), columns 8 (lane & 7) .. +7 of the scratch block.
   __device__ __forceinline__ static uint4 epi_read(const lds_char* scr, int q, int lane) {
     const int r = 8 * q + (lane >> 3), c = lane & 7;
-    const int f = (r >> 1) & 15;
+    const int f = r & 15;
     const u32x4_t v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
         scr + r * 128 + ((((2 * c) ^ f) >> 1) << 4));
     // Half-chunks 2c and 2c + 1 sit swapped when f is odd.
@@ -1165,23 +1169,38 @@ struct Gemm {
     const bool n_ok = n < pd.N;
     if (V == DOWN_DH && p.pre) {
       // GA = bf16(pre > 0 ? 2 * GH * pre : 0), GH the bf16-rounded dH
-      // (grouped_gemm.py:751-766), with PRE from load_pre.
+      // (grouped_gemm.py:751-766), with PRE from load_pre. With row_dot, the
+      // wave also sums GH * PRE^2 over each row's 64 columns (8 lanes of 8
+      // columns, added with DPP moves in a fixed order): the gradient of the
+      // row's routing weight is that sum over the row's blocks divided by
+      // the weight (the module's H' is w * relu(z)^2).
+      const bool dot = p.row_dot != nullptr;
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const uint4 gh = epi_read(scr, qq, lane);
         const int m = mb + 8 * qq + (lane >> 3);
-        if (m >= pd.M || !n_ok) continue;
-        const uint32_t gw[4] = {gh.x, gh.y, gh.z, gh.w};
-        const uint32_t pw[4] = {pr[qq].x, pr[qq].y, pr[qq].z, pr[qq].w};
-        uint32_t o[4];
+        float s = 0.0f;
+        if (m < pd.M && n_ok) {
+          const uint32_t gw[4] = {gh.x, gh.y, gh.z, gh.w};
+          const uint32_t pw[4] = {pr[qq].x, pr[qq].y, pr[qq].z, pr[qq].w};
+          uint32_t o[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float pl = lo_f32(pw[t]), ph = hi_f32(pw[t]);
-          o[t] = pack_bf16(pl > 0.0f ? lo_f32(gw[t]) * 2.0f * pl : 0.0f,
-                           ph > 0.0f ? hi_f32(gw[t]) * 2.0f * ph : 0.0f);
+          for (int t = 0; t < 4; ++t) {
+            const float pl = lo_f32(pw[t]), ph = hi_f32(pw[t]);
+            o[t] = pack_bf16(pl > 0.0f ? lo_f32(gw[t]) * 2.0f * pl : 0.0f,
+                             ph > 0.0f ? hi_f32(gw[t]) * 2.0f * ph : 0.0f);
+            if (dot) s += lo_f32(gw[t]) * (pl * pl) + hi_f32(gw[t]) * (ph * ph);
+          }
+          *reinterpret_cast<uint4*>(p.c + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n) =
+              make_uint4(o[0], o[1], o[2], o[3]);
         }
-        *reinterpret_cast<uint4*>(p.c + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n) =
-            make_uint4(o[0], o[1], o[2], o[3]);
+        if (dot) {
+          s += dpp_f32<0xB1>(s);   // quad_perm [1, 0, 3, 2]
+          s += dpp_f32<0x4E>(s);   // quad_perm [2, 3, 0, 1]
+          s += dpp_f32<0x141>(s);  // row_half_mirror: the other quad of 8 lanes
+          if ((lane & 7) == 0 && m < pd.M && pd.nb < pd.N)
+            p.row_dot[((int64_t)pd.cr + m) * p.ld_rd + ((pd.cc + pd.nb) >> 6)] = s;
+        }
       }
       return;
     }
@@ -1954,10 +1973,11 @@ extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64
                                      const int32_t* eto, const int32_t* ewo,
                                      const int32_t* widths, const int32_t* tpe, int32_t E,
                                      int64_t hidden, int64_t max_width, int64_t rows_bound,
-                                     vmoe_stream_t stream) {
+                                     float* row_dot, int64_t ld_row_dot, vmoe_stream_t stream) {
   int st = check_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
   if (st) return st;
   if (!grad_y || !w2 || !grad_h || gy_rows < 0) return VMOE_ERR_INVALID_ARG;
+  if (row_dot && (!pre_act || ld_row_dot < (max_width + 63) / 64)) return VMOE_ERR_INVALID_ARG;
   if (!src_ld_ok(ldgy, hidden, gather_map) || !ld_ok(ldw2) || !ld_ok(ldgh) || ldw2 < hidden ||
       ldgh < max_width)
     return VMOE_ERR_UNSUPPORTED;
@@ -1971,6 +1991,7 @@ extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64
   p.pre = pre_act;
   p.row_scale = row_scale;
   p.gscale = grad_scale;
+  p.row_dot = row_dot; p.ld_rd = ld_row_dot;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
   return launch<DOWN_DH>(p, row_items<DOWN_DH>(rows_bound, E, max_width),

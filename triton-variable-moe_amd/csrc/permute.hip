@@ -342,6 +342,34 @@ __global__ __launch_bounds__(kThreads) void combine_wgrad_kernel(
   }
 }
 
+// Routing-weight gradient of the module path, whose up GEMM writes
+// H' = bf16(w * relu(z)^2): dL/dw of a row is sum_c dL/dH'[c] * relu(z)[c]^2.
+// The dH GEMM leaves row_dot[row][b] = sum over block b of
+// bf16(w * dL/dH') * PRE^2 (vmoe_gemm_down_bwd_dh); here the blocks are
+// summed in order and divided by w, one thread per assignment:
+//   gw[a] = bf16(sum_b row_dot[row][b] / w[row]), row = assignment_row[a],
+// 0 where row < 0 (a dropped assignment) or w[row] == 0.
+__global__ __launch_bounds__(kThreads) void routing_wgrad_kernel(
+    const float* __restrict__ row_dot, int64_t ld, int nblk, int64_t rows,
+    const float* __restrict__ row_weight, const int32_t* __restrict__ assignment_row,
+    int64_t A, uint16_t* __restrict__ gw) {
+  for (int64_t a = (int64_t)blockIdx.x * kThreads + threadIdx.x; a < A;
+       a += (int64_t)gridDim.x * kThreads) {
+    const int32_t row = assignment_row[a];
+    float g = 0.0f;
+    if (row >= 0 && row < rows) {
+      const float w = row_weight[row];
+      if (w != 0.0f) {
+        const float* rd = row_dot + (int64_t)row * ld;
+        float s = 0.0f;
+        for (int b = 0; b < nblk; ++b) s += rd[b];
+        g = s / w;
+      }
+    }
+    gw[a] = (uint16_t)f32_to_bf16(g);
+  }
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 inline int row_grid(int64_t rows) {
@@ -476,6 +504,25 @@ extern "C" int vmoe_combine_weight_grad(const uint16_t* grad, int64_t ldg, const
   else
     hipLaunchKernelGGL((combine_wgrad_kernel<1>), grid, block, 0, s, grad, ldg, y, y_rows, ldy,
                        assignment_row, top_k, grad_weights, num_tokens, hidden);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_routing_weight_grad(const float* row_dot, int64_t ld_row_dot,
+                                        int32_t num_blocks, int64_t rows,
+                                        const float* row_weight, const int32_t* assignment_row,
+                                        int64_t num_assignments, uint16_t* grad_weights,
+                                        vmoe_stream_t stream) {
+  if (num_assignments < 0 || rows < 0 || num_blocks < 0 || ld_row_dot < num_blocks)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_assignments == 0) return VMOE_OK;
+  if (!grad_weights || !assignment_row || (rows > 0 && (!row_weight || (num_blocks > 0 && !row_dot))))
+    return VMOE_ERR_INVALID_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t g = std::min<int64_t>((num_assignments + kThreads - 1) / kThreads, 65536);
+  hipLaunchKernelGGL(routing_wgrad_kernel, dim3((unsigned)g), dim3(kThreads), 0, s, row_dot,
+                     ld_row_dot, num_blocks, rows, row_weight, assignment_row, num_assignments,
+                     grad_weights);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }

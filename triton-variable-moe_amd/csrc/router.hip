@@ -637,6 +637,59 @@ __global__ __launch_bounds__(kRtThreads) void router_aux_bwd_kernel(
   }
 }
 
+// Gradient of the routing weights with respect to the logits (opt-in; the
+// reference's weights get none, scatter.py:176), one wave per token, lane j
+// < k holding slot j: p_j = sigmoid(float(L[t, s_j])) as in the forward,
+// g_j = grad_w[t, j], then
+//   normalised:   S = sum_j p_j + 1e-20, dp_j = (g_j - sum_i g_i p_i / S) / S
+//   otherwise:    dp_j = g_j
+// and grad[t, e] = bf16(dp_j p_j (1 - p_j)) for e = s_j, 0 for the other
+// experts (torch.topk's backward scatters into zeros; sigmoid's is
+// g y (1 - y)). The sums run in the DPP order of wave_sum_f32.
+template <int VPL>
+__global__ __launch_bounds__(kRtThreads) void router_weight_bwd_kernel(
+    const uint16_t* __restrict__ logits, int64_t ldl, int64_t T, int E, int k, int norm,
+    const int32_t* __restrict__ sel32, const int64_t* __restrict__ sel64,
+    const uint16_t* __restrict__ gw, int64_t ldgw, uint16_t* __restrict__ grad, int64_t ldg) {
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  for (int64_t t = (int64_t)blockIdx.x * kRtWaves + wv; t < T;
+       t += (int64_t)gridDim.x * kRtWaves) {
+    int e = -1;
+    float p = 0.0f, g = 0.0f;
+    if (lane < k) {
+      e = sel32 ? sel32[t * k + lane] : (int)sel64[t * k + lane];
+      if (e >= 0 && e < E) {
+        p = sigmoidf(bf16_to_f32(logits[t * ldl + e]));
+        g = bf16_to_f32(gw[t * ldgw + lane]);
+      } else {
+        e = -1;
+      }
+    }
+    float dp = g;
+    if (norm) {
+      const float S = wave_sum_f32(p) + 1e-20f;
+      const float gp = wave_sum_f32(g * p);
+      dp = (g - gp / S) / S;
+    }
+    const float dl = dp * p * (1.0f - p);
+    float val[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) val[v] = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      const int ej = __shfl(e, j, kWave);
+      const float dj = __shfl(dl, j, kWave);
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+        if (ej == lane + v * kWave) val[v] = dj;
+    }
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int ee = lane + v * kWave;
+      if (ee < E) grad[t * ldg + ee] = (uint16_t)f32_to_bf16(val[v]);
+    }
+  }
+}
+
 inline int vpl_of(int E) {
   int v = 1;
   while (v * kWave < E) v <<= 1;
@@ -905,6 +958,43 @@ extern "C" int vmoe_router_aux_bwd(const uint16_t* logits, int64_t ld_logits, in
     VMOE_RB_CASE(16)
     VMOE_RB_CASE(32)
 #undef VMOE_RB_CASE
+    default:
+      return VMOE_ERR_UNSUPPORTED;
+  }
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_router_weight_bwd(const uint16_t* logits, int64_t ld_logits,
+                                      int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                                      int32_t normalize, const int32_t* selected,
+                                      const int64_t* selected_i64, const uint16_t* grad_weights,
+                                      int64_t ld_grad_weights, uint16_t* grad_logits,
+                                      int64_t ld_grad, vmoe_stream_t stream) {
+  if (num_tokens < 0 || num_experts <= 0 || top_k <= 0 || top_k > num_experts ||
+      ld_logits < num_experts || ld_grad < num_experts || ld_grad_weights < top_k)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_experts > kRtMaxExperts || top_k > kWave) return VMOE_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return VMOE_OK;
+  if (!logits || !grad_weights || !grad_logits || (!selected == !selected_i64))
+    return VMOE_ERR_INVALID_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t g = std::min<int64_t>((num_tokens + kRtWaves - 1) / kRtWaves, 4096);
+  switch (vpl_of(num_experts)) {
+#define VMOE_RW_CASE(V)                                                                      \
+  case V:                                                                                    \
+    hipLaunchKernelGGL(router_weight_bwd_kernel<V>, dim3((unsigned)g), dim3(kRtThreads), 0,  \
+                       s, logits, ld_logits, num_tokens, num_experts, top_k, normalize,       \
+                       selected, selected_i64, grad_weights, ld_grad_weights, grad_logits,    \
+                       ld_grad);                                                              \
+    break;
+    VMOE_RW_CASE(1)
+    VMOE_RW_CASE(2)
+    VMOE_RW_CASE(4)
+    VMOE_RW_CASE(8)
+    VMOE_RW_CASE(16)
+    VMOE_RW_CASE(32)
+#undef VMOE_RW_CASE
     default:
       return VMOE_ERR_UNSUPPORTED;
   }

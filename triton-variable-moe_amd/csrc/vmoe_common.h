@@ -43,6 +43,13 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) { return pack_bf16(f, 0
 __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
+// v of the lane a DPP control selects (every lane active; quad_perm 0xB1 /
+// 0x4E swap lanes 1 / 2 apart, row_half_mirror 0x141 reverses 8 lanes).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
 // Count of set bits of `mask` in lanes below the calling lane.
 __device__ __forceinline__ int lanes_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),

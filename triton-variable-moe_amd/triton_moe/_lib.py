@@ -36,6 +36,7 @@ _SIGNATURES = {
                            _vp],
     "vmoe_combine": [_vp, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp],
     "vmoe_combine_weight_grad": [_vp, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _vp],
+    "vmoe_routing_weight_grad": [_vp, _i64, _i32, _i64, _vp, _vp, _i64, _vp, _vp],
     "vmoe_gemm_up_fwd": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp,
                          _vp, _vp, _i32, _i64, _i64, _i64, _vp],
     "vmoe_gemm_down_fwd": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
@@ -49,7 +50,7 @@ _SIGNATURES = {
     "vmoe_gemm_up_bwd_dw": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp,
                             _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
     "vmoe_gemm_down_bwd_dh": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp,
-                              _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+                              _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _i64, _vp],
     "vmoe_gemm_down_bwd_dw": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
                               _vp, _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
     "vmoe_zero_tail_cols": [_vp, _i64, _vp, _vp, _i32, _i64, _i64, _vp],
@@ -60,6 +61,8 @@ _SIGNATURES = {
     "vmoe_router_aux": [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "vmoe_router_aux_bwd": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                             _vp],
+    "vmoe_router_weight_bwd": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _i64,
+                               _vp],
 }
 _RESTYPES = {
     "vmoe_status_string": ctypes.c_char_p,

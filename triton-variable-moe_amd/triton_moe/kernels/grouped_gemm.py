@@ -334,12 +334,13 @@ def _grad_source(grad_y, m: GemmMeta, gather_map):
 
 def down_bwd_dh(grad_y, w2, m: GemmMeta, hidden: int, zero_tails: bool,
                 pre: torch.Tensor | None = None, gather_map: torch.Tensor | None = None,
-                row_scale: torch.Tensor | None = None):
+                row_scale: torch.Tensor | None = None, row_dot: torch.Tensor | None = None):
     """grad_intermediate [rows, max_width] = grad_y_e @ W2_e^T; with pre, the
     relu^2 gradient GA instead (fused in the epilogue). With gather_map,
     grad_y holds one row per token and row r is grad_y[gather_map[r]] (-1:
     zeros); with row_scale (fp32 per row) the gradient w.r.t. H is scaled by
-    it before the relu^2 rule."""
+    it before the relu^2 rule. row_dot (fp32 [rows, ceil(max_width / 64)],
+    needs pre) receives per 64-column block the sums of GH * pre^2."""
     g, ldg, g_rows, gs = _grad_source(grad_y, m, gather_map)
     w2 = _bf16(w2, "grouped_gemm_down_backward w2")
     _need(w2.shape[1] == hidden and g.shape[1] == hidden,
@@ -350,11 +351,16 @@ def down_bwd_dh(grad_y, w2, m: GemmMeta, hidden: int, zero_tails: bool,
         _need(pre.shape[0] >= m.rows and pre.stride(0) == grad_h.stride(0),
               "pre_act must match the [rows, max_expert_width] layout")
     gm = None if gather_map is None else _i32(gather_map)
+    if row_dot is not None:
+        _need(pre is not None and row_dot.dtype == torch.float32 and row_dot.stride(1) == 1
+              and row_dot.shape[0] >= m.rows and row_dot.shape[1] >= (m.max_width + 63) // 64,
+              "row_dot must be fp32 [rows, ceil(max_width / 64)] and needs pre_act")
     if m.rows > 0:
         _lib.call("vmoe_gemm_down_bwd_dh", g.data_ptr(), ldg, g_rows, _lib.ptr(gm),
                   _lib.ptr(gs), w2.data_ptr(), w2.stride(0), _lib.ptr(pre),
                   _lib.ptr(_f32_rows(row_scale, m.rows, "row_scale")), grad_h.data_ptr(),
                   grad_h.stride(0), *_meta_args(m), hidden, m.max_width, m.rows,
+                  _lib.ptr(row_dot), 0 if row_dot is None else row_dot.stride(0),
                   _lib.stream(g.device))
         if zero_tails:
             _zero_tails(grad_h, m)
@@ -704,13 +710,16 @@ class RoutedMoEOp(torch.autograd.Function):
     rule (w_r (G @ W2^T) = GY @ W2^T), and the dW2 GEMM reads G through the
     map against H' (H'^T G = H^T GY). The products are the reference's; only
     where they round to bf16 moves. The routing weights get no gradient, as
-    in the reference (scatter.py:176).
+    in the reference (scatter.py:176), unless they are passed as `weights`
+    (bf16 [A], the tensor row_weight was formed from): then the dH GEMM also
+    sums GH * PRE^2 per row and block, and dL/dw = that sum / w (H' = w h,
+    h = relu(z)^2 read back as PRE^2) is returned for them.
     """
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx, x_flat, w1, w2, meta, gather_map, row_weight, assignment_row, top_k,
-                hidden_size):
+                hidden_size, weights=None):
         from .gather import combine_rows
 
         h, pre = up_fwd(x_flat, w1, meta, _lib.ACT_RELU_SQUARED, True, zero_tails=False,
@@ -721,6 +730,7 @@ class RoutedMoEOp(torch.autograd.Function):
         ctx.meta = meta
         ctx.hidden_size = hidden_size
         ctx.top_k = top_k
+        ctx.weights_shape = None if weights is None else weights.shape
         return out
 
     @staticmethod
@@ -739,7 +749,13 @@ class RoutedMoEOp(torch.autograd.Function):
         main = torch.cuda.current_stream(grad_out.device)
         side = _side_stream(grad_out.device) if BACKWARD_SIDE_STREAM else main
         side.wait_stream(main)
-        ga = down_bwd_dh(grad_out, w2, m, d, False, pre=pre, gather_map=gm, row_scale=rw)
+        row_dot = None
+        if ctx.weights_shape is not None and ctx.needs_input_grad[9]:
+            nblk = (m.max_width + 63) // 64
+            alloc = torch.empty if m.uniform else torch.zeros  # blocks past w_e stay 0
+            row_dot = alloc(m.rows, nblk, dtype=torch.float32, device=grad_out.device)
+        ga = down_bwd_dh(grad_out, w2, m, d, False, pre=pre, gather_map=gm, row_scale=rw,
+                         row_dot=row_dot)
         with torch.cuda.stream(side):
             grad_w2 = down_bwd_dw(grad_out, h, w2, m, d, gather_map=gm)
         side.wait_stream(main)
@@ -754,4 +770,11 @@ class RoutedMoEOp(torch.autograd.Function):
             t.record_stream(side)
         for t in (grad_w1, grad_w2):
             t.record_stream(main)
-        return grad_x, grad_w1, grad_w2, None, None, None, None, None, None
+        grad_weights = None
+        if row_dot is not None:
+            grad_weights = torch.empty(ctx.weights_shape, dtype=torch.bfloat16,
+                                       device=grad_out.device)
+            _lib.call("vmoe_routing_weight_grad", row_dot.data_ptr(), row_dot.stride(0),
+                      row_dot.shape[1], m.rows, rw.data_ptr(), ar.data_ptr(), ar.numel(),
+                      grad_weights.data_ptr(), _lib.stream(grad_out.device))
+        return grad_x, grad_w1, grad_w2, None, None, None, None, None, None, grad_weights

@@ -7,7 +7,8 @@ PyTorch launches per step. Here one kernel does the routing and the
 per-token reductions, and one single-workgroup kernel finishes the losses
 after the routing counts exist. The losses are differentiable with respect
 to the router logits (their gradient is one elementwise kernel); the top-k
-weights are not, as in the reference (scatter.py:176).
+weights are not, as in the reference (scatter.py:176), unless a caller opts
+in through RouterWeightOp (TritonMoEConfig.routing_weight_grad).
 
 Top-k: the expert ids come out in torch.topk's order on ROCm, ties
 included, and the normalised weights carry the bits of the reference's
@@ -170,6 +171,38 @@ class RouterAuxOp(torch.autograd.Function):
                   _lib.ptr(gz), _lib.ptr(glb), _lib.ptr(gcl), grad.data_ptr(), grad.stride(0),
                   _lib.stream(logits.device))
         return grad, None, None, None, None, None, None
+
+
+class RouterWeightOp(torch.autograd.Function):
+    """The routing weights router_topk returned, as a differentiable function
+    of the router logits (opt-in; the reference's weights get no gradient,
+    scatter.py:176): backward is the chain of the reference's
+    sigmoid -> topk -> normalise (moe.py:168-176) for the selected experts,
+    0 for the others (vmoe_router_weight_bwd)."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, logits, weights, selected, normalize):
+        ctx.save_for_backward(logits, selected)
+        ctx.normalize = bool(normalize)
+        return weights.clone()
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, g_w):
+        logits, selected = ctx.saved_tensors
+        T, E = logits.shape
+        k = selected.shape[-1]
+        g = g_w.reshape(T, k).to(torch.bfloat16).contiguous()
+        sel = selected.reshape(T, k).contiguous()
+        is64 = sel.dtype == torch.int64
+        grad = torch.empty(T, E, dtype=torch.bfloat16, device=logits.device)
+        _lib.call("vmoe_router_weight_bwd", logits.data_ptr(), logits.stride(0), T, E, k,
+                  int(ctx.normalize), None if is64 else sel.data_ptr(),
+                  sel.data_ptr() if is64 else None, g.data_ptr(), g.stride(0), grad.data_ptr(),
+                  grad.stride(0), _lib.stream(logits.device))
+        return grad, None, None, None
 
 
 def load_balance_coef(expert_sizes) -> list[float]:

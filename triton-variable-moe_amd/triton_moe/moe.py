@@ -37,7 +37,8 @@ from . import _lib
 from .kernels.fused_cumsum import route_device
 from .kernels.gather import combine_rows
 from .kernels.grouped_gemm import GemmMeta, RoutedMoEOp, down_fwd, up_fwd
-from .kernels.router import RouterAuxOp, RouterLinear, load_balance_coef, router_topk
+from .kernels.router import (RouterAuxOp, RouterLinear, RouterWeightOp, load_balance_coef,
+                             router_topk)
 
 
 @dataclass
@@ -50,6 +51,10 @@ class TritonMoEConfig:
     norm_topk_prob: bool = True
     block_size: int = 64
     use_megablocks_gather_scatter: bool = False
+    # Not in the reference (its routing weights get no gradient, scatter.py:176):
+    # when set, forward() differentiates the output through the routing
+    # weights into the router logits.
+    routing_weight_grad: bool = False
 
 
 class TritonMoEMLP(nn.Module):
@@ -164,7 +169,9 @@ class TritonMoEMLP(nn.Module):
         return aux_loss, f_i.to(dtype)
 
     def _experts(self, x_flat, top_k_weights_flat, selected_experts_flat):
-        """Routing + expert MLP + combine on the HIP kernels, no host sync."""
+        """Routing + expert MLP + combine on the HIP kernels, no host sync.
+        The expert path differentiates through top_k_weights_flat only when
+        it requires grad (routing_weight_grad)."""
         k = self.num_active_experts
         # Pad rows of the row map are -1 (the GEMMs' fused gather reads zeros
         # for them); row_weight holds each row's routing weight.
@@ -174,9 +181,12 @@ class TritonMoEMLP(nn.Module):
         # out of the routing kernel (moe.py:193-202 of the reference).
         meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
                         self.expert_widths_t, r.padded_counts, self.num_experts,
-                        self.max_expert_width, r.rows_bound)
+                        self.max_expert_width, r.rows_bound,
+                        uniform=len(set(self.expert_widths)) == 1)
+        weights = top_k_weights_flat if top_k_weights_flat.requires_grad else None
         output_flat = RoutedMoEOp.apply(x_flat, self.w1, self.w2, meta, r.gather_map,
-                                        r.row_weight, r.assignment_row, k, self.config.n_embd)
+                                        r.row_weight, r.assignment_row, k, self.config.n_embd,
+                                        weights)
         return output_flat, r.tokens_per_expert
 
     @torch.compiler.disable
@@ -188,8 +198,12 @@ class TritonMoEMLP(nn.Module):
         x_flat = rearrange(x, "b s d -> (b s) d")
         router_logits = self.router(x_flat)
         state = router_topk(router_logits, self.num_active_experts, self.norm_topk_prob)
+        weights = state.weights
+        if self.config.routing_weight_grad and torch.is_grad_enabled():
+            weights = RouterWeightOp.apply(router_logits, weights, state.selected,
+                                           self.norm_topk_prob)
         output_flat, tokens_per_expert = self._experts(
-            x_flat, state.weights.reshape(-1), state.selected.reshape(-1))
+            x_flat, weights.reshape(-1), state.selected.reshape(-1))
         output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
         aux_loss, f_i = self._aux(router_logits, state, tokens_per_expert, x.dtype)
         return output, aux_loss, f_i
