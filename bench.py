@@ -61,6 +61,8 @@ def parse():
                     help="only measure the box's practical ceilings: dense bf16 torch.matmul "
                          "(hipBLASLt) at square and MoE-like shapes, and device copy / fill "
                          "bandwidth")
+    ap.add_argument("--graph", action="store_true",
+                    help="also time the step replayed from a HIP graph (graph_ms_per_step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 1 GiB device buffer 5 times: the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -236,6 +238,47 @@ def make_step(m, xb):
     return step
 
 
+def time_graph_steps(m, xb, steps, warmup):
+    """The same step captured once into a HIP graph (torch.cuda.graph) and
+    replayed: forward and backward of out.sum()'s gradient (a broadcast row
+    of ones, passed directly, so that no reduction kernel with a memset node
+    sits in the graph); gradients are re-created inside the capture
+    (zero_grad(set_to_none=True)), as the eager step does. Every launch of the
+    eager step except the loss reduction and its fills is replayed; the host's
+    per-launch work is gone."""
+    import torch
+
+    T, d = xb.shape[1], xb.shape[2]
+    gout = torch.ones(1, 1, d, dtype=xb.dtype, device=xb.device).expand(xb.shape)
+
+    def step():
+        m.zero_grad(set_to_none=True)
+        xb.grad = None
+        out, _, _ = m(xb)
+        out.backward(gout)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    del g
+    return ms
+
+
 def time_steps(m, xb, steps, warmup):
     import torch
 
@@ -317,6 +360,13 @@ def kernel_breakdown(m, xb, steps):
     side = gg.BACKWARD_SIDE_STREAM
     gg.BACKWARD_SIDE_STREAM = False
     try:
+        # A bounded spin kernel (torch.cuda._sleep) holds the GPU while the
+        # host queues every timed step, so the launches then run back to
+        # back: an event pair around a launch the host has not yet queued
+        # would also time the host's launch latency (small configurations
+        # are host-bound otherwise).
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(3e6) * steps)
         for _ in range(steps):
             timer.new_step()
             step()
@@ -406,6 +456,7 @@ def main():
 
     ms = time_steps(m, xb, args.steps, args.warmup)
     value = flops / (ms * 1e-3) / 1e12
+    graph_ms = time_graph_steps(m, xb, args.steps, args.warmup) if args.graph else None
     kern = kernel_breakdown(m, xb, args.kernel_steps)
     gemm_names = [n for n in kern if n.startswith("gemm_")]
     gemm_us = sum(kern[n] for n in gemm_names)
@@ -463,6 +514,7 @@ def main():
         "routing_us": round(kern["route"], 2),
         "router_topk_us": round(kern.get("router_topk", 0.0), 2),
         "kernel_us": {n: round(v, 2) for n, v in kern.items()},
+        "graph_ms_per_step": None if graph_ms is None else round(graph_ms, 4),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),

@@ -766,10 +766,12 @@ class RoutedMoEOp(torch.autograd.Function):
         main.wait_stream(side)
         # Cross-stream lifetimes for the caching allocator: main's tensors
         # read on the side stream, the side stream's results used on main.
-        for t in (grad_out, ga, h, x_flat, gm, w1, w2):
-            t.record_stream(side)
-        for t in (grad_w1, grad_w2):
-            t.record_stream(main)
+        # (Under graph capture the graph's private pool keeps them alive.)
+        if side is not main and not torch.cuda.is_current_stream_capturing():
+            for t in (grad_out, ga, h, x_flat, gm, w1, w2):
+                t.record_stream(side)
+            for t in (grad_w1, grad_w2):
+                t.record_stream(main)
         grad_weights = None
         if row_dot is not None:
             grad_weights = torch.empty(ctx.weights_shape, dtype=torch.bfloat16,
