@@ -392,12 +392,15 @@ __host__ __device__ __forceinline__ int work_items(int tiles, int chunks) {
 struct Meta {
   int pre[kMaxExperts + 1];
   int rec[6][kRecExperts];
-  int lane_beg[kMaxLanes + 1];  // dW GEMMs: first item of each lane (lane_beg[NL] = total)
+  // dW GEMMs: first item of each lane (lane_beg[NL] = total); row-tiled
+  // GEMMs: first item of each XCD's range (lane_beg[8] = total)
+  int lane_beg[kMaxLanes + 1];
 };
 
 // Work-item range of workgroup b. Round-robin: XCD x (hardware deals
-// workgroup b to XCD b % 8) owns the contiguous range [x * total / 8,
-// (x + 1) * total / 8), so the tiles of one expert share an L2, and its
+// workgroup b to XCD b % 8) owns the contiguous range [lane_beg[x],
+// lane_beg[x + 1]) of items, an eighth of the estimated cost (see
+// build_meta), so the tiles of one expert share an L2, and its
 // workgroups take every (grid / 8)-th item. Contig (grid a multiple of
 // 8 * kLane): the j-th workgroup of XCD x (j = b / 8) is slot j % kLane of
 // lane l = x * (grid / 8 / kLane) + j / kLane; lane l owns items
@@ -425,8 +428,8 @@ __device__ __forceinline__ Range item_range(int total, const int* lane_beg) {
     r.end = lane_beg[lane + 1];
     r.stride = 1;
   } else {
-    r.beg = (int)((int64_t)total * xcd / 8) + j;
-    r.end = (int)((int64_t)total * (xcd + 1) / 8);
+    r.beg = lane_beg[xcd] + j;
+    r.end = lane_beg[xcd + 1];
     r.stride = per;
   }
   return r;
@@ -765,7 +768,12 @@ struct Gemm {
   // lanes of the many small ones. Lane l starts at the first item at or
   // after cumulative cost cost_total * l / NL. `cpre` is LDS scratch for
   // E + 1 ints (the ring, before its first use).
-  static constexpr int kItemCost = 2, kEpiCost = 4;
+  // Row-tiled GEMMs split their items into the 8 XCDs' ranges the same way,
+  // an item (a tile) costing its k-steps plus kTileCost: where K differs
+  // between experts (K = w_e for the down projection and dX), equal item
+  // counts gave the XCDs holding the widest experts several times the work
+  // of the others (workgroups ending between 430 and 1225 us at cfg4).
+  static constexpr int kItemCost = 2, kEpiCost = 4, kTileCost = 3;
   __device__ static int build_meta(const Args& p, Meta& mt, long long* scan,
                                    __attribute__((address_space(3))) int* cpre) {
     constexpr bool CONTIG = Cfg<V>::contig;
@@ -785,6 +793,8 @@ struct Gemm {
         items = work_items<V>(tiles, chunks);
         if (CONTIG)
           cost = cdiv(tiles, kLane) * (cdiv(q.K, BK) + kItemCost * chunks + kEpiCost);
+        else
+          cost = items * (cdiv(q.K, BK) + kTileCost);
       }
       // One scan of (cost << 32 | items): both prefixes stay below 2^31.
       long long total;
@@ -792,7 +802,7 @@ struct Gemm {
           ((long long)cost << 32) | (long long)items, scan, &total);
       if (e < p.E) {
         mt.pre[e] = (int)(base + (ex & 0xFFFFFFFFll));
-        if (CONTIG) cpre[e] = (int)(cbase + (ex >> 32));
+        cpre[e] = (int)(cbase + (ex >> 32));
       }
       base += total & 0xFFFFFFFFll;
       cbase += total >> 32;
@@ -800,11 +810,11 @@ struct Gemm {
     }
     if (threadIdx.x == 0) {
       mt.pre[p.E] = (int)base;
-      if (CONTIG) cpre[p.E] = (int)cbase;
+      cpre[p.E] = (int)cbase;
     }
     __syncthreads();
-    if (CONTIG) {
-      const int NL = (int)gridDim.x / kLane;
+    {
+      const int NL = CONTIG ? (int)gridDim.x / kLane : 8;
       for (int l = threadIdx.x; l <= NL; l += kThreads) {
         int item = (int)base;
         if (l == 0 || cbase == 0) {
@@ -826,13 +836,20 @@ struct Gemm {
           const Prob q = T::prob(p, r);
           int tiles, chunks;
           expert_work<V>(p, q, tiles, chunks);
-          const int gcost = cdiv(q.K, BK) + kItemCost * chunks + kEpiCost;
           const int o = target - cpre[e];
-          const int g = udiv_small(o, gcost), rem = o - g * gcost;
-          // first item of group g starting at or after rem: chunk c starts
-          // at cost c * (kDwChunk / BK + kItemCost); past the last chunk,
-          // the next group's first item
-          item = mt.pre[e] + g * chunks + min(chunks, cdiv(rem, kDwChunk / BK + kItemCost));
+          if (CONTIG) {
+            const int gcost = cdiv(q.K, BK) + kItemCost * chunks + kEpiCost;
+            const int g = udiv_small(o, gcost), rem = o - g * gcost;
+            // first item of group g starting at or after rem: chunk c starts
+            // at cost c * (kDwChunk / BK + kItemCost); past the last chunk,
+            // the next group's first item
+            item = mt.pre[e] + g * chunks + min(chunks, cdiv(rem, kDwChunk / BK + kItemCost));
+          } else {
+            // the first tile starting at or after the target
+            const int tcost = cdiv(q.K, BK) + kTileCost;
+            const int g = udiv_small(o, tcost);
+            item = mt.pre[e] + min(tiles, g + (o - g * tcost > 0 ? 1 : 0));
+          }
         }
         mt.lane_beg[l] = item;
       }
