@@ -298,7 +298,9 @@ def time_steps(m, xb, steps, warmup):
 OP_OF = {
     "vmoe_router_logits": ("router_logits",),
     "vmoe_router_topk": ("router_topk",),
+    "vmoe_router_topk_hist": ("router_topk",),
     "vmoe_route": ("route",),
+    "vmoe_route_counted": ("route",),
     "vmoe_gemm_up_fwd": ("gemm_up_fwd",),
     "vmoe_gemm_down_fwd": ("gemm_down_fwd",),
     "vmoe_combine": ("combine", "gather_bwd_combine"),
@@ -510,7 +512,9 @@ def main():
         "gemm_pct_mfma_peak": round(100 * gemm_tflops / PEAK_BF16_TFLOPS, 2),
         "permutation_gbs": round(perm_gbs, 1),
         "permutation_pct_hbm_peak": round(100 * perm_gbs / PEAK_HBM_GBS, 2),
-        "permutation_scope": "both combines + routing (vmoe_route), bytes and time",
+        "permutation_scope": "both combines + routing (vmoe_route_counted; the per-tile "
+                             "expert counts come out of the top-k launch, router_topk_us), "
+                             "bytes and time",
         "routing_us": round(kern["route"], 2),
         "router_topk_us": round(kern.get("router_topk", 0.0), 2),
         "kernel_us": {n: round(v, 2) for n, v in kern.items()},

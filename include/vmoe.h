@@ -84,6 +84,24 @@ int vmoe_route(const void* selected_experts, int32_t selected_is_int64,
                float* row_weight, void* workspace, size_t workspace_bytes,
                vmoe_stream_t stream);
 
+/* vmoe_route for selections whose per-block histograms vmoe_router_topk_hist
+ * already wrote into `workspace` (vmoe_route_counted_workspace_bytes(
+ * num_assignments / top_k, num_experts, top_k) bytes; same tokens, experts,
+ * k and the selected ids that call wrote): the counting launch is skipped,
+ * everything else, outputs and status codes included, is vmoe_route's
+ * (VMOE_ERR_UNSUPPORTED where vmoe_router_topk_hist does not apply). The two launches of vmoe_route become one after the top-k
+ * kernel. Same replacement as vmoe_route (fused_cumsum.py:85-171 with
+ * grouped_gemm.py:104-149); the reference counts inside torch.bincount. */
+int vmoe_route_counted(const void* selected_experts, int32_t selected_is_int64,
+                       int64_t num_assignments, int32_t num_experts, int32_t top_k,
+                       int32_t block_size, int32_t rounding, int32_t* bin_ids, int32_t* indices,
+                       int32_t* tokens_per_expert, int32_t* bins, int32_t* padded_bins,
+                       int32_t* row_src, int32_t* gather_map, int32_t gather_map_pad,
+                       int64_t row_capacity, int32_t* assignment_row, int32_t* info,
+                       int32_t* expert_offsets, int32_t* padded_counts,
+                       const uint16_t* weights, float* row_weight, void* workspace,
+                       size_t workspace_bytes, vmoe_stream_t stream);
+
 /* vmoe_route without a workspace argument and without any allocation: the
  * workspace is a file-scope device array of 1 MiB per GPU (each GPU the
  * library runs on holds it until the process ends). No counterpart in the
@@ -153,6 +171,31 @@ int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64_t num_toke
                      int32_t* selected_i32, int64_t* selected_i64, float* probs, float* lse,
                      float* partial, size_t partial_floats, int32_t* num_partial_rows,
                      vmoe_stream_t stream);
+/* vmoe_router_topk that also counts how many of its selections went to each
+ * expert in every block of consecutive assignments (1 to 8 blocks per
+ * routing tile of 1024 assignments, one top-k workgroup each, so the launch
+ * stays near 256 workgroups), into route_workspace
+ * (vmoe_route_counted_workspace_bytes(T, E, k) bytes) in the layout
+ * vmoe_route_counted reads. weights, selected, probs and lse are
+ * vmoe_router_topk's, bit for bit; partial has
+ * vmoe_router_topk_hist_blocks(T, E, k) rows of E + 1 floats (returned in
+ * *num_partial_rows), so vmoe_router_aux adds the per-token terms in another
+ * fixed order. Applies when vmoe_router_topk_hist_blocks > 0 (E % 8 == 0,
+ * E <= 128, k <= 8 dividing 1024, T > 0, E * blocks <= 65536),
+ * ld_logits % 8 == 0 and logits / probs are 16-byte aligned; otherwise
+ * VMOE_ERR_UNSUPPORTED and nothing is launched (use vmoe_router_topk +
+ * vmoe_route). Replaces the same reference lines as vmoe_router_topk
+ * (moe.py:168-176) and the torch.bincount of fused_route
+ * (fused_cumsum.py:134). */
+int vmoe_router_topk_hist_blocks(int64_t num_tokens, int32_t num_experts, int32_t top_k);
+size_t vmoe_route_counted_workspace_bytes(int64_t num_tokens, int32_t num_experts,
+                                          int32_t top_k);
+int vmoe_router_topk_hist(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
+                          int32_t num_experts, int32_t top_k, int32_t normalize,
+                          uint16_t* weights, int32_t* selected_i32, int64_t* selected_i64,
+                          float* probs, float* lse, float* partial, size_t partial_floats,
+                          int32_t* num_partial_rows, void* route_workspace,
+                          size_t route_workspace_bytes, vmoe_stream_t stream);
 int vmoe_router_aux(const float* partial, int32_t num_partial_rows, int64_t num_tokens,
                     int32_t num_experts, const int32_t* tokens_per_expert, const float* coef,
                     const float* widths_normalized, uint16_t* f_i, float* f_i_f32, float* p_i,

@@ -93,6 +93,37 @@ def test_argument_checks_return_invalid_arg():
     assert lib.vmoe_router_topk(1, 8, 4, 8, 2, 1, 1, 1, None, None, 1, 1, 0, None,
                                 None) == _lib.ERR_WORKSPACE
     assert lib.vmoe_router_partial_floats(16384, 64) % 65 == 0
+    # top-k with the routing histograms: one workgroup per 1024-assignment
+    # tile where the grouped kernel applies and k divides 1024, else 0
+    assert lib.vmoe_router_topk_hist_blocks(16384, 64, 8) == 256    # 2 per tile
+    assert lib.vmoe_router_topk_hist_blocks(32768, 128, 8) == 256   # 1 per tile
+    assert lib.vmoe_router_topk_hist_blocks(8192, 8, 2) == 128      # 8 per tile
+    assert lib.vmoe_router_topk_hist_blocks(1000, 64, 8) == 64
+    assert lib.vmoe_router_topk_hist_blocks(262144, 128, 8) == 0   # over 65536 counts
+    assert lib.vmoe_route_counted_workspace_bytes(16384, 64, 8) > \
+        lib.vmoe_route_workspace_bytes(131072, 64)
+    assert lib.vmoe_route_counted_workspace_bytes(16384, 64, 3) == 0
+    assert lib.vmoe_router_topk_hist_blocks(16384, 64, 3) == 0
+    assert lib.vmoe_router_topk_hist_blocks(16384, 12, 2) == 0
+    assert lib.vmoe_router_topk_hist_blocks(16384, 256, 8) == 0
+    assert lib.vmoe_router_topk_hist_blocks(0, 64, 8) == 0
+    # (logits at 16, ld 64, 1000 tokens, 64 experts, k 8); unsupported shapes
+    # launch nothing; short partial rows or routing workspace are refused
+    hist = (16, 64, 1000, 64, 8, 1, 16, 16, None, None, 16, 16)
+    assert lib.vmoe_router_topk_hist(16, 64, 1000, 64, 3, 1, 16, 16, None, None, 16, 16,
+                                     1 << 20, None, 16, 1 << 20, None) == _lib.ERR_UNSUPPORTED
+    assert lib.vmoe_router_topk_hist(*hist, 63 * 65, None, 16, 1 << 20,
+                                     None) == _lib.ERR_WORKSPACE
+    assert lib.vmoe_router_topk_hist(*hist, 64 * 65, None, 16, 64, None) == _lib.ERR_WORKSPACE
+    assert lib.vmoe_router_topk_hist(*hist, 64 * 65, None, None, 1 << 20,
+                                     None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_route_counted(None, 0, -1, 4, 1, 64, 0, None, None, None, None, None,
+                                  None, None, 0, 0, None, None, None, None, None, None, None,
+                                  0, None) == _lib.ERR_INVALID_ARG
+    # counts the top-k launch cannot have written (k = 3) are unsupported
+    assert lib.vmoe_route_counted(1, 0, 6, 64, 3, 64, 0, 1, 1, 1, 1, 1, 1, 1, 0, 512, 1, 1,
+                                  None, None, None, None, 1, 1 << 20,
+                                  None) == _lib.ERR_UNSUPPORTED
     # router logits: ld below the row is invalid; E % 8 != 0 is unsupported
     assert lib.vmoe_router_logits(1, 32, 4, 64, 1, 64, 8, 1, 8, None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_router_logits(16, 256, 4, 256, 16, 256, 7, 8, 8, None) == _lib.ERR_UNSUPPORTED

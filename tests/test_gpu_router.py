@@ -272,3 +272,79 @@ def test_router_weight_bwd_vs_oracle(T, E, k, norm, device):
         d = (got - ref.float()).abs()
         bound = ref.abs().float() * 2.0 ** -8 + 1e-5 * ref.abs().max().float()
         assert bool((d <= bound).all()), float((d - bound).max())
+
+
+HIST_SHAPES = {  # tokens, experts, k, Zipf alpha (None: plain logits)
+    "cfg1": (8192, 8, 2, None),
+    "cfg2": (16384, 16, 2, None),
+    "cfg3_a1": (16384, 64, 8, 1.0),
+    "cfg4": (32768, 128, 8, None),
+    "partial_tile": (1000, 64, 8, None),
+    "k4": (3001, 16, 4, 2.0),
+    "k1": (333, 64, 1, None),
+    "one_token": (1, 64, 8, None),
+    "fallback_k3": (2000, 64, 3, None),
+    "fallback_e256": (500, 256, 8, None),
+}
+
+
+@pytest.mark.parametrize("name", list(HIST_SHAPES))
+def test_router_topk_hist_routes_like_two_launches(name, device):
+    """router_topk(route_hist=True) + route_device(workspace=) (the top-k
+    kernel counts each 1024-assignment tile, the routing skips its counting
+    launch) gives the outputs of router_topk + route_device bit for bit; the
+    workspace holds each tile's expert histogram; the auxiliary losses, whose
+    per-token terms are then summed in other blocks, agree to fp32 rounding."""
+    from triton_moe import _lib
+    from triton_moe.kernels.fused_cumsum import route_device
+    from triton_moe.kernels.router import RouterAuxOp
+
+    T, E, k, alpha = HIST_SHAPES[name]
+    L = _logits(T, E, seed=T + E, ties=True)
+    if alpha is not None:
+        ranks = np.random.default_rng(0).permutation(E) + 1
+        L = (L.float() + torch.tensor(-1.2 * alpha * np.log(ranks))).to(torch.bfloat16)
+    L = L.to(device)
+    blocks = int(_lib.lib().vmoe_router_topk_hist_blocks(T, E, k))
+    assert (blocks > 0) == (not name.startswith("fallback"))
+    a = router_topk(L, k, True, want_probs=True, index_dtype=torch.int64)
+    h = router_topk(L, k, True, want_probs=True, index_dtype=torch.int64, route_hist=True)
+    for f in ("weights", "selected", "probs", "lse"):
+        assert bits_equal(getattr(h, f), getattr(a, f)), f"{name}: {f}"
+    if blocks == 0:
+        assert h.route_ws is None
+        return
+    assert h.partial_rows == blocks
+    A = T * k
+    ntiles = -(-A // 1024)
+    S = blocks // ntiles  # count columns per routing tile
+    assert blocks == ntiles * S and S in (1, 2, 4, 8)
+    span = 1024 // S
+    counts = h.route_ws[:E * blocks].view(E, blocks).cpu()
+    bad = h.route_ws[E * blocks:E * blocks + blocks].cpu()
+    flat = a.selected.reshape(-1).cpu()
+    for t in range(blocks):
+        want = torch.bincount(flat[t * span:(t + 1) * span], minlength=E)
+        assert torch.equal(counts[:, t], want.to(torch.int32)), f"{name}: block {t} histogram"
+    assert int(bad.abs().sum()) == 0
+    wf = a.weights.reshape(-1)
+    r1 = route_device(a.selected.reshape(-1), E, k, 64, "up", map_pad=-1, weights=wf)
+    r2 = route_device(h.selected.reshape(-1), E, k, 64, "up", map_pad=-1, weights=wf,
+                      workspace=h.route_ws)
+    torch.cuda.synchronize()
+    P = int(r1.info[_lib.INFO_ROWS])
+    assert torch.equal(r1.info, r2.info)
+    for f in ("bin_ids", "indices", "tokens_per_expert", "bins", "padded_bins",
+              "assignment_row", "expert_offsets", "padded_counts"):
+        assert torch.equal(getattr(r1, f), getattr(r2, f)), f"{name}: {f}"
+    for f in ("row_src", "gather_map", "row_weight"):
+        assert bits_equal(getattr(r1, f)[:P], getattr(r2, f)[:P]), f"{name}: {f}"
+    # auxiliary losses from the two blockings of the per-token sums
+    coef = torch.full((E,), float(E), device=device)
+    wn = torch.ones(E, device=device)
+    la = RouterAuxOp.apply(L, a.lse, a.partial, a.partial_rows, r1.tokens_per_expert, coef, wn)
+    lh = RouterAuxOp.apply(L, h.lse, h.partial, h.partial_rows, r2.tokens_per_expert, coef, wn)
+    # z_loss is bf16 (one rounding step apart at most), the two losses fp32
+    # sums of T terms, f_i a function of the counts alone
+    for x, y, what, rtol in zip(la, lh, ("z", "lb", "cl", "f_i"), (2.0 ** -7, 1e-5, 1e-5, 0)):
+        assert torch.allclose(x.float(), y.float(), rtol=rtol, atol=0), f"{name}: aux {what}"

@@ -36,7 +36,7 @@ namespace {
 // against 10.9 + 2.7 us.
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / kWave;
-constexpr int kTile = 1024;                     // assignments per tile
+constexpr int kTile = kRouteTile;               // assignments per tile
 constexpr int kWaveSpan = kTile / kRouteWaves;  // contiguous assignments per wave
 constexpr int kMaxExperts = 2048;  // the placement's per-wave tables, 17 E ints, fit the LDS
 constexpr int kScanThreads = 1024;
@@ -46,9 +46,10 @@ __device__ __forceinline__ int64_t load_sel(const void* sel, int is64, int64_t p
               : (int64_t)reinterpret_cast<const int32_t*>(sel)[p];
 }
 
-// Workspace layout (int32): counts [E * ntiles], bad-id flag per tile
-// [ntiles], then per expert: start (first unkept sorted position), kept,
-// bs (bins[e-1]), ps (padded_bins[e-1]).
+// Workspace layout (int32): counts [E * ntiles * S], bad-id flag per count
+// column [ntiles * S], then per expert: start (first unkept sorted
+// position), kept, bs (bins[e-1]), ps (padded_bins[e-1]). S = 1 (one count
+// column per tile) except after vmoe_router_topk_hist (route_hist_split).
 struct RouteWs {
   int32_t* counts;
   int32_t* bad;
@@ -58,15 +59,15 @@ struct RouteWs {
   int32_t* ps;
 };
 
-__host__ __device__ inline int64_t route_ntiles(int64_t A) { return (A + kTile - 1) / kTile; }
+__host__ __device__ inline int64_t route_ntiles(int64_t A) { return route_tiles(A); }
 
-__host__ __device__ inline RouteWs route_ws(void* base, int64_t A, int E) {
+__host__ __device__ inline RouteWs route_ws(void* base, int64_t A, int E, int S = 1) {
   RouteWs w;
   int32_t* p = reinterpret_cast<int32_t*>(base);
   w.counts = p;
-  p += (int64_t)E * route_ntiles(A);
+  p += (int64_t)E * route_ntiles(A) * S;
   w.bad = p;
-  p += route_ntiles(A);
+  p += route_ntiles(A) * S;
   w.start = p; p += E;
   w.kept = p; p += E;
   w.bs = p; p += E;
@@ -351,7 +352,7 @@ constexpr int kFusedMaxExperts = 1024;
 constexpr int64_t kFusedMaxCounts = 65536;
 
 __global__ __launch_bounds__(kRouteThreads) void route_fused_kernel(
-    const void* __restrict__ sel, int is64, int64_t A, int E, int nbits, int ntiles,
+    const void* __restrict__ sel, int is64, int64_t A, int E, int nbits, int ntiles, int S,
     int block, int mode, int top_k, RouteWs ws, int32_t* __restrict__ tpe,
     int32_t* __restrict__ bins, int32_t* __restrict__ padded_bins,
     int32_t* __restrict__ bin_ids, int32_t* __restrict__ indices,
@@ -377,19 +378,21 @@ __global__ __launch_bounds__(kRouteThreads) void route_fused_kernel(
   const TileSel ts = load_tile(sel, is64, A, E, b, row_weight ? weights : nullptr);
 
   // Totals and this tile's prefix: G lanes per expert (a power of two that
-  // divides the wave), each summing every G-th tile, so a thread has all of
-  // its counts loads in flight at once; then a butterfly over the G lanes.
+  // divides the wave), each summing every G-th count column (S per tile), so
+  // a thread has all of its counts loads in flight at once; then a
+  // butterfly over the G lanes.
   int G = kWave;
   while (G > 1 && G * E > kRouteThreads) G >>= 1;
   const int j = tid & (G - 1);
+  const int ncols = ntiles * S, bcol = b * S;
   for (int e = tid / G; e < E; e += kRouteThreads / G) {
-    const int32_t* c = ws.counts + (int64_t)e * ntiles;
+    const int32_t* c = ws.counts + (int64_t)e * ncols;
     int32_t tot = 0, pre = 0;
 #pragma unroll 8
-    for (int t = j; t < ntiles; t += G) {
+    for (int t = j; t < ncols; t += G) {
       const int32_t v = c[t];
       tot += v;
-      pre += t < b ? v : 0;
+      pre += t < bcol ? v : 0;
     }
     for (int off = G / 2; off > 0; off >>= 1) {
       tot += __shfl_xor(tot, off, kWave);
@@ -434,7 +437,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_fused_kernel(
   }
   if (b == 0) {
     bool bad = false;
-    for (int t = tid; t < ntiles; t += kRouteThreads) bad |= ws.bad[t] != 0;
+    for (int t = tid; t < ntiles * S; t += kRouteThreads) bad |= ws.bad[t] != 0;
     if (bad) any_bad = 1;
   }
   __syncthreads();
@@ -519,19 +522,33 @@ using namespace vmoe;
 
 extern "C" int vmoe_route_max_experts(void) { return kMaxExperts; }
 
-extern "C" size_t vmoe_route_workspace_bytes(int64_t A, int32_t E) {
-  if (A < 0 || E <= 0) return 0;
-  const size_t nt = (size_t)route_ntiles(A);
+namespace {
+size_t route_ws_size(int64_t A, int E, int S) {
+  const size_t nt = (size_t)route_ntiles(A) * (size_t)S;
   return sizeof(int32_t) * ((size_t)E * nt + nt + 4 * (size_t)E) + 256;
 }
+}  // namespace
 
-extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_k,
-                          int32_t block, int32_t rounding, int32_t* bin_ids, int32_t* indices,
-                          int32_t* tpe, int32_t* bins, int32_t* padded_bins, int32_t* row_src,
-                          int32_t* gather_map, int32_t gather_map_pad, int64_t row_capacity,
-                          int32_t* assignment_row, int32_t* info, int32_t* expert_offsets,
-                          int32_t* padded_counts, const uint16_t* weights, float* row_weight,
-                          void* workspace, size_t ws_bytes, vmoe_stream_t stream) {
+extern "C" size_t vmoe_route_workspace_bytes(int64_t A, int32_t E) {
+  if (A < 0 || E <= 0) return 0;
+  return route_ws_size(A, E, 1);
+}
+
+extern "C" size_t vmoe_route_counted_workspace_bytes(int64_t T, int32_t E, int32_t top_k) {
+  const int S = T > 0 && E > 0 ? route_hist_split(T, E, top_k) : 0;
+  return S ? route_ws_size(T * top_k, E, S) : 0;
+}
+
+namespace {
+// vmoe_route; `counted`: the workspace already holds the per-tile counts and
+// bad-id flags (vmoe_router_topk_hist), so launch 1 is skipped.
+int route_impl(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_k,
+               int32_t block, int32_t rounding, int32_t* bin_ids, int32_t* indices,
+               int32_t* tpe, int32_t* bins, int32_t* padded_bins, int32_t* row_src,
+               int32_t* gather_map, int32_t gather_map_pad, int64_t row_capacity,
+               int32_t* assignment_row, int32_t* info, int32_t* expert_offsets,
+               int32_t* padded_counts, const uint16_t* weights, float* row_weight,
+               void* workspace, size_t ws_bytes, vmoe_stream_t stream, bool counted) {
   if (A < 0 || E <= 0 || top_k <= 0 || block <= 0 || row_capacity < 0)
     return VMOE_ERR_INVALID_ARG;
   if (rounding < VMOE_ROUND_UP || rounding > VMOE_ROUND_NEAREST) return VMOE_ERR_INVALID_ARG;
@@ -540,22 +557,27 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
   if (A > 0 && (!sel || !bin_ids || !indices || !assignment_row)) return VMOE_ERR_INVALID_ARG;
   if (row_capacity > 0 && (!row_src || !gather_map)) return VMOE_ERR_INVALID_ARG;
   if (row_weight && !weights) return VMOE_ERR_INVALID_ARG;
-  if (ws_bytes < vmoe_route_workspace_bytes(A, E)) return VMOE_ERR_WORKSPACE;
+  // counted: the S count columns per tile of vmoe_router_topk_hist for the
+  // same tokens, experts and k
+  const int S = counted ? (A % top_k == 0 ? route_hist_split(A / top_k, E, top_k) : 0) : 1;
+  if (S == 0) return VMOE_ERR_UNSUPPORTED;
+  if (ws_bytes < route_ws_size(A, E, S)) return VMOE_ERR_WORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
   const int ntiles = (int)route_ntiles(A);
-  RouteWs ws = route_ws(workspace, A, E);
-  if (ntiles > 0) {
+  RouteWs ws = route_ws(workspace, A, E, S);
+  if (ntiles > 0 && !counted) {
     hipLaunchKernelGGL(route_hist_kernel, dim3(ntiles), dim3(kRouteThreads),
                        sizeof(int32_t) * E, s, sel, is64, A, E, ntiles, ws.counts, ws.bad);
     VMOE_CHECK_LAUNCH();
   }
   int nbits = 1;
   while ((1 << nbits) < E) ++nbits;
-  if (E <= kFusedMaxExperts && (int64_t)E * ntiles <= kFusedMaxCounts) {
+  // (route_hist_split keeps the counted case inside these limits)
+  if (E <= kFusedMaxExperts && (int64_t)E * ntiles * S <= kFusedMaxCounts) {
     hipLaunchKernelGGL(route_fused_kernel, dim3(std::max(ntiles, 1)), dim3(kRouteThreads),
                        sizeof(int32_t) * (kRouteWaves + 7) * E, s, sel, is64, A, E, nbits,
-                       ntiles, block, rounding, top_k, ws, tpe, bins, padded_bins, bin_ids,
+                       ntiles, S, block, rounding, top_k, ws, tpe, bins, padded_bins, bin_ids,
                        indices, row_src, gather_map, gather_map_pad, row_capacity,
                        assignment_row, weights, row_weight, info, expert_offsets,
                        padded_counts);
@@ -576,6 +598,35 @@ extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, i
     VMOE_CHECK_LAUNCH();
   }
   return VMOE_OK;
+}
+}  // namespace
+
+extern "C" int vmoe_route(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_k,
+                          int32_t block, int32_t rounding, int32_t* bin_ids, int32_t* indices,
+                          int32_t* tpe, int32_t* bins, int32_t* padded_bins, int32_t* row_src,
+                          int32_t* gather_map, int32_t gather_map_pad, int64_t row_capacity,
+                          int32_t* assignment_row, int32_t* info, int32_t* expert_offsets,
+                          int32_t* padded_counts, const uint16_t* weights, float* row_weight,
+                          void* workspace, size_t ws_bytes, vmoe_stream_t stream) {
+  return route_impl(sel, is64, A, E, top_k, block, rounding, bin_ids, indices, tpe, bins,
+                    padded_bins, row_src, gather_map, gather_map_pad, row_capacity,
+                    assignment_row, info, expert_offsets, padded_counts, weights, row_weight,
+                    workspace, ws_bytes, stream, false);
+}
+
+extern "C" int vmoe_route_counted(const void* sel, int32_t is64, int64_t A, int32_t E,
+                                  int32_t top_k, int32_t block, int32_t rounding,
+                                  int32_t* bin_ids, int32_t* indices, int32_t* tpe,
+                                  int32_t* bins, int32_t* padded_bins, int32_t* row_src,
+                                  int32_t* gather_map, int32_t gather_map_pad,
+                                  int64_t row_capacity, int32_t* assignment_row, int32_t* info,
+                                  int32_t* expert_offsets, int32_t* padded_counts,
+                                  const uint16_t* weights, float* row_weight, void* workspace,
+                                  size_t ws_bytes, vmoe_stream_t stream) {
+  return route_impl(sel, is64, A, E, top_k, block, rounding, bin_ids, indices, tpe, bins,
+                    padded_bins, row_src, gather_map, gather_map_pad, row_capacity,
+                    assignment_row, info, expert_offsets, padded_counts, weights, row_weight,
+                    workspace, ws_bytes, stream, true);
 }
 
 // vmoe_route_static: vmoe_route with its workspace in a file-scope device

@@ -401,9 +401,18 @@ __global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
     const uint16_t* __restrict__ logits, int64_t ldl, int64_t T, int E, int k, int norm,
     uint16_t* __restrict__ weights, int32_t* __restrict__ selected32,
     int64_t* __restrict__ selected64, float* __restrict__ probs, float* __restrict__ lse_out,
-    float* __restrict__ partial, int64_t per) {
+    float* __restrict__ partial, int64_t per, int32_t* __restrict__ hist_counts,
+    int32_t* __restrict__ hist_bad, int hist_cols) {
   constexpr int TPW = kWave / G;  // tokens per wave and batch
   __shared__ float red[kGrpWaves][kGrpMaxExperts + 1];
+  // With hist_counts, the workgroup's per * k assignments are count column
+  // blockIdx.x of the routing (kRouteTile / (per * k) columns per tile): its
+  // expert histogram for vmoe_route_counted.
+  __shared__ int32_t thist[kGrpMaxExperts];
+  if (hist_counts) {
+    for (int e = threadIdx.x; e < E; e += kGrpThreads) thist[e] = 0;
+    __syncthreads();
+  }
   const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
   const int r = lane & (G - 1), slot = lane / G;
   const int e0 = 8 * r;
@@ -501,6 +510,7 @@ __global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
           weights[t * k + j] = (uint16_t)f32_to_bf16(norm ? v / (vsum + 1e-20f) : v);
           if (selected32) selected32[t * k + j] = ex[j];
           if (selected64) selected64[t * k + j] = ex[j];
+          if (hist_counts) atomicAdd(&thist[ex[j]], 1);
         }
       }
     }
@@ -523,6 +533,13 @@ __global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
 #pragma unroll
     for (int w = 0; w < kGrpWaves; ++w) sum += red[w][e];
     partial[(int64_t)blockIdx.x * (E + 1) + e] = sum;
+  }
+  if (hist_counts) {
+    // Every written id is a real expert (E >= 8 >= k keys beat the empty
+    // ones), so the tile's bad-id flag is 0.
+    for (int e = threadIdx.x; e < E; e += kGrpThreads)
+      hist_counts[(int64_t)e * hist_cols + blockIdx.x] = thist[e];
+    if (threadIdx.x == 0) hist_bad[blockIdx.x] = 0;
   }
 }
 
@@ -721,6 +738,47 @@ inline int router_blocks(int64_t T, int E) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(b, kRtMaxBlocks));
 }
 
+// Workgroups of vmoe_router_topk_hist: S per routing tile (S =
+// route_hist_split), kRouteTile / (S k) tokens each, on the grouped top-k
+// kernel; 0 where that launch does not apply.
+static_assert(kGrpMaxExperts == 128 && kRtMaxBlocks >= 1024, "route_hist_split's limits");
+inline int router_hist_blocks(int64_t T, int E, int k) {
+  const int S = route_hist_split(T, E, k);
+  return S ? (int)(route_tiles(T * k) * S) : 0;
+}
+
+// The grouped top-k launch for G lanes per token (hist_counts nullable).
+int topk_group_launch(int G, int nblk, hipStream_t s, const uint16_t* logits, int64_t ld,
+                      int64_t T, int E, int k, int norm, uint16_t* weights, int32_t* sel32,
+                      int64_t* sel64, float* probs, float* lse, float* partial, int64_t per,
+                      int32_t* hist_counts, int32_t* hist_bad) {
+  switch (G) {
+#define VMOE_RT_GRP(GG)                                                                        \
+  case GG:                                                                                     \
+    hipLaunchKernelGGL(router_topk_group_kernel<GG>, dim3(nblk), dim3(kGrpThreads), 0, s,       \
+                       logits, ld, T, E, k, norm, weights, sel32, sel64, probs, lse, partial,   \
+                       per, hist_counts, hist_bad, nblk);                                      \
+    break;
+    VMOE_RT_GRP(1)
+    VMOE_RT_GRP(2)
+    VMOE_RT_GRP(4)
+    VMOE_RT_GRP(8)
+    VMOE_RT_GRP(16)
+#undef VMOE_RT_GRP
+    default:
+      return VMOE_ERR_UNSUPPORTED;
+  }
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+// Shapes and layouts the grouped top-k kernel reads (16-byte logits rows).
+bool group_kernel_ok(const uint16_t* logits, int64_t ld, int E, int k, const float* probs) {
+  return E % 8 == 0 && E <= kGrpMaxExperts && k <= 8 && ld % 8 == 0 &&
+         reinterpret_cast<uintptr_t>(logits) % 16 == 0 &&
+         (!probs || reinterpret_cast<uintptr_t>(probs) % 16 == 0);
+}
+
 // Router logits L = bf16(x W^T) (nn.Linear without bias) for E <= 32 NT
 // experts: a workgroup takes 32 tokens and its 4 waves split K into quarters.
 // A wave walks its quarter in chunks of 64 k (one 128-byte line per row):
@@ -866,28 +924,10 @@ extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64
   if (num_partial_rows) *num_partial_rows = nblk;
   const int64_t per = (num_tokens + nblk - 1) / nblk;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (num_experts % 8 == 0 && num_experts <= kGrpMaxExperts && top_k <= 8 &&
-      ld_logits % 8 == 0 && reinterpret_cast<uintptr_t>(logits) % 16 == 0 &&
-      (!probs || reinterpret_cast<uintptr_t>(probs) % 16 == 0)) {
-    switch (group_size(num_experts)) {
-#define VMOE_RT_GRP(G)                                                                      \
-  case G:                                                                                   \
-    hipLaunchKernelGGL(router_topk_group_kernel<G>, dim3(nblk), dim3(kGrpThreads), 0, s,     \
-                       logits, ld_logits, num_tokens, num_experts, top_k, normalize, weights, \
-                       selected_i32, selected_i64, probs, lse, partial, per);                \
-    break;
-      VMOE_RT_GRP(1)
-      VMOE_RT_GRP(2)
-      VMOE_RT_GRP(4)
-      VMOE_RT_GRP(8)
-      VMOE_RT_GRP(16)
-#undef VMOE_RT_GRP
-      default:
-        return VMOE_ERR_UNSUPPORTED;
-    }
-    VMOE_CHECK_LAUNCH();
-    return VMOE_OK;
-  }
+  if (group_kernel_ok(logits, ld_logits, num_experts, top_k, probs))
+    return topk_group_launch(group_size(num_experts), nblk, s, logits, ld_logits, num_tokens,
+                             num_experts, top_k, normalize, weights, selected_i32, selected_i64,
+                             probs, lse, partial, per, nullptr, nullptr);
   const int vpl = vpl_of(num_experts);
   const size_t lds = sizeof(float) * (topk_threads(vpl) / kWave) * (num_experts + 1);
   switch (vpl) {
@@ -910,6 +950,41 @@ extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64
   }
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
+}
+
+extern "C" int vmoe_router_topk_hist_blocks(int64_t num_tokens, int32_t num_experts,
+                                            int32_t top_k) {
+  return router_hist_blocks(num_tokens, num_experts, top_k);
+}
+
+extern "C" int vmoe_router_topk_hist(const uint16_t* logits, int64_t ld_logits,
+                                     int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                                     int32_t normalize, uint16_t* weights, int32_t* selected_i32,
+                                     int64_t* selected_i64, float* probs, float* lse,
+                                     float* partial, size_t partial_floats,
+                                     int32_t* num_partial_rows, void* route_workspace,
+                                     size_t route_workspace_bytes, vmoe_stream_t stream) {
+  if (num_tokens < 0 || num_experts <= 0 || top_k <= 0 || top_k > num_experts ||
+      ld_logits < num_experts)
+    return VMOE_ERR_INVALID_ARG;
+  if (!weights || !partial || !lse || !route_workspace || (!selected_i32 && !selected_i64) ||
+      (num_tokens > 0 && !logits))
+    return VMOE_ERR_INVALID_ARG;
+  const int nblk = router_hist_blocks(num_tokens, num_experts, top_k);
+  if (nblk == 0 || !group_kernel_ok(logits, ld_logits, num_experts, top_k, probs))
+    return VMOE_ERR_UNSUPPORTED;
+  if (partial_floats < (size_t)nblk * (size_t)(num_experts + 1) ||
+      route_workspace_bytes < vmoe_route_counted_workspace_bytes(num_tokens, num_experts, top_k))
+    return VMOE_ERR_WORKSPACE;
+  if (num_partial_rows) *num_partial_rows = nblk;
+  // counts [E][nblk] (one column per workgroup), then a bad-id flag per column
+  const int S = route_hist_split(num_tokens, num_experts, top_k);
+  int32_t* counts = static_cast<int32_t*>(route_workspace);
+  return topk_group_launch(group_size(num_experts), nblk, reinterpret_cast<hipStream_t>(stream),
+                           logits, ld_logits, num_tokens, num_experts, top_k, normalize, weights,
+                           selected_i32, selected_i64, probs, lse, partial,
+                           kRouteTile / (top_k * S), counts,
+                           counts + (int64_t)num_experts * nblk);
 }
 
 extern "C" int vmoe_router_aux(const float* partial, int32_t num_partial_rows,

@@ -93,4 +93,30 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* smem, T* total) {
   return excl;
 }
 
+// Routing tiles: vmoe_route counts the expert ids of every tile of
+// kRouteTile consecutive assignments. Its workspace starts with those counts,
+// expert-major int32 [E][tiles], followed by one bad-id flag per tile;
+// vmoe_router_topk_hist writes the same two arrays.
+constexpr int kRouteTile = 1024;
+__host__ __device__ inline int64_t route_tiles(int64_t A) {
+  return (A + kRouteTile - 1) / kRouteTile;
+}
+
+// Count columns per routing tile written by vmoe_router_topk_hist for T
+// tokens, E experts and top_k k: each top-k workgroup counts S consecutive
+// column blocks' worth of kRouteTile / S assignments (kRouteTile / (S k)
+// tokens), S the power of two <= 8 that keeps the launch near 256
+// workgroups; the counts array is then [E][tiles * S]. 0 where that launch
+// does not apply: the grouped top-k kernel's experts (E % 8 == 0, E <= 128)
+// and k <= 8 dividing kRouteTile, T > 0, at most 1024 workgroups, and E
+// tiles S <= 65536 counts (what one placement workgroup sums).
+inline int route_hist_split(int64_t T, int E, int k) {
+  if (T <= 0 || E % 8 != 0 || E > 128 || k <= 0 || k > 8 || kRouteTile % k != 0) return 0;
+  const int64_t nt = route_tiles(T * k);
+  int S = 1;
+  while (S < 8 && nt * S * 2 <= 256) S *= 2;
+  if (nt * S > 1024 || (int64_t)E * nt * S > 65536) return 0;
+  return S;
+}
+
 }  // namespace vmoe

@@ -28,6 +28,9 @@ _SIGNATURES = {
     "vmoe_route_workspace_bytes": [_i64, _i32],
     "vmoe_route": [_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                    _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp],
+    "vmoe_route_counted": [_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
+                           _vp, _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                           ctypes.c_size_t, _vp],
     "vmoe_route_static": [_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "vmoe_row_maps": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _i64, _vp, _vp, _vp, _vp],
@@ -58,6 +61,10 @@ _SIGNATURES = {
     "vmoe_router_partial_floats": [_i64, _i32],
     "vmoe_router_topk": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                          ctypes.c_size_t, _vp, _vp],
+    "vmoe_router_topk_hist_blocks": [_i64, _i32, _i32],
+    "vmoe_route_counted_workspace_bytes": [_i64, _i32, _i32],
+    "vmoe_router_topk_hist": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                              ctypes.c_size_t, _vp, _vp, ctypes.c_size_t, _vp],
     "vmoe_router_aux": [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "vmoe_router_aux_bwd": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                             _vp],
@@ -67,6 +74,7 @@ _SIGNATURES = {
 _RESTYPES = {
     "vmoe_status_string": ctypes.c_char_p,
     "vmoe_route_workspace_bytes": ctypes.c_size_t,
+    "vmoe_route_counted_workspace_bytes": ctypes.c_size_t,
     "vmoe_gemm_dw_workspace_bytes": ctypes.c_size_t,
     "vmoe_router_partial_floats": ctypes.c_size_t,
 }

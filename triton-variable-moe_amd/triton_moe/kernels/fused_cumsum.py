@@ -8,7 +8,8 @@ then placement; a single-workgroup scan in between for more than 1024 experts
 or 65,536 tile counts) produces the sorted arrays, histogram, both cumulative
 sums, the padded-row maps and the gather map at once, and only "down"/"nearest"
 rounding (whose output length is data dependent) reads anything back to the
-host.
+host. The module's forward takes the histograms from its top-k launch
+(router_topk(route_hist=True)) and runs the placement alone.
 """
 
 from __future__ import annotations
@@ -54,13 +55,17 @@ def rows_upper_bound(num_assignments: int, num_experts: int, block_size: int,
 
 def route_device(selected: torch.Tensor, num_experts: int, top_k: int, block_size: int,
                  rounding: str = "up", map_pad: int = 0,
-                 weights: torch.Tensor | None = None) -> Route:
+                 weights: torch.Tensor | None = None,
+                 workspace: torch.Tensor | None = None) -> Route:
     """Runs the routing chain on the current stream; never syncs.
 
     map_pad is the gather_map entry of pad rows: 0 as in the reference's
     precompute_gather_map, -1 for the module's fused row gather (the GEMMs
     read zeros for it). With weights (bf16, one per assignment) the route
-    also holds row_weight[row] = weights[row_src[row]] (0 on pad rows)."""
+    also holds row_weight[row] = weights[row_src[row]] (0 on pad rows).
+    workspace: the RouterState.route_ws of the router_topk(route_hist=True)
+    call that produced `selected`; its per-tile histograms replace the
+    routing's own counting launch (vmoe_route_counted)."""
     _lib.require_gpu(selected)
     if rounding not in _lib.ROUNDING:
         raise AssertionError(f"Invalid rounding mode: {rounding}")
@@ -84,8 +89,14 @@ def route_device(selected: torch.Tensor, num_experts: int, top_k: int, block_siz
             raise ValueError("weights must be bf16 with one entry per assignment")
         weights = weights.reshape(-1).contiguous()
     nrw = max(cap, 1) if weights is not None else 0
+    if workspace is not None:
+        need = int(_lib.lib().vmoe_route_counted_workspace_bytes(A // int(top_k), E, int(top_k)))
+        if (workspace.dtype != torch.int32 or need == 0 or A % int(top_k) or
+                workspace.numel() * 4 < need or workspace.device != dev):
+            raise ValueError("workspace must be the routing workspace of the "
+                             "router_topk(route_hist=True) call that selected these experts")
     sizes = [max(A, 1), max(A, 1), E, E, E, max(cap, 1), max(cap, 1), max(A, 1), _lib.INFO_LEN,
-             E + 1, E, nrw, (ws_bytes + 3) // 4]
+             E + 1, E, nrw, 0 if workspace is not None else (ws_bytes + 3) // 4]
     offs, n = [], 0
     for sz in sizes:
         offs.append(n)
@@ -94,7 +105,10 @@ def route_device(selected: torch.Tensor, num_experts: int, top_k: int, block_siz
     (bin_ids, indices, tpe, bins, padded, row_src, gmap, arow, info, eto, ptpe, rw,
      ws) = (buf[o:o + sz] for o, sz in zip(offs, sizes))
     rw = rw.view(torch.float32) if weights is not None else None
-    _lib.call("vmoe_route", sel.data_ptr(), int(sel.dtype == torch.int64), A, E, int(top_k),
+    entry = "vmoe_route"
+    if workspace is not None:
+        entry, ws, ws_bytes = "vmoe_route_counted", workspace, workspace.numel() * 4
+    _lib.call(entry, sel.data_ptr(), int(sel.dtype == torch.int64), A, E, int(top_k),
               int(block_size), _lib.ROUNDING[rounding], bin_ids.data_ptr(), indices.data_ptr(),
               tpe.data_ptr(), bins.data_ptr(), padded.data_ptr(), row_src.data_ptr(),
               gmap.data_ptr(), int(map_pad), cap, arow.data_ptr(), info.data_ptr(), eto.data_ptr(),

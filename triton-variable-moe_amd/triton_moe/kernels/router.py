@@ -39,11 +39,20 @@ class RouterState:
     lse: torch.Tensor          # [T] fp32, bf16-rounded logsumexp of each row
     partial: torch.Tensor      # per-workgroup sums for the auxiliary losses
     partial_rows: int
+    # With route_hist: the routing workspace holding the per-tile expert
+    # histograms of `selected` (route_device(..., workspace=) then skips its
+    # counting launch); None when the top-k kernel did not count.
+    route_ws: torch.Tensor | None = None
 
 
 def router_topk(logits: torch.Tensor, top_k: int, normalize: bool = True,
-                want_probs: bool = False, index_dtype=torch.int32) -> RouterState:
-    """sigmoid + top-k + normalisation of bf16 router logits [T, E] (no host sync)."""
+                want_probs: bool = False, index_dtype=torch.int32,
+                route_hist: bool = False) -> RouterState:
+    """sigmoid + top-k + normalisation of bf16 router logits [T, E] (no host sync).
+
+    route_hist: where the shape allows it (vmoe_router_topk_hist), the same
+    launch also writes the per-tile expert histograms the routing needs, into
+    a routing workspace returned as RouterState.route_ws."""
     _lib.require_gpu(logits)
     if logits.dtype != torch.bfloat16:
         raise NotImplementedError(f"router logits must be bfloat16 (got {logits.dtype})")
@@ -51,20 +60,34 @@ def router_topk(logits: torch.Tensor, top_k: int, normalize: bool = True,
         logits = logits.reshape(-1, logits.shape[-1]).contiguous()
     T, E = logits.shape
     dev = logits.device
-    nfl = int(_lib.lib().vmoe_router_partial_floats(T, E))
-    rows = nfl // (E + 1)
+    L = _lib.lib()
+    hist_rows = int(L.vmoe_router_topk_hist_blocks(T, E, int(top_k))) if route_hist else 0
+    if hist_rows and (logits.stride(0) % 8 or logits.data_ptr() % 16):
+        hist_rows = 0
+    rows = hist_rows or int(L.vmoe_router_partial_floats(T, E)) // (E + 1)
+    nfl = rows * (E + 1)
     f32 = torch.float32
     weights = torch.empty(T, top_k, dtype=torch.bfloat16, device=dev)
     selected = torch.empty(T, top_k, dtype=index_dtype, device=dev)
     probs = torch.empty(T, E, dtype=f32, device=dev) if want_probs else None
-    scratch = torch.empty(T + nfl, dtype=f32, device=dev)
-    lse, partial = scratch[:T], scratch[T:]
+    # lse first, then the partial rows at a 16-byte aligned offset
+    off = (T + 3) // 4 * 4
+    scratch = torch.empty(off + nfl, dtype=f32, device=dev)
+    lse, partial = scratch[:T], scratch[off:]
     is64 = index_dtype == torch.int64
-    _lib.call("vmoe_router_topk", logits.data_ptr(), logits.stride(0), T, E, int(top_k),
-              int(bool(normalize)), weights.data_ptr(), None if is64 else selected.data_ptr(),
-              selected.data_ptr() if is64 else None, _lib.ptr(probs), lse.data_ptr(),
-              partial.data_ptr(), nfl, None, _lib.stream(dev))
-    return RouterState(weights, selected, probs, lse, partial, rows)
+    args = (logits.data_ptr(), logits.stride(0), T, E, int(top_k), int(bool(normalize)),
+            weights.data_ptr(), None if is64 else selected.data_ptr(),
+            selected.data_ptr() if is64 else None, _lib.ptr(probs), lse.data_ptr(),
+            partial.data_ptr(), nfl, None)
+    route_ws = None
+    if hist_rows:
+        ws_bytes = int(L.vmoe_route_counted_workspace_bytes(T, E, int(top_k)))
+        route_ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.int32, device=dev)
+        _lib.call("vmoe_router_topk_hist", *args, route_ws.data_ptr(), route_ws.numel() * 4,
+                  _lib.stream(dev))
+    else:
+        _lib.call("vmoe_router_topk", *args, _lib.stream(dev))
+    return RouterState(weights, selected, probs, lse, partial, rows, route_ws)
 
 
 def router_logits_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:

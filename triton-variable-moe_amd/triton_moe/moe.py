@@ -168,15 +168,16 @@ class TritonMoEMLP(nn.Module):
         }
         return aux_loss, f_i.to(dtype)
 
-    def _experts(self, x_flat, top_k_weights_flat, selected_experts_flat):
+    def _experts(self, x_flat, top_k_weights_flat, selected_experts_flat, route_ws=None):
         """Routing + expert MLP + combine on the HIP kernels, no host sync.
         The expert path differentiates through top_k_weights_flat only when
-        it requires grad (routing_weight_grad)."""
+        it requires grad (routing_weight_grad). route_ws: the top-k call's
+        per-tile histograms (RouterState.route_ws), or None."""
         k = self.num_active_experts
         # Pad rows of the row map are -1 (the GEMMs' fused gather reads zeros
         # for them); row_weight holds each row's routing weight.
         r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
-                         map_pad=-1, weights=top_k_weights_flat)
+                         map_pad=-1, weights=top_k_weights_flat, workspace=route_ws)
         # expert_token_offsets = [0, padded_bins] and the padded counts come
         # out of the routing kernel (moe.py:193-202 of the reference).
         meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
@@ -197,13 +198,14 @@ class TritonMoEMLP(nn.Module):
         batch_size, _seq_len, _n_embd = x.shape
         x_flat = rearrange(x, "b s d -> (b s) d")
         router_logits = self.router(x_flat)
-        state = router_topk(router_logits, self.num_active_experts, self.norm_topk_prob)
+        state = router_topk(router_logits, self.num_active_experts, self.norm_topk_prob,
+                            route_hist=True)
         weights = state.weights
         if self.config.routing_weight_grad and torch.is_grad_enabled():
             weights = RouterWeightOp.apply(router_logits, weights, state.selected,
                                            self.norm_topk_prob)
         output_flat, tokens_per_expert = self._experts(
-            x_flat, weights.reshape(-1), state.selected.reshape(-1))
+            x_flat, weights.reshape(-1), state.selected.reshape(-1), state.route_ws)
         output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
         aux_loss, f_i = self._aux(router_logits, state, tokens_per_expert, x.dtype)
         return output, aux_loss, f_i
@@ -265,13 +267,14 @@ class TritonMoEMLP(nn.Module):
             x_flat = rearrange(x, "b s d -> (b s) d")
         with profiler.step("routing"):
             router_logits = self.router(x_flat)
-            state = router_topk(router_logits, self.num_active_experts, self.norm_topk_prob)
+            state = router_topk(router_logits, self.num_active_experts, self.norm_topk_prob,
+                                route_hist=True)
             top_k_weights_flat = state.weights.reshape(-1)
             selected_experts_flat = state.selected.reshape(-1)
         k = self.num_active_experts
         with profiler.step("fused_route"):
             r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
-                             map_pad=-1, weights=top_k_weights_flat)
+                             map_pad=-1, weights=top_k_weights_flat, workspace=state.route_ws)
             meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
                             self.expert_widths_t, r.padded_counts, self.num_experts,
                             self.max_expert_width, r.rows_bound)
