@@ -333,21 +333,39 @@ int vmoe_relu2_grad(const uint16_t* grad_h, const uint16_t* pre_act, int64_t ld,
                     uint16_t* grad_act, int64_t ldo, int64_t rows, int64_t cols,
                     vmoe_stream_t stream);
 
-/* SwiGLU activation for activation="swiglu": the gate and up halves of an
- * expert's W1 columns (gate at ewo_e + c, up at ewo_e + w_e + c, the
- * reference's layout, triton_moe/kernels/grouped_gemm.py:295-297) are run as
- * two grouped GEMMs without activation, then
- *   vmoe_swiglu:      H = bf16(silu(gate) * up)   (grouped_gemm.py:347-349)
- *   vmoe_swiglu_grad: grad_gate = bf16(gh * up * s * (1 + gate * (1 - s))),
- *                     grad_up = bf16(gh * gate * s), s = sigmoid(gate)
- * The reference's swiglu backward is an unfinished placeholder
- * (grouped_gemm.py:768-790); vmoe_swiglu_grad is the derivative of its
- * forward. Elementwise over [rows, cols]; cols, ld, ldo, ldgh multiples of 8. */
-int vmoe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t ld, uint16_t* h, int64_t ldo,
-                int64_t rows, int64_t cols, vmoe_stream_t stream);
-int vmoe_swiglu_grad(const uint16_t* grad_h, int64_t ldgh, const uint16_t* gate,
-                     const uint16_t* up, int64_t ld, uint16_t* grad_gate, uint16_t* grad_up,
-                     int64_t ldo, int64_t rows, int64_t cols, vmoe_stream_t stream);
+/* SwiGLU up projection (activation="swiglu"; the reference's
+ * _grouped_gemm_up_kernel with ACTIVATION == 2, triton_moe/kernels/
+ * grouped_gemm.py:293-349): expert e's gate columns are W1[:, ewo_e + c] and
+ * its up columns W1[:, ewo_e + w_e + c], c < w_e (ewo need not be contiguous
+ * in steps of 2 w_e; widths <= max_width, multiples of 8). One GEMM stages
+ * both halves of 128 output columns per tile and, from the fp32
+ * accumulators g and u,
+ *   out  = bf16(row_scale * (g * sigmoid(g)) * u)   (row_scale nullable: 1)
+ *   gate = bf16(g), up = bf16(u)
+ * each output nullable (not all three), [rows, max_width] with row stride
+ * ldo; rows, gather_map and the other arguments as vmoe_gemm_up_fwd. The
+ * reference saves the gate as pre_act. */
+int vmoe_gemm_up_glu(const uint16_t* x, int64_t ldx, int64_t x_rows, const int32_t* gather_map,
+                     const uint16_t* w1, int64_t ldw1, uint16_t* out, uint16_t* gate,
+                     uint16_t* up, int64_t ldo, const float* row_scale, const int32_t* eto,
+                     const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
+                     int32_t num_experts, int64_t hidden, int64_t max_width,
+                     int64_t rows_bound, vmoe_stream_t stream);
+
+/* SwiGLU backward (the reference's is an unfinished placeholder,
+ * grouped_gemm.py:768-790; this is the derivative of the forward above):
+ * for each row r of expert e (eto[e] <= r < eto[e+1], r < rows) and c < w_e,
+ *   grad_gu[r, c]       = dG = bf16(gh * u * s * (1 + g * (1 - s)))
+ *   grad_gu[r, w_e + c] = dU = bf16(gh * g * s),   s = sigmoid(g)
+ * from grad_h (gh), gate (g) and up (u) at [r, c]; rows past the expert's
+ * min(tpe[e], eto[e+1] - eto[e]) get zeros. grad_gu [rows, >= 2 max_width]
+ * is then the gradient of the expert's 2 w_e contiguous W1 columns: one
+ * vmoe_gemm_up_bwd_dx and one vmoe_gemm_up_bwd_dw with widths 2 w_e give
+ * grad_x and grad_w1. Strides and max_width multiples of 8. */
+int vmoe_glu_grad(const uint16_t* grad_h, int64_t ldgh, const uint16_t* gate,
+                  const uint16_t* up, int64_t ld, uint16_t* grad_gu, int64_t ldo,
+                  const int32_t* eto, const int32_t* widths, const int32_t* tpe,
+                  int32_t num_experts, int64_t rows, int64_t max_width, vmoe_stream_t stream);
 
 /* grad_x = GA_e @ W1_e^T, GA = gradient w.r.t. the pre-activation (the output
  * of vmoe_relu2_grad, or grad_h itself for activation "none").

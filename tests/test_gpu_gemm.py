@@ -23,7 +23,7 @@ from triton_moe.kernels import (
     grouped_gemm_up_backward,
 )
 
-from _util import LOOSE, TIGHT, assert_close_norm, expert_rows
+from _util import LOOSE, TIGHT, assert_close_norm, bits_equal, expert_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -528,8 +528,9 @@ def test_swiglu_forward_backward(public_backward, skew, device):
     """activation="swiglu" (gate at ewo_e + c, up at ewo_e + w_e + c, as the
     reference's forward, grouped_gemm.py:295-349) against float64 autograd of
     the oracle; the backward the reference leaves unfinished (:768-790) is
-    held to the same LOOSE normwise tolerance (gate, up, dG, dU and the two
-    dX halves are rounded to bf16)."""
+    held to the same LOOSE normwise tolerance (gate, up, dG and dU are
+    rounded to bf16). test_swiglu_rounding_order holds both at TIGHT to an
+    fp32 reference with the kernels' rounding points."""
     from oracle import eager
     from triton_moe.kernels import grouped_gemm_up_autograd, grouped_gemm_up_backward
 
@@ -591,3 +592,81 @@ def test_swiglu_gather_map_path(device):
                                        activation="swiglu", gather_map=gmd)
     assert_close_norm(gx, xg64.grad, LOOSE, "swiglu grad_x gm")
     assert_close_norm(gw1, w164.grad, LOOSE, "swiglu grad_w1 gm")
+
+
+def _glu_ref32(c, xg, w1, offs, G):
+    """fp32 swiglu with the fused kernels' rounding points: H = bf16(silu(g) u)
+    and gate = bf16(g) from fp32 g, u; the backward from the bf16 gate and up
+    (dG, dU rounded to bf16) with grad_x one fp32 sum over both halves and
+    grad_w1 per column, each rounded once."""
+    P, max_w, d = c["P"], c["max_w"], c["d"]
+    h = torch.zeros(P, max_w)
+    gate = torch.zeros(P, max_w)
+    gx = torch.zeros(P, d)
+    gw1 = torch.zeros(w1.shape)
+    for e, (r0, r1) in enumerate(c["rows"]):
+        w, o = c["widths"][e], offs[e]
+        x32 = xg[r0:r1].float()
+        wg, wu = w1[:, o:o + w].float(), w1[:, o + w:o + 2 * w].float()
+        g, u = x32 @ wg, x32 @ wu
+        h[r0:r1, :w] = bf(g * torch.sigmoid(g) * u)
+        gate[r0:r1, :w] = bf(g)
+        gb, ub = bf(g), bf(u)
+        sg = torch.sigmoid(gb)
+        gh = G[r0:r1, :w].float()
+        dg = bf(gh * ub * sg * (1 + gb * (1 - sg)))
+        du = bf(gh * gb * sg)
+        gx[r0:r1] = bf(dg @ wg.T + du @ wu.T)
+        gw1[:, o:o + w] = bf(x32.T @ dg)
+        gw1[:, o + w:o + 2 * w] = bf(x32.T @ du)
+    return h, gate, gx, gw1
+
+
+@pytest.mark.parametrize("gapped,public_backward", [(False, False), (False, True),
+                                                    (True, False), (True, True)])
+def test_swiglu_rounding_order(gapped, public_backward, device):
+    """The fused swiglu (one GEMM whose epilogue forms silu(g) u from the fp32
+    accumulators, the reference's order, grouped_gemm.py:347-349; backward
+    as [dG | dU] through one dX and one dW GEMM) against an fp32 reference
+    with the same rounding points at TIGHT, with W1's expert column ranges
+    contiguous (2 w_e apart) or with gaps between them (the backward then
+    gathers the ranges into a contiguous copy)."""
+    from triton_moe.kernels import grouped_gemm_up_autograd, grouped_gemm_up_backward
+
+    c = _swiglu_case(seed=51, skew=True)
+    offs = c["offs2"]
+    w1 = c["w1s"]
+    if gapped:
+        offs = [o + 8 * e for e, o in enumerate(offs)]
+        g = torch.Generator().manual_seed(52)
+        w1 = (torch.randn(c["d"], offs[-1] + 16, generator=g) * 0.05).to(torch.bfloat16)
+    ewo = torch.tensor(offs, dtype=torch.int32).to(device)
+    eto, _, wid, tpe = _meta_dev(c, device)
+    G = torch.randn(c["P"], c["max_w"], generator=torch.Generator().manual_seed(53))
+    G = G.to(torch.bfloat16)
+    for e, (r0, r1) in enumerate(c["rows"]):
+        G[r0:r1, c["widths"][e]:] = 0
+    h_ref, gate_ref, gx_ref, gw1_ref = _glu_ref32(c, c["xg"], w1, offs, G.float())
+    xg, w1d = c["xg"].to(device), w1.to(device)
+    out, pre = grouped_gemm_up(xg, w1d, eto, ewo, wid, tpe, c["max_w"], activation="swiglu",
+                               save_pre_act=True)
+    assert_close_norm(out, h_ref, TIGHT, "fused swiglu H")
+    assert_close_norm(pre, gate_ref, TIGHT, "fused swiglu gate")
+    if public_backward:
+        gx, gw1 = grouped_gemm_up_backward(G.to(device), xg, w1d, pre, eto, ewo, wid, tpe,
+                                           c["d"], activation="swiglu")
+    else:
+        xr = xg.clone().requires_grad_(True)
+        w1r = w1d.clone().requires_grad_(True)
+        o2 = grouped_gemm_up_autograd(xr, w1r, eto, ewo, wid, tpe, c["max_w"], c["d"],
+                                      activation="swiglu")
+        assert bits_equal(o2, out)
+        o2.backward(G.to(device))
+        gx, gw1 = xr.grad, w1r.grad
+    assert_close_norm(gx, gx_ref, TIGHT, "fused swiglu grad_x")
+    assert_close_norm(gw1, gw1_ref, TIGHT, "fused swiglu grad_w1")
+    if gapped:
+        used = torch.zeros(w1.shape[1], dtype=torch.bool)
+        for e, o in enumerate(offs[:-1]):
+            used[o:o + 2 * c["widths"][e]] = True
+        assert int(gw1.cpu()[:, ~used].abs().sum()) == 0, "columns outside the experts"

@@ -74,7 +74,7 @@ constexpr int kRecExperts = 256;   // per-expert metadata also held in LDS up to
 constexpr int kLane = 4;           // dW GEMMs: workgroups of one XCD that share each K chunk
 constexpr int kMaxLanes = 64;      // dW GEMMs: lanes (grid / kLane) a launch may have
 
-enum Variant { UP_FWD = 0, DOWN_FWD, UP_DX, UP_DW, DOWN_DH, DOWN_DW };
+enum Variant { UP_FWD = 0, DOWN_FWD, UP_DX, UP_DW, DOWN_DH, DOWN_DW, UP_GLU };
 
 struct Args {
   const uint16_t* a;     // A source
@@ -85,7 +85,8 @@ struct Args {
   int64_t ldb;
   uint16_t* c;
   int64_t ldc;
-  uint16_t* c2;          // UP_FWD: pre_act output (nullable)
+  uint16_t* c2;          // UP_FWD: pre_act output; UP_GLU: gate output (nullable)
+  uint16_t* c3;          // UP_GLU: up output (nullable); c, c2 and c3 share ldc
   const uint16_t* pre;   // DOWN_DH: pre_act input -> fused relu^2 gradient (nullable)
   const int32_t* b_map;  // row gather for B (T-form; no variant uses it), nullable
   int64_t b_rows;        // rows of B's gathered source
@@ -178,6 +179,14 @@ struct Traits<UP_FWD> {
     return q;
   }
 };
+
+// SwiGLU up projection (the reference's ACTIVATION == 2 path,
+// grouped_gemm.py:293-349): the B tile's 256 staged columns are the gate
+// columns W1[:, ewo + n] and the up columns W1[:, ewo + w + n] of 128 output
+// columns n, interleaved per 32 (setup_glu), so that each consumer wave
+// holds gate and up of the same 32 outputs in its two accumulator blocks.
+template <>
+struct Traits<UP_GLU> : Traits<UP_FWD> {};
 
 template <>
 struct Traits<DOWN_FWD> {
@@ -293,6 +302,11 @@ struct Cfg {
 
 __host__ __device__ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// Output columns of a tile: BN, except UP_GLU, whose BN staged columns are
+// the gate and up halves of BN / 2 outputs.
+template <int V>
+__host__ __device__ constexpr int out_cols() { return V == UP_GLU ? Cfg<V>::BN / 2 : Cfg<V>::BN; }
+
 // Split-K chunk of the dW GEMMs: K rows per work item (p.kc is 0 or this).
 // Small chunks let the contiguous item ranges balance experts of very
 // different row counts; the chunks of one tile inside one range accumulate
@@ -305,7 +319,7 @@ constexpr int kDwChunk = 512;
 template <int V>
 __device__ __forceinline__ void expert_work(const Args& p, const Prob& q, int& tiles,
                                             int& chunks) {
-  constexpr int BM = Cfg<V>::BM, BN = Cfg<V>::BN;
+  constexpr int BM = Cfg<V>::BM, BN = out_cols<V>();
   tiles = (q.M > 0 && q.N > 0) ? cdiv(q.M, BM) * cdiv(q.N, BN) : 0;
   chunks = (Cfg<V>::contig && p.kc > 0 && tiles > 0 && q.K > kDwChunk) ? cdiv(q.K, kDwChunk) : 1;
 }
@@ -320,6 +334,9 @@ __device__ __forceinline__ int udiv_small(int x, int d) {
   q += (q + 1) * d <= x ? 1 : 0;
   return q;
 }
+
+// sigmoid in fp32, 1 / (1 + exp(-x)) with the precise exp.
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -537,7 +554,7 @@ struct Gemm {
   // item's last stage, kStages - 1 stages ahead of the consumers, and every
   // item has at least one stage, so the slot of item n - kStages - 1 is the
   // newest one a consumer can still be reading.
-  static constexpr bool kScaled = V == UP_FWD || V == DOWN_DH;
+  static constexpr bool kScaled = V == UP_FWD || V == UP_GLU || V == DOWN_DH;
   static constexpr int kScaleSlots = kStages + 1;
   struct TMap {
     __amdgpu_buffer_rsrc_t mrs;  // over the row map
@@ -633,6 +650,28 @@ struct Gemm {
       // the column offset, to which the gathered row's offset is added.
       s.off[i] = map ? (uint32_t)(c * 16)
                      : (s.ok[i] ? (uint32_t)(c * 16 + (int64_t)krow * ld * 2) : kOob);
+    }
+  }
+
+  // UP_GLU's B operand (T-form, no map): staged chunk q (8 columns) of a
+  // k-row holds output columns 32 (q / 8) + 8 (q % 4) .. + 7 of the tile, from
+  // the gate columns (c0 + n) for q % 8 < 4 and from the up columns
+  // (c0 + up + n) otherwise; out_valid output columns are real.
+  __device__ static void setup_glu(Src<PWB>& s, const uint16_t* base, int64_t ld, int64_t r0,
+                                   int64_t c0, int up, int out_valid) {
+    constexpr int LPR = Dma<BN>::LPR, RPI = Dma<BN>::RPI;
+    const int lane = threadIdx.x & 63, wave = pwave();
+    s.rsrc = make_rsrc(base + r0 * ld + c0);
+    s.ld2 = (uint32_t)(ld * 2);
+#pragma unroll
+    for (int i = 0; i < PWB; ++i) {
+      const int krow = (wave * PWB + i) * RPI + lane / LPR;
+      const int c = (lane % LPR) ^ tswz(krow);
+      const int oc = (c >> 3) * 4 + (c & 3);  // output chunk
+      s.idx[i] = krow;
+      s.ok[i] = oc * 8 < out_valid;
+      s.off[i] = s.ok[i] ? (uint32_t)(oc * 16 + ((c >> 2) & 1) * up * 2 + (int64_t)krow * ld * 2)
+                         : kOob;
     }
   }
 
@@ -903,10 +942,11 @@ struct Gemm {
     const int chunk = local - group * chunks;
     const int tile = Cfg<V>::contig ? group * kLane + slot : group;
     w.skip = tile >= tiles;
-    const int n_tiles = cdiv(w.q.N, BN);
+    constexpr int BNO = out_cols<V>();
+    const int n_tiles = cdiv(w.q.N, BNO);
     const int mt_idx = n_tiles == 1 ? tile : udiv_small(tile, n_tiles);
     w.m0 = mt_idx * BM;
-    w.n0 = (tile - mt_idx * n_tiles) * BN;
+    w.n0 = (tile - mt_idx * n_tiles) * BNO;
     w.kbeg = 0;
     w.chunk = chunk;
     w.chunks = chunks;
@@ -944,7 +984,9 @@ struct Gemm {
     else
       setup_t<BM, PWA, T::t_map>(sa, tm, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.kbeg,
                                  q.ac + w.m0, q.M - w.m0, w.klen, !T::t_map_b);
-    if (T::b_k)
+    if (V == UP_GLU)
+      setup_glu(sb, p.b, p.ldb, q.br + w.kbeg, q.bc + w.n0, q.N, q.N - w.n0);
+    else if (T::b_k)
       setup_k<BN, PWB, false>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg, q.N - w.n0,
                               nullptr);
     else
@@ -1014,8 +1056,10 @@ struct Gemm {
   // ds_read_b128 phase covers two whole rows over all 64 banks.
   static constexpr int EPI_BYTES = 32 * 64 * 2;
   static_assert(WN == 64 && FN == 2 && FM == 2, "epilogue assumes 64x64 wave tiles");
-  // UP_FWD with relu^2 stores PRE and H; every other variant one output.
-  static constexpr int NOUT = V == UP_FWD ? 2 : 1;
+  // UP_FWD with relu^2 stores PRE and H; UP_GLU [gate | up] blocks and H
+  // (the right half of its H blocks is unused); every other variant one
+  // output.
+  static constexpr int NOUT = V == UP_FWD || V == UP_GLU ? 2 : 1;
 
   // Pending blocks are units u = out * FM + i (output-major, row block i);
   // every unit index is a compile-time constant where the block is used, so
@@ -1119,8 +1163,33 @@ struct Gemm {
       return;
     }
     pd.mb = w.m0 + wm * WM;
-    pd.nb = w.n0 + wn * WN;
+    pd.nb = w.n0 + wn * (V == UP_GLU ? WN / 2 : WN);
     pd.M = q.M; pd.N = q.N; pd.cr = q.cr; pd.cc = q.cc;
+    if constexpr (V == UP_GLU) {
+      // Block j = 0 holds the gate g, j = 1 the up projection u of the same
+      // 32 outputs: gate and up (bf16) go to unit (0, i), H = bf16(g
+      // sigmoid(g) u) (from the fp32 accumulators, times the row factor) to
+      // unit (1, i).
+      const int rows = pd.mb >= q.M ? 0 : (pd.mb + 32 >= q.M ? 1 : 3);
+      pd.mask = (p.c ? rows << FM : 0) | (p.c2 || p.c3 ? rows : 0);
+      if (pd.mask == 0) return;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const float ga = acc[i][0][4 * g + 2 * hh], gb = acc[i][0][4 * g + 2 * hh + 1];
+            const float ua = acc[i][1][4 * g + 2 * hh], ub = acc[i][1][4 * g + 2 * hh + 1];
+            pd.pk[0][i][0][2 * g + hh] = pack_bf16(ga, gb);
+            pd.pk[0][i][1][2 * g + hh] = pack_bf16(ua, ub);
+            pd.pk[1][i][0][2 * g + hh] =
+                pack_bf16(sc[i] * ((ga * sigmoid_f32(ga)) * ua),
+                          sc[i] * ((gb * sigmoid_f32(gb)) * ub));
+            pd.pk[1][i][1][2 * g + hh] = 0u;
+          }
+      return;
+    }
     const bool two = V == UP_FWD && p.act == VMOE_ACT_RELU_SQUARED && p.c2;
     // Row blocks starting inside the problem (wave-uniform): none, the first, or both.
     const int rows = pd.mb >= q.M ? 0 : (pd.mb + 32 >= q.M ? 1 : 3);
@@ -1218,6 +1287,22 @@ struct Gemm {
           if ((lane & 7) == 0 && m < pd.M && pd.nb < pd.N)
             p.row_dot[((int64_t)pd.cr + m) * p.ld_rd + ((pd.cc + pd.nb) >> 6)] = s;
         }
+      }
+      return;
+    }
+    if constexpr (V == UP_GLU) {
+      // Chunk c of a scratch row: unit 0 gate (c < 4) / up (c >= 4), unit 1
+      // H (c < 4), at output column nb + 8 (c % 4).
+      const int c = lane & 7;
+      const int ng = pd.nb + 8 * (c & 3);
+      uint16_t* go = OUT == 1 ? (c < 4 ? p.c : nullptr) : (c < 4 ? p.c2 : p.c3);
+      const bool ok = go != nullptr && ng < pd.N;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const uint4 v = epi_read(scr, qq, lane);
+        const int m = mb + 8 * qq + (lane >> 3);
+        if (ok && m < pd.M)
+          *reinterpret_cast<uint4*>(go + ((int64_t)pd.cr + m) * p.ldc + pd.cc + ng) = v;
       }
       return;
     }
@@ -1536,7 +1621,8 @@ struct Gemm {
       // (measured at cfg3, same box, three runs: up fwd -6 us, dH -1.6 us;
       // on the down projection, with 8 k-steps per item, +14 us).
       const int stagger =
-          (V == UP_FWD || V == DOWN_DH) ? (int)((blockIdx.x >> 3) % (unsigned)gap) : 0;
+          (V == UP_FWD || V == UP_GLU || V == DOWN_DH) ? (int)((blockIdx.x >> 3) % (unsigned)gap)
+                                                       : 0;
       int kt = 0;
       if (pd.mask & 1) load_pre<0>(p, pd, pr);
 #pragma unroll
@@ -1621,53 +1707,63 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
   G::run(p, (lds_char*)ring, meta, (lds_char*)epi, (lds_char*)wins, (lds_char*)scl);
 }
 
-// SwiGLU on [rows, cols] bf16 pairs (gate g, up u) from the two halves of an
-// expert's W1 columns (the reference's layout, grouped_gemm.py:295-297 and its
-// epilogue silu(gate) * up, :347-349):
-//   forward   H  = bf16(silu(g) * u),            silu(g) = g * sigmoid(g)
-//   backward  dG = bf16(gh * u * s * (1 + g (1 - s))), dU = bf16(gh * g * s),
-//             s = sigmoid(g)
-// The reference's backward for it is an unfinished placeholder
-// (grouped_gemm.py:768-790); this is the derivative of the forward above.
-__device__ __forceinline__ float sigm(float g) { return 1.0f / (1.0f + expf(-g)); }
+// SwiGLU (activation "swiglu"; the reference's forward epilogue
+// silu(gate) * up, grouped_gemm.py:347-349, and an unfinished backward,
+// :768-790): the forward is the UP_GLU GEMM; its derivative is
+//   dG = bf16(gh * u * s * (1 + g (1 - s))), dU = bf16(gh * g * s),
+//   s = sigmoid(g), from the bf16 gate g and up u the forward stored.
 
-template <bool BWD>
-__global__ __launch_bounds__(256) void swiglu_kernel(
+// SwiGLU backward into the layout of the fused up projection's backward
+// GEMMs: for row r of expert e (eto[e] <= r < eto[e+1]) and c < w_e,
+// grad_gu[r, c] = dG and grad_gu[r, w_e + c] = dU (formulas above), from
+// grad_h, gate and up at [r, c]; rows r >= eto[e] + min(tpe[e], eto[e+1] -
+// eto[e]) of the expert hold zeros there. [dG | dU] per row is then the A
+// operand of one dX GEMM and one dW GEMM over the expert's 2 w_e contiguous
+// W1 columns. One wave per row.
+__global__ __launch_bounds__(256) void glu_grad_kernel(
     const uint16_t* __restrict__ gh, int64_t ldgh, const uint16_t* __restrict__ gate,
-    const uint16_t* __restrict__ up, int64_t ld, uint16_t* __restrict__ o0,
-    uint16_t* __restrict__ o1, int64_t ldo, int64_t rows, int64_t cols) {
-  const int64_t vpr = cols / 8;
-  const int64_t total = rows * vpr;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / vpr, c = (i % vpr) * 8;
-    const uint4 gv = *reinterpret_cast<const uint4*>(gate + r * ld + c);
-    const uint4 uv = *reinterpret_cast<const uint4*>(up + r * ld + c);
-    uint4 hv = make_uint4(0, 0, 0, 0);
-    if (BWD) hv = *reinterpret_cast<const uint4*>(gh + r * ldgh + c);
+    const uint16_t* __restrict__ up, int64_t ld, uint16_t* __restrict__ ggu, int64_t ldo,
+    const int32_t* __restrict__ eto, const int32_t* __restrict__ widths,
+    const int32_t* __restrict__ tpe, int E, int64_t rows, int max_width) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows || r < eto[0] || r >= eto[E]) return;
+  // the expert: the last e with eto[e] <= r (an empty expert before it has
+  // a smaller index, one after it starts past r)
+  int lo = 0, hi = E;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (eto[mid] <= r) lo = mid; else hi = mid;
+  }
+  const int e = lo, w = min(widths[e], max_width);
+  const bool live = r - eto[e] < min(tpe[e], eto[e + 1] - eto[e]);
+  for (int c = lane * 8; c < w; c += 64 * 8) {
+    uint4 gv = make_uint4(0, 0, 0, 0), uv = gv, hv = gv;
+    if (live) {
+      gv = *reinterpret_cast<const uint4*>(gate + r * ld + c);
+      uv = *reinterpret_cast<const uint4*>(up + r * ld + c);
+      hv = *reinterpret_cast<const uint4*>(gh + r * ldgh + c);
+    }
     const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
     const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
     uint32_t a[4], b[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float gf[2] = {lo_f32(gw[j]), hi_f32(gw[j])}, uf[2] = {lo_f32(uw[j]), hi_f32(uw[j])};
-      float hf[2] = {lo_f32(hw[j]), hi_f32(hw[j])}, ra[2], rb[2];
+      float ra[2], rb[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const float sg = sigm(gf[h]);
-        if (BWD) {
-          ra[h] = hf[h] * uf[h] * sg * (1.0f + gf[h] * (1.0f - sg));
-          rb[h] = hf[h] * gf[h] * sg;
-        } else {
-          ra[h] = gf[h] * sg * uf[h];
-          rb[h] = 0.0f;
-        }
+        const float g = h ? hi_f32(gw[j]) : lo_f32(gw[j]);
+        const float u = h ? hi_f32(uw[j]) : lo_f32(uw[j]);
+        const float d = h ? hi_f32(hw[j]) : lo_f32(hw[j]);
+        const float sg = sigmoid_f32(g);
+        ra[h] = d * u * sg * (1.0f + g * (1.0f - sg));
+        rb[h] = d * g * sg;
       }
       a[j] = pack_bf16(ra[0], ra[1]);
       b[j] = pack_bf16(rb[0], rb[1]);
     }
-    *reinterpret_cast<uint4*>(o0 + r * ldo + c) = make_uint4(a[0], a[1], a[2], a[3]);
-    if (BWD) *reinterpret_cast<uint4*>(o1 + r * ldo + c) = make_uint4(b[0], b[1], b[2], b[3]);
+    *reinterpret_cast<uint4*>(ggu + r * ldo + c) = make_uint4(a[0], a[1], a[2], a[3]);
+    *reinterpret_cast<uint4*>(ggu + r * ldo + w + c) = make_uint4(b[0], b[1], b[2], b[3]);
   }
 }
 
@@ -1766,7 +1862,7 @@ int64_t tiles_max(int64_t mmax, int64_t nmax) {
 template <int V>
 int64_t row_items(int64_t rows_bound, int E, int64_t nmax) {
   return ((rows_bound + Cfg<V>::BM - 1) / Cfg<V>::BM + E) *
-         ((nmax + Cfg<V>::BN - 1) / Cfg<V>::BN);
+         ((nmax + out_cols<V>() - 1) / out_cols<V>());
 }
 
 // dW GEMM with split-K (one launch; split tiles are summed in the kernel).
@@ -1855,6 +1951,33 @@ extern "C" int vmoe_gemm_up_fwd(const uint16_t* x, int64_t ldx, int64_t x_rows,
                         reinterpret_cast<hipStream_t>(stream));
 }
 
+extern "C" int vmoe_gemm_up_glu(const uint16_t* x, int64_t ldx, int64_t x_rows,
+                                const int32_t* gather_map, const uint16_t* w1, int64_t ldw1,
+                                uint16_t* out, uint16_t* gate, uint16_t* up, int64_t ldo,
+                                const float* row_scale, const int32_t* eto, const int32_t* ewo,
+                                const int32_t* widths, const int32_t* tpe, int32_t E,
+                                int64_t hidden, int64_t max_width, int64_t rows_bound,
+                                vmoe_stream_t stream) {
+  int st = check_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
+  if (st) return st;
+  if (!x || !w1 || (!out && !gate && !up) || x_rows < 0) return VMOE_ERR_INVALID_ARG;
+  if (!src_ld_ok(ldx, hidden, gather_map) || !ld_ok(ldw1) || !ld_ok(ldo) || ldo < max_width)
+    return VMOE_ERR_UNSUPPORTED;
+  if (!a16(x) || !a16(w1) || (out && !a16(out)) || (gate && !a16(gate)) || (up && !a16(up)))
+    return VMOE_ERR_UNSUPPORTED;
+  if ((gather_map && !span_ok(x_rows, ldx)) || !span_ok(hidden, ldw1))
+    return VMOE_ERR_UNSUPPORTED;
+  Args p{};
+  p.a = x; p.lda = ldx; p.a_map = gather_map; p.a_rows = gather_map ? x_rows : 0;
+  p.b = w1; p.ldb = ldw1;
+  p.c = out; p.c2 = gate; p.c3 = up; p.ldc = ldo;
+  p.row_scale = row_scale;
+  p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
+  p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
+  return launch<UP_GLU>(p, row_items<UP_GLU>(rows_bound, E, max_width),
+                        reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" int vmoe_gemm_down_fwd(const uint16_t* h, int64_t ldh, const uint16_t* w2,
                                   int64_t ldw2, uint16_t* y, int64_t ldy, const int32_t* eto,
                                   const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
@@ -1877,38 +2000,22 @@ extern "C" int vmoe_gemm_down_fwd(const uint16_t* h, int64_t ldh, const uint16_t
                           reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int vmoe_swiglu(const uint16_t* gate, const uint16_t* up, int64_t ld, uint16_t* h,
-                           int64_t ldo, int64_t rows, int64_t cols, vmoe_stream_t stream) {
-  if (rows < 0 || cols < 0 || ld < cols || ldo < cols) return VMOE_ERR_INVALID_ARG;
-  if (rows == 0 || cols == 0) return VMOE_OK;
-  if (!gate || !up || !h) return VMOE_ERR_INVALID_ARG;
-  if (cols % 8 || ld % 8 || ldo % 8 || !a16(gate) || !a16(up) || !a16(h))
-    return VMOE_ERR_UNSUPPORTED;
-  const int64_t n = rows * (cols / 8);
-  const int64_t grid = std::min<int64_t>((n + 255) / 256, 65536);
-  hipLaunchKernelGGL(swiglu_kernel<false>, dim3((unsigned)grid), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), nullptr, 0, gate, up, ld, h,
-                     nullptr, ldo, rows, cols);
-  VMOE_CHECK_LAUNCH();
-  return VMOE_OK;
-}
-
-extern "C" int vmoe_swiglu_grad(const uint16_t* grad_h, int64_t ldgh, const uint16_t* gate,
-                                const uint16_t* up, int64_t ld, uint16_t* grad_gate,
-                                uint16_t* grad_up, int64_t ldo, int64_t rows, int64_t cols,
-                                vmoe_stream_t stream) {
-  if (rows < 0 || cols < 0 || ld < cols || ldo < cols || ldgh < cols)
+extern "C" int vmoe_glu_grad(const uint16_t* grad_h, int64_t ldgh, const uint16_t* gate,
+                             const uint16_t* up, int64_t ld, uint16_t* grad_gu, int64_t ldo,
+                             const int32_t* eto, const int32_t* widths, const int32_t* tpe,
+                             int32_t E, int64_t rows, int64_t max_width, vmoe_stream_t stream) {
+  if (rows < 0 || E <= 0 || max_width < 0 || ld < max_width || ldgh < max_width ||
+      ldo < 2 * max_width)
     return VMOE_ERR_INVALID_ARG;
-  if (rows == 0 || cols == 0) return VMOE_OK;
-  if (!grad_h || !gate || !up || !grad_gate || !grad_up) return VMOE_ERR_INVALID_ARG;
-  if (cols % 8 || ld % 8 || ldo % 8 || ldgh % 8 || !a16(grad_h) || !a16(gate) || !a16(up) ||
-      !a16(grad_gate) || !a16(grad_up))
+  if (rows == 0 || max_width == 0) return VMOE_OK;
+  if (!grad_h || !gate || !up || !grad_gu || !eto || !widths || !tpe)
+    return VMOE_ERR_INVALID_ARG;
+  if (E > kMaxExperts || max_width % 8 || ld % 8 || ldo % 8 || ldgh % 8 || !a16(grad_h) ||
+      !a16(gate) || !a16(up) || !a16(grad_gu) || max_width > INT32_MAX / 2)
     return VMOE_ERR_UNSUPPORTED;
-  const int64_t n = rows * (cols / 8);
-  const int64_t grid = std::min<int64_t>((n + 255) / 256, 65536);
-  hipLaunchKernelGGL(swiglu_kernel<true>, dim3((unsigned)grid), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), grad_h, ldgh, gate, up, ld,
-                     grad_gate, grad_up, ldo, rows, cols);
+  hipLaunchKernelGGL(glu_grad_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), grad_h, ldgh, gate, up, ld, grad_gu,
+                     ldo, eto, widths, tpe, E, rows, (int)max_width);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }

@@ -45,8 +45,10 @@ _SIGNATURES = {
     "vmoe_gemm_down_fwd": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
                            _i64, _i64, _vp],
     "vmoe_relu2_grad": [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp],
-    "vmoe_swiglu": [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp],
-    "vmoe_swiglu_grad": [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp],
+    "vmoe_gemm_up_glu": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+                         _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "vmoe_glu_grad": [_vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i32, _i64, _i64,
+                      _vp],
     "vmoe_gemm_up_bwd_dx": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
                             _i64, _i64, _vp],
     "vmoe_gemm_dw_workspace_bytes": [_i32, _i64, _i64, _i64],

@@ -32,7 +32,7 @@ from .gather import row_maps
 _ACTIVATIONS = {"none": _lib.ACT_NONE, "relu_squared": _lib.ACT_RELU_SQUARED}
 
 
-ACT_SWIGLU = 2  # host-side only: two grouped GEMMs without activation + vmoe_swiglu
+ACT_SWIGLU = 2  # host-side code of activation="swiglu" (vmoe_gemm_up_glu)
 
 
 def _activation_code(activation: str) -> int:
@@ -414,78 +414,110 @@ def precompute_gather_map(indices, bin_ids, bins, padded_bins, top_k):
 # ---------------------------------------------------------------------------
 # SwiGLU: expert e's gate columns are W1[:, ewo_e : ewo_e + w_e] and its up
 # columns W1[:, ewo_e + w_e : ewo_e + 2 w_e] (the reference's layout,
-# grouped_gemm.py:295-297). The halves are gathered into two contiguous
-# weight matrices, each run as a plain grouped GEMM, and combined by the
-# elementwise vmoe_swiglu / vmoe_swiglu_grad kernels.
+# grouped_gemm.py:295-297). The forward is one grouped GEMM whose epilogue
+# forms H = bf16(silu(g) u) from the fp32 accumulators (vmoe_gemm_up_glu);
+# the backward writes [dG | dU] per expert row (vmoe_glu_grad), the
+# gradient of the expert's 2 w_e W1 columns, so grad_x and grad_w1 are one
+# dX and one dW GEMM over widths 2 w_e.
 # ---------------------------------------------------------------------------
 
 
-def swiglu_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, w1_cols: int):
-    """(GemmMeta over the compacted halves, gate column index, up column index)."""
+@dataclass
+class GluMeta:
+    """fwd: the forward's metadata (widths w_e, gate columns at ewo_e);
+    bwd: the backward GEMMs' (widths 2 w_e over contiguous column ranges);
+    cols: W1 columns of those ranges when W1's own expert ranges are not
+    contiguous (None: bwd addresses W1 directly)."""
+
+    fwd: GemmMeta
+    bwd: GemmMeta
+    cols: torch.Tensor | None
+
+
+def glu_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, w1_cols: int) -> GluMeta:
+    """Validates swiglu metadata on the host (one device->host copy)."""
     E = int(torch.as_tensor(widths).numel())
     if E == 0:
         raise ValueError("expert_widths is empty")
-    h_ewo = _i32(ewo)[:E + 1].cpu().tolist()
-    h_w = _i32(widths)[:E].cpu().tolist()
+    eto_d, ewo_d, w_d, tpe_d = _i32(eto), _i32(ewo), _i32(widths), _i32(tpe)
+    if eto_d.numel() < E + 1 or ewo_d.numel() < E + 1 or tpe_d.numel() < E:
+        raise ValueError("expert metadata shorter than num_experts (+1)")
+    h_ewo = ewo_d[:E + 1].cpu().tolist()
+    h_w = w_d[:E].cpu().tolist()
     if any(w < 0 or o < 0 or o + 2 * w > w1_cols for o, w in zip(h_ewo, h_w)):
         raise ValueError("swiglu: expert gate/up columns exceed the weight matrix")
+    # The forward reads only ewo_e (gate) and ewo_e + w_e (up) of each
+    # expert; rows, widths and alignment are checked as for any grouped GEMM
+    # (widths 2 w_e over a contiguous stand-in column layout).
     cum = [0]
     for w in h_w:
-        cum.append(cum[-1] + w)
-    dev = torch.as_tensor(widths).device
-    gate = torch.cat([torch.arange(o, o + w) for o, w in zip(h_ewo, h_w)] or
-                     [torch.zeros(0, dtype=torch.long)]).to(dev)
-    up = torch.cat([torch.arange(o + w, o + 2 * w) for o, w in zip(h_ewo, h_w)] or
-                   [torch.zeros(0, dtype=torch.long)]).to(dev)
-    m = host_meta(eto, torch.tensor(cum, dtype=torch.int32, device=dev), widths, tpe,
-                  max_width, hidden, None, cum[-1])
-    return m, gate, up
+        cum.append(cum[-1] + 2 * w)
+    cum_d = torch.tensor(cum, dtype=torch.int32, device=w_d.device)
+    if any(o % 8 for o in h_ewo):
+        raise NotImplementedError("expert weight offsets must be multiples of 8")
+    chk = host_meta(eto_d, cum_d, w_d * 2, tpe_d, 2 * int(max_width), hidden, None, cum[-1])
+    if any(w > max_width for w in h_w):
+        raise ValueError("expert width outside [0, max_expert_width]")
+    fwd = GemmMeta(eto_d, ewo_d, w_d, tpe_d, E, int(max_width), chk.rows, chk.full_rows, False,
+                   all(w == max_width for w in h_w))
+    contiguous = all(h_ewo[e + 1] == h_ewo[e] + 2 * h_w[e] for e in range(E))
+    cols = None
+    dev = w_d.device
+    if contiguous:
+        bwd = host_meta(eto_d, ewo_d, w_d * 2, tpe_d, 2 * int(max_width), hidden, None, w1_cols)
+    else:
+        cols = torch.cat([torch.arange(o, o + 2 * w) for o, w in zip(h_ewo, h_w)]).to(dev)
+        bwd = chk
+    return GluMeta(fwd, bwd, cols)
 
 
-def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
-    """H = bf16(silu(gate) * up) elementwise (vmoe_swiglu)."""
-    gate, up = _same_ld(gate, up)
-    h = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
-    _lib.call("vmoe_swiglu", gate.data_ptr(), up.data_ptr(), gate.stride(0), h.data_ptr(),
-              h.stride(0), gate.shape[0], gate.shape[1], _lib.stream(gate.device))
-    return h
-
-
-def swiglu_grad(grad_h: torch.Tensor, gate: torch.Tensor, up: torch.Tensor):
-    """(grad_gate, grad_up) of swiglu (vmoe_swiglu_grad)."""
-    grad_h = _bf16(grad_h, "swiglu grad_output")
-    gate, up = _same_ld(gate, up)
-    gg = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
-    gu = torch.empty_like(gg)
-    _lib.call("vmoe_swiglu_grad", grad_h.data_ptr(), grad_h.stride(0), gate.data_ptr(),
-              up.data_ptr(), gate.stride(0), gg.data_ptr(), gu.data_ptr(), gg.stride(0),
-              gate.shape[0], gate.shape[1], _lib.stream(gate.device))
-    return gg, gu
-
-
-def swiglu_fwd(x, w1, m: GemmMeta, gate_idx, up_idx, gather_map=None):
-    """(H, gate, up), each [rows, max_width] with zero column tails."""
+def glu_fwd(x, w1, m: GemmMeta, want_h: bool, want_gate: bool, want_up: bool,
+            gather_map=None):
+    """(H, gate, up) of the swiglu up projection, each [rows, max_width] with
+    zero column tails (None where not wanted)."""
+    x = _bf16(x, "grouped_gemm_up x")
     w1 = _bf16(w1, "grouped_gemm_up w1")
-    g, _ = up_fwd(x, w1.index_select(1, gate_idx), m, _lib.ACT_NONE, False, zero_tails=True,
-                  gather_map=gather_map)
-    u, _ = up_fwd(x, w1.index_select(1, up_idx), m, _lib.ACT_NONE, False, zero_tails=True,
-                  gather_map=gather_map)
-    return swiglu(g, u), g, u
+    hidden = x.shape[1]
+    _need(w1.shape[0] == hidden, "w1 rows must equal the hidden size of x")
+    if gather_map is None:
+        _need(x.shape[0] >= m.rows, "x has fewer rows than expert_token_offsets[-1]")
+    else:
+        _need(gather_map.numel() >= m.rows, "gather_map shorter than the padded row count")
+    outs = [_alloc(m.rows, m.max_width, x, not m.full_rows) if want else None
+            for want in (want_h, want_gate, want_up)]
+    gm = None if gather_map is None else _i32(gather_map)
+    if m.rows > 0:
+        _lib.call("vmoe_gemm_up_glu", x.data_ptr(), x.stride(0), x.shape[0], _lib.ptr(gm),
+                  w1.data_ptr(), w1.stride(0), *(_lib.ptr(o) for o in outs), m.max_width, None,
+                  *_meta_args(m), hidden, m.max_width, m.rows, _lib.stream(x.device))
+        for o in outs:
+            if o is not None:
+                _zero_tails(o, m)
+    return tuple(outs)
 
 
-def swiglu_bwd(grad_h, x, w1, gate, up, m: GemmMeta, gate_idx, up_idx, hidden: int,
-               gather_map=None):
+def glu_bwd(grad_h, x, w1, gate, up, gm_: GluMeta, hidden: int, gather_map=None):
     """(grad_x in gathered rows, grad_w1 in W1's gate/up layout)."""
     w1 = _bf16(w1, "grouped_gemm_up_backward w1")
-    _need(grad_h.shape == gate.shape, "grad_output and pre_act shapes differ")
-    gg, gu = swiglu_grad(grad_h, gate, up)
-    w1g, w1u = w1.index_select(1, gate_idx), w1.index_select(1, up_idx)
-    # one bf16 rounding of the fp32 sum of the two bf16 halves
-    grad_x = up_bwd_dx(gg, w1g, m, hidden).float()
-    grad_x = (grad_x + up_bwd_dx(gu, w1u, m, hidden).float()).to(torch.bfloat16)
+    grad_h = _bf16(grad_h, "grouped_gemm_up_backward grad_output")
+    m = gm_.fwd
+    _need(grad_h.shape == gate.shape == up.shape, "grad_output and pre_act shapes differ")
+    _need(grad_h.shape[0] >= m.rows and grad_h.shape[1] >= m.max_width,
+          "grad_output smaller than [rows, max_expert_width]")
+    ggu = torch.empty(m.rows, 2 * m.max_width, dtype=torch.bfloat16, device=grad_h.device)
+    if m.rows > 0:
+        gate, up = _same_ld(gate, up)
+        _lib.call("vmoe_glu_grad", grad_h.data_ptr(), grad_h.stride(0), gate.data_ptr(),
+                  up.data_ptr(), gate.stride(0), ggu.data_ptr(), ggu.stride(0),
+                  m.eto.data_ptr(), m.widths.data_ptr(), m.tpe.data_ptr(), m.num_experts,
+                  m.rows, m.max_width, _lib.stream(grad_h.device))
+    wb = w1 if gm_.cols is None else w1.index_select(1, gm_.cols)
+    grad_x = up_bwd_dx(ggu, wb, gm_.bwd, hidden)
+    gw = up_bwd_dw(ggu, x, wb, gm_.bwd, hidden, gather_map)
+    if gm_.cols is None:
+        return grad_x, gw
     grad_w1 = torch.zeros_like(w1)
-    grad_w1.index_copy_(1, gate_idx, up_bwd_dw(gg, x, w1g, m, hidden, gather_map))
-    grad_w1.index_copy_(1, up_idx, up_bwd_dw(gu, x, w1u, m, hidden, gather_map))
+    grad_w1.index_copy_(1, gm_.cols, gw)
     return grad_x, grad_w1
 
 
@@ -501,10 +533,10 @@ def grouped_gemm_up(x, w1, expert_token_offsets, expert_weight_offsets, expert_w
     _lib.require_gpu(x)
     act = _activation_code(activation)
     if act == ACT_SWIGLU:
-        m, gi, ui = swiglu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
-                                tokens_per_expert, int(max_expert_width), x.shape[1],
-                                w1.shape[1])
-        h, g, _ = swiglu_fwd(x, w1, m, gi, ui, gather_map)
+        gmeta = glu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                         tokens_per_expert, int(max_expert_width), x.shape[1], w1.shape[1])
+        # pre_act is the gate, as the reference saves it (grouped_gemm.py:339-346)
+        h, g, _ = glu_fwd(x, w1, gmeta.fwd, True, save_pre_act, False, gather_map)
         return (h, g) if save_pre_act else h
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1])
@@ -538,15 +570,11 @@ def grouped_gemm_up_backward(grad_output, x, w1, pre_act, expert_token_offsets,
         # pre_act holds the gate; the up half is recomputed from x (the
         # reference keeps only the gate and leaves this backward unfinished,
         # grouped_gemm.py:768-790).
-        m, gi, ui = swiglu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
-                                tokens_per_expert, grad_output.shape[1], int(hidden_size),
-                                w1.shape[1])
-        w1b = _bf16(w1, "grouped_gemm_up_backward w1")
-        up, _ = up_fwd(x, w1b.index_select(1, ui), m, _lib.ACT_NONE, False, zero_tails=True,
-                       gather_map=gather_map)
+        gmeta = glu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                         tokens_per_expert, grad_output.shape[1], int(hidden_size), w1.shape[1])
+        _, _, up = glu_fwd(x, w1, gmeta.fwd, False, False, True, gather_map)
         gate = _bf16(pre_act, "grouped_gemm_up_backward pre_act")
-        return swiglu_bwd(grad_output, x, w1b, gate, up, m, gi, ui, int(hidden_size),
-                          gather_map)
+        return glu_bwd(grad_output, x, w1, gate, up, gmeta, int(hidden_size), gather_map)
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, grad_output.shape[1], int(hidden_size), None,
                   w1.shape[1])
@@ -584,13 +612,11 @@ class GroupedGemmUp(torch.autograd.Function):
         ctx.use_gather_map = use_gm
         xs = (x_flat.to(w1.dtype), w1) if use_gm else (x, w1)
         if act == ACT_SWIGLU:
-            m, gi, ui = swiglu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
-                                    tokens_per_expert, int(max_expert_width), x.shape[1],
-                                    w1.shape[1])
-            out, gate, up = swiglu_fwd(x, w1, m, gi, ui)
-            ctx.swiglu = (gi, ui)
+            gmeta = glu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
+                             tokens_per_expert, int(max_expert_width), x.shape[1], w1.shape[1])
+            out, gate, up = glu_fwd(x, w1, gmeta.fwd, True, True, True)
             ctx.save_for_backward(*xs, gate, up, *((gather_map,) if use_gm else ()))
-            ctx.meta = m
+            ctx.meta = gmeta
             ctx.hidden_size = hidden_size
             ctx.act = act
             return out
@@ -611,8 +637,8 @@ class GroupedGemmUp(torch.autograd.Function):
             saved = ctx.saved_tensors
             x_for_dw, w1, gate, up = saved[:4]
             gm = saved[4] if ctx.use_gather_map else None
-            grad_x, grad_w1 = swiglu_bwd(grad_output, x_for_dw, w1, gate, up, ctx.meta,
-                                         *ctx.swiglu, int(ctx.hidden_size), gm)
+            grad_x, grad_w1 = glu_bwd(grad_output, x_for_dw, w1, gate, up, ctx.meta,
+                                      int(ctx.hidden_size), gm)
             return grad_x, grad_w1, None, None, None, None, None, None, None, None, None
         if ctx.use_gather_map:
             x_for_dw, w1, pre, gm = ctx.saved_tensors
