@@ -388,8 +388,20 @@ __global__ __launch_bounds__(kRouteThreads) void route_fused_kernel(
   for (int e = tid / G; e < E; e += kRouteThreads / G) {
     const int32_t* c = ws.counts + (int64_t)e * ncols;
     int32_t tot = 0, pre = 0;
+    int t = j;
+    // 16 loads in flight per round (one round at cfg3's 256 columns)
+    for (; t + 15 * G < ncols; t += 16 * G) {
+      int32_t v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = c[t + u * G];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        tot += v[u];
+        pre += t + u * G < bcol ? v[u] : 0;
+      }
+    }
 #pragma unroll 8
-    for (int t = j; t < ncols; t += G) {
+    for (; t < ncols; t += G) {
       const int32_t v = c[t];
       tot += v;
       pre += t < bcol ? v : 0;
