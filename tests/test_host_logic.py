@@ -125,3 +125,28 @@ def test_rows_upper_bound_holds(mode):
         sel = rng.integers(0, E, A)
         r = oroute.route(sel, E, b, mode)
         assert int(r["padded_bins"][-1]) <= rows_upper_bound(A, E, b, mode)
+
+
+def test_glu_meta_layouts():
+    """swiglu metadata: the forward keeps the caller's gate offsets and widths;
+    the backward GEMMs get widths 2 w_e over W1's own column ranges when they
+    are contiguous (2 w_e apart), else over a gathered contiguous copy whose
+    column index lists every expert's gate and up columns in order."""
+    from triton_moe.kernels.grouped_gemm import glu_meta
+
+    t = lambda v: torch.tensor(v, dtype=torch.int32)  # noqa: E731
+    eto, tpe, widths = t([0, 64, 64, 192]), t([64, 0, 128]), t([16, 8, 16])
+    m = glu_meta(eto, t([0, 32, 48, 80]), widths, tpe, 16, 64, 80)
+    assert m.cols is None
+    assert m.fwd.ewo.tolist() == [0, 32, 48, 80] and m.fwd.widths.tolist() == [16, 8, 16]
+    assert m.bwd.widths.tolist() == [32, 16, 32] and m.bwd.max_width == 32
+    assert m.bwd.ewo.tolist() == [0, 32, 48, 80] and m.bwd.full_cols
+    # gaps of 8 columns between the experts' ranges
+    m = glu_meta(eto, t([0, 40, 64, 104]), widths, tpe, 16, 64, 104)
+    assert m.bwd.ewo.tolist() == [0, 32, 48, 80]
+    want = list(range(0, 32)) + list(range(40, 56)) + list(range(64, 96))
+    assert m.cols.tolist() == want
+    with pytest.raises(ValueError, match="exceed"):
+        glu_meta(eto, t([0, 32, 48, 80]), widths, tpe, 16, 64, 72)
+    with pytest.raises(NotImplementedError, match="multiples of 8"):
+        glu_meta(eto, t([0, 36, 52, 84]), widths, tpe, 16, 64, 96)
