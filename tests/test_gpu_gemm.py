@@ -670,3 +670,42 @@ def test_swiglu_rounding_order(gapped, public_backward, device):
         for e, o in enumerate(offs[:-1]):
             used[o:o + 2 * c["widths"][e]] = True
         assert int(gw1.cpu()[:, ~used].abs().sum()) == 0, "columns outside the experts"
+
+
+def test_glu_row_scale_and_gather_map_capi(device):
+    """vmoe_gemm_up_glu through the C ABI with a gather map and row factors:
+    out = bf16(row_scale * silu(g) u), gate = bf16(g), up = bf16(u) from the
+    fp32 accumulators of x[map[row]] (pad rows, map -1, read zeros)."""
+    from triton_moe import _lib
+    from triton_moe.kernels.grouped_gemm import _meta_args, glu_meta
+
+    c = _swiglu_case(seed=61, skew=True)
+    eto, _, wid, tpe = _meta_dev(c, device)
+    ewo = torch.tensor(c["offs2"], dtype=torch.int32, device=device)
+    T = 300
+    g = torch.Generator().manual_seed(62)
+    x_flat = torch.randn(T, c["d"], generator=g).to(torch.bfloat16)
+    gm = torch.randint(-1, T, (c["P"],), dtype=torch.int32, generator=g)
+    rs = torch.rand(c["P"], generator=g)
+    m = glu_meta(eto, ewo, wid, tpe, c["max_w"], c["d"], c["w1s"].shape[1]).fwd
+    P, mw = c["P"], c["max_w"]
+    outs = [torch.zeros(P, mw, dtype=torch.bfloat16, device=device) for _ in range(3)]
+    # device copies held for the whole (asynchronous) launch
+    xd, w1d, gmd, rsd = (t.to(device) for t in (x_flat, c["w1s"], gm, rs))
+    _lib.call("vmoe_gemm_up_glu", xd.data_ptr(), xd.stride(0), T, gmd.data_ptr(),
+              w1d.data_ptr(), w1d.stride(0), *(o.data_ptr() for o in outs), mw,
+              rsd.data_ptr(), *_meta_args(m), c["d"], mw, P, _lib.stream(device))
+    torch.cuda.synchronize()
+    xs = torch.where((gm >= 0)[:, None], x_flat[gm.clamp(min=0).long()], torch.zeros(()))
+    h_ref, g_ref, u_ref = (torch.zeros(P, mw) for _ in range(3))
+    for e, (r0, r1) in enumerate(c["rows"]):
+        w, o = c["widths"][e], c["offs2"][e]
+        x32 = xs[r0:r1].float()
+        gg_ = x32 @ c["w1s"][:, o:o + w].float()
+        uu = x32 @ c["w1s"][:, o + w:o + 2 * w].float()
+        h_ref[r0:r1, :w] = bf(rs[r0:r1, None] * (gg_ * torch.sigmoid(gg_) * uu))
+        g_ref[r0:r1, :w] = bf(gg_)
+        u_ref[r0:r1, :w] = bf(uu)
+    assert_close_norm(outs[0], h_ref, TIGHT, "glu H with row factors")
+    assert_close_norm(outs[1], g_ref, TIGHT, "glu gate")
+    assert_close_norm(outs[2], u_ref, TIGHT, "glu up")
