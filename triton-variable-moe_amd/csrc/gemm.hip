@@ -473,26 +473,18 @@ struct Gemm {
   // is). Items then have an even number of k-steps (an odd one gets a k-step
   // of zeros), so pairs never straddle items. The ring is the A pair slots,
   // then kStages B stages; otherwise kStages stages of A then B.
-  // The dX GEMM pairs its B operand instead (W1 read K-contiguous, 16 KiB
-  // per stage, where its A pairs gained little); its A then stays on the
-  // plain ring and its epilogue scratch is halved to fit the LDS.
-  static constexpr bool PAIR_A = V == DOWN_FWD;
-  static constexpr bool PAIR_B = V == UP_DX;
-  static constexpr bool PAIRED = PAIR_A || PAIR_B;
+  static constexpr bool PAIR_A = V == DOWN_FWD || V == UP_DX;
   static constexpr int kPairSlots = 3;
-  static constexpr int A_RING = PAIR_A ? kPairSlots * 2 * A_STAGE : kStages * A_STAGE;
-  static constexpr int B_RING = PAIR_B ? kPairSlots * 2 * B_STAGE : kStages * B_STAGE;
-  static constexpr int RING = PAIRED ? A_RING + B_RING : kStages * STAGE;
+  static constexpr int A_RING = PAIR_A ? kPairSlots * 2 * A_STAGE : 0;
+  static constexpr int RING = PAIR_A ? A_RING + kStages * B_STAGE : kStages * STAGE;
   template <typename P>
   __device__ static P* a_at(P* ring, int s) {
-    return PAIR_A ? ring + ((s >> 1) % kPairSlots) * (2 * A_STAGE)
-           : PAIRED ? ring + (s % kStages) * A_STAGE : ring + (s % kStages) * STAGE;
+    return PAIR_A ? ring + ((s >> 1) % kPairSlots) * (2 * A_STAGE) : ring + (s % kStages) * STAGE;
   }
   template <typename P>
   __device__ static P* b_at(P* ring, int s) {
-    return PAIR_B ? ring + A_RING + ((s >> 1) % kPairSlots) * (2 * B_STAGE)
-           : PAIRED ? ring + A_RING + (s % kStages) * B_STAGE
-                    : ring + (s % kStages) * STAGE + A_STAGE;
+    return PAIR_A ? ring + A_RING + (s % kStages) * B_STAGE
+                  : ring + (s % kStages) * STAGE + A_STAGE;
   }
   // DMA instructions per producer wave per stage for an operand of R rows/cols.
   template <int R>
@@ -507,7 +499,6 @@ struct Gemm {
   static constexpr int PWA = Dma<BM>::PW, PWB = Dma<BN>::PW;
   static constexpr int PT = PWA + PWB;  // DMA instructions per stage per producer thread
   static constexpr int PWA_S = PAIR_A ? 2 * PWA : PWA;  // A DMAs per issue (a pair: two stages)
-  static constexpr int PWB_S = PAIR_B ? 2 * PWB : PWB;  // B DMAs per issue
   __device__ static int pwave() { return (threadIdx.x >> 6) - kConsumers; }
 
   // LDS address of this wave's first DMA slot of an operand stage, uniform:
@@ -966,7 +957,7 @@ struct Gemm {
     }
     w.klen = K - w.kbeg;
     w.nk = w.klen > 0 && !w.skip ? cdiv(w.klen, BK) : 0;
-    if (PAIRED) w.nk = (w.nk + 1) & ~1;  // pairs of k-steps
+    if (PAIR_A) w.nk = (w.nk + 1) & ~1;  // pairs of k-steps
     return w;
   }
 
@@ -984,7 +975,7 @@ struct Gemm {
     tm.on = true;
   }
 
-  __device__ static void setup(const Args& p, const Work& w, Src<PWA_S>& sa, Src<PWB_S>& sb,
+  __device__ static void setup(const Args& p, const Work& w, Src<PWA_S>& sa, Src<PWB>& sb,
                                TMap& tm) {
     const Prob& q = w.q;
     if constexpr (T::a_k)
@@ -993,18 +984,18 @@ struct Gemm {
     else
       setup_t<BM, PWA, T::t_map>(sa, tm, p.a, p.lda, p.a_map, p.a_rows, q.ar + w.kbeg,
                                  q.ac + w.m0, q.M - w.m0, w.klen, !T::t_map_b);
-    if constexpr (V == UP_GLU)
+    if (V == UP_GLU)
       setup_glu(sb, p.b, p.ldb, q.br + w.kbeg, q.bc + w.n0, q.N, q.N - w.n0);
-    else if constexpr (T::b_k)
-      setup_k<BN, PWB_S, PAIR_B>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg,
-                                 q.N - w.n0, nullptr);
+    else if (T::b_k)
+      setup_k<BN, PWB, false>(sb, p.b, p.ldb, nullptr, 0, q.br + w.n0, q.bc + w.kbeg, q.N - w.n0,
+                              nullptr);
     else
       setup_t<BN, PWB, T::t_map_b>(sb, tm, p.b, p.ldb, p.b_map, p.b_rows, q.br + w.kbeg,
                                    q.bc + w.n0, q.N - w.n0, w.klen, T::t_map_b);
   }
 
   // Issues k-step kt of item w as global stage s (A of a pair: on even kt).
-  __device__ static void issue(const Work& w, const Src<PWA_S>& sa, const Src<PWB_S>& sb,
+  __device__ static void issue(const Work& w, const Src<PWA_S>& sa, const Src<PWB>& sb,
                                TMap& tm, int kt, lds_char* ring, int s) {
     const int k0 = kt * BK;
     if constexpr (T::a_k) {
@@ -1012,11 +1003,8 @@ struct Gemm {
     } else {
       issue_t<BM, PWA, T::t_map>(sa, tm, kt, w.klen, a_at(ring, s));
     }
-    if constexpr (T::b_k) {
-      if (!PAIR_B || (kt & 1) == 0) issue_k<BN, PWB_S, PAIR_B>(sb, k0, w.klen, b_at(ring, s));
-    } else {
-      issue_t<BN, PWB, T::t_map_b>(sb, tm, kt, w.klen, b_at(ring, s));
-    }
+    if (T::b_k) issue_k<BN, PWB, false>(sb, k0, w.klen, b_at(ring, s));
+    else issue_t<BN, PWB, T::t_map_b>(sb, tm, kt, w.klen, b_at(ring, s));
   }
 
   // Multiplies one staged k-tile into the wave's accumulators.
@@ -1034,8 +1022,7 @@ struct Gemm {
                 : T::a_k ? frag_k(ca, wm * WM + i * 32, ks) : frag_t<BM>(ca, wm * WM + i * 32, ks);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = PAIR_B ? frag_kp(cb, s & 1, wn * WN + j * 32, ks)
-                 : T::b_k ? frag_k(cb, wn * WN + j * 32, ks) : frag_t<BN>(cb, wn * WN + j * 32, ks);
+        bfr[j] = T::b_k ? frag_k(cb, wn * WN + j * 32, ks) : frag_t<BN>(cb, wn * WN + j * 32, ks);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1067,10 +1054,7 @@ struct Gemm {
   // (r >> 1) swizzle conflicts 2-way there and takes twice the cycles), and
   // 16 rows with one half-chunk then fill the 32 banks exactly; a 16-lane
   // ds_read_b128 phase covers two whole rows over all 64 banks.
-  // The dX GEMM (B pairs) stages a block as two 16-row halves in half the
-  // scratch, which its LDS budget needs.
-  static constexpr int EPI_ROWS = PAIR_B ? 16 : 32;
-  static constexpr int EPI_BYTES = EPI_ROWS * 64 * 2;
+  static constexpr int EPI_BYTES = 32 * 64 * 2;
   static_assert(WN == 64 && FN == 2 && FM == 2, "epilogue assumes 64x64 wave tiles");
   // UP_FWD with relu^2 stores PRE and H; UP_GLU [gate | up] blocks and H
   // (the right half of its H blocks is unused); every other variant one
@@ -1093,19 +1077,16 @@ struct Gemm {
   // Packed block (out, i) into the wave's scratch: lane (r = lane & 31,
   // h = lane >> 5) holds for each (j, g) the 4 values at columns
   // 32j + 8g + 4h .. +3 of row r.
-  // HALF >= 0: only rows 16 HALF .. + 15, at scratch rows 0 .. 15.
-  template <int OUT, int I, int HALF = -1>
+  template <int OUT, int I>
   __device__ __forceinline__ static void epi_write(lds_char* scr, const Pending& pd, int lane) {
     const int r = lane & 31, h = lane >> 5;
-    if (HALF >= 0 && (r >> 4) != HALF) return;
-    const int rs = HALF >= 0 ? r & 15 : r;
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const u32x2_t v = {pd.pk[OUT][I][j][2 * g], pd.pk[OUT][I][j][2 * g + 1]};
         *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(
-            scr + epi_off(rs, 2 * (4 * j + g) + h)) = v;
+            scr + epi_off(r, 2 * (4 * j + g) + h)) = v;
       }
   }
 
@@ -1269,23 +1250,6 @@ struct Gemm {
     int lane = threadIdx.x & 63;
     asm volatile("" : "+v"(lane));
     const int mb = pd.mb + I * 32;
-    if constexpr (EPI_ROWS == 16) {
-      const int n = pd.nb + 8 * (lane & 7);
-      const bool n_ok = n < pd.N;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        if (hf == 0) epi_write<OUT, I, 0>(scr, pd, lane);
-        else epi_write<OUT, I, 1>(scr, pd, lane);
-#pragma unroll
-        for (int qq = 0; qq < 2; ++qq) {
-          const uint4 v = epi_read(scr, qq, lane);
-          const int m = mb + 16 * hf + 8 * qq + (lane >> 3);
-          if (m < pd.M && n_ok)
-            *reinterpret_cast<uint4*>(p.c + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n) = v;
-        }
-      }
-      return;
-    }
     epi_write<OUT, I>(scr, pd, lane);
     const int n = pd.nb + 8 * (lane & 7);
     const bool n_ok = n < pd.N;
@@ -1486,7 +1450,7 @@ struct Gemm {
     int ei = 0, ela = 0;
     Work wi;
     Src<PWA_S> sa;
-    Src<PWB_S> sb;
+    Src<PWB> sb;
     TMap tm;
     const bool mapped = ((T::t_map || T::k_map) && p.a_map) || (T::t_map_b && p.b_map);
     if (mapped) tm.mrs = make_rsrc(T::t_map_b ? p.b_map : p.a_map);
@@ -1586,25 +1550,17 @@ struct Gemm {
       // consumers then read stage s), and refill the buffer the consumers
       // read in the previous step, which every wave has left by now.
       // With A pairs an even stage issues 2 PWA + PWB DMAs and an odd one
-      // PWB (B pairs: PWA + 2 PWB and PWA), so two consecutive stages still
-      // issue 2 PT.
+      // PWB, so two consecutive stages still issue 2 PT.
       const int after = issued - 1 - s;
       if (after >= 2) {
         wait_vmcnt<2 * PT>();
       } else if (after == 1) {
-        if constexpr (PAIR_A) {
-          if ((s & 1) == 1)
-            wait_vmcnt<2 * PWA + PWB>();  // stage s + 1 is even
-          else
-            wait_vmcnt<PWB>();
-        } else if constexpr (PAIR_B) {
-          if ((s & 1) == 1)
-            wait_vmcnt<PWA + 2 * PWB>();
-          else
-            wait_vmcnt<PWA>();
-        } else {
+        if (!PAIR_A)
           wait_vmcnt<PT>();
-        }
+        else if ((s & 1) == 1)
+          wait_vmcnt<2 * PWA + PWB>();  // stage s + 1 is even
+        else
+          wait_vmcnt<PWB>();
       } else {
         wait_vmcnt<0>();
       }
