@@ -89,9 +89,10 @@ int vmoe_route(const void* selected_experts, int32_t selected_is_int64,
  * num_assignments / top_k, num_experts, top_k) bytes; same tokens, experts,
  * k and the selected ids that call wrote): the counting launch is skipped,
  * everything else, outputs and status codes included, is vmoe_route's
- * (VMOE_ERR_UNSUPPORTED where vmoe_router_topk_hist does not apply). The two launches of vmoe_route become one after the top-k
- * kernel. Same replacement as vmoe_route (fused_cumsum.py:85-171 with
- * grouped_gemm.py:104-149); the reference counts inside torch.bincount. */
+ * (VMOE_ERR_UNSUPPORTED where vmoe_router_topk_hist does not apply): after
+ * the top-k kernel, routing is one launch instead of two. Same replacement
+ * as vmoe_route (fused_cumsum.py:85-171 with grouped_gemm.py:104-149); the
+ * reference counts inside torch.bincount. */
 int vmoe_route_counted(const void* selected_experts, int32_t selected_is_int64,
                        int64_t num_assignments, int32_t num_experts, int32_t top_k,
                        int32_t block_size, int32_t rounding, int32_t* bin_ids, int32_t* indices,
