@@ -1307,12 +1307,25 @@ struct Gemm {
       return;
     }
     uint16_t* out = (NOUT == 2 && OUT == 0) ? p.c2 : p.c;
+    // The [rows, d] outputs of DOWN_FWD and UP_DX (268 MB at cfg3), which
+    // only the combine reads (itself with non-temporal loads), are stored
+    // non-temporally so they do not evict the operands these GEMMs re-read
+    // (cfg3: dX 135 -> 122 us, down fwd 128 -> 121 us; the combines read
+    // them 7 us slower each, the step is ~1 % shorter); the other outputs
+    // are read right after by the next GEMM.
+    constexpr bool kStream = V == DOWN_FWD || V == UP_DX;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const uint4 v = epi_read(scr, qq, lane);
       const int m = mb + 8 * qq + (lane >> 3);
-      if (m < pd.M && n_ok)
-        *reinterpret_cast<uint4*>(out + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n) = v;
+      if (m < pd.M && n_ok) {
+        u32x4_t* dst = reinterpret_cast<u32x4_t*>(out + ((int64_t)pd.cr + m) * p.ldc + pd.cc + n);
+        const u32x4_t val = {v.x, v.y, v.z, v.w};
+        if (kStream)
+          __builtin_nontemporal_store(val, dst);
+        else
+          *dst = val;
+      }
     }
   }
 
