@@ -34,8 +34,10 @@ enum vmoe_status {
 /* Rounding modes of fused_route (triton_moe/kernels/fused_cumsum.py:126-128). */
 enum vmoe_rounding { VMOE_ROUND_UP = 0, VMOE_ROUND_DOWN = 1, VMOE_ROUND_NEAREST = 2 };
 
-/* Activations of grouped_gemm_up (triton_moe/kernels/grouped_gemm.py:435). */
-enum vmoe_activation { VMOE_ACT_NONE = 0, VMOE_ACT_RELU_SQUARED = 1 };
+/* Activations of grouped_gemm_up (triton_moe/kernels/grouped_gemm.py:435).
+ * VMOE_ACT_SWIGLU is taken by the fp32 GEMMs only; the bf16 SwiGLU forward is
+ * vmoe_gemm_up_glu. */
+enum vmoe_activation { VMOE_ACT_NONE = 0, VMOE_ACT_RELU_SQUARED = 1, VMOE_ACT_SWIGLU = 2 };
 
 /* Bits of info[VMOE_INFO_ERRORS] written by vmoe_route. */
 enum vmoe_route_error { VMOE_ROUTE_BAD_EXPERT_ID = 1, VMOE_ROUTE_ROW_OVERFLOW = 2 };
@@ -451,6 +453,76 @@ int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint16_t* grad_y
 int vmoe_zero_tail_cols(uint16_t* buf, int64_t ld, const int32_t* eto, const int32_t* widths,
                         int32_t num_experts, int64_t max_width, int64_t rows_bound,
                         vmoe_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * fp32 grouped GEMMs: the float32 inputs of grouped_gemm_up / _down and their
+ * backward and autograd functions (the reference's kernels are dtype-generic:
+ * triton_moe/kernels/grouped_gemm.py:217-1162; its fp32 autograd tests:
+ * tests/test_grouped_gemm_backward.py:151-208). fp32 in, fp32 fma
+ * accumulation in k order, fp32 out. Metadata, rows_bound and the rows each
+ * expert covers are as for the bf16 GEMMs above; no alignment or multiple-of-8
+ * requirement. Only the rows and columns the experts cover are written: the
+ * caller zero-fills the rest (as the reference's torch.zeros outputs are).
+ * activation: VMOE_ACT_NONE, VMOE_ACT_RELU_SQUARED or VMOE_ACT_SWIGLU, whose
+ * gate columns of expert e are ewo[e] + [0, w_e) and its up columns
+ * ewo[e] + w_e + [0, w_e) (grouped_gemm.py:295-297).
+ * ---------------------------------------------------------------------- */
+
+/* out = act(x_e @ W1_e) [rows, ldo >= max_width] (grouped_gemm.py:217-368).
+ * relu^2: pre_act = relu(z) (optional), out = pre_act^2. SwiGLU: pre_act =
+ * the gate g, up = u, out = g * sigmoid(g) * u (each optional, out or one of
+ * the others required). x rows through gather_map when it is non-null (a map
+ * entry outside [0, x_rows) reads zeros). */
+int vmoe_gemm_f32_up_fwd(const float* x, int64_t ldx, int64_t x_rows, const int32_t* gather_map,
+                         const float* w1, int64_t ldw1, float* out, float* pre_act, float* up,
+                         int64_t ldo, int32_t activation, const int32_t* eto,
+                         const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
+                         int32_t num_experts, int64_t hidden, int64_t max_width,
+                         int64_t rows_bound, vmoe_stream_t stream);
+
+/* y = h_e @ W2_e [rows, hidden] (grouped_gemm.py:485-584). */
+int vmoe_gemm_f32_down_fwd(const float* h, int64_t ldh, const float* w2, int64_t ldw2, float* y,
+                           int64_t ldy, const int32_t* eto, const int32_t* ewo,
+                           const int32_t* widths, const int32_t* tpe, int32_t num_experts,
+                           int64_t hidden, int64_t max_width, int64_t rows_bound,
+                           vmoe_stream_t stream);
+
+/* grad_x [rows, hidden] = GA_e @ W1_e^T (grouped_gemm.py:659-807), GA the
+ * gradient w.r.t. the pre-activation formed from grad_h (the gradient of the
+ * activated output) as it is loaded: relu^2 GA = pre > 0 ? grad_h * 2 * pre :
+ * 0 (pre_act = relu(z)); SwiGLU [dG | dU] over the expert's 2 w_e columns
+ * from the gate (pre_act) and up; none GA = grad_h. grad_h, pre_act and up
+ * share the leading dimension ldg >= max_width. */
+int vmoe_gemm_f32_up_bwd_dx(const float* grad_h, const float* pre_act, const float* up,
+                            int64_t ldg, int32_t activation, const float* w1, int64_t ldw1,
+                            float* grad_x, int64_t ldgx, const int32_t* eto, const int32_t* ewo,
+                            const int32_t* widths, const int32_t* tpe, int32_t num_experts,
+                            int64_t hidden, int64_t max_width, int64_t rows_bound,
+                            vmoe_stream_t stream);
+
+/* grad_w1 = X_e^T @ GA_e into W1's layout (grouped_gemm.py:810-972), GA as
+ * for vmoe_gemm_f32_up_bwd_dx, X through gather_map when it is non-null. */
+int vmoe_gemm_f32_up_bwd_dw(const float* x, int64_t ldx, int64_t x_rows,
+                            const int32_t* gather_map, const float* grad_h, const float* pre_act,
+                            const float* up, int64_t ldg, int32_t activation, float* grad_w1,
+                            int64_t ldgw, const int32_t* eto, const int32_t* ewo,
+                            const int32_t* widths, const int32_t* tpe, int32_t num_experts,
+                            int64_t hidden, int64_t max_width, int64_t rows_bound,
+                            vmoe_stream_t stream);
+
+/* grad_h [rows, max_width] = grad_y_e @ W2_e^T (grouped_gemm.py:975-1068). */
+int vmoe_gemm_f32_down_bwd_dh(const float* grad_y, int64_t ldgy, const float* w2, int64_t ldw2,
+                              float* grad_h, int64_t ldgh, const int32_t* eto,
+                              const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
+                              int32_t num_experts, int64_t hidden, int64_t max_width,
+                              int64_t rows_bound, vmoe_stream_t stream);
+
+/* grad_w2 = H_e^T @ grad_y_e into W2's layout (grouped_gemm.py:1071-1162). */
+int vmoe_gemm_f32_down_bwd_dw(const float* h, int64_t ldh, const float* grad_y, int64_t ldgy,
+                              float* grad_w2, int64_t ldgw, const int32_t* eto,
+                              const int32_t* ewo, const int32_t* widths, const int32_t* tpe,
+                              int32_t num_experts, int64_t hidden, int64_t max_width,
+                              int64_t rows_bound, vmoe_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -25,7 +25,10 @@ def test_header_declares_expected_entry_points():
     for must in ("vmoe_route", "vmoe_row_maps", "vmoe_gather", "vmoe_combine",
                  "vmoe_gemm_up_fwd", "vmoe_gemm_down_fwd", "vmoe_gemm_up_bwd_dx",
                  "vmoe_gemm_up_bwd_dw", "vmoe_gemm_down_bwd_dh", "vmoe_gemm_down_bwd_dw",
-                 "vmoe_zero_tail_cols", "vmoe_status_string", "vmoe_gather_tokens"):
+                 "vmoe_zero_tail_cols", "vmoe_status_string", "vmoe_gather_tokens",
+                 "vmoe_gemm_f32_up_fwd", "vmoe_gemm_f32_down_fwd", "vmoe_gemm_f32_up_bwd_dx",
+                 "vmoe_gemm_f32_up_bwd_dw", "vmoe_gemm_f32_down_bwd_dh",
+                 "vmoe_gemm_f32_down_bwd_dw"):
         assert must in names
 
 
@@ -144,6 +147,27 @@ def test_argument_checks_return_invalid_arg():
     # a row-weight output without the weights it is read from
     assert lib.vmoe_route(1, 0, 4, 4, 1, 64, 0, 1, 1, 1, 1, 1, 1, 1, 0, 8, 1, 1, None, None,
                           None, 1, 1, 4096, None) == _lib.ERR_INVALID_ARG
+    # fp32 GEMMs: bad activation, missing pre/up for the activation's rule,
+    # leading dimensions below the row, no output at all
+    assert lib.vmoe_gemm_f32_up_fwd(1, 16, 4, None, 1, 16, 1, None, None, 16, 3, 1, 1, 1, 1, 2,
+                                    16, 16, 64, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gemm_f32_up_fwd(1, 8, 4, None, 1, 16, 1, None, None, 16, 1, 1, 1, 1, 1, 2,
+                                    16, 16, 64, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gemm_f32_up_fwd(1, 16, 4, None, 1, 16, None, None, None, 16, 1, 1, 1, 1, 1,
+                                    2, 16, 16, 64, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gemm_f32_up_bwd_dx(1, None, None, 16, 1, 1, 16, 1, 16, 1, 1, 1, 1, 2, 16,
+                                       16, 64, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gemm_f32_up_bwd_dw(1, 16, 4, None, 1, 1, None, 16, 2, 1, 16, 1, 1, 1, 1, 2,
+                                       16, 16, 64, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gemm_f32_down_fwd(1, 16, 1, 8, 1, 16, 1, 1, 1, 1, 2, 16, 16, 64,
+                                      None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gemm_f32_down_bwd_dh(1, 16, 1, 16, 1, 8, 1, 1, 1, 1, 2, 16, 16, 64,
+                                         None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gemm_f32_down_bwd_dw(1, 16, 1, 16, 1, 16, None, 1, 1, 1, 2, 16, 16, 64,
+                                         None) == _lib.ERR_INVALID_ARG
+    # no rows: nothing to launch
+    assert lib.vmoe_gemm_f32_down_fwd(1, 16, 1, 16, 1, 16, 1, 1, 1, 1, 2, 16, 16, 0,
+                                      None) == _lib.OK
 
 
 def test_check_maps_status_to_exceptions():

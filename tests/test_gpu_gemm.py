@@ -500,14 +500,17 @@ def test_reference_module_chain_autograd(activation, device):
     assert_close_norm(w1.grad, w164.grad, LOOSE, "chain swiglu grad_w1")
 
 
-def test_fp32_inputs_not_supported(device):
-    """The reference also accepts fp32 (tf32 tl.dot); here bf16 only, loudly."""
+def test_fp16_inputs_not_supported(device):
+    """bf16 and fp32 (tests/test_gpu_gemm_f32.py) are taken; fp16 is refused
+    loudly rather than cast."""
     eto = torch.tensor([0, 128, 256], dtype=torch.int32, device=device)
     wid = torch.tensor([128, 128], dtype=torch.int32, device=device)
-    x = torch.randn(256, 64, device=device)
-    w1 = torch.randn(64, 256, device=device)
+    x = torch.randn(256, 64, device=device).half()
+    w1 = torch.randn(64, 256, device=device).half()
     with pytest.raises(NotImplementedError, match="bfloat16"):
         grouped_gemm_up(x, w1, eto, eto, wid, wid, 128)
+    with pytest.raises(NotImplementedError, match="float32"):
+        grouped_gemm_up(x, w1.float(), eto, eto, wid, wid, 128)
 
 
 def _swiglu_case(seed=31, skew=False):

@@ -1,0 +1,436 @@
+// fp32 grouped GEMMs: the float32 inputs of the public grouped-GEMM API.
+//
+// The reference's grouped-GEMM kernels take fp32 as well as bf16 operands
+// (triton_moe/kernels/grouped_gemm.py:217-1162, dtype-generic tl.dot with an
+// fp32 accumulator); its autograd tests and forward/backward benchmark run
+// them in fp32 (tests/test_grouped_gemm_backward.py:151-208). The bf16 kernels
+// of gemm.hip stage bf16 tiles for MFMA and cannot take fp32, so this file
+// holds one LDS-tiled fp32 VALU kernel for all six forms (up forward with its
+// activation, down forward, and both backward GEMMs of each). Every product
+// is an fp32 fma in k order per output, outputs are stored in fp32, and the
+// activation gradients (relu^2, SwiGLU's [dG | dU]) are formed from
+// grad/pre/up as the operand tile is loaded, as the reference's backward
+// kernels do (grouped_gemm.py:751-764, 914-927), so no launch sits between
+// the GEMMs. This is the path for fp32 callers; the bf16 module path never
+// uses it.
+//
+// Tiles: 64 x 64 outputs per 256-thread workgroup, 4 x 4 per thread, k steps
+// of 16 staged in LDS. Workgroups stride over the experts' tiles in order,
+// read from the metadata on the device (no host sync).
+#include "vmoe_common.h"
+
+namespace vmoe {
+namespace {
+
+enum F32Form { F_UP_FWD, F_DOWN_FWD, F_UP_DX, F_UP_DW, F_DOWN_DH, F_DOWN_DW };
+
+constexpr int kT = 64;        // tile edge
+constexpr int kBK = 16;       // k per LDS stage
+constexpr int kThreads = 256;
+constexpr int kPad = kT + 4;  // LDS row length (floats)
+
+struct F32Args {
+  // token-row operand: x (up forms), h (down forms) or grad_y (dH)
+  const float* a;
+  int64_t lda, a_rows;
+  const int32_t* a_map;  // x rows through a gather map (up forms), may be null
+  // weights: w1 or w2 (forward, dX and dH), or grad_y (down dW)
+  const float* b;
+  int64_t ldb;
+  // gradient of the up projection's output with pre (relu(z) or the gate)
+  // and up (SwiGLU), all [rows, max_width] with leading dimension ldg
+  const float *g, *pre, *up;
+  int64_t ldg;
+  float *c, *c2, *c3;
+  int64_t ldc;
+  const int32_t *eto, *ewo, *widths, *tpe;
+  int E, act;
+  int64_t hidden, max_width, rows_bound;
+};
+
+struct F32Prob {
+  int64_t M, N, K, t0, w0, w;
+};
+
+__device__ __forceinline__ int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Rows of expert e: [t0, t0 + rows), rows = min(tpe, eto[e+1] - eto[e]) and
+// inside [0, rows_bound).
+template <int F>
+__device__ F32Prob f32_prob(const F32Args& p, int e) {
+  F32Prob q;
+  const int64_t t0 = p.eto[e];
+  const int64_t t1 = min((int64_t)p.eto[e + 1], p.rows_bound);
+  int64_t rows = min((int64_t)p.tpe[e], t1 - t0);
+  if (t0 < 0 || rows < 0) rows = 0;
+  const int64_t w = max((int64_t)0, min((int64_t)p.widths[e], p.max_width));
+  // the SwiGLU backward GEMMs run over the expert's gate and up columns
+  const int64_t wg = p.act == VMOE_ACT_SWIGLU ? 2 * w : w;
+  q.t0 = t0;
+  q.w0 = p.ewo[e];
+  q.w = w;
+  switch (F) {
+    case F_UP_FWD: q.M = rows; q.N = w; q.K = p.hidden; break;
+    case F_DOWN_FWD: q.M = rows; q.N = p.hidden; q.K = w; break;
+    case F_UP_DX: q.M = rows; q.N = p.hidden; q.K = wg; break;
+    case F_UP_DW: q.M = p.hidden; q.N = wg; q.K = rows; break;
+    case F_DOWN_DH: q.M = rows; q.N = w; q.K = p.hidden; break;
+    default: q.M = w; q.N = p.hidden; q.K = rows; break;  // F_DOWN_DW
+  }
+  return q;
+}
+
+__device__ __forceinline__ float sigmoid32(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+// The gradient w.r.t. the up projection's pre-activation at row r, column c
+// (c < 2w for SwiGLU: c < w is the gate's, c >= w the up half's).
+__device__ __forceinline__ float act_grad(const F32Args& p, int64_t r, int64_t c, int64_t w) {
+  if (p.act == VMOE_ACT_SWIGLU) {
+    const int64_t cc = c < w ? c : c - w;
+    const int64_t o = r * p.ldg + cc;
+    const float gr = p.g[o], gate = p.pre[o], s = sigmoid32(gate);
+    return c < w ? gr * p.up[o] * s * (1.0f + gate * (1.0f - s)) : gr * gate * s;
+  }
+  const int64_t o = r * p.ldg + c;
+  const float gr = p.g[o];
+  if (p.act == VMOE_ACT_RELU_SQUARED) {
+    const float pr = p.pre[o];
+    return pr > 0.0f ? gr * 2.0f * pr : 0.0f;
+  }
+  return gr;
+}
+
+// x row of padded row r (through the gather map when there is one; a map
+// entry outside [0, a_rows) reads zeros).
+__device__ __forceinline__ const float* token_row(const F32Args& p, int64_t r) {
+  if (!p.a_map) return p.a + r * p.lda;
+  const int64_t s = p.a_map[r];
+  return s >= 0 && s < p.a_rows ? p.a + s * p.lda : nullptr;
+}
+
+// A(m, k) of the tile's problem (0 outside M x K).
+template <int F>
+__device__ __forceinline__ float f32_a(const F32Args& p, const F32Prob& q, int64_t m, int64_t k) {
+  if (m >= q.M || k >= q.K) return 0.0f;
+  switch (F) {
+    case F_UP_FWD: {
+      const float* row = token_row(p, q.t0 + m);
+      return row ? row[k] : 0.0f;
+    }
+    case F_DOWN_FWD:
+    case F_DOWN_DH: return p.a[(q.t0 + m) * p.lda + k];
+    case F_UP_DX: return act_grad(p, q.t0 + m, k, q.w);
+    case F_UP_DW: {
+      const float* row = token_row(p, q.t0 + k);
+      return row ? row[m] : 0.0f;
+    }
+    default: return p.a[(q.t0 + k) * p.lda + m];  // F_DOWN_DW: h^T
+  }
+}
+
+// B(k, n); `second` selects the SwiGLU up half of W1 in the up forward.
+template <int F>
+__device__ __forceinline__ float f32_b(const F32Args& p, const F32Prob& q, int64_t k, int64_t n,
+                                       bool second) {
+  if (k >= q.K || n >= q.N) return 0.0f;
+  switch (F) {
+    case F_UP_FWD: return p.b[k * p.ldb + q.w0 + (second ? q.w : 0) + n];
+    case F_DOWN_FWD: return p.b[(q.w0 + k) * p.ldb + n];
+    case F_UP_DX: return p.b[n * p.ldb + q.w0 + k];  // W1^T
+    case F_UP_DW: return act_grad(p, q.t0 + k, n, q.w);
+    case F_DOWN_DH: return p.b[(q.w0 + n) * p.ldb + k];  // W2^T
+    default: return p.b[(q.t0 + k) * p.ldb + n];  // F_DOWN_DW: grad_y
+  }
+}
+
+// Whether A / B are contiguous along k (decides which thread loads what).
+template <int F>
+constexpr bool a_k_contig() { return F == F_UP_FWD || F == F_DOWN_FWD || F == F_UP_DX || F == F_DOWN_DH; }
+template <int F>
+constexpr bool b_k_contig() { return F == F_UP_DX || F == F_DOWN_DH; }
+
+// Loads a kBK x kT stage into lds[k][i]: 4 elements per thread, consecutive
+// threads along the operand's contiguous dimension.
+template <bool KCONTIG, typename Fn>
+__device__ __forceinline__ void stage(float (*lds)[kPad], Fn&& at) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int k, x;
+    if (KCONTIG) {
+      k = tid & (kBK - 1);
+      x = (tid >> 4) + 16 * i;
+    } else {
+      x = tid & (kT - 1);
+      k = (tid >> 6) + 4 * i;
+    }
+    lds[k][x] = at(k, x);
+  }
+}
+
+template <int F>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_f32_kernel(F32Args p) {
+  __shared__ float As[kBK][kPad];
+  __shared__ float Bs[kBK][kPad];
+  __shared__ float Us[kBK][kPad];  // SwiGLU up half (up forward only)
+  const bool glu = F == F_UP_FWD && p.act == VMOE_ACT_SWIGLU;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  int e = 0;
+  int64_t before = 0;  // tiles of experts < e
+  F32Prob q{};
+  int64_t tiles = 0, tn_count = 1;
+  bool have = false;
+  for (int64_t t = blockIdx.x;; t += gridDim.x) {
+    // experts are visited in order and t only grows, so one pass over them
+    while (true) {
+      if (!have) {
+        if (e >= p.E) break;
+        q = f32_prob<F>(p, e);
+        tn_count = cdiv64(q.N, kT);
+        tiles = cdiv64(q.M, kT) * tn_count;
+        have = true;
+      }
+      if (t < before + tiles) break;
+      before += tiles;
+      ++e;
+      have = false;
+    }
+    if (!have) break;
+    const int64_t local = t - before;
+    const int64_t m0 = (local / tn_count) * kT, n0 = (local % tn_count) * kT;
+    float acc[4][4] = {}, acc_up[4][4] = {};
+    for (int64_t k0 = 0; k0 < q.K; k0 += kBK) {
+      stage<a_k_contig<F>()>(As, [&](int k, int x) { return f32_a<F>(p, q, m0 + x, k0 + k); });
+      stage<b_k_contig<F>()>(Bs, [&](int k, int x) { return f32_b<F>(p, q, k0 + k, n0 + x, false); });
+      if (glu)
+        stage<false>(Us, [&](int k, int x) { return f32_b<F>(p, q, k0 + k, n0 + x, true); });
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < kBK; ++k) {
+        float a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = As[k][ty + 16 * i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = Bs[k][tx + 16 * j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        if (glu) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) b[j] = Us[k][tx + 16 * j];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc_up[i][j] = fmaf(a[i], b[j], acc_up[i][j]);
+        }
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t m = m0 + ty + 16 * i;
+      if (m >= q.M) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t n = n0 + tx + 16 * j;
+        if (n >= q.N) continue;
+        const float z = acc[i][j];
+        if (F == F_UP_DW) {
+          p.c[m * p.ldc + q.w0 + n] = z;
+        } else if (F == F_DOWN_DW) {
+          p.c[(q.w0 + m) * p.ldc + n] = z;
+        } else {
+          const int64_t o = (q.t0 + m) * p.ldc + n;
+          if (F == F_UP_FWD && p.act == VMOE_ACT_RELU_SQUARED) {
+            const float r = fmaxf(z, 0.0f);
+            if (p.c2) p.c2[o] = r;
+            p.c[o] = r * r;
+          } else if (F == F_UP_FWD && glu) {
+            const float u = acc_up[i][j];
+            if (p.c2) p.c2[o] = z;
+            if (p.c3) p.c3[o] = u;
+            if (p.c) p.c[o] = z * sigmoid32(z) * u;
+          } else {
+            p.c[o] = z;
+          }
+        }
+      }
+    }
+  }
+}
+
+// Upper bound of the tiles of one launch (sizes the grid; workgroups past
+// the real count leave at once).
+int64_t tile_bound(int64_t E, int64_t m_bound, int64_t n_bound, bool rows_m) {
+  const int64_t tn = (n_bound + kT - 1) / kT;
+  const int64_t tm = rows_m ? (m_bound + kT - 1) / kT + E : E * ((m_bound + kT - 1) / kT);
+  return tm * tn;
+}
+
+template <int F>
+int f32_launch(const F32Args& p, int64_t bound, hipStream_t s) {
+  if (bound <= 0 || p.rows_bound == 0 || p.max_width == 0) return VMOE_OK;  // no work
+  const int64_t grid = bound < 2048 ? bound : 2048;
+  hipLaunchKernelGGL(grouped_gemm_f32_kernel<F>, dim3((unsigned)grid), dim3(kThreads), 0, s, p);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+int f32_common(const int32_t* eto, const int32_t* ewo, const int32_t* widths,
+               const int32_t* tpe, int32_t E, int64_t hidden, int64_t max_width,
+               int64_t rows_bound) {
+  if (!eto || !ewo || !widths || !tpe || E <= 0 || hidden <= 0 || max_width < 0 ||
+      rows_bound < 0)
+    return VMOE_ERR_INVALID_ARG;
+  return VMOE_OK;
+}
+
+F32Args f32_args(const int32_t* eto, const int32_t* ewo, const int32_t* widths,
+                 const int32_t* tpe, int32_t E, int64_t hidden, int64_t max_width,
+                 int64_t rows_bound, int act) {
+  F32Args p{};
+  p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
+  p.E = E; p.act = act; p.hidden = hidden; p.max_width = max_width; p.rows_bound = rows_bound;
+  return p;
+}
+
+bool act_ok(int act) {
+  return act == VMOE_ACT_NONE || act == VMOE_ACT_RELU_SQUARED || act == VMOE_ACT_SWIGLU;
+}
+
+// grad/pre/up of the backward GEMMs: pre is needed for relu^2, pre and up
+// for SwiGLU.
+bool grad_ok(const float* g, const float* pre, const float* up, int64_t ldg, int64_t max_width,
+             int act) {
+  if (!g || ldg < max_width || ldg <= 0) return false;
+  if (act == VMOE_ACT_RELU_SQUARED && !pre) return false;
+  if (act == VMOE_ACT_SWIGLU && (!pre || !up)) return false;
+  return true;
+}
+
+}  // namespace
+}  // namespace vmoe
+
+using namespace vmoe;
+
+extern "C" int vmoe_gemm_f32_up_fwd(const float* x, int64_t ldx, int64_t x_rows,
+                                    const int32_t* gather_map, const float* w1, int64_t ldw1,
+                                    float* out, float* pre_act, float* up, int64_t ldo,
+                                    int32_t activation, const int32_t* eto, const int32_t* ewo,
+                                    const int32_t* widths, const int32_t* tpe, int32_t E,
+                                    int64_t hidden, int64_t max_width, int64_t rows_bound,
+                                    vmoe_stream_t stream) {
+  int st = f32_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
+  if (st) return st;
+  if (!act_ok(activation) || !x || !w1 || x_rows < 0 || ldx < hidden || ldw1 <= 0 ||
+      ldo < max_width || ldo <= 0)
+    return VMOE_ERR_INVALID_ARG;
+  if (!out && !(activation == VMOE_ACT_SWIGLU && (pre_act || up))) return VMOE_ERR_INVALID_ARG;
+  F32Args p = f32_args(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound, activation);
+  p.a = x; p.lda = ldx; p.a_rows = x_rows; p.a_map = gather_map;
+  p.b = w1; p.ldb = ldw1;
+  p.c = out; p.ldc = ldo;
+  p.c2 = activation == VMOE_ACT_NONE ? nullptr : pre_act;
+  p.c3 = activation == VMOE_ACT_SWIGLU ? up : nullptr;
+  return f32_launch<F_UP_FWD>(p, tile_bound(E, rows_bound, max_width, true),
+                              reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int vmoe_gemm_f32_down_fwd(const float* h, int64_t ldh, const float* w2, int64_t ldw2,
+                                      float* y, int64_t ldy, const int32_t* eto,
+                                      const int32_t* ewo, const int32_t* widths,
+                                      const int32_t* tpe, int32_t E, int64_t hidden,
+                                      int64_t max_width, int64_t rows_bound,
+                                      vmoe_stream_t stream) {
+  int st = f32_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
+  if (st) return st;
+  if (!h || !w2 || !y || ldh < max_width || ldh <= 0 || ldw2 < hidden || ldy < hidden)
+    return VMOE_ERR_INVALID_ARG;
+  F32Args p = f32_args(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound, VMOE_ACT_NONE);
+  p.a = h; p.lda = ldh;
+  p.b = w2; p.ldb = ldw2;
+  p.c = y; p.ldc = ldy;
+  return f32_launch<F_DOWN_FWD>(p, tile_bound(E, rows_bound, hidden, true),
+                                reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int vmoe_gemm_f32_up_bwd_dx(const float* grad_h, const float* pre_act,
+                                       const float* up, int64_t ldg, int32_t activation,
+                                       const float* w1, int64_t ldw1, float* grad_x,
+                                       int64_t ldgx, const int32_t* eto, const int32_t* ewo,
+                                       const int32_t* widths, const int32_t* tpe, int32_t E,
+                                       int64_t hidden, int64_t max_width, int64_t rows_bound,
+                                       vmoe_stream_t stream) {
+  int st = f32_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
+  if (st) return st;
+  if (!act_ok(activation) || !grad_ok(grad_h, pre_act, up, ldg, max_width, activation) || !w1 ||
+      ldw1 <= 0 || !grad_x || ldgx < hidden)
+    return VMOE_ERR_INVALID_ARG;
+  F32Args p = f32_args(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound, activation);
+  p.g = grad_h; p.pre = pre_act; p.up = up; p.ldg = ldg;
+  p.b = w1; p.ldb = ldw1;
+  p.c = grad_x; p.ldc = ldgx;
+  return f32_launch<F_UP_DX>(p, tile_bound(E, rows_bound, hidden, true),
+                             reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int vmoe_gemm_f32_up_bwd_dw(const float* x, int64_t ldx, int64_t x_rows,
+                                       const int32_t* gather_map, const float* grad_h,
+                                       const float* pre_act, const float* up, int64_t ldg,
+                                       int32_t activation, float* grad_w1, int64_t ldgw,
+                                       const int32_t* eto, const int32_t* ewo,
+                                       const int32_t* widths, const int32_t* tpe, int32_t E,
+                                       int64_t hidden, int64_t max_width, int64_t rows_bound,
+                                       vmoe_stream_t stream) {
+  int st = f32_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
+  if (st) return st;
+  if (!act_ok(activation) || !grad_ok(grad_h, pre_act, up, ldg, max_width, activation) || !x ||
+      x_rows < 0 || ldx < hidden || !grad_w1 || ldgw <= 0)
+    return VMOE_ERR_INVALID_ARG;
+  F32Args p = f32_args(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound, activation);
+  p.a = x; p.lda = ldx; p.a_rows = x_rows; p.a_map = gather_map;
+  p.g = grad_h; p.pre = pre_act; p.up = up; p.ldg = ldg;
+  p.c = grad_w1; p.ldc = ldgw;
+  const int64_t n_bound = activation == VMOE_ACT_SWIGLU ? 2 * max_width : max_width;
+  return f32_launch<F_UP_DW>(p, tile_bound(E, hidden, n_bound, false),
+                             reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int vmoe_gemm_f32_down_bwd_dh(const float* grad_y, int64_t ldgy, const float* w2,
+                                         int64_t ldw2, float* grad_h, int64_t ldgh,
+                                         const int32_t* eto, const int32_t* ewo,
+                                         const int32_t* widths, const int32_t* tpe, int32_t E,
+                                         int64_t hidden, int64_t max_width, int64_t rows_bound,
+                                         vmoe_stream_t stream) {
+  int st = f32_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
+  if (st) return st;
+  if (!grad_y || ldgy < hidden || !w2 || ldw2 < hidden || !grad_h || ldgh < max_width ||
+      ldgh <= 0)
+    return VMOE_ERR_INVALID_ARG;
+  F32Args p = f32_args(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound, VMOE_ACT_NONE);
+  p.a = grad_y; p.lda = ldgy;
+  p.b = w2; p.ldb = ldw2;
+  p.c = grad_h; p.ldc = ldgh;
+  return f32_launch<F_DOWN_DH>(p, tile_bound(E, rows_bound, max_width, true),
+                               reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int vmoe_gemm_f32_down_bwd_dw(const float* h, int64_t ldh, const float* grad_y,
+                                         int64_t ldgy, float* grad_w2, int64_t ldgw,
+                                         const int32_t* eto, const int32_t* ewo,
+                                         const int32_t* widths, const int32_t* tpe, int32_t E,
+                                         int64_t hidden, int64_t max_width, int64_t rows_bound,
+                                         vmoe_stream_t stream) {
+  int st = f32_common(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound);
+  if (st) return st;
+  if (!h || ldh < max_width || ldh <= 0 || !grad_y || ldgy < hidden || !grad_w2 ||
+      ldgw < hidden)
+    return VMOE_ERR_INVALID_ARG;
+  F32Args p = f32_args(eto, ewo, widths, tpe, E, hidden, max_width, rows_bound, VMOE_ACT_NONE);
+  p.a = h; p.lda = ldh;
+  p.b = grad_y; p.ldb = ldgy;
+  p.c = grad_w2; p.ldc = ldgw;
+  return f32_launch<F_DOWN_DW>(p, tile_bound(E, max_width, hidden, false),
+                               reinterpret_cast<hipStream_t>(stream));
+}

@@ -59,6 +59,18 @@ _SIGNATURES = {
     "vmoe_gemm_down_bwd_dw": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
                               _vp, _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
     "vmoe_zero_tail_cols": [_vp, _i64, _vp, _vp, _i32, _i64, _i64, _vp],
+    "vmoe_gemm_f32_up_fwd": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _vp,
+                             _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "vmoe_gemm_f32_down_fwd": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
+                               _i64, _i64, _vp],
+    "vmoe_gemm_f32_up_bwd_dx": [_vp, _vp, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
+                                _vp, _i32, _i64, _i64, _i64, _vp],
+    "vmoe_gemm_f32_up_bwd_dw": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _i64, _vp,
+                                _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "vmoe_gemm_f32_down_bwd_dh": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32,
+                                  _i64, _i64, _i64, _vp],
+    "vmoe_gemm_f32_down_bwd_dw": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32,
+                                  _i64, _i64, _i64, _vp],
     "vmoe_router_logits": [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp],
     "vmoe_router_partial_floats": [_i64, _i32],
     "vmoe_router_topk": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -84,7 +96,7 @@ _RESTYPES = {
 # Status codes (include/vmoe.h).
 OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_WORKSPACE = 0, 1, 2, 3, 4
 ROUNDING = {"up": 0, "down": 1, "nearest": 2}
-ACT_NONE, ACT_RELU_SQUARED = 0, 1
+ACT_NONE, ACT_RELU_SQUARED, ACT_SWIGLU = 0, 1, 2
 INFO_ROWS, INFO_KEPT, INFO_ERRORS, INFO_LEN = 0, 1, 2, 4
 ROUTE_BAD_EXPERT_ID, ROUTE_ROW_OVERFLOW = 1, 2
 

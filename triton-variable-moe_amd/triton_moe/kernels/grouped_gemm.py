@@ -32,7 +32,7 @@ from .gather import row_maps
 _ACTIVATIONS = {"none": _lib.ACT_NONE, "relu_squared": _lib.ACT_RELU_SQUARED}
 
 
-ACT_SWIGLU = 2  # host-side code of activation="swiglu" (vmoe_gemm_up_glu)
+ACT_SWIGLU = _lib.ACT_SWIGLU  # activation="swiglu" (vmoe_gemm_up_glu; fp32: VMOE_ACT_SWIGLU)
 
 
 def _activation_code(activation: str) -> int:
@@ -397,6 +397,135 @@ def down_bwd(grad_y, h, w2, m: GemmMeta, hidden: int, zero_tails: bool,
 
 
 # ---------------------------------------------------------------------------
+# fp32 path: float32 weights (the reference's kernels are dtype-generic and
+# its autograd tests run fp32, tests/test_grouped_gemm_backward.py:151-208).
+# One fp32 VALU kernel per GEMM form (csrc/gemm_f32.hip); outputs are fp32
+# and zero outside the rows and columns the experts cover.
+# ---------------------------------------------------------------------------
+
+
+def _is_f32(w: torch.Tensor) -> bool:
+    return w.dtype == torch.float32
+
+
+def _f32(t: torch.Tensor, what: str) -> torch.Tensor:
+    """A float32 operand with unit column stride (bf16 inputs are widened,
+    as the reference's autograd casts x to the weights' dtype)."""
+    if t.dtype == torch.bfloat16:
+        t = t.float()
+    if t.dtype != torch.float32:
+        raise NotImplementedError(f"{what}: expected float32 with float32 weights (got {t.dtype})")
+    ok = t.dim() == 2 and t.stride(-1) == 1 and t.stride(0) >= max(t.shape[1], 1)
+    return t if ok else t.contiguous()
+
+
+def _f32_zeros(rows, cols, device):
+    return torch.zeros(rows, cols, dtype=torch.float32, device=device)
+
+
+def f32_up_fwd(x, w1, m: GemmMeta, act: int, gather_map=None, want_out=True, want_pre=False,
+               want_up=False):
+    """(out, pre, up) of the up projection in fp32: relu^2 pre = relu(z);
+    SwiGLU (m = GluMeta.fwd) pre = gate, up = u; tensors not asked for are None."""
+    x = _f32(x, "grouped_gemm_up x")
+    w1 = _f32(w1, "grouped_gemm_up w1")
+    hidden = x.shape[1]
+    _need(w1.shape[0] == hidden, "w1 rows must equal the hidden size of x")
+    if gather_map is None:
+        _need(x.shape[0] >= m.rows, "x has fewer rows than expert_token_offsets[-1]")
+    else:
+        _need(gather_map.numel() >= m.rows, "gather_map shorter than the padded row count")
+    dev = x.device
+    out = _f32_zeros(m.rows, m.max_width, dev) if want_out else None
+    pre = _f32_zeros(m.rows, m.max_width, dev) if want_pre else None
+    up = _f32_zeros(m.rows, m.max_width, dev) if want_up and act == ACT_SWIGLU else None
+    gm = None if gather_map is None else _i32(gather_map)
+    if m.rows > 0:
+        _lib.call("vmoe_gemm_f32_up_fwd", x.data_ptr(), x.stride(0), x.shape[0], _lib.ptr(gm),
+                  w1.data_ptr(), w1.stride(0), _lib.ptr(out),
+                  _lib.ptr(pre) if act != _lib.ACT_NONE else None, _lib.ptr(up), m.max_width,
+                  act, *_meta_args(m), hidden, m.max_width, m.rows, _lib.stream(dev))
+    return out, pre, up
+
+
+def f32_down_fwd(h, w2, m: GemmMeta, hidden: int):
+    h = _f32(h, "grouped_gemm_down intermediate")
+    w2 = _f32(w2, "grouped_gemm_down w2")
+    _need(w2.shape[1] == hidden, "w2 columns must equal hidden_size")
+    _need(h.shape[0] >= m.rows and h.shape[1] >= m.max_width,
+          "intermediate smaller than [rows, max_expert_width]")
+    y = _f32_zeros(m.rows, hidden, h.device)
+    if m.rows > 0:
+        _lib.call("vmoe_gemm_f32_down_fwd", h.data_ptr(), h.stride(0), w2.data_ptr(),
+                  w2.stride(0), y.data_ptr(), y.stride(0), *_meta_args(m), hidden, m.max_width,
+                  m.rows, _lib.stream(h.device))
+    return y
+
+
+def f32_up_bwd(grad_h, x, w1, pre, up, m: GemmMeta, hidden: int, act: int, gather_map=None):
+    """(grad_x in gathered rows, grad_w1) in fp32 from the gradient of the
+    activated output; pre is relu(z) (relu^2) or the gate (SwiGLU, with up)."""
+    grad_h = _f32(grad_h, "grouped_gemm_up_backward grad_output").contiguous()
+    x = _f32(x, "grouped_gemm_up_backward x")
+    w1 = _f32(w1, "grouped_gemm_up_backward w1")
+    _need(w1.shape[0] == hidden and x.shape[1] == hidden, "x / w1 do not match hidden_size")
+    _need(grad_h.shape[0] >= m.rows and grad_h.shape[1] >= m.max_width,
+          "grad_output smaller than [rows, max_expert_width]")
+    ops = [grad_h]
+    for t, what, needed in ((pre, "pre_act", act != _lib.ACT_NONE),
+                            (up, "up", act == ACT_SWIGLU)):
+        if not needed:
+            ops.append(None)
+            continue
+        _need(t is not None, f"grouped_gemm_up_backward needs {what}")
+        t = _f32(t, f"grouped_gemm_up_backward {what}").contiguous()
+        _need(t.shape == grad_h.shape, f"{what} and grad_output shapes differ")
+        ops.append(t)
+    if gather_map is None:
+        _need(x.shape[0] >= m.rows, "x has fewer rows than expert_token_offsets[-1]")
+    else:
+        _need(gather_map.numel() >= m.rows, "gather_map shorter than the padded row count")
+    dev = grad_h.device
+    grad_x = _f32_zeros(m.rows, hidden, dev)
+    grad_w1 = torch.zeros(w1.shape, dtype=torch.float32, device=dev)
+    gm = None if gather_map is None else _i32(gather_map)
+    g, p_, u = ops
+    if m.rows > 0:
+        _lib.call("vmoe_gemm_f32_up_bwd_dx", g.data_ptr(), _lib.ptr(p_), _lib.ptr(u),
+                  g.stride(0), act, w1.data_ptr(), w1.stride(0), grad_x.data_ptr(),
+                  grad_x.stride(0), *_meta_args(m), hidden, m.max_width, m.rows,
+                  _lib.stream(dev))
+        _lib.call("vmoe_gemm_f32_up_bwd_dw", x.data_ptr(), x.stride(0), x.shape[0],
+                  _lib.ptr(gm), g.data_ptr(), _lib.ptr(p_), _lib.ptr(u), g.stride(0), act,
+                  grad_w1.data_ptr(), grad_w1.stride(0), *_meta_args(m), hidden, m.max_width,
+                  m.rows, _lib.stream(dev))
+    return grad_x, grad_w1
+
+
+def f32_down_bwd(grad_y, h, w2, m: GemmMeta, hidden: int):
+    """(grad_intermediate [rows, max_width], grad_w2) in fp32."""
+    grad_y = _f32(grad_y, "grouped_gemm_down_backward grad_output")
+    h = _f32(h, "grouped_gemm_down_backward intermediate")
+    w2 = _f32(w2, "grouped_gemm_down_backward w2")
+    _need(w2.shape[1] == hidden and grad_y.shape[1] == hidden,
+          "grad_output / w2 do not match hidden_size")
+    _need(grad_y.shape[0] >= m.rows, "grad_output has fewer rows than the padded row count")
+    _need(h.shape[0] >= m.rows and h.shape[1] >= m.max_width,
+          "intermediate smaller than [rows, max_expert_width]")
+    dev = grad_y.device
+    grad_h = _f32_zeros(m.rows, m.max_width, dev)
+    grad_w2 = torch.zeros(w2.shape, dtype=torch.float32, device=dev)
+    if m.rows > 0:
+        _lib.call("vmoe_gemm_f32_down_bwd_dh", grad_y.data_ptr(), grad_y.stride(0),
+                  w2.data_ptr(), w2.stride(0), grad_h.data_ptr(), grad_h.stride(0),
+                  *_meta_args(m), hidden, m.max_width, m.rows, _lib.stream(dev))
+        _lib.call("vmoe_gemm_f32_down_bwd_dw", h.data_ptr(), h.stride(0), grad_y.data_ptr(),
+                  grad_y.stride(0), grad_w2.data_ptr(), grad_w2.stride(0), *_meta_args(m),
+                  hidden, m.max_width, m.rows, _lib.stream(dev))
+    return grad_h, grad_w2
+
+
+# ---------------------------------------------------------------------------
 # Public API (reference signatures)
 # ---------------------------------------------------------------------------
 
@@ -536,10 +665,16 @@ def grouped_gemm_up(x, w1, expert_token_offsets, expert_weight_offsets, expert_w
         gmeta = glu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                          tokens_per_expert, int(max_expert_width), x.shape[1], w1.shape[1])
         # pre_act is the gate, as the reference saves it (grouped_gemm.py:339-346)
-        h, g, _ = glu_fwd(x, w1, gmeta.fwd, True, save_pre_act, False, gather_map)
+        if _is_f32(w1):
+            h, g, _ = f32_up_fwd(x, w1, gmeta.fwd, act, gather_map, want_pre=save_pre_act)
+        else:
+            h, g, _ = glu_fwd(x, w1, gmeta.fwd, True, save_pre_act, False, gather_map)
         return (h, g) if save_pre_act else h
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1])
+    if _is_f32(w1):
+        out, pre, _ = f32_up_fwd(x, w1, m, act, gather_map, want_pre=save_pre_act)
+        return (out, pre) if save_pre_act else out
     # With gather_map, rows are read as x[gather_map[row]] inside the kernel
     # (the reference's USE_GATHER_MAP path, grouped_gemm.py:289-292).
     out, pre = up_fwd(x, w1, m, act, save_pre_act, zero_tails=True, gather_map=gather_map)
@@ -556,6 +691,8 @@ def grouped_gemm_down(intermediate, w2, expert_token_offsets, expert_weight_offs
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, intermediate.shape[1], int(hidden_size),
                   intermediate.shape[0], w2.shape[0])
+    if _is_f32(w2):
+        return f32_down_fwd(intermediate, w2, m, int(hidden_size))
     return down_fwd(intermediate, w2, m, int(hidden_size))
 
 
@@ -572,12 +709,20 @@ def grouped_gemm_up_backward(grad_output, x, w1, pre_act, expert_token_offsets,
         # grouped_gemm.py:768-790).
         gmeta = glu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                          tokens_per_expert, grad_output.shape[1], int(hidden_size), w1.shape[1])
+        if _is_f32(w1):
+            _, _, up = f32_up_fwd(x, w1, gmeta.fwd, act, gather_map, want_out=False,
+                                  want_up=True)
+            return f32_up_bwd(grad_output, x, w1, pre_act, up, gmeta.fwd, int(hidden_size), act,
+                              gather_map)
         _, _, up = glu_fwd(x, w1, gmeta.fwd, False, False, True, gather_map)
         gate = _bf16(pre_act, "grouped_gemm_up_backward pre_act")
         return glu_bwd(grad_output, x, w1, gate, up, gmeta, int(hidden_size), gather_map)
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, grad_output.shape[1], int(hidden_size), None,
                   w1.shape[1])
+    if _is_f32(w1):
+        return f32_up_bwd(grad_output, x, w1, pre_act, None, m, int(hidden_size), act,
+                          gather_map)
     return up_bwd(grad_output, x, w1, pre_act, m, int(hidden_size), act, gather_map)
 
 
@@ -590,6 +735,8 @@ def grouped_gemm_down_backward(grad_output, intermediate, w2, expert_token_offse
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, int(max_expert_width), int(hidden_size),
                   intermediate.shape[0], w2.shape[0])
+    if _is_f32(w2):
+        return f32_down_bwd(grad_output, intermediate, w2, m, int(hidden_size))
     return down_bwd(grad_output, intermediate, w2, m, int(hidden_size), zero_tails=True)
 
 
@@ -611,10 +758,14 @@ class GroupedGemmUp(torch.autograd.Function):
         use_gm = x_flat is not None and gather_map is not None
         ctx.use_gather_map = use_gm
         xs = (x_flat.to(w1.dtype), w1) if use_gm else (x, w1)
+        ctx.f32 = _is_f32(w1)
         if act == ACT_SWIGLU:
             gmeta = glu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                              tokens_per_expert, int(max_expert_width), x.shape[1], w1.shape[1])
-            out, gate, up = glu_fwd(x, w1, gmeta.fwd, True, True, True)
+            if ctx.f32:
+                out, gate, up = f32_up_fwd(x, w1, gmeta.fwd, act, want_pre=True, want_up=True)
+            else:
+                out, gate, up = glu_fwd(x, w1, gmeta.fwd, True, True, True)
             ctx.save_for_backward(*xs, gate, up, *((gather_map,) if use_gm else ()))
             ctx.meta = gmeta
             ctx.hidden_size = hidden_size
@@ -622,7 +773,10 @@ class GroupedGemmUp(torch.autograd.Function):
             return out
         m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                       tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1])
-        out, pre = up_fwd(x, w1, m, act, True, zero_tails=True)
+        if ctx.f32:
+            out, pre, _ = f32_up_fwd(x, w1, m, act, want_pre=True)
+        else:
+            out, pre = up_fwd(x, w1, m, act, True, zero_tails=True)
         ctx.save_for_backward(*xs, pre, *((gather_map,) if use_gm else ()))
         ctx.meta = m
         ctx.hidden_size = hidden_size
@@ -637,15 +791,23 @@ class GroupedGemmUp(torch.autograd.Function):
             saved = ctx.saved_tensors
             x_for_dw, w1, gate, up = saved[:4]
             gm = saved[4] if ctx.use_gather_map else None
-            grad_x, grad_w1 = glu_bwd(grad_output, x_for_dw, w1, gate, up, ctx.meta,
-                                      int(ctx.hidden_size), gm)
+            if ctx.f32:
+                grad_x, grad_w1 = f32_up_bwd(grad_output, x_for_dw, w1, gate, up, ctx.meta.fwd,
+                                             int(ctx.hidden_size), ctx.act, gm)
+            else:
+                grad_x, grad_w1 = glu_bwd(grad_output, x_for_dw, w1, gate, up, ctx.meta,
+                                          int(ctx.hidden_size), gm)
             return grad_x, grad_w1, None, None, None, None, None, None, None, None, None
         if ctx.use_gather_map:
             x_for_dw, w1, pre, gm = ctx.saved_tensors
         else:
             (x_for_dw, w1, pre), gm = ctx.saved_tensors, None
-        grad_x, grad_w1 = up_bwd(grad_output, x_for_dw, w1, pre, ctx.meta,
-                                 int(ctx.hidden_size), ctx.act, gm)
+        if ctx.f32:
+            grad_x, grad_w1 = f32_up_bwd(grad_output, x_for_dw, w1, pre, None, ctx.meta,
+                                         int(ctx.hidden_size), ctx.act, gm)
+        else:
+            grad_x, grad_w1 = up_bwd(grad_output, x_for_dw, w1, pre, ctx.meta,
+                                     int(ctx.hidden_size), ctx.act, gm)
         return grad_x, grad_w1, None, None, None, None, None, None, None, None, None
 
 
@@ -661,7 +823,8 @@ class GroupedGemmDown(torch.autograd.Function):
         m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                       tokens_per_expert, int(max_expert_width), int(hidden_size),
                       intermediate.shape[0], w2.shape[0])
-        out = down_fwd(intermediate, w2, m, int(hidden_size))
+        ctx.f32 = _is_f32(w2)
+        out = (f32_down_fwd if ctx.f32 else down_fwd)(intermediate, w2, m, int(hidden_size))
         ctx.save_for_backward(intermediate, w2)
         ctx.meta = m
         ctx.hidden_size = hidden_size
@@ -672,8 +835,12 @@ class GroupedGemmDown(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, grad_output):
         intermediate, w2 = ctx.saved_tensors
-        grad_int, grad_w2 = down_bwd(grad_output, intermediate, w2, ctx.meta,
-                                     int(ctx.hidden_size), zero_tails=True)
+        if ctx.f32:
+            grad_int, grad_w2 = f32_down_bwd(grad_output, intermediate, w2, ctx.meta,
+                                             int(ctx.hidden_size))
+        else:
+            grad_int, grad_w2 = down_bwd(grad_output, intermediate, w2, ctx.meta,
+                                         int(ctx.hidden_size), zero_tails=True)
         return grad_int, grad_w2, None, None, None, None, None, None
 
 
