@@ -63,6 +63,9 @@ def parse():
                          "bandwidth")
     ap.add_argument("--graph", action="store_true",
                     help="also time the step replayed from a HIP graph (graph_ms_per_step)")
+    ap.add_argument("--fp32-gemm", action="store_true",
+                    help="only time the fp32 grouped GEMMs (float32 weights on the public API) "
+                         "at cfg3's shapes with balanced routing")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 1 GiB device buffer 5 times: the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters")
@@ -155,6 +158,61 @@ def ceiling():
     out["bandwidth_tbs"]["copy_read_plus_write"] = round(2 * n / timed(lambda: y.copy_(x), 20) / 1e12, 2)
     out["bandwidth_tbs"]["fill_write"] = round(n / timed(lambda: y.fill_(1), 20) / 1e12, 2)
     print(json.dumps({"ceiling": out, "device": torch.cuda.get_device_name(0)}))
+
+
+def fp32_gemm():
+    """The fp32 grouped GEMMs (csrc/gemm_f32.hip) at cfg3's shapes: 64 experts
+    of width 256, n_embd 1024, 16384 tokens x top-8 routed evenly (2048 rows
+    per expert), through the public functions (each call includes its output's
+    zero fill). Rates are against the 157.3 TFLOP/s dense fp32 peak."""
+    import torch
+
+    from triton_moe.kernels import (grouped_gemm_down, grouped_gemm_down_backward,
+                                    grouped_gemm_up, grouped_gemm_up_backward)
+
+    dev = torch.device("cuda:0")
+    d, sizes, k, T, _ = CONFIGS["cfg3"]
+    E, w = sizes[0]
+    rows = T * k // E
+    P = rows * E
+    g = torch.Generator(device=dev).manual_seed(0)
+    eto = torch.arange(0, P + 1, rows, dtype=torch.int32, device=dev)
+    ewo = torch.arange(0, E * w + 1, w, dtype=torch.int32, device=dev)
+    wid = torch.full((E,), w, dtype=torch.int32, device=dev)
+    tpe = torch.full((E,), rows, dtype=torch.int32, device=dev)
+    x = torch.randn(P, d, device=dev, generator=g)
+    w1 = torch.randn(d, E * w, device=dev, generator=g) * 0.03
+    w2 = torch.randn(E * w, d, device=dev, generator=g) * 0.03
+    gy = torch.randn(P, d, device=dev, generator=g)
+    h, pre = grouped_gemm_up(x, w1, eto, ewo, wid, tpe, w, save_pre_act=True)
+    gh, _ = grouped_gemm_down_backward(gy, h, w2, eto, ewo, wid, tpe, d, w)
+    calls = {
+        "up_fwd": (1, lambda: grouped_gemm_up(x, w1, eto, ewo, wid, tpe, w, save_pre_act=True)),
+        "down_fwd": (1, lambda: grouped_gemm_down(h, w2, eto, ewo, wid, tpe, d)),
+        "down_bwd_dh_dw": (2, lambda: grouped_gemm_down_backward(gy, h, w2, eto, ewo, wid, tpe,
+                                                                  d, w)),
+        "up_bwd_dx_dw": (2, lambda: grouped_gemm_up_backward(gh, x, w1, pre, eto, ewo, wid, tpe,
+                                                              d)),
+    }
+    flops = 2.0 * P * d * w
+    out = {}
+    for name, (n, fn) in calls.items():
+        fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / 5 * 1e3
+        out[name] = {"us": round(us, 1), "tflops": round(n * flops / (us * 1e-6) / 1e12, 2)}
+    total_us = sum(v["us"] for v in out.values())
+    print(json.dumps({"fp32_gemm": out, "gemm_flops_each": flops,
+                      "step_tflops": round(6 * flops / (total_us * 1e-6) / 1e12, 2),
+                      "peak_tflops_fp32": 157.3,
+                      "shape": f"cfg3 balanced: P={P}, d={d}, E={E}, w={w}"}))
 
 
 def copy_calibration():
@@ -446,6 +504,9 @@ def main():
         return
     if args.ceiling:
         ceiling()
+        return
+    if args.fp32_gemm:
+        fp32_gemm()
         return
     torch.manual_seed(0)
     m, xb, info = build_workload(args.config, device)

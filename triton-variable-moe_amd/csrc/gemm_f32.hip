@@ -168,12 +168,14 @@ __device__ __forceinline__ void stage(float (*lds)[kPad], Fn&& at) {
   }
 }
 
-template <int F>
+// GLU: the SwiGLU up forward (a second accumulator over the up columns); its
+// own instance, so the other forms do not carry its registers.
+template <int F, bool GLU>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_f32_kernel(F32Args p) {
   __shared__ float As[kBK][kPad];
   __shared__ float Bs[kBK][kPad];
-  __shared__ float Us[kBK][kPad];  // SwiGLU up half (up forward only)
-  const bool glu = F == F_UP_FWD && p.act == VMOE_ACT_SWIGLU;
+  __shared__ float Us[GLU ? kBK : 1][kPad];  // SwiGLU up half
+  constexpr bool glu = GLU && F == F_UP_FWD;
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
   int e = 0;
   int64_t before = 0;  // tiles of experts < e
@@ -198,11 +200,11 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f32_kernel(F32Args p) {
     if (!have) break;
     const int64_t local = t - before;
     const int64_t m0 = (local / tn_count) * kT, n0 = (local % tn_count) * kT;
-    float acc[4][4] = {}, acc_up[4][4] = {};
+    float acc[4][4] = {}, acc_up[glu ? 4 : 1][4] = {};
     for (int64_t k0 = 0; k0 < q.K; k0 += kBK) {
       stage<a_k_contig<F>()>(As, [&](int k, int x) { return f32_a<F>(p, q, m0 + x, k0 + k); });
       stage<b_k_contig<F>()>(Bs, [&](int k, int x) { return f32_b<F>(p, q, k0 + k, n0 + x, false); });
-      if (glu)
+      if constexpr (glu)
         stage<false>(Us, [&](int k, int x) { return f32_b<F>(p, q, k0 + k, n0 + x, true); });
       __syncthreads();
 #pragma unroll
@@ -216,7 +218,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f32_kernel(F32Args p) {
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
-        if (glu) {
+        if constexpr (glu) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) b[j] = Us[k][tx + 16 * j];
 #pragma unroll
@@ -246,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f32_kernel(F32Args p) {
             const float r = fmaxf(z, 0.0f);
             if (p.c2) p.c2[o] = r;
             p.c[o] = r * r;
-          } else if (F == F_UP_FWD && glu) {
+          } else if constexpr (glu) {
             const float u = acc_up[i][j];
             if (p.c2) p.c2[o] = z;
             if (p.c3) p.c3[o] = u;
@@ -268,11 +270,12 @@ int64_t tile_bound(int64_t E, int64_t m_bound, int64_t n_bound, bool rows_m) {
   return tm * tn;
 }
 
-template <int F>
+template <int F, bool GLU = false>
 int f32_launch(const F32Args& p, int64_t bound, hipStream_t s) {
   if (bound <= 0 || p.rows_bound == 0 || p.max_width == 0) return VMOE_OK;  // no work
   const int64_t grid = bound < 2048 ? bound : 2048;
-  hipLaunchKernelGGL(grouped_gemm_f32_kernel<F>, dim3((unsigned)grid), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL((grouped_gemm_f32_kernel<F, GLU>), dim3((unsigned)grid), dim3(kThreads), 0, s,
+                     p);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }
@@ -333,8 +336,10 @@ extern "C" int vmoe_gemm_f32_up_fwd(const float* x, int64_t ldx, int64_t x_rows,
   p.c = out; p.ldc = ldo;
   p.c2 = activation == VMOE_ACT_NONE ? nullptr : pre_act;
   p.c3 = activation == VMOE_ACT_SWIGLU ? up : nullptr;
-  return f32_launch<F_UP_FWD>(p, tile_bound(E, rows_bound, max_width, true),
-                              reinterpret_cast<hipStream_t>(stream));
+  const int64_t bound = tile_bound(E, rows_bound, max_width, true);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return activation == VMOE_ACT_SWIGLU ? f32_launch<F_UP_FWD, true>(p, bound, s)
+                                       : f32_launch<F_UP_FWD>(p, bound, s);
 }
 
 extern "C" int vmoe_gemm_f32_down_fwd(const float* h, int64_t ldh, const float* w2, int64_t ldw2,
