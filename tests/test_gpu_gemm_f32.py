@@ -221,3 +221,52 @@ def test_f32_bf16_activations_widened(device):
     a = grouped_gemm_up(xb.to(device), w1.to(device), eto, eto, wid, wid, 64)
     b = grouped_gemm_up(xb.float().to(device), w1.to(device), eto, eto, wid, wid, 64)
     assert torch.equal(a, b)
+
+
+def test_f32_empty_routing(device):
+    """No rows at all (every expert empty): zero-row outputs, zero weight
+    gradients, nothing launched."""
+    E, d, w = 3, 32, 16
+    eto = torch.zeros(E + 1, dtype=torch.int32, device=device)
+    ewo = torch.arange(0, E * w + 1, w, dtype=torch.int32, device=device)
+    wid = torch.full((E,), w, dtype=torch.int32, device=device)
+    tpe = torch.zeros(E, dtype=torch.int32, device=device)
+    x = torch.randn(0, d, device=device, requires_grad=True)
+    w1 = torch.randn(d, E * w, device=device, requires_grad=True)
+    w2 = torch.randn(E * w, d, device=device, requires_grad=True)
+    h = grouped_gemm_up_autograd(x, w1, eto, ewo, wid, tpe, w, d, "relu_squared")
+    y = grouped_gemm_down_autograd(h, w2, eto, ewo, wid, tpe, d, w)
+    assert h.shape == (0, w) and y.shape == (0, d)
+    y.sum().backward()
+    assert w1.grad.abs().sum().item() == 0 and w2.grad.abs().sum().item() == 0
+    assert x.grad.shape == (0, d)
+
+
+@pytest.mark.parametrize("act", ["relu_squared", "swiglu"])
+def test_f32_gather_map_pad_rows_read_zeros(act, device):
+    """Map entries of -1 (the module's pad rows) read zero token rows in the
+    up forward and contribute nothing to grad_w1: same results as a gathered
+    x with zero rows there."""
+    rows, widths, d, _ = CASES["ragged"]
+    m1 = 2 if act == "swiglu" else 1
+    eto, tpe, offs1 = _meta(rows, widths, False, m1)
+    P = sum(rows)
+    gen = torch.Generator().manual_seed(17)
+    T = 40
+    x_flat = torch.randn(T, d, generator=gen)
+    gm = torch.randint(0, T, (P,), generator=gen, dtype=torch.int32)
+    gm[::5] = -1
+    xg = torch.where((gm >= 0)[:, None], x_flat[gm.clamp(min=0).long()], torch.zeros(()))
+    w1 = torch.randn(d, m1 * sum(widths), generator=gen) * 0.1
+    args = (_dev(eto, device), _dev(offs1, device), _dev(widths, device), _dev(tpe, device))
+    xf, xgd, w1d, gmd = x_flat.to(device), xg.to(device), w1.to(device), gm.to(device)
+    h_map, pre_map = grouped_gemm_up(xf, w1d, *args, max(widths), activation=act,
+                                     save_pre_act=True, gather_map=gmd)
+    h_ref, pre_ref = grouped_gemm_up(xgd, w1d, *args, max(widths), activation=act,
+                                     save_pre_act=True)
+    assert torch.equal(h_map, h_ref) and torch.equal(pre_map, pre_ref)
+    gh = torch.randn(h_ref.shape, generator=gen).to(device)
+    _, gw_map = grouped_gemm_up_backward(gh, xf, w1d, pre_ref, *args, d, activation=act,
+                                         gather_map=gmd)
+    _, gw_ref = grouped_gemm_up_backward(gh, xgd, w1d, pre_ref, *args, d, activation=act)
+    assert torch.equal(gw_map, gw_ref)
