@@ -15,7 +15,8 @@
 // uses it.
 //
 // Tiles: 64 x 64 outputs per 256-thread workgroup, 4 x 4 per thread, k steps
-// of 16 staged in LDS. Workgroups stride over the experts' tiles in order,
+// of 16 staged in LDS, each thread loading runs of 4 consecutive elements
+// (16-byte loads where the address is aligned and the run in range). Workgroups stride over the experts' tiles in order,
 // read from the metadata on the device (no host sync).
 #include "vmoe_common.h"
 
@@ -149,10 +150,72 @@ constexpr bool a_k_contig() { return F == F_UP_FWD || F == F_DOWN_FWD || F == F_
 template <int F>
 constexpr bool b_k_contig() { return F == F_UP_DX || F == F_DOWN_DH; }
 
-// Loads a kBK x kT stage into lds[k][i]: 4 elements per thread, consecutive
-// threads along the operand's contiguous dimension.
+// Four consecutive floats from ptr of which `valid` are in range (the rest
+// read as 0): one 16-byte load when all four are and the address allows it.
+__device__ __forceinline__ float4 load_run(const float* ptr, int64_t valid) {
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (!ptr || valid <= 0) return v;
+  if (valid >= 4 && (reinterpret_cast<uintptr_t>(ptr) & 15) == 0)
+    return *reinterpret_cast<const float4*>(ptr);
+  v.x = ptr[0];
+  if (valid > 1) v.y = ptr[1];
+  if (valid > 2) v.z = ptr[2];
+  if (valid > 3) v.w = ptr[3];
+  return v;
+}
+
+// Four elements of A from (m, k) along its contiguous dimension (k for the
+// K-contiguous forms, m otherwise); not for up dX, whose A is the
+// activation gradient (stage_elem).
+template <int F>
+__device__ __forceinline__ float4 f32_a_run(const F32Args& p, const F32Prob& q, int64_t m,
+                                            int64_t k) {
+  const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  switch (F) {
+    case F_UP_FWD: {
+      if (m >= q.M) return z;
+      const float* row = token_row(p, q.t0 + m);
+      return load_run(row ? row + k : nullptr, q.K - k);
+    }
+    case F_DOWN_FWD:
+    case F_DOWN_DH:
+      return m < q.M ? load_run(p.a + (q.t0 + m) * p.lda + k, q.K - k) : z;
+    case F_UP_DW: {
+      if (k >= q.K) return z;
+      const float* row = token_row(p, q.t0 + k);
+      return load_run(row ? row + m : nullptr, q.M - m);
+    }
+    default:  // F_DOWN_DW: h^T
+      return k < q.K ? load_run(p.a + (q.t0 + k) * p.lda + m, q.M - m) : z;
+  }
+}
+
+// Four elements of B from (k, n) along its contiguous dimension (k for up dX
+// and down dH, n otherwise); not for up dW, whose B is the activation
+// gradient (stage_elem).
+template <int F>
+__device__ __forceinline__ float4 f32_b_run(const F32Args& p, const F32Prob& q, int64_t k,
+                                            int64_t n, bool second) {
+  const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  switch (F) {
+    case F_UP_FWD:
+      return k < q.K ? load_run(p.b + k * p.ldb + q.w0 + (second ? q.w : 0) + n, q.N - n) : z;
+    case F_DOWN_FWD:
+      return k < q.K ? load_run(p.b + (q.w0 + k) * p.ldb + n, q.N - n) : z;
+    case F_UP_DX:  // W1^T
+      return n < q.N ? load_run(p.b + n * p.ldb + q.w0 + k, q.K - k) : z;
+    case F_DOWN_DH:  // W2^T
+      return n < q.N ? load_run(p.b + (q.w0 + n) * p.ldb + k, q.K - k) : z;
+    default:  // F_DOWN_DW: grad_y
+      return k < q.K ? load_run(p.b + (q.t0 + k) * p.ldb + n, q.N - n) : z;
+  }
+}
+
+// Loads a kBK x kT stage into lds[k][x] element by element, consecutive
+// lanes along the operand's contiguous dimension (the activation-gradient
+// operands, formed per element).
 template <bool KCONTIG, typename Fn>
-__device__ __forceinline__ void stage(float (*lds)[kPad], Fn&& at) {
+__device__ __forceinline__ void stage_elem(float (*lds)[kPad], Fn&& at) {
   const int tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -165,6 +228,28 @@ __device__ __forceinline__ void stage(float (*lds)[kPad], Fn&& at) {
       k = (tid >> 6) + 4 * i;
     }
     lds[k][x] = at(k, x);
+  }
+}
+
+// Loads a kBK x kT stage into lds[k][x]: one run of 4 elements per thread
+// along the operand's contiguous dimension (k when KCONTIG, x otherwise).
+template <bool KCONTIG, typename Fn>
+__device__ __forceinline__ void stage(float (*lds)[kPad], Fn&& run) {
+  const int tid = threadIdx.x;
+  if (KCONTIG) {
+    const int x = tid >> 2, k = (tid & 3) * 4;
+    const float4 v = run(k, x);
+    lds[k][x] = v.x;
+    lds[k + 1][x] = v.y;
+    lds[k + 2][x] = v.z;
+    lds[k + 3][x] = v.w;
+  } else {
+    const int x = (tid & 15) * 4, k = tid >> 4;
+    const float4 v = run(k, x);
+    lds[k][x] = v.x;
+    lds[k][x + 1] = v.y;
+    lds[k][x + 2] = v.z;
+    lds[k][x + 3] = v.w;
   }
 }
 
@@ -202,10 +287,18 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f32_kernel(F32Args p) {
     const int64_t m0 = (local / tn_count) * kT, n0 = (local % tn_count) * kT;
     float acc[4][4] = {}, acc_up[glu ? 4 : 1][4] = {};
     for (int64_t k0 = 0; k0 < q.K; k0 += kBK) {
-      stage<a_k_contig<F>()>(As, [&](int k, int x) { return f32_a<F>(p, q, m0 + x, k0 + k); });
-      stage<b_k_contig<F>()>(Bs, [&](int k, int x) { return f32_b<F>(p, q, k0 + k, n0 + x, false); });
+      if constexpr (F == F_UP_DX)
+        stage_elem<true>(As, [&](int k, int x) { return f32_a<F>(p, q, m0 + x, k0 + k); });
+      else
+        stage<a_k_contig<F>()>(As, [&](int k, int x) { return f32_a_run<F>(p, q, m0 + x, k0 + k); });
+      if constexpr (F == F_UP_DW)
+        stage_elem<false>(Bs, [&](int k, int x) { return f32_b<F>(p, q, k0 + k, n0 + x, false); });
+      else
+        stage<b_k_contig<F>()>(Bs, [&](int k, int x) {
+          return f32_b_run<F>(p, q, k0 + k, n0 + x, false);
+        });
       if constexpr (glu)
-        stage<false>(Us, [&](int k, int x) { return f32_b<F>(p, q, k0 + k, n0 + x, true); });
+        stage<false>(Us, [&](int k, int x) { return f32_b_run<F>(p, q, k0 + k, n0 + x, true); });
       __syncthreads();
 #pragma unroll
       for (int k = 0; k < kBK; ++k) {
