@@ -500,6 +500,13 @@ int vmoe_gemm_f32_up_bwd_dx(const float* grad_h, const float* pre_act, const flo
                             int64_t hidden, int64_t max_width, int64_t rows_bound,
                             vmoe_stream_t stream);
 
+/* grad_act = pre_act > 0 ? grad_h * 2 * pre_act : 0, elementwise over
+ * [rows, cols] in fp32 (the relu^2 rule of grouped_gemm.py:751-764): GA formed
+ * once for the fp32 dX and dW GEMMs, which then take it with
+ * VMOE_ACT_NONE. grad_h and pre_act share ld. */
+int vmoe_f32_relu2_grad(const float* grad_h, const float* pre_act, int64_t ld, float* grad_act,
+                        int64_t ldo, int64_t rows, int64_t cols, vmoe_stream_t stream);
+
 /* grad_w1 = X_e^T @ GA_e into W1's layout (grouped_gemm.py:810-972), GA as
  * for vmoe_gemm_f32_up_bwd_dx, X through gather_map when it is non-null. */
 int vmoe_gemm_f32_up_bwd_dw(const float* x, int64_t ldx, int64_t x_rows,

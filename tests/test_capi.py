@@ -28,7 +28,7 @@ def test_header_declares_expected_entry_points():
                  "vmoe_zero_tail_cols", "vmoe_status_string", "vmoe_gather_tokens",
                  "vmoe_gemm_f32_up_fwd", "vmoe_gemm_f32_down_fwd", "vmoe_gemm_f32_up_bwd_dx",
                  "vmoe_gemm_f32_up_bwd_dw", "vmoe_gemm_f32_down_bwd_dh",
-                 "vmoe_gemm_f32_down_bwd_dw"):
+                 "vmoe_gemm_f32_down_bwd_dw", "vmoe_f32_relu2_grad"):
         assert must in names
 
 
@@ -165,6 +165,8 @@ def test_argument_checks_return_invalid_arg():
                                          None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_gemm_f32_down_bwd_dw(1, 16, 1, 16, 1, 16, None, 1, 1, 1, 2, 16, 16, 64,
                                          None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_f32_relu2_grad(1, 1, 8, 1, 16, 4, 16, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_f32_relu2_grad(None, None, 16, None, 16, 0, 16, None) == _lib.OK
     # no rows: nothing to launch
     assert lib.vmoe_gemm_f32_down_fwd(1, 16, 1, 16, 1, 16, 1, 1, 1, 1, 2, 16, 16, 0,
                                       None) == _lib.OK

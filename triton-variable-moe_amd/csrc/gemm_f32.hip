@@ -18,6 +18,8 @@
 // of 16 staged in LDS, each thread loading runs of 4 consecutive elements
 // (16-byte loads where the address is aligned and the run in range). Workgroups stride over the experts' tiles in order,
 // read from the metadata on the device (no host sync).
+#include <algorithm>
+
 #include "vmoe_common.h"
 
 namespace vmoe {
@@ -405,10 +407,37 @@ bool grad_ok(const float* g, const float* pre, const float* up, int64_t ldg, int
   return true;
 }
 
+__global__ __launch_bounds__(256) void f32_relu2_grad_kernel(const float* g, const float* pre,
+                                                             int64_t ld, float* ga, int64_t ldo,
+                                                             int64_t rows, int64_t cols) {
+  const int64_t n = rows * cols;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / cols, c = i - r * cols;
+    const float pr = pre[r * ld + c];
+    ga[r * ldo + c] = pr > 0.0f ? g[r * ld + c] * 2.0f * pr : 0.0f;
+  }
+}
+
 }  // namespace
 }  // namespace vmoe
 
 using namespace vmoe;
+
+extern "C" int vmoe_f32_relu2_grad(const float* grad_h, const float* pre_act, int64_t ld,
+                                   float* grad_act, int64_t ldo, int64_t rows, int64_t cols,
+                                   vmoe_stream_t stream) {
+  if (rows < 0 || cols < 0 || ld < cols || ldo < cols) return VMOE_ERR_INVALID_ARG;
+  if (rows == 0 || cols == 0) return VMOE_OK;
+  if (!grad_h || !pre_act || !grad_act) return VMOE_ERR_INVALID_ARG;
+  const int64_t n = rows * cols;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
+  hipLaunchKernelGGL(f32_relu2_grad_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), grad_h, pre_act, ld, grad_act, ldo,
+                     rows, cols);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
 
 extern "C" int vmoe_gemm_f32_up_fwd(const float* x, int64_t ldx, int64_t x_rows,
                                     const int32_t* gather_map, const float* w1, int64_t ldw1,

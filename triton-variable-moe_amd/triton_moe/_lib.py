@@ -67,6 +67,7 @@ _SIGNATURES = {
                                 _vp, _i32, _i64, _i64, _i64, _vp],
     "vmoe_gemm_f32_up_bwd_dw": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _i64, _vp,
                                 _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "vmoe_f32_relu2_grad": [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp],
     "vmoe_gemm_f32_down_bwd_dh": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32,
                                   _i64, _i64, _i64, _vp],
     "vmoe_gemm_f32_down_bwd_dw": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32,

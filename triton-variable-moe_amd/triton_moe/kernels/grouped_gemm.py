@@ -490,6 +490,12 @@ def f32_up_bwd(grad_h, x, w1, pre, up, m: GemmMeta, hidden: int, act: int, gathe
     grad_w1 = torch.zeros(w1.shape, dtype=torch.float32, device=dev)
     gm = None if gather_map is None else _i32(gather_map)
     g, p_, u = ops
+    if act == _lib.ACT_RELU_SQUARED and g.numel() > 0:
+        # GA formed once; both GEMMs then read it as a plain operand
+        ga = torch.empty_like(g)
+        _lib.call("vmoe_f32_relu2_grad", g.data_ptr(), p_.data_ptr(), g.stride(0), ga.data_ptr(),
+                  ga.stride(0), g.shape[0], g.shape[1], _lib.stream(dev))
+        g, p_, act = ga, None, _lib.ACT_NONE
     if m.rows > 0:
         _lib.call("vmoe_gemm_f32_up_bwd_dx", g.data_ptr(), _lib.ptr(p_), _lib.ptr(u),
                   g.stride(0), act, w1.data_ptr(), w1.stride(0), grad_x.data_ptr(),
