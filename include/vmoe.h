@@ -280,11 +280,32 @@ int vmoe_combine_weight_grad(const uint16_t* grad, int64_t ldg, const uint16_t* 
  * dL/dw = sum_c dL/dH'[c] relu(z)[c]^2:
  *   grad_weights[a] = bf16( sum_{b < num_blocks} row_dot[row][b] / row_weight[row] ),
  *   row = assignment_row[a], with row_dot from vmoe_gemm_down_bwd_dh; 0 when
- *   row < 0, row >= rows or row_weight[row] == 0. */
+ *   row < 0, row >= rows or |row_weight[row]| < 2^-64 (zero and bf16
+ *   denormals: the division loses those, vmoe_routing_weight_grad_direct
+ *   fills them). */
 int vmoe_routing_weight_grad(const float* row_dot, int64_t ld_row_dot, int32_t num_blocks,
                              int64_t rows, const float* row_weight,
                              const int32_t* assignment_row, int64_t num_assignments,
                              uint16_t* grad_weights, vmoe_stream_t stream);
+
+/* vmoe_routing_weight_grad_direct: the entries of the same gradient whose
+ * row weight is below 2^-64 in magnitude, from the definition
+ *   grad_weights[a] = bf16( sum_{c < w_e} (grad_y[a / top_k] . w2[ewo[e] + c])
+ *                           * pre_act[row][c]^2 ),
+ * row = assignment_row[a], e the expert with eto[e] <= row < eto[e+1], the
+ * dots in fp32 (grad_y rows past gy_rows count as zero; ldgy = 0 reads one
+ * row for all), times the bf16 scalar *grad_scale when it is not NULL (as
+ * vmoe_gemm_down_bwd_dh's). Other entries are left as they are, so it runs after
+ * vmoe_routing_weight_grad; with no tiny weight it reads assignment_row and
+ * row_weight once. pre_act [rows, ld_pre >= max width] as for
+ * vmoe_gemm_down_bwd_dh; eto/ewo/widths as for the GEMMs below. */
+int vmoe_routing_weight_grad_direct(const uint16_t* grad_y, int64_t ldgy, int64_t gy_rows,
+                                    const uint16_t* grad_scale, const uint16_t* w2, int64_t ldw2, const uint16_t* pre_act,
+                                    int64_t ld_pre, const float* row_weight,
+                                    const int32_t* assignment_row, int64_t num_assignments,
+                                    int32_t top_k, const int32_t* eto, const int32_t* ewo,
+                                    const int32_t* widths, int32_t num_experts, int64_t hidden,
+                                    int64_t rows, uint16_t* grad_weights, vmoe_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Variable-width grouped GEMMs (bf16 in, fp32 MFMA accumulate, bf16 out).

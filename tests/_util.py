@@ -35,6 +35,18 @@ def assert_close_norm(got, ref, tol=TIGHT, what=""):
     assert mx <= tol[0] and mn <= tol[1], f"{what}: normwise max {mx:.3e} mean {mn:.3e} > {tol}"
 
 
+def bf16_ulps(got: torch.Tensor, ref: torch.Tensor) -> torch.Tensor:
+    """Distance in bf16 units in the last place between two bf16 tensors
+    (int64, elementwise): the bit patterns mapped to a monotone integer
+    line (sign-magnitude to two's complement), so +0 and -0 are 0 apart and
+    neighbouring values across zero 1 apart."""
+    def line(t):
+        i = t.detach().cpu().to(torch.bfloat16).contiguous().view(torch.int16).to(torch.int64)
+        mag = i & 0x7FFF
+        return torch.where(i < 0, -mag, mag)
+    return (line(got) - line(ref)).abs()
+
+
 def bits_equal(got: torch.Tensor, ref: torch.Tensor) -> bool:
     g = got.detach().cpu().contiguous()
     r = ref.detach().cpu().to(g.dtype).contiguous()

@@ -76,6 +76,13 @@ def test_argument_checks_return_invalid_arg():
     assert lib.vmoe_routing_weight_grad(1, 2, 4, 8, 1, 1, 16, 1, None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_routing_weight_grad(1, 4, 4, 8, None, 1, 16, 1, None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_routing_weight_grad(None, 4, 4, 8, 1, None, 0, None, None) == _lib.OK
+    # its direct form for tiny weights: ldw2 below hidden, top_k 0, missing pre_act
+    f = lib.vmoe_routing_weight_grad_direct
+    args = [1, 64, 8, None, 1, 64, 1, 256, 1, 1, 16, 2, 1, 1, 1, 4, 64, 32, 1, None]
+    assert f(*args[:4], 1, 32, *args[6:]) == _lib.ERR_INVALID_ARG
+    assert f(*args[:11], 0, *args[12:]) == _lib.ERR_INVALID_ARG
+    assert f(*args[:6], None, *args[7:]) == _lib.ERR_INVALID_ARG
+    assert f(*args[:10], 0, *args[11:]) == _lib.OK  # no assignments: nothing to do
     # its logit gradient: both or neither index arrays, k above one wave
     assert lib.vmoe_router_weight_bwd(1, 8, 4, 8, 2, 1, 1, 1, 1, 2, 1, 8,
                                       None) == _lib.ERR_INVALID_ARG

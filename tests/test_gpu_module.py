@@ -16,13 +16,15 @@ from __future__ import annotations
 
 import contextlib
 
+import numpy as np
 import pytest
 import torch
 
 from oracle import eager
 from triton_moe import TritonMoEConfig, TritonMoEMLP
 
-from _util import LOOSE, TIGHT, assert_close_norm, bits_equal, make_problem, zipf_bias
+from _util import (LOOSE, TIGHT, assert_close_norm, bf16_ulps, bits_equal, make_problem,
+                   zipf_bias)
 
 pytestmark = pytest.mark.gpu
 
@@ -372,3 +374,76 @@ def test_routing_weight_grad(name, device):
     # the router weight's gradient is the linear layer's backward of it
     wr_ref = store["glogits"].float().t() @ p["x"].to(device).float()
     assert_close_norm(grads[True][3], wr_ref, TIGHT, f"{name} router weight grad")
+
+
+@pytest.mark.parametrize("name", ["ref_small", "ref_variable", "cfg2"])
+def test_routing_weight_grad_at_zero_and_denormal_weights(name, device):
+    """The routing-weight gradient where the bf16 weight is 0 or a denormal:
+    the module forms dL/dw from the dH GEMM's row sums of w * (G W2^T) *
+    relu(z)^2 divided by w, which cannot recover these, so they take the
+    direct form sum_c (G[t] . W2[c]) relu(z)[c]^2. Checked entry by entry
+    against the fp32 oracle's G[t] . Y[row] (Y = relu(x W1_e)^2 W2_e
+    unweighted), which does not depend on w; the forward output is checked
+    too (a zero weight removes that slot's contribution)."""
+    B, S, d, sizes, k, b, _alpha = CONFIGS[name]
+    T = B * S
+    p = make_problem(T, d, sizes, k, b, seed=3, device=device)
+    wts = p["wts"].cpu().clone().reshape(-1)
+    A = wts.numel()
+    zero = torch.zeros(A, dtype=torch.bool)
+    zero[::7] = True
+    den = torch.zeros(A, dtype=torch.bool)
+    den[3::11] = True
+    den &= ~zero
+    wts[zero] = 0
+    # bf16 denormals (below 2^-126): 2^-130 and 2^-133
+    wts[den] = torch.tensor([2.0 ** -130, 2.0 ** -133], dtype=torch.bfloat16).repeat(
+        int(den.sum()) // 2 + 1)[:int(den.sum())]
+    assert (wts[den].float() < 2.0 ** -126).all() and (wts[den] != 0).all()
+    m = _module(p, d, sizes, k, b, device)
+    x_flat = p["x"].to(device)
+    w = wts.to(device).requires_grad_(True)
+    sel = p["sel"].reshape(-1).to(device)
+    out, _tpe = m._experts(x_flat, w, sel)
+    G = torch.randn(T, d, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    out.backward(G.to(device))
+    got = w.grad.float().cpu()
+    prob = eager.Problem(p["x"].float(), p["w1"].float(), p["w2"].float(), p["widths"],
+                         p["offsets"], p["sel"].cpu(), wts.view(T, k).float(), b)
+    ff = eager.forward(prob, "fp32")
+    ar = ff["route"]["assignment_row"]
+    ref = eager.combine_weight_grad(G.float(), ff["y"], ar, k, T)
+    assert_close_norm(out.float(), ff["out"], LOOSE, f"{name} out")
+    scale = ref.abs().max().item()
+    tiny = zero | den
+    err = (got - ref).abs()
+    # every entry: within 3 % of itself plus 1 % of the largest entry (bf16
+    # PRE and bf16 GH against the unrounded chain; a lost gradient fails)
+    bad = err > 3e-2 * ref.abs() + 1e-2 * scale
+    assert not bad.any(), (name, int(bad.sum()), err[bad][:8], ref[bad][:8])
+    assert_close_norm(got, ref, LOOSE, f"{name} all entries")
+    # the tiny-weight entries are real gradients, not zeros, and equal the
+    # direct form on the module's own bf16 PRE (float64 here) up to fp32 sums
+    assert (got[tiny] != 0).float().mean() > 0.99
+    pre = eager.forward(prob, "bf16", ff["route"])["pre_act"].double()
+    G64, W2 = G.double(), p["w2"].double()
+    ar_t = torch.as_tensor(ar, dtype=torch.int64)
+    rows_ = ar_t[tiny]
+    toks = torch.nonzero(tiny).reshape(-1) // k
+    ends = torch.as_tensor(np.asarray(ff["route"]["padded_bins"], np.int64))
+    exp_of = torch.searchsorted(ends, rows_, right=True)  # rows [ends[e-1], ends[e]) are e's
+    ref_b = torch.zeros(int(tiny.sum()), dtype=torch.float64)
+    mag = torch.zeros_like(ref_b)  # sum of the terms' magnitudes
+    for e, (w_, o) in enumerate(zip(p["widths"], p["offsets"])):
+        sel_e = exp_of == e
+        if sel_e.any():
+            terms = (G64[toks[sel_e]] @ W2[o:o + w_].T) * pre[rows_[sel_e], :w_] ** 2
+            ref_b[sel_e] = terms.sum(1)
+            mag[sel_e] = terms.abs().sum(1)
+    # the entries are bf16: 99.9 % within one unit in the last place of the
+    # rounded float64 value; the rest (sums that cancel) within 1e-4 of their
+    # terms' magnitude (fp32 sums, and PRE bits that may differ by one ulp)
+    ulps = bf16_ulps(w.grad[tiny.to(device)], ref_b.to(torch.bfloat16))
+    assert float((ulps <= 1).double().mean()) >= 0.999, (name, int(ulps.max()))
+    err_b = (got[tiny].double() - ref_b).abs()
+    assert (err_b <= 2.0 ** -8 * ref_b.abs() + 1e-4 * mag).all(), (name, int(ulps.max()))

@@ -362,6 +362,12 @@ __global__ __launch_bounds__(kThreads) void combine_wgrad_kernel(
 // summed in order and divided by w, one thread per assignment:
 //   gw[a] = bf16(sum_b row_dot[row][b] / w[row]), row = assignment_row[a],
 // 0 where row < 0 (a dropped assignment) or w[row] == 0.
+// Routing weights below this magnitude (zero and every bf16 denormal among
+// them) take the direct form of their gradient: the dH GEMM's row sums hold
+// w * (G W2^T) * relu(z)^2 rounded through bf16(w * (G W2^T)), and dividing
+// them by such a w is 0 / 0 at w = 0 and loses the gradient's bits below.
+constexpr float kTinyWeight = 0x1p-64f;
+
 __global__ __launch_bounds__(kThreads) void routing_wgrad_kernel(
     const float* __restrict__ row_dot, int64_t ld, int nblk, int64_t rows,
     const float* __restrict__ row_weight, const int32_t* __restrict__ assignment_row,
@@ -372,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void routing_wgrad_kernel(
     float g = 0.0f;
     if (row >= 0 && row < rows) {
       const float w = row_weight[row];
-      if (w != 0.0f) {
+      if (!(fabsf(w) < kTinyWeight)) {
         const float* rd = row_dot + (int64_t)row * ld;
         float s = 0.0f;
         for (int b = 0; b < nblk; ++b) s += rd[b];
@@ -380,6 +386,72 @@ __global__ __launch_bounds__(kThreads) void routing_wgrad_kernel(
       }
     }
     gw[a] = (uint16_t)f32_to_bf16(g);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// The gradient of the routing weights below kTinyWeight, from its definition
+// dL/dw = sum_c (G[t] . W2[ewo[e] + c]) * pre[row][c]^2, G's row t = a / top_k
+// and e the expert whose rows [eto[e], eto[e+1]) hold `row`. Each lane tests
+// one assignment; the wave then works through the tiny ones it found (one
+// fp32 dot of length hidden per column, summed across the wave), so the
+// launch costs one read of assignment_row and row_weight when there are
+// none. Only the tiny entries of gw are written.
+__global__ __launch_bounds__(kThreads) void routing_wgrad_direct_kernel(
+    const uint16_t* __restrict__ gy, int64_t ldgy, int64_t gy_rows,
+    const uint16_t* __restrict__ grad_scale, const uint16_t* __restrict__ w2, int64_t ldw2,
+    const uint16_t* __restrict__ pre,
+    int64_t ldp, const float* __restrict__ row_weight,
+    const int32_t* __restrict__ assignment_row, int64_t A, int top_k,
+    const int32_t* __restrict__ eto, const int32_t* __restrict__ ewo,
+    const int32_t* __restrict__ widths, int E, int64_t hidden, int64_t rows,
+    uint16_t* __restrict__ gw) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t nwaves = (int64_t)gridDim.x * kRowsPerBlock;
+  for (int64_t base = ((int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave) * kWave;
+       base < A; base += nwaves * kWave) {
+    const int64_t a = base + lane;
+    int32_t row = -1;
+    bool tiny = false;
+    if (a < A) {
+      row = assignment_row[a];
+      tiny = row >= 0 && row < rows && fabsf(row_weight[row]) < kTinyWeight;
+    }
+    uint64_t mask = ballot64(tiny);
+    while (mask) {
+      const int src = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      const int32_t r = __shfl(row, src);
+      const int64_t aa = base + src;
+      const int64_t tok = aa / top_k;
+      int lo = 0, hi = E;  // eto[lo] <= r < eto[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (eto[mid] <= r) lo = mid; else hi = mid;
+      }
+      const int width = widths[lo];
+      const int64_t col0 = ewo[lo];
+      float s = 0.0f;
+      if (tok < gy_rows) {
+        const uint16_t* g = gy + tok * ldgy;
+        const uint16_t* p = pre + (int64_t)r * ldp;
+        for (int c = 0; c < width; ++c) {
+          const uint16_t* wr = w2 + (col0 + c) * ldw2;
+          float d = 0.0f;
+          for (int64_t j = lane; j < hidden; j += kWave) d += bf16_to_f32(g[j]) * bf16_to_f32(wr[j]);
+          d = wave_sum(d);
+          const float pc = bf16_to_f32(p[c]);
+          s += d * (pc * pc);
+        }
+      }
+      if (grad_scale) s *= bf16_to_f32(*grad_scale);
+      if (lane == 0) gw[aa] = (uint16_t)f32_to_bf16(s);
+    }
   }
 }
 
@@ -536,6 +608,30 @@ extern "C" int vmoe_routing_weight_grad(const float* row_dot, int64_t ld_row_dot
   hipLaunchKernelGGL(routing_wgrad_kernel, dim3((unsigned)g), dim3(kThreads), 0, s, row_dot,
                      ld_row_dot, num_blocks, rows, row_weight, assignment_row, num_assignments,
                      grad_weights);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+extern "C" int vmoe_routing_weight_grad_direct(
+    const uint16_t* grad_y, int64_t ldgy, int64_t gy_rows, const uint16_t* grad_scale,
+    const uint16_t* w2, int64_t ldw2, const uint16_t* pre_act, int64_t ld_pre,
+    const float* row_weight,
+    const int32_t* assignment_row, int64_t num_assignments, int32_t top_k, const int32_t* eto,
+    const int32_t* ewo, const int32_t* widths, int32_t num_experts, int64_t hidden, int64_t rows,
+    uint16_t* grad_weights, vmoe_stream_t stream) {
+  if (num_assignments < 0 || rows < 0 || top_k <= 0 || num_experts <= 0 || hidden < 0 ||
+      gy_rows < 0 || ldgy < 0 || ldw2 < hidden || ld_pre < 0)
+    return VMOE_ERR_INVALID_ARG;
+  if (num_assignments == 0 || rows == 0) return VMOE_OK;
+  if (!grad_weights || !assignment_row || !row_weight || !eto || !ewo || !widths || !pre_act ||
+      (hidden > 0 && (!w2 || (gy_rows > 0 && !grad_y))))
+    return VMOE_ERR_INVALID_ARG;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t g = std::min<int64_t>((num_assignments + kThreads - 1) / kThreads, 65536);
+  hipLaunchKernelGGL(routing_wgrad_direct_kernel, dim3((unsigned)g), dim3(kThreads), 0, s,
+                     grad_y, ldgy, gy_rows, grad_scale, w2, ldw2, pre_act, ld_pre, row_weight,
+                     assignment_row, num_assignments, top_k, eto, ewo, widths, num_experts,
+                     hidden, rows, grad_weights);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }

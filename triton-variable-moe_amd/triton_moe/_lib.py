@@ -40,6 +40,8 @@ _SIGNATURES = {
     "vmoe_combine": [_vp, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp],
     "vmoe_combine_weight_grad": [_vp, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _vp],
     "vmoe_routing_weight_grad": [_vp, _i64, _i32, _i64, _vp, _vp, _i64, _vp, _vp],
+    "vmoe_routing_weight_grad_direct": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _i64,
+                                        _i32, _vp, _vp, _vp, _i32, _i64, _i64, _vp, _vp],
     "vmoe_gemm_up_fwd": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp,
                          _vp, _vp, _i32, _i64, _i64, _i64, _vp],
     "vmoe_gemm_down_fwd": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,

@@ -975,7 +975,16 @@ class RoutedMoEOp(torch.autograd.Function):
         if row_dot is not None:
             grad_weights = torch.empty(ctx.weights_shape, dtype=torch.bfloat16,
                                        device=grad_out.device)
+            st = _lib.stream(grad_out.device)
             _lib.call("vmoe_routing_weight_grad", row_dot.data_ptr(), row_dot.stride(0),
                       row_dot.shape[1], m.rows, rw.data_ptr(), ar.data_ptr(), ar.numel(),
-                      grad_weights.data_ptr(), _lib.stream(grad_out.device))
+                      grad_weights.data_ptr(), st)
+            # weights of magnitude below 2^-64 (zero included): from the
+            # unscaled gradient, which the division above cannot recover
+            g, ldg, g_rows, gs = _grad_source(grad_out, m, gm)
+            _lib.call("vmoe_routing_weight_grad_direct", g.data_ptr(), ldg, g_rows,
+                      _lib.ptr(gs), w2.data_ptr(), w2.stride(0), pre.data_ptr(), pre.stride(0),
+                      rw.data_ptr(), ar.data_ptr(), ar.numel(), ctx.top_k, m.eto.data_ptr(),
+                      m.ewo.data_ptr(), m.widths.data_ptr(), m.num_experts, d, m.rows,
+                      grad_weights.data_ptr(), st)
         return grad_x, grad_w1, grad_w2, None, None, None, None, None, None, grad_weights
