@@ -61,8 +61,11 @@ def parse():
                     help="only measure the box's practical ceilings: dense bf16 torch.matmul "
                          "(hipBLASLt) at square and MoE-like shapes, and device copy / fill "
                          "bandwidth")
-    ap.add_argument("--graph", action="store_true",
-                    help="also time the step replayed from a HIP graph (graph_ms_per_step)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="skip timing the step replayed from a HIP graph (graph_ms_per_step)")
+    ap.add_argument("--other-configs", default="cfg1,cfg2,cfg4",
+                    help="comma-separated configurations also measured (fewer steps) and "
+                         "reported under other_configs; empty to skip")
     ap.add_argument("--fp32-gemm", action="store_true",
                     help="only time the fp32 grouped GEMMs (float32 weights on the public API) "
                          "at cfg3's shapes with balanced routing")
@@ -485,6 +488,67 @@ def cpu_model():
     return platform.processor()
 
 
+def measure(name, device, steps, warmup, kernel_steps, graph):
+    """Times one configuration: eager steps (and HIP-graph replays when
+    `graph`), then the per-launch breakdown. Returns the figures and the
+    workload (model, input, routing) for the CPU baseline."""
+    import torch
+
+    torch.manual_seed(0)
+    m, xb, info = build_workload(name, device)
+    flops, counts, sel = gemm_flops(m, xb)
+    ms = time_steps(m, xb, steps, warmup)
+    graph_ms = time_graph_steps(m, xb, steps, warmup) if graph else None
+    kern = kernel_breakdown(m, xb, kernel_steps)
+    gemm_names = [n for n in kern if n.startswith("gemm_")]
+    gemm_us = sum(kern[n] for n in gemm_names)
+    gemm_tflops = flops / (gemm_us * 1e-6) / 1e12
+    dom = max(gemm_names, key=lambda n: kern[n])
+    achieved = flops / 6.0 / (kern[dom] * 1e-6) / 1e12
+
+    d, sizes, k, T, _ = CONFIGS[name]
+    A = T * k
+    E = m.num_experts
+    widths = [w for c, w in sizes for _ in range(c)]
+    nw = sum(int(n) * w for n, w in zip(counts, widths))
+    # Permutation and routing bytes: each combine reads the k rows of every
+    # token and the row of each assignment and writes the token rows; the
+    # routing reads the ids (int32) and bf16 weights and writes bin_ids,
+    # indices and assignment_row per assignment and row_src, gather_map and
+    # the fp32 row weight per padded row (+ five E-long arrays).
+    P = sum(-(-int(n) // 64) * 64 for n in counts)
+    perm_bytes = {
+        "combine": 2 * A * d + 2 * T * d + 4 * A,
+        "gather_bwd_combine": 2 * A * d + 2 * T * d + 4 * A,
+        "route": 6 * A + 12 * A + 12 * P + 20 * E,
+    }
+    perm_us = sum(kern[n] for n in perm_bytes)
+    perm_gbs = sum(perm_bytes.values()) / (perm_us * 1e-6) / 1e9
+    return {
+        "m": m, "xb": xb, "sel": sel, "info": info, "counts": counts, "flops": flops,
+        "ms": ms, "graph_ms": graph_ms, "kern": kern, "gemm_tflops": gemm_tflops,
+        "dom": dom, "achieved": achieved, "A": A, "T": T, "d": d, "nw": nw,
+        "W": sum(widths), "perm_gbs": perm_gbs,
+    }
+
+
+def summary(name, r):
+    """The compact record of a configuration in `other_configs`."""
+    d, sizes, k, T, _ = CONFIGS[name]
+    return {
+        "workload": f"n_embd={d}, expert_sizes={sizes}, top_k={k}, tokens={T}, block_size=64",
+        "ms_per_step": round(r["ms"], 4),
+        "graph_ms_per_step": None if r["graph_ms"] is None else round(r["graph_ms"], 4),
+        "eager_over_graph": None if r["graph_ms"] is None else round(r["ms"] / r["graph_ms"], 3),
+        "value_tflops": round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 2),
+        "gemm_tflops_kernel_time": round(r["gemm_tflops"], 2),
+        "gemm_pct_mfma_peak": round(100 * r["gemm_tflops"] / PEAK_BF16_TFLOPS, 2),
+        "permutation_pct_hbm_peak": round(100 * r["perm_gbs"] / PEAK_HBM_GBS, 2),
+        "tokens_per_expert_min_max": [min(r["counts"]), max(r["counts"])],
+        "kernel_us": {n: round(v, 2) for n, v in r["kern"].items()},
+    }
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -508,47 +572,23 @@ def main():
     if args.fp32_gemm:
         fp32_gemm()
         return
-    torch.manual_seed(0)
-    m, xb, info = build_workload(args.config, device)
-    flops, counts, sel = gemm_flops(m, xb)
 
     if args.profile_steps:
+        torch.manual_seed(0)
+        m, xb, _info = build_workload(args.config, device)
         time_steps(m, xb, args.profile_steps, 1)
         print(json.dumps({"profile_steps": args.profile_steps, "config": args.config}))
         return
 
-    ms = time_steps(m, xb, args.steps, args.warmup)
+    r = measure(args.config, device, args.steps, args.warmup, args.kernel_steps, not args.no_graph)
+    m, xb, sel, info, counts, flops = r["m"], r["xb"], r["sel"], r["info"], r["counts"], r["flops"]
+    ms, kern, dom = r["ms"], r["kern"], r["dom"]
     value = flops / (ms * 1e-3) / 1e12
-    graph_ms = time_graph_steps(m, xb, args.steps, args.warmup) if args.graph else None
-    kern = kernel_breakdown(m, xb, args.kernel_steps)
-    gemm_names = [n for n in kern if n.startswith("gemm_")]
-    gemm_us = sum(kern[n] for n in gemm_names)
-    per_gemm_flops = flops / 6.0
-    gemm_tflops = flops / (gemm_us * 1e-6) / 1e12
-    dom = max(gemm_names, key=lambda n: kern[n])
-    achieved = per_gemm_flops / (kern[dom] * 1e-6) / 1e12
-
     d, sizes, k, T, _ = CONFIGS[args.config]
-    A = T * k
-    E = m.num_experts
-    widths = [w for c, w in sizes for _ in range(c)]
-    nw = sum(int(n) * w for n, w in zip(counts, widths))
-    dom_bytes = gemm_bytes(dom, A, T, d, nw, sum(widths))
-    ai = per_gemm_flops / dom_bytes
+    dom_bytes = gemm_bytes(dom, r["A"], T, d, r["nw"], r["W"])
+    ai = flops / 6.0 / dom_bytes
     ai_bound = min(PEAK_BF16_TFLOPS, ai * PEAK_HBM_GBS / 1e3)
-    # Permutation and routing bytes: each combine reads the k rows of every
-    # token and the row of each assignment and writes the token rows; the
-    # routing reads the ids (int32) and bf16 weights and writes bin_ids,
-    # indices and assignment_row per assignment and row_src, gather_map and
-    # the fp32 row weight per padded row (+ five E-long arrays).
-    P = sum(-(-int(n) // 64) * 64 for n in counts)
-    perm_bytes = {
-        "combine": 2 * A * d + 2 * T * d + 4 * A,
-        "gather_bwd_combine": 2 * A * d + 2 * T * d + 4 * A,
-        "route": 6 * A + 12 * A + 12 * P + 20 * E,
-    }
-    perm_us = sum(kern[n] for n in perm_bytes)
-    perm_gbs = sum(perm_bytes.values()) / (perm_us * 1e-6) / 1e9
+    achieved = r["achieved"]
 
     result = {
         "metric": "MoE fwd+bwd ms + grouped-GEMM TFLOP/s (% MFMA peak), 64 experts k=8 bf16",
@@ -569,17 +609,17 @@ def main():
                    "zipf_alpha": info.get("alpha"),
                    "tokens_per_expert_min_max": [min(counts), max(counts)]},
         "gemm_flops_per_step": flops,
-        "gemm_tflops_kernel_time": round(gemm_tflops, 2),
-        "gemm_pct_mfma_peak": round(100 * gemm_tflops / PEAK_BF16_TFLOPS, 2),
-        "permutation_gbs": round(perm_gbs, 1),
-        "permutation_pct_hbm_peak": round(100 * perm_gbs / PEAK_HBM_GBS, 2),
+        "gemm_tflops_kernel_time": round(r["gemm_tflops"], 2),
+        "gemm_pct_mfma_peak": round(100 * r["gemm_tflops"] / PEAK_BF16_TFLOPS, 2),
+        "permutation_gbs": round(r["perm_gbs"], 1),
+        "permutation_pct_hbm_peak": round(100 * r["perm_gbs"] / PEAK_HBM_GBS, 2),
         "permutation_scope": "both combines + routing (vmoe_route_counted; the per-tile "
                              "expert counts come out of the top-k launch, router_topk_us), "
                              "bytes and time",
         "routing_us": round(kern["route"], 2),
         "router_topk_us": round(kern.get("router_topk", 0.0), 2),
         "kernel_us": {n: round(v, 2) for n, v in kern.items()},
-        "graph_ms_per_step": None if graph_ms is None else round(graph_ms, 4),
+        "graph_ms_per_step": None if r["graph_ms"] is None else round(r["graph_ms"], 4),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
@@ -596,6 +636,17 @@ def main():
             "kind": "port", "ms_per_step": round(sec * 1e3, 1),
             "sample": f"full {args.config} step (fp32 eager per-expert-loop oracle, fwd+bwd), "
                       f"median of {args.cpu_iters} after 1 warmup, {cpu_model()}"}
+    del m, xb, sel, r
+    others = [c for c in args.other_configs.split(",") if c and c != args.config]
+    if others:
+        result["other_configs"] = {}
+        for name in others:
+            torch.cuda.empty_cache()
+            o = measure(name, device, min(args.steps, 20), min(args.warmup, 5),
+                        min(args.kernel_steps, 5), not args.no_graph)
+            result["other_configs"][name] = summary(name, o)
+            del o
+            print(f"# {name} done", file=sys.stderr, flush=True)
     print(json.dumps(result))
 
 
