@@ -47,6 +47,28 @@ def bf16_ulps(got: torch.Tensor, ref: torch.Tensor) -> torch.Tensor:
     return (line(got) - line(ref)).abs()
 
 
+def parity_stats(got: torch.Tensor, ref: torch.Tensor, mag: torch.Tensor) -> dict:
+    """ulp-level agreement of a bf16 result with an oracle that rounds at the
+    same points (ref, rounded to bf16 here): shares of elements bit-equal and
+    within 1 and 2 ulps, the largest ulp distance, and the largest
+    conditioned error (|d| - ulp(ref)) / (2^-8 * mag), mag the sum of the
+    magnitudes of the terms each element sums: an element whose terms agree
+    to one rounding each stays at or below 1 however much its sum cancels."""
+    r = ref.detach().cpu().float().to(torch.bfloat16)
+    g = got.detach().cpu().to(torch.bfloat16)
+    u = bf16_ulps(g, r)
+    n = max(u.numel(), 1)
+    rf = r.float()
+    # one bf16 ulp of |ref|: 2^(e - 7) for normal values, 2^-133 below
+    e = torch.frexp(rf.abs().clamp_min(2.0 ** -126))[1].to(torch.float32)
+    ulp = torch.pow(2.0, e - 8)
+    d = (g.float() - rf).abs()
+    cond = ((d - ulp).clamp_min(0) / (2.0 ** -8 * mag.detach().cpu().float()).clamp_min(1e-30))
+    return {"eq": float((u == 0).sum()) / n, "ulp1": float((u <= 1).sum()) / n,
+            "ulp2": float((u <= 2).sum()) / n, "max_ulp": int(u.max()) if u.numel() else 0,
+            "cond": float(cond.max()) if cond.numel() else 0.0}
+
+
 def bits_equal(got: torch.Tensor, ref: torch.Tensor) -> bool:
     g = got.detach().cpu().contiguous()
     r = ref.detach().cpu().to(g.dtype).contiguous()
