@@ -224,6 +224,39 @@ int vmoe_router_weight_bwd(const uint16_t* logits, int64_t ld_logits, int64_t nu
                            const uint16_t* grad_weights, int64_t ld_grad_weights,
                            uint16_t* grad_logits, int64_t ld_grad, vmoe_stream_t stream);
 
+/* fp32 forms of the router entry points for a float32 module (the
+ * reference's TritonMoEMLP runs in whatever dtype its parameters have; a
+ * float32 one has float32 logits, weights and logit gradients, moe.py:166-176,
+ * 253-257): the same kernels, arguments and limits, with logits, weights,
+ * f_i, z_loss, grad_weights and grad_logits as fp32. logsumexp and its square
+ * are not rounded (torch evaluates them in fp32 for fp32 logits) and
+ * f_i = tpe / sum tpe unrounded (moe.py:257 casts to x.dtype). */
+int vmoe_router_topk_f32(const float* logits, int64_t ld_logits, int64_t num_tokens,
+                         int32_t num_experts, int32_t top_k, int32_t normalize, float* weights,
+                         int32_t* selected_i32, int64_t* selected_i64, float* probs, float* lse,
+                         float* partial, size_t partial_floats, int32_t* num_partial_rows,
+                         vmoe_stream_t stream);
+int vmoe_router_topk_hist_f32(const float* logits, int64_t ld_logits, int64_t num_tokens,
+                              int32_t num_experts, int32_t top_k, int32_t normalize,
+                              float* weights, int32_t* selected_i32, int64_t* selected_i64,
+                              float* probs, float* lse, float* partial, size_t partial_floats,
+                              int32_t* num_partial_rows, void* route_workspace,
+                              size_t route_workspace_bytes, vmoe_stream_t stream);
+int vmoe_router_aux_f32(const float* partial, int32_t num_partial_rows, int64_t num_tokens,
+                        int32_t num_experts, const int32_t* tokens_per_expert, const float* coef,
+                        const float* widths_normalized, float* f_i, float* f_i_f32, float* p_i,
+                        float* z_loss, float* losses, vmoe_stream_t stream);
+int vmoe_router_aux_bwd_f32(const float* logits, int64_t ld_logits, int64_t num_tokens,
+                            int32_t num_experts, const float* lse, const float* f_i_f32,
+                            const float* coef, const float* widths_normalized,
+                            const float* grad_z, const float* grad_lb, const float* grad_cl,
+                            float* grad_logits, int64_t ld_grad, vmoe_stream_t stream);
+int vmoe_router_weight_bwd_f32(const float* logits, int64_t ld_logits, int64_t num_tokens,
+                               int32_t num_experts, int32_t top_k, int32_t normalize,
+                               const int32_t* selected_i32, const int64_t* selected_i64,
+                               const float* grad_weights, int64_t ld_grad_weights,
+                               float* grad_logits, int64_t ld_grad, vmoe_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Token permutation (bf16).
  * vmoe_gather: out[r] = x[row_src[r] / top_k] (times weights[row_src[r]] when
@@ -306,6 +339,34 @@ int vmoe_routing_weight_grad_direct(const uint16_t* grad_y, int64_t ldgy, int64_
                                     int32_t top_k, const int32_t* eto, const int32_t* ewo,
                                     const int32_t* widths, int32_t num_experts, int64_t hidden,
                                     int64_t rows, uint16_t* grad_weights, vmoe_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Token permutation in fp32, for a float32 module (the reference's gather and
+ * scatter kernels are dtype-generic; gather.py:63-115, 177-218,
+ * scatter.py:61-69, 133, 141-189): arguments as in the bf16 forms, all rows
+ * fp32, every product and sum in fp32 (slots summed in ascending j).
+ * vmoe_combine_f32: out[t] = sum_j y[row(t, j)] * weights[t*k+j] (weights
+ *   NULL: 1), the reference's padded_scatter in fp32.
+ * vmoe_gather_f32: out[r] = x[row_src[r] / top_k] * weights[row_src[r]]
+ *   (weights NULL: 1), zeros where row_src[r] < 0; ldx = 0 reads one row
+ *   for every token (a broadcast output gradient).
+ * vmoe_combine_weight_grad_f32: grad_weights[t*k+j] = sum_c grad[t, c] *
+ *   y[row(t, j), c], 0 for slots with no row (opt-in; the reference returns
+ *   None, scatter.py:176).
+ * 4-float vectors where row starts are 16-byte aligned, single floats
+ * otherwise; no alignment rule.
+ * ---------------------------------------------------------------------- */
+int vmoe_combine_f32(const float* y, int64_t y_rows, int64_t ldy, const int32_t* assignment_row,
+                     const float* weights, int32_t top_k, float* out, int64_t ldo,
+                     int64_t num_tokens, int64_t hidden, vmoe_stream_t stream);
+int vmoe_gather_f32(const float* x, int64_t x_rows, int64_t ldx, const int32_t* row_src,
+                    int32_t top_k, const float* weights, int64_t num_weights, float* out,
+                    int64_t ldo, int64_t num_rows, const int32_t* num_rows_dev, int64_t hidden,
+                    vmoe_stream_t stream);
+int vmoe_combine_weight_grad_f32(const float* grad, int64_t ldg, const float* y, int64_t y_rows,
+                                 int64_t ldy, const int32_t* assignment_row, int32_t top_k,
+                                 float* grad_weights, int64_t num_tokens, int64_t hidden,
+                                 vmoe_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Variable-width grouped GEMMs (bf16 in, fp32 MFMA accumulate, bf16 out).

@@ -83,6 +83,24 @@ def test_argument_checks_return_invalid_arg():
     assert f(*args[:11], 0, *args[12:]) == _lib.ERR_INVALID_ARG
     assert f(*args[:6], None, *args[7:]) == _lib.ERR_INVALID_ARG
     assert f(*args[:10], 0, *args[11:]) == _lib.OK  # no assignments: nothing to do
+    # fp32 permutation: bad top_k, short ldo, missing output
+    assert lib.vmoe_combine_f32(1, 8, 16, 1, None, 0, 1, 16, 4, 16,
+                                None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_combine_f32(1, 8, 16, 1, None, 2, 1, 8, 4, 16, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_gather_f32(1, 8, 16, 1, 2, None, 0, None, 16, 4, None, 16,
+                               None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_combine_weight_grad_f32(1, 16, 1, 8, 8, 1, 2, 1, 4, 16,
+                                            None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_combine_f32(None, 0, 16, None, None, 2, None, 16, 0, 16, None) == _lib.OK
+    # fp32 router: k > E invalid, more than 2048 experts unsupported; aux needs outputs
+    assert lib.vmoe_router_topk_f32(1, 8, 4, 8, 9, 1, 1, 1, None, None, 1, 1, 1 << 20, None,
+                                    None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_router_topk_f32(1, 4096, 4, 4096, 8, 1, 1, 1, None, None, 1, 1, 1 << 20,
+                                    None, None) == _lib.ERR_UNSUPPORTED
+    assert lib.vmoe_router_aux_f32(1, 1, 4, 8, 1, 1, 1, None, 1, 1, 1, 1,
+                                   None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_router_weight_bwd_f32(1, 8, 4, 8, 2, 1, 1, 1, 1, 2, 1, 8,
+                                          None) == _lib.ERR_INVALID_ARG
     # its logit gradient: both or neither index arrays, k above one wave
     assert lib.vmoe_router_weight_bwd(1, 8, 4, 8, 2, 1, 1, 1, 1, 2, 1, 8,
                                       None) == _lib.ERR_INVALID_ARG

@@ -240,3 +240,56 @@ def test_padded_scatter_weight_grad_opt_in(device):
         assert wd.grad is not None and wd.grad.dtype == torch.bfloat16
         assert bool(((wd.grad.cpu().double() - ref).abs() <= tol).all())
         assert bits_equal(yd.grad, _ref_gather(G, maps, k, wts))
+
+
+@pytest.mark.parametrize("T,d,E,k,b", [(128, 128, 4, 2, 128), (1024, 256, 8, 2, 128),
+                                       (300, 100, 5, 2, 8), (257, 2058, 7, 3, 64)])
+def test_f32_gather_combine_and_weight_grad(T, d, E, k, b, device):
+    """The fp32 permutation (vmoe_gather_f32, vmoe_combine_f32,
+    vmoe_combine_weight_grad_f32) through the public API in float32:
+    gathers are exact copies / single fp32 products, the combine is the fp32
+    sum in slot order (bit-equal to the same sum on the host), and the
+    weight gradient is within fp32 summation order of float64. Odd d takes
+    the scalar path."""
+    x, sel, wts, r, maps = _setup(T, d, E, k, b, device)
+    x32 = x.float() + torch.randn(T, d, generator=torch.Generator().manual_seed(1)) * 1e-3
+    w32 = wts.float() * (1 + 1e-3 * torch.rand(T, k, generator=torch.Generator().manual_seed(2)))
+    dev = lambda a: torch.as_tensor(a).to(device)  # noqa: E731
+    P = int(r["padded_bins"][-1])
+    rs = torch.from_numpy(maps["row_src"]).long()
+    ok = rs >= 0
+    got = padded_gather(x32.to(device), dev(r["indices"]), dev(r["bin_ids"]), dev(r["bins"]),
+                        dev(r["padded_bins"]), k)
+    ref = torch.zeros(P, d)
+    ref[ok] = x32[rs[ok] // k]
+    assert got.dtype == torch.float32 and torch.equal(got.cpu(), ref)
+    gw = gather_rows(x32.to(device), dev(maps["row_src"]).int(), k, P,
+                     weights=w32.reshape(-1).to(device))
+    refw = torch.zeros(P, d)
+    refw[ok] = x32[rs[ok] // k] * w32.reshape(-1)[rs[ok]][:, None]
+    assert torch.equal(gw.cpu(), refw)
+    # combine: sum over slots in ascending j, fp32, with and without weights
+    y = torch.randn(P, d, generator=torch.Generator().manual_seed(3))
+    ar = torch.from_numpy(maps["assignment_row"]).long().view(T, k)
+    for w in (None, w32):
+        out = combine_rows(y.to(device), dev(maps["assignment_row"]).int(), k, T,
+                           weights=None if w is None else w.reshape(-1).to(device))
+        ref = torch.zeros(T, d)
+        for j in range(k):
+            rows = ar[:, j]
+            m = rows >= 0
+            slot = torch.zeros(T, d)
+            slot[m] = y[rows[m]] * (1.0 if w is None else w[m, j][:, None])
+            ref = ref + slot
+        assert torch.equal(out.cpu(), ref), "fp32 combine"
+    # weight gradient of the weighted fp32 scatter (opt-in)
+    G = torch.randn(T, d, generator=torch.Generator().manual_seed(4))
+    yy = y.to(device).requires_grad_(False)
+    ws = w32.reshape(-1).to(device).requires_grad_(True)
+    out = padded_scatter_autograd(yy, dev(r["indices"]), dev(r["bin_ids"]), ws, dev(r["bins"]),
+                                  dev(r["padded_bins"]), k, weight_grad=True)
+    out.backward(G.to(device))
+    refg = eager.combine_weight_grad(G, y, maps["assignment_row"], k, T)
+    assert ws.grad.dtype == torch.float32
+    mag = eager.combine_weight_grad(G.abs(), y.abs(), maps["assignment_row"], k, T)
+    assert ((ws.grad.cpu().double() - refg).abs() <= 1e-6 * mag + 1e-30).all()

@@ -21,7 +21,8 @@ REPO = HERE.parent
 CSRC = HERE / "csrc"
 OUT = HERE / "triton_moe" / "libvmoe.so"
 OBJ = HERE / "_build"
-SOURCES = ["route.hip", "permute.hip", "gemm.hip", "gemm_f32.hip", "router.hip", "capi.hip"]
+SOURCES = ["route.hip", "permute.hip", "permute_f32.hip", "gemm.hip", "gemm_f32.hip", "router.hip",
+           "capi.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -112,6 +112,27 @@ __device__ __forceinline__ float wave_max_f32(float v) {
 // sigmoid as torch evaluates it for fp32 (1 / (1 + exp(-x)), precise exp).
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Element type of the logits, the routing weights and the logit gradients:
+// bf16 bit patterns (F32 = false, the module in bf16) or fp32 (the module in
+// fp32). torch evaluates logsumexp and its square in the logits' dtype, so
+// for bf16 each is rounded to bf16 once; for fp32 they stay fp32.
+template <bool F32>
+struct RtElt;
+template <>
+struct RtElt<false> {
+  using T = uint16_t;
+  __device__ static float ld(const T* p) { return bf16_to_f32(*p); }
+  __device__ static T cvt(float v) { return (T)f32_to_bf16(v); }
+  __device__ static float rnd(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+};
+template <>
+struct RtElt<true> {
+  using T = float;
+  __device__ static float ld(const T* p) { return *p; }
+  __device__ static T cvt(float v) { return v; }
+  __device__ static float rnd(float v) { return v; }
+};
+
 // ---- torch.topk's output order and torch.sum's order, for one token ----
 //
 // The reference takes torch.topk(sigmoid(L.float()), k) (moe.py:168-170).
@@ -256,10 +277,10 @@ __device__ __forceinline__ void topk_order_lanes(float& my_v, int& my_e, int k, 
 // Block b handles tokens [b * per, min(T, (b + 1) * per)); its waves take
 // batches of TB consecutive tokens in turn. partial[b][e] = sum of p[t][e]
 // over the block's tokens (e < E); partial[b][E] = sum of bf16(bf16(lse_t)^2).
-template <int VPL>
+template <int VPL, bool F32>
 __global__ __launch_bounds__(topk_threads(VPL)) void router_topk_kernel(
-    const uint16_t* __restrict__ logits, int64_t ldl, int64_t T, int E, int k, int norm,
-    uint16_t* __restrict__ weights, int32_t* __restrict__ selected32,
+    const typename RtElt<F32>::T* __restrict__ logits, int64_t ldl, int64_t T, int E, int k,
+    int norm, typename RtElt<F32>::T* __restrict__ weights, int32_t* __restrict__ selected32,
     int64_t* __restrict__ selected64, float* __restrict__ probs, float* __restrict__ lse_out,
     float* __restrict__ partial, int64_t per) {
   constexpr int TB = TokBatch<VPL>::value;
@@ -278,7 +299,7 @@ __global__ __launch_bounds__(topk_threads(VPL)) void router_topk_kernel(
 #pragma unroll
       for (int v = 0; v < VPL; ++v) {
         const int e = lane + v * kWave;
-        lgb[u][v] = (tb + u < t_end && e < E) ? bf16_to_f32(logits[(tb + u) * ldl + e])
+        lgb[u][v] = (tb + u < t_end && e < E) ? RtElt<F32>::ld(logits + (tb + u) * ldl + e)
                                                : -INFINITY;
       }
 #pragma unroll
@@ -302,9 +323,9 @@ __global__ __launch_bounds__(topk_threads(VPL)) void router_topk_kernel(
       for (int v = 0; v < VPL; ++v)
         if (lane + v * kWave < E) se += expf(lgb[u][v] - m);
       se = wave_sum_f32(se);
-      const float lse = bf16_to_f32(f32_to_bf16(logf(se) + m));
+      const float lse = RtElt<F32>::rnd(logf(se) + m);
       if (lse_out && lane == 0) lse_out[t] = lse;
-      zsum += bf16_to_f32(f32_to_bf16(lse * lse));
+      zsum += RtElt<F32>::rnd(lse * lse);
       // top-k: k rounds of a wave arg-max; keys order by value, then by the
       // lower expert index. p >= 0, so its bits order like its value.
       uint32_t taken = 0;
@@ -347,7 +368,7 @@ __global__ __launch_bounds__(topk_threads(VPL)) void router_topk_kernel(
       }  // k > 32: a stable sort, the selection order
       if (lane < k) {
         const float wv_ = norm ? my_v / (vsum + 1e-20f) : my_v;
-        weights[t * k + lane] = (uint16_t)f32_to_bf16(wv_);
+        weights[t * k + lane] = RtElt<F32>::cvt(wv_);
         if (selected32) selected32[t * k + lane] = my_e;
         if (selected64) selected64[t * k + lane] = my_e;
       }
@@ -396,10 +417,10 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-template <int G>
+template <int G, bool F32>
 __global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
-    const uint16_t* __restrict__ logits, int64_t ldl, int64_t T, int E, int k, int norm,
-    uint16_t* __restrict__ weights, int32_t* __restrict__ selected32,
+    const typename RtElt<F32>::T* __restrict__ logits, int64_t ldl, int64_t T, int E, int k,
+    int norm, typename RtElt<F32>::T* __restrict__ weights, int32_t* __restrict__ selected32,
     int64_t* __restrict__ selected64, float* __restrict__ probs, float* __restrict__ lse_out,
     float* __restrict__ partial, int64_t per, int32_t* __restrict__ hist_counts,
     int32_t* __restrict__ hist_bad, int hist_cols) {
@@ -427,12 +448,19 @@ __global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
     const bool ok = t < t_end && part_ok;
     float x[8];
     if (ok) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(logits + t * ldl + e0);
-      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+      if constexpr (F32) {
+        const float4 a = *reinterpret_cast<const float4*>(logits + t * ldl + e0);
+        const float4 b = *reinterpret_cast<const float4*>(logits + t * ldl + e0 + 4);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+      } else {
+        const uint4 raw = *reinterpret_cast<const uint4*>(logits + t * ldl + e0);
+        const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        x[2 * v] = __uint_as_float(w4[v] << 16);
-        x[2 * v + 1] = __uint_as_float(w4[v] & 0xFFFF0000u);
+        for (int v = 0; v < 4; ++v) {
+          x[2 * v] = __uint_as_float(w4[v] << 16);
+          x[2 * v + 1] = __uint_as_float(w4[v] & 0xFFFF0000u);
+        }
       }
     } else {
 #pragma unroll
@@ -462,11 +490,11 @@ __global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
     }
 #pragma unroll
     for (int st = 1; st < G; st <<= 1) se += __shfl_xor(se, st, kWave);
-    const float lse = bf16_to_f32(f32_to_bf16(logf(se) + m));
+    const float lse = RtElt<F32>::rnd(logf(se) + m);
     const bool tok = t < t_end;
     if (tok && r == 0) {
       if (lse_out) lse_out[t] = lse;
-      zsum += bf16_to_f32(f32_to_bf16(lse * lse));
+      zsum += RtElt<F32>::rnd(lse * lse);
     }
     // keys: value bits, then the lower expert index (p >= 0 orders like its
     // bits); 0 for no expert, below every real key.
@@ -507,7 +535,7 @@ __global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
       for (int j = 0; j < 8; ++j) {
         if (j < k && (j & (G - 1)) == r) {
           const float v = __uint_as_float(pb[j]);
-          weights[t * k + j] = (uint16_t)f32_to_bf16(norm ? v / (vsum + 1e-20f) : v);
+          weights[t * k + j] = RtElt<F32>::cvt(norm ? v / (vsum + 1e-20f) : v);
           if (selected32) selected32[t * k + j] = ex[j];
           if (selected64) selected64[t * k + j] = ex[j];
           if (hist_counts) atomicAdd(&thist[ex[j]], 1);
@@ -548,11 +576,13 @@ __global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
 // loss. Columns go 64 at a time (one per lane); wave w adds rows w, w + 16, ...
 // with 8 independent loads in flight, then the 16 wave sums are added in
 // wave order.
+template <bool F32>
 __global__ __launch_bounds__(kAuxThreads) void router_aux_kernel(
     const float* __restrict__ partial, int nblk, int64_t T, int E,
     const int32_t* __restrict__ tokens_per_expert, const float* __restrict__ coef,
-    const float* __restrict__ wn, uint16_t* __restrict__ f_i, float* __restrict__ f_i32,
-    float* __restrict__ p_i, uint16_t* __restrict__ z_out, float* __restrict__ out_scalars) {
+    const float* __restrict__ wn, typename RtElt<F32>::T* __restrict__ f_i,
+    float* __restrict__ f_i32, float* __restrict__ p_i, typename RtElt<F32>::T* __restrict__ z_out,
+    float* __restrict__ out_scalars) {
   __shared__ float wsum[kAuxWaves][kWave];
   __shared__ long long sh_cnt[kAuxWaves];
   __shared__ float sh_z;
@@ -596,9 +626,9 @@ __global__ __launch_bounds__(kAuxThreads) void router_aux_kernel(
         sh_z = col;
       } else {
         const float pe = col * invT;
-        // f_i = (tpe.float() / tpe.sum()).to(bf16)
-        const float fe = bf16_to_f32(f32_to_bf16((float)tokens_per_expert[c] / total));
-        f_i[c] = (uint16_t)f32_to_bf16(fe);
+        // f_i = (tpe.float() / tpe.sum()).to(dtype)
+        const float fe = RtElt<F32>::rnd((float)tokens_per_expert[c] / total);
+        f_i[c] = RtElt<F32>::cvt(fe);
         f_i32[c] = fe;
         p_i[c] = pe;
         lb += coef[c] * fe * pe;
@@ -614,7 +644,7 @@ __global__ __launch_bounds__(kAuxThreads) void router_aux_kernel(
       cl += __shfl_xor(cl, off, kWave);
     }
     if (lane == 0) {
-      *z_out = (uint16_t)f32_to_bf16(sh_z * invT);
+      *z_out = RtElt<F32>::cvt(sh_z * invT);
       out_scalars[0] = lb;
       out_scalars[1] = cl;
     }
@@ -622,13 +652,13 @@ __global__ __launch_bounds__(kAuxThreads) void router_aux_kernel(
 }
 
 // dL for every logit (one wave per token).
-template <int VPL>
+template <int VPL, bool F32>
 __global__ __launch_bounds__(kRtThreads) void router_aux_bwd_kernel(
-    const uint16_t* __restrict__ logits, int64_t ldl, int64_t T, int E,
+    const typename RtElt<F32>::T* __restrict__ logits, int64_t ldl, int64_t T, int E,
     const float* __restrict__ lse, const float* __restrict__ f_i32,
     const float* __restrict__ coef, const float* __restrict__ wn,
     const float* __restrict__ g_z, const float* __restrict__ g_lb,
-    const float* __restrict__ g_cl, uint16_t* __restrict__ grad, int64_t ldg) {
+    const float* __restrict__ g_cl, typename RtElt<F32>::T* __restrict__ grad, int64_t ldg) {
   const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
   const float invT = 1.0f / (float)T;
   const float gz = g_z ? *g_z : 0.0f, glb = g_lb ? *g_lb : 0.0f, gcl = g_cl ? *g_cl : 0.0f;
@@ -646,10 +676,10 @@ __global__ __launch_bounds__(kRtThreads) void router_aux_bwd_kernel(
     for (int v = 0; v < VPL; ++v) {
       const int e = lane + v * kWave;
       if (e >= E) continue;
-      const float x = bf16_to_f32(logits[t * ldl + e]);
+      const float x = RtElt<F32>::ld(logits + t * ldl + e);
       const float p = sigmoidf(x);
       const float d = zt * expf(x - l) + ce[v] * p * (1.0f - p);
-      grad[t * ldg + e] = (uint16_t)f32_to_bf16(d);
+      grad[t * ldg + e] = RtElt<F32>::cvt(d);
     }
   }
 }
@@ -663,11 +693,12 @@ __global__ __launch_bounds__(kRtThreads) void router_aux_bwd_kernel(
 // and grad[t, e] = bf16(dp_j p_j (1 - p_j)) for e = s_j, 0 for the other
 // experts (torch.topk's backward scatters into zeros; sigmoid's is
 // g y (1 - y)). The sums run in the DPP order of wave_sum_f32.
-template <int VPL>
+template <int VPL, bool F32>
 __global__ __launch_bounds__(kRtThreads) void router_weight_bwd_kernel(
-    const uint16_t* __restrict__ logits, int64_t ldl, int64_t T, int E, int k, int norm,
-    const int32_t* __restrict__ sel32, const int64_t* __restrict__ sel64,
-    const uint16_t* __restrict__ gw, int64_t ldgw, uint16_t* __restrict__ grad, int64_t ldg) {
+    const typename RtElt<F32>::T* __restrict__ logits, int64_t ldl, int64_t T, int E, int k,
+    int norm, const int32_t* __restrict__ sel32, const int64_t* __restrict__ sel64,
+    const typename RtElt<F32>::T* __restrict__ gw, int64_t ldgw,
+    typename RtElt<F32>::T* __restrict__ grad, int64_t ldg) {
   const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
   for (int64_t t = (int64_t)blockIdx.x * kRtWaves + wv; t < T;
        t += (int64_t)gridDim.x * kRtWaves) {
@@ -676,8 +707,8 @@ __global__ __launch_bounds__(kRtThreads) void router_weight_bwd_kernel(
     if (lane < k) {
       e = sel32 ? sel32[t * k + lane] : (int)sel64[t * k + lane];
       if (e >= 0 && e < E) {
-        p = sigmoidf(bf16_to_f32(logits[t * ldl + e]));
-        g = bf16_to_f32(gw[t * ldgw + lane]);
+        p = sigmoidf(RtElt<F32>::ld(logits + t * ldl + e));
+        g = RtElt<F32>::ld(gw + t * ldgw + lane);
       } else {
         e = -1;
       }
@@ -702,7 +733,7 @@ __global__ __launch_bounds__(kRtThreads) void router_weight_bwd_kernel(
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
       const int ee = lane + v * kWave;
-      if (ee < E) grad[t * ldg + ee] = (uint16_t)f32_to_bf16(val[v]);
+      if (ee < E) grad[t * ldg + ee] = RtElt<F32>::cvt(val[v]);
     }
   }
 }
@@ -748,14 +779,17 @@ inline int router_hist_blocks(int64_t T, int E, int k) {
 }
 
 // The grouped top-k launch for G lanes per token (hist_counts nullable).
-int topk_group_launch(int G, int nblk, hipStream_t s, const uint16_t* logits, int64_t ld,
-                      int64_t T, int E, int k, int norm, uint16_t* weights, int32_t* sel32,
-                      int64_t* sel64, float* probs, float* lse, float* partial, int64_t per,
+template <bool F32>
+int topk_group_launch(int G, int nblk, hipStream_t s, const typename RtElt<F32>::T* logits,
+                      int64_t ld, int64_t T, int E, int k, int norm,
+                      typename RtElt<F32>::T* weights, int32_t* sel32, int64_t* sel64,
+                      float* probs, float* lse, float* partial, int64_t per,
                       int32_t* hist_counts, int32_t* hist_bad) {
   switch (G) {
 #define VMOE_RT_GRP(GG)                                                                        \
   case GG:                                                                                     \
-    hipLaunchKernelGGL(router_topk_group_kernel<GG>, dim3(nblk), dim3(kGrpThreads), 0, s,       \
+    hipLaunchKernelGGL((router_topk_group_kernel<GG, F32>), dim3(nblk), dim3(kGrpThreads), 0, \
+                       s,                                                                      \
                        logits, ld, T, E, k, norm, weights, sel32, sel64, probs, lse, partial,   \
                        per, hist_counts, hist_bad, nblk);                                      \
     break;
@@ -773,7 +807,7 @@ int topk_group_launch(int G, int nblk, hipStream_t s, const uint16_t* logits, in
 }
 
 // Shapes and layouts the grouped top-k kernel reads (16-byte logits rows).
-bool group_kernel_ok(const uint16_t* logits, int64_t ld, int E, int k, const float* probs) {
+bool group_kernel_ok(const void* logits, int64_t ld, int E, int k, const float* probs) {
   return E % 8 == 0 && E <= kGrpMaxExperts && k <= 8 && ld % 8 == 0 &&
          reinterpret_cast<uintptr_t>(logits) % 16 == 0 &&
          (!probs || reinterpret_cast<uintptr_t>(probs) % 16 == 0);
@@ -907,11 +941,12 @@ extern "C" size_t vmoe_router_partial_floats(int64_t num_tokens, int32_t num_exp
   return (size_t)router_blocks(num_tokens, num_experts) * (size_t)(num_experts + 1);
 }
 
-extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
-                                int32_t num_experts, int32_t top_k, int32_t normalize,
-                                uint16_t* weights, int32_t* selected_i32, int64_t* selected_i64,
-                                float* probs, float* lse, float* partial, size_t partial_floats,
-                                int32_t* num_partial_rows, vmoe_stream_t stream) {
+template <bool F32>
+int router_topk_impl(const typename RtElt<F32>::T* logits, int64_t ld_logits, int64_t num_tokens,
+                     int32_t num_experts, int32_t top_k, int32_t normalize,
+                     typename RtElt<F32>::T* weights, int32_t* selected_i32,
+                     int64_t* selected_i64, float* probs, float* lse, float* partial,
+                     size_t partial_floats, int32_t* num_partial_rows, vmoe_stream_t stream) {
   if (num_tokens < 0 || num_experts <= 0 || top_k <= 0 || top_k > num_experts ||
       ld_logits < num_experts)
     return VMOE_ERR_INVALID_ARG;
@@ -925,18 +960,18 @@ extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64
   const int64_t per = (num_tokens + nblk - 1) / nblk;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (group_kernel_ok(logits, ld_logits, num_experts, top_k, probs))
-    return topk_group_launch(group_size(num_experts), nblk, s, logits, ld_logits, num_tokens,
-                             num_experts, top_k, normalize, weights, selected_i32, selected_i64,
-                             probs, lse, partial, per, nullptr, nullptr);
+    return topk_group_launch<F32>(group_size(num_experts), nblk, s, logits, ld_logits,
+                                  num_tokens, num_experts, top_k, normalize, weights,
+                                  selected_i32, selected_i64, probs, lse, partial, per, nullptr,
+                                  nullptr);
   const int vpl = vpl_of(num_experts);
   const size_t lds = sizeof(float) * (topk_threads(vpl) / kWave) * (num_experts + 1);
   switch (vpl) {
 #define VMOE_RT_CASE(V)                                                                      \
   case V:                                                                                    \
-    hipLaunchKernelGGL(router_topk_kernel<V>, dim3(nblk), dim3(topk_threads(V)), lds, s,      \
-                       logits,                                                                \
-                       ld_logits, num_tokens, num_experts, top_k, normalize, weights,         \
-                       selected_i32, selected_i64, probs, lse, partial, per);                \
+    hipLaunchKernelGGL((router_topk_kernel<V, F32>), dim3(nblk), dim3(topk_threads(V)), lds, \
+                       s, logits, ld_logits, num_tokens, num_experts, top_k, normalize,       \
+                       weights, selected_i32, selected_i64, probs, lse, partial, per);        \
     break;
     VMOE_RT_CASE(1)
     VMOE_RT_CASE(2)
@@ -952,18 +987,14 @@ extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64
   return VMOE_OK;
 }
 
-extern "C" int vmoe_router_topk_hist_blocks(int64_t num_tokens, int32_t num_experts,
-                                            int32_t top_k) {
-  return router_hist_blocks(num_tokens, num_experts, top_k);
-}
-
-extern "C" int vmoe_router_topk_hist(const uint16_t* logits, int64_t ld_logits,
-                                     int64_t num_tokens, int32_t num_experts, int32_t top_k,
-                                     int32_t normalize, uint16_t* weights, int32_t* selected_i32,
-                                     int64_t* selected_i64, float* probs, float* lse,
-                                     float* partial, size_t partial_floats,
-                                     int32_t* num_partial_rows, void* route_workspace,
-                                     size_t route_workspace_bytes, vmoe_stream_t stream) {
+template <bool F32>
+int router_topk_hist_impl(const typename RtElt<F32>::T* logits, int64_t ld_logits,
+                          int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                          int32_t normalize, typename RtElt<F32>::T* weights,
+                          int32_t* selected_i32, int64_t* selected_i64, float* probs, float* lse,
+                          float* partial, size_t partial_floats, int32_t* num_partial_rows,
+                          void* route_workspace, size_t route_workspace_bytes,
+                          vmoe_stream_t stream) {
   if (num_tokens < 0 || num_experts <= 0 || top_k <= 0 || top_k > num_experts ||
       ld_logits < num_experts)
     return VMOE_ERR_INVALID_ARG;
@@ -980,37 +1011,38 @@ extern "C" int vmoe_router_topk_hist(const uint16_t* logits, int64_t ld_logits,
   // counts [E][nblk] (one column per workgroup), then a bad-id flag per column
   const int S = route_hist_split(num_tokens, num_experts, top_k);
   int32_t* counts = static_cast<int32_t*>(route_workspace);
-  return topk_group_launch(group_size(num_experts), nblk, reinterpret_cast<hipStream_t>(stream),
-                           logits, ld_logits, num_tokens, num_experts, top_k, normalize, weights,
-                           selected_i32, selected_i64, probs, lse, partial,
-                           kRouteTile / (top_k * S), counts,
-                           counts + (int64_t)num_experts * nblk);
+  return topk_group_launch<F32>(group_size(num_experts), nblk,
+                                reinterpret_cast<hipStream_t>(stream), logits, ld_logits,
+                                num_tokens, num_experts, top_k, normalize, weights, selected_i32,
+                                selected_i64, probs, lse, partial, kRouteTile / (top_k * S),
+                                counts, counts + (int64_t)num_experts * nblk);
 }
 
-extern "C" int vmoe_router_aux(const float* partial, int32_t num_partial_rows,
-                               int64_t num_tokens, int32_t num_experts,
-                               const int32_t* tokens_per_expert, const float* coef,
-                               const float* widths_normalized, uint16_t* f_i, float* f_i_f32,
-                               float* p_i, uint16_t* z_loss, float* losses,
-                               vmoe_stream_t stream) {
+template <bool F32>
+int router_aux_impl(const float* partial, int32_t num_partial_rows, int64_t num_tokens,
+                    int32_t num_experts, const int32_t* tokens_per_expert, const float* coef,
+                    const float* widths_normalized, typename RtElt<F32>::T* f_i, float* f_i_f32,
+                    float* p_i, typename RtElt<F32>::T* z_loss, float* losses,
+                    vmoe_stream_t stream) {
   if (num_partial_rows <= 0 || num_tokens < 0 || num_experts <= 0) return VMOE_ERR_INVALID_ARG;
   if (!partial || !tokens_per_expert || !coef || !widths_normalized || !f_i || !f_i_f32 ||
       !p_i || !z_loss || !losses)
     return VMOE_ERR_INVALID_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(router_aux_kernel, dim3(1), dim3(kAuxThreads), 0, s, partial,
+  hipLaunchKernelGGL(router_aux_kernel<F32>, dim3(1), dim3(kAuxThreads), 0, s, partial,
                      num_partial_rows, num_tokens, num_experts, tokens_per_expert, coef,
                      widths_normalized, f_i, f_i_f32, p_i, z_loss, losses);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }
 
-extern "C" int vmoe_router_aux_bwd(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
-                                   int32_t num_experts, const float* lse, const float* f_i_f32,
-                                   const float* coef, const float* widths_normalized,
-                                   const float* grad_z, const float* grad_lb,
-                                   const float* grad_cl, uint16_t* grad_logits, int64_t ld_grad,
-                                   vmoe_stream_t stream) {
+template <bool F32>
+int router_aux_bwd_impl(const typename RtElt<F32>::T* logits, int64_t ld_logits,
+                        int64_t num_tokens, int32_t num_experts, const float* lse,
+                        const float* f_i_f32, const float* coef, const float* widths_normalized,
+                        const float* grad_z, const float* grad_lb, const float* grad_cl,
+                        typename RtElt<F32>::T* grad_logits, int64_t ld_grad,
+                        vmoe_stream_t stream) {
   if (num_tokens < 0 || num_experts <= 0 || ld_logits < num_experts || ld_grad < num_experts)
     return VMOE_ERR_INVALID_ARG;
   if (num_experts > kRtMaxExperts) return VMOE_ERR_UNSUPPORTED;
@@ -1022,8 +1054,8 @@ extern "C" int vmoe_router_aux_bwd(const uint16_t* logits, int64_t ld_logits, in
   switch (vpl_of(num_experts)) {
 #define VMOE_RB_CASE(V)                                                                       \
   case V:                                                                                     \
-    hipLaunchKernelGGL(router_aux_bwd_kernel<V>, dim3((unsigned)g), dim3(kRtThreads), 0, s,   \
-                       logits, ld_logits, num_tokens, num_experts, lse, f_i_f32, coef,         \
+    hipLaunchKernelGGL((router_aux_bwd_kernel<V, F32>), dim3((unsigned)g), dim3(kRtThreads),   \
+                       0, s, logits, ld_logits, num_tokens, num_experts, lse, f_i_f32, coef,   \
                        widths_normalized, grad_z, grad_lb, grad_cl, grad_logits, ld_grad);    \
     break;
     VMOE_RB_CASE(1)
@@ -1040,12 +1072,14 @@ extern "C" int vmoe_router_aux_bwd(const uint16_t* logits, int64_t ld_logits, in
   return VMOE_OK;
 }
 
-extern "C" int vmoe_router_weight_bwd(const uint16_t* logits, int64_t ld_logits,
-                                      int64_t num_tokens, int32_t num_experts, int32_t top_k,
-                                      int32_t normalize, const int32_t* selected,
-                                      const int64_t* selected_i64, const uint16_t* grad_weights,
-                                      int64_t ld_grad_weights, uint16_t* grad_logits,
-                                      int64_t ld_grad, vmoe_stream_t stream) {
+template <bool F32>
+int router_weight_bwd_impl(const typename RtElt<F32>::T* logits, int64_t ld_logits,
+                           int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                           int32_t normalize, const int32_t* selected,
+                           const int64_t* selected_i64,
+                           const typename RtElt<F32>::T* grad_weights, int64_t ld_grad_weights,
+                           typename RtElt<F32>::T* grad_logits, int64_t ld_grad,
+                           vmoe_stream_t stream) {
   if (num_tokens < 0 || num_experts <= 0 || top_k <= 0 || top_k > num_experts ||
       ld_logits < num_experts || ld_grad < num_experts || ld_grad_weights < top_k)
     return VMOE_ERR_INVALID_ARG;
@@ -1058,10 +1092,10 @@ extern "C" int vmoe_router_weight_bwd(const uint16_t* logits, int64_t ld_logits,
   switch (vpl_of(num_experts)) {
 #define VMOE_RW_CASE(V)                                                                      \
   case V:                                                                                    \
-    hipLaunchKernelGGL(router_weight_bwd_kernel<V>, dim3((unsigned)g), dim3(kRtThreads), 0,  \
-                       s, logits, ld_logits, num_tokens, num_experts, top_k, normalize,       \
-                       selected, selected_i64, grad_weights, ld_grad_weights, grad_logits,    \
-                       ld_grad);                                                              \
+    hipLaunchKernelGGL((router_weight_bwd_kernel<V, F32>), dim3((unsigned)g),                 \
+                       dim3(kRtThreads), 0, s, logits, ld_logits, num_tokens, num_experts,    \
+                       top_k, normalize, selected, selected_i64, grad_weights,                \
+                       ld_grad_weights, grad_logits, ld_grad);                                \
     break;
     VMOE_RW_CASE(1)
     VMOE_RW_CASE(2)
@@ -1075,6 +1109,126 @@ extern "C" int vmoe_router_weight_bwd(const uint16_t* logits, int64_t ld_logits,
   }
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
+}
+
+extern "C" int vmoe_router_topk(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
+                                int32_t num_experts, int32_t top_k, int32_t normalize,
+                                uint16_t* weights, int32_t* selected_i32, int64_t* selected_i64,
+                                float* probs, float* lse, float* partial, size_t partial_floats,
+                                int32_t* num_partial_rows, vmoe_stream_t stream) {
+  return router_topk_impl<false>(logits, ld_logits, num_tokens, num_experts, top_k, normalize,
+                                 weights, selected_i32, selected_i64, probs, lse, partial,
+                                 partial_floats, num_partial_rows, stream);
+}
+
+extern "C" int vmoe_router_topk_f32(const float* logits, int64_t ld_logits, int64_t num_tokens,
+                                    int32_t num_experts, int32_t top_k, int32_t normalize,
+                                    float* weights, int32_t* selected_i32, int64_t* selected_i64,
+                                    float* probs, float* lse, float* partial,
+                                    size_t partial_floats, int32_t* num_partial_rows,
+                                    vmoe_stream_t stream) {
+  return router_topk_impl<true>(logits, ld_logits, num_tokens, num_experts, top_k, normalize,
+                                weights, selected_i32, selected_i64, probs, lse, partial,
+                                partial_floats, num_partial_rows, stream);
+}
+
+extern "C" int vmoe_router_topk_hist_blocks(int64_t num_tokens, int32_t num_experts,
+                                            int32_t top_k) {
+  return router_hist_blocks(num_tokens, num_experts, top_k);
+}
+
+extern "C" int vmoe_router_topk_hist(const uint16_t* logits, int64_t ld_logits,
+                                     int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                                     int32_t normalize, uint16_t* weights, int32_t* selected_i32,
+                                     int64_t* selected_i64, float* probs, float* lse,
+                                     float* partial, size_t partial_floats,
+                                     int32_t* num_partial_rows, void* route_workspace,
+                                     size_t route_workspace_bytes, vmoe_stream_t stream) {
+  return router_topk_hist_impl<false>(logits, ld_logits, num_tokens, num_experts, top_k,
+                                      normalize, weights, selected_i32, selected_i64, probs,
+                                      lse, partial, partial_floats, num_partial_rows,
+                                      route_workspace, route_workspace_bytes, stream);
+}
+
+extern "C" int vmoe_router_topk_hist_f32(const float* logits, int64_t ld_logits,
+                                         int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                                         int32_t normalize, float* weights,
+                                         int32_t* selected_i32, int64_t* selected_i64,
+                                         float* probs, float* lse, float* partial,
+                                         size_t partial_floats, int32_t* num_partial_rows,
+                                         void* route_workspace, size_t route_workspace_bytes,
+                                         vmoe_stream_t stream) {
+  return router_topk_hist_impl<true>(logits, ld_logits, num_tokens, num_experts, top_k,
+                                     normalize, weights, selected_i32, selected_i64, probs, lse,
+                                     partial, partial_floats, num_partial_rows, route_workspace,
+                                     route_workspace_bytes, stream);
+}
+
+extern "C" int vmoe_router_aux(const float* partial, int32_t num_partial_rows,
+                               int64_t num_tokens, int32_t num_experts,
+                               const int32_t* tokens_per_expert, const float* coef,
+                               const float* widths_normalized, uint16_t* f_i, float* f_i_f32,
+                               float* p_i, uint16_t* z_loss, float* losses,
+                               vmoe_stream_t stream) {
+  return router_aux_impl<false>(partial, num_partial_rows, num_tokens, num_experts,
+                                tokens_per_expert, coef, widths_normalized, f_i, f_i_f32, p_i,
+                                z_loss, losses, stream);
+}
+
+extern "C" int vmoe_router_aux_f32(const float* partial, int32_t num_partial_rows,
+                                   int64_t num_tokens, int32_t num_experts,
+                                   const int32_t* tokens_per_expert, const float* coef,
+                                   const float* widths_normalized, float* f_i, float* f_i_f32,
+                                   float* p_i, float* z_loss, float* losses,
+                                   vmoe_stream_t stream) {
+  return router_aux_impl<true>(partial, num_partial_rows, num_tokens, num_experts,
+                               tokens_per_expert, coef, widths_normalized, f_i, f_i_f32, p_i,
+                               z_loss, losses, stream);
+}
+
+extern "C" int vmoe_router_aux_bwd(const uint16_t* logits, int64_t ld_logits, int64_t num_tokens,
+                                   int32_t num_experts, const float* lse, const float* f_i_f32,
+                                   const float* coef, const float* widths_normalized,
+                                   const float* grad_z, const float* grad_lb,
+                                   const float* grad_cl, uint16_t* grad_logits, int64_t ld_grad,
+                                   vmoe_stream_t stream) {
+  return router_aux_bwd_impl<false>(logits, ld_logits, num_tokens, num_experts, lse, f_i_f32,
+                                    coef, widths_normalized, grad_z, grad_lb, grad_cl,
+                                    grad_logits, ld_grad, stream);
+}
+
+extern "C" int vmoe_router_aux_bwd_f32(const float* logits, int64_t ld_logits,
+                                       int64_t num_tokens, int32_t num_experts, const float* lse,
+                                       const float* f_i_f32, const float* coef,
+                                       const float* widths_normalized, const float* grad_z,
+                                       const float* grad_lb, const float* grad_cl,
+                                       float* grad_logits, int64_t ld_grad,
+                                       vmoe_stream_t stream) {
+  return router_aux_bwd_impl<true>(logits, ld_logits, num_tokens, num_experts, lse, f_i_f32,
+                                   coef, widths_normalized, grad_z, grad_lb, grad_cl,
+                                   grad_logits, ld_grad, stream);
+}
+
+extern "C" int vmoe_router_weight_bwd(const uint16_t* logits, int64_t ld_logits,
+                                      int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                                      int32_t normalize, const int32_t* selected,
+                                      const int64_t* selected_i64, const uint16_t* grad_weights,
+                                      int64_t ld_grad_weights, uint16_t* grad_logits,
+                                      int64_t ld_grad, vmoe_stream_t stream) {
+  return router_weight_bwd_impl<false>(logits, ld_logits, num_tokens, num_experts, top_k,
+                                       normalize, selected, selected_i64, grad_weights,
+                                       ld_grad_weights, grad_logits, ld_grad, stream);
+}
+
+extern "C" int vmoe_router_weight_bwd_f32(const float* logits, int64_t ld_logits,
+                                          int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                                          int32_t normalize, const int32_t* selected,
+                                          const int64_t* selected_i64, const float* grad_weights,
+                                          int64_t ld_grad_weights, float* grad_logits,
+                                          int64_t ld_grad, vmoe_stream_t stream) {
+  return router_weight_bwd_impl<true>(logits, ld_logits, num_tokens, num_experts, top_k,
+                                      normalize, selected, selected_i64, grad_weights,
+                                      ld_grad_weights, grad_logits, ld_grad, stream);
 }
 
 extern "C" int vmoe_router_logits(const uint16_t* x, int64_t ldx, int64_t num_tokens,

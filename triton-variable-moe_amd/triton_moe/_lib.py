@@ -79,6 +79,19 @@ _SIGNATURES = {
     "vmoe_router_topk": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                          ctypes.c_size_t, _vp, _vp],
     "vmoe_router_topk_hist_blocks": [_i64, _i32, _i32],
+    "vmoe_router_topk_f32": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                             ctypes.c_size_t, _vp, _vp],
+    "vmoe_router_topk_hist_f32": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
+                                  _vp, ctypes.c_size_t, _vp, _vp, ctypes.c_size_t, _vp],
+    "vmoe_router_aux_f32": [_vp, _i32, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "vmoe_router_aux_bwd_f32": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                _i64, _vp],
+    "vmoe_router_weight_bwd_f32": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp,
+                                   _i64, _vp],
+    "vmoe_combine_f32": [_vp, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp],
+    "vmoe_gather_f32": [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp],
+    "vmoe_combine_weight_grad_f32": [_vp, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64,
+                                     _vp],
     "vmoe_route_counted_workspace_bytes": [_i64, _i32, _i32],
     "vmoe_router_topk_hist": [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                               ctypes.c_size_t, _vp, _vp, ctypes.c_size_t, _vp],

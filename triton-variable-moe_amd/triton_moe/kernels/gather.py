@@ -24,6 +24,22 @@ def _require_bf16(t: torch.Tensor, what: str) -> None:
         raise NotImplementedError(f"{what}: only bfloat16 tensors are supported (got {t.dtype})")
 
 
+def _require_dtype(t: torch.Tensor, what: str) -> bool:
+    """True for fp32 rows (the *_f32 entry points), False for bf16."""
+    if t.dtype not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError(f"{what}: bfloat16 or float32 tensors only (got {t.dtype})")
+    return t.dtype == torch.float32
+
+
+def _broadcast_rows(t: torch.Tensor):
+    """(tensor, leading dimension): a row-broadcast t (row stride 0) as its
+    single row with leading dimension 0, else t with unit column stride."""
+    if t.shape[0] > 0 and t.stride(0) == 0:
+        return (t[:1] if t.stride(1) == 1 else t[:1].contiguous()), 0
+    t = _row_major(t)
+    return t, t.stride(0)
+
+
 def _row_major(t: torch.Tensor) -> torch.Tensor:
     """2-D view with unit column stride (the kernels take any row stride)."""
     return t if t.stride(-1) == 1 else t.contiguous()
@@ -59,10 +75,20 @@ def gather_rows(x: torch.Tensor, row_src: torch.Tensor, top_k: int, num_rows: in
     With assignment_row (the map vmoe_route produces with row_src) the copy
     runs token by token and reads each row of x once; a row-broadcast x (row
     stride 0, such as the gradient of out.sum()) is then read from a single row.
+    fp32 x (with fp32 weights) goes to vmoe_gather_f32, row by row.
     """
-    _require_bf16(x, "gather")
     hidden = x.shape[1]
     tokens = x.shape[0]
+    if _require_dtype(x, "gather"):
+        x, ldx = _broadcast_rows(x)
+        out = torch.empty(num_rows, hidden, dtype=x.dtype, device=x.device)
+        if num_rows == 0 or hidden == 0:
+            return out
+        w = None if weights is None else weights.to(x.dtype).contiguous()
+        _lib.call("vmoe_gather_f32", x.data_ptr(), tokens, ldx, row_src.data_ptr(), int(top_k),
+                  _lib.ptr(w), 0 if w is None else w.numel(), out.data_ptr(), out.stride(0),
+                  num_rows, _lib.ptr(num_rows_dev), hidden, _lib.stream(x.device))
+        return out
     token_major = (assignment_row is not None and hidden % 8 == 0
                    and assignment_row.numel() == tokens * top_k and top_k <= 64)
     if token_major and tokens > 0 and x.stride(0) == 0:
@@ -89,8 +115,9 @@ def gather_rows(x: torch.Tensor, row_src: torch.Tensor, top_k: int, num_rows: in
 
 def combine_rows(y: torch.Tensor, assignment_row: torch.Tensor, top_k: int, num_tokens: int,
                  weights: torch.Tensor | None = None) -> torch.Tensor:
-    """out[t] = bf16(sum_j f32(bf16(y[row(t,j)] * w[t*k+j]))), unplaced slots add 0."""
-    _require_bf16(y, "scatter")
+    """out[t] = bf16(sum_j f32(bf16(y[row(t,j)] * w[t*k+j]))), unplaced slots add 0
+    (fp32 y: the same sum in fp32 with no roundings, vmoe_combine_f32)."""
+    sfx = "_f32" if _require_dtype(y, "scatter") else ""
     y = _row_major(y)
     hidden = y.shape[1]
     out = torch.empty(num_tokens, hidden, dtype=y.dtype, device=y.device)
@@ -99,9 +126,9 @@ def combine_rows(y: torch.Tensor, assignment_row: torch.Tensor, top_k: int, num_
     w = None
     if weights is not None:
         w = weights.to(y.dtype).contiguous()
-    _lib.call("vmoe_combine", y.data_ptr(), y.shape[0], y.stride(0), assignment_row.data_ptr(),
-              _lib.ptr(w), int(top_k), out.data_ptr(), out.stride(0), num_tokens, hidden,
-              _lib.stream(y.device))
+    _lib.call("vmoe_combine" + sfx, y.data_ptr(), y.shape[0], y.stride(0),
+              assignment_row.data_ptr(), _lib.ptr(w), int(top_k), out.data_ptr(), out.stride(0),
+              num_tokens, hidden, _lib.stream(y.device))
     return out
 
 
@@ -111,20 +138,19 @@ def combine_weight_grad(grad: torch.Tensor, y: torch.Tensor, assignment_row: tor
 
     The routing-weight gradient of combine_rows(y, ..., weights=w), with each
     slot's bf16 rounding taken as identity. A row-broadcast grad (row stride
-    0, the gradient of out.sum()) is read from its single row."""
-    _require_bf16(y, "combine weight gradient")
-    _require_bf16(grad, "combine weight gradient")
+    0, the gradient of out.sum()) is read from its single row. fp32 y and grad
+    go to vmoe_combine_weight_grad_f32."""
+    f32 = _require_dtype(y, "combine weight gradient")
+    if _require_dtype(grad, "combine weight gradient") != f32:
+        raise NotImplementedError("combine weight gradient: grad and y dtypes differ")
+    sfx = "_f32" if f32 else ""
     y = _row_major(y)
     tokens, hidden = grad.shape
-    if tokens > 0 and grad.stride(0) == 0:
-        grad, ldg = (grad[:1] if grad.stride(1) == 1 else grad[:1].contiguous()), 0
-    else:
-        grad = _row_major(grad)
-        ldg = grad.stride(0)
+    grad, ldg = _broadcast_rows(grad)
     gw = torch.empty(tokens * top_k, dtype=torch.float32, device=y.device)
     if gw.numel() == 0:
         return gw
-    _lib.call("vmoe_combine_weight_grad", grad.data_ptr(), ldg, y.data_ptr(), y.shape[0],
+    _lib.call("vmoe_combine_weight_grad" + sfx, grad.data_ptr(), ldg, y.data_ptr(), y.shape[0],
               y.stride(0), assignment_row.data_ptr(), int(top_k), gw.data_ptr(), tokens, hidden,
               _lib.stream(y.device))
     return gw

@@ -890,6 +890,58 @@ def _side_stream(device) -> torch.cuda.Stream:
     return st
 
 
+class RoutedMoEOpF32(torch.autograd.Function):
+    """The module's expert path for float32 parameters, as one autograd node:
+    the reference's chain in fp32 (padded_gather, grouped_gemm_up/down and
+    padded_scatter as TritonMoEMLP.forward calls them, moe.py:203-240, its
+    kernels being dtype-generic) on the fp32 kernels. The up GEMM reads
+    x_flat through the row map (relu^2, PRE = relu(z) kept), the down GEMM
+    writes Y, and the combine weights and sums each token's k rows, the
+    weight on Y as in the reference. Backward: the output gradient gathered
+    into rows with the weights (GY[r] = G[t] w, scatter.py:141-189), dH and
+    dW2 from GY, the relu^2 rule once (GA), dX and dW1 (x through the map),
+    and the unweighted combine of dX. `weights` (fp32 [A]) gets
+    dL/dw = G[t] . Y[row] when it requires grad (opt-in; the reference
+    returns None, scatter.py:176)."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, x_flat, w1, w2, meta, gather_map, row_src, assignment_row, weights, top_k,
+                hidden_size):
+        from .gather import combine_rows
+
+        h, pre, _ = f32_up_fwd(x_flat, w1, meta, _lib.ACT_RELU_SQUARED, gather_map,
+                               want_pre=True)
+        y = f32_down_fwd(h, w2, meta, hidden_size)
+        out = combine_rows(y, assignment_row, top_k, x_flat.shape[0], weights=weights)
+        ctx.save_for_backward(x_flat, w1, w2, h, pre, y, gather_map, row_src, assignment_row,
+                              weights)
+        ctx.meta = meta
+        ctx.hidden_size = hidden_size
+        ctx.top_k = top_k
+        return out
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, grad_out):
+        from .gather import combine_rows, combine_weight_grad, gather_rows
+
+        x_flat, w1, w2, h, pre, y, gm, rs, ar, weights = ctx.saved_tensors
+        m, d, k = ctx.meta, ctx.hidden_size, ctx.top_k
+        T = x_flat.shape[0]
+        grad_out = grad_out.to(torch.float32)
+        gy = gather_rows(grad_out, rs, k, m.rows, weights=weights)
+        grad_h, grad_w2 = f32_down_bwd(gy, h, w2, m, d)
+        grad_xg, grad_w1 = f32_up_bwd(grad_h, x_flat, w1, pre, None, m, d,
+                                      _lib.ACT_RELU_SQUARED, gm)
+        grad_x = combine_rows(grad_xg, ar, k, T)
+        grad_w = None
+        if ctx.needs_input_grad[7]:
+            grad_w = combine_weight_grad(grad_out, y, ar, k).to(weights.dtype)
+        return grad_x, grad_w1, grad_w2, None, None, None, None, grad_w, None, None
+
+
 class RoutedMoEOp(torch.autograd.Function):
     """The module's expert path after routing, as one autograd node: token
     gather, grouped GEMM up with relu^2, grouped GEMM down, weighted combine,

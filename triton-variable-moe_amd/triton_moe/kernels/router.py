@@ -33,10 +33,10 @@ from .. import _lib
 class RouterState:
     """Outputs of router_topk."""
 
-    weights: torch.Tensor      # [T, k] bf16 (normalised when requested)
+    weights: torch.Tensor      # [T, k] in the logits' dtype (normalised when requested)
     selected: torch.Tensor     # [T, k] int32 or int64 expert ids
     probs: torch.Tensor | None  # [T, E] fp32 sigmoid(logits), when requested
-    lse: torch.Tensor          # [T] fp32, bf16-rounded logsumexp of each row
+    lse: torch.Tensor          # [T] fp32 logsumexp of each row (bf16-rounded for bf16 logits)
     partial: torch.Tensor      # per-workgroup sums for the auxiliary losses
     partial_rows: int
     # With route_hist: the routing workspace holding the per-tile expert
@@ -48,14 +48,18 @@ class RouterState:
 def router_topk(logits: torch.Tensor, top_k: int, normalize: bool = True,
                 want_probs: bool = False, index_dtype=torch.int32,
                 route_hist: bool = False) -> RouterState:
-    """sigmoid + top-k + normalisation of bf16 router logits [T, E] (no host sync).
+    """sigmoid + top-k + normalisation of bf16 or fp32 router logits [T, E]
+    (no host sync); the weights come out in the logits' dtype, as the
+    reference's .to(x.dtype) of them (moe.py:176).
 
     route_hist: where the shape allows it (vmoe_router_topk_hist), the same
     launch also writes the per-tile expert histograms the routing needs, into
     a routing workspace returned as RouterState.route_ws."""
     _lib.require_gpu(logits)
-    if logits.dtype != torch.bfloat16:
-        raise NotImplementedError(f"router logits must be bfloat16 (got {logits.dtype})")
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError(f"router logits must be bfloat16 or float32 "
+                                  f"(got {logits.dtype})")
+    sfx = "_f32" if logits.dtype == torch.float32 else ""
     if logits.dim() != 2 or logits.stride(-1) != 1:
         logits = logits.reshape(-1, logits.shape[-1]).contiguous()
     T, E = logits.shape
@@ -67,7 +71,7 @@ def router_topk(logits: torch.Tensor, top_k: int, normalize: bool = True,
     rows = hist_rows or int(L.vmoe_router_partial_floats(T, E)) // (E + 1)
     nfl = rows * (E + 1)
     f32 = torch.float32
-    weights = torch.empty(T, top_k, dtype=torch.bfloat16, device=dev)
+    weights = torch.empty(T, top_k, dtype=logits.dtype, device=dev)
     selected = torch.empty(T, top_k, dtype=index_dtype, device=dev)
     probs = torch.empty(T, E, dtype=f32, device=dev) if want_probs else None
     # lse first, then the partial rows at a 16-byte aligned offset
@@ -83,10 +87,10 @@ def router_topk(logits: torch.Tensor, top_k: int, normalize: bool = True,
     if hist_rows:
         ws_bytes = int(L.vmoe_route_counted_workspace_bytes(T, E, int(top_k)))
         route_ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.int32, device=dev)
-        _lib.call("vmoe_router_topk_hist", *args, route_ws.data_ptr(), route_ws.numel() * 4,
-                  _lib.stream(dev))
+        _lib.call("vmoe_router_topk_hist" + sfx, *args, route_ws.data_ptr(),
+                  route_ws.numel() * 4, _lib.stream(dev))
     else:
-        _lib.call("vmoe_router_topk", *args, _lib.stream(dev))
+        _lib.call("vmoe_router_topk" + sfx, *args, _lib.stream(dev))
     return RouterState(weights, selected, probs, lse, partial, rows, route_ws)
 
 
@@ -157,19 +161,22 @@ class RouterLinear(nn.Linear):
 
 class RouterAuxOp(torch.autograd.Function):
     """(z_loss, load_balance_loss, compute_loss, f_i) from the router state and
-    the routing counts; backward gives the router-logit gradient."""
+    the routing counts; backward gives the router-logit gradient. z_loss, f_i
+    and the gradient are in the logits' dtype (bf16 or fp32)."""
 
     @staticmethod
     @custom_fwd(device_type="cuda")
     def forward(ctx, logits, lse, partial, partial_rows, tokens_per_expert, coef, wn):
         T, E = logits.shape
         dev = logits.device
-        f_i = torch.empty(E, dtype=torch.bfloat16, device=dev)
+        dt = logits.dtype
+        f_i = torch.empty(E, dtype=dt, device=dev)
         f32 = torch.empty(2 * E + 2, dtype=torch.float32, device=dev)
         f_i32, p_i, losses = f32[:E], f32[E:2 * E], f32[2 * E:]
-        z = torch.empty((), dtype=torch.bfloat16, device=dev)
+        z = torch.empty((), dtype=dt, device=dev)
         tpe = tokens_per_expert.to(torch.int32).contiguous()
-        _lib.call("vmoe_router_aux", partial.data_ptr(), int(partial_rows), T, E,
+        sfx = "_f32" if dt == torch.float32 else ""
+        _lib.call("vmoe_router_aux" + sfx, partial.data_ptr(), int(partial_rows), T, E,
                   tpe.data_ptr(), coef.data_ptr(), wn.data_ptr(), f_i.data_ptr(),
                   f_i32.data_ptr(), p_i.data_ptr(), z.data_ptr(), losses.data_ptr(),
                   _lib.stream(dev))
@@ -189,7 +196,8 @@ class RouterAuxOp(torch.autograd.Function):
 
         gz, glb, gcl = scalar(g_z), scalar(g_lb), scalar(g_cl)
         grad = torch.empty_like(logits)
-        _lib.call("vmoe_router_aux_bwd", logits.data_ptr(), logits.stride(0), T, E,
+        sfx = "_f32" if logits.dtype == torch.float32 else ""
+        _lib.call("vmoe_router_aux_bwd" + sfx, logits.data_ptr(), logits.stride(0), T, E,
                   lse.data_ptr(), f_i32.data_ptr(), coef.data_ptr(), wn.data_ptr(),
                   _lib.ptr(gz), _lib.ptr(glb), _lib.ptr(gcl), grad.data_ptr(), grad.stride(0),
                   _lib.stream(logits.device))
@@ -217,11 +225,13 @@ class RouterWeightOp(torch.autograd.Function):
         logits, selected = ctx.saved_tensors
         T, E = logits.shape
         k = selected.shape[-1]
-        g = g_w.reshape(T, k).to(torch.bfloat16).contiguous()
+        dt = logits.dtype
+        g = g_w.reshape(T, k).to(dt).contiguous()
         sel = selected.reshape(T, k).contiguous()
         is64 = sel.dtype == torch.int64
-        grad = torch.empty(T, E, dtype=torch.bfloat16, device=logits.device)
-        _lib.call("vmoe_router_weight_bwd", logits.data_ptr(), logits.stride(0), T, E, k,
+        grad = torch.empty(T, E, dtype=dt, device=logits.device)
+        sfx = "_f32" if dt == torch.float32 else ""
+        _lib.call("vmoe_router_weight_bwd" + sfx, logits.data_ptr(), logits.stride(0), T, E, k,
                   int(ctx.normalize), None if is64 else sel.data_ptr(),
                   sel.data_ptr() if is64 else None, g.data_ptr(), g.stride(0), grad.data_ptr(),
                   grad.stride(0), _lib.stream(logits.device))

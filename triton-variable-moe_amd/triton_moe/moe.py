@@ -36,7 +36,8 @@ from .kernels import (
 from . import _lib
 from .kernels.fused_cumsum import route_device
 from .kernels.gather import combine_rows
-from .kernels.grouped_gemm import GemmMeta, RoutedMoEOp, down_fwd, up_fwd
+from .kernels.grouped_gemm import (GemmMeta, RoutedMoEOp, RoutedMoEOpF32, down_fwd,
+                                   f32_down_fwd, f32_up_fwd, up_fwd)
 from .kernels.router import (RouterAuxOp, RouterLinear, RouterWeightOp, load_balance_coef,
                              router_topk)
 
@@ -174,6 +175,9 @@ class TritonMoEMLP(nn.Module):
         it requires grad (routing_weight_grad). route_ws: the top-k call's
         per-tile histograms (RouterState.route_ws), or None."""
         k = self.num_active_experts
+        if self.w1.dtype == torch.float32:
+            return self._experts_f32(x_flat, top_k_weights_flat, selected_experts_flat,
+                                     route_ws)
         # Pad rows of the row map are -1 (the GEMMs' fused gather reads zeros
         # for them); row_weight holds each row's routing weight.
         r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
@@ -188,6 +192,21 @@ class TritonMoEMLP(nn.Module):
         output_flat = RoutedMoEOp.apply(x_flat, self.w1, self.w2, meta, r.gather_map,
                                         r.row_weight, r.assignment_row, k, self.config.n_embd,
                                         weights)
+        return output_flat, r.tokens_per_expert
+
+    def _experts_f32(self, x_flat, top_k_weights_flat, selected_experts_flat, route_ws=None):
+        """The expert path of a float32 module (RoutedMoEOpF32): the same
+        routing, the fp32 GEMMs and permutation, the routing weights applied
+        in the combine as in the reference."""
+        k = self.num_active_experts
+        r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
+                         map_pad=-1, workspace=route_ws)
+        meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
+                        self.expert_widths_t, r.padded_counts, self.num_experts,
+                        self.max_expert_width, r.rows_bound)
+        w = top_k_weights_flat.to(torch.float32)
+        output_flat = RoutedMoEOpF32.apply(x_flat, self.w1, self.w2, meta, r.gather_map,
+                                           r.row_src, r.assignment_row, w, k, self.config.n_embd)
         return output_flat, r.tokens_per_expert
 
     @torch.compiler.disable
@@ -272,9 +291,11 @@ class TritonMoEMLP(nn.Module):
             top_k_weights_flat = state.weights.reshape(-1)
             selected_experts_flat = state.selected.reshape(-1)
         k = self.num_active_experts
+        f32 = self.w1.dtype == torch.float32
         with profiler.step("fused_route"):
             r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
-                             map_pad=-1, weights=top_k_weights_flat, workspace=state.route_ws)
+                             map_pad=-1, weights=None if f32 else top_k_weights_flat,
+                             workspace=state.route_ws)
             meta = GemmMeta(r.expert_offsets, self.expert_weight_offsets_t,
                             self.expert_widths_t, r.padded_counts, self.num_experts,
                             self.max_expert_width, r.rows_bound)
@@ -283,14 +304,24 @@ class TritonMoEMLP(nn.Module):
         # The token gather has no launch of its own (the up GEMM reads x_flat
         # through the gather map), so its step is "gather+gemm_up".
         with torch.no_grad():
-            with profiler.step("gather+gemm_up"):
-                h, _pre = up_fwd(x_flat, self.w1, meta, _lib.ACT_RELU_SQUARED, False,
-                                 zero_tails=False, gather_map=r.gather_map,
-                                 row_scale=r.row_weight)
-            with profiler.step("gemm_down"):
-                y = down_fwd(h, self.w2, meta, self.config.n_embd)
-            with profiler.step("scatter"):
-                output_flat = combine_rows(y, r.assignment_row, k, x_flat.shape[0])
+            if f32:  # the weights go on Y in the combine, as in the reference
+                with profiler.step("gather+gemm_up"):
+                    h, _pre, _ = f32_up_fwd(x_flat, self.w1, meta, _lib.ACT_RELU_SQUARED,
+                                            r.gather_map)
+                with profiler.step("gemm_down"):
+                    y = f32_down_fwd(h, self.w2, meta, self.config.n_embd)
+                with profiler.step("scatter"):
+                    output_flat = combine_rows(y, r.assignment_row, k, x_flat.shape[0],
+                                               weights=top_k_weights_flat)
+            else:
+                with profiler.step("gather+gemm_up"):
+                    h, _pre = up_fwd(x_flat, self.w1, meta, _lib.ACT_RELU_SQUARED, False,
+                                     zero_tails=False, gather_map=r.gather_map,
+                                     row_scale=r.row_weight)
+                with profiler.step("gemm_down"):
+                    y = down_fwd(h, self.w2, meta, self.config.n_embd)
+                with profiler.step("scatter"):
+                    output_flat = combine_rows(y, r.assignment_row, k, x_flat.shape[0])
         with profiler.step("reshape"):
             output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
         with profiler.step("aux_loss"):
