@@ -37,6 +37,8 @@ CASES = {
     "ragged": ([70, 0, 133, 64, 1], [64, 128, 32, 96, 8], 96, False),
     "uncovered": ([100, 64, 37], [48, 64, 16], 128, True),  # tpe < row range
     "wide": ([300, 257], [256, 512], 256, False),
+    # hidden, widths and offsets off the bf16 kernels' multiple-of-8 rule
+    "unaligned": ([50, 33, 0, 17], [12, 20, 36, 5], 100, False),
 }
 
 
@@ -123,7 +125,7 @@ def test_f32_forward(name, act, device):
 
 @pytest.mark.parametrize("use_map", [False, True])
 @pytest.mark.parametrize("act", ["none", "relu_squared", "swiglu"])
-@pytest.mark.parametrize("name", ["ref_fixture", "ragged", "uncovered"])
+@pytest.mark.parametrize("name", ["ref_fixture", "ragged", "uncovered", "unaligned"])
 def test_f32_autograd_chain(name, act, use_map, device):
     """up_autograd -> down_autograd -> (Y * G).sum() -> backward (the
     reference's test_grouped_gemm_backward flow in fp32; with x_flat and
@@ -270,3 +272,49 @@ def test_f32_gather_map_pad_rows_read_zeros(act, device):
                                          gather_map=gmd)
     _, gw_ref = grouped_gemm_up_backward(gh, xgd, w1d, pre_ref, *args, d, activation=act)
     assert torch.equal(gw_map, gw_ref)
+
+
+def test_f32_in_kernel_relu2_rule_matches_formed_ga(device):
+    """vmoe_gemm_f32_up_bwd_dx / _dw with VMOE_ACT_RELU_SQUARED (the relu^2
+    gradient formed while the operand is loaded) against the path the Python
+    layer takes (vmoe_f32_relu2_grad, then VMOE_ACT_NONE): the same products,
+    so the same bits. vmoe_f32_relu2_grad itself on strided rows (ld > cols)
+    against its formula."""
+    from triton_moe import _lib
+
+    rows, widths, d, short = CASES["ragged"]
+    eto, tpe, offs = _meta(rows, widths, short)
+    P, W, mw = sum(rows), sum(widths), max(widths)
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(P, d, generator=g).to(device)
+    w1 = (torch.randn(d, W, generator=g) * 0.1).to(device)
+    gbuf = torch.randn(P, mw + 24, generator=g).to(device)
+    pbuf = torch.relu(torch.randn(P, mw + 24, generator=g)).to(device)
+    gh, pre = gbuf[:, :mw], pbuf[:, :mw]  # strided views, ld = mw + 24
+    keep = [_dev(eto, device), _dev(offs, device), _dev(widths, device), _dev(tpe, device)]
+    meta = tuple(t.data_ptr() for t in keep)
+    st = _lib.stream(device)
+    gabuf = torch.full((P, mw + 8), float("nan"), device=device)
+    ga = gabuf[:, :mw]
+    _lib.call("vmoe_f32_relu2_grad", gh.data_ptr(), pre.data_ptr(), gh.stride(0), ga.data_ptr(),
+              ga.stride(0), P, mw, st)
+    ref = torch.where(pre > 0, gh * 2.0 * pre, torch.zeros_like(pre))
+    assert torch.equal(ga, ref)
+    assert torch.isnan(gabuf[:, mw:]).all()  # the row padding is not written
+
+    def run(op, act):
+        gx = torch.zeros(P, d, device=device)
+        gw = torch.zeros(d, W, device=device)
+        p_ = pre.data_ptr() if act else None
+        _lib.call("vmoe_gemm_f32_up_bwd_dx", op.data_ptr(), p_, None, op.stride(0), act,
+                  w1.data_ptr(), w1.stride(0), gx.data_ptr(), gx.stride(0), *meta, len(widths),
+                  d, mw, P, st)
+        _lib.call("vmoe_gemm_f32_up_bwd_dw", x.data_ptr(), x.stride(0), P, None, op.data_ptr(),
+                  p_, None, op.stride(0), act, gw.data_ptr(), gw.stride(0), *meta, len(widths),
+                  d, mw, P, st)
+        return gx, gw
+
+    gx_a, gw_a = run(ga, _lib.ACT_NONE)
+    gx_b, gw_b = run(gh, _lib.ACT_RELU_SQUARED)
+    assert torch.equal(gx_a, gx_b) and torch.equal(gw_a, gw_b)
+    assert gx_a.abs().sum() > 0 and gw_a.abs().sum() > 0

@@ -272,11 +272,11 @@ def test_forward_profiled(device):
     out2, aux2, f2 = m.forward_profiled(x.detach(), rec)
     torch.cuda.synchronize()
     names = [n for n, _, _ in rec.steps]
-    assert names == ["flatten", "routing", "fused_route", "gather+gemm_up", "gemm_down",
+    assert names == ["flatten", "routing", "fused_route", "gather", "gemm_up", "gemm_down",
                      "scatter", "reshape", "aux_loss"]
     ms = {n: a.elapsed_time(b) for n, a, b in rec.steps}
     # each expert-path step holds a launch of its own
-    for n in ("gather+gemm_up", "gemm_down", "scatter"):
+    for n in ("gemm_up", "gemm_down", "scatter"):
         assert ms[n] > 0.0, (n, ms)
     assert bits_equal(out2, out.detach()) and torch.equal(f2, f_i)
     assert not out2.requires_grad

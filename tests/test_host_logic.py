@@ -150,3 +150,33 @@ def test_glu_meta_layouts():
         glu_meta(eto, t([0, 32, 48, 80]), widths, tpe, 16, 64, 72)
     with pytest.raises(NotImplementedError, match="multiples of 8"):
         glu_meta(eto, t([0, 36, 52, 84]), widths, tpe, 16, 64, 96)
+
+
+@pytest.mark.parametrize("sizes", [[(8, 256)], [(2, 128), (3, 64)], [(1, 128), (1, 64)],
+                                   [(1, 256), (4, 128), (1, 64), (3, 32)],
+                                   [(32, 1024), (64, 512), (32, 256)]])
+def test_load_balance_coef_from_group_buffers(sizes):
+    """The module's load-balance coefficients come from its grouping buffers
+    and equal the closed form of router.load_balance_coef; with them the one
+    dot product sum_e coef f p reproduces the reference's three formulas
+    (moe.py:276-303), restated here from the buffers as the reference uses
+    them (uniform: E f.p; no group: f.p; groups: mean_g size_g sum_{e in g} f p)."""
+    from triton_moe.kernels.router import load_balance_coef
+
+    m = TritonMoEMLP(TritonMoEConfig(n_embd=32, expert_sizes=sizes, num_active_experts=1,
+                                     block_size=32))
+    coef = m.load_balance_coef()
+    assert coef.tolist() == pytest.approx(load_balance_coef(sizes), rel=0, abs=1e-6)
+    g = torch.Generator().manual_seed(len(sizes))
+    f = torch.rand(m.num_experts, generator=g, dtype=torch.float64)
+    p = torch.rand(m.num_experts, generator=g, dtype=torch.float64)
+    if len(set(m.expert_widths)) == 1:
+        ref = m.num_experts * (f @ p)
+    elif m._num_valid_groups == 0:
+        ref = f @ p
+    else:
+        fp = (f * p).index_select(0, m.valid_expert_indices)
+        memb = m.group_membership.double().index_select(0, m.valid_expert_indices)
+        ref = (m.group_sizes.double() * (fp @ memb)).mean()
+    # coef is fp32 (size / num_groups rounded once)
+    assert (coef.double() * f * p).sum().item() == pytest.approx(ref.item(), rel=1e-6)

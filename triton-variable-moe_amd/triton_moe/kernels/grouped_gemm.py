@@ -68,8 +68,10 @@ def _i32(t: torch.Tensor) -> torch.Tensor:
 
 
 def host_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, rows: int | None,
-              total_width: int | None) -> GemmMeta:
-    """Validates caller metadata on the host (one device->host copy)."""
+              total_width: int | None, align8: bool = True) -> GemmMeta:
+    """Validates caller metadata on the host (one device->host copy).
+    align8: the bf16 kernels' rule that hidden, widths and offsets are
+    multiples of 8 (the fp32 kernels have none, so their callers pass False)."""
     eto_d, ewo_d, w_d, tpe_d = _i32(eto), _i32(ewo), _i32(widths), _i32(tpe)
     E = w_d.numel()
     if E == 0:
@@ -81,7 +83,8 @@ def host_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, rows: int | No
     h_w, h_tpe = host[2 * E + 2:3 * E + 2], host[3 * E + 2:]
     if rows is None:
         rows = h_eto[E]
-    if any(v % 8 for v in h_w) or any(v % 8 for v in h_ewo) or hidden % 8 or max_width % 8:
+    if align8 and (any(v % 8 for v in h_w) or any(v % 8 for v in h_ewo) or hidden % 8 or
+                   max_width % 8):
         raise NotImplementedError(
             "hidden size, expert widths and weight offsets must be multiples of 8")
     if any(w < 0 or w > max_width for w in h_w):
@@ -569,8 +572,10 @@ class GluMeta:
     cols: torch.Tensor | None
 
 
-def glu_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, w1_cols: int) -> GluMeta:
-    """Validates swiglu metadata on the host (one device->host copy)."""
+def glu_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, w1_cols: int,
+             align8: bool = True) -> GluMeta:
+    """Validates swiglu metadata on the host (one device->host copy); align8
+    as for host_meta."""
     E = int(torch.as_tensor(widths).numel())
     if E == 0:
         raise ValueError("expert_widths is empty")
@@ -588,9 +593,10 @@ def glu_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, w1_cols: int) -
     for w in h_w:
         cum.append(cum[-1] + 2 * w)
     cum_d = torch.tensor(cum, dtype=torch.int32, device=w_d.device)
-    if any(o % 8 for o in h_ewo):
+    if align8 and any(o % 8 for o in h_ewo):
         raise NotImplementedError("expert weight offsets must be multiples of 8")
-    chk = host_meta(eto_d, cum_d, w_d * 2, tpe_d, 2 * int(max_width), hidden, None, cum[-1])
+    chk = host_meta(eto_d, cum_d, w_d * 2, tpe_d, 2 * int(max_width), hidden, None, cum[-1],
+                    align8)
     if any(w > max_width for w in h_w):
         raise ValueError("expert width outside [0, max_expert_width]")
     fwd = GemmMeta(eto_d, ewo_d, w_d, tpe_d, E, int(max_width), chk.rows, chk.full_rows, False,
@@ -599,7 +605,8 @@ def glu_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, w1_cols: int) -
     cols = None
     dev = w_d.device
     if contiguous:
-        bwd = host_meta(eto_d, ewo_d, w_d * 2, tpe_d, 2 * int(max_width), hidden, None, w1_cols)
+        bwd = host_meta(eto_d, ewo_d, w_d * 2, tpe_d, 2 * int(max_width), hidden, None, w1_cols,
+                        align8)
     else:
         cols = torch.cat([torch.arange(o, o + 2 * w) for o, w in zip(h_ewo, h_w)]).to(dev)
         bwd = chk
@@ -669,7 +676,8 @@ def grouped_gemm_up(x, w1, expert_token_offsets, expert_weight_offsets, expert_w
     act = _activation_code(activation)
     if act == ACT_SWIGLU:
         gmeta = glu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
-                         tokens_per_expert, int(max_expert_width), x.shape[1], w1.shape[1])
+                         tokens_per_expert, int(max_expert_width), x.shape[1], w1.shape[1],
+                         align8=not _is_f32(w1))
         # pre_act is the gate, as the reference saves it (grouped_gemm.py:339-346)
         if _is_f32(w1):
             h, g, _ = f32_up_fwd(x, w1, gmeta.fwd, act, gather_map, want_pre=save_pre_act)
@@ -677,7 +685,8 @@ def grouped_gemm_up(x, w1, expert_token_offsets, expert_weight_offsets, expert_w
             h, g, _ = glu_fwd(x, w1, gmeta.fwd, True, save_pre_act, False, gather_map)
         return (h, g) if save_pre_act else h
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
-                  tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1])
+                  tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1],
+                  align8=not _is_f32(w1))
     if _is_f32(w1):
         out, pre, _ = f32_up_fwd(x, w1, m, act, gather_map, want_pre=save_pre_act)
         return (out, pre) if save_pre_act else out
@@ -696,7 +705,8 @@ def grouped_gemm_down(intermediate, w2, expert_token_offsets, expert_weight_offs
     _lib.require_gpu(intermediate)
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, intermediate.shape[1], int(hidden_size),
-                  intermediate.shape[0], w2.shape[0])
+                  intermediate.shape[0], w2.shape[0],
+                  align8=not _is_f32(w2))
     if _is_f32(w2):
         return f32_down_fwd(intermediate, w2, m, int(hidden_size))
     return down_fwd(intermediate, w2, m, int(hidden_size))
@@ -714,7 +724,8 @@ def grouped_gemm_up_backward(grad_output, x, w1, pre_act, expert_token_offsets,
         # reference keeps only the gate and leaves this backward unfinished,
         # grouped_gemm.py:768-790).
         gmeta = glu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
-                         tokens_per_expert, grad_output.shape[1], int(hidden_size), w1.shape[1])
+                         tokens_per_expert, grad_output.shape[1], int(hidden_size), w1.shape[1],
+                         align8=not _is_f32(w1))
         if _is_f32(w1):
             _, _, up = f32_up_fwd(x, w1, gmeta.fwd, act, gather_map, want_out=False,
                                   want_up=True)
@@ -725,7 +736,8 @@ def grouped_gemm_up_backward(grad_output, x, w1, pre_act, expert_token_offsets,
         return glu_bwd(grad_output, x, w1, gate, up, gmeta, int(hidden_size), gather_map)
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, grad_output.shape[1], int(hidden_size), None,
-                  w1.shape[1])
+                  w1.shape[1],
+                  align8=not _is_f32(w1))
     if _is_f32(w1):
         return f32_up_bwd(grad_output, x, w1, pre_act, None, m, int(hidden_size), act,
                           gather_map)
@@ -740,7 +752,8 @@ def grouped_gemm_down_backward(grad_output, intermediate, w2, expert_token_offse
     _lib.require_gpu(grad_output)
     m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                   tokens_per_expert, int(max_expert_width), int(hidden_size),
-                  intermediate.shape[0], w2.shape[0])
+                  intermediate.shape[0], w2.shape[0],
+                  align8=not _is_f32(w2))
     if _is_f32(w2):
         return f32_down_bwd(grad_output, intermediate, w2, m, int(hidden_size))
     return down_bwd(grad_output, intermediate, w2, m, int(hidden_size), zero_tails=True)
@@ -767,7 +780,8 @@ class GroupedGemmUp(torch.autograd.Function):
         ctx.f32 = _is_f32(w1)
         if act == ACT_SWIGLU:
             gmeta = glu_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
-                             tokens_per_expert, int(max_expert_width), x.shape[1], w1.shape[1])
+                             tokens_per_expert, int(max_expert_width), x.shape[1], w1.shape[1],
+                             align8=not _is_f32(w1))
             if ctx.f32:
                 out, gate, up = f32_up_fwd(x, w1, gmeta.fwd, act, want_pre=True, want_up=True)
             else:
@@ -778,7 +792,8 @@ class GroupedGemmUp(torch.autograd.Function):
             ctx.act = act
             return out
         m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
-                      tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1])
+                      tokens_per_expert, int(max_expert_width), x.shape[1], None, w1.shape[1],
+                      align8=not _is_f32(w1))
         if ctx.f32:
             out, pre, _ = f32_up_fwd(x, w1, m, act, want_pre=True)
         else:
@@ -828,7 +843,8 @@ class GroupedGemmDown(torch.autograd.Function):
         intermediate = intermediate.to(w2.dtype)
         m = host_meta(expert_token_offsets, expert_weight_offsets, expert_widths,
                       tokens_per_expert, int(max_expert_width), int(hidden_size),
-                      intermediate.shape[0], w2.shape[0])
+                      intermediate.shape[0], w2.shape[0],
+                      align8=not _is_f32(w2))
         ctx.f32 = _is_f32(w2)
         out = (f32_down_fwd if ctx.f32 else down_fwd)(intermediate, w2, m, int(hidden_size))
         ctx.save_for_backward(intermediate, w2)

@@ -38,8 +38,7 @@ from .kernels.fused_cumsum import route_device
 from .kernels.gather import combine_rows
 from .kernels.grouped_gemm import (GemmMeta, RoutedMoEOp, RoutedMoEOpF32, down_fwd,
                                    f32_down_fwd, f32_up_fwd, up_fwd)
-from .kernels.router import (RouterAuxOp, RouterLinear, RouterWeightOp, load_balance_coef,
-                             router_topk)
+from .kernels.router import RouterAuxOp, RouterLinear, RouterWeightOp, router_topk
 
 
 @dataclass
@@ -105,6 +104,12 @@ class TritonMoEMLP(nn.Module):
                          dtype=torch.float32),
             persistent=False)
 
+        # Expert groups (runs of two or more experts of one width) as the
+        # reference's buffers (moe.py:93-132): group_membership [E, G],
+        # group_sizes [G], valid_expert_indices. The load-balance loss reads
+        # them through load_balance_coef(); valid_expert_indices is kept for
+        # attribute compatibility (the per-expert coefficients already give
+        # lone experts weight 0, so no index_select is needed).
         expert_to_group = []
         group_sizes = []
         valid_group_idx = 0
@@ -145,13 +150,29 @@ class TritonMoEMLP(nn.Module):
                          want_probs=True, index_dtype=torch.int64)
         return router_logits, st.probs, st.weights.to(x_flat.dtype), st.selected
 
+    def load_balance_coef(self) -> torch.Tensor:
+        """fp32 [E] per-expert weights that fold the reference's three
+        load-balance formulas (moe.py:276-303) into one dot product
+        sum_e coef[e] f_i[e] p_i[e], read off the grouping buffers above
+        (group_membership, group_sizes; moe.py:93-132 builds the same ones):
+        E for uniform widths; 1 without a group of two or more experts;
+        otherwise group_size / num_groups for an expert of a group (its row
+        of group_membership) and 0 for a lone expert."""
+        E = self.num_experts
+        dev = self.expert_widths_t.device
+        if len(set(self.expert_widths)) == 1:
+            return torch.full((E,), float(E), dtype=torch.float32, device=dev)
+        if self._num_valid_groups == 0:
+            return torch.ones(E, dtype=torch.float32, device=dev)
+        per_group = self.group_sizes.float() / self._num_valid_groups
+        return self.group_membership.float() @ per_group
+
     def _aux_tables(self, device):
         """fp32 load-balance coefficients and normalised widths on `device`."""
         key = (str(device), self.expert_widths_normalized.dtype)
         cache = getattr(self, "_aux_cache", None)
         if cache is None or cache[0] != key:
-            coef = torch.tensor(load_balance_coef(self.config.expert_sizes),
-                                dtype=torch.float32, device=device)
+            coef = self.load_balance_coef().to(device=device, dtype=torch.float32)
             wn = self.expert_widths_normalized.to(device=device, dtype=torch.float32)
             self._aux_cache = cache = (key, coef, wn)
         return cache[1], cache[2]
@@ -300,12 +321,15 @@ class TritonMoEMLP(nn.Module):
                             self.expert_widths_t, r.padded_counts, self.num_experts,
                             self.max_expert_width, r.rows_bound)
         # Forward only, as the reference's (its GEMM calls carry no autograd):
-        # the three launches of RoutedMoEOp.forward, each timed on its own.
-        # The token gather has no launch of its own (the up GEMM reads x_flat
-        # through the gather map), so its step is "gather+gemm_up".
+        # the three launches of RoutedMoEOp.forward, each timed on its own,
+        # under the reference's step names. The token gather has no launch of
+        # its own (the up GEMM reads x_flat through the gather map), so its
+        # "gather" step is empty and "gemm_up" holds the gather's reads.
         with torch.no_grad():
+            with profiler.step("gather"):
+                pass
             if f32:  # the weights go on Y in the combine, as in the reference
-                with profiler.step("gather+gemm_up"):
+                with profiler.step("gemm_up"):
                     h, _pre, _ = f32_up_fwd(x_flat, self.w1, meta, _lib.ACT_RELU_SQUARED,
                                             r.gather_map)
                 with profiler.step("gemm_down"):
@@ -314,7 +338,7 @@ class TritonMoEMLP(nn.Module):
                     output_flat = combine_rows(y, r.assignment_row, k, x_flat.shape[0],
                                                weights=top_k_weights_flat)
             else:
-                with profiler.step("gather+gemm_up"):
+                with profiler.step("gemm_up"):
                     h, _pre = up_fwd(x_flat, self.w1, meta, _lib.ACT_RELU_SQUARED, False,
                                      zero_tails=False, gather_map=r.gather_map,
                                      row_scale=r.row_weight)
