@@ -613,6 +613,111 @@ int vmoe_gemm_f32_down_bwd_dw(const float* h, int64_t ldh, const float* grad_y, 
                               int32_t num_experts, int64_t hidden, int64_t max_width,
                               int64_t rows_bound, vmoe_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * The module's expert path, one call per direction: the routing placement,
+ * the up GEMM reading x through the row map (H' = bf16(w relu(z)^2), PRE =
+ * relu(z)), the down GEMM and the unweighted combine of TritonMoEMLP.forward
+ * (triton_moe/moe.py:186-250: fused_route's placement, padded_gather,
+ * grouped_gemm_up, grouped_gemm_down, padded_scatter), and their backward,
+ * as sequences of the entry points above. No counterpart in the reference
+ * (its module makes these calls one by one from Python); for bindings whose
+ * per-call cost matters (small batches).
+ *
+ * Buffers are the caller's: `saved` (kept from the forward to the backward),
+ * one scratch buffer per direction (used only during the call), sized by
+ * vmoe_expert_layout: out[0] saved bytes, out[1] forward scratch bytes,
+ * out[2] backward scratch bytes, out[3] the padded-row bound rows_bound =
+ * T k + E (block_size - 1), out[4 + s] the byte offset in `saved` of slot s
+ * below (each 256-byte aligned; the routing arrays are vmoe_route's, with
+ * gather_map_pad -1, row_weight from the weights, dropless rounding; H and
+ * PRE bf16 [rows_bound, max_width]). counted != 0: the forward will get the
+ * routing workspace of vmoe_router_topk_hist (its scratch then holds no
+ * routing workspace). Rows past the routed count are left unwritten.
+ * ---------------------------------------------------------------------- */
+enum vmoe_expert_slot {
+  VMOE_X_BIN_IDS = 0, VMOE_X_INDICES, VMOE_X_TPE, VMOE_X_BINS, VMOE_X_PADDED_BINS,
+  VMOE_X_ROW_SRC, VMOE_X_GATHER_MAP, VMOE_X_ASSIGNMENT_ROW, VMOE_X_INFO,
+  VMOE_X_EXPERT_OFFSETS, VMOE_X_PADDED_COUNTS, VMOE_X_ROW_WEIGHT, VMOE_X_H, VMOE_X_PRE,
+  VMOE_X_NSLOTS
+};
+int vmoe_expert_layout(int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                       int32_t block_size, int64_t hidden, int64_t max_width, int32_t counted,
+                       int64_t* out /* [4 + VMOE_X_NSLOTS] */);
+/* out[t] = bf16(sum_j Y'[row(t, j)]), Y' = H' W2_e, H' = bf16(w relu(x[t] W1_e)^2)
+ * for the routing of selected / weights (bf16 [T k]); route_workspace: the
+ * counted routing workspace (vmoe_route_counted) or NULL (vmoe_route, its
+ * workspace in the scratch). ewo / widths [E(+1)] device int32 as for the
+ * GEMMs; the GEMMs' alignment rules apply. */
+int vmoe_expert_forward(const void* selected, int32_t selected_is_int64, const uint16_t* weights,
+                        int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                        int32_t block_size, void* route_workspace, size_t route_workspace_bytes,
+                        const uint16_t* x, int64_t ldx, const uint16_t* w1, int64_t ldw1,
+                        const uint16_t* w2, int64_t ldw2, const int32_t* ewo,
+                        const int32_t* widths, int64_t hidden, int64_t max_width, void* saved,
+                        void* scratch, uint16_t* out, int64_t ldo, vmoe_stream_t stream);
+/* Gradients of vmoe_expert_forward for the output gradient grad_out [T, hidden]
+ * (ldg = 0 reads one row for every token; grad_scale nullable, as for
+ * vmoe_gemm_down_bwd_dh): grad_x [T, hidden], grad_w1 / grad_w2 (every column /
+ * row an expert covers), and with grad_weights != NULL the routing weights'
+ * (vmoe_routing_weight_grad, then its direct form). dW2 and dW1 run on
+ * side_stream when it is not NULL (ordered by events; the call returns with
+ * `stream` waiting for it), with dw_workspace (vmoe_gemm_dw_workspace_bytes
+ * at E, hidden, max_width, rows_bound) used by both in turn. */
+int vmoe_expert_backward(const void* saved, int64_t num_tokens, int32_t num_experts,
+                         int32_t top_k, int32_t block_size, const uint16_t* x, int64_t ldx,
+                         const uint16_t* w1, int64_t ldw1, const uint16_t* w2, int64_t ldw2,
+                         const int32_t* ewo, const int32_t* widths, int64_t hidden,
+                         int64_t max_width, const uint16_t* grad_out, int64_t ldg,
+                         const uint16_t* grad_scale, uint16_t* grad_x, int64_t ldgx,
+                         uint16_t* grad_w1, int64_t ldgw1, uint16_t* grad_w2, int64_t ldgw2,
+                         uint16_t* grad_weights, void* scratch, void* dw_workspace,
+                         size_t dw_workspace_bytes, vmoe_stream_t stream,
+                         vmoe_stream_t side_stream);
+
+/* ------------------------------------------------------------------------
+ * The whole layer after the router Linear, one call per direction: from
+ * bf16 router logits [T, E] (contiguous, 16-byte aligned) the top-k
+ * (vmoe_router_topk_hist where it applies, else vmoe_router_topk + the
+ * routing's own count), the expert path of vmoe_expert_forward, and the
+ * auxiliary losses (vmoe_router_aux): TritonMoEMLP.forward after
+ * self.router (triton_moe/moe.py:167-303). No counterpart in the reference
+ * (for bindings whose per-call cost matters). vmoe_moe_layout: out[0..3] as
+ * vmoe_expert_layout's, out[4 + s] the expert slots, out[4 + VMOE_X_NSLOTS + s]
+ * the slots below (selected int32 [T k], weights bf16 [T k], lse fp32 [T],
+ * f_i fp32 [E]), out[4 + VMOE_X_NSLOTS + VMOE_M_NSLOTS] 1 when the counted
+ * top-k applies. Outputs: out [T, hidden], z_loss (bf16 scalar),
+ * losses[0..1] (load balance, compute; fp32), f_i bf16 [E].
+ * vmoe_moe_backward: grad_out nullable (then no x / w1 / w2 gradients);
+ * grad_logits [T, E] bf16 nullable, else the auxiliary losses' logit
+ * gradient for the device fp32 scalars grad_z / grad_lb / grad_cl
+ * (nullable = 0; not all NULL unless weight_grad), plus with weight_grad the
+ * routing weights' chain (vmoe_routing_weight_grad, its direct form and
+ * vmoe_router_weight_bwd), the two added as bf16(a + b).
+ * ---------------------------------------------------------------------- */
+enum vmoe_moe_slot { VMOE_M_SELECTED = 0, VMOE_M_WEIGHTS, VMOE_M_LSE, VMOE_M_F_I32, VMOE_M_NSLOTS };
+int vmoe_moe_layout(int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t block_size,
+                    int64_t hidden, int64_t max_width,
+                    int64_t* out /* [5 + VMOE_X_NSLOTS + VMOE_M_NSLOTS] */);
+int vmoe_moe_forward(const uint16_t* logits, int64_t num_tokens, int32_t num_experts,
+                     int32_t top_k, int32_t normalize, int32_t block_size, const uint16_t* x,
+                     int64_t ldx, const uint16_t* w1, int64_t ldw1, const uint16_t* w2,
+                     int64_t ldw2, const int32_t* ewo, const int32_t* widths, int64_t hidden,
+                     int64_t max_width, const float* coef, const float* widths_normalized,
+                     void* saved, void* scratch, uint16_t* out, int64_t ldo, uint16_t* z_loss,
+                     float* losses, uint16_t* f_i, vmoe_stream_t stream);
+int vmoe_moe_backward(const void* saved, const uint16_t* logits, int64_t num_tokens,
+                      int32_t num_experts, int32_t top_k, int32_t normalize, int32_t block_size,
+                      const uint16_t* x, int64_t ldx, const uint16_t* w1, int64_t ldw1,
+                      const uint16_t* w2, int64_t ldw2, const int32_t* ewo,
+                      const int32_t* widths, int64_t hidden, int64_t max_width,
+                      const float* coef, const float* widths_normalized,
+                      const uint16_t* grad_out, int64_t ldg, const uint16_t* grad_scale,
+                      const float* grad_z, const float* grad_lb, const float* grad_cl,
+                      int32_t weight_grad, uint16_t* grad_x, int64_t ldgx, uint16_t* grad_w1,
+                      int64_t ldgw1, uint16_t* grad_w2, int64_t ldgw2, uint16_t* grad_logits,
+                      void* scratch, void* dw_workspace, size_t dw_workspace_bytes,
+                      vmoe_stream_t stream, vmoe_stream_t side_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -240,7 +240,7 @@ def test_backward_side_stream_same_bits(name, device):
             torch.cuda.synchronize()
             return out
         finally:
-            gg.BACKWARD_SIDE_STREAM = True
+            gg.BACKWARD_SIDE_STREAM = None
 
     one, two = grads(False), grads(True)
     for a, b in zip(one, two):
@@ -515,3 +515,73 @@ def test_routing_weight_grad_at_zero_and_denormal_weights(name, device):
     assert float((ulps <= 1).double().mean()) >= 0.999, (name, int(ulps.max()))
     err_b = (got[tiny].double() - ref_b).abs()
     assert (err_b <= 2.0 ** -8 * ref_b.abs() + 1e-4 * mag).all(), (name, int(ulps.max()))
+
+
+@pytest.mark.parametrize("name,grad", [("ref_variable", "random"), ("cfg1", "sum"),
+                                       ("cfg2", "scaled"), ("cfg3_a1", "random")])
+def test_fused_expert_path_same_bits_as_per_kernel_path(name, grad, device):
+    """The module after its router Linear as one library call per direction
+    (vmoe_moe_forward / _backward, the default) gives the bits of the
+    per-kernel calls (router_topk, RoutedMoEOp, RouterAuxOp,
+    RouterWeightOp): output, auxiliary losses, f_i, the x / w1 / w2 / router
+    gradients with the opt-in routing-weight gradient, over three steps (the
+    output's loss, plus the auxiliary losses, the auxiliary losses alone),
+    with and without the backward's second stream."""
+    from triton_moe.kernels import grouped_gemm as gg
+
+    B, S, d, sizes, k, b, alpha = CONFIGS[name]
+    E = sum(c for c, _ in sizes)
+    bias = zipf_bias(E, alpha=alpha) if alpha is not None else None
+    p = make_problem(B * S, d, sizes, k, b, seed=5, skew=bias, device=device)
+    G = torch.randn(B, S, d, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    results = {}
+    for fused in (False, True):
+        for side in (False, True):
+            gg.FUSED_EXPERT_PATH, gg.BACKWARD_SIDE_STREAM = fused, side
+            try:
+                cfg = TritonMoEConfig(n_embd=d, expert_sizes=sizes, num_active_experts=k,
+                                      block_size=b, routing_weight_grad=True)
+                m = TritonMoEMLP(cfg).to(device).to(torch.bfloat16)
+                with torch.no_grad():
+                    m.router.weight.copy_(p["wr"])
+                    m.w1.copy_(p["w1"])
+                    m.w2.copy_(p["w2"])
+                if bias is not None:
+                    m.router.register_forward_hook(
+                        lambda mod, inp, out: out + bias.to(out.device, out.dtype))
+                x = p["x"].view(B, S, d).to(device).requires_grad_(True)
+                steps = []
+                for step in range(3):
+                    x.grad = None
+                    m.zero_grad(set_to_none=True)
+                    out, aux, f_i = m(x)
+                    if grad == "random":
+                        loss = (out * G.to(device)).sum()
+                    elif grad == "sum":
+                        loss = out.sum()
+                    else:
+                        loss = out.sum() * 0.75
+                    if step == 1:  # the auxiliary losses too
+                        loss = loss + aux["router_z_loss"] * 0.1 + \
+                            aux["load_balance_loss"] * 0.01 + aux["compute_loss"] * 0.01
+                    if step == 2:  # the auxiliary losses alone
+                        loss = aux["router_z_loss"] + aux["load_balance_loss"]
+                    loss.backward()
+                    grads = [t.grad.clone() if t.grad is not None else None
+                             for t in (x, m.w1, m.w2, m.router.weight)]
+                    steps.append((out.detach().clone(), f_i.clone(),
+                                  aux["router_z_loss"].detach().clone(),
+                                  aux["load_balance_loss"].detach().clone(),
+                                  aux["compute_loss"].detach().clone(), *grads))
+                torch.cuda.synchronize()
+                results[(fused, side)] = steps
+            finally:
+                gg.FUSED_EXPERT_PATH, gg.BACKWARD_SIDE_STREAM = True, None
+    ref = results[(False, False)]
+    for key, steps in results.items():
+        for i, (s_ref, s_got) in enumerate(zip(ref, steps)):
+            for j, (a, b_) in enumerate(zip(s_ref, s_got)):
+                if a is None or b_ is None:
+                    assert a is None and b_ is None, (name, key, i, j)
+                    continue
+                assert bits_equal(a, b_), (name, key, i, j)

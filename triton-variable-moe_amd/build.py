@@ -22,7 +22,7 @@ CSRC = HERE / "csrc"
 OUT = HERE / "triton_moe" / "libvmoe.so"
 OBJ = HERE / "_build"
 SOURCES = ["route.hip", "permute.hip", "permute_f32.hip", "gemm.hip", "gemm_f32.hip", "router.hip",
-           "capi.hip"]
+           "expert.hip", "capi.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -40,6 +40,20 @@ _SIGNATURES = {
     "vmoe_combine": [_vp, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp],
     "vmoe_combine_weight_grad": [_vp, _i64, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _vp],
     "vmoe_routing_weight_grad": [_vp, _i64, _i32, _i64, _vp, _vp, _i64, _vp, _vp],
+    "vmoe_expert_layout": [_i64, _i32, _i32, _i32, _i64, _i64, _i32, _vp],
+    "vmoe_moe_layout": [_i64, _i32, _i32, _i32, _i64, _i64, _vp],
+    "vmoe_moe_forward": [_vp, _i64, _i32, _i32, _i32, _i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp,
+                         _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp],
+    "vmoe_moe_backward": [_vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _i64, _vp, _i64, _vp,
+                          _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
+                          _i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, ctypes.c_size_t,
+                          _vp, _vp],
+    "vmoe_expert_forward": [_vp, _i32, _vp, _i64, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp,
+                            _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp,
+                            _i64, _vp],
+    "vmoe_expert_backward": [_vp, _i64, _i32, _i32, _i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp,
+                             _vp, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
+                             _vp, _vp, _vp, ctypes.c_size_t, _vp, _vp],
     "vmoe_routing_weight_grad_direct": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _i64,
                                         _i32, _vp, _vp, _vp, _i32, _i64, _i64, _vp, _vp],
     "vmoe_gemm_up_fwd": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp,
@@ -114,6 +128,11 @@ OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_LAUNCH, ERR_WORKSPACE = 0, 1, 2, 3, 4
 ROUNDING = {"up": 0, "down": 1, "nearest": 2}
 ACT_NONE, ACT_RELU_SQUARED, ACT_SWIGLU = 0, 1, 2
 INFO_ROWS, INFO_KEPT, INFO_ERRORS, INFO_LEN = 0, 1, 2, 4
+# Slots of vmoe_expert_layout's saved buffer (enum vmoe_expert_slot).
+(X_BIN_IDS, X_INDICES, X_TPE, X_BINS, X_PADDED_BINS, X_ROW_SRC, X_GATHER_MAP, X_ASSIGNMENT_ROW,
+ X_INFO, X_EXPERT_OFFSETS, X_PADDED_COUNTS, X_ROW_WEIGHT, X_H, X_PRE, X_NSLOTS) = range(15)
+# Slots of vmoe_moe_layout's saved buffer after the expert ones (enum vmoe_moe_slot).
+M_SELECTED, M_WEIGHTS, M_LSE, M_F_I32, M_NSLOTS = range(5)
 ROUTE_BAD_EXPERT_ID, ROUTE_ROW_OVERFLOW = 1, 2
 
 _lib = None
@@ -164,13 +183,21 @@ def set_launch_timer(timer) -> None:
     _launch_timer = timer
 
 
+_FNS: dict = {}
+
+
 def call(name: str, *args) -> None:
+    fn = _FNS.get(name)
+    if fn is None:
+        fn = _FNS[name] = getattr(lib(), name)
     timer = _launch_timer
     if timer is None:
-        check(getattr(lib(), name)(*args), name)
+        status = fn(*args)
+        if status != OK:
+            check(status, name)
         return
     timer.begin(name)
-    status = getattr(lib(), name)(*args)
+    status = fn(*args)
     timer.end(name)
     check(status, name)
 
@@ -180,7 +207,15 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw hipStream_t of the device's current stream (what
+    torch.cuda.current_stream(device).cuda_stream returns, without building
+    a Stream object)."""
+    if not isinstance(device, (torch.device, int)):
+        device = torch.device(device)
+    idx = device.index if isinstance(device, torch.device) else device
+    if idx is None:
+        idx = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 def require_gpu(t: torch.Tensor, what: str = "Input") -> None:

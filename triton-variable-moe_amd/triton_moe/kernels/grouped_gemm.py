@@ -20,6 +20,7 @@ syncs: the kernels find their tiles on the device.
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -162,11 +163,17 @@ def _dw_workspace(m: GemmMeta, hidden: int, device) -> torch.Tensor:
     a launch starts, and every launch leaves them zero, so one zero-filled
     buffer per (device, stream) is kept and reused: calls on one stream run
     in order, and calls on different streams get different buffers."""
-    n = max(int(_lib.lib().vmoe_gemm_dw_workspace_bytes(m.num_experts, hidden, m.max_width,
-                                                        max(m.rows, 1))), 16)
+    return _dw_workspace_bytes(m.num_experts, hidden, m.max_width, m.rows, device,
+                               _lib.stream(device))
+
+
+def _dw_workspace_bytes(E: int, hidden: int, max_width: int, rows: int, device,
+                        stream: int) -> torch.Tensor:
+    """_dw_workspace for the dW GEMMs launched on the raw stream handle `stream`."""
+    n = max(int(_lib.lib().vmoe_gemm_dw_workspace_bytes(E, hidden, max_width,
+                                                        max(rows, 1))), 16)
     device = torch.device(device)
-    key = (device.index if device.index is not None else torch.cuda.current_device(),
-           _lib.stream(device))
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _DW_WORKSPACES.get(key)
     if ws is None or ws.numel() < n:
         # zero_() is a fill kernel, so this also holds under graph capture
@@ -889,9 +896,40 @@ def grouped_gemm_down_autograd(intermediate, w2, expert_token_offsets, expert_we
 
 
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
-# RoutedMoEOp.backward runs its weight-gradient GEMMs on a side stream when
-# True; False keeps every launch on the current stream (per-kernel timing).
-BACKWARD_SIDE_STREAM = True
+# The module's backward runs its weight-gradient GEMMs on a side stream
+# (beside dH and dX) when True, keeps every launch on the current stream
+# when False (per-kernel timing), and decides by size when None: the second
+# stream takes 20 / 65 us off an eager cfg3 / cfg4 step, whose GPU time
+# dominates, but its event hand-overs add 75-80 us of host time to the
+# host-bound cfg1 / cfg2 steps, and graph replays ran slower with it
+# (cfg3 0.808 against 0.783 ms), so it is left out under graph capture.
+BACKWARD_SIDE_STREAM: bool | None = None
+SIDE_STREAM_MIN_WORK = 2 ** 34  # assignments x max expert width x hidden
+
+
+def _use_side_stream(assignments: int, max_width: int, hidden: int) -> bool:
+    if BACKWARD_SIDE_STREAM is not None:
+        return BACKWARD_SIDE_STREAM
+    return (assignments * max_width * hidden >= SIDE_STREAM_MIN_WORK and
+            not torch.cuda.is_current_stream_capturing())
+
+
+_ORDER_EVENTS: dict[int, list] = {}
+
+
+def _order(waiter: torch.cuda.Stream, signaler: torch.cuda.Stream, slot: int) -> None:
+    """waiter waits for the work queued on signaler so far: one of a few
+    reused events per device, recorded on signaler, waited on by waiter
+    (Stream.wait_stream makes a new event every time, about twice the cost).
+    A slot's event is recorded again only after its wait was queued, so
+    reuse never loses a dependency."""
+    idx = signaler.device.index
+    evs = _ORDER_EVENTS.get(idx)
+    if evs is None:
+        evs = _ORDER_EVENTS[idx] = [torch.cuda.Event() for _ in range(3)]
+    ev = evs[slot]
+    ev.record(signaler)
+    waiter.wait_event(ev)
 
 
 def _side_stream(device) -> torch.cuda.Stream:
@@ -904,6 +942,217 @@ def _side_stream(device) -> torch.cuda.Stream:
         st = torch.cuda.Stream(device=idx)
         _SIDE_STREAMS[idx] = st
     return st
+
+
+# The module's bf16 expert path as one library call per direction
+# (ExpertPathOp); False: one call per kernel (RoutedMoEOp), the same kernels
+# and bits. The per-kernel form also runs whenever a launch timer is set.
+FUSED_EXPERT_PATH = True
+
+_LAYOUTS: dict[tuple, tuple] = {}
+
+
+def expert_layout(T: int, E: int, k: int, block_size: int, hidden: int, max_width: int,
+                  counted: bool) -> tuple:
+    """(saved_bytes, fwd_scratch_bytes, bwd_scratch_bytes, rows_bound, slot offsets) of
+    vmoe_expert_forward / _backward, cached per shape."""
+    key = (T, E, k, block_size, hidden, max_width, counted)
+    lay = _LAYOUTS.get(key)
+    if lay is None:
+        out = (ctypes.c_int64 * (4 + _lib.X_NSLOTS))()
+        _lib.check(_lib.lib().vmoe_expert_layout(T, E, k, block_size, hidden, max_width,
+                                                  int(counted), out), "vmoe_expert_layout")
+        lay = _LAYOUTS[key] = (out[0], out[1], out[2], out[3], tuple(out[4:]))
+    return lay
+
+
+class ExpertPathOp(torch.autograd.Function):
+    """RoutedMoEOp's forward and backward, each as one library call
+    (vmoe_expert_forward / vmoe_expert_backward): the same kernels in the
+    same order with the same operands, so the same bits, without the
+    per-kernel wrappers, allocations and stream hand-overs in Python.
+    Buffers: one `saved` block (routing arrays, row weights, H', PRE) kept
+    for the backward and one scratch block per direction.
+
+    forward(x_flat, w1, w2, weights, selected, route_ws, widths, ewo, top_k,
+    block_size, max_width, weights_grad) -> (out, tokens_per_expert): weights
+    bf16 [T k] (differentiated when weights_grad), selected int32/int64
+    [T k], route_ws the counted routing workspace or None."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, x_flat, w1, w2, weights, selected, route_ws, widths, ewo, top_k,
+                block_size, max_width, weights_grad):
+        T, d = x_flat.shape
+        E = widths.numel()
+        dev = x_flat.device
+        x_flat = _bf16(x_flat, "TritonMoEMLP x")
+        saved_b, fwd_b, _, rows, slots = expert_layout(T, E, top_k, block_size, d, max_width,
+                                                       route_ws is not None)
+        saved = torch.empty(saved_b, dtype=torch.uint8, device=dev)
+        scratch = torch.empty(fwd_b, dtype=torch.uint8, device=dev)
+        out = torch.empty(T, d, dtype=torch.bfloat16, device=dev)
+        sel = selected.reshape(-1)
+        if T == 0:
+            saved.zero_()  # no routing runs: zero counts
+        _lib.call("vmoe_expert_forward", sel.data_ptr(), int(sel.dtype == torch.int64),
+                  weights.data_ptr(), T, E, top_k, block_size, _lib.ptr(route_ws),
+                  0 if route_ws is None else route_ws.numel() * route_ws.element_size(),
+                  x_flat.data_ptr(), x_flat.stride(0), w1.data_ptr(), w1.stride(0),
+                  w2.data_ptr(), w2.stride(0), ewo.data_ptr(), widths.data_ptr(), d, max_width,
+                  saved.data_ptr(), scratch.data_ptr(), out.data_ptr(), out.stride(0),
+                  _lib.stream(dev))
+        o = slots[_lib.X_TPE]
+        tpe = saved[o:o + 4 * E].view(torch.int32)
+        ctx.save_for_backward(x_flat, w1, w2, widths, ewo, saved)
+        ctx.dims = (T, E, top_k, block_size, d, max_width, rows)
+        ctx.weights_grad = bool(weights_grad)
+        ctx.mark_non_differentiable(tpe)
+        return out, tpe
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, grad_out, _grad_tpe):
+        x_flat, w1, w2, widths, ewo, saved = ctx.saved_tensors
+        T, E, k, b, d, max_width, rows = ctx.dims
+        dev = grad_out.device
+        _, _, bwd_b, _, _ = expert_layout(T, E, k, b, d, max_width, True)
+        if (grad_out.dtype == torch.bfloat16 and T > 0 and grad_out.stride(0) == 0 and
+                grad_out.stride(1) == 0):
+            g, ldg, gs = _ones_row(d, dev), 0, grad_out  # c * out.sum(): ones, scaled by c
+        else:
+            (g, ldg), gs = _token_source(grad_out), None
+        grad_x = torch.empty(T, d, dtype=torch.bfloat16, device=dev)
+        grad_w1 = torch.empty_like(w1)
+        grad_w2 = torch.empty_like(w2)
+        grad_w = (torch.empty(T * k, dtype=torch.bfloat16, device=dev) if ctx.weights_grad
+                  and ctx.needs_input_grad[3] else None)
+        scratch = torch.empty(bwd_b, dtype=torch.uint8, device=dev)
+        main = torch.cuda.current_stream(dev)
+        side = _side_stream(dev) if _use_side_stream(T * k, max_width, d) else None
+        ws = _dw_workspace_bytes(E, d, max_width, rows, dev,
+                                 side.cuda_stream if side is not None else main.cuda_stream)
+        _lib.call("vmoe_expert_backward", saved.data_ptr(), T, E, k, b, x_flat.data_ptr(),
+                  x_flat.stride(0), w1.data_ptr(), w1.stride(0), w2.data_ptr(), w2.stride(0),
+                  ewo.data_ptr(), widths.data_ptr(), d, max_width, g.data_ptr(), ldg,
+                  _lib.ptr(gs), grad_x.data_ptr(), grad_x.stride(0), grad_w1.data_ptr(),
+                  grad_w1.stride(0), grad_w2.data_ptr(), grad_w2.stride(0), _lib.ptr(grad_w),
+                  scratch.data_ptr(), ws.data_ptr(), ws.numel(), main.cuda_stream,
+                  None if side is None else side.cuda_stream)
+        return (grad_x, grad_w1, grad_w2, grad_w, None, None, None, None, None, None, None,
+                None)
+
+
+def moe_layout(T: int, E: int, k: int, block_size: int, hidden: int, max_width: int) -> tuple:
+    """(saved_bytes, fwd_scratch_bytes, bwd_scratch_bytes, rows_bound, expert slot
+    offsets, layer slot offsets, counted) of vmoe_moe_forward / _backward, cached."""
+    key = ("moe", T, E, k, block_size, hidden, max_width)
+    lay = _LAYOUTS.get(key)
+    if lay is None:
+        n = 5 + _lib.X_NSLOTS + _lib.M_NSLOTS
+        out = (ctypes.c_int64 * n)()
+        _lib.check(_lib.lib().vmoe_moe_layout(T, E, k, block_size, hidden, max_width, out),
+                   "vmoe_moe_layout")
+        xs = 4 + _lib.X_NSLOTS
+        lay = _LAYOUTS[key] = (out[0], out[1], out[2], out[3], tuple(out[4:xs]),
+                               tuple(out[xs:xs + _lib.M_NSLOTS]), bool(out[n - 1]))
+    return lay
+
+
+class MoELayerOp(torch.autograd.Function):
+    """TritonMoEMLP.forward after the router Linear as one autograd node and
+    one library call per direction (vmoe_moe_forward / vmoe_moe_backward):
+    top-k, routing, the expert path and the auxiliary losses, with the
+    kernels, operands and order of the per-op path (router_topk,
+    ExpertPathOp / RoutedMoEOp, RouterAuxOp, RouterWeightOp), so the same
+    bits.
+
+    forward(logits, x_flat, w1, w2, widths, ewo, coef, wn, top_k, block_size,
+    max_width, normalize, weight_grad) -> (out, z_loss, load_balance_loss,
+    compute_loss, f_i). The logits get the auxiliary losses' gradient and,
+    with weight_grad, the routing weights' chain; f_i has none."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, logits, x_flat, w1, w2, widths, ewo, coef, wn, top_k, block_size,
+                max_width, normalize, weight_grad):
+        T, d = x_flat.shape
+        E = widths.numel()
+        dev = x_flat.device
+        x_flat = _bf16(x_flat, "TritonMoEMLP x")
+        if not logits.is_contiguous() or logits.data_ptr() % 16:
+            logits = logits.contiguous().clone()
+        saved_b, fwd_b, _, rows, _, _, _ = moe_layout(T, E, top_k, block_size, d, max_width)
+        saved = torch.empty(saved_b, dtype=torch.uint8, device=dev)
+        scratch = torch.empty(fwd_b, dtype=torch.uint8, device=dev)
+        out = torch.empty(T, d, dtype=torch.bfloat16, device=dev)
+        z = torch.empty((), dtype=torch.bfloat16, device=dev)
+        losses = torch.empty(2, dtype=torch.float32, device=dev)
+        f_i = torch.empty(E, dtype=torch.bfloat16, device=dev)
+        if T == 0:
+            z.zero_(), losses.zero_(), f_i.zero_()
+        _lib.call("vmoe_moe_forward", logits.data_ptr(), T, E, top_k, int(bool(normalize)),
+                  block_size, x_flat.data_ptr(), x_flat.stride(0), w1.data_ptr(), w1.stride(0),
+                  w2.data_ptr(), w2.stride(0), ewo.data_ptr(), widths.data_ptr(), d, max_width,
+                  coef.data_ptr(), wn.data_ptr(), saved.data_ptr(), scratch.data_ptr(),
+                  out.data_ptr(), out.stride(0), z.data_ptr(), losses.data_ptr(), f_i.data_ptr(),
+                  _lib.stream(dev))
+        ctx.save_for_backward(logits, x_flat, w1, w2, widths, ewo, coef, wn, saved)
+        ctx.dims = (T, E, top_k, block_size, d, max_width, rows, int(bool(normalize)))
+        ctx.weight_grad = bool(weight_grad)
+        ctx.mark_non_differentiable(f_i)
+        # unused outputs arrive as None (not zeros), so a loss that leaves out
+        # the auxiliary losses gives the router no gradient, as in the reference
+        ctx.set_materialize_grads(False)
+        return out, z, losses[0], losses[1], f_i
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, grad_out, g_z, g_lb, g_cl, _g_fi):
+        logits, x_flat, w1, w2, widths, ewo, coef, wn, saved = ctx.saved_tensors
+        T, E, k, b, d, max_width, rows, norm = ctx.dims
+        dev = logits.device
+        _, _, bwd_b, _, _, _, _ = moe_layout(T, E, k, b, d, max_width)
+
+        def scalar(g):
+            return None if g is None else g.detach().to(torch.float32).reshape(()).contiguous()
+
+        gz, glb, gcl = scalar(g_z), scalar(g_lb), scalar(g_cl)
+        want_x = grad_out is not None and any(ctx.needs_input_grad[1:4])
+        want_logits = ctx.needs_input_grad[0] and (
+            gz is not None or glb is not None or gcl is not None or (ctx.weight_grad and want_x))
+        grad_x = grad_w1 = grad_w2 = grad_logits = None
+        g = gs = None
+        ldg = 0
+        if want_x:
+            if (grad_out.dtype == torch.bfloat16 and T > 0 and grad_out.stride(0) == 0 and
+                    grad_out.stride(1) == 0):
+                g, ldg, gs = _ones_row(d, dev), 0, grad_out  # c * out.sum(): ones times c
+            else:
+                (g, ldg), gs = _token_source(grad_out), None
+            grad_x = torch.empty(T, d, dtype=torch.bfloat16, device=dev)
+            grad_w1 = torch.empty_like(w1)
+            grad_w2 = torch.empty_like(w2)
+        if want_logits:
+            grad_logits = torch.empty(T, E, dtype=torch.bfloat16, device=dev)
+        if not want_x and not want_logits:
+            return (None,) * 13
+        scratch = torch.empty(bwd_b, dtype=torch.uint8, device=dev)
+        main = torch.cuda.current_stream(dev)
+        side = _side_stream(dev) if _use_side_stream(T * k, max_width, d) else None
+        ws = _dw_workspace_bytes(E, d, max_width, rows, dev,
+                                 side.cuda_stream if side is not None else main.cuda_stream)
+        _lib.call("vmoe_moe_backward", saved.data_ptr(), logits.data_ptr(), T, E, k, norm, b,
+                  x_flat.data_ptr(), x_flat.stride(0), w1.data_ptr(), w1.stride(0),
+                  w2.data_ptr(), w2.stride(0), ewo.data_ptr(), widths.data_ptr(), d, max_width,
+                  coef.data_ptr(), wn.data_ptr(), _lib.ptr(g), ldg, _lib.ptr(gs), _lib.ptr(gz),
+                  _lib.ptr(glb), _lib.ptr(gcl), int(ctx.weight_grad), _lib.ptr(grad_x),
+                  d, _lib.ptr(grad_w1), w1.stride(0), _lib.ptr(grad_w2), w2.stride(0),
+                  _lib.ptr(grad_logits), scratch.data_ptr(), ws.data_ptr(), ws.numel(),
+                  main.cuda_stream, None if side is None else side.cuda_stream)
+        return (grad_logits, grad_x, grad_w1, grad_w2) + (None,) * 9
 
 
 class RoutedMoEOpF32(torch.autograd.Function):
@@ -1014,8 +1263,10 @@ class RoutedMoEOp(torch.autograd.Function):
         # fewer than the CUs; the other stream's workgroups take the CUs
         # those tails leave idle.
         main = torch.cuda.current_stream(grad_out.device)
-        side = _side_stream(grad_out.device) if BACKWARD_SIDE_STREAM else main
-        side.wait_stream(main)
+        side = (_side_stream(grad_out.device)
+                if _use_side_stream(ctx.top_k * x_flat.shape[0], m.max_width, d) else main)
+        if side is not main:
+            _order(side, main, 0)
         row_dot = None
         if ctx.weights_shape is not None and ctx.needs_input_grad[9]:
             nblk = (m.max_width + 63) // 64
@@ -1025,12 +1276,14 @@ class RoutedMoEOp(torch.autograd.Function):
                          row_dot=row_dot)
         with torch.cuda.stream(side):
             grad_w2 = down_bwd_dw(grad_out, h, w2, m, d, gather_map=gm)
-        side.wait_stream(main)
+        if side is not main:
+            _order(side, main, 1)
         with torch.cuda.stream(side):
             grad_w1 = up_bwd_dw(ga, x_flat, w1, m, d, gm)
         grad_xg = up_bwd_dx(ga, w1, m, d)
         grad_x = combine_rows(grad_xg, ar, ctx.top_k, x_flat.shape[0])
-        main.wait_stream(side)
+        if side is not main:
+            _order(main, side, 2)
         # Cross-stream lifetimes for the caching allocator: main's tensors
         # read on the side stream, the side stream's results used on main.
         # (Under graph capture the graph's private pool keeps them alive.)

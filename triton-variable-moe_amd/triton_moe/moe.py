@@ -36,8 +36,9 @@ from .kernels import (
 from . import _lib
 from .kernels.fused_cumsum import route_device
 from .kernels.gather import combine_rows
-from .kernels.grouped_gemm import (GemmMeta, RoutedMoEOp, RoutedMoEOpF32, down_fwd,
-                                   f32_down_fwd, f32_up_fwd, up_fwd)
+from .kernels import grouped_gemm as gg
+from .kernels.grouped_gemm import (ExpertPathOp, GemmMeta, MoELayerOp, RoutedMoEOp,
+                                   RoutedMoEOpF32, down_fwd, f32_down_fwd, f32_up_fwd, up_fwd)
 from .kernels.router import RouterAuxOp, RouterLinear, RouterWeightOp, router_topk
 
 
@@ -199,6 +200,11 @@ class TritonMoEMLP(nn.Module):
         if self.w1.dtype == torch.float32:
             return self._experts_f32(x_flat, top_k_weights_flat, selected_experts_flat,
                                      route_ws)
+        if gg.FUSED_EXPERT_PATH and _lib._launch_timer is None:
+            return ExpertPathOp.apply(x_flat, self.w1, self.w2, top_k_weights_flat,
+                                      selected_experts_flat, route_ws, self.expert_widths_t,
+                                      self.expert_weight_offsets_t, k, self.block_size,
+                                      self.max_expert_width, top_k_weights_flat.requires_grad)
         # Pad rows of the row map are -1 (the GEMMs' fused gather reads zeros
         # for them); row_weight holds each row's routing weight.
         r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
@@ -235,9 +241,20 @@ class TritonMoEMLP(nn.Module):
         self, x: torch.Tensor
     ) -> tuple[torch.Tensor, dict[str, torch.Tensor] | None, torch.Tensor | None]:
         """x [batch, seq, n_embd] -> (output [batch, seq, n_embd], aux_loss dict, f_i)."""
-        batch_size, _seq_len, _n_embd = x.shape
-        x_flat = rearrange(x, "b s d -> (b s) d")
+        batch_size, seq_len, n_embd = x.shape
+        x_flat = x.reshape(batch_size * seq_len, n_embd)  # rearrange "b s d -> (b s) d"
         router_logits = self.router(x_flat)
+        if (gg.FUSED_EXPERT_PATH and _lib._launch_timer is None and
+                self.w1.dtype == torch.bfloat16 and router_logits.dtype == torch.bfloat16):
+            # everything after the router Linear: one node, one call each way
+            coef, wn = self._aux_tables(router_logits.device)
+            out, z, lb, cl, f_i = MoELayerOp.apply(
+                router_logits, x_flat, self.w1, self.w2, self.expert_widths_t,
+                self.expert_weight_offsets_t, coef, wn, self.num_active_experts,
+                self.block_size, self.max_expert_width, self.norm_topk_prob,
+                self.config.routing_weight_grad and torch.is_grad_enabled())
+            aux_loss = {"router_z_loss": z, "load_balance_loss": lb, "compute_loss": cl}
+            return out.view(batch_size, seq_len, n_embd), aux_loss, f_i.to(x.dtype)
         state = router_topk(router_logits, self.num_active_experts, self.norm_topk_prob,
                             route_hist=True)
         weights = state.weights
@@ -246,7 +263,7 @@ class TritonMoEMLP(nn.Module):
                                            self.norm_topk_prob)
         output_flat, tokens_per_expert = self._experts(
             x_flat, weights.reshape(-1), state.selected.reshape(-1), state.route_ws)
-        output = rearrange(output_flat, "(b s) d -> b s d", b=batch_size)
+        output = output_flat.view(batch_size, seq_len, n_embd)
         aux_loss, f_i = self._aux(router_logits, state, tokens_per_expert, x.dtype)
         return output, aux_loss, f_i
 
