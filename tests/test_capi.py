@@ -101,6 +101,26 @@ def test_argument_checks_return_invalid_arg():
                                    None) == _lib.ERR_INVALID_ARG
     assert lib.vmoe_router_weight_bwd_f32(1, 8, 4, 8, 2, 1, 1, 1, 1, 2, 1, 8,
                                           None) == _lib.ERR_INVALID_ARG
+    # layer / expert path: layouts, and calls with missing buffers
+    lay = (ctypes.c_int64 * (5 + _lib.X_NSLOTS + _lib.M_NSLOTS))()
+    assert lib.vmoe_moe_layout(16384, 64, 8, 64, 1024, 256, lay) == _lib.OK
+    assert lay[3] == 16384 * 8 + 64 * 63                 # rows bound of a dropless routing
+    assert lay[4 + _lib.X_NSLOTS + _lib.M_NSLOTS] == 1   # the counted top-k applies
+    offs = list(lay[4:4 + _lib.X_NSLOTS + _lib.M_NSLOTS])
+    assert offs == sorted(offs) and all(o % 256 == 0 for o in offs) and offs[-1] < lay[0]
+    assert lay[4 + _lib.X_H] + 2 * lay[3] * 256 <= lay[4 + _lib.X_PRE]
+    assert lib.vmoe_moe_layout(100, 6, 3, 64, 96, 128, lay) == _lib.OK
+    assert lay[4 + _lib.X_NSLOTS + _lib.M_NSLOTS] == 0   # E % 8 != 0: plain top-k
+    assert lib.vmoe_moe_layout(100, 0, 2, 64, 96, 128, lay) == _lib.ERR_INVALID_ARG
+    xl = (ctypes.c_int64 * (4 + _lib.X_NSLOTS))()
+    assert lib.vmoe_expert_layout(128, 4, 2, 128, 64, 256, 1, xl) == _lib.OK
+    assert lib.vmoe_expert_layout(128, 4, 2, 128, 64, 256, 0, xl) == _lib.OK
+    assert lib.vmoe_expert_layout(-1, 4, 2, 128, 64, 256, 0, xl) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_moe_forward(1, 128, 4, 2, 1, 128, 1, 64, 1, 256, 1, 64, 1, 1, 64, 256,
+                                1, 1, None, 1, 1, 64, 1, 1, 1, None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_moe_forward(None, 0, 4, 2, 1, 128, None, 64, None, 256, None, 64, None,
+                                None, 64, 256, None, None, None, None, None, 64, None, None,
+                                None, None) == _lib.OK                    # no tokens
     # its logit gradient: both or neither index arrays, k above one wave
     assert lib.vmoe_router_weight_bwd(1, 8, 4, 8, 2, 1, 1, 1, 1, 2, 1, 8,
                                       None) == _lib.ERR_INVALID_ARG
