@@ -14,8 +14,8 @@
 // the GEMMs. This is the path for fp32 callers; the bf16 module path never
 // uses it.
 //
-// Tiles: 64 x 64 outputs per 256-thread workgroup, 4 x 4 per thread, k steps
-// of 16 staged in LDS, each thread loading runs of 4 consecutive elements
+// Tiles: 64 x 64 outputs per 256-thread workgroup, 4 x 4 per thread (4
+// consecutive rows by 4 consecutive columns), k steps of 16 staged in LDS, each thread loading runs of 4 consecutive elements
 // (16-byte loads where the address is aligned and the run in range). Workgroups stride over the experts' tiles in order,
 // read from the metadata on the device (no host sync).
 #include <algorithm>
@@ -259,9 +259,9 @@ __device__ __forceinline__ void stage(float (*lds)[kPad], Fn&& run) {
 // own instance, so the other forms do not carry its registers.
 template <int F, bool GLU>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_f32_kernel(F32Args p) {
-  __shared__ float As[kBK][kPad];
-  __shared__ float Bs[kBK][kPad];
-  __shared__ float Us[GLU ? kBK : 1][kPad];  // SwiGLU up half
+  __shared__ __align__(16) float As[kBK][kPad];
+  __shared__ __align__(16) float Bs[kBK][kPad];
+  __shared__ __align__(16) float Us[GLU ? kBK : 1][kPad];  // SwiGLU up half
   constexpr bool glu = GLU && F == F_UP_FWD;
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
   int e = 0;
@@ -304,18 +304,20 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f32_kernel(F32Args p) {
       __syncthreads();
 #pragma unroll
       for (int k = 0; k < kBK; ++k) {
-        float a[4], b[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = As[k][ty + 16 * i];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = Bs[k][tx + 16 * j];
+        // each thread's 4 rows / 4 columns are consecutive: one 16-byte LDS
+        // read per operand (the 16 lanes of a row group read 256 contiguous
+        // bytes of B, and share one address of A)
+        const float4 av = *reinterpret_cast<const float4*>(&As[k][4 * ty]);
+        const float4 bv = *reinterpret_cast<const float4*>(&Bs[k][4 * tx]);
+        const float a[4] = {av.x, av.y, av.z, av.w};
+        float b[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
         if constexpr (glu) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) b[j] = Us[k][tx + 16 * j];
+          const float4 uv = *reinterpret_cast<const float4*>(&Us[k][4 * tx]);
+          b[0] = uv.x; b[1] = uv.y; b[2] = uv.z; b[3] = uv.w;
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -326,11 +328,11 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f32_kernel(F32Args p) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t m = m0 + ty + 16 * i;
+      const int64_t m = m0 + 4 * ty + i;
       if (m >= q.M) continue;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int64_t n = n0 + tx + 16 * j;
+        const int64_t n = n0 + 4 * tx + j;
         if (n >= q.N) continue;
         const float z = acc[i][j];
         if (F == F_UP_DW) {
