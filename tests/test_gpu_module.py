@@ -585,3 +585,67 @@ def test_fused_expert_path_same_bits_as_per_kernel_path(name, grad, device):
                     assert a is None and b_ is None, (name, key, i, j)
                     continue
                 assert bits_equal(a, b_), (name, key, i, j)
+
+
+@pytest.mark.parametrize("name", ["ref_variable", "cfg2", "cfg4_small"])
+def test_compact_intermediates(name, device):
+    """TritonMoEConfig(compact_intermediates=True): H', PRE and GA per width
+    group, sum_e rows_e w_e elements. The row-tiled GEMMs compute every tile
+    as the padded layout does, so out and x.grad are the same bits; the dW
+    GEMMs cut their K ranges per launch, so w1 / w2 gradients may differ in
+    fp32 summation order (held to the padded run at the ulp level, and to
+    the bf16w oracle normwise). The saved intermediates shrink to the
+    compact size."""
+    from triton_moe.kernels import grouped_gemm as gg
+
+    shapes = dict(CONFIGS, cfg4_small=(1, 4096, 512, [(4, 1024), (8, 512), (4, 256)], 8, 64,
+                                        None))
+    B, S, d, sizes, k, b, _alpha = shapes[name]
+    T = B * S
+    p = make_problem(T, d, sizes, k, b, seed=2, device=device)
+    G = torch.randn(B, S, d, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    res, saved_elems = {}, {}
+    orig = gg.CompactRoutedMoEOp.forward
+
+    def spy(ctx, *a):
+        out = orig(ctx, *a)
+        hs = ctx.to_save[6:]  # the tensors forward passed to save_for_backward: H', PRE
+        saved_elems["compact"] = sum(t.numel() for t in hs)
+        return out
+
+    for compact in (False, True):
+        cfg = TritonMoEConfig(n_embd=d, expert_sizes=sizes, num_active_experts=k, block_size=b,
+                              compact_intermediates=compact)
+        m = TritonMoEMLP(cfg).to(device).to(torch.bfloat16)
+        with torch.no_grad():
+            m.router.weight.copy_(p["wr"])
+            m.w1.copy_(p["w1"])
+            m.w2.copy_(p["w2"])
+        x = p["x"].view(B, S, d).to(device).requires_grad_(True)
+        gg.CompactRoutedMoEOp.forward = staticmethod(spy)
+        try:
+            out, aux, f_i = m(x)
+        finally:
+            gg.CompactRoutedMoEOp.forward = staticmethod(orig)
+        out.backward(G.to(device))
+        res[compact] = (out.detach(), x.grad, m.w1.grad, m.w2.grad, f_i,
+                        aux["load_balance_loss"].detach())
+    a, c = res[False], res[True]
+    assert bits_equal(a[0], c[0]) and bits_equal(a[1], c[1])
+    assert bits_equal(a[4], c[4]) and bits_equal(a[5], c[5])
+    for ga, gc, what in ((a[2], c[2], "w1"), (a[3], c[3], "w2")):
+        st = parity_stats(gc, ga, ga.abs().float() + 1e-30)
+        assert st["ulp1"] >= 0.999 and st["ulp2"] >= 0.9995, (name, what, st)
+    prob = eager.Problem(p["x"].float(), p["w1"].float(), p["w2"].float(), p["widths"],
+                         p["offsets"], p["sel"].cpu(), p["wts"].cpu().float(), b)
+    fb = eager.forward(prob, "bf16w")
+    bb = eager.backward(prob, fb, G.reshape(T, d).float(), "bf16w")
+    assert_close_norm(c[2], bb["grad_w1"], TIGHT, f"{name} compact grad_w1")
+    assert_close_norm(c[3], bb["grad_w2"], TIGHT, f"{name} compact grad_w2")
+    # H' and PRE: 2 x sum over groups of rows_g x w_g, against 2 x rows x max_width padded
+    r = fb["route"]
+    pb = [0] + [int(v) for v in r["padded_bins"]]
+    widths = p["widths"]
+    compact_elems = 2 * sum((pb[e + 1] - pb[e]) * widths[e] for e in range(len(widths)))
+    assert saved_elems["compact"] == compact_elems
+    assert compact_elems < 2 * pb[-1] * max(widths)

@@ -225,13 +225,18 @@ def up_fwd(x, w1, m: GemmMeta, act: int, save_pre: bool, zero_tails: bool,
     return out, pre
 
 
-def down_fwd(h, w2, m: GemmMeta, hidden: int):
+def down_fwd(h, w2, m: GemmMeta, hidden: int, out: torch.Tensor | None = None):
+    """Y_e = H_e @ W2_e; out (nullable): a [rows, hidden] bf16 view to write
+    Y into (the rows the experts cover are written)."""
     h = _bf16(h, "grouped_gemm_down intermediate")
     w2 = _bf16(w2, "grouped_gemm_down w2")
     _need(w2.shape[1] == hidden, "w2 columns must equal hidden_size")
     _need(h.shape[0] >= m.rows and h.shape[1] >= m.max_width,
           "intermediate smaller than [rows, max_expert_width]")
-    y = _alloc(m.rows, hidden, h, not m.full_rows)
+    if out is not None:
+        _need(out.dtype == torch.bfloat16 and out.stride(1) == 1 and out.shape[0] >= m.rows and
+              out.shape[1] == hidden, "out must be bf16 [rows, hidden]")
+    y = out if out is not None else _alloc(m.rows, hidden, h, not m.full_rows)
     if m.rows > 0:
         _lib.call("vmoe_gemm_down_fwd", h.data_ptr(), h.stride(0), w2.data_ptr(), w2.stride(0),
                   y.data_ptr(), y.stride(0), *_meta_args(m), hidden, m.max_width, m.rows,
@@ -255,15 +260,18 @@ def relu2_grad(grad_h: torch.Tensor, pre: torch.Tensor) -> torch.Tensor:
     return ga
 
 
-def up_bwd_dx(ga, w1, m: GemmMeta, hidden: int):
+def up_bwd_dx(ga, w1, m: GemmMeta, hidden: int, out: torch.Tensor | None = None):
     """grad_x in gathered rows = GA_e @ W1_e^T, from GA, the gradient w.r.t. the
-    up projection's pre-activation."""
+    up projection's pre-activation; out as for down_fwd."""
     ga = _bf16(ga, "grouped_gemm_up_backward grad_output")
     w1 = _bf16(w1, "grouped_gemm_up_backward w1")
     _need(w1.shape[0] == hidden, "w1 does not match hidden_size")
     _need(ga.shape[0] >= m.rows and ga.shape[1] >= m.max_width,
           "grad_output smaller than [rows, max_expert_width]")
-    grad_x = _alloc(m.rows, hidden, ga, not m.full_rows)
+    if out is not None:
+        _need(out.dtype == torch.bfloat16 and out.stride(1) == 1 and out.shape[0] >= m.rows and
+              out.shape[1] == hidden, "out must be bf16 [rows, hidden]")
+    grad_x = out if out is not None else _alloc(m.rows, hidden, ga, not m.full_rows)
     if m.rows > 0:
         _lib.call("vmoe_gemm_up_bwd_dx", ga.data_ptr(), ga.stride(0), w1.data_ptr(),
                   w1.stride(0), grad_x.data_ptr(), grad_x.stride(0), *_meta_args(m), hidden,
@@ -271,8 +279,10 @@ def up_bwd_dx(ga, w1, m: GemmMeta, hidden: int):
     return grad_x
 
 
-def up_bwd_dw(ga, x, w1, m: GemmMeta, hidden: int, gather_map: torch.Tensor | None):
-    """grad_w1 = X_e^T @ GA_e, X_e read through gather_map when given."""
+def up_bwd_dw(ga, x, w1, m: GemmMeta, hidden: int, gather_map: torch.Tensor | None,
+              out: torch.Tensor | None = None):
+    """grad_w1 = X_e^T @ GA_e, X_e read through gather_map when given; out
+    (nullable): a tensor like w1 whose experts' columns are written."""
     ga = _bf16(ga, "grouped_gemm_up_backward grad_output")
     x = _bf16(x, "grouped_gemm_up_backward x")
     w1 = _bf16(w1, "grouped_gemm_up_backward w1")
@@ -281,7 +291,12 @@ def up_bwd_dw(ga, x, w1, m: GemmMeta, hidden: int, gather_map: torch.Tensor | No
         _need(x.shape[0] >= m.rows, "x has fewer rows than expert_token_offsets[-1]")
     else:
         _need(gather_map.numel() >= m.rows, "gather_map shorter than the padded row count")
-    grad_w1 = torch.zeros_like(w1) if not m.full_cols else torch.empty_like(w1)
+    if out is not None:
+        _need(out.shape == w1.shape and out.dtype == w1.dtype and out.stride() == w1.stride(),
+              "out must be laid out like w1")
+        grad_w1 = out
+    else:
+        grad_w1 = torch.zeros_like(w1) if not m.full_cols else torch.empty_like(w1)
     dev = ga.device
     gm = None if gather_map is None else _i32(gather_map)
     ws = _dw_workspace(m, hidden, dev)
@@ -378,8 +393,9 @@ def down_bwd_dh(grad_y, w2, m: GemmMeta, hidden: int, zero_tails: bool,
 
 
 def down_bwd_dw(grad_y, h, w2, m: GemmMeta, hidden: int,
-                gather_map: torch.Tensor | None = None):
-    """grad_w2 = H_e^T @ grad_y_e (grad_y through gather_map when given)."""
+                gather_map: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """grad_w2 = H_e^T @ grad_y_e (grad_y through gather_map when given); out
+    (nullable): a tensor like w2 whose experts' rows are written."""
     g, ldg, g_rows, gs = _grad_source(grad_y, m, gather_map)
     h = _bf16(h, "grouped_gemm_down_backward intermediate")
     w2 = _bf16(w2, "grouped_gemm_down_backward w2")
@@ -387,7 +403,12 @@ def down_bwd_dw(grad_y, h, w2, m: GemmMeta, hidden: int,
           "grad_output / w2 do not match hidden_size")
     _need(h.shape[0] >= m.rows and h.shape[1] >= m.max_width,
           "intermediate smaller than [rows, max_expert_width]")
-    grad_w2 = torch.zeros_like(w2) if not m.full_cols else torch.empty_like(w2)
+    if out is not None:
+        _need(out.shape == w2.shape and out.dtype == w2.dtype and out.stride() == w2.stride(),
+              "out must be laid out like w2")
+        grad_w2 = out
+    else:
+        grad_w2 = torch.zeros_like(w2) if not m.full_cols else torch.empty_like(w2)
     gm = None if gather_map is None else _i32(gather_map)
     dev = g.device
     ws = _dw_workspace(m, hidden, dev)
@@ -1153,6 +1174,75 @@ class MoELayerOp(torch.autograd.Function):
                   _lib.ptr(grad_logits), scratch.data_ptr(), ws.data_ptr(), ws.numel(),
                   main.cuda_stream, None if side is None else side.cuda_stream)
         return (grad_logits, grad_x, grad_w1, grad_w2) + (None,) * 9
+
+
+class CompactRoutedMoEOp(torch.autograd.Function):
+    """RoutedMoEOp with its per-row intermediates (H', PRE, GA) stored per
+    width group instead of in one [rows, max_width] block: each group of
+    consecutive experts of one width w_g keeps [rows of the group, w_g], so
+    the three take sum_e rows_e w_e elements instead of rows x max_width
+    (the compact layout the reference's grouped_gemm.py:13-16 leaves for a
+    later version). The kernels are the same, launched once per group on the
+    group's rows (row maps, row weights and outputs as views at the group's
+    first row); Y' and the dX rows stay [rows, hidden] for the combines.
+    Needs the groups' exact row counts, so the caller reads the routing's
+    padded counts back once per forward (TritonMoEConfig.compact_intermediates).
+
+    groups: [(GemmMeta of the group, first row, (first, last) weight rows /
+    columns)], rows: the routed row count. The routing weights get no
+    gradient here."""
+
+    @staticmethod
+    @custom_fwd(device_type="cuda")
+    def forward(ctx, x_flat, w1, w2, groups, gather_map, row_weight, assignment_row, top_k,
+                hidden_size, rows):
+        from .gather import combine_rows
+
+        dev = x_flat.device
+        y = torch.empty(rows, hidden_size, dtype=torch.bfloat16, device=dev)
+        hs, pres = [], []
+        for m, r0, _cols in groups:
+            r1 = r0 + m.rows
+            h, pre = up_fwd(x_flat, w1, m, _lib.ACT_RELU_SQUARED, True, zero_tails=False,
+                            gather_map=gather_map[r0:r1], row_scale=row_weight[r0:r1])
+            down_fwd(h, w2, m, hidden_size, out=y[r0:r1])
+            hs.append(h)
+            pres.append(pre)
+        out = combine_rows(y, assignment_row, top_k, x_flat.shape[0])
+        ctx.save_for_backward(x_flat, w1, w2, gather_map, row_weight, assignment_row, *hs, *pres)
+        ctx.groups = groups
+        ctx.hidden_size = hidden_size
+        ctx.top_k = top_k
+        ctx.rows = rows
+        return out
+
+    @staticmethod
+    @custom_bwd(device_type="cuda")
+    @once_differentiable
+    def backward(ctx, grad_out):
+        from .gather import combine_rows
+
+        x_flat, w1, w2, gm, rw, ar, *rest = ctx.saved_tensors
+        n = len(ctx.groups)
+        hs, pres = rest[:n], rest[n:]
+        d = ctx.hidden_size
+        dev = grad_out.device
+        grad_xg = torch.empty(ctx.rows, d, dtype=torch.bfloat16, device=dev)
+        grad_w1 = torch.empty_like(w1)
+        grad_w2 = torch.empty_like(w2)
+        for (m, r0, (c0, c1)), h, pre in zip(ctx.groups, hs, pres):
+            if m.rows == 0:  # no rows routed to the group: its weight gradients are 0
+                grad_w1[:, c0:c1].zero_()
+                grad_w2[c0:c1].zero_()
+                continue
+            r1 = r0 + m.rows
+            ga = down_bwd_dh(grad_out, w2, m, d, False, pre=pre, gather_map=gm[r0:r1],
+                             row_scale=rw[r0:r1])
+            down_bwd_dw(grad_out, h, w2, m, d, gather_map=gm[r0:r1], out=grad_w2)
+            up_bwd_dx(ga, w1, m, d, out=grad_xg[r0:r1])
+            up_bwd_dw(ga, x_flat, w1, m, d, gm[r0:r1], out=grad_w1)
+        grad_x = combine_rows(grad_xg, ar, ctx.top_k, x_flat.shape[0])
+        return grad_x, grad_w1, grad_w2, None, None, None, None, None, None, None
 
 
 class RoutedMoEOpF32(torch.autograd.Function):

@@ -37,8 +37,9 @@ from . import _lib
 from .kernels.fused_cumsum import route_device
 from .kernels.gather import combine_rows
 from .kernels import grouped_gemm as gg
-from .kernels.grouped_gemm import (ExpertPathOp, GemmMeta, MoELayerOp, RoutedMoEOp,
-                                   RoutedMoEOpF32, down_fwd, f32_down_fwd, f32_up_fwd, up_fwd)
+from .kernels.grouped_gemm import (CompactRoutedMoEOp, ExpertPathOp, GemmMeta, MoELayerOp,
+                                   RoutedMoEOp, RoutedMoEOpF32, down_fwd, f32_down_fwd,
+                                   f32_up_fwd, up_fwd)
 from .kernels.router import RouterAuxOp, RouterLinear, RouterWeightOp, router_topk
 
 
@@ -56,6 +57,12 @@ class TritonMoEConfig:
     # when set, forward() differentiates the output through the routing
     # weights into the router logits.
     routing_weight_grad: bool = False
+    # Not in the reference (its grouped_gemm.py:13-16 plans it for a later
+    # version): keep the expert intermediates per width group, sum_e rows_e w_e
+    # elements instead of rows x max_width, at the cost of one device->host
+    # read of the routing's counts per forward. No effect when every expert
+    # has the same width; not with routing_weight_grad.
+    compact_intermediates: bool = False
 
 
 class TritonMoEMLP(nn.Module):
@@ -84,6 +91,16 @@ class TritonMoEMLP(nn.Module):
                 self.expert_offsets.append(self.expert_offsets[-1] + size)
         self.total_expert_width = self.expert_offsets[-1]
         self.max_expert_width = max(self.expert_widths)
+        # runs of consecutive experts of one width: (first, end, width)
+        self._width_groups = []
+        for e, w in enumerate(self.expert_widths):
+            if self._width_groups and self._width_groups[-1][2] == w:
+                self._width_groups[-1][1] = e + 1
+            else:
+                self._width_groups.append([e, e + 1, w])
+        if config.compact_intermediates and config.routing_weight_grad:
+            raise NotImplementedError(
+                "compact_intermediates does not support routing_weight_grad")
 
         self.router = RouterLinear(config.n_embd, self.num_experts, bias=False)
         self.w1 = nn.Parameter(torch.empty(config.n_embd, self.total_expert_width))
@@ -200,6 +217,9 @@ class TritonMoEMLP(nn.Module):
         if self.w1.dtype == torch.float32:
             return self._experts_f32(x_flat, top_k_weights_flat, selected_experts_flat,
                                      route_ws)
+        if self._compact():
+            return self._experts_compact(x_flat, top_k_weights_flat, selected_experts_flat,
+                                         route_ws)
         if gg.FUSED_EXPERT_PATH and _lib._launch_timer is None:
             return ExpertPathOp.apply(x_flat, self.w1, self.w2, top_k_weights_flat,
                                       selected_experts_flat, route_ws, self.expert_widths_t,
@@ -220,6 +240,33 @@ class TritonMoEMLP(nn.Module):
                                         r.row_weight, r.assignment_row, k, self.config.n_embd,
                                         weights)
         return output_flat, r.tokens_per_expert
+
+    def _compact(self) -> bool:
+        return (self.config.compact_intermediates and len(self._width_groups) > 1 and
+                self.w1.dtype == torch.bfloat16)
+
+    def _experts_compact(self, x_flat, top_k_weights_flat, selected_experts_flat,
+                         route_ws=None):
+        """The expert path with the intermediates per width group
+        (CompactRoutedMoEOp); reads the padded counts back once."""
+        k = self.num_active_experts
+        r = route_device(selected_experts_flat, self.num_experts, k, self.block_size, "up",
+                         map_pad=-1, weights=top_k_weights_flat, workspace=route_ws)
+        eto = [0] + r.padded_bins.cpu().tolist()  # the one device->host read
+        dev = x_flat.device
+        groups = []
+        for e0, e1, w in self._width_groups:
+            r0 = eto[e0]
+            eto_g = torch.tensor([v - r0 for v in eto[e0:e1 + 1]], dtype=torch.int32,
+                                 device=dev)
+            m = GemmMeta(eto_g, self.expert_weight_offsets_t[e0:e1 + 1],
+                         self.expert_widths_t[e0:e1], r.padded_counts[e0:e1], e1 - e0, w,
+                         eto[e1] - r0, full_rows=True, full_cols=False, uniform=True)
+            groups.append((m, r0, (self.expert_offsets[e0], self.expert_offsets[e1])))
+        out = CompactRoutedMoEOp.apply(x_flat, self.w1, self.w2, groups, r.gather_map,
+                                       r.row_weight, r.assignment_row, k, self.config.n_embd,
+                                       eto[-1])
+        return out, r.tokens_per_expert
 
     def _experts_f32(self, x_flat, top_k_weights_flat, selected_experts_flat, route_ws=None):
         """The expert path of a float32 module (RoutedMoEOpF32): the same
@@ -244,7 +291,7 @@ class TritonMoEMLP(nn.Module):
         batch_size, seq_len, n_embd = x.shape
         x_flat = x.reshape(batch_size * seq_len, n_embd)  # rearrange "b s d -> (b s) d"
         router_logits = self.router(x_flat)
-        if (gg.FUSED_EXPERT_PATH and _lib._launch_timer is None and
+        if (gg.FUSED_EXPERT_PATH and _lib._launch_timer is None and not self._compact() and
                 self.w1.dtype == torch.bfloat16 and router_logits.dtype == torch.bfloat16):
             # everything after the router Linear: one node, one call each way
             coef, wn = self._aux_tables(router_logits.device)
