@@ -35,6 +35,10 @@ sys.path.insert(0, str(REPO / "triton-variable-moe_amd"))
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+# The box's measured device copy rate (read + write, 1 GiB, torch copy_;
+# bench.py --ceiling, profiles/practical_ceiling.md): the practical ceiling of
+# a row-copy kernel such as the combine.
+COPY_GBS = 5260.0
 
 CONFIGS = {
     # name: (n_embd, expert_sizes, top_k, tokens, zipf)
@@ -528,7 +532,7 @@ def measure(name, device, steps, warmup, kernel_steps, graph):
         "m": m, "xb": xb, "sel": sel, "info": info, "counts": counts, "flops": flops,
         "ms": ms, "graph_ms": graph_ms, "kern": kern, "gemm_tflops": gemm_tflops,
         "dom": dom, "achieved": achieved, "A": A, "T": T, "d": d, "nw": nw,
-        "W": sum(widths), "perm_gbs": perm_gbs,
+        "W": sum(widths), "perm_gbs": perm_gbs, "perm_us": perm_us,
     }
 
 
@@ -613,6 +617,8 @@ def main():
         "gemm_pct_mfma_peak": round(100 * r["gemm_tflops"] / PEAK_BF16_TFLOPS, 2),
         "permutation_gbs": round(r["perm_gbs"], 1),
         "permutation_pct_hbm_peak": round(100 * r["perm_gbs"] / PEAK_HBM_GBS, 2),
+        "permutation_pct_copy_rate": round(100 * r["perm_gbs"] / COPY_GBS, 2),
+        "permutation_us": round(r["perm_us"], 2),
         "permutation_scope": "both combines + routing (vmoe_route_counted; the per-tile "
                              "expert counts come out of the top-k launch, router_topk_us), "
                              "bytes and time",

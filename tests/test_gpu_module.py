@@ -649,3 +649,22 @@ def test_compact_intermediates(name, device):
     compact_elems = 2 * sum((pb[e + 1] - pb[e]) * widths[e] for e in range(len(widths)))
     assert saved_elems["compact"] == compact_elems
     assert compact_elems < 2 * pb[-1] * max(widths)
+
+
+@pytest.mark.parametrize("mode", ["no_grad", "inference_mode"])
+def test_forward_without_autograd_same_bits(mode, device):
+    """Under torch.no_grad() and torch.inference_mode() the module's forward
+    (one library call after the router Linear) gives the bits of the
+    forward that records the graph, and nothing requires grad."""
+    B, S, d, sizes, k, b, _alpha = CONFIGS["cfg2"]
+    p = make_problem(B * S, d, sizes, k, b, seed=6, device=device)
+    m = _module(p, d, sizes, k, b, device)
+    x = p["x"].view(B, S, d).to(device)
+    out_g, aux_g, f_g = m(x.clone().requires_grad_(True))
+    ctx = torch.no_grad() if mode == "no_grad" else torch.inference_mode()
+    with ctx:
+        out, aux, f_i = m(x)
+    assert not out.requires_grad and not aux["router_z_loss"].requires_grad
+    assert bits_equal(out, out_g.detach()) and bits_equal(f_i, f_g)
+    for key in aux:
+        assert bits_equal(aux[key], aux_g[key].detach()), key
