@@ -378,10 +378,11 @@ OP_OF = {
 
 
 class LaunchTimer:
-    """HIP events recorded on the current (launch) stream right before and
-    after every C-ABI launch of a step, so each kernel is timed where it runs
-    in the real step (after the kernels that precede it, with their caches
-    and write-backs), not in a loop of its own."""
+    """A HIP event pair around every C-ABI launch of a step, bound to the
+    launched kernels' own dispatches (vmoe_set_launch_timing), so each kernel
+    is timed where it runs in the real step (after the kernels that precede
+    it, with their caches and write-backs), not in a loop of its own, and
+    without the gaps that event records between the kernels would add."""
 
     def __init__(self):
         import torch
@@ -395,17 +396,28 @@ class LaunchTimer:
         self.seen = {}
 
     def begin(self, name):
+        from triton_moe import _lib
+
         e0 = self.torch.cuda.Event(enable_timing=True)
+        e1 = self.torch.cuda.Event(enable_timing=True)
+        # recorded once so that the events exist; the entry point's kernels
+        # then record them again on their own dispatch (vmoe_set_launch_timing:
+        # start of the first kernel, end of the last), so the pair times the
+        # kernels and not the event records around them
         e0.record()
-        self.open = e0
+        e1.record()
+        _lib.lib().vmoe_set_launch_timing(e0.cuda_event, e1.cuda_event)
+        self.open = (e0, e1)
 
     def end(self, name):
-        e1 = self.torch.cuda.Event(enable_timing=True)
-        e1.record()
+        from triton_moe import _lib
+
+        _lib.lib().vmoe_set_launch_timing(None, None)
+        e0, e1 = self.open
         n = self.seen.get(name, 0)
         self.seen[name] = n + 1
         ops = OP_OF.get(name, (name,))
-        self.marks.append((ops[min(n, len(ops) - 1)], self.open, e1))
+        self.marks.append((ops[min(n, len(ops) - 1)], e0, e1))
 
 
 def kernel_breakdown(m, xb, steps):

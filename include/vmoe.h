@@ -45,6 +45,14 @@ enum vmoe_info_slot { VMOE_INFO_ROWS = 0, VMOE_INFO_KEPT = 1, VMOE_INFO_ERRORS =
 
 const char* vmoe_status_string(int status);
 int vmoe_version(void);
+/* Measurement hook (no counterpart in the reference; for benchmarks that time
+ * each entry point): while stop_event is non-NULL, every kernel the calling
+ * host thread launches carries the two hipEvent_t handles on its own dispatch
+ * (hipExtLaunchKernelGGL): the first launch records start_event at its start,
+ * each launch records stop_event at its end, so the pair spans the kernels of
+ * the next entry point without the gaps of separate event records. Pass NULL,
+ * NULL to switch it off. VMOE_ERR_INVALID_ARG for a start without a stop. */
+int vmoe_set_launch_timing(void* start_event, void* stop_event);
 /* Largest num_experts vmoe_route accepts. */
 int vmoe_route_max_experts(void);
 

@@ -227,6 +227,14 @@ def test_check_maps_status_to_exceptions():
     _lib.check(_lib.OK, "x")
 
 
+def test_launch_timing_hook_arguments():
+    """vmoe_set_launch_timing: a start event needs a stop event; NULL, NULL
+    switches it off (no GPU call is made)."""
+    lib = _lib.lib()
+    assert lib.vmoe_set_launch_timing(ctypes.c_void_p(8), None) == _lib.ERR_INVALID_ARG
+    assert lib.vmoe_set_launch_timing(None, None) == _lib.OK
+
+
 def test_launch_timer_sees_every_call():
     """The observer hook (bench.py's per-launch timing) is called around each
     entry point, also when the call fails its argument checks."""

@@ -16,3 +16,14 @@ extern "C" const char* vmoe_status_string(int status) {
 }
 
 extern "C" int vmoe_version(void) { return 1; }
+
+namespace vmoe {
+thread_local LaunchTiming g_launch_timing = {nullptr, nullptr};
+}
+
+extern "C" int vmoe_set_launch_timing(void* start_event, void* stop_event) {
+  if (start_event && !stop_event) return VMOE_ERR_INVALID_ARG;
+  vmoe::g_launch_timing.start = reinterpret_cast<hipEvent_t>(start_event);
+  vmoe::g_launch_timing.stop = reinterpret_cast<hipEvent_t>(stop_event);
+  return VMOE_OK;
+}

@@ -224,7 +224,7 @@ extern "C" int vmoe_expert_backward(
   if (row_dot) {
     // blocks at or past an expert's width are not written by the dH GEMM
     const int64_t n = L.cap * L.nblk;
-    hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 4096)),
+    VMOE_LAUNCH(zero_f32_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 4096)),
                        dim3(256), 0, main_s, row_dot, n);
     VMOE_CHECK_LAUNCH();
   }
@@ -418,7 +418,7 @@ extern "C" int vmoe_moe_backward(
                                     top_k, dst, E, stream));
     if (aux) {
       const int64_t n = T * E;
-      hipLaunchKernelGGL(add_bf16_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 4096)),
+      VMOE_LAUNCH(add_bf16_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 4096)),
                          dim3(256), 0, reinterpret_cast<hipStream_t>(stream), grad_logits, dst, n);
       VMOE_CHECK_LAUNCH();
     }

@@ -1849,7 +1849,7 @@ template <int V>
 int launch(Args p, int64_t items_bound, hipStream_t s) {
   if (items_bound <= 0) return VMOE_OK;
   p.grid = Cfg<V>::contig ? lane_grid() : gemm_grid(items_bound);
-  hipLaunchKernelGGL(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
+  VMOE_LAUNCH(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }
@@ -1897,7 +1897,7 @@ int launch_dw(Args p, int64_t tmax, void* ws, size_t ws_bytes, hipStream_t s) {
   if (ws_bytes < dw_workspace<V>(p.grid)) return VMOE_ERR_WORKSPACE;
   p.arrive = reinterpret_cast<uint32_t*>(ws);
   p.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + dw_arrive_bytes(p.grid));
-  hipLaunchKernelGGL(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
+  VMOE_LAUNCH(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
 }
@@ -2026,7 +2026,7 @@ extern "C" int vmoe_glu_grad(const uint16_t* grad_h, int64_t ldgh, const uint16_
   if (E > kMaxExperts || max_width % 8 || ld % 8 || ldo % 8 || ldgh % 8 || !a16(grad_h) ||
       !a16(gate) || !a16(up) || !a16(grad_gu) || max_width > INT32_MAX / 2)
     return VMOE_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(glu_grad_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+  VMOE_LAUNCH(glu_grad_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), grad_h, ldgh, gate, up, ld, grad_gu,
                      ldo, eto, widths, tpe, E, rows, (int)max_width);
   VMOE_CHECK_LAUNCH();
@@ -2043,7 +2043,7 @@ extern "C" int vmoe_relu2_grad(const uint16_t* grad_h, const uint16_t* pre_act, 
     return VMOE_ERR_UNSUPPORTED;
   const int64_t n = rows * (cols / 8);
   const int64_t grid = std::min<int64_t>((n + 255) / 256, 65536);
-  hipLaunchKernelGGL(relu2_grad_kernel, dim3((unsigned)grid), dim3(256), 0,
+  VMOE_LAUNCH(relu2_grad_kernel, dim3((unsigned)grid), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), grad_h, pre_act, ld, grad_act, ldo,
                      rows, cols);
   VMOE_CHECK_LAUNCH();

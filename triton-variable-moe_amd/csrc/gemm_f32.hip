@@ -371,7 +371,7 @@ template <int F, bool GLU = false>
 int f32_launch(const F32Args& p, int64_t bound, hipStream_t s) {
   if (bound <= 0 || p.rows_bound == 0 || p.max_width == 0) return VMOE_OK;  // no work
   const int64_t grid = bound < 2048 ? bound : 2048;
-  hipLaunchKernelGGL((grouped_gemm_f32_kernel<F, GLU>), dim3((unsigned)grid), dim3(kThreads), 0, s,
+  VMOE_LAUNCH((grouped_gemm_f32_kernel<F, GLU>), dim3((unsigned)grid), dim3(kThreads), 0, s,
                      p);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
@@ -434,7 +434,7 @@ extern "C" int vmoe_f32_relu2_grad(const float* grad_h, const float* pre_act, in
   if (!grad_h || !pre_act || !grad_act) return VMOE_ERR_INVALID_ARG;
   const int64_t n = rows * cols;
   const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
-  hipLaunchKernelGGL(f32_relu2_grad_kernel, dim3((unsigned)blocks), dim3(256), 0,
+  VMOE_LAUNCH(f32_relu2_grad_kernel, dim3((unsigned)blocks), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), grad_h, pre_act, ld, grad_act, ldo,
                      rows, cols);
   VMOE_CHECK_LAUNCH();

@@ -482,17 +482,17 @@ extern "C" int vmoe_gather(const uint16_t* x, int64_t x_rows, int64_t ldx,
   const dim3 grid(row_grid(num_rows)), block(kThreads);
   if (vec) {
     if (weights)
-      hipLaunchKernelGGL((gather_kernel<8, true>), grid, block, 0, s, x, x_rows, ldx, row_src,
+      VMOE_LAUNCH((gather_kernel<8, true>), grid, block, 0, s, x, x_rows, ldx, row_src,
                          top_k, weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
     else
-      hipLaunchKernelGGL((gather_kernel<8, false>), grid, block, 0, s, x, x_rows, ldx, row_src,
+      VMOE_LAUNCH((gather_kernel<8, false>), grid, block, 0, s, x, x_rows, ldx, row_src,
                          top_k, weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
   } else {
     if (weights)
-      hipLaunchKernelGGL((gather_kernel<1, true>), grid, block, 0, s, x, x_rows, ldx, row_src,
+      VMOE_LAUNCH((gather_kernel<1, true>), grid, block, 0, s, x, x_rows, ldx, row_src,
                          top_k, weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
     else
-      hipLaunchKernelGGL((gather_kernel<1, false>), grid, block, 0, s, x, x_rows, ldx, row_src,
+      VMOE_LAUNCH((gather_kernel<1, false>), grid, block, 0, s, x, x_rows, ldx, row_src,
                          top_k, weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
   }
   VMOE_CHECK_LAUNCH();
@@ -519,11 +519,11 @@ extern "C" int vmoe_gather_tokens(const uint16_t* x, int64_t ldx,
       1024, std::max<int64_t>(1, (num_rows + kRowsPerBlock * kWave - 1) / (kRowsPerBlock * kWave)));
   const dim3 grid(tok_blocks + pad_blocks), block(kThreads);
   if (weights)
-    hipLaunchKernelGGL((gather_tokens_kernel<true, 2>), grid, block, 0, s, x, ldx,
+    VMOE_LAUNCH((gather_tokens_kernel<true, 2>), grid, block, 0, s, x, ldx,
                        assignment_row, num_tokens, top_k, weights, row_src, out, ldo, num_rows,
                        num_rows_dev, hidden, tok_blocks);
   else
-    hipLaunchKernelGGL((gather_tokens_kernel<false, 2>), grid, block, 0, s, x, ldx,
+    VMOE_LAUNCH((gather_tokens_kernel<false, 2>), grid, block, 0, s, x, ldx,
                        assignment_row, num_tokens, top_k, weights, row_src, out, ldo, num_rows,
                        num_rows_dev, hidden, tok_blocks);
   VMOE_CHECK_LAUNCH();
@@ -544,25 +544,25 @@ extern "C" int vmoe_combine(const uint16_t* y, int64_t y_rows, int64_t ldy,
   const dim3 grid(row_grid(num_tokens)), block(kThreads);
   if (vec && top_k <= 8) {
     if (weights)
-      hipLaunchKernelGGL((combine_k_kernel<8, true, 2>), grid, block, 0, s, y, y_rows, ldy,
+      VMOE_LAUNCH((combine_k_kernel<8, true, 2>), grid, block, 0, s, y, y_rows, ldy,
                          assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
     else
-      hipLaunchKernelGGL((combine_k_kernel<8, false, 2>), grid, block, 0, s, y, y_rows, ldy,
+      VMOE_LAUNCH((combine_k_kernel<8, false, 2>), grid, block, 0, s, y, y_rows, ldy,
                          assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
   } else if (vec) {
     // Two 16-byte chunks per lane cover d <= 1024 in one pass.
     if (weights)
-      hipLaunchKernelGGL((combine_kernel<8, true, 2>), grid, block, 0, s, y, y_rows, ldy,
+      VMOE_LAUNCH((combine_kernel<8, true, 2>), grid, block, 0, s, y, y_rows, ldy,
                          assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
     else
-      hipLaunchKernelGGL((combine_kernel<8, false, 2>), grid, block, 0, s, y, y_rows, ldy,
+      VMOE_LAUNCH((combine_kernel<8, false, 2>), grid, block, 0, s, y, y_rows, ldy,
                          assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
   } else {
     if (weights)
-      hipLaunchKernelGGL((combine_kernel<1, true, 4>), grid, block, 0, s, y, y_rows, ldy,
+      VMOE_LAUNCH((combine_kernel<1, true, 4>), grid, block, 0, s, y, y_rows, ldy,
                          assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
     else
-      hipLaunchKernelGGL((combine_kernel<1, false, 4>), grid, block, 0, s, y, y_rows, ldy,
+      VMOE_LAUNCH((combine_kernel<1, false, 4>), grid, block, 0, s, y, y_rows, ldy,
                          assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
   }
   VMOE_CHECK_LAUNCH();
@@ -584,10 +584,10 @@ extern "C" int vmoe_combine_weight_grad(const uint16_t* grad, int64_t ldg, const
                    aligned16(grad);
   const dim3 grid(row_grid(num_tokens)), block(kThreads);
   if (vec)
-    hipLaunchKernelGGL((combine_wgrad_kernel<8>), grid, block, 0, s, grad, ldg, y, y_rows, ldy,
+    VMOE_LAUNCH((combine_wgrad_kernel<8>), grid, block, 0, s, grad, ldg, y, y_rows, ldy,
                        assignment_row, top_k, grad_weights, num_tokens, hidden);
   else
-    hipLaunchKernelGGL((combine_wgrad_kernel<1>), grid, block, 0, s, grad, ldg, y, y_rows, ldy,
+    VMOE_LAUNCH((combine_wgrad_kernel<1>), grid, block, 0, s, grad, ldg, y, y_rows, ldy,
                        assignment_row, top_k, grad_weights, num_tokens, hidden);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
@@ -605,7 +605,7 @@ extern "C" int vmoe_routing_weight_grad(const float* row_dot, int64_t ld_row_dot
     return VMOE_ERR_INVALID_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t g = std::min<int64_t>((num_assignments + kThreads - 1) / kThreads, 65536);
-  hipLaunchKernelGGL(routing_wgrad_kernel, dim3((unsigned)g), dim3(kThreads), 0, s, row_dot,
+  VMOE_LAUNCH(routing_wgrad_kernel, dim3((unsigned)g), dim3(kThreads), 0, s, row_dot,
                      ld_row_dot, num_blocks, rows, row_weight, assignment_row, num_assignments,
                      grad_weights);
   VMOE_CHECK_LAUNCH();
@@ -628,7 +628,7 @@ extern "C" int vmoe_routing_weight_grad_direct(
     return VMOE_ERR_INVALID_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t g = std::min<int64_t>((num_assignments + kThreads - 1) / kThreads, 65536);
-  hipLaunchKernelGGL(routing_wgrad_direct_kernel, dim3((unsigned)g), dim3(kThreads), 0, s,
+  VMOE_LAUNCH(routing_wgrad_direct_kernel, dim3((unsigned)g), dim3(kThreads), 0, s,
                      grad_y, ldgy, gy_rows, grad_scale, w2, ldw2, pre_act, ld_pre, row_weight,
                      assignment_row, num_assignments, top_k, eto, ewo, widths, num_experts,
                      hidden, rows, grad_weights);
@@ -643,7 +643,7 @@ extern "C" int vmoe_zero_tail_cols(uint16_t* buf, int64_t ld, const int32_t* eto
   if (rows_bound == 0 || max_width == 0) return VMOE_OK;
   if (!buf || !eto || !widths) return VMOE_ERR_INVALID_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(zero_tail_kernel, dim3(row_grid(rows_bound)), dim3(kThreads), 0, s, buf,
+  VMOE_LAUNCH(zero_tail_kernel, dim3(row_grid(rows_bound)), dim3(kThreads), 0, s, buf,
                      ld, eto, widths, E, max_width, rows_bound);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;

@@ -162,10 +162,10 @@ extern "C" int vmoe_combine_f32(const float* y, int64_t y_rows, int64_t ldy,
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(row_grid(num_tokens)), block(kThreads);
   if ((y_rows == 0 || vec4_ok(y, ldy, hidden)) && vec4_ok(out, ldo, hidden))
-    hipLaunchKernelGGL(combine_f32_kernel<4>, grid, block, 0, s, y, y_rows, ldy, assignment_row,
+    VMOE_LAUNCH(combine_f32_kernel<4>, grid, block, 0, s, y, y_rows, ldy, assignment_row,
                        weights, top_k, out, ldo, num_tokens, hidden);
   else
-    hipLaunchKernelGGL(combine_f32_kernel<1>, grid, block, 0, s, y, y_rows, ldy, assignment_row,
+    VMOE_LAUNCH(combine_f32_kernel<1>, grid, block, 0, s, y, y_rows, ldy, assignment_row,
                        weights, top_k, out, ldo, num_tokens, hidden);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
@@ -184,10 +184,10 @@ extern "C" int vmoe_gather_f32(const float* x, int64_t x_rows, int64_t ldx,
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(row_grid(num_rows)), block(kThreads);
   if ((x_rows == 0 || vec4_ok(x, ldx, hidden)) && vec4_ok(out, ldo, hidden))
-    hipLaunchKernelGGL(gather_f32_kernel<4>, grid, block, 0, s, x, x_rows, ldx, row_src, top_k,
+    VMOE_LAUNCH(gather_f32_kernel<4>, grid, block, 0, s, x, x_rows, ldx, row_src, top_k,
                        weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
   else
-    hipLaunchKernelGGL(gather_f32_kernel<1>, grid, block, 0, s, x, x_rows, ldx, row_src, top_k,
+    VMOE_LAUNCH(gather_f32_kernel<1>, grid, block, 0, s, x, x_rows, ldx, row_src, top_k,
                        weights, num_weights, out, ldo, num_rows, num_rows_dev, hidden);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;
@@ -206,10 +206,10 @@ extern "C" int vmoe_combine_weight_grad_f32(const float* grad, int64_t ldg, cons
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(row_grid(num_tokens)), block(kThreads);
   if (vec4_ok(grad, ldg, hidden) && (y_rows == 0 || vec4_ok(y, ldy, hidden)))
-    hipLaunchKernelGGL(combine_wgrad_f32_kernel<4>, grid, block, 0, s, grad, ldg, y, y_rows, ldy,
+    VMOE_LAUNCH(combine_wgrad_f32_kernel<4>, grid, block, 0, s, grad, ldg, y, y_rows, ldy,
                        assignment_row, top_k, grad_weights, num_tokens, hidden);
   else
-    hipLaunchKernelGGL(combine_wgrad_f32_kernel<1>, grid, block, 0, s, grad, ldg, y, y_rows, ldy,
+    VMOE_LAUNCH(combine_wgrad_f32_kernel<1>, grid, block, 0, s, grad, ldg, y, y_rows, ldy,
                        assignment_row, top_k, grad_weights, num_tokens, hidden);
   VMOE_CHECK_LAUNCH();
   return VMOE_OK;

@@ -492,6 +492,165 @@ __global__ __launch_bounds__(kRouteThreads) void route_fused_kernel(
                row_src, gather_map, row_capacity, assignment_row, row_weight);
 }
 
+// The same launch for E <= 64 experts, with two workgroup barriers instead
+// of the nine of route_fused_kernel: lane e of every wave holds expert e, so
+// each wave runs the scans over experts itself (shuffles, no LDS) and reads
+// the values of its assignments' experts with shuffles. Thread t of
+// workgroup b places assignment b * kTile + t; its rank among equal ids in
+// its wave comes from ballots over the id bits, the counts of the waves
+// before it from an LDS table [wave][expert].
+constexpr int kSmallExperts = kWave;
+static_assert(kTile == kRouteThreads, "one assignment per thread");
+
+__global__ __launch_bounds__(kRouteThreads) void route_small_kernel(
+    const void* __restrict__ sel, int is64, int64_t A, int E, int nbits, int ntiles, int S,
+    int block, int mode, int top_k, RouteWs ws, int32_t* __restrict__ tpe,
+    int32_t* __restrict__ bins, int32_t* __restrict__ padded_bins,
+    int32_t* __restrict__ bin_ids, int32_t* __restrict__ indices,
+    int32_t* __restrict__ row_src, int32_t* __restrict__ gather_map, int32_t map_pad,
+    int64_t row_capacity, int32_t* __restrict__ assignment_row,
+    const uint16_t* __restrict__ weights, float* __restrict__ row_weight,
+    int32_t* __restrict__ info, int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ padded_counts) {
+  __shared__ int32_t wcnt[kRouteWaves][kSmallExperts];  // ids of expert e in wave w
+  __shared__ int32_t cnt_s[kSmallExperts], pre_s[kSmallExperts];
+  __shared__ int32_t any_bad;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int b = blockIdx.x;
+  wcnt[wave][lane] = 0;
+  if (tid == 0) any_bad = 0;
+  const int64_t p = (int64_t)b * kTile + tid;
+  int32_t e = -1;
+  uint16_t wv = 0;
+  if (p < A) {
+    const int64_t ev = load_sel(sel, is64, p);
+    if (row_weight) wv = weights[p];
+    e = ev >= 0 && ev < E ? (int32_t)ev : -1;
+  }
+  // Totals and this tile's prefix per expert, G lanes per expert (as in
+  // route_fused_kernel); workgroup 0 also collects the bad-id flags.
+  int G = kWave;
+  while (G > 1 && G * E > kRouteThreads) G >>= 1;
+  const int j = tid & (G - 1), ex = tid / G;
+  const int ncols = ntiles * S, bcol = b * S;
+  int32_t tot = 0, pre = 0;
+  if (ex < E) {
+    const int32_t* c = ws.counts + (int64_t)ex * ncols;
+    int t = j;
+    for (; t + 15 * G < ncols; t += 16 * G) {
+      int32_t v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = c[t + u * G];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        tot += v[u];
+        pre += t + u * G < bcol ? v[u] : 0;
+      }
+    }
+#pragma unroll 8
+    for (; t < ncols; t += G) {
+      const int32_t v = c[t];
+      tot += v;
+      pre += t < bcol ? v : 0;
+    }
+  }
+  bool bad = false;
+  if (b == 0)
+    for (int t = tid; t < ncols; t += kRouteThreads) bad |= ws.bad[t] != 0;
+  __syncthreads();  // wcnt zeroed
+  for (int off = G / 2; off > 0; off >>= 1) {
+    tot += __shfl_xor(tot, off, kWave);
+    pre += __shfl_xor(pre, off, kWave);
+  }
+  if (ex < E && j == 0) {
+    cnt_s[ex] = tot;
+    pre_s[ex] = pre;
+  }
+  if (bad) any_bad = 1;
+  // Rank among the equal ids of this wave; the lowest lane of each id
+  // records the id's count in this wave.
+  const bool valid = e >= 0;
+  const int ee = valid ? e : 0;
+  uint64_t same = ballot64(valid);
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool on = (ee >> bit) & 1;
+    const uint64_t ones = ballot64(valid && on);
+    same &= on ? ones : ~ones;
+  }
+  const int rank = lanes_below(same);
+  if (valid && rank == 0) wcnt[wave][ee] = __popcll(same);
+  __syncthreads();
+
+  // Per expert (lane x = expert x): count, rounded count, kept, and the
+  // exclusive scans over experts of all three.
+  const int32_t cx = lane < E ? cnt_s[lane] : 0;
+  const int32_t px = lane < E ? pre_s[lane] : 0;
+  const int32_t rx = lane < E ? round_count(cx, block, mode) : 0;
+  const int32_t kx = min(cx, rx);
+  const int32_t ic = wave_inclusive_scan(cx), ik = wave_inclusive_scan(kx),
+                ir = wave_inclusive_scan(rx);
+  const int32_t bsx = ik - kx, psx = ir - rx;
+  (void)ic;
+  // Counts of expert e in the waves before this one.
+  int32_t before = 0;
+  for (int w = 0; w < wave; ++w) before += wcnt[w][ee];
+  const int32_t pre_e = __shfl(px, ee, kWave), kept_e = __shfl(kx, ee, kWave);
+  const int32_t bs_e = __shfl(bsx, ee, kWave), ps_e = __shfl(psx, ee, kWave);
+  if (valid) {
+    const int32_t q = pre_e + before + rank;  // rank inside expert e
+    if (q < kept_e) {
+      const int32_t i = bs_e + q;
+      const int64_t row = (int64_t)ps_e + q;
+      bin_ids[i] = e;
+      indices[i] = (int32_t)p;
+      assignment_row[p] = (int32_t)row;
+      if (row < row_capacity) {
+        row_src[row] = (int32_t)p;
+        gather_map[row] = (int32_t)(p / top_k);
+        if (row_weight) row_weight[row] = __uint_as_float((uint32_t)wv << 16);
+      }
+    } else {
+      assignment_row[p] = -1;
+    }
+  }
+  if (b == 0 && wave == 0) {
+    if (lane < E) {
+      tpe[lane] = cx;
+      bins[lane] = ik;
+      padded_bins[lane] = ir;
+      // The module's expert_token_offsets = [0, padded_bins] and padded
+      // tokens_per_expert = diff(padded_bins) (moe.py:193-202).
+      if (expert_offsets) {
+        expert_offsets[lane + 1] = ir;
+        if (lane == 0) expert_offsets[0] = 0;
+      }
+      if (padded_counts) padded_counts[lane] = rx;
+    }
+    const int32_t tot_k = __shfl(ik, kWave - 1, kWave), tot_r = __shfl(ir, kWave - 1, kWave);
+    if (lane == 0) {
+      int32_t err = any_bad ? (int32_t)VMOE_ROUTE_BAD_EXPERT_ID : 0;
+      if ((int64_t)tot_r > row_capacity) err |= (int32_t)VMOE_ROUTE_ROW_OVERFLOW;
+      info[VMOE_INFO_ROWS] = tot_r;
+      info[VMOE_INFO_KEPT] = tot_k;
+      info[VMOE_INFO_ERRORS] = err;
+      info[3] = 0;
+    }
+  }
+  // Pad rows [ps + kept, ps + rounded) of the experts this workgroup owns.
+  for (int x = b + (int)gridDim.x * wave; x < E; x += (int)gridDim.x * kRouteWaves) {
+    const int32_t kept_x = __shfl(kx, x, kWave), rnd_x = __shfl(rx, x, kWave);
+    const int32_t ps_x = __shfl(psx, x, kWave);
+    for (int32_t q = kept_x + lane; q < rnd_x; q += kWave) {
+      const int64_t row = (int64_t)ps_x + q;
+      if (row < row_capacity) {
+        row_src[row] = -1;
+        gather_map[row] = map_pad;
+        if (row_weight) row_weight[row] = 0.0f;
+      }
+    }
+  }
+}
+
 // Row maps from caller arrays (vmoe_row_maps): init, then place.
 __global__ void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -579,15 +738,24 @@ int route_impl(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_
   const int ntiles = (int)route_ntiles(A);
   RouteWs ws = route_ws(workspace, A, E, S);
   if (ntiles > 0 && !counted) {
-    hipLaunchKernelGGL(route_hist_kernel, dim3(ntiles), dim3(kRouteThreads),
+    VMOE_LAUNCH(route_hist_kernel, dim3(ntiles), dim3(kRouteThreads),
                        sizeof(int32_t) * E, s, sel, is64, A, E, ntiles, ws.counts, ws.bad);
     VMOE_CHECK_LAUNCH();
   }
   int nbits = 1;
   while ((1 << nbits) < E) ++nbits;
   // (route_hist_split keeps the counted case inside these limits)
+  if (E <= kSmallExperts && (int64_t)E * ntiles * S <= kFusedMaxCounts) {
+    VMOE_LAUNCH(route_small_kernel, dim3(std::max(ntiles, 1)), dim3(kRouteThreads), 0, s,
+                       sel, is64, A, E, nbits, ntiles, S, block, rounding, top_k, ws, tpe, bins,
+                       padded_bins, bin_ids, indices, row_src, gather_map, gather_map_pad,
+                       row_capacity, assignment_row, weights, row_weight, info, expert_offsets,
+                       padded_counts);
+    VMOE_CHECK_LAUNCH();
+    return VMOE_OK;
+  }
   if (E <= kFusedMaxExperts && (int64_t)E * ntiles * S <= kFusedMaxCounts) {
-    hipLaunchKernelGGL(route_fused_kernel, dim3(std::max(ntiles, 1)), dim3(kRouteThreads),
+    VMOE_LAUNCH(route_fused_kernel, dim3(std::max(ntiles, 1)), dim3(kRouteThreads),
                        sizeof(int32_t) * (kRouteWaves + 7) * E, s, sel, is64, A, E, nbits,
                        ntiles, S, block, rounding, top_k, ws, tpe, bins, padded_bins, bin_ids,
                        indices, row_src, gather_map, gather_map_pad, row_capacity,
@@ -596,13 +764,13 @@ int route_impl(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_
     VMOE_CHECK_LAUNCH();
     return VMOE_OK;
   }
-  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), sizeof(int32_t) * (4 * E + 1),
+  VMOE_LAUNCH(route_scan_kernel, dim3(1), dim3(kScanThreads), sizeof(int32_t) * (4 * E + 1),
                      s, ws, E, ntiles, block, rounding, tpe, bins, padded_bins, row_src,
                      gather_map, gather_map_pad, row_weight, row_capacity, info,
                      expert_offsets, padded_counts);
   VMOE_CHECK_LAUNCH();
   if (ntiles > 0) {
-    hipLaunchKernelGGL(route_place_kernel, dim3(ntiles), dim3(kRouteThreads),
+    VMOE_LAUNCH(route_place_kernel, dim3(ntiles), dim3(kRouteThreads),
                        sizeof(int32_t) * (kRouteWaves + 1) * E, s, sel, is64, A, E, nbits,
                        ntiles,
                        top_k, ws, bin_ids, indices, row_src, gather_map, row_capacity,
@@ -706,22 +874,22 @@ extern "C" int vmoe_row_maps(const int32_t* indices, const int32_t* bin_ids,
     return VMOE_ERR_INVALID_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (row_src && num_rows > 0) {
-    hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for(num_rows, 256)), dim3(256), 0, s, row_src,
+    VMOE_LAUNCH(fill_i32_kernel, dim3(grid_for(num_rows, 256)), dim3(256), 0, s, row_src,
                        num_rows, -1);
     VMOE_CHECK_LAUNCH();
   }
   if (gather_map && num_rows > 0) {
-    hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for(num_rows, 256)), dim3(256), 0, s,
+    VMOE_LAUNCH(fill_i32_kernel, dim3(grid_for(num_rows, 256)), dim3(256), 0, s,
                        gather_map, num_rows, 0);
     VMOE_CHECK_LAUNCH();
   }
   if (assignment_row && num_assignments > 0) {
-    hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for(num_assignments, 256)), dim3(256), 0, s,
+    VMOE_LAUNCH(fill_i32_kernel, dim3(grid_for(num_assignments, 256)), dim3(256), 0, s,
                        assignment_row, num_assignments, -1);
     VMOE_CHECK_LAUNCH();
   }
   if (num_sorted > 0) {
-    hipLaunchKernelGGL(row_maps_place_kernel, dim3(grid_for(num_sorted, 256)), dim3(256), 0, s,
+    VMOE_LAUNCH(row_maps_place_kernel, dim3(grid_for(num_sorted, 256)), dim3(256), 0, s,
                        indices, bin_ids, bins, padded_bins, num_sorted, E, top_k, num_rows,
                        num_assignments, row_src, gather_map, assignment_row);
     VMOE_CHECK_LAUNCH();

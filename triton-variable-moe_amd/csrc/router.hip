@@ -788,7 +788,7 @@ int topk_group_launch(int G, int nblk, hipStream_t s, const typename RtElt<F32>:
   switch (G) {
 #define VMOE_RT_GRP(GG)                                                                        \
   case GG:                                                                                     \
-    hipLaunchKernelGGL((router_topk_group_kernel<GG, F32>), dim3(nblk), dim3(kGrpThreads), 0, \
+    VMOE_LAUNCH((router_topk_group_kernel<GG, F32>), dim3(nblk), dim3(kGrpThreads), 0, \
                        s,                                                                      \
                        logits, ld, T, E, k, norm, weights, sel32, sel64, probs, lse, partial,   \
                        per, hist_counts, hist_bad, nblk);                                      \
@@ -969,7 +969,7 @@ int router_topk_impl(const typename RtElt<F32>::T* logits, int64_t ld_logits, in
   switch (vpl) {
 #define VMOE_RT_CASE(V)                                                                      \
   case V:                                                                                    \
-    hipLaunchKernelGGL((router_topk_kernel<V, F32>), dim3(nblk), dim3(topk_threads(V)), lds, \
+    VMOE_LAUNCH((router_topk_kernel<V, F32>), dim3(nblk), dim3(topk_threads(V)), lds, \
                        s, logits, ld_logits, num_tokens, num_experts, top_k, normalize,       \
                        weights, selected_i32, selected_i64, probs, lse, partial, per);        \
     break;
@@ -1029,7 +1029,7 @@ int router_aux_impl(const float* partial, int32_t num_partial_rows, int64_t num_
       !p_i || !z_loss || !losses)
     return VMOE_ERR_INVALID_ARG;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(router_aux_kernel<F32>, dim3(1), dim3(kAuxThreads), 0, s, partial,
+  VMOE_LAUNCH(router_aux_kernel<F32>, dim3(1), dim3(kAuxThreads), 0, s, partial,
                      num_partial_rows, num_tokens, num_experts, tokens_per_expert, coef,
                      widths_normalized, f_i, f_i_f32, p_i, z_loss, losses);
   VMOE_CHECK_LAUNCH();
@@ -1054,7 +1054,7 @@ int router_aux_bwd_impl(const typename RtElt<F32>::T* logits, int64_t ld_logits,
   switch (vpl_of(num_experts)) {
 #define VMOE_RB_CASE(V)                                                                       \
   case V:                                                                                     \
-    hipLaunchKernelGGL((router_aux_bwd_kernel<V, F32>), dim3((unsigned)g), dim3(kRtThreads),   \
+    VMOE_LAUNCH((router_aux_bwd_kernel<V, F32>), dim3((unsigned)g), dim3(kRtThreads),   \
                        0, s, logits, ld_logits, num_tokens, num_experts, lse, f_i_f32, coef,   \
                        widths_normalized, grad_z, grad_lb, grad_cl, grad_logits, ld_grad);    \
     break;
@@ -1092,7 +1092,7 @@ int router_weight_bwd_impl(const typename RtElt<F32>::T* logits, int64_t ld_logi
   switch (vpl_of(num_experts)) {
 #define VMOE_RW_CASE(V)                                                                      \
   case V:                                                                                    \
-    hipLaunchKernelGGL((router_weight_bwd_kernel<V, F32>), dim3((unsigned)g),                 \
+    VMOE_LAUNCH((router_weight_bwd_kernel<V, F32>), dim3((unsigned)g),                 \
                        dim3(kRtThreads), 0, s, logits, ld_logits, num_tokens, num_experts,    \
                        top_k, normalize, selected, selected_i64, grad_weights,                \
                        ld_grad_weights, grad_logits, ld_grad);                                \
@@ -1250,7 +1250,7 @@ extern "C" int vmoe_router_logits(const uint16_t* x, int64_t ldx, int64_t num_to
   switch ((num_experts + 31) / 32) {
 #define VMOE_RL_CASE(N)                                                                   \
   case N:                                                                                 \
-    hipLaunchKernelGGL(router_logits_kernel<N>, grid, dim3(kRlThreads), 0, s, x, ldx,      \
+    VMOE_LAUNCH(router_logits_kernel<N>, grid, dim3(kRlThreads), 0, s, x, ldx,      \
                        num_tokens, (int)hidden, weight, ldw, num_experts, logits, ld_logits); \
     break;
     VMOE_RL_CASE(1)

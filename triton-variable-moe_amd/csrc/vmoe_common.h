@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 #include "vmoe.h"
@@ -9,6 +10,33 @@
 #define VMOE_CHECK_LAUNCH()                                   \
   do {                                                        \
     if (hipGetLastError() != hipSuccess) return VMOE_ERR_LAUNCH; \
+  } while (0)
+
+namespace vmoe {
+
+// Dispatch timing (vmoe_set_launch_timing, for measurement): while a stop
+// event is set on the calling host thread, every launch goes through
+// hipExtLaunchKernelGGL with the events bound to the dispatch itself; the
+// first launch takes the start event, every launch the stop event, so the
+// pair spans the kernels of one entry point without the event-record gaps
+// around them.
+struct LaunchTiming {
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+extern thread_local LaunchTiming g_launch_timing;
+
+}  // namespace vmoe
+
+#define VMOE_LAUNCH(K, G, B, SH, S, ...)                                                   \
+  do {                                                                                     \
+    if (::vmoe::g_launch_timing.stop) {                                                    \
+      hipExtLaunchKernelGGL(K, G, B, SH, S, ::vmoe::g_launch_timing.start,                 \
+                            ::vmoe::g_launch_timing.stop, 0, __VA_ARGS__);                 \
+      ::vmoe::g_launch_timing.start = nullptr;                                             \
+    } else {                                                                               \
+      hipLaunchKernelGGL(K, G, B, SH, S, __VA_ARGS__);                                     \
+    }                                                                                      \
   } while (0)
 
 namespace vmoe {

@@ -24,6 +24,7 @@ _i32 = ctypes.c_int32
 _SIGNATURES = {
     "vmoe_status_string": [ctypes.c_int],
     "vmoe_version": [],
+    "vmoe_set_launch_timing": [_vp, _vp],
     "vmoe_route_max_experts": [],
     "vmoe_route_workspace_bytes": [_i64, _i32],
     "vmoe_route": [_vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
