@@ -1195,6 +1195,21 @@ struct Gemm {
     const int rows = pd.mb >= q.M ? 0 : (pd.mb + 32 >= q.M ? 1 : 3);
     pd.mask = (rows << (FM * (NOUT - 1))) | (two ? rows : 0);
     if (pd.mask == 0) return;
+    // The activation is uniform, so it selects one of two straight-line
+    // loops (per-element selects cost two VALU instructions per pair, and a
+    // wave64 VALU instruction four cycles of the SIMD).
+    if (NOUT == 2 && p.act == VMOE_ACT_RELU_SQUARED)
+      stash_units<true>(acc, sc, pd);
+    else
+      stash_units<false>(acc, sc, pd);
+  }
+
+  // Packed bf16 units of the pending tile: PRE = relu(acc) and H = sc *
+  // relu(acc)^2 (R2), or H = sc * acc. Every store goes to a fixed element,
+  // which keeps the pending tile in registers.
+  template <bool R2>
+  __device__ __forceinline__ static void stash_units(const f32x16_t (&acc)[FM][FN],
+                                                     const float (&sc)[FM], Pending& pd) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1204,15 +1219,13 @@ struct Gemm {
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             const float a = acc[i][j][4 * g + 2 * hh], b = acc[i][j][4 * g + 2 * hh + 1];
-            if (NOUT == 2) {
-              // Selects, not branches: every store below goes to a fixed
-              // element, which keeps the pending tile in registers.
-              const bool r2 = p.act == VMOE_ACT_RELU_SQUARED;
-              const float ra = r2 ? fmaxf(a, 0.0f) : a, rb = r2 ? fmaxf(b, 0.0f) : b;
+            if (NOUT == 2 && R2) {
+              const float ra = fmaxf(a, 0.0f), rb = fmaxf(b, 0.0f);
               pd.pk[0][i][j][2 * g + hh] = pack_bf16(ra, rb);
-              pd.pk[NOUT - 1][i][j][2 * g + hh] =
-                  pack_bf16(sc[i] * (r2 ? ra * ra : ra), sc[i] * (r2 ? rb * rb : rb));
+              pd.pk[NOUT - 1][i][j][2 * g + hh] = pack_bf16(sc[i] * (ra * ra), sc[i] * (rb * rb));
             } else {
+              // without relu^2 the up projection's PRE unit is never stored
+              // (pd.mask), so its registers are left as they are
               pd.pk[NOUT - 1][i][j][2 * g + hh] = pack_bf16(sc[i] * a, sc[i] * b);
             }
           }
