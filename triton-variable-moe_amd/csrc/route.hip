@@ -1,5 +1,6 @@
 // Routing on gfx950: stable counting sort of expert ids, histogram, rounded
-// inclusive scans and the padded-row maps, in three launches.
+// inclusive scans and the padded-row maps, in two launches (one after the
+// module's top-k, which writes the histograms; three above 1024 experts).
 //
 // Semantics follow fused_route (triton_moe/kernels/fused_cumsum.py:85-171):
 //   sorted order = torch.sort(selected, stable=True), i.e. by expert id, ties
@@ -13,13 +14,14 @@
 //   padded_bins[e-1] + q, and gather_map[row] = assignment / top_k.
 //
 // Stable counting sort, MI355X style: the assignments are cut into tiles of
-// kTile; launch 1 counts experts per tile in LDS; launch 2 (one workgroup)
-// runs a single flat exclusive scan over counts laid out expert-major
-// [E][tiles], which yields for every (expert, tile) the first sorted position
-// -- expert-major order of the scan is exactly the sort key order; launch 3
-// re-reads each tile and ranks equal ids within a wave with ballots, so the
-// order inside an expert is the original order (stable), without any
-// comparison sort.
+// kTile; launch 1 counts experts per tile in LDS; the placement launch then
+// derives, in every workgroup, the first sorted position of each (expert,
+// tile) from those counts (expert-major order of the prefix is exactly the
+// sort key order), re-reads its tile and ranks equal ids within a wave with
+// ballots, so the order inside an expert is the original order (stable),
+// without any comparison sort (route_small_kernel for E <= 64,
+// route_fused_kernel up to 1024 experts; beyond that a single-workgroup scan
+// launch, route_scan_kernel, and route_place_kernel).
 
 #include <algorithm>
 #include <mutex>
