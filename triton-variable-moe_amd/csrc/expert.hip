@@ -229,21 +229,36 @@ extern "C" int vmoe_expert_backward(
     VMOE_CHECK_LAUNCH();
   }
   // dW2 (needs only G and H') runs on the side stream beside dH; dW1 beside
-  // dX and the combine once GA exists.
+  // dX and the combine once GA exists. With one stream the two GEMMs of each
+  // pair share one launch, on half of the CUs each (gemm_pair_begin).
   if (two) VMOE_TRY(order(side_s, main_s, ev[0]));
-  VMOE_TRY(vmoe_gemm_down_bwd_dh(grad_out, ldg, num_tokens, gmap, grad_scale, w2, ldw2, pre, rw,
+  if (!two) gemm_pair_begin();
+  int st = vmoe_gemm_down_bwd_dh(grad_out, ldg, num_tokens, gmap, grad_scale, w2, ldw2, pre, rw,
                                  ga, max_width, eto, ewo, widths, ptpe, E, hidden, max_width,
-                                 L.cap, row_dot, L.nblk, stream));
-  VMOE_TRY(vmoe_gemm_down_bwd_dw(h, max_width, grad_out, ldg, num_tokens, gmap, grad_scale,
-                                 grad_w2, ldgw2, eto, ewo, widths, ptpe, E, hidden, max_width,
-                                 L.cap, dw_workspace, dw_workspace_bytes,
-                                 reinterpret_cast<vmoe_stream_t>(side_s)));
+                                 L.cap, row_dot, L.nblk, stream);
+  if (st == VMOE_OK)
+    st = vmoe_gemm_down_bwd_dw(h, max_width, grad_out, ldg, num_tokens, gmap, grad_scale, grad_w2,
+                               ldgw2, eto, ewo, widths, ptpe, E, hidden, max_width, L.cap,
+                               dw_workspace, dw_workspace_bytes,
+                               reinterpret_cast<vmoe_stream_t>(side_s));
+  if (!two) {
+    const int st2 = gemm_pair_end();
+    if (st == VMOE_OK) st = st2;
+  }
+  VMOE_TRY(st);
   if (two) VMOE_TRY(order(side_s, main_s, ev[1]));
-  VMOE_TRY(vmoe_gemm_up_bwd_dw(x, ldx, num_tokens, gmap, ga, max_width, grad_w1, ldgw1, eto, ewo,
-                               widths, ptpe, E, hidden, max_width, L.cap, dw_workspace,
-                               dw_workspace_bytes, reinterpret_cast<vmoe_stream_t>(side_s)));
-  VMOE_TRY(vmoe_gemm_up_bwd_dx(ga, max_width, w1, ldw1, gxg, hidden, eto, ewo, widths, ptpe, E,
-                               hidden, max_width, L.cap, stream));
+  if (!two) gemm_pair_begin();
+  st = vmoe_gemm_up_bwd_dw(x, ldx, num_tokens, gmap, ga, max_width, grad_w1, ldgw1, eto, ewo,
+                           widths, ptpe, E, hidden, max_width, L.cap, dw_workspace,
+                           dw_workspace_bytes, reinterpret_cast<vmoe_stream_t>(side_s));
+  if (st == VMOE_OK)
+    st = vmoe_gemm_up_bwd_dx(ga, max_width, w1, ldw1, gxg, hidden, eto, ewo, widths, ptpe, E,
+                             hidden, max_width, L.cap, stream);
+  if (!two) {
+    const int st2 = gemm_pair_end();
+    if (st == VMOE_OK) st = st2;
+  }
+  VMOE_TRY(st);
   VMOE_TRY(vmoe_combine(gxg, L.cap, hidden, arow, nullptr, k, grad_x, ldgx, num_tokens, hidden,
                         stream));
   if (two) VMOE_TRY(order(main_s, side_s, ev[2]));

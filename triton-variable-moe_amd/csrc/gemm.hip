@@ -104,6 +104,7 @@ struct Args {
   float* partial;    // fp32 partial tiles of split tiles (2 slots per workgroup)
   uint32_t* arrive;  // split-K arrival words, kConsumers per workgroup (zero between launches)
   int grid;          // GEMM workgroups
+  int paired;        // 1: one of the two GEMMs of grouped_gemm_pair_kernel (see vblock)
   float* row_dot;    // DOWN_DH with pre: per (row, 64-column block) sum of GH * PRE^2 (nullable)
   int64_t ld_rd;     // its leading dimension (floats)
 };
@@ -429,9 +430,19 @@ struct Range {
   int beg, end, stride, lin, slot;
 };
 
+// The workgroup's index among the p.grid workgroups of its GEMM. A paired
+// launch (grouped_gemm_pair_kernel) deals consecutive groups of 8 workgroups
+// to its two GEMMs in turn, so each GEMM holds p.grid = gridDim.x / 2 of them,
+// the same number on every XCD, and its k-th workgroup still sits on XCD
+// k mod 8.
+__device__ __forceinline__ int vblock(const Args& p) {
+  const int b = blockIdx.x;
+  return p.paired ? ((b >> 4) << 3) | (b & 7) : b;
+}
+
 template <bool CONTIG>
-__device__ __forceinline__ Range item_range(int total, const int* lane_beg) {
-  const int G = gridDim.x, b = blockIdx.x;
+__device__ __forceinline__ Range item_range(const Args& p, int total, const int* lane_beg) {
+  const int G = p.grid, b = vblock(p);
   const int xcd = b & 7, per = G >> 3, j = b >> 3;
   Range r;
   r.lin = xcd * per + j;
@@ -853,7 +864,7 @@ struct Gemm {
     }
     __syncthreads();
     {
-      const int NL = CONTIG ? (int)gridDim.x / kLane : 8;
+      const int NL = CONTIG ? p.grid / kLane : 8;
       for (int l = threadIdx.x; l <= NL; l += kThreads) {
         int item = (int)base;
         if (l == 0 || cbase == 0) {
@@ -1420,7 +1431,7 @@ struct Gemm {
   __device__ static bool split_arrive(const Args& p, const Meta& mt, const Range& rg, int a,
                                       int chunks, int seg_item, f32x16_t (&acc)[FM][FN]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int NL = (int)gridDim.x / kLane, me = rg.lin / kLane, ts = rg.slot;
+    const int NL = p.grid / kLane, me = rg.lin / kLane, ts = rg.slot;
     const int* lb = mt.lane_beg;
     int L0 = me;
     while (L0 > 0 && lb[L0] > a) --L0;
@@ -1647,7 +1658,7 @@ struct Gemm {
       // (measured at cfg3, same box, three runs: up fwd -6 us, dH -1.6 us;
       // on the down projection, with 8 k-steps per item, +14 us).
       const int stagger =
-          (V == UP_FWD || V == UP_GLU || V == DOWN_DH) ? (int)((blockIdx.x >> 3) % (unsigned)gap)
+          (V == UP_FWD || V == UP_GLU || V == DOWN_DH) ? (int)((vblock(p) >> 3) % (unsigned)gap)
                                                        : 0;
       int kt = 0;
       if (pd.mask & 1) load_pre<0>(p, pd, pr);
@@ -1703,7 +1714,7 @@ struct Gemm {
                              lds_char* wins, lds_char* scl) {
     const int total = build_meta(p, mt, (long long*)(char*)ring,
                                  (__attribute__((address_space(3))) int*)(ring + 256));
-    const Range rg = item_range<Cfg<V>::contig>(total, mt.lane_beg);
+    const Range rg = item_range<Cfg<V>::contig>(p, total, mt.lane_beg);
     if (rg.beg >= rg.end) return;
     const int wave = threadIdx.x >> 6;
     if (wave >= kConsumers)
@@ -1713,24 +1724,52 @@ struct Gemm {
   }
 };
 
+// LDS of one GEMM workgroup, carved from one buffer: the DMA ring, the
+// consumers' epilogue scratch, the per-expert tables, the producers' row-map
+// windows (two per wave, for the gathered operands) and the row-factor slots.
 template <int V>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
+struct Lds {
   using G = Gemm<V>;
-  __shared__ __align__(1024) char ring[G::RING];
-  __shared__ __align__(16) char epi[kConsumers * G::EPI_BYTES];
-  __shared__ Meta meta;
-  // Row-map windows of the producers (two per wave), for the T-form gather.
-  constexpr int WIN_BYTES =
+  static constexpr int WIN_BYTES =
       Traits<V>::t_map || Traits<V>::t_map_b || Traits<V>::k_map ? 2 * kProducers * G::kWinBytes
                                                                   : 16;
-  __shared__ __align__(16) char wins[WIN_BYTES];
-  // Per-row output factors, kScaleSlots slots of BM floats.
-  constexpr int SCL_BYTES = G::kScaled ? G::kScaleSlots * G::BM * 4 : 16;
-  __shared__ __align__(16) char scl[SCL_BYTES];
-  static_assert(G::RING + kConsumers * G::EPI_BYTES + sizeof(Meta) + WIN_BYTES + SCL_BYTES <=
-                    160 * 1024,
-                "LDS budget of a gfx950 CU");
-  G::run(p, (lds_char*)ring, meta, (lds_char*)epi, (lds_char*)wins, (lds_char*)scl);
+  static constexpr int SCL_BYTES = G::kScaled ? G::kScaleSlots * G::BM * 4 : 16;
+  static constexpr int up16(int n) { return (n + 15) / 16 * 16; }
+  static constexpr int RING = 0;
+  static constexpr int EPI = RING + up16(G::RING);
+  static constexpr int META = EPI + kConsumers * G::EPI_BYTES;
+  static constexpr int WINS = META + up16((int)sizeof(Meta));
+  static constexpr int SCL = WINS + WIN_BYTES;
+  static constexpr int BYTES = SCL + SCL_BYTES;
+  static_assert(BYTES <= 160 * 1024, "LDS budget of a gfx950 CU");
+  static_assert(G::RING % 1024 == 0, "the ring's stages keep their 1 KiB alignment");
+
+  __device__ static void run(const Args& p, char* lds) {
+    G::run(p, (lds_char*)(lds + RING), *reinterpret_cast<Meta*>(lds + META),
+           (lds_char*)(lds + EPI), (lds_char*)(lds + WINS), (lds_char*)(lds + SCL));
+  }
+};
+
+template <int V>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Args p) {
+  __shared__ __align__(1024) char lds[Lds<V>::BYTES];
+  Lds<V>::run(p, lds);
+}
+
+// Two independent GEMMs in one launch (the backward's dH with dW2, dX with
+// dW1, on small problems): workgroups take the two in turn by groups of 8,
+// so each GEMM runs on half of every XCD's CUs. Beside each other, the
+// tiles left over by one GEMM's last round and the start and end of each
+// launch overlap the other's work, which two launches on one stream leave
+// idle, without the event hand-overs of a second stream.
+template <int V1, int V2>
+__global__ __launch_bounds__(kThreads) void grouped_gemm_pair_kernel(Args p1, Args p2) {
+  constexpr int B = Lds<V1>::BYTES > Lds<V2>::BYTES ? Lds<V1>::BYTES : Lds<V2>::BYTES;
+  __shared__ __align__(1024) char lds[B];
+  if (((blockIdx.x >> 3) & 1) == 0)
+    Lds<V1>::run(p1, lds);
+  else
+    Lds<V2>::run(p2, lds);
 }
 
 // SwiGLU (activation "swiglu"; the reference's forward epilogue
@@ -1858,13 +1897,94 @@ int lane_grid() {
 }
 static_assert(kMaxLanes * kLane % (8 * kLane) == 0, "whole lanes on every XCD");
 
+// Paired launches (gemm_pair_begin / gemm_pair_end): while a pair is open on
+// the calling host thread, the first GEMM launch is held and the second goes
+// out with it as one grouped_gemm_pair_kernel, each on half of every XCD's
+// CUs (pair_grid workgroups, whole dW lanes).
+struct HeldGemm {
+  int variant;
+  Args p;
+  hipStream_t s;
+  int solo_grid;  // its grid as a launch of its own
+};
+thread_local int g_pair_open = 0;  // 0: no pair, 1: open, 2: holding the first GEMM
+thread_local HeldGemm g_held;
+
+int pair_grid() {
+  const int half = cu_count() / 2 / (8 * kLane) * (8 * kLane);
+  return std::max(8 * kLane, std::min(half, kMaxLanes * kLane));
+}
+
+template <int V>
+int launch_solo(Args p, hipStream_t s) {
+  VMOE_LAUNCH(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+int launch_variant(int v, const Args& p, hipStream_t s) {
+  switch (v) {
+    case UP_FWD: return launch_solo<UP_FWD>(p, s);
+    case DOWN_FWD: return launch_solo<DOWN_FWD>(p, s);
+    case UP_DX: return launch_solo<UP_DX>(p, s);
+    case UP_DW: return launch_solo<UP_DW>(p, s);
+    case DOWN_DH: return launch_solo<DOWN_DH>(p, s);
+    case DOWN_DW: return launch_solo<DOWN_DW>(p, s);
+    case UP_GLU: return launch_solo<UP_GLU>(p, s);
+  }
+  return VMOE_ERR_INVALID_ARG;
+}
+
+template <int V1, int V2>
+int launch_pair_kernel(const Args& p1, const Args& p2, hipStream_t s) {
+  VMOE_LAUNCH((grouped_gemm_pair_kernel<V1, V2>), dim3((unsigned)(2 * p1.grid)), dim3(kThreads),
+              0, s, p1, p2);
+  VMOE_CHECK_LAUNCH();
+  return VMOE_OK;
+}
+
+// Launches GEMM V with arguments p (p.grid: its grid as a launch of its own),
+// or holds it / pairs it with the held one while a pair is open.
+template <int V>
+int submit(Args p, hipStream_t s) {
+  if (g_pair_open == 0) return launch_solo<V>(p, s);
+  const int solo = p.grid;
+  p.grid = pair_grid();
+  p.paired = 1;
+  if (g_pair_open == 1 || g_held.s != s) {
+    if (g_pair_open == 2) {  // another stream: the held GEMM goes alone
+      HeldGemm h = g_held;
+      h.p.grid = h.solo_grid;
+      h.p.paired = 0;
+      const int st = launch_variant(h.variant, h.p, h.s);
+      if (st) return st;
+    }
+    g_held = HeldGemm{V, p, s, solo};
+    g_pair_open = 2;
+    return VMOE_OK;
+  }
+  const HeldGemm h = g_held;
+  g_pair_open = 1;
+  if (h.variant == DOWN_DH && V == DOWN_DW) return launch_pair_kernel<DOWN_DH, DOWN_DW>(h.p, p, s);
+  if (h.variant == DOWN_DW && V == DOWN_DH) return launch_pair_kernel<DOWN_DW, DOWN_DH>(h.p, p, s);
+  if (h.variant == UP_DW && V == UP_DX) return launch_pair_kernel<UP_DW, UP_DX>(h.p, p, s);
+  if (h.variant == UP_DX && V == UP_DW) return launch_pair_kernel<UP_DX, UP_DW>(h.p, p, s);
+  // no paired instance: each alone
+  Args a = h.p;
+  a.grid = h.solo_grid;
+  a.paired = 0;
+  int st = launch_variant(h.variant, a, s);
+  if (st) return st;
+  p.grid = solo;
+  p.paired = 0;
+  return launch_solo<V>(p, s);
+}
+
 template <int V>
 int launch(Args p, int64_t items_bound, hipStream_t s) {
   if (items_bound <= 0) return VMOE_OK;
   p.grid = Cfg<V>::contig ? lane_grid() : gemm_grid(items_bound);
-  VMOE_LAUNCH(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
-  VMOE_CHECK_LAUNCH();
-  return VMOE_OK;
+  return submit<V>(p, s);
 }
 
 // Workspace of a split dW launch: the arrival words (kConsumers per
@@ -1908,11 +2028,11 @@ int launch_dw(Args p, int64_t tmax, void* ws, size_t ws_bytes, hipStream_t s) {
   p.kc = kDwChunk;
   p.grid = lane_grid();
   if (ws_bytes < dw_workspace<V>(p.grid)) return VMOE_ERR_WORKSPACE;
+  // (a paired launch runs on pair_grid() <= lane_grid() workgroups, whose
+  // arrival words and partial slots are a prefix of these)
   p.arrive = reinterpret_cast<uint32_t*>(ws);
   p.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + dw_arrive_bytes(p.grid));
-  VMOE_LAUNCH(grouped_gemm_kernel<V>, dim3((unsigned)p.grid), dim3(kThreads), 0, s, p);
-  VMOE_CHECK_LAUNCH();
-  return VMOE_OK;
+  return submit<V>(p, s);
 }
 
 // Shared argument checks. Every dimension the kernels vectorise over must be a
@@ -1944,6 +2064,21 @@ inline bool src_ld_ok(int64_t ld, int64_t cols, const int32_t* map) {
 inline bool span_ok(int64_t rows, int64_t ld) { return rows * ld * 2 < ((int64_t)1 << 31); }
 
 }  // namespace
+
+void gemm_pair_begin() { g_pair_open = 1; }
+
+int gemm_pair_end() {
+  int st = VMOE_OK;
+  if (g_pair_open == 2) {
+    HeldGemm h = g_held;
+    h.p.grid = h.solo_grid;
+    h.p.paired = 0;
+    st = launch_variant(h.variant, h.p, h.s);
+  }
+  g_pair_open = 0;
+  return st;
+}
+
 }  // namespace vmoe
 
 using namespace vmoe;

@@ -26,6 +26,15 @@ struct LaunchTiming {
 };
 extern thread_local LaunchTiming g_launch_timing;
 
+// gemm.hip: between gemm_pair_begin() and gemm_pair_end(), the calling host
+// thread's GEMM launches go out two at a time (those on one stream), each
+// pair as one launch of grouped_gemm_pair_kernel with the CUs split between
+// the two (dH with dW2, dX with dW1; other pairs launch one after the
+// other). gemm_pair_end() launches a GEMM still held alone and returns its
+// status.
+void gemm_pair_begin();
+int gemm_pair_end();
+
 }  // namespace vmoe
 
 #define VMOE_LAUNCH(K, G, B, SH, S, ...)                                                   \

@@ -919,13 +919,17 @@ def grouped_gemm_down_autograd(intermediate, w2, expert_token_offsets, expert_we
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
 # The module's backward runs its weight-gradient GEMMs on a side stream
 # (beside dH and dX) when True, keeps every launch on the current stream
-# when False (per-kernel timing), and decides by size when None: the second
-# stream takes 20 / 65 us off an eager cfg3 / cfg4 step, whose GPU time
-# dominates, but its event hand-overs add 75-80 us of host time to the
-# host-bound cfg1 / cfg2 steps, and graph replays ran slower with it
-# (cfg3 0.808 against 0.783 ms), so it is left out under graph capture.
+# when False, and decides by size when None. On one stream the fused path
+# (vmoe_moe_backward) pairs each weight-gradient GEMM with dH / dX in one
+# launch, each on half of the CUs; the per-kernel path (and its timing)
+# launches them one after the other. Measured per eager step (same box,
+# interleaved): cfg3 0.779-0.781 ms paired against 0.789-0.791 with the
+# second stream, cfg4 5.29 against 5.01-5.05; cfg1 / cfg2 pay 75-80 us of
+# host time for the second stream's event hand-overs, and graph replays ran
+# slower with it (cfg3 0.808 against 0.783 ms before the pairing), so it is
+# left out under graph capture.
 BACKWARD_SIDE_STREAM: bool | None = None
-SIDE_STREAM_MIN_WORK = 2 ** 34  # assignments x max expert width x hidden
+SIDE_STREAM_MIN_WORK = 2 ** 37  # assignments x max expert width x hidden
 
 
 def _use_side_stream(assignments: int, max_width: int, hidden: int) -> bool:
