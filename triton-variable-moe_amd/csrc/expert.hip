@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <mutex>
 
+#include "router_aux.h"
 #include "vmoe_common.h"
 
 namespace vmoe {
@@ -136,15 +137,18 @@ extern "C" int vmoe_expert_layout(int64_t num_tokens, int32_t num_experts, int32
   return VMOE_OK;
 }
 
-extern "C" int vmoe_expert_forward(const void* selected, int32_t selected_is_int64,
-                                   const uint16_t* weights, int64_t num_tokens,
-                                   int32_t num_experts, int32_t top_k, int32_t block_size,
-                                   void* route_workspace, size_t route_workspace_bytes,
-                                   const uint16_t* x, int64_t ldx, const uint16_t* w1,
-                                   int64_t ldw1, const uint16_t* w2, int64_t ldw2,
-                                   const int32_t* ewo, const int32_t* widths, int64_t hidden,
-                                   int64_t max_width, void* saved, void* scratch, uint16_t* out,
-                                   int64_t ldo, vmoe_stream_t stream) {
+namespace vmoe {
+namespace {
+// vmoe_expert_forward; `aux` (with a routing workspace of counts): the
+// auxiliary losses go into the routing launch where it can take them
+// (route_counted_aux sets *aux_done).
+int expert_forward(const void* selected, int32_t selected_is_int64, const uint16_t* weights,
+                   int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t block_size,
+                   void* route_workspace, size_t route_workspace_bytes, const uint16_t* x,
+                   int64_t ldx, const uint16_t* w1, int64_t ldw1, const uint16_t* w2,
+                   int64_t ldw2, const int32_t* ewo, const int32_t* widths, int64_t hidden,
+                   int64_t max_width, void* saved, void* scratch, uint16_t* out, int64_t ldo,
+                   vmoe_stream_t stream, const RouteAux* aux, bool* aux_done) {
   Layout L;
   if (!make_layout(num_tokens, num_experts, top_k, block_size, hidden, max_width,
                    route_workspace != nullptr, L))
@@ -165,13 +169,13 @@ extern "C" int vmoe_expert_forward(const void* selected, int32_t selected_is_int
   uint16_t* y = at<uint16_t>(scratch, L.f_y);
   // routing placement, pad rows of the map -1 (the GEMMs' gather reads zeros)
   if (route_workspace) {
-    VMOE_TRY(vmoe_route_counted(
+    VMOE_TRY(route_counted_aux(
         selected, selected_is_int64, L.A, E, k, block_size, VMOE_ROUND_UP,
         at<int32_t>(saved, L.slot[VMOE_X_BIN_IDS]), at<int32_t>(saved, L.slot[VMOE_X_INDICES]),
         at<int32_t>(saved, L.slot[VMOE_X_TPE]), at<int32_t>(saved, L.slot[VMOE_X_BINS]),
         at<int32_t>(saved, L.slot[VMOE_X_PADDED_BINS]), row_src, gmap, -1, L.cap, arow,
         at<int32_t>(saved, L.slot[VMOE_X_INFO]), eto, ptpe, weights, rw, route_workspace,
-        route_workspace_bytes, stream));
+        route_workspace_bytes, stream, aux, aux_done));
   } else {
     VMOE_TRY(vmoe_route(
         selected, selected_is_int64, L.A, E, k, block_size, VMOE_ROUND_UP,
@@ -188,6 +192,23 @@ extern "C" int vmoe_expert_forward(const void* selected, int32_t selected_is_int
   VMOE_TRY(vmoe_gemm_down_fwd(h, max_width, w2, ldw2, y, hidden, eto, ewo, widths, ptpe, E,
                               hidden, max_width, L.cap, stream));
   return vmoe_combine(y, L.cap, hidden, arow, nullptr, k, out, ldo, num_tokens, hidden, stream);
+}
+}  // namespace
+}  // namespace vmoe
+
+extern "C" int vmoe_expert_forward(const void* selected, int32_t selected_is_int64,
+                                   const uint16_t* weights, int64_t num_tokens,
+                                   int32_t num_experts, int32_t top_k, int32_t block_size,
+                                   void* route_workspace, size_t route_workspace_bytes,
+                                   const uint16_t* x, int64_t ldx, const uint16_t* w1,
+                                   int64_t ldw1, const uint16_t* w2, int64_t ldw2,
+                                   const int32_t* ewo, const int32_t* widths, int64_t hidden,
+                                   int64_t max_width, void* saved, void* scratch, uint16_t* out,
+                                   int64_t ldo, vmoe_stream_t stream) {
+  return expert_forward(selected, selected_is_int64, weights, num_tokens, num_experts, top_k,
+                        block_size, route_workspace, route_workspace_bytes, x, ldx, w1, ldw1, w2,
+                        ldw2, ewo, widths, hidden, max_width, saved, scratch, out, ldo, stream,
+                        nullptr, nullptr);
 }
 
 extern "C" int vmoe_expert_backward(
@@ -384,9 +405,17 @@ extern "C" int vmoe_moe_forward(const uint16_t* logits, int64_t num_tokens, int3
     VMOE_TRY(vmoe_router_topk(logits, E, num_tokens, E, top_k, normalize, wts, sel, nullptr,
                               nullptr, lse, partial, nfl, nullptr, stream));
   }
-  VMOE_TRY(vmoe_expert_forward(sel, 0, wts, num_tokens, E, top_k, block_size, route_ws,
-                               M.route_ws_bytes, x, ldx, w1, ldw1, w2, ldw2, ewo, widths, hidden,
-                               max_width, saved, scratch, out, ldo, stream));
+  // The losses ride in the routing launch where it takes them (E <= 64),
+  // else they get their own launch after the expert path.
+  const RouteAux aux = {partial, (int)M.partial_rows, num_tokens, coef, widths_normalized,
+                        f_i, at<float>(saved, M.slot[VMOE_M_F_I32]),
+                        at<float>(scratch, M.f_p_i), z_loss, losses};
+  bool aux_done = false;
+  VMOE_TRY(expert_forward(sel, 0, wts, num_tokens, E, top_k, block_size, route_ws,
+                          M.route_ws_bytes, x, ldx, w1, ldw1, w2, ldw2, ewo, widths, hidden,
+                          max_width, saved, scratch, out, ldo, stream,
+                          M.counted ? &aux : nullptr, &aux_done));
+  if (aux_done) return VMOE_OK;
   return vmoe_router_aux(partial, (int32_t)M.partial_rows, num_tokens, E,
                          at<int32_t>(saved, M.x.slot[VMOE_X_TPE]), coef, widths_normalized, f_i,
                          at<float>(saved, M.slot[VMOE_M_F_I32]), at<float>(scratch, M.f_p_i),

@@ -26,6 +26,7 @@
 #include <algorithm>
 #include <mutex>
 
+#include "router_aux.h"
 #include "vmoe_common.h"
 
 namespace vmoe {
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_small_kernel(
     int64_t row_capacity, int32_t* __restrict__ assignment_row,
     const uint16_t* __restrict__ weights, float* __restrict__ row_weight,
     int32_t* __restrict__ info, int32_t* __restrict__ expert_offsets,
-    int32_t* __restrict__ padded_counts) {
+    int32_t* __restrict__ padded_counts, RouteAux aux) {
   __shared__ int32_t wcnt[kRouteWaves][kSmallExperts];  // ids of expert e in wave w
   __shared__ int32_t cnt_s[kSmallExperts], pre_s[kSmallExperts];
   __shared__ int32_t any_bad;
@@ -582,6 +583,15 @@ __global__ __launch_bounds__(kRouteThreads) void route_small_kernel(
   const int rank = lanes_below(same);
   if (valid && rank == 0) wcnt[wave][ee] = __popcll(same);
   __syncthreads();
+  // The workgroup after the placement ones (launched only with aux.partial)
+  // owns no assignments; it forms the auxiliary losses from the expert
+  // totals it has just summed.
+  const int nplace = max(ntiles, 1);
+  if (b == nplace) {
+    router_aux_block<false>(aux.partial, aux.nblk, aux.T, E, cnt_s, aux.coef, aux.wn, aux.f_i,
+                            aux.f_i32, aux.p_i, aux.z, aux.losses);
+    return;
+  }
 
   // Per expert (lane x = expert x): count, rounded count, kept, and the
   // exclusive scans over experts of all three.
@@ -639,7 +649,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_small_kernel(
     }
   }
   // Pad rows [ps + kept, ps + rounded) of the experts this workgroup owns.
-  for (int x = b + (int)gridDim.x * wave; x < E; x += (int)gridDim.x * kRouteWaves) {
+  for (int x = b + nplace * wave; x < E; x += nplace * kRouteWaves) {
     const int32_t kept_x = __shfl(kx, x, kWave), rnd_x = __shfl(rx, x, kWave);
     const int32_t ps_x = __shfl(psx, x, kWave);
     for (int32_t q = kept_x + lane; q < rnd_x; q += kWave) {
@@ -721,7 +731,8 @@ int route_impl(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_
                int32_t* gather_map, int32_t gather_map_pad, int64_t row_capacity,
                int32_t* assignment_row, int32_t* info, int32_t* expert_offsets,
                int32_t* padded_counts, const uint16_t* weights, float* row_weight,
-               void* workspace, size_t ws_bytes, vmoe_stream_t stream, bool counted) {
+               void* workspace, size_t ws_bytes, vmoe_stream_t stream, bool counted,
+               const RouteAux* aux = nullptr, bool* aux_done = nullptr) {
   if (A < 0 || E <= 0 || top_k <= 0 || block <= 0 || row_capacity < 0)
     return VMOE_ERR_INVALID_ARG;
   if (rounding < VMOE_ROUND_UP || rounding > VMOE_ROUND_NEAREST) return VMOE_ERR_INVALID_ARG;
@@ -748,12 +759,16 @@ int route_impl(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_
   while ((1 << nbits) < E) ++nbits;
   // (route_hist_split keeps the counted case inside these limits)
   if (E <= kSmallExperts && (int64_t)E * ntiles * S <= kFusedMaxCounts) {
-    VMOE_LAUNCH(route_small_kernel, dim3(std::max(ntiles, 1)), dim3(kRouteThreads), 0, s,
-                       sel, is64, A, E, nbits, ntiles, S, block, rounding, top_k, ws, tpe, bins,
-                       padded_bins, bin_ids, indices, row_src, gather_map, gather_map_pad,
-                       row_capacity, assignment_row, weights, row_weight, info, expert_offsets,
-                       padded_counts);
+    static_assert(kAuxThreads == kRouteThreads, "the loss workgroup runs in the routing launch");
+    const bool with_aux = aux && aux->partial;
+    const RouteAux none = {};
+    VMOE_LAUNCH(route_small_kernel, dim3(std::max(ntiles, 1) + (with_aux ? 1 : 0)),
+                       dim3(kRouteThreads), 0, s, sel, is64, A, E, nbits, ntiles, S, block,
+                       rounding, top_k, ws, tpe, bins, padded_bins, bin_ids, indices, row_src,
+                       gather_map, gather_map_pad, row_capacity, assignment_row, weights,
+                       row_weight, info, expert_offsets, padded_counts, with_aux ? *aux : none);
     VMOE_CHECK_LAUNCH();
+    if (with_aux && aux_done) *aux_done = true;
     return VMOE_OK;
   }
   if (E <= kFusedMaxExperts && (int64_t)E * ntiles * S <= kFusedMaxCounts) {
@@ -810,6 +825,26 @@ extern "C" int vmoe_route_counted(const void* sel, int32_t is64, int64_t A, int3
                     assignment_row, info, expert_offsets, padded_counts, weights, row_weight,
                     workspace, ws_bytes, stream, true);
 }
+
+namespace vmoe {
+int route_counted_aux(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_k,
+                      int32_t block, int32_t rounding, int32_t* bin_ids, int32_t* indices,
+                      int32_t* tpe, int32_t* bins, int32_t* padded_bins, int32_t* row_src,
+                      int32_t* gather_map, int32_t gather_map_pad, int64_t row_capacity,
+                      int32_t* assignment_row, int32_t* info, int32_t* expert_offsets,
+                      int32_t* padded_counts, const uint16_t* weights, float* row_weight,
+                      void* workspace, size_t ws_bytes, vmoe_stream_t stream,
+                      const RouteAux* aux, bool* aux_done) {
+  if (aux && aux->partial &&
+      (aux->nblk <= 0 || aux->T < 0 || !aux->coef || !aux->wn || !aux->f_i || !aux->f_i32 ||
+       !aux->p_i || !aux->z || !aux->losses))
+    return VMOE_ERR_INVALID_ARG;
+  return route_impl(sel, is64, A, E, top_k, block, rounding, bin_ids, indices, tpe, bins,
+                    padded_bins, row_src, gather_map, gather_map_pad, row_capacity,
+                    assignment_row, info, expert_offsets, padded_counts, weights, row_weight,
+                    workspace, ws_bytes, stream, true, aux, aux_done);
+}
+}  // namespace vmoe
 
 // vmoe_route_static: vmoe_route with its workspace in a file-scope device
 // array, for callers that cannot allocate. Each GPU the library runs on holds

@@ -27,6 +27,7 @@
 
 #include <algorithm>
 
+#include "router_aux.h"
 #include "vmoe_common.h"
 
 namespace vmoe {
@@ -40,8 +41,6 @@ constexpr int kRtWaves = kRtThreads / kWave;
 __host__ __device__ constexpr int topk_threads(int vpl) { return vpl <= 8 ? 1024 : 256; }
 constexpr int kRtMaxExperts = 2048;
 constexpr int kRtMaxBlocks = 1024;
-constexpr int kAuxThreads = 1024;
-constexpr int kAuxWaves = kAuxThreads / kWave;
 
 // Tokens whose logits a wave loads together before working on them (their
 // loads are in flight at once).
@@ -112,26 +111,6 @@ __device__ __forceinline__ float wave_max_f32(float v) {
 // sigmoid as torch evaluates it for fp32 (1 / (1 + exp(-x)), precise exp).
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Element type of the logits, the routing weights and the logit gradients:
-// bf16 bit patterns (F32 = false, the module in bf16) or fp32 (the module in
-// fp32). torch evaluates logsumexp and its square in the logits' dtype, so
-// for bf16 each is rounded to bf16 once; for fp32 they stay fp32.
-template <bool F32>
-struct RtElt;
-template <>
-struct RtElt<false> {
-  using T = uint16_t;
-  __device__ static float ld(const T* p) { return bf16_to_f32(*p); }
-  __device__ static T cvt(float v) { return (T)f32_to_bf16(v); }
-  __device__ static float rnd(float v) { return bf16_to_f32(f32_to_bf16(v)); }
-};
-template <>
-struct RtElt<true> {
-  using T = float;
-  __device__ static float ld(const T* p) { return *p; }
-  __device__ static T cvt(float v) { return v; }
-  __device__ static float rnd(float v) { return v; }
-};
 
 // ---- torch.topk's output order and torch.sum's order, for one token ----
 //
@@ -571,11 +550,7 @@ __global__ __launch_bounds__(kGrpThreads) void router_topk_group_kernel(
   }
 }
 
-// One workgroup: sums the block partials in a fixed order and forms the
-// losses: z_out (bf16) = z_loss, out_scalars[0] = load balance, [1] = compute
-// loss. Columns go 64 at a time (one per lane); wave w adds rows w, w + 16, ...
-// with 8 independent loads in flight, then the 16 wave sums are added in
-// wave order.
+// One workgroup: the auxiliary losses (router_aux_block).
 template <bool F32>
 __global__ __launch_bounds__(kAuxThreads) void router_aux_kernel(
     const float* __restrict__ partial, int nblk, int64_t T, int E,
@@ -583,72 +558,8 @@ __global__ __launch_bounds__(kAuxThreads) void router_aux_kernel(
     const float* __restrict__ wn, typename RtElt<F32>::T* __restrict__ f_i,
     float* __restrict__ f_i32, float* __restrict__ p_i, typename RtElt<F32>::T* __restrict__ z_out,
     float* __restrict__ out_scalars) {
-  __shared__ float wsum[kAuxWaves][kWave];
-  __shared__ long long sh_cnt[kAuxWaves];
-  __shared__ float sh_z;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
-  // total routed assignments
-  long long cnt = 0;
-  for (int e = tid; e < E; e += kAuxThreads) cnt += tokens_per_expert[e];
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, kWave);
-  if (lane == 0) sh_cnt[wv] = cnt;
-  __syncthreads();
-  long long total_i = 0;
-#pragma unroll
-  for (int w = 0; w < kAuxWaves; ++w) total_i += sh_cnt[w];
-  const float total = (float)total_i;
-  const float invT = T > 0 ? 1.0f / (float)T : 0.0f;
-  float lb = 0.0f, cl = 0.0f;
-  for (int c0 = 0; c0 <= E; c0 += kWave) {
-    const int c = c0 + lane;
-    float s = 0.0f;
-    if (c <= E) {
-      float acc[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-      int b = wv;
-      for (; b + 7 * kAuxWaves < nblk; b += 8 * kAuxWaves) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] += partial[(int64_t)(b + i * kAuxWaves) * (E + 1) + c];
-      }
-      for (int i = 0; b < nblk; b += kAuxWaves, ++i) acc[i] += partial[(int64_t)b * (E + 1) + c];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s += acc[i];
-    }
-    wsum[wv][lane] = s;
-    __syncthreads();
-    if (wv == 0 && c <= E) {
-      float col = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kAuxWaves; ++w) col += wsum[w][lane];
-      if (c == E) {
-        sh_z = col;
-      } else {
-        const float pe = col * invT;
-        // f_i = (tpe.float() / tpe.sum()).to(dtype)
-        const float fe = RtElt<F32>::rnd((float)tokens_per_expert[c] / total);
-        f_i[c] = RtElt<F32>::cvt(fe);
-        f_i32[c] = fe;
-        p_i[c] = pe;
-        lb += coef[c] * fe * pe;
-        cl += wn[c] * pe;
-      }
-    }
-    __syncthreads();
-  }
-  if (wv == 0) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      lb += __shfl_xor(lb, off, kWave);
-      cl += __shfl_xor(cl, off, kWave);
-    }
-    if (lane == 0) {
-      *z_out = RtElt<F32>::cvt(sh_z * invT);
-      out_scalars[0] = lb;
-      out_scalars[1] = cl;
-    }
-  }
+  router_aux_block<F32>(partial, nblk, T, E, tokens_per_expert, coef, wn, f_i, f_i32, p_i, z_out,
+                        out_scalars);
 }
 
 // dL for every logit (one wave per token).
