@@ -1,8 +1,9 @@
 """A training step of TritonMoEMLP captured into a HIP graph (torch.cuda.graph)
 and replayed: every kernel launch goes through the C ABI on torch's current
 stream, the expert path needs no host sync, and the backward's second stream
-joins the capture through stream waits. Each replay (with eager steps run in
-between) must reproduce the eager step's output and gradients bit for bit."""
+(forced on here; by default only large layers take it) joins the capture
+through stream waits. Each replay (with eager steps run in between) must
+reproduce the eager step's output and gradients bit for bit."""
 
 from __future__ import annotations
 
@@ -16,9 +17,18 @@ from _util import bits_equal, make_problem
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(params=[None, True], ids=["default", "side_stream"])
+def side_stream_mode(request):
+    from triton_moe.kernels import grouped_gemm as gg
+
+    gg.BACKWARD_SIDE_STREAM = request.param
+    yield request.param
+    gg.BACKWARD_SIDE_STREAM = None
+
+
 @pytest.mark.parametrize("B,S,d,sizes,k", [(4, 256, 256, [(4, 512), (4, 256)], 2),
                                            (8, 1024, 768, [(8, 512)], 2)])
-def test_graph_replay_matches_eager(B, S, d, sizes, k, device):
+def test_graph_replay_matches_eager(B, S, d, sizes, k, side_stream_mode, device):
     p = make_problem(B * S, d, sizes, k, 64, seed=3, device=device)
     cfg = TritonMoEConfig(n_embd=d, expert_sizes=sizes, num_active_experts=k, block_size=64)
     m = TritonMoEMLP(cfg).to(device).to(torch.bfloat16)

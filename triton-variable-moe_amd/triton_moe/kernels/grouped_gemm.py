@@ -925,9 +925,9 @@ _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
 # launches them one after the other. Measured per eager step (same box,
 # interleaved): cfg3 0.779-0.781 ms paired against 0.789-0.791 with the
 # second stream, cfg4 5.29 against 5.01-5.05; cfg1 / cfg2 pay 75-80 us of
-# host time for the second stream's event hand-overs, and graph replays ran
-# slower with it (cfg3 0.808 against 0.783 ms before the pairing), so it is
-# left out under graph capture.
+# host time for the second stream's event hand-overs. HIP-graph replays
+# follow the same rule (the side stream joins the capture through the
+# stream waits): cfg4 5.12-5.13 ms with it against 5.30-5.32 paired.
 BACKWARD_SIDE_STREAM: bool | None = None
 SIDE_STREAM_MIN_WORK = 2 ** 37  # assignments x max expert width x hidden
 
@@ -935,8 +935,7 @@ SIDE_STREAM_MIN_WORK = 2 ** 37  # assignments x max expert width x hidden
 def _use_side_stream(assignments: int, max_width: int, hidden: int) -> bool:
     if BACKWARD_SIDE_STREAM is not None:
         return BACKWARD_SIDE_STREAM
-    return (assignments * max_width * hidden >= SIDE_STREAM_MIN_WORK and
-            not torch.cuda.is_current_stream_capturing())
+    return assignments * max_width * hidden >= SIDE_STREAM_MIN_WORK
 
 
 _ORDER_EVENTS: dict[int, list] = {}
