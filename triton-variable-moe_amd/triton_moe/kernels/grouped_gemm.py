@@ -1084,6 +1084,29 @@ def moe_layout(T: int, E: int, k: int, block_size: int, hidden: int, max_width: 
     return lay
 
 
+_MOE_PLANS: dict[tuple, tuple] = {}
+
+
+def _moe_plan(T: int, E: int, k: int, block_size: int, hidden: int, max_width: int,
+              device: torch.device) -> tuple:
+    """Everything MoELayerOp's two calls need that depends on the shape only,
+    looked up once: (saved_bytes, fwd_scratch_bytes, bwd_scratch_bytes,
+    rows_bound, dW workspace bytes, side stream by size, the ones row of
+    out.sum()'s gradient, the two library functions). An eager step at cfg1
+    is host-bound, so per-step Python is step time."""
+    key = (T, E, k, block_size, hidden, max_width, device.index)
+    plan = _MOE_PLANS.get(key)
+    if plan is None:
+        saved_b, fwd_b, bwd_b, rows, _, _, _ = moe_layout(T, E, k, block_size, hidden, max_width)
+        ws_n = max(int(_lib.lib().vmoe_gemm_dw_workspace_bytes(E, hidden, max_width,
+                                                               max(rows, 1))), 16)
+        plan = _MOE_PLANS[key] = (
+            saved_b, fwd_b, bwd_b, rows, ws_n,
+            T * k * max_width * hidden >= SIDE_STREAM_MIN_WORK, _ones_row(hidden, device),
+            _lib.lib().vmoe_moe_forward, _lib.lib().vmoe_moe_backward)
+    return plan
+
+
 class MoELayerOp(torch.autograd.Function):
     """TritonMoEMLP.forward after the router Linear as one autograd node and
     one library call per direction (vmoe_moe_forward / vmoe_moe_backward):
@@ -1102,28 +1125,32 @@ class MoELayerOp(torch.autograd.Function):
     def forward(ctx, logits, x_flat, w1, w2, widths, ewo, coef, wn, top_k, block_size,
                 max_width, normalize, weight_grad):
         T, d = x_flat.shape
-        E = widths.numel()
+        E = widths.shape[0]
         dev = x_flat.device
         x_flat = _bf16(x_flat, "TritonMoEMLP x")
         if not logits.is_contiguous() or logits.data_ptr() % 16:
             logits = logits.contiguous().clone()
-        saved_b, fwd_b, _, rows, _, _, _ = moe_layout(T, E, top_k, block_size, d, max_width)
-        saved = torch.empty(saved_b, dtype=torch.uint8, device=dev)
-        scratch = torch.empty(fwd_b, dtype=torch.uint8, device=dev)
+        plan = _moe_plan(T, E, top_k, block_size, d, max_width, dev)
+        saved = torch.empty(plan[0], dtype=torch.uint8, device=dev)
+        scratch = torch.empty(plan[1], dtype=torch.uint8, device=dev)
         out = torch.empty(T, d, dtype=torch.bfloat16, device=dev)
         z = torch.empty((), dtype=torch.bfloat16, device=dev)
         losses = torch.empty(2, dtype=torch.float32, device=dev)
         f_i = torch.empty(E, dtype=torch.bfloat16, device=dev)
         if T == 0:
             z.zero_(), losses.zero_(), f_i.zero_()
-        _lib.call("vmoe_moe_forward", logits.data_ptr(), T, E, top_k, int(bool(normalize)),
-                  block_size, x_flat.data_ptr(), x_flat.stride(0), w1.data_ptr(), w1.stride(0),
-                  w2.data_ptr(), w2.stride(0), ewo.data_ptr(), widths.data_ptr(), d, max_width,
-                  coef.data_ptr(), wn.data_ptr(), saved.data_ptr(), scratch.data_ptr(),
-                  out.data_ptr(), out.stride(0), z.data_ptr(), losses.data_ptr(), f_i.data_ptr(),
-                  _lib.stream(dev))
-        ctx.save_for_backward(logits, x_flat, w1, w2, widths, ewo, coef, wn, saved)
-        ctx.dims = (T, E, top_k, block_size, d, max_width, rows, int(bool(normalize)))
+        st = plan[7](logits.data_ptr(), T, E, top_k, int(bool(normalize)), block_size,
+                     x_flat.data_ptr(), x_flat.stride(0), w1.data_ptr(), w1.stride(0),
+                     w2.data_ptr(), w2.stride(0), ewo.data_ptr(), widths.data_ptr(), d, max_width,
+                     coef.data_ptr(), wn.data_ptr(), saved.data_ptr(), scratch.data_ptr(),
+                     out.data_ptr(), d, z.data_ptr(), losses.data_ptr(), f_i.data_ptr(),
+                     _lib.stream(dev))
+        if st != _lib.OK:
+            _lib.check(st, "vmoe_moe_forward")
+        ctx.save_for_backward(logits, x_flat, w1, w2, saved)
+        # the module's constant tables (buffers, never written in place)
+        ctx.tables = (widths, ewo, coef, wn)
+        ctx.dims = (T, E, top_k, block_size, d, max_width, int(bool(normalize)))
         ctx.weight_grad = bool(weight_grad)
         ctx.mark_non_differentiable(f_i)
         # unused outputs arrive as None (not zeros), so a loss that leaves out
@@ -1135,17 +1162,19 @@ class MoELayerOp(torch.autograd.Function):
     @custom_bwd(device_type="cuda")
     @once_differentiable
     def backward(ctx, grad_out, g_z, g_lb, g_cl, _g_fi):
-        logits, x_flat, w1, w2, widths, ewo, coef, wn, saved = ctx.saved_tensors
-        T, E, k, b, d, max_width, rows, norm = ctx.dims
+        logits, x_flat, w1, w2, saved = ctx.saved_tensors
+        widths, ewo, coef, wn = ctx.tables
+        T, E, k, b, d, max_width, norm = ctx.dims
         dev = logits.device
-        _, _, bwd_b, _, _, _, _ = moe_layout(T, E, k, b, d, max_width)
+        plan = _moe_plan(T, E, k, b, d, max_width, dev)
 
         def scalar(g):
             return None if g is None else g.detach().to(torch.float32).reshape(()).contiguous()
 
         gz, glb, gcl = scalar(g_z), scalar(g_lb), scalar(g_cl)
-        want_x = grad_out is not None and any(ctx.needs_input_grad[1:4])
-        want_logits = ctx.needs_input_grad[0] and (
+        need = ctx.needs_input_grad
+        want_x = grad_out is not None and (need[1] or need[2] or need[3])
+        want_logits = need[0] and (
             gz is not None or glb is not None or gcl is not None or (ctx.weight_grad and want_x))
         grad_x = grad_w1 = grad_w2 = grad_logits = None
         g = gs = None
@@ -1153,7 +1182,7 @@ class MoELayerOp(torch.autograd.Function):
         if want_x:
             if (grad_out.dtype == torch.bfloat16 and T > 0 and grad_out.stride(0) == 0 and
                     grad_out.stride(1) == 0):
-                g, ldg, gs = _ones_row(d, dev), 0, grad_out  # c * out.sum(): ones times c
+                g, ldg, gs = plan[6], 0, grad_out  # c * out.sum(): ones times c
             else:
                 (g, ldg), gs = _token_source(grad_out), None
             grad_x = torch.empty(T, d, dtype=torch.bfloat16, device=dev)
@@ -1163,19 +1192,24 @@ class MoELayerOp(torch.autograd.Function):
             grad_logits = torch.empty(T, E, dtype=torch.bfloat16, device=dev)
         if not want_x and not want_logits:
             return (None,) * 13
-        scratch = torch.empty(bwd_b, dtype=torch.uint8, device=dev)
-        main = torch.cuda.current_stream(dev)
-        side = _side_stream(dev) if _use_side_stream(T * k, max_width, d) else None
-        ws = _dw_workspace_bytes(E, d, max_width, rows, dev,
-                                 side.cuda_stream if side is not None else main.cuda_stream)
-        _lib.call("vmoe_moe_backward", saved.data_ptr(), logits.data_ptr(), T, E, k, norm, b,
-                  x_flat.data_ptr(), x_flat.stride(0), w1.data_ptr(), w1.stride(0),
-                  w2.data_ptr(), w2.stride(0), ewo.data_ptr(), widths.data_ptr(), d, max_width,
-                  coef.data_ptr(), wn.data_ptr(), _lib.ptr(g), ldg, _lib.ptr(gs), _lib.ptr(gz),
-                  _lib.ptr(glb), _lib.ptr(gcl), int(ctx.weight_grad), _lib.ptr(grad_x),
-                  d, _lib.ptr(grad_w1), w1.stride(0), _lib.ptr(grad_w2), w2.stride(0),
-                  _lib.ptr(grad_logits), scratch.data_ptr(), ws.data_ptr(), ws.numel(),
-                  main.cuda_stream, None if side is None else side.cuda_stream)
+        scratch = torch.empty(plan[2], dtype=torch.uint8, device=dev)
+        main = _lib.stream(dev)
+        use_side = BACKWARD_SIDE_STREAM if BACKWARD_SIDE_STREAM is not None else plan[5]
+        side = _side_stream(dev).cuda_stream if use_side else None
+        ws_stream = side if side is not None else main
+        ws = _DW_WORKSPACES.get((dev.index, ws_stream))
+        if ws is None or ws.numel() < plan[4]:
+            ws = _dw_workspace_bytes(E, d, max_width, plan[3], dev, ws_stream)
+        ptr = _lib.ptr
+        st = plan[8](saved.data_ptr(), logits.data_ptr(), T, E, k, norm, b,
+                     x_flat.data_ptr(), x_flat.stride(0), w1.data_ptr(), w1.stride(0),
+                     w2.data_ptr(), w2.stride(0), ewo.data_ptr(), widths.data_ptr(), d, max_width,
+                     coef.data_ptr(), wn.data_ptr(), ptr(g), ldg, ptr(gs), ptr(gz), ptr(glb),
+                     ptr(gcl), int(ctx.weight_grad), ptr(grad_x), d, ptr(grad_w1), w1.stride(0),
+                     ptr(grad_w2), w2.stride(0), ptr(grad_logits), scratch.data_ptr(),
+                     ws.data_ptr(), ws.numel(), main, side)
+        if st != _lib.OK:
+            _lib.check(st, "vmoe_moe_backward")
         return (grad_logits, grad_x, grad_w1, grad_w2) + (None,) * 9
 
 
