@@ -471,15 +471,20 @@ int vmoe_gemm_up_bwd_dx(const uint16_t* grad_act, int64_t ldg, const uint16_t* w
                         int64_t rows_bound, vmoe_stream_t stream);
 
 /* Workspace of the two dW GEMMs' split-K on the current device: arrival
- * words, then fp32 partial tiles. The arrival words (the first 256-byte
- * aligned region) must be zero when a call starts, and every call leaves
- * them zero: zero-fill a workspace once when it is allocated and reuse it
- * for calls in stream order; calls that may overlap need workspaces of their
- * own. A dW call with workspace == NULL runs without split-K (same result to
+ * words, then fp32 partial tiles. The arrival words (the first
+ * vmoe_gemm_dw_workspace_zero_bytes() bytes) must be zero when a call starts,
+ * and every call leaves them zero: zero-fill them once when the workspace is
+ * allocated and reuse it for calls in stream order; calls that may overlap
+ * need workspaces of their own. The partial tiles need no initial value. A
+ * dW call with workspace == NULL runs without split-K (same result to
  * summation order, one work item per output tile, slow when one expert holds
  * most tokens). */
 size_t vmoe_gemm_dw_workspace_bytes(int32_t num_experts, int64_t hidden, int64_t max_width,
                                     int64_t rows_bound);
+/* Bytes at the start of a dW workspace that must be zero when a call starts
+ * (the arrival words; a multiple of 256, at most 8 KiB). No counterpart in
+ * the reference, whose Triton dW kernels need no workspace. */
+size_t vmoe_gemm_dw_workspace_zero_bytes(void);
 
 /* grad_w1[:, ewo[e]:+w_e] = X_e^T @ GA_e, X_e rows read as x[gather_map[row]]
  * when gather_map != NULL (fused gather), else x[row]. K (the expert's rows) is

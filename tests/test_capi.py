@@ -49,6 +49,11 @@ def test_status_strings_and_queries():
     ws = lib.vmoe_route_workspace_bytes(262144, 128)
     assert ws >= 4 * 128 * (262144 // 1024)
     assert lib.vmoe_route_workspace_bytes(-1, 4) == 0
+    # the dW workspace's arrival words: a 256-byte multiple, at most 8 KiB,
+    # a prefix of the whole workspace
+    z = lib.vmoe_gemm_dw_workspace_zero_bytes()
+    assert 0 < z <= 8192 and z % 256 == 0
+    assert lib.vmoe_gemm_dw_workspace_bytes(64, 1024, 256, 140000) > z
 
 
 def test_argument_checks_return_invalid_arg():

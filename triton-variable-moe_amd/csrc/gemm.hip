@@ -2225,6 +2225,11 @@ extern "C" size_t vmoe_gemm_dw_workspace_bytes(int32_t E, int64_t hidden, int64_
   return std::max(dw_workspace<UP_DW>(grid), dw_workspace<DOWN_DW>(grid));
 }
 
+extern "C" size_t vmoe_gemm_dw_workspace_zero_bytes(void) {
+  // launch_dw's arrival words for the largest grid a dW launch takes
+  return dw_arrive_bytes(kMaxLanes * kLane);
+}
+
 extern "C" int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
                                    const int32_t* gather_map, const uint16_t* grad_act,
                                    int64_t ldg, uint16_t* grad_w1, int64_t ldgw,

@@ -69,6 +69,7 @@ _SIGNATURES = {
     "vmoe_gemm_up_bwd_dx": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64,
                             _i64, _i64, _vp],
     "vmoe_gemm_dw_workspace_bytes": [_i32, _i64, _i64, _i64],
+    "vmoe_gemm_dw_workspace_zero_bytes": [],
     "vmoe_gemm_up_bwd_dw": [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp,
                             _i32, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
     "vmoe_gemm_down_bwd_dh": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp,
@@ -121,6 +122,7 @@ _RESTYPES = {
     "vmoe_route_workspace_bytes": ctypes.c_size_t,
     "vmoe_route_counted_workspace_bytes": ctypes.c_size_t,
     "vmoe_gemm_dw_workspace_bytes": ctypes.c_size_t,
+    "vmoe_gemm_dw_workspace_zero_bytes": ctypes.c_size_t,
     "vmoe_router_partial_floats": ctypes.c_size_t,
 }
 

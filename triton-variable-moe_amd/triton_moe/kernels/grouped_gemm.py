@@ -176,8 +176,12 @@ def _dw_workspace_bytes(E: int, hidden: int, max_width: int, rows: int, device,
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _DW_WORKSPACES.get(key)
     if ws is None or ws.numel() < n:
-        # zero_() is a fill kernel, so this also holds under graph capture
-        ws = torch.empty(n, dtype=torch.uint8, device=device).zero_()
+        # Only the arrival words at the start must be zero (the partial tiles
+        # need no initial value); zero_() is a fill kernel, so this also holds
+        # under graph capture, where a workspace made during the capture is
+        # cleared again at every replay (8 KiB, not the whole 64 MiB).
+        ws = torch.empty(n, dtype=torch.uint8, device=device)
+        ws[:min(n, int(_lib.lib().vmoe_gemm_dw_workspace_zero_bytes()))].zero_()
         _DW_WORKSPACES[key] = ws
     return ws
 
