@@ -38,6 +38,9 @@ CONFIGS = {
     "cfg2": (8, 2048, 768, [(4, 512), (8, 256), (4, 128)], 2, 64, None),
     "cfg3": (1, 16384, 1024, [(64, 256)], 8, 64, 3.0),
     "cfg3_a1": (1, 16384, 1024, [(64, 256)], 8, 64, 1.0),  # the benchmark's alpha
+    # more than 64 experts: the layer's auxiliary losses take a launch of their
+    # own instead of riding in the routing launch
+    "e128": (2, 1024, 256, [(96, 128), (32, 64)], 4, 64, 1.0),
 }
 
 
@@ -528,7 +531,8 @@ def test_routing_weight_grad_at_zero_and_denormal_weights(name, device):
 
 
 @pytest.mark.parametrize("name,grad", [("ref_variable", "random"), ("cfg1", "sum"),
-                                       ("cfg2", "scaled"), ("cfg3_a1", "random")])
+                                       ("cfg2", "scaled"), ("cfg3_a1", "random"),
+                                       ("e128", "random")])
 def test_fused_expert_path_same_bits_as_per_kernel_path(name, grad, device):
     """The module after its router Linear as one library call per direction
     (vmoe_moe_forward / _backward, the default) gives the bits of the
