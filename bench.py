@@ -76,6 +76,10 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 1 GiB device buffer 5 times: the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--host-profile", action="store_true",
+                    help="only measure where the host time of an eager step of --config goes: "
+                         "issue and completion rates, the library calls' host time, and "
+                         "torch.profiler's CPU table over the steps")
     return ap.parse_args()
 
 
@@ -565,6 +569,69 @@ def summary(name, r):
     }
 
 
+def host_profile(name, device, steps):
+    """Host side of the eager step of `name`: how fast the host issues steps
+    (timed before the final synchronize) against how fast they complete, the
+    host time inside the two library calls of the layer (vmoe_moe_forward /
+    vmoe_moe_backward, bound ctypes functions timed around the call), and
+    torch.profiler's CPU-only table over the same steps (self time per op, the
+    autograd device thread included). Prints text, not a bench line."""
+    import torch
+    from torch.profiler import ProfilerActivity, profile
+
+    from triton_moe.kernels import grouped_gemm as gg
+
+    torch.manual_seed(0)
+    m, xb, _info = build_workload(name, device)
+    step = make_step(m, xb)
+    for _ in range(20):
+        step()
+    torch.cuda.synchronize()
+    print(f"# host profile, {name}, {steps} eager steps per measurement")
+    for n in (20, steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            step()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        print(f"steps {n}: host issue {1e6 * (t1 - t0) / n:.1f} us/step, completion "
+              f"{1e6 * (t2 - t0) / n:.1f} us/step")
+    # host time inside the layer's two library calls
+    acc = {}
+
+    def timed(fn, what):
+        def call(*a):
+            t = time.perf_counter()
+            r = fn(*a)
+            acc.setdefault(what, []).append(time.perf_counter() - t)
+            return r
+        return call
+
+    plans = dict(gg._MOE_PLANS)
+    for key, plan in plans.items():
+        gg._MOE_PLANS[key] = plan[:7] + (timed(plan[7], "vmoe_moe_forward"),
+                                         timed(plan[8], "vmoe_moe_backward"))
+    try:
+        for _ in range(steps):
+            torch.cuda.synchronize()
+            step()
+        torch.cuda.synchronize()
+    finally:
+        gg._MOE_PLANS.update(plans)
+    for what, v in acc.items():
+        v = sorted(v)
+        print(f"{what}: median {1e6 * v[len(v) // 2]:.1f} us host time per call "
+              f"(min {1e6 * v[0]:.1f}), {len(v)} calls")
+    with profile(activities=[ProfilerActivity.CPU]) as prof:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    print(f"torch.profiler, CPU only, {steps} steps (times are totals over the steps):")
+    print(prof.key_averages().table(sort_by="self_cpu_time_total", row_limit=25))
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -587,6 +654,9 @@ def main():
         return
     if args.fp32_gemm:
         fp32_gemm()
+        return
+    if args.host_profile:
+        host_profile(args.config, device, args.steps)
         return
 
     if args.profile_steps:

@@ -219,6 +219,30 @@ def test_forward_deterministic(device):
         assert bits_equal(a, b)
 
 
+def test_autocast_region_same_bits(device):
+    """A bf16 layer run inside torch.autocast (bf16), forward and backward,
+    gives the bits it gives outside: nothing in the layer after the router
+    Linear is an op autocast would change, and the Linear is already bf16."""
+    B, S, d, sizes, k, b, _ = CONFIGS["ref_variable"]
+    p = make_problem(B * S, d, sizes, k, b, seed=11, device=device)
+    m = _module(p, d, sizes, k, b, device)
+    G = torch.randn(B, S, d, generator=torch.Generator().manual_seed(12)).to(
+        torch.bfloat16).to(device)
+    res = []
+    for ctx in (contextlib.nullcontext(), torch.autocast("cuda", dtype=torch.bfloat16)):
+        x = p["x"].view(B, S, d).to(device).requires_grad_(True)
+        m.zero_grad(set_to_none=True)
+        with ctx:
+            out, aux, f_i = m(x)
+            loss = (out * G).sum() + aux["router_z_loss"] + aux["load_balance_loss"]
+        loss.backward()
+        res.append((out.detach().clone(), aux["router_z_loss"].detach().clone(), f_i.clone(),
+                    x.grad.clone(), m.w1.grad.clone(), m.w2.grad.clone(),
+                    m.router.weight.grad.clone()))
+    for a, c, what in zip(res[0], res[1], ("out", "z", "f_i", "x", "w1", "w2", "router")):
+        assert bits_equal(a, c), what
+
+
 @pytest.mark.parametrize("name", ["cfg1", "cfg3"])
 def test_backward_stream_modes(name, device):
     """The backward runs its weight-gradient GEMMs on a second stream beside

@@ -1122,10 +1122,15 @@ class MoELayerOp(torch.autograd.Function):
     forward(logits, x_flat, w1, w2, widths, ewo, coef, wn, top_k, block_size,
     max_width, normalize, weight_grad) -> (out, z_loss, load_balance_loss,
     compute_loss, f_i). The logits get the auxiliary losses' gradient and,
-    with weight_grad, the routing weights' chain; f_i has none."""
+    with weight_grad, the routing weights' chain; f_i has none.
+
+    Unlike the per-kernel ops it carries no torch.amp custom_fwd / custom_bwd:
+    neither direction runs an op that autocast would change (allocations with
+    explicit dtypes and one library call), so the autocast context those
+    decorators enter around the backward (~12 us of host time per step on an
+    eager cfg1 step, which is host-bound) changes nothing but the time."""
 
     @staticmethod
-    @custom_fwd(device_type="cuda")
     def forward(ctx, logits, x_flat, w1, w2, widths, ewo, coef, wn, top_k, block_size,
                 max_width, normalize, weight_grad):
         T, d = x_flat.shape
@@ -1163,7 +1168,6 @@ class MoELayerOp(torch.autograd.Function):
         return out, z, losses[0], losses[1], f_i
 
     @staticmethod
-    @custom_bwd(device_type="cuda")
     @once_differentiable
     def backward(ctx, grad_out, g_z, g_lb, g_cl, _g_fi):
         logits, x_flat, w1, w2, saved = ctx.saved_tensors
