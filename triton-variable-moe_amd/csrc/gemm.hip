@@ -44,6 +44,7 @@
 //    finishes a tile's last segment.
 
 #include <algorithm>
+#include <atomic>
 
 #include "vmoe_common.h"
 
@@ -1862,19 +1863,20 @@ __global__ __launch_bounds__(256) void relu2_grad_kernel(const uint16_t* __restr
 
 inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Compute units of the current device (cached per device id).
+// Compute units of the current device (cached per device id; host threads
+// may race to fill an entry, and all of them store the same value).
 int cu_count() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 static_assert(kDwChunk % Cfg<UP_DW>::BK == 0 &&
