@@ -158,7 +158,8 @@ int vmoe_row_maps(const int32_t* indices, const int32_t* bin_ids, const int32_t*
  *   sums for vmoe_router_aux (vmoe_router_partial_floats(T, E) floats; the
  *   row count is returned in *num_partial_rows). Limits: E <= 2048, k <= 64.
  * vmoe_router_aux: after routing, z_loss (bf16), [load_balance, compute] (fp32
- *   in losses[0..1]), f_i = bf16(tpe / sum tpe) (bf16 and fp32 copies) and
+ *   in losses[0..1]), f_i = bf16(tpe / sum tpe) (bf16 and fp32 copies; 0 when
+ *   nothing was routed) and
  *   p_i = mean_t p [E] fp32. coef[e] is the load-balance weight of expert e:
  *   E for uniform widths, 1 without expert groups, else
  *   group_size / num_groups for experts in a group and 0 otherwise

@@ -41,6 +41,7 @@ CONFIGS = {
     # more than 64 experts: the layer's auxiliary losses take a launch of their
     # own instead of riding in the routing launch
     "e128": (2, 1024, 256, [(96, 128), (32, 64)], 4, 64, 1.0),
+    "one_token": (1, 1, 256, [(2, 256), (2, 128)], 2, 64, None),
 }
 
 
@@ -217,6 +218,31 @@ def test_forward_deterministic(device):
     assert bits_equal(out1, out2)
     for a, b in zip(g1, (x.grad, m.w1.grad, m.w2.grad)):
         assert bits_equal(a, b)
+
+
+@pytest.mark.parametrize("fused,dtype", [(True, torch.bfloat16), (False, torch.bfloat16),
+                                         (True, torch.float32)])
+def test_no_tokens(fused, dtype, device):
+    """A batch with no tokens: an empty output, zero weight gradients (the
+    reference's grouped-GEMM backward returns zeros for empty inputs), an
+    empty input gradient."""
+    from triton_moe.kernels import grouped_gemm as gg
+
+    d, sizes, k, b = 128, [(2, 128), (2, 64)], 2, 64
+    cfg = TritonMoEConfig(n_embd=d, expert_sizes=sizes, num_active_experts=k, block_size=b)
+    m = TritonMoEMLP(cfg).to(device).to(dtype)
+    gg.FUSED_EXPERT_PATH = fused
+    try:
+        x = torch.zeros(1, 0, d, dtype=dtype, device=device, requires_grad=True)
+        out, aux, f_i = m(x)
+        assert out.shape == (1, 0, d)
+        out.sum().backward()
+        torch.cuda.synchronize()
+        assert x.grad is not None and x.grad.shape == (1, 0, d)
+        assert m.w1.grad is not None and int(torch.count_nonzero(m.w1.grad)) == 0
+        assert m.w2.grad is not None and int(torch.count_nonzero(m.w2.grad)) == 0
+    finally:
+        gg.FUSED_EXPERT_PATH = True
 
 
 def test_autocast_region_same_bits(device):

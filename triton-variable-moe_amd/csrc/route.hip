@@ -740,7 +740,7 @@ int route_impl(const void* sel, int32_t is64, int64_t A, int32_t E, int32_t top_
   if (!tpe || !bins || !padded_bins || !info || !workspace) return VMOE_ERR_INVALID_ARG;
   if (A > 0 && (!sel || !bin_ids || !indices || !assignment_row)) return VMOE_ERR_INVALID_ARG;
   if (row_capacity > 0 && (!row_src || !gather_map)) return VMOE_ERR_INVALID_ARG;
-  if (row_weight && !weights) return VMOE_ERR_INVALID_ARG;
+  if (A > 0 && row_weight && !weights) return VMOE_ERR_INVALID_ARG;
   // counted: the S count columns per tile of vmoe_router_topk_hist for the
   // same tokens, experts and k
   const int S = counted ? (A % top_k == 0 ? route_hist_split(A / top_k, E, top_k) : 0) : 1;

@@ -862,8 +862,10 @@ int router_topk_impl(const typename RtElt<F32>::T* logits, int64_t ld_logits, in
       ld_logits < num_experts)
     return VMOE_ERR_INVALID_ARG;
   if (num_experts > kRtMaxExperts || top_k > kWave) return VMOE_ERR_UNSUPPORTED;
-  if (!weights || !partial || !lse || (!selected_i32 && !selected_i64) ||
-      (num_tokens > 0 && !logits))
+  // with no tokens only the partial rows (zeros) are written; empty outputs
+  // may come as NULL
+  if (!partial || (num_tokens > 0 && (!weights || !lse || (!selected_i32 && !selected_i64) ||
+                                      !logits)))
     return VMOE_ERR_INVALID_ARG;
   const int nblk = router_blocks(num_tokens, num_experts);
   if (partial_floats < (size_t)nblk * (size_t)(num_experts + 1)) return VMOE_ERR_WORKSPACE;

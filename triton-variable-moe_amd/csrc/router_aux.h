@@ -94,8 +94,9 @@ __device__ __forceinline__ void router_aux_block(
         sh_z = col;
       } else {
         const float pe = col * invT;
-        // f_i = (tpe.float() / tpe.sum()).to(dtype)
-        const float fe = RtElt<F32>::rnd((float)tokens_per_expert[c] / total);
+        // f_i = (tpe.float() / tpe.sum()).to(dtype); 0 when nothing was routed
+        const float fe =
+            total_i > 0 ? RtElt<F32>::rnd((float)tokens_per_expert[c] / total) : 0.0f;
         f_i[c] = RtElt<F32>::cvt(fe);
         f_i32[c] = fe;
         p_i[c] = pe;

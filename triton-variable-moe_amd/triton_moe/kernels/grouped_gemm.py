@@ -1052,8 +1052,9 @@ class ExpertPathOp(torch.autograd.Function):
         else:
             (g, ldg), gs = _token_source(grad_out), None
         grad_x = torch.empty(T, d, dtype=torch.bfloat16, device=dev)
-        grad_w1 = torch.empty_like(w1)
-        grad_w2 = torch.empty_like(w2)
+        # no tokens: the library writes nothing, the weight gradients are zero
+        grad_w1 = torch.empty_like(w1) if T > 0 else torch.zeros_like(w1)
+        grad_w2 = torch.empty_like(w2) if T > 0 else torch.zeros_like(w2)
         grad_w = (torch.empty(T * k, dtype=torch.bfloat16, device=dev) if ctx.weights_grad
                   and ctx.needs_input_grad[3] else None)
         scratch = torch.empty(bwd_b, dtype=torch.uint8, device=dev)
@@ -1194,8 +1195,9 @@ class MoELayerOp(torch.autograd.Function):
             else:
                 (g, ldg), gs = _token_source(grad_out), None
             grad_x = torch.empty(T, d, dtype=torch.bfloat16, device=dev)
-            grad_w1 = torch.empty_like(w1)
-            grad_w2 = torch.empty_like(w2)
+            # no tokens: the library writes nothing, the weight gradients are zero
+            grad_w1 = torch.empty_like(w1) if T > 0 else torch.zeros_like(w1)
+            grad_w2 = torch.empty_like(w2) if T > 0 else torch.zeros_like(w2)
         if want_logits:
             grad_logits = torch.empty(T, E, dtype=torch.bfloat16, device=dev)
         if not want_x and not want_logits:
@@ -1219,6 +1221,25 @@ class MoELayerOp(torch.autograd.Function):
         if st != _lib.OK:
             _lib.check(st, "vmoe_moe_backward")
         return (grad_logits, grad_x, grad_w1, grad_w2) + (None,) * 9
+
+
+class NoTokensOp(torch.autograd.Function):
+    """The expert path of a batch without tokens: forward(x_flat [0, d], w1,
+    w2) -> an empty [0, d] output; the backward gives an empty input gradient
+    and zero weight gradients, as the reference's grouped GEMMs return zeros
+    for empty inputs (grouped_gemm.py:1214-1215, 1333-1334)."""
+
+    @staticmethod
+    def forward(ctx, x_flat, w1, w2):
+        ctx.save_for_backward(w1, w2)
+        return x_flat.new_empty(0, x_flat.shape[1])
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_out):
+        w1, w2 = ctx.saved_tensors
+        return (grad_out.new_empty(0, grad_out.shape[1]), torch.zeros_like(w1),
+                torch.zeros_like(w2))
 
 
 class CompactRoutedMoEOp(torch.autograd.Function):

@@ -38,6 +38,7 @@ from .kernels.fused_cumsum import route_device
 from .kernels.gather import combine_rows
 from .kernels import grouped_gemm as gg
 from .kernels.grouped_gemm import (CompactRoutedMoEOp, ExpertPathOp, GemmMeta, MoELayerOp,
+                                   NoTokensOp,
                                    RoutedMoEOp, RoutedMoEOpF32, down_fwd, f32_down_fwd,
                                    f32_up_fwd, up_fwd)
 from .kernels.router import RouterAuxOp, RouterLinear, RouterWeightOp, router_topk
@@ -214,6 +215,10 @@ class TritonMoEMLP(nn.Module):
         it requires grad (routing_weight_grad). route_ws: the top-k call's
         per-tile histograms (RouterState.route_ws), or None."""
         k = self.num_active_experts
+        if x_flat.shape[0] == 0:
+            # no tokens: an empty output and zero weight gradients, no launch
+            tpe = torch.zeros(self.num_experts, dtype=torch.int32, device=x_flat.device)
+            return NoTokensOp.apply(x_flat, self.w1, self.w2), tpe
         if self.w1.dtype == torch.float32:
             return self._experts_f32(x_flat, top_k_weights_flat, selected_experts_flat,
                                      route_ws)
@@ -291,7 +296,10 @@ class TritonMoEMLP(nn.Module):
         batch_size, seq_len, n_embd = x.shape
         x_flat = x.reshape(batch_size * seq_len, n_embd)  # rearrange "b s d -> (b s) d"
         router_logits = self.router(x_flat)
-        if (gg.FUSED_EXPERT_PATH and _lib._launch_timer is None and not self._compact() and
+        # (a batch without tokens always takes the one-node path, which returns
+        # an empty output, zero losses and zero weight gradients)
+        if ((x_flat.shape[0] == 0 or (gg.FUSED_EXPERT_PATH and _lib._launch_timer is None and
+                                      not self._compact())) and
                 self.w1.dtype == torch.bfloat16 and router_logits.dtype == torch.bfloat16):
             # everything after the router Linear: one node, one call each way
             coef, wn = self._aux_tables(router_logits.device)
