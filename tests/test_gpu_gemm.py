@@ -35,8 +35,9 @@ CASES = [
     (256, 64, [(2, 64), (2, 128)], 2, 64, False),      # tiles wider than the problem
     (2048, 768, [(4, 512), (8, 256), (4, 128)], 2, 64, False),  # config-2 widths
     (2048, 1024, [(64, 256)], 8, 64, True),            # config-3 shape, skewed, empties
+    (1024, 2048, [(2, 1024), (2, 512)], 2, 64, False),  # d x max width >= 2^21: dW lanes of 8
 ]
-IDS = ["small", "uniform", "variable", "tiny_tiles", "var3", "skew64"]
+IDS = ["small", "uniform", "variable", "tiny_tiles", "var3", "skew64", "wide_lanes8"]
 
 
 def _case(T, d, sizes, k, b, skew, seed=0):
@@ -256,23 +257,26 @@ def test_up_dw_row_map(with_workspace, device):
     assert_close_norm(gw, ref, TIGHT, f"GW1 map ws={with_workspace}")
 
 
-def test_dw_split_tiles_across_many_lanes(device):
+@pytest.mark.parametrize("d,widths,hot", [(512, [256, 128, 256], 30000),
+                                          (2048, [1024, 512, 1024], 6000)],
+                         ids=["lanes4", "lanes8"])
+def test_dw_split_tiles_across_many_lanes(d, widths, hot, device):
     """One expert holds almost every row, so its tiles' K chunks span many
     workgroup lanes (three or more segments per tile): the wave finishing a
     tile's last segment sums the partials in lane order. Checked against the
     per-expert reference, for bitwise determinism over repeated calls (the
     arrival words are left zero for the next call), and against the split-K
-    free path within the summation-order tolerance."""
+    free path within the summation-order tolerance. d x max width >= 2^21
+    takes lanes of 8 workgroups, smaller shapes lanes of 4."""
     from triton_moe import _lib
     from triton_moe.kernels.grouped_gemm import _dw_workspace, host_meta
 
     g = torch.Generator().manual_seed(11)
-    d, widths = 512, [256, 128, 256]
     E = len(widths)
     offsets = [0]
     for w in widths:
         offsets.append(offsets[-1] + w)
-    counts = [30000, 64, 0]          # hot, small, empty
+    counts = [hot, 64, 0]            # hot, small, empty
     pad = [(c + 63) // 64 * 64 for c in counts]
     eto = torch.tensor([0] + list(torch.tensor(pad).cumsum(0)), dtype=torch.int32)
     P, W, max_w = int(eto[-1]), offsets[-1], max(widths)
@@ -323,7 +327,8 @@ def test_dw_split_tiles_across_many_lanes(device):
     assert_close_norm(a2, ref2, TIGHT, "dW2 split across lanes")
     for _ in range(3):
         assert torch.equal(dw1(ws), a1) and torch.equal(dw2(ws), a2)
-    assert int(ws[:256].count_nonzero()) == 0, "arrival words left non-zero"
+    zb = int(_lib.lib().vmoe_gemm_dw_workspace_zero_bytes())
+    assert int(ws[:zb].count_nonzero()) == 0, "arrival words left non-zero"
     assert_close_norm(dw1(None), ref1, TIGHT, "dW1 without split-K")
     assert_close_norm(dw2(None), ref2, TIGHT, "dW2 without split-K")
 

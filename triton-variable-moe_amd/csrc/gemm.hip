@@ -18,8 +18,8 @@
 //    and empty experts cost nothing. Row-tiled GEMMs: XCD x owns a
 //    contiguous eighth of the work items (the tiles of one expert share that
 //    XCD's L2) and its workgroups take every (grid / 8)-th item. dW GEMMs:
-//    lanes of kLane workgroups on one XCD take contiguous item ranges (see
-//    item_range).
+//    lanes of 4 or 8 workgroups (by shape, lane_shift) on one XCD take
+//    contiguous item ranges (see item_range).
 //  * 128x256 output tiles; 8 consumer waves in a 2x4 grid, 64x64 fp32
 //    accumulators per wave (two consumer waves per SIMD), and 4 producer
 //    waves that issue every DMA.
@@ -72,8 +72,11 @@ constexpr int kWaves = kConsumers + kProducers;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxExperts = 2048;  // per-expert work prefix held in LDS
 constexpr int kRecExperts = 256;   // per-expert metadata also held in LDS up to this E
-constexpr int kLane = 4;           // dW GEMMs: workgroups of one XCD that share each K chunk
-constexpr int kMaxLanes = 64;      // dW GEMMs: lanes (grid / kLane) a launch may have
+// dW GEMMs: the workgroups of one XCD that share each K chunk form a lane of
+// 1 << p.lsh of them (lane_shift: 4, or 8 for large d x w tiles per expert)
+constexpr int kMaxLaneShift = 3;
+constexpr int kMaxLanes = 64;      // dW GEMMs: lanes (grid >> lsh) a launch may have
+constexpr int kMaxDwGrid = kMaxLanes << 2;  // dW grid limit (lanes of 4 fill lane_beg)
 
 enum Variant { UP_FWD = 0, DOWN_FWD, UP_DX, UP_DW, DOWN_DH, DOWN_DW, UP_GLU };
 
@@ -102,6 +105,7 @@ struct Args {
   int act;
   int64_t rows_bound;
   int kc;          // K rows per work item for the dW GEMMs (0 = whole K)
+  int lsh = 2;     // dW GEMMs: log2 of the workgroups per lane (lane_shift)
   float* partial;    // fp32 partial tiles of split tiles (2 slots per workgroup)
   uint32_t* arrive;  // split-K arrival words, kConsumers per workgroup (zero between launches)
   int grid;          // GEMM workgroups
@@ -397,12 +401,12 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, ld
 
 // Work items of an expert with `tiles` output tiles and `chunks` K chunks.
 // Row-tiled GEMMs: one item per tile. dW GEMMs: the tiles form groups of
-// kLane and an item is (tile group, chunk); the kLane workgroups of a lane
-// (all on one XCD) each take one tile of the group, so they read the same
-// K chunk of the shared operand at the same time and it comes from HBM once.
+// 1 << lsh and an item is (tile group, chunk); the workgroups of a lane (all
+// on one XCD) each take one tile of the group, so they read the same K chunk
+// of the shared operand at the same time and it comes from HBM once.
 template <int V>
-__host__ __device__ __forceinline__ int work_items(int tiles, int chunks) {
-  return Cfg<V>::contig ? cdiv(tiles, kLane) * chunks : tiles * chunks;
+__host__ __device__ __forceinline__ int work_items(int tiles, int chunks, int lsh) {
+  return Cfg<V>::contig ? ((tiles + (1 << lsh) - 1) >> lsh) * chunks : tiles * chunks;
 }
 
 // Per-expert tables of a launch, built once per workgroup: the exclusive
@@ -420,13 +424,13 @@ struct Meta {
 // workgroup b to XCD b % 8) owns the contiguous range [lane_beg[x],
 // lane_beg[x + 1]) of items, an eighth of the estimated cost (see
 // build_meta), so the tiles of one expert share an L2, and its
-// workgroups take every (grid / 8)-th item. Contig (grid a multiple of
-// 8 * kLane): the j-th workgroup of XCD x (j = b / 8) is slot j % kLane of
-// lane l = x * (grid / 8 / kLane) + j / kLane; lane l owns items
-// [lane_beg[l], lane_beg[l + 1]) of the NL = grid / kLane lanes (equal
-// shares of the k-steps, see build_meta), and its slot s works on tile
-// kLane * group + s of each. lin = kLane * l + s names the workgroup's
-// split-K partial slots.
+// workgroups take every (grid / 8)-th item. Contig (lanes of L = 1 << lsh
+// workgroups, grid a multiple of 8 L): the j-th workgroup of XCD x
+// (j = b / 8) is slot j % L of lane l = x * (grid / 8 / L) + j / L; lane l
+// owns items [lane_beg[l], lane_beg[l + 1]) of the NL = grid / L lanes
+// (equal shares of the k-steps, see build_meta), and its slot s works on
+// tile L * group + s of each. lin = L * l + s names the workgroup's split-K
+// partial slots.
 struct Range {
   int beg, end, stride, lin, slot;
 };
@@ -449,10 +453,10 @@ __device__ __forceinline__ Range item_range(const Args& p, int total, const int*
   r.lin = xcd * per + j;
   r.slot = 0;
   if (CONTIG) {
-    const int NL = G / kLane;
-    const int lane = xcd * (NL >> 3) + j / kLane;
-    r.slot = j % kLane;
-    r.lin = lane * kLane + r.slot;
+    const int NL = G >> p.lsh;
+    const int lane = xcd * (NL >> 3) + (j >> p.lsh);
+    r.slot = j & ((1 << p.lsh) - 1);
+    r.lin = (lane << p.lsh) + r.slot;
     r.beg = lane_beg[lane];
     r.end = lane_beg[lane + 1];
     r.stride = 1;
@@ -810,7 +814,7 @@ struct Gemm {
 
   // Builds the per-expert tables (all threads; `scan` is 16 longs of LDS).
   // Returns the total number of work items.
-  // Contig (dW) GEMMs also split the items into NL = grid / kLane lane
+  // Contig (dW) GEMMs also split the items into NL = grid >> lsh lane
   // ranges of equal estimated cost, in k-step units: an item costs its
   // chunk's k-steps (1 .. kDwChunk / BK) plus kItemCost for starting it, and
   // a tile group kEpiCost more for its epilogue (measured: an item start
@@ -841,9 +845,10 @@ struct Gemm {
         const Prob q = T::prob(p, r);
         int tiles, chunks;
         expert_work<V>(p, q, tiles, chunks);
-        items = work_items<V>(tiles, chunks);
+        items = work_items<V>(tiles, chunks, p.lsh);
         if (CONTIG)
-          cost = cdiv(tiles, kLane) * (cdiv(q.K, BK) + kItemCost * chunks + kEpiCost);
+          cost = ((tiles + (1 << p.lsh) - 1) >> p.lsh) *
+                 (cdiv(q.K, BK) + kItemCost * chunks + kEpiCost);
         else
           cost = items * (cdiv(q.K, BK) + kTileCost);
       }
@@ -865,7 +870,7 @@ struct Gemm {
     }
     __syncthreads();
     {
-      const int NL = CONTIG ? p.grid / kLane : 8;
+      const int NL = CONTIG ? p.grid >> p.lsh : 8;
       for (int l = threadIdx.x; l <= NL; l += kThreads) {
         int item = (int)base;
         if (l == 0 || cbase == 0) {
@@ -952,7 +957,7 @@ struct Gemm {
     const int local = item - __builtin_amdgcn_readfirstlane(mt.pre[e]);
     const int group = chunks == 1 ? local : udiv_small(local, chunks);
     const int chunk = local - group * chunks;
-    const int tile = Cfg<V>::contig ? group * kLane + slot : group;
+    const int tile = Cfg<V>::contig ? (group << p.lsh) + slot : group;
     w.skip = tile >= tiles;
     constexpr int BNO = out_cols<V>();
     const int n_tiles = cdiv(w.q.N, BNO);
@@ -1432,7 +1437,7 @@ struct Gemm {
   __device__ static bool split_arrive(const Args& p, const Meta& mt, const Range& rg, int a,
                                       int chunks, int seg_item, f32x16_t (&acc)[FM][FN]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int NL = p.grid / kLane, me = rg.lin / kLane, ts = rg.slot;
+    const int NL = p.grid >> p.lsh, me = rg.lin >> p.lsh, ts = rg.slot;
     const int* lb = mt.lane_beg;
     int L0 = me;
     while (L0 > 0 && lb[L0] > a) --L0;
@@ -1450,7 +1455,7 @@ struct Gemm {
     uint32_t old = 0;
     if (lane == 0)
       old = __builtin_amdgcn_atomic_inc32(
-          p.arrive + ((int64_t)(L0 * kLane + ts) * kConsumers + wave), (uint32_t)(nseg - 1),
+          p.arrive + ((int64_t)((L0 << p.lsh) + ts) * kConsumers + wave), (uint32_t)(nseg - 1),
           __ATOMIC_RELAXED, "agent");
     old = __builtin_amdgcn_readfirstlane(old);
     if (old != (uint32_t)(nseg - 1)) return false;
@@ -1459,7 +1464,7 @@ struct Gemm {
     for (int l = L0; l < NL && t < nseg; ++l) {
       const int b0 = lb[l];
       if (lb[l + 1] == b0) continue;
-      const int slot = 2 * (l * kLane + ts) + (l == L0 && l0_inside ? 1 : 0);
+      const int slot = 2 * ((l << p.lsh) + ts) + (l == L0 && l0_inside ? 1 : 0);
       // own >= 2: the sum is rebuilt from the slots, own included.
       if (own >= 2 && t == 0)
         add_partial<true>(p, slot, acc);
@@ -1891,13 +1896,24 @@ int gemm_grid(int64_t items_bound) {
   return (int)std::min<int64_t>(cus, (items_bound + 7) / 8 * 8);
 }
 
-// Grid of the dW GEMMs: whole lanes on every XCD (a multiple of 8 * kLane),
-// one workgroup per CU where the device allows.
+// Grid of the dW GEMMs: whole lanes of either width on every XCD (a
+// multiple of 8 << kMaxLaneShift), one workgroup per CU where the device
+// allows, at most kMaxDwGrid (lanes of 4 then fill lane_beg[]).
+constexpr int kLaneGridStep = 8 << kMaxLaneShift;
 int lane_grid() {
-  const int g = std::max(8 * kLane, cu_count() / (8 * kLane) * (8 * kLane));
-  return std::min(g, kMaxLanes * kLane);  // lane_beg[] holds kMaxLanes + 1 entries
+  const int g = std::max(kLaneGridStep, cu_count() / kLaneGridStep * kLaneGridStep);
+  return std::min(g, kMaxDwGrid);
 }
-static_assert(kMaxLanes * kLane % (8 * kLane) == 0, "whole lanes on every XCD");
+static_assert(kMaxDwGrid % kLaneGridStep == 0, "whole lanes on every XCD");
+
+// Workgroups per lane of a dW GEMM (as a shift), from its shape: lanes of 8
+// where an expert's output has many tiles (d x max width >= 2^21, e.g.
+// 2048 x 1024), else 4. Measured on whole steps against lanes of 4: the
+// cfg4 shape (d 2048, widths up to 1024) 1.6 % faster (dW1 900 -> 842 us);
+// d 1024 x 256 1 % slower, d 768 x 512 3.5-4 % slower.
+int lane_shift(int64_t hidden, int64_t max_width) {
+  return hidden * max_width >= (int64_t(1) << 21) ? 3 : 2;
+}
 
 // Paired launches (gemm_pair_begin / gemm_pair_end): while a pair is open on
 // the calling host thread, the first GEMM launch is held and the second goes
@@ -1913,8 +1929,8 @@ thread_local int g_pair_open = 0;  // 0: no pair, 1: open, 2: holding the first 
 thread_local HeldGemm g_held;
 
 int pair_grid() {
-  const int half = cu_count() / 2 / (8 * kLane) * (8 * kLane);
-  return std::max(8 * kLane, std::min(half, kMaxLanes * kLane));
+  const int half = cu_count() / 2 / kLaneGridStep * kLaneGridStep;
+  return std::max(kLaneGridStep, std::min(half, kMaxDwGrid));
 }
 
 template <int V>
@@ -2015,8 +2031,10 @@ int64_t row_items(int64_t rows_bound, int E, int64_t nmax) {
 
 // dW GEMM with split-K (one launch; split tiles are summed in the kernel).
 template <int V>
-int launch_dw(Args p, int64_t tmax, void* ws, size_t ws_bytes, hipStream_t s) {
+int launch_dw(Args p, int64_t tmax, int64_t max_width, void* ws, size_t ws_bytes,
+              hipStream_t s) {
   const int64_t E = p.E;
+  p.lsh = lane_shift(p.hidden, max_width);
   if (!ws) {
     p.kc = 0;
     p.partial = nullptr;
@@ -2229,7 +2247,7 @@ extern "C" size_t vmoe_gemm_dw_workspace_bytes(int32_t E, int64_t hidden, int64_
 
 extern "C" size_t vmoe_gemm_dw_workspace_zero_bytes(void) {
   // launch_dw's arrival words for the largest grid a dW launch takes
-  return dw_arrive_bytes(kMaxLanes * kLane);
+  return dw_arrive_bytes(kMaxDwGrid);
 }
 
 extern "C" int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_rows,
@@ -2253,8 +2271,8 @@ extern "C" int vmoe_gemm_up_bwd_dw(const uint16_t* x, int64_t ldx, int64_t x_row
   p.c = grad_w1; p.ldc = ldgw;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
-  return launch_dw<UP_DW>(p, tiles_max<UP_DW>(hidden, max_width), workspace, workspace_bytes,
-                          reinterpret_cast<hipStream_t>(stream));
+  return launch_dw<UP_DW>(p, tiles_max<UP_DW>(hidden, max_width), max_width, workspace,
+                          workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int vmoe_gemm_down_bwd_dh(const uint16_t* grad_y, int64_t ldgy, int64_t gy_rows,
@@ -2312,6 +2330,6 @@ extern "C" int vmoe_gemm_down_bwd_dw(const uint16_t* h, int64_t ldh, const uint1
   p.c = grad_w2; p.ldc = ldgw;
   p.eto = eto; p.ewo = ewo; p.widths = widths; p.tpe = tpe;
   p.E = E; p.hidden = (int)hidden; p.act = VMOE_ACT_NONE; p.rows_bound = rows_bound;
-  return launch_dw<DOWN_DW>(p, tiles_max<DOWN_DW>(hidden, max_width), workspace,
+  return launch_dw<DOWN_DW>(p, tiles_max<DOWN_DW>(hidden, max_width), max_width, workspace,
                             workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
