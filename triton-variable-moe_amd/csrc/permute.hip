@@ -542,7 +542,15 @@ extern "C" int vmoe_combine(const uint16_t* y, int64_t y_rows, int64_t ldy,
   const bool vec = hidden % 8 == 0 && ldy % 8 == 0 && ldo % 8 == 0 && aligned16(y) &&
                    aligned16(out);
   const dim3 grid(row_grid(num_tokens)), block(kThreads);
-  if (vec && top_k <= 8) {
+  if (vec && top_k <= 2) {
+    // (fewer slot registers: more waves in flight for the short sums)
+    if (weights)
+      VMOE_LAUNCH((combine_k_kernel<2, true, 2>), grid, block, 0, s, y, y_rows, ldy,
+                         assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
+    else
+      VMOE_LAUNCH((combine_k_kernel<2, false, 2>), grid, block, 0, s, y, y_rows, ldy,
+                         assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
+  } else if (vec && top_k <= 8) {
     if (weights)
       VMOE_LAUNCH((combine_k_kernel<8, true, 2>), grid, block, 0, s, y, y_rows, ldy,
                          assignment_row, weights, top_k, out, ldo, num_tokens, hidden);
