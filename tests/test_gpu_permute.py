@@ -293,3 +293,42 @@ def test_f32_gather_combine_and_weight_grad(T, d, E, k, b, device):
     assert ws.grad.dtype == torch.float32
     mag = eager.combine_weight_grad(G.abs(), y.abs(), maps["assignment_row"], k, T)
     assert ((ws.grad.cpu().double() - refg).abs() <= 1e-6 * mag + 1e-30).all()
+
+
+def test_public_api_empty_inputs(device):
+    """No routed tokens through the public operators: the reference returns
+    zero tensors early (gather.py:93-94, scatter.py:101-102,
+    grouped_gemm.py:430-433, 617-618, 1214-1215, 1333-1334): the padded
+    gather is [padded rows, d] of zeros, the scatter [tokens, d] of zeros,
+    the grouped GEMMs [0, width] / [0, d], their weight gradients zeros."""
+    from triton_moe.kernels import (fused_route, grouped_gemm_down, grouped_gemm_down_backward,
+                                    grouped_gemm_up, grouped_gemm_up_backward, padded_gather,
+                                    padded_scatter)
+
+    d, E, k, b, max_w = 64, 4, 2, 64, 128
+    widths = torch.tensor([128, 64, 128, 64], dtype=torch.int32, device=device)
+    ewo = torch.tensor([0, 128, 192, 320, 384], dtype=torch.int32, device=device)
+    W = 384
+    w1 = torch.randn(d, W, device=device).to(torch.bfloat16)
+    w2 = torch.randn(W, d, device=device).to(torch.bfloat16)
+    sel = torch.empty(0, dtype=torch.int64, device=device)
+    bin_ids, indices, tpe, bins, padded_bins = fused_route(sel, E, block_size=b)
+    x = torch.zeros(0, d, dtype=torch.bfloat16, device=device)
+    xg = padded_gather(x, indices, bin_ids, bins, padded_bins, k)
+    assert xg.shape == (int(padded_bins[-1]), d) and int(xg.count_nonzero()) == 0
+    eto = torch.zeros(E + 1, dtype=torch.int32, device=device)
+    ptpe = torch.zeros(E, dtype=torch.int32, device=device)
+    x0 = torch.zeros(0, d, dtype=torch.bfloat16, device=device)
+    h, pre = grouped_gemm_up(x0, w1, eto, ewo, widths, ptpe, max_w, save_pre_act=True)
+    assert h.shape == (0, max_w) and pre.shape == (0, max_w)
+    y = grouped_gemm_down(h, w2, eto, ewo, widths, ptpe, d)
+    assert y.shape == (0, d)
+    gy = torch.zeros(0, d, dtype=torch.bfloat16, device=device)
+    gh, gw2 = grouped_gemm_down_backward(gy, h, w2, eto, ewo, widths, ptpe, d, max_w)
+    assert gh.shape == (0, max_w) and gw2.shape == w2.shape and int(gw2.count_nonzero()) == 0
+    gx, gw1 = grouped_gemm_up_backward(gh, x0, w1, pre, eto, ewo, widths, ptpe, d)
+    assert gx.shape == (0, d) and gw1.shape == w1.shape and int(gw1.count_nonzero()) == 0
+    wts = torch.zeros(0, dtype=torch.bfloat16, device=device)
+    out = padded_scatter(xg, indices, bin_ids, wts, bins, padded_bins, k)
+    assert out.shape == (0, d)
+    torch.cuda.synchronize()

@@ -301,6 +301,8 @@ def up_bwd_dw(ga, x, w1, m: GemmMeta, hidden: int, gather_map: torch.Tensor | No
         grad_w1 = out
     else:
         grad_w1 = torch.zeros_like(w1) if not m.full_cols else torch.empty_like(w1)
+    if m.rows == 0:  # no routed rows: zero gradients, no launch
+        return grad_w1.zero_()
     dev = ga.device
     gm = None if gather_map is None else _i32(gather_map)
     ws = _dw_workspace(m, hidden, dev)
@@ -413,6 +415,8 @@ def down_bwd_dw(grad_y, h, w2, m: GemmMeta, hidden: int,
         grad_w2 = out
     else:
         grad_w2 = torch.zeros_like(w2) if not m.full_cols else torch.empty_like(w2)
+    if m.rows == 0:  # no routed rows: zero gradients, no launch
+        return grad_w2.zero_()
     gm = None if gather_map is None else _i32(gather_map)
     dev = g.device
     ws = _dw_workspace(m, hidden, dev)
