@@ -1124,10 +1124,12 @@ class MoELayerOp(torch.autograd.Function):
     ExpertPathOp / RoutedMoEOp, RouterAuxOp, RouterWeightOp), so the same
     bits.
 
-    forward(logits, x_flat, w1, w2, widths, ewo, coef, wn, top_k, block_size,
-    max_width, normalize, weight_grad) -> (out, z_loss, load_balance_loss,
-    compute_loss, f_i). The logits get the auxiliary losses' gradient and,
-    with weight_grad, the routing weights' chain; f_i has none.
+    forward(logits, x_flat, w1, w2, consts) -> (out, z_loss,
+    load_balance_loss, compute_loss, f_i), consts = (widths, ewo, coef, wn,
+    top_k, block_size, max_width, normalize, weight_grad): the module's
+    constant tables and settings in one argument, since autograd's per-call
+    work grows with the argument count. The logits get the auxiliary losses'
+    gradient and, with weight_grad, the routing weights' chain; f_i has none.
 
     Unlike the per-kernel ops it carries no torch.amp custom_fwd / custom_bwd:
     neither direction runs an op that autocast would change (allocations with
@@ -1136,8 +1138,8 @@ class MoELayerOp(torch.autograd.Function):
     eager cfg1 step, which is host-bound) changes nothing but the time."""
 
     @staticmethod
-    def forward(ctx, logits, x_flat, w1, w2, widths, ewo, coef, wn, top_k, block_size,
-                max_width, normalize, weight_grad):
+    def forward(ctx, logits, x_flat, w1, w2, consts):
+        widths, ewo, coef, wn, top_k, block_size, max_width, normalize, weight_grad = consts
         T, d = x_flat.shape
         E = widths.shape[0]
         dev = x_flat.device
@@ -1163,9 +1165,8 @@ class MoELayerOp(torch.autograd.Function):
             _lib.check(st, "vmoe_moe_forward")
         ctx.save_for_backward(logits, x_flat, w1, w2, saved)
         # the module's constant tables (buffers, never written in place)
-        ctx.tables = (widths, ewo, coef, wn)
-        ctx.dims = (T, E, top_k, block_size, d, max_width, int(bool(normalize)))
-        ctx.weight_grad = bool(weight_grad)
+        ctx.consts = consts
+        ctx.dims = (T, E, d, int(bool(normalize)))
         ctx.mark_non_differentiable(f_i)
         # unused outputs arrive as None (not zeros), so a loss that leaves out
         # the auxiliary losses gives the router no gradient, as in the reference
@@ -1176,8 +1177,8 @@ class MoELayerOp(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, grad_out, g_z, g_lb, g_cl, _g_fi):
         logits, x_flat, w1, w2, saved = ctx.saved_tensors
-        widths, ewo, coef, wn = ctx.tables
-        T, E, k, b, d, max_width, norm = ctx.dims
+        widths, ewo, coef, wn, k, b, max_width, _, weight_grad = ctx.consts
+        T, E, d, norm = ctx.dims
         dev = logits.device
         plan = _moe_plan(T, E, k, b, d, max_width, dev)
 
@@ -1188,7 +1189,7 @@ class MoELayerOp(torch.autograd.Function):
         need = ctx.needs_input_grad
         want_x = grad_out is not None and (need[1] or need[2] or need[3])
         want_logits = need[0] and (
-            gz is not None or glb is not None or gcl is not None or (ctx.weight_grad and want_x))
+            gz is not None or glb is not None or gcl is not None or (weight_grad and want_x))
         grad_x = grad_w1 = grad_w2 = grad_logits = None
         g = gs = None
         ldg = 0
@@ -1205,7 +1206,7 @@ class MoELayerOp(torch.autograd.Function):
         if want_logits:
             grad_logits = torch.empty(T, E, dtype=torch.bfloat16, device=dev)
         if not want_x and not want_logits:
-            return (None,) * 13
+            return None, None, None, None, None
         scratch = torch.empty(plan[2], dtype=torch.uint8, device=dev)
         main = _lib.stream(dev)
         use_side = BACKWARD_SIDE_STREAM if BACKWARD_SIDE_STREAM is not None else plan[5]
@@ -1219,12 +1220,12 @@ class MoELayerOp(torch.autograd.Function):
                      x_flat.data_ptr(), x_flat.stride(0), w1.data_ptr(), w1.stride(0),
                      w2.data_ptr(), w2.stride(0), ewo.data_ptr(), widths.data_ptr(), d, max_width,
                      coef.data_ptr(), wn.data_ptr(), ptr(g), ldg, ptr(gs), ptr(gz), ptr(glb),
-                     ptr(gcl), int(ctx.weight_grad), ptr(grad_x), d, ptr(grad_w1), w1.stride(0),
+                     ptr(gcl), int(bool(weight_grad)), ptr(grad_x), d, ptr(grad_w1), w1.stride(0),
                      ptr(grad_w2), w2.stride(0), ptr(grad_logits), scratch.data_ptr(),
                      ws.data_ptr(), ws.numel(), main, side)
         if st != _lib.OK:
             _lib.check(st, "vmoe_moe_backward")
-        return (grad_logits, grad_x, grad_w1, grad_w2) + (None,) * 9
+        return grad_logits, grad_x, grad_w1, grad_w2, None
 
 
 class NoTokensOp(torch.autograd.Function):

@@ -304,10 +304,11 @@ class TritonMoEMLP(nn.Module):
             # everything after the router Linear: one node, one call each way
             coef, wn = self._aux_tables(router_logits.device)
             out, z, lb, cl, f_i = MoELayerOp.apply(
-                router_logits, x_flat, self.w1, self.w2, self.expert_widths_t,
-                self.expert_weight_offsets_t, coef, wn, self.num_active_experts,
-                self.block_size, self.max_expert_width, self.norm_topk_prob,
-                self.config.routing_weight_grad and torch.is_grad_enabled())
+                router_logits, x_flat, self.w1, self.w2,
+                (self.expert_widths_t, self.expert_weight_offsets_t, coef, wn,
+                 self.num_active_experts, self.block_size, self.max_expert_width,
+                 self.norm_topk_prob,
+                 self.config.routing_weight_grad and torch.is_grad_enabled()))
             aux_loss = {"router_z_loss": z, "load_balance_loss": lb, "compute_loss": cl}
             return out.view(batch_size, seq_len, n_embd), aux_loss, f_i.to(x.dtype)
         state = router_topk(router_logits, self.num_active_experts, self.norm_topk_prob,
