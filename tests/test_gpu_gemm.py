@@ -36,8 +36,11 @@ CASES = [
     (2048, 768, [(4, 512), (8, 256), (4, 128)], 2, 64, False),  # config-2 widths
     (2048, 1024, [(64, 256)], 8, 64, True),            # config-3 shape, skewed, empties
     (1024, 2048, [(2, 1024), (2, 512)], 2, 64, False),  # d x max width >= 2^21: dW lanes of 8
+    # hidden and widths multiples of 8 only: every K loop ends in a partial
+    # stage (K = 200 or a width of 40 / 24 / 8), top_k 1
+    (300, 200, [(3, 40), (2, 24), (1, 8)], 1, 64, False),
 ]
-IDS = ["small", "uniform", "variable", "tiny_tiles", "var3", "skew64", "wide_lanes8"]
+IDS = ["small", "uniform", "variable", "tiny_tiles", "var3", "skew64", "wide_lanes8", "mult8"]
 
 
 def _case(T, d, sizes, k, b, skew, seed=0):

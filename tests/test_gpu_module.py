@@ -42,6 +42,11 @@ CONFIGS = {
     # own instead of riding in the routing launch
     "e128": (2, 1024, 256, [(96, 128), (32, 64)], 4, 64, 1.0),
     "one_token": (1, 1, 256, [(2, 256), (2, 128)], 2, 64, None),
+    # hidden a multiple of 8 only (every K = hidden loop ends in a partial
+    # stage), widths that cut the 256-wide tiles, top_k 1 and an odd top_k,
+    # token counts that fill no tile
+    "odd_k1": (1, 300, 200, [(3, 64), (2, 128)], 1, 64, 2.0),
+    "odd_k3": (3, 100, 136, [(5, 64), (3, 192)], 3, 64, None),
 }
 
 
@@ -582,7 +587,7 @@ def test_routing_weight_grad_at_zero_and_denormal_weights(name, device):
 
 @pytest.mark.parametrize("name,grad", [("ref_variable", "random"), ("cfg1", "sum"),
                                        ("cfg2", "scaled"), ("cfg3_a1", "random"),
-                                       ("e128", "random")])
+                                       ("e128", "random"), ("odd_k3", "random")])
 def test_fused_expert_path_same_bits_as_per_kernel_path(name, grad, device):
     """The module after its router Linear as one library call per direction
     (vmoe_moe_forward / _backward, the default) gives the bits of the

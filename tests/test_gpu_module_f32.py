@@ -32,6 +32,9 @@ SHAPES = {
     "ref_variable": (4, 256, 256, [(4, 512), (4, 256)], 2, 128),
     "cfg2_small": (2, 512, 768, [(4, 512), (8, 256), (4, 128)], 2, 64),
     "k8_64": (1, 2048, 256, [(64, 128)], 8, 64),
+    # hidden and offsets off every vector width (rows of 98 floats are 8-byte
+    # aligned at best), widths of 4 to 20 (blocks of 4 rows), an odd top_k
+    "unaligned": (1, 300, 98, [(3, 12), (2, 20), (1, 4)], 3, 4),
 }
 
 
