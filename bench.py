@@ -636,8 +636,8 @@ def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU (expert/data "
-                          "parallel) scaling is a design in DESIGN.md, not a measured path",
+        print(json.dumps({"error": "this build runs on one GPU only (--gpus 1); the expert/data "
+                          "parallel sharding of the layer is designed, not built or measured",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
