@@ -225,6 +225,31 @@ def test_forward_deterministic(device):
         assert bits_equal(a, b)
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_backward_twice_with_retain_graph(fused, device):
+    """backward(retain_graph=True) twice through one forward: the backward
+    only reads what the forward saved, so the second pass gives the first
+    pass's gradients again and the accumulated .grad is exactly twice them
+    (x, w1, w2 and, through the auxiliary losses, the router weight)."""
+    from triton_moe.kernels import grouped_gemm as gg
+
+    gg.FUSED_EXPERT_PATH = fused
+    try:
+        m, x, out, aux, _, _ = _run("ref_variable", device)
+        G = torch.randn(x.shape, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+        loss = (out.float() * G.to(device).float()).sum() + sum(aux.values())
+        params = (x, m.w1, m.w2, m.router.weight)
+        loss.backward(retain_graph=True)
+        first = [p.grad.clone() for p in params]
+        loss.backward()
+        torch.cuda.synchronize()
+        for p, g1, what in zip(params, first, ("x", "w1", "w2", "router")):
+            assert torch.isfinite(g1.float()).all() and int(torch.count_nonzero(g1)) > 0, what
+            assert bits_equal(p.grad, g1 * 2), what
+    finally:
+        gg.FUSED_EXPERT_PATH = True
+
+
 @pytest.mark.parametrize("fused,dtype", [(True, torch.bfloat16), (False, torch.bfloat16),
                                          (True, torch.float32)])
 def test_no_tokens(fused, dtype, device):
