@@ -720,3 +720,30 @@ def test_glu_row_scale_and_gather_map_capi(device):
     assert_close_norm(outs[0], h_ref, TIGHT, "glu H with row factors")
     assert_close_norm(outs[1], g_ref, TIGHT, "glu gate")
     assert_close_norm(outs[2], u_ref, TIGHT, "glu up")
+
+
+def test_column_slice_operands(device):
+    """grouped_gemm_up / _down on column slices of wider tensors (rows 2 bytes
+    past a 16-byte boundary) give the bits of contiguous copies."""
+    c = _case(1024, 256, [(4, 512), (4, 256)], 2, 128, False)
+    eto, ewo, wid, tpe = _meta_dev(c, device)
+    P, d, W, max_w = c["P"], c["d"], c["W"], c["max_w"]
+    g = torch.Generator().manual_seed(4)
+    xw = torch.randn(P, d + 8, generator=g).to(torch.bfloat16).to(device)
+    w1w = (torch.randn(d, W + 8, generator=g) * 0.05).to(torch.bfloat16).to(device)
+    w2w = (torch.randn(W, d + 8, generator=g) * 0.05).to(torch.bfloat16).to(device)
+    res = []
+    for sliced in (True, False):
+        def view(t, n):
+            v = t[:, 1:1 + n]
+            return v if sliced else v.contiguous()
+        x, w1, w2 = view(xw, d), view(w1w, W), view(w2w, d)
+        if sliced:
+            assert x.data_ptr() % 16 == 2 and w1.data_ptr() % 16 == 2
+        h, pre = grouped_gemm_up(x, w1, eto, ewo, wid, tpe, max_w, activation="relu_squared",
+                                 save_pre_act=True)
+        y = grouped_gemm_down(h, w2, eto, ewo, wid, tpe, d)
+        res.append((h, pre, y))
+    torch.cuda.synchronize()
+    for a, b in zip(*res):
+        assert bits_equal(a, b)

@@ -250,6 +250,42 @@ def test_backward_twice_with_retain_graph(fused, device):
         gg.FUSED_EXPERT_PATH = True
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_column_slice_input_same_bits(fused, device):
+    """An input that is a column slice of a wider tensor (rows start 2 bytes
+    past a 16-byte boundary) gives the bits of the same values stored
+    contiguously: output, losses and every gradient (the GEMMs' operands are
+    copied to aligned rows first). The router Linear is fed a contiguous copy
+    in both runs, since hipBLASLt may pick another kernel for another layout."""
+    from triton_moe.kernels import grouped_gemm as gg
+
+    B, S, d, sizes, k, b, _ = CONFIGS["ref_variable"]
+    g = torch.Generator().manual_seed(11)
+    wide = torch.randn(B, S, d + 8, generator=g).to(torch.bfloat16).to(device)
+    G = torch.randn(B, S, d, generator=g).to(torch.bfloat16).to(device)
+    p = make_problem(B * S, d, sizes, k, b, seed=0, device=device)
+    gg.FUSED_EXPERT_PATH = fused
+    try:
+        res = []
+        for sliced in (True, False):
+            m = _module(p, d, sizes, k, b, device)
+            m.router.register_forward_pre_hook(lambda mod, args: (args[0].contiguous(),))
+            src = wide.detach().clone().requires_grad_(True)
+            x = src[:, :, 1:1 + d] if sliced else src[:, :, 1:1 + d].contiguous()
+            if sliced:
+                assert x.data_ptr() % 16 == 2
+            out, aux, f_i = m(x)
+            loss = (out.float() * G.float()).sum() + sum(aux.values())
+            loss.backward()
+            res.append([out, f_i, *aux.values(), src.grad, m.w1.grad, m.w2.grad,
+                        m.router.weight.grad])
+        torch.cuda.synchronize()
+        for a, c in zip(*res):
+            assert bits_equal(a, c)
+    finally:
+        gg.FUSED_EXPERT_PATH = True
+
+
 @pytest.mark.parametrize("fused,dtype", [(True, torch.bfloat16), (False, torch.bfloat16),
                                          (True, torch.float32)])
 def test_no_tokens(fused, dtype, device):

@@ -109,9 +109,14 @@ def host_meta(eto, ewo, widths, tpe, max_width: int, hidden: int, rows: int | No
 
 
 def _bf16(t: torch.Tensor, what: str) -> torch.Tensor:
+    """t as the bf16 GEMMs read it: unit column stride, rows 16-byte aligned
+    (row stride a multiple of 8 elements, 16-byte aligned start). Any other
+    view, such as a column slice, is copied into a fresh tensor."""
     if t.dtype != torch.bfloat16:
         raise NotImplementedError(f"{what}: only bfloat16 is supported (got {t.dtype})")
-    return t if t.stride(-1) == 1 and t.stride(0) % 8 == 0 else t.contiguous()
+    if t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
 
 
 def _need(cond: bool, msg: str) -> None:
