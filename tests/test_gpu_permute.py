@@ -126,6 +126,29 @@ def test_strided_and_broadcast_inputs(device):
     assert bits_equal(yd.grad, _ref_gather(ones, maps, k, wts))
 
 
+def test_column_slice_inputs(device):
+    """Column slices of wider tensors (rows 2 bytes past a 16-byte boundary)
+    as gather source, weighted gather source and scatter input: the bits of
+    the contiguous case (the kernels' element-wise paths)."""
+    T, d, E, k, b = 256, 128, 4, 2, 64
+    x, sel, wts, r, maps = _setup(T, d, E, k, b, device, seed=8)
+    dev = lambda a: torch.as_tensor(a).to(device)  # noqa: E731
+    idx, bid, bins, pb = (dev(r[n]) for n in ("indices", "bin_ids", "bins", "padded_bins"))
+    wide = torch.zeros(T, d + 8, dtype=torch.bfloat16)
+    wide[:, 1:1 + d] = x
+    xs = wide.to(device)[:, 1:1 + d]
+    assert xs.data_ptr() % 16 == 2
+    got = padded_gather(xs, idx, bid, bins, pb, k)
+    assert bits_equal(got, _ref_gather(x, maps, k))
+    wv = wts.reshape(-1).to(device)
+    P = got.shape[0]
+    ywide = torch.zeros(P, d + 8, dtype=torch.bfloat16, device=device)
+    ywide[:, 1:1 + d] = got
+    ys = ywide[:, 1:1 + d]
+    assert bits_equal(padded_scatter(ys, idx, bid, wv, bins, pb, k),
+                      padded_scatter(got, idx, bid, wv, bins, pb, k))
+
+
 def test_route_maps_feed_permutation(device):
     """route_device's own maps give the same gather as the public API."""
     T, d, E, k = 1000, 256, 16, 4
