@@ -286,6 +286,32 @@ def test_column_slice_input_same_bits(fused, device):
         gg.FUSED_EXPERT_PATH = True
 
 
+def test_strided_router_logits_same_bits(device):
+    """Router logits handed on as a strided view (a forward hook on the
+    router returning a column slice of a wider tensor) give the bits of the
+    plain logits: output, losses, f_i and the x / router gradients."""
+    B, S, d, sizes, k, b, _ = CONFIGS["ref_variable"]
+    E = sum(c for c, _ in sizes)
+    p = make_problem(B * S, d, sizes, k, b, seed=2, device=device)
+    G = torch.randn(B, S, d, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    res = []
+    for strided in (True, False):
+        m = _module(p, d, sizes, k, b, device)
+        if strided:
+            def hook(mod, inp, out):
+                wide = torch.cat([out[:, :1], out, out[:, :7]], dim=1)
+                return wide[:, 1:1 + E]
+            m.router.register_forward_hook(hook)
+        x = p["x"].view(B, S, d).to(device).requires_grad_(True)
+        out, aux, f_i = m(x)
+        loss = (out.float() * G.to(device).float()).sum() + sum(aux.values())
+        loss.backward()
+        res.append([out, f_i, *aux.values(), x.grad, m.router.weight.grad, m.w1.grad])
+    torch.cuda.synchronize()
+    for a, c in zip(*res):
+        assert bits_equal(a, c)
+
+
 @pytest.mark.parametrize("fused,dtype", [(True, torch.bfloat16), (False, torch.bfloat16),
                                          (True, torch.float32)])
 def test_no_tokens(fused, dtype, device):

@@ -1150,7 +1150,7 @@ class MoELayerOp(torch.autograd.Function):
         dev = x_flat.device
         x_flat = _bf16(x_flat, "TritonMoEMLP x")
         if not logits.is_contiguous() or logits.data_ptr() % 16:
-            logits = logits.contiguous().clone()
+            logits = logits.clone(memory_format=torch.contiguous_format)
         plan = _moe_plan(T, E, top_k, block_size, d, max_width, dev)
         saved = torch.empty(plan[0], dtype=torch.uint8, device=dev)
         scratch = torch.empty(plan[1], dtype=torch.uint8, device=dev)
