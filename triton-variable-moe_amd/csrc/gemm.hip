@@ -1490,6 +1490,10 @@ struct Gemm {
   // waits for its window explicitly.
   __device__ static void run_producer(const Args& p, lds_char* ring, lds_char* wins,
                                       lds_char* scl, const Meta& mt, const Range& rg) {
+    // The producer wave of each SIMD issues ahead of its two consumer waves
+    // when both have an instruction ready: the DMAs are the stage's long pole
+    // (s_setprio orders issue only; results do not change).
+    __builtin_amdgcn_s_setprio(2);
     int ei = 0, ela = 0;
     Work wi;
     Src<PWA_S> sa;
