@@ -1139,8 +1139,9 @@ class MoELayerOp(torch.autograd.Function):
     Unlike the per-kernel ops it carries no torch.amp custom_fwd / custom_bwd:
     neither direction runs an op that autocast would change (allocations with
     explicit dtypes and one library call), so the autocast context those
-    decorators enter around the backward (~12 us of host time per step on an
-    eager cfg1 step, which is host-bound) changes nothing but the time."""
+    decorators enter around the backward (~12 us of host time per eager cfg1
+    step, whose pace the host sets on slower host CPUs) changes nothing but
+    the time."""
 
     @staticmethod
     def forward(ctx, logits, x_flat, w1, w2, consts):
